@@ -1,0 +1,113 @@
+/* lockstep_amd: the Lockstep contract matrix-multiply path on MI355X (gfx950).
+ *
+ * A plain C ABI over hand-written HIP kernels.  Every pointer is a device pointer unless
+ * stated otherwise; sizes and leading dimensions are in elements; `stream` is a hipStream_t
+ * (NULL = the legacy default stream).  Every entry point is stream-ordered, returns 0 on
+ * success or an LSK_ERR_* code, and leaves a message for lsk_last_error() on failure.
+ * Nothing here allocates device memory unless its comment says so; workspace comes from
+ * the caller.  Results are bit-identical to the reference functions cited on each entry
+ * point, for every input, on every launch (no floating-point atomics, no split-K of
+ * anything but exact integer sums).
+ */
+#ifndef LOCKSTEP_AMD_H
+#define LOCKSTEP_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define LSK_OK 0
+#define LSK_ERR_ARG 1          /* bad shape, stride, alignment or dtype */
+#define LSK_ERR_HIP 2          /* a HIP launch or runtime call failed */
+#define LSK_ERR_UNSUPPORTED 3  /* valid input this build does not handle */
+
+/* element types */
+typedef enum {
+  LSK_F32 = 0,
+  LSK_BF16 = 1,
+  LSK_F16 = 2,
+  LSK_I32 = 3,
+  LSK_I8 = 4,
+  LSK_BF16_AS_F32 = 5 /* binary32 storage holding bf16-rounded values (moe_ref's bfr) */
+} lsk_dtype;
+
+/* epilogue orders applied to the exact int32 accumulator */
+typedef enum {
+  LSK_EPI_V21 = 0,  /* out(fl32(fl32(acc)*ws[n])*asc[m]); bias: out(fl32(out) + b[n]) */
+  LSK_EPI_V2 = 1,   /* out(fl32(fl32(fl32(acc)*asc[m])*ws[n]) + b[n]) (legacy order) */
+  LSK_EPI_POW2 = 2, /* fl32(acc) * 2^-(shift + erow[m] + ecol[n]) (exact scaling) */
+  LSK_EPI_RAW = 3   /* the int32 accumulator itself */
+} lsk_epilogue;
+
+/* The last error message of the calling thread ("" if none). */
+const char* lsk_last_error(void);
+
+/* Library version string. */
+const char* lsk_version(void);
+
+/* Per-row int8 quantisation.
+ * Replaces moe_ref.rowquant (reference/moe_ref.py:27-37), lockstep_fullstack.quantize_rows_int8
+ * (reference/lockstep_fullstack.py:476-481) and the inline quant of contract_common.w8a8_linear
+ * (reference/contract_common.py:168-169):
+ *   asc[m] = fl32(max(max_k |x[m,k]|, fl32(1e-8)) / 127)       (true division)
+ *   q[m,k] = clamp(rint_even(fl32(x[m,k] / asc[m])), -127, 127)
+ * x: [M, K] of x_dtype (LSK_F32 / LSK_BF16 / LSK_F16), row stride ldx; q: [M, K] int8, row
+ * stride ldq; asc: [M] float. */
+int lsk_rowquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                 int8_t* q, int64_t ldq, float* asc, void* stream);
+
+/* Exact int8 x int8 -> int32 GEMM with a contract epilogue, c[m, n] = sum_k a[m,k] * w[n,k].
+ * Replaces moe_ref.int_mm + lin_epilogue / lin_epilogue_b (reference/moe_ref.py:40-55,164-169),
+ * lockstep_fullstack._int_mm_exact + the w8a8_matmul epilogue (reference/lockstep_fullstack.py:484-527),
+ * the _int_mm + epilogue of contract_common.w8a8_linear (reference/contract_common.py:170-174)
+ * and ref_block_v1.gemm_int + its pow2 dequant (reference/ref_block_v1.py:132-133,167,193,198,218).
+ * a: [M, K] int8 (row stride lda); w: [N, K] int8 (row stride ldw; the reference's b8 = W8.t());
+ * out: [M, N] of out_dtype (row stride ldo).  `order` is an lsk_epilogue; asc/ws are used by
+ * V21/V2, bias is optional (NULL), erow/ecol/shift by POW2, out_dtype must be LSK_I32 for RAW.
+ * M may be 0.  K is bounded by 133144 (|acc| <= K * 127^2 < 2^31). */
+int lsk_gemm_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
+                  int64_t M, int64_t N, int64_t K, int order,
+                  const float* asc, const float* ws, const float* bias,
+                  const int32_t* erow, const int32_t* ecol, int shift,
+                  void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* The contract epilogue alone, over an existing int32 accumulator acc [M, N] (row stride ldc).
+ * Replaces moe_ref.lin_epilogue / lin_epilogue_b (reference/moe_ref.py:40-42,164-169) when the
+ * caller keeps the reference's separate int_mm and epilogue calls.  Same parameters as
+ * lsk_gemm_w8a8; RAW is not accepted. */
+int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, int64_t N, int order,
+                       const float* asc, const float* ws, const float* bias,
+                       const int32_t* erow, const int32_t* ecol, int shift,
+                       void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* Bytes of caller workspace lsk_w8a8_matmul needs for M rows of width K. */
+int64_t lsk_w8a8_matmul_workspace(int64_t M, int64_t K);
+
+/* The whole dense contract linear: row quant of x, exact GEMM, epilogue `order` (V21 or V2).
+ * Replaces lockstep_fullstack.w8a8_matmul (reference/lockstep_fullstack.py:503-530; order V21)
+ * and the forward of contract_common.w8a8_linear (reference/contract_common.py:166-174; order V2).
+ * x: [M, K] of x_dtype (row stride ldx); w: [N, K] int8; ws: [N]; bias: [N] or NULL;
+ * out: [M, N] of out_dtype.  workspace: device memory of lsk_w8a8_matmul_workspace(M, K) bytes,
+ * 256-byte aligned. */
+int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                    const int8_t* w, int64_t ldw, int64_t N, const float* ws, const float* bias,
+                    int order, void* out, int out_dtype, int64_t ldo,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Power-of-two int8 quantisation of ref_block_v1 (reference/ref_block_v1.py:56-72,122-130).
+ * mode 0 = per tensor (quant8_dyn: one exponent e_out[0]); 1 = per row (quant8_rows: e_out[M]);
+ * 2 = per column (quant8_cols: e_out[K]).  e = 6 - (biased_exp(m) - 127), minus 1 when
+ * fl32(m * 2^e) > 127, clipped to [-32, 40] (per tensor: 0 and q = 0 when m == 0);
+ * q = clamp(rint_even(fl32(x * 2^e)), -127, 127).  x: [M, K] binary32 (row stride ldx);
+ * q: [M, K] int8 (row stride ldq); e_out: int32.  workspace: 4 * (M + K + 64) bytes. */
+int lsk_quant8_pow2(const float* x, int64_t M, int64_t K, int64_t ldx, int mode,
+                    int8_t* q, int64_t ldq, int32_t* e_out, void* workspace, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOCKSTEP_AMD_H */

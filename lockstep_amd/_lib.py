@@ -1,0 +1,104 @@
+"""ctypes bindings of liblockstep_amd.so (the C ABI declared in include/lockstep_amd.h).
+
+The library is loaded from this package directory; if it is missing the first call raises,
+naming the build command.  There is no CPU fallback anywhere in this package: every entry
+point runs the HIP kernels or raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblockstep_amd.so")
+
+LSK_F32, LSK_BF16, LSK_F16, LSK_I32, LSK_I8, LSK_BF16_AS_F32 = 0, 1, 2, 3, 4, 5
+EPI_V21, EPI_V2, EPI_POW2, EPI_RAW = 0, 1, 2, 3
+
+_DTYPE = {torch.float32: LSK_F32, torch.bfloat16: LSK_BF16, torch.float16: LSK_F16,
+          torch.int32: LSK_I32, torch.int8: LSK_I8}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+
+# name -> (restype, argtypes); kept in the order of include/lockstep_amd.h
+SIGNATURES = {
+    "lsk_last_error": (ctypes.c_char_p, []),
+    "lsk_version": (ctypes.c_char_p, []),
+    "lsk_rowquant": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _P]),
+    "lsk_gemm_w8a8": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I64, _P]),
+    "lsk_epilogue_apply": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I64, _P]),
+    "lsk_w8a8_matmul_workspace": (_I64, [_I64, _I64]),
+    "lsk_w8a8_matmul": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P, _I64, _P]),
+    "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class LockstepError(RuntimeError):
+    pass
+
+
+def load(path: str = LIB_PATH):
+    """Load the shared library (once) and bind every exported symbol."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise LockstepError("%s is not built: run `python -m lockstep_amd.build` (hipcc, gfx950)" % path)
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return load().lsk_last_error().decode(errors="replace")
+
+
+def call(name: str, *args):
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        raise LockstepError("%s failed (code %d): %s" % (name, rc, last_error()))
+    return rc
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE[dt]
+    except KeyError:
+        raise TypeError("unsupported dtype %s" % dt) from None
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_cuda(*ts, what: str = "lockstep_amd"):
+    """Every tensor argument must live on one ROCm device; CPU tensors are refused (this
+    package has no CPU path; the reference's own functions are the CPU path)."""
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError("%s: expected a GPU tensor, got %s" % (what, type(t).__name__ if not isinstance(t, torch.Tensor) else t.device))
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("%s: tensors on %s and %s" % (what, dev, t.device))
+    return dev

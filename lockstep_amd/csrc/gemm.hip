@@ -1,0 +1,332 @@
+// Dense contract GEMM on gfx950: exact int8 x int8 -> int32 on MFMA, fused binary32 epilogue.
+//
+//   prefill (M > 32): LDS-staged MFMA tiles, v_mfma_i32_16x16x64_i8, double-buffered 128-byte
+//                     K stages, XOR-swizzled 16-byte LDS chunks, XCD-aware tile order.
+//   decode  (M <= 32): weight-streaming GEMV on the same MFMA (rows padded to 16 in registers),
+//                     K split over the block's waves and reduced exactly in LDS.
+//   generic:          any stride / alignment / K, one thread per output (correctness path).
+//
+// Integer accumulation is exact in any order (|acc| <= K * 127^2 < 2^31 for K <= 133144), so
+// tiling and K-splits never change a bit; the epilogue is applied once per output element.
+#include "lsk_common.h"
+
+namespace {
+
+constexpr int kBK = 128;  // bytes of K per LDS stage (8 chunks of 16 B per row)
+
+LSK_DEV v4i mfma16(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+
+LSK_DEV v4i zero4() { return v4i{0, 0, 0, 0}; }
+
+// Map a hardware block id to a logical tile id so that the blocks one XCD runs (hardware ids
+// congruent mod 8) form one contiguous run of logical ids, then walk logical ids M-fastest
+// inside groups of `gm` M-tiles: tiles that run together share weight and activation panels
+// in the XCD's own L2.
+LSK_DEV void tile_coords(int nblocks, int mtiles, int ntiles, int gm, int& mt, int& nt) {
+  const int b = blockIdx.x;
+  const int per = nblocks / 8, rem = nblocks % 8;
+  const int x = b % 8, i = b / 8;
+  const int L = x * per + (x < rem ? x : rem) + i;
+  const int group = L / (gm * ntiles);
+  const int first_m = group * gm;
+  const int gsize = (mtiles - first_m) < gm ? (mtiles - first_m) : gm;
+  const int r = L - group * gm * ntiles;
+  mt = first_m + r % gsize;
+  nt = r / gsize;
+}
+
+template <int BM, int BN, int WM, int WN>
+struct Cfg {
+  static constexpr int kThreads = WM * WN * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int TM = WTM / 16, TN = WTN / 16;
+  static constexpr int kAChunks = BM * kBK / 16, kBChunks = BN * kBK / 16;
+  static constexpr int kAPer = kAChunks / kThreads, kBPer = kBChunks / kThreads;
+  static_assert(kAChunks % kThreads == 0 && kBChunks % kThreads == 0, "tile/threads mismatch");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be a multiple of 16");
+};
+
+// C[m, n] = sum_k A[m, k] * W[n, k]; A and W K-contiguous, K % 16 == 0, 16-byte aligned rows.
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
+    const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ W, int64_t ldw, int M, int N, int K,
+    EpiParams ep) {
+  using C = Cfg<BM, BN, WM, WN>;
+  __shared__ v4i sA[2][BM * 8];
+  __shared__ v4i sB[2][BN * 8];
+
+  const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN;
+  int mt, nt;
+  tile_coords(mtiles * ntiles, mtiles, ntiles, 16, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  v4i acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = zero4();
+
+  v4i ra[C::kAPer], rb[C::kBPer];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < C::kAPer; ++j) {
+      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
+      const int gm = m0 + row, gk = k0 + c * 16;
+      ra[j] = (gm < M && gk < K) ? *(const v4i*)(A + (int64_t)gm * lda + gk) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < C::kBPer; ++j) {
+      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
+      const int gn = n0 + row, gk = k0 + c * 16;
+      rb[j] = (gn < N && gk < K) ? *(const v4i*)(W + (int64_t)gn * ldw + gk) : zero4();
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < C::kAPer; ++j) {
+      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
+      sA[buf][row * 8 + (c ^ (row & 7))] = ra[j];
+    }
+#pragma unroll
+    for (int j = 0; j < C::kBPer; ++j) {
+      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
+      sB[buf][row * 8 + (c ^ (row & 7))] = rb[j];
+    }
+  };
+
+  const int nk = (K + kBK - 1) / kBK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = ks * 4 + (lane >> 4);
+      v4i af[C::TM], bf[C::TN];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) {
+        const int r = wm * C::WTM + i * 16 + (lane & 15);
+        af[i] = sA[buf][r * 8 + (c ^ (r & 7))];
+      }
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        const int r = wn * C::WTN + j * 16 + (lane & 15);
+        bf[j] = sB[buf][r * 8 + (c ^ (r & 7))];
+      }
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // D[i][j] of one 16x16 MFMA tile lives in lane (j + 16 * (i / 4)), register i % 4.
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + wm * C::WTM + i * 16 + (lane >> 4) * 4 + r;
+        const int n = n0 + wn * C::WTN + j * 16 + (lane & 15);
+        if (m < M && n < N) epilogue_store(ep, m, n, acc[i][j][r]);
+      }
+}
+
+// Decode GEMV: one block per 16 output columns; its 4 waves take interleaved 256-byte K slabs;
+// each lane streams 64 contiguous weight bytes per slab (4 MFMAs).  MT 16-row tiles cover M.
+template <int MT>
+__global__ __launch_bounds__(256) void gemv_i8_mfma_kernel(const int8_t* __restrict__ A, int64_t lda,
+                                                           const int8_t* __restrict__ W, int64_t ldw, int M,
+                                                           int N, int K, EpiParams ep) {
+  __shared__ v4i red[3][MT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int n = n0 + col;
+  const bool nvalid = n < N;
+  const int8_t* wrow = W + (int64_t)(nvalid ? n : 0) * ldw;
+
+  v4i acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = zero4();
+
+  for (int kb = wave * 256; kb < K; kb += 4 * 256) {
+    const int k = kb + kg * 64;
+    v4i w4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w4[j] = (nvalid && k + j * 16 < K) ? *(const v4i*)(wrow + k + j * 16) : zero4();
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 16 + col;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v4i a = (m < M && k + j * 16 < K) ? *(const v4i*)(A + (int64_t)m * lda + k + j * 16) : zero4();
+        acc[t] = mfma16(a, w4[j], acc[t]);
+      }
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[wave - 1][t][lane] = acc[t];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    v4i s = acc[t];
+#pragma unroll
+    for (int w = 0; w < 3; ++w) s += red[w][t][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + (lane >> 4) * 4 + r;
+      if (m < M && nvalid) epilogue_store(ep, m, n, s[r]);
+    }
+  }
+}
+
+// Correctness path for shapes the tiled kernels do not take (odd K, unaligned rows).
+__global__ __launch_bounds__(256) void gemm_i8_generic_kernel(const int8_t* __restrict__ A, int64_t lda,
+                                                              const int8_t* __restrict__ W, int64_t ldw, int64_t M,
+                                                              int64_t N, int64_t K, EpiParams ep) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * N) return;
+  const int64_t m = idx / N, n = idx - m * N;
+  const int8_t* a = A + m * lda;
+  const int8_t* w = W + n * ldw;
+  int32_t s = 0;
+  for (int64_t k = 0; k < K; ++k) s += (int32_t)a[k] * (int32_t)w[k];
+  epilogue_store(ep, m, n, s);
+}
+
+// The epilogue alone over an existing int32 accumulator (the reference's separate
+// lin_epilogue / lin_epilogue_b calls on the result of int_mm).
+__global__ __launch_bounds__(256) void epilogue_apply_kernel(const int32_t* __restrict__ acc, int64_t ldc,
+                                                             int64_t M, int64_t N, EpiParams ep) {
+  const int64_t total = M * N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / N, n = i - m * N;
+    epilogue_store(ep, m, n, acc[m * ldc + n]);
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+namespace lsk {
+
+// Shape checks shared by the dense and grouped entry points.
+int validate_epilogue(int order, int out_dtype, const float* asc, const float* ws, int64_t M, const char* who) {
+  LSK_REQUIRE(order >= LSK_EPI_V21 && order <= LSK_EPI_RAW, "%s: unknown epilogue order %d", who, order);
+  if (order == LSK_EPI_RAW) {
+    LSK_REQUIRE(out_dtype == LSK_I32, "%s: the RAW epilogue writes int32 (out_dtype %d)", who, out_dtype);
+  } else if (order == LSK_EPI_POW2) {
+    LSK_REQUIRE(out_dtype == LSK_F32, "%s: the POW2 epilogue writes binary32 (out_dtype %d)", who, out_dtype);
+  } else {
+    LSK_REQUIRE(out_dtype == LSK_F32 || out_dtype == LSK_BF16 || out_dtype == LSK_F16 || out_dtype == LSK_BF16_AS_F32,
+                "%s: out_dtype %d not one of f32/bf16/f16/bf16-as-f32", who, out_dtype);
+    LSK_REQUIRE(M == 0 || (asc && ws), "%s: asc and ws are required by the V21/V2 epilogues", who);
+  }
+  return LSK_OK;
+}
+
+int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                const EpiParams& ep, hipStream_t s) {
+  if (M == 0 || N == 0) return LSK_OK;
+  const bool fast = (K % 16 == 0) && (lda % 16 == 0) && (ldw % 16 == 0) && aligned16(a) && aligned16(w) &&
+                    M <= 0x7fffffff && N <= 0x7fffffff && K > 0;
+  if (!fast) {
+    const int64_t total = M * N;
+    const int64_t blocks = (total + 255) / 256;
+    LSK_REQUIRE(blocks <= 0x7fffffff, "gemm: M*N=%lld too large for the generic path", (long long)total);
+    hipLaunchKernelGGL(gemm_i8_generic_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a, lda, w, ldw, M, N, K, ep);
+    return check_launch("gemm_i8_generic_kernel");
+  }
+  const int iM = (int)M, iN = (int)N, iK = (int)K;
+  if (M <= 16) {
+    hipLaunchKernelGGL(gemv_i8_mfma_kernel<1>, dim3((unsigned)((N + 15) / 16)), dim3(256), 0, s, a, lda, w, ldw, iM,
+                       iN, iK, ep);
+    return check_launch("gemv_i8_mfma_kernel<1>");
+  }
+  if (M <= 32) {
+    hipLaunchKernelGGL(gemv_i8_mfma_kernel<2>, dim3((unsigned)((N + 15) / 16)), dim3(256), 0, s, a, lda, w, ldw, iM,
+                       iN, iK, ep);
+    return check_launch("gemv_i8_mfma_kernel<2>");
+  }
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  LSK_REQUIRE(tiles <= 0x7fffffff, "gemm: too many tiles");
+  hipLaunchKernelGGL((gemm_i8_mfma_kernel<128, 128, 2, 2>), dim3((unsigned)tiles), dim3(256), 0, s, a, lda, w, ldw,
+                     iM, iN, iK, ep);
+  return check_launch("gemm_i8_mfma_kernel<128,128,2,2>");
+}
+
+}  // namespace lsk
+
+extern "C" int lsk_gemm_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N,
+                             int64_t K, int order, const float* asc, const float* ws, const float* bias,
+                             const int32_t* erow, const int32_t* ecol, int shift, void* out, int out_dtype,
+                             int64_t ldo, void* stream) {
+  LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_gemm_w8a8: negative size M=%lld N=%lld K=%lld", (long long)M,
+              (long long)N, (long long)K);
+  LSK_REQUIRE(K <= 133144, "lsk_gemm_w8a8: K=%lld exceeds the int32-exact bound 133144", (long long)K);
+  int rc = lsk::validate_epilogue(order, out_dtype, asc, ws, M, "lsk_gemm_w8a8");
+  if (rc) return rc;
+  if (M == 0 || N == 0) return LSK_OK;
+  LSK_REQUIRE(out && ((a && w) || K == 0), "lsk_gemm_w8a8: null pointer");
+  LSK_REQUIRE(lda >= K && ldw >= K && ldo >= N, "lsk_gemm_w8a8: leading dimension too small");
+  EpiParams ep{order, out_dtype, ws, asc, bias, erow, ecol, shift, out, ldo};
+  return lsk::launch_gemm(a, lda, w, ldw, M, N, K, ep, (hipStream_t)stream);
+}
+
+extern "C" int64_t lsk_w8a8_matmul_workspace(int64_t M, int64_t K) {
+  const int64_t ldq = (K + 15) / 16 * 16;
+  return ((M * ldq + 255) / 256) * 256 + ((M * 4 + 255) / 256) * 256;
+}
+
+extern "C" int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                               int64_t ldw, int64_t N, const float* ws, const float* bias, int order, void* out,
+                               int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream) {
+  LSK_REQUIRE(order == LSK_EPI_V21 || order == LSK_EPI_V2, "lsk_w8a8_matmul: order must be V21 or V2");
+  LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_w8a8_matmul: negative size");
+  int rc = lsk::validate_epilogue(order, out_dtype, (const float*)1, ws, M, "lsk_w8a8_matmul");
+  if (rc) return rc;
+  if (M == 0 || N == 0) return LSK_OK;
+  const int64_t need = lsk_w8a8_matmul_workspace(M, K);
+  LSK_REQUIRE(workspace && workspace_bytes >= need, "lsk_w8a8_matmul: workspace of %lld bytes needed",
+              (long long)need);
+  LSK_REQUIRE(((uintptr_t)workspace & 255) == 0, "lsk_w8a8_matmul: workspace must be 256-byte aligned");
+  const int64_t ldq = (K + 15) / 16 * 16;
+  int8_t* q = (int8_t*)workspace;
+  float* asc = (float*)((char*)workspace + ((M * ldq + 255) / 256) * 256);
+  rc = lsk_rowquant(x, x_dtype, M, K, ldx, q, ldq, asc, stream);
+  if (rc) return rc;
+  return lsk_gemm_w8a8(q, ldq, w, ldw, M, N, K, order, asc, ws, bias, nullptr, nullptr, 0, out, out_dtype, ldo,
+                       stream);
+}
+
+extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, int64_t N, int order,
+                                  const float* asc, const float* ws, const float* bias, const int32_t* erow,
+                                  const int32_t* ecol, int shift, void* out, int out_dtype, int64_t ldo,
+                                  void* stream) {
+  LSK_REQUIRE(M >= 0 && N >= 0, "lsk_epilogue_apply: negative size");
+  LSK_REQUIRE(order != LSK_EPI_RAW, "lsk_epilogue_apply: RAW is a copy, not an epilogue");
+  int rc = lsk::validate_epilogue(order, out_dtype, asc, ws, M, "lsk_epilogue_apply");
+  if (rc) return rc;
+  if (M == 0 || N == 0) return LSK_OK;
+  LSK_REQUIRE(acc && out, "lsk_epilogue_apply: null pointer");
+  LSK_REQUIRE(ldc >= N && ldo >= N, "lsk_epilogue_apply: leading dimension below N");
+  EpiParams ep{order, out_dtype, ws, asc, bias, erow, ecol, shift, out, ldo};
+  int64_t blocks = (M * N + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(epilogue_apply_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, acc, ldc, M,
+                     N, ep);
+  return lsk::check_launch("epilogue_apply_kernel");
+}

@@ -1,0 +1,145 @@
+// Shared device helpers for the contract GEMM kernels (gfx950 only).
+//
+// Every binary32 operation in an epilogue must be one IEEE operation rounded to nearest
+// even, in the declared order.  The build passes -ffp-contract=off; the pragma below makes
+// the sources safe under any flag set, so no multiply and add are ever fused into an FMA.
+#pragma once
+#pragma clang fp contract(off)
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lockstep_amd.h"
+
+#define LSK_DEV __device__ __forceinline__
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+// binary32 -> bf16, round to nearest even; every NaN becomes 0x7FC0 (the conversion torch's
+// c10::BFloat16 performs, which is what the reference's `.to(torch.bfloat16)` runs).
+LSK_DEV uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+LSK_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// fl32 -> bf16 -> fl32 (one bf16 rounding, kept in binary32)
+LSK_DEV float bfr(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// exact 2^e for e in [-149, 127] (subnormal powers included), built from bits
+LSK_DEV float pow2f(int e) {
+  if (e >= -126) return __uint_as_float((uint32_t)(e + 127) << 23);
+  return __uint_as_float(1u << (e + 149));
+}
+
+LSK_DEV float f32_mul(float a, float b) { return a * b; }
+LSK_DEV float f32_add(float a, float b) { return a + b; }
+LSK_DEV float f32_div(float a, float b) { return a / b; }   // correctly rounded (build flag)
+
+// Load one activation element of the given dtype as binary32 (bf16 and f16 widen exactly).
+LSK_DEV float load_as_f32(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case LSK_BF16: return bf16_to_f32(((const uint16_t*)p)[i]);
+    case LSK_F16: return (float)(((const _Float16*)p)[i]);
+    default: return ((const float*)p)[i];
+  }
+}
+
+// Store binary32 `y` rounded to the output dtype.  Returns the stored value widened back to
+// binary32 (what the reference's next `.float()` sees).
+LSK_DEV float store_out(void* out, int dtype, int64_t i, float y) {
+  switch (dtype) {
+    case LSK_BF16: {
+      uint16_t b = f32_to_bf16(y);
+      ((uint16_t*)out)[i] = b;
+      return bf16_to_f32(b);
+    }
+    case LSK_F16: {
+      _Float16 h = (_Float16)y;
+      ((_Float16*)out)[i] = h;
+      return (float)h;
+    }
+    case LSK_BF16_AS_F32: {
+      float r = bfr(y);
+      ((float*)out)[i] = r;
+      return r;
+    }
+    default:
+      ((float*)out)[i] = y;
+      return y;
+  }
+}
+
+LSK_DEV float round_out(int dtype, float y) {
+  switch (dtype) {
+    case LSK_BF16:
+    case LSK_BF16_AS_F32: return bfr(y);
+    case LSK_F16: return (float)(_Float16)y;
+    default: return y;
+  }
+}
+
+// The contract epilogues, applied to one exact int32 accumulator.
+//   V21  (moe_ref.py:40-42, lockstep_fullstack.py:524-527): y = fl32(fl32(acc)*ws[n])*asc[m],
+//        rounded to the output type; a bias is a second rounding: out(fl32(y_out) + b[n]).
+//   V2   (contract_common.py:172-174): y = fl32(fl32(acc)*asc[m])*ws[n] (+ b[n]) then one cast.
+//   POW2 (ref_block_v1.py:167,193,198,218): fl32(acc) * 2^-(shift + erow[m] + ecol[n]), exact.
+struct EpiParams {
+  int order;                 // lsk_epilogue
+  int out_dtype;             // lsk_dtype
+  const float* ws;           // [N]
+  const float* asc;          // [M] (indexed by the logical output row)
+  const float* bias;         // [N] or null
+  const int32_t* erow;       // [M] or null (POW2)
+  const int32_t* ecol;       // [N] or null (POW2)
+  int shift;                 // POW2 scalar
+  void* out;
+  int64_t ldo;               // elements
+};
+
+LSK_DEV void epilogue_store(const EpiParams& p, int64_t m, int64_t n, int32_t acc) {
+  const int64_t o = m * p.ldo + n;
+  if (p.order == LSK_EPI_RAW) {
+    ((int32_t*)p.out)[o] = acc;
+    return;
+  }
+  const float v = (float)acc;  // int32 -> binary32, round to nearest even
+  if (p.order == LSK_EPI_V21) {
+    float y = f32_mul(f32_mul(v, p.ws[n]), p.asc[m]);
+    if (p.bias) {
+      y = round_out(p.out_dtype, y);
+      y = f32_add(y, p.bias[n]);
+    }
+    store_out(p.out, p.out_dtype, o, y);
+  } else if (p.order == LSK_EPI_V2) {
+    float y = f32_mul(f32_mul(v, p.asc[m]), p.ws[n]);
+    if (p.bias) y = f32_add(y, p.bias[n]);
+    store_out(p.out, p.out_dtype, o, y);
+  } else {  // LSK_EPI_POW2
+    int s = p.shift;
+    if (p.erow) s += p.erow[m];
+    if (p.ecol) s += p.ecol[n];
+    float y = f32_mul(v, pow2f(-s));
+    store_out(p.out, p.out_dtype, o, y);
+  }
+}
+
+// Thread-local last-error string shared by every entry point.
+namespace lsk {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace lsk
+
+#define LSK_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      lsk::set_error(__VA_ARGS__);    \
+      return LSK_ERR_ARG;             \
+    }                                 \
+  } while (0)

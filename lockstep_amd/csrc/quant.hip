@@ -1,0 +1,245 @@
+// Activation quantisers: the contract's per-row int8 quant (true-division scale) and the
+// power-of-two quantisers of the golden training block.
+#include "lsk_common.h"
+
+namespace {
+
+constexpr float kAmaxFloor = 0x1.5798eep-27f;  // binary32 nearest 1e-8 (torch clamp(min=1e-8))
+
+// Block-wide max of non-negative floats; every thread gets the result.
+template <int THREADS>
+LSK_DEV float block_max(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < THREADS / 64; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+LSK_DEV int8_t quant_one(float v, float s) {
+  float t = rintf(f32_div(v, s));  // fl32(x / asc), then round half to even
+  t = fminf(fmaxf(t, -127.0f), 127.0f);
+  return (int8_t)(int)t;
+}
+
+// One block per row.  Pass 1: amax over the row (exact, order-free).  Pass 2: quantise.
+// Vector path: 8 elements per thread-step when the row is 16-byte aligned and K % 8 == 0.
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void rowquant_kernel(const void* __restrict__ x, int dtype,
+                                                           int64_t K, int64_t ldx,
+                                                           int8_t* __restrict__ q, int64_t ldq,
+                                                           float* __restrict__ asc, int vec) {
+  __shared__ float red[THREADS / 64];
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t base = m * ldx;
+  float am = 0.0f;
+  if (vec) {
+    const int64_t K8 = K >> 3;
+    for (int64_t c = tid; c < K8; c += THREADS) {
+      if (dtype == LSK_F32) {
+        const float4* p = (const float4*)((const float*)x + base) + 2 * c;
+        float4 a = p[0], b = p[1];
+        am = fmaxf(am, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        am = fmaxf(am, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+      } else {
+        const uint4 u = ((const uint4*)((const uint16_t*)x + base))[c];
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float lo, hi;
+          if (dtype == LSK_BF16) {
+            lo = bf16_to_f32((uint16_t)(w[j] & 0xffff));
+            hi = bf16_to_f32((uint16_t)(w[j] >> 16));
+          } else {
+            lo = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffff));
+            hi = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+          }
+          am = fmaxf(am, fmaxf(fabsf(lo), fabsf(hi)));
+        }
+      }
+    }
+  } else {
+    for (int64_t k = tid; k < K; k += THREADS) am = fmaxf(am, fabsf(load_as_f32(x, dtype, base + k)));
+  }
+  am = block_max<THREADS>(am, red);
+  am = fmaxf(am, kAmaxFloor);
+  const float s = f32_div(am, 127.0f);
+  if (tid == 0) asc[m] = s;
+  int8_t* qrow = q + m * ldq;
+  if (vec) {
+    const int64_t K8 = K >> 3;
+    for (int64_t c = tid; c < K8; c += THREADS) {
+      float v[8];
+      if (dtype == LSK_F32) {
+        const float4* p = (const float4*)((const float*)x + base) + 2 * c;
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      } else {
+        const uint4 u = ((const uint4*)((const uint16_t*)x + base))[c];
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (dtype == LSK_BF16) {
+            v[2 * j] = bf16_to_f32((uint16_t)(w[j] & 0xffff));
+            v[2 * j + 1] = bf16_to_f32((uint16_t)(w[j] >> 16));
+          } else {
+            v[2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffff));
+            v[2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+          }
+        }
+      }
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lo |= ((uint32_t)(uint8_t)quant_one(v[j], s)) << (8 * j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hi |= ((uint32_t)(uint8_t)quant_one(v[4 + j], s)) << (8 * j);
+      ((uint2*)qrow)[c] = make_uint2(lo, hi);
+    }
+  } else {
+    for (int64_t k = tid; k < K; k += THREADS) qrow[k] = quant_one(load_as_f32(x, dtype, base + k), s);
+  }
+}
+
+// ---------------------------------------------------------------- power-of-two quantisers
+// e = 6 - (biased_exp(m) - 127); e -= 1 if fl32(m * 2^e) > 127; e = 0 where m == 0; clip [-32, 40]
+LSK_DEV int pow2_exponent(float m) {
+  if (m == 0.0f) return 0;
+  int e = 6 - ((int)(__float_as_uint(m) >> 23) - 127);
+  // The decrement can change the clipped result only for e in [-31, 40]; there 2^e is a
+  // normal binary32 and m * 2^e is exact (a power-of-two scaling of a normal number).
+  if (e >= -31 && e <= 40 && f32_mul(m, pow2f(e)) > 127.0f) e -= 1;
+  return e < -32 ? -32 : (e > 40 ? 40 : e);
+}
+
+LSK_DEV int8_t quant_pow2_one(float v, float scale) {
+  float t = rintf(f32_mul(v, scale));
+  t = fminf(fmaxf(t, -127.0f), 127.0f);
+  return (int8_t)(int)t;
+}
+
+// |x| max over the whole tensor as order-free integer atomics on the float bits.
+__global__ __launch_bounds__(256) void amax_all_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                       int64_t ldx, uint32_t* __restrict__ out) {
+  __shared__ float red[4];
+  float am = 0.0f;
+  const int64_t total = M * K;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / K, c = i - r * K;
+    am = fmaxf(am, fabsf(x[r * ldx + c]));
+  }
+  am = block_max<256>(am, red);
+  if (threadIdx.x == 0) atomicMax(out, __float_as_uint(am));
+}
+
+__global__ __launch_bounds__(256) void amax_cols_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                        int64_t ldx, uint32_t* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= K) return;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, r1 = r0 + 64 < M ? r0 + 64 : M;
+  float am = 0.0f;
+  for (int64_t r = r0; r < r1; ++r) am = fmaxf(am, fabsf(x[r * ldx + c]));
+  atomicMax(out + c, __float_as_uint(am));
+}
+
+// mode 0: tensor exponent from amax_bits[0]; mode 2: column exponents from amax_bits[K]
+__global__ __launch_bounds__(256) void quant_pow2_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                         int64_t ldx, int mode,
+                                                         const uint32_t* __restrict__ amax_bits,
+                                                         int8_t* __restrict__ q, int64_t ldq,
+                                                         int32_t* __restrict__ e_out) {
+  const int64_t total = M * K;
+  if (mode == 0 && blockIdx.x == 0 && threadIdx.x == 0) e_out[0] = pow2_exponent(__uint_as_float(amax_bits[0]));
+  if (mode == 2) {
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < K; c += (int64_t)gridDim.x * 256)
+      e_out[c] = pow2_exponent(__uint_as_float(amax_bits[c]));
+  }
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / K, c = i - r * K;
+    const float m = __uint_as_float(amax_bits[mode == 0 ? 0 : c]);
+    const float v = x[r * ldx + c];
+    int8_t qq = 0;
+    if (!(mode == 0 && m == 0.0f)) qq = quant_pow2_one(v, pow2f(pow2_exponent(m)));
+    q[r * ldq + c] = qq;
+  }
+}
+
+__global__ __launch_bounds__(256) void quant_pow2_rows_kernel(const float* __restrict__ x, int64_t K, int64_t ldx,
+                                                              int8_t* __restrict__ q, int64_t ldq,
+                                                              int32_t* __restrict__ e_out) {
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  float am = 0.0f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) am = fmaxf(am, fabsf(x[m * ldx + k]));
+  am = block_max<256>(am, red);
+  const int e = pow2_exponent(am);
+  if (threadIdx.x == 0) e_out[m] = e;
+  const float sc = pow2f(e);
+  for (int64_t k = threadIdx.x; k < K; k += 256) q[m * ldq + k] = quant_pow2_one(x[m * ldx + k], sc);
+}
+
+}  // namespace
+
+extern "C" int lsk_rowquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q,
+                            int64_t ldq, float* asc, void* stream) {
+  LSK_REQUIRE(M >= 0 && K >= 0, "lsk_rowquant: negative size M=%lld K=%lld", (long long)M, (long long)K);
+  LSK_REQUIRE(x_dtype == LSK_F32 || x_dtype == LSK_BF16 || x_dtype == LSK_F16,
+              "lsk_rowquant: x_dtype %d not one of f32/bf16/f16", x_dtype);
+  if (M == 0) return LSK_OK;
+  LSK_REQUIRE(x && q && asc, "lsk_rowquant: null pointer");
+  LSK_REQUIRE(ldx >= K && ldq >= K, "lsk_rowquant: ldx=%lld / ldq=%lld below K=%lld", (long long)ldx,
+              (long long)ldq, (long long)K);
+  LSK_REQUIRE(M <= 0x7fffffff, "lsk_rowquant: M=%lld exceeds the grid", (long long)M);
+  const int esz = x_dtype == LSK_F32 ? 4 : 2;
+  const int vec = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
+                  ((uintptr_t)q % 8 == 0) && ((ldx * esz) % 16 == 0);
+  hipLaunchKernelGGL(rowquant_kernel<256>, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, x, x_dtype, K,
+                     ldx, q, ldq, asc, vec);
+  return lsk::check_launch("rowquant_kernel");
+}
+
+extern "C" int lsk_quant8_pow2(const float* x, int64_t M, int64_t K, int64_t ldx, int mode, int8_t* q,
+                               int64_t ldq, int32_t* e_out, void* workspace, void* stream) {
+  LSK_REQUIRE(M >= 0 && K >= 0, "lsk_quant8_pow2: negative size");
+  LSK_REQUIRE(mode >= 0 && mode <= 2, "lsk_quant8_pow2: mode %d not in {0,1,2}", mode);
+  LSK_REQUIRE(ldx >= K && ldq >= K, "lsk_quant8_pow2: leading dimension below K");
+  hipStream_t s = (hipStream_t)stream;
+  if (mode == 1) {
+    if (M == 0) return LSK_OK;
+    LSK_REQUIRE(M <= 0x7fffffff, "lsk_quant8_pow2: M too large");
+    hipLaunchKernelGGL(quant_pow2_rows_kernel, dim3((unsigned)M), dim3(256), 0, s, x, K, ldx, q, ldq, e_out);
+    return lsk::check_launch("quant_pow2_rows_kernel");
+  }
+  LSK_REQUIRE(workspace, "lsk_quant8_pow2: workspace required");
+  uint32_t* amax = (uint32_t*)workspace;
+  const int64_t nam = mode == 0 ? 1 : K;
+  if (nam > 0) {
+    if (hipMemsetAsync(amax, 0, nam * sizeof(uint32_t), s) != hipSuccess) {
+      lsk::set_error("lsk_quant8_pow2: hipMemsetAsync failed");
+      return LSK_ERR_HIP;
+    }
+  }
+  if (M > 0 && K > 0) {
+    if (mode == 0) {
+      const int64_t total = M * K;
+      int64_t blocks = (total + 255) / 256;
+      if (blocks > 4096) blocks = 4096;
+      hipLaunchKernelGGL(amax_all_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, amax);
+    } else {
+      dim3 g((unsigned)((K + 255) / 256), (unsigned)((M + 63) / 64));
+      hipLaunchKernelGGL(amax_cols_kernel, g, dim3(256), 0, s, x, M, K, ldx, amax);
+    }
+    int rc = lsk::check_launch("amax kernel");
+    if (rc) return rc;
+  }
+  int64_t blocks = (M * K + 255) / 256;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(quant_pow2_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, mode, amax, q, ldq,
+                     e_out);
+  return lsk::check_launch("quant_pow2_kernel");
+}

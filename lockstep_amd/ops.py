@@ -1,0 +1,135 @@
+"""Torch-level wrappers over the C ABI: shape / dtype / stride handling, output allocation.
+
+These are the building blocks of the drop-in modules (`lockstep_fullstack`, `moe_ref`,
+`contract_common`, `ref_block_v1`, `moe_mxfp4`), which keep the reference's signatures.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib as L
+
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    """x [..., K] -> a 2-D view/copy [rows, K] with unit stride along K."""
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.shape[-1] > 0 and x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2
+
+
+def weight_nk(b8: torch.Tensor) -> torch.Tensor:
+    """The reference passes weights as b8 [K, N] = W8.t() of a row-major W8 [N, K].  Return
+    W8 [N, K] with unit stride along K: a free view when b8 is that transpose, else a copy."""
+    w = b8.t()
+    if w.shape[-1] > 0 and w.stride(-1) != 1:
+        w = w.contiguous()
+    return w
+
+
+def _f32(t):
+    if t is None:
+        return None
+    t = t.to(torch.float32)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def rowquant(x: torch.Tensor):
+    """Per-row int8 quant of x [..., K] (f32 / bf16 / f16; other float dtypes go through f32).
+    Returns (q int8 [..., K], asc f32 [...])."""
+    L.require_cuda(x, what="rowquant")
+    if x.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        x = x.to(torch.float32)
+    lead = x.shape[:-1]
+    K = x.shape[-1]
+    x2 = _rows(x)
+    M = x2.shape[0]
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    asc = torch.empty((M,), dtype=torch.float32, device=x.device)
+    L.call("lsk_rowquant", L.ptr(x2), L.dtype_code(x2.dtype), M, K, x2.stride(0) if M else K,
+           L.ptr(q), K, L.ptr(asc), L.stream_of(x))
+    return q.reshape(*lead, K), asc.reshape(lead)
+
+
+def gemm(a8: torch.Tensor, w_nk: torch.Tensor, order: int, out_dtype: int, asc=None, ws=None, bias=None,
+         erow=None, ecol=None, shift: int = 0, out: torch.Tensor = None) -> torch.Tensor:
+    """Exact GEMM a8 [M, K] x w_nk [N, K]^T with the given epilogue, out [M, N]."""
+    L.require_cuda(a8, w_nk, asc, ws, bias, erow, ecol, what="gemm")
+    if a8.dtype != torch.int8 or w_nk.dtype != torch.int8:
+        raise TypeError("gemm: int8 operands required, got %s x %s" % (a8.dtype, w_nk.dtype))
+    M, K = a8.shape
+    N, K2 = w_nk.shape
+    if K != K2:
+        raise ValueError("gemm: K mismatch %d vs %d" % (K, K2))
+    a8 = a8 if (K == 0 or a8.stride(-1) == 1) else a8.contiguous()
+    tdt = {L.LSK_F32: torch.float32, L.LSK_BF16: torch.bfloat16, L.LSK_F16: torch.float16,
+           L.LSK_I32: torch.int32, L.LSK_BF16_AS_F32: torch.float32}[out_dtype]
+    if out is None:
+        out = torch.empty((M, N), dtype=tdt, device=a8.device)
+    asc, ws, bias = _f32(asc), _f32(ws), _f32(bias)
+    erow = None if erow is None else erow.to(torch.int32).contiguous()
+    ecol = None if ecol is None else ecol.to(torch.int32).contiguous()
+    if M and N:
+        L.call("lsk_gemm_w8a8", L.ptr(a8), a8.stride(0) if M > 1 else max(K, 1), L.ptr(w_nk),
+               w_nk.stride(0) if N > 1 else max(K, 1), M, N, K, order, L.ptr(asc), L.ptr(ws), L.ptr(bias),
+               L.ptr(erow), L.ptr(ecol), int(shift), L.ptr(out), out_dtype, out.stride(0), L.stream_of(a8))
+    return out
+
+
+def epilogue(acc: torch.Tensor, order: int, out_dtype: int, asc=None, ws=None, bias=None,
+             erow=None, ecol=None, shift: int = 0) -> torch.Tensor:
+    """The contract epilogue over an existing int32 accumulator [M, N]."""
+    L.require_cuda(acc, asc, ws, bias, erow, ecol, what="epilogue")
+    if acc.dtype != torch.int32:
+        acc = acc.to(torch.int32)
+    acc = acc if acc.is_contiguous() else acc.contiguous()
+    M, N = acc.shape
+    tdt = {L.LSK_F32: torch.float32, L.LSK_BF16: torch.bfloat16, L.LSK_F16: torch.float16,
+           L.LSK_BF16_AS_F32: torch.float32}[out_dtype]
+    out = torch.empty((M, N), dtype=tdt, device=acc.device)
+    asc, ws, bias = _f32(asc), _f32(ws), _f32(bias)
+    erow = None if erow is None else erow.to(torch.int32).contiguous()
+    ecol = None if ecol is None else ecol.to(torch.int32).contiguous()
+    if M and N:
+        L.call("lsk_epilogue_apply", L.ptr(acc), N, M, N, order, L.ptr(asc), L.ptr(ws), L.ptr(bias),
+               L.ptr(erow), L.ptr(ecol), int(shift), L.ptr(out), out_dtype, N, L.stream_of(acc))
+    return out
+
+
+def w8a8_matmul(x2: torch.Tensor, w_nk: torch.Tensor, ws: torch.Tensor, bias, order: int,
+                out_dtype: int) -> torch.Tensor:
+    """Row quant + exact GEMM + epilogue in two launches, x2 [M, K] -> [M, N]."""
+    L.require_cuda(x2, w_nk, ws, bias, what="w8a8_matmul")
+    if x2.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        x2 = x2.to(torch.float32)
+    x2 = _rows(x2)
+    M, K = x2.shape
+    N = w_nk.shape[0]
+    tdt = {L.LSK_F32: torch.float32, L.LSK_BF16: torch.bfloat16, L.LSK_F16: torch.float16,
+           L.LSK_BF16_AS_F32: torch.float32}[out_dtype]
+    out = torch.empty((M, N), dtype=tdt, device=x2.device)
+    if M == 0 or N == 0:
+        return out
+    nbytes = L.load().lsk_w8a8_matmul_workspace(M, K)
+    ws_buf = torch.empty((nbytes,), dtype=torch.uint8, device=x2.device)
+    ws, bias = _f32(ws), _f32(bias)
+    L.call("lsk_w8a8_matmul", L.ptr(x2), L.dtype_code(x2.dtype), x2.stride(0) if M > 1 else max(K, 1), M, K,
+           L.ptr(w_nk), w_nk.stride(0) if N > 1 else max(K, 1), N, L.ptr(ws), L.ptr(bias), order, L.ptr(out),
+           out_dtype, N, L.ptr(ws_buf), nbytes, L.stream_of(x2))
+    return out
+
+
+def quant8_pow2(x: torch.Tensor, mode: int):
+    """Power-of-two quant of x [M, K] binary32: mode 0 tensor, 1 rows, 2 columns.
+    Returns (q int8 [M, K], e int32 [1] / [M] / [K])."""
+    L.require_cuda(x, what="quant8_pow2")
+    x = x.to(torch.float32)
+    x = x if x.is_contiguous() else x.contiguous()
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    ne = {0: 1, 1: M, 2: K}[mode]
+    e = torch.zeros((max(ne, 1),), dtype=torch.int32, device=x.device)
+    work = torch.empty((4 * (M + K + 64),), dtype=torch.uint8, device=x.device)
+    L.call("lsk_quant8_pow2", L.ptr(x), M, K, max(K, 1), mode, L.ptr(q), max(K, 1), L.ptr(e), L.ptr(work),
+           L.stream_of(x))
+    return q, e[:ne]

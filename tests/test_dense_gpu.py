@@ -1,0 +1,245 @@
+"""GPU parity of the dense contract path: bit equality with the oracle (and, through it, with
+the reference's published conformance digests) on seeded inputs and edge shapes."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_dev, bits, dev, f16_bits, f32_bits, say, to_dev
+from oracle import contract as C
+from vector_inputs import linear_inputs, load_vectors
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import lockstep_amd._lib as L
+    L.load()
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ------------------------------------------------------------------ the published vectors
+def test_conformance_vectors_on_gpu():
+    from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import moe_ref as MR
+    V = load_vectors()
+    _, x, W, bias = linear_inputs()
+    xd = bf16_dev(x)
+    q, asc = FS.quantize_rows_int8(xd.float())
+    assert C.digest(bits(q), "int8") == V["act_quant.q"]["sha256"]
+    assert C.digest(bits(asc).view(F32), "float32") == V["act_quant.asc"]["sha256"]
+    W8, ws = FS.quantize_weight_int8(bf16_dev(W))
+    assert C.digest(bits(W8), "int8") == V["weight_quant.w8"]["sha256"]
+    assert C.digest(bits(ws).view(F32), "float32") == V["weight_quant.ws"]["sha256"]
+    bd = to_dev(bias)
+    y = FS.w8a8_matmul(xd, W8, ws, None, out_dtype=torch.bfloat16)
+    assert C.digest(bits(y), "bfloat16") == V["linear.v2_1.no_bias"]["sha256"]
+    yb = FS.w8a8_matmul(xd, W8, ws, bd, out_dtype=torch.bfloat16)
+    assert C.digest(bits(yb), "bfloat16") == V["linear.v2_1.bias"]["sha256"]
+    # moe_ref's separate int_mm + lin_epilogue(_b), and the fused form
+    q2, asc2 = MR.rowquant(xd)
+    acc = MR.int_mm(q2, W8.t())
+    y2 = MR.lin_epilogue(acc, ws, asc2).to(torch.bfloat16)
+    assert C.digest(bits(y2), "bfloat16") == V["linear.v2_1.no_bias"]["sha256"]
+    y3 = MR.lin_epilogue_b(acc, ws, asc2, bd).to(torch.bfloat16)
+    assert C.digest(bits(y3), "bfloat16") == V["linear.v2_1.bias"]["sha256"]
+    y4 = MR.linear(q2, asc2, W8.t(), ws, bd).to(torch.bfloat16)
+    assert C.digest(bits(y4), "bfloat16") == V["linear.v2_1.bias"]["sha256"]
+
+
+# ------------------------------------------------------------------ row quant
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(1, 16), (3, 37), (7, 512), (33, 4096), (2, 18944), (0, 64)])
+def test_rowquant_parity(dtype, shape):
+    from lockstep_amd import moe_ref as MR
+    say("rowquant", dtype, shape)
+    r = _rng(hash((str(dtype), shape)) % 2**32)
+    x = (r.standard_normal(shape) * 3).astype(F32)
+    if shape[0] > 2:
+        x[1] = 0.0
+        x[2, :3] = [1e-30, -1e-40, 0.5]
+    xt = torch.from_numpy(x).to(dtype)
+    xr = xt.float().numpy()                      # the values the reference sees after .float()
+    q, asc = MR.rowquant(xt.to(dev()))
+    qo, asco = C.rowquant(xr)
+    assert np.array_equal(bits(q), qo)
+    assert np.array_equal(bits(asc), f32_bits(asco))
+
+
+# ------------------------------------------------------------------ exact GEMM
+GEMM_SHAPES = [
+    (1, 1, 16), (1, 17, 64), (5, 16, 128), (16, 33, 144), (17, 64, 512), (31, 100, 2880),
+    (32, 256, 4096), (33, 130, 256), (64, 64, 64), (127, 255, 1024), (128, 128, 128),
+    (129, 257, 640), (300, 1000, 2048), (16, 3584, 3584),
+]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_int_mm_parity(M, N, K):
+    from lockstep_amd import moe_ref as MR
+    say("int_mm", M, N, K)
+    r = _rng(M * 1000003 + N * 1009 + K)
+    a = r.integers(-127, 128, (M, K), dtype=np.int8)
+    w = r.integers(-127, 128, (N, K), dtype=np.int8)
+    acc = MR.int_mm(to_dev(a), to_dev(w).t())
+    assert np.array_equal(bits(acc), C.int_mm(a, w.T))
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 5, 7), (4, 9, 100), (17, 3, 33), (2, 2, 0)])
+def test_int_mm_generic_path(M, N, K):
+    """K not a multiple of 16 and K == 0 take the generic kernel; results stay exact."""
+    from lockstep_amd import moe_ref as MR
+    r = _rng(M + N + K)
+    a = r.integers(-127, 128, (M, K), dtype=np.int8)
+    w = r.integers(-127, 128, (N, K), dtype=np.int8)
+    acc = MR.int_mm(to_dev(a), to_dev(w).t())
+    assert np.array_equal(bits(acc), C.int_mm(a, w.T) if K else np.zeros((M, N), np.int32))
+
+
+def test_int_mm_extremes_and_strided_operands():
+    from lockstep_amd import moe_ref as MR
+    K = 18944
+    a = np.full((3, K), -127, np.int8)
+    a[1] = 127
+    w = np.full((20, K), 127, np.int8)
+    acc = MR.int_mm(to_dev(a), to_dev(w).t())
+    assert np.array_equal(bits(acc), C.int_mm(a, w.T))
+    assert int(bits(acc)[0, 0]) == -K * 127 * 127
+    # a [K, N] weight that is NOT the transpose of a row-major [N, K]: copied, same result
+    r = _rng(99)
+    a = r.integers(-127, 128, (40, 96), dtype=np.int8)
+    b = r.integers(-127, 128, (96, 50), dtype=np.int8)
+    acc = MR.int_mm(to_dev(a), to_dev(b))
+    assert np.array_equal(bits(acc), C.int_mm(a, b))
+
+
+# ------------------------------------------------------------------ epilogues
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (8, 100, 512), (32, 48, 1024), (200, 300, 768)])
+@pytest.mark.parametrize("use_bias", [False, True])
+@pytest.mark.parametrize("out", ["bf16", "f32", "f16"])
+def test_w8a8_matmul_parity(M, N, K, use_bias, out):
+    from lockstep_amd import lockstep_fullstack as FS
+    say("w8a8_matmul", M, N, K, use_bias, out)
+    r = _rng(M * 7 + N * 11 + K * 13 + use_bias)
+    x = (r.standard_normal((M, K)) * 2).astype(F32)
+    x[r.random((M, K)) < 0.001] = 20.0
+    xb = C.bfr(x)
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    bias = (r.standard_normal(N) * 0.1).astype(F32) if use_bias else None
+    tdt = {"bf16": torch.bfloat16, "f32": torch.float32, "f16": torch.float16}[out]
+    y = FS.w8a8_matmul(bf16_dev(xb), to_dev(W8), to_dev(ws), to_dev(bias) if use_bias else None, out_dtype=tdt)
+    ref = C.w8a8_matmul(xb, W8, ws, bias, out)
+    if out == "f16":
+        ref = f16_bits(ref)
+    elif out == "f32":
+        ref = f32_bits(ref)
+    assert np.array_equal(bits(y), ref)
+
+
+def test_w8a8_matmul_fp32_input_and_zero_rows():
+    from lockstep_amd import lockstep_fullstack as FS
+    r = _rng(5)
+    x = r.standard_normal((2, 3, 256)).astype(F32)
+    W8 = r.integers(-127, 128, (40, 256), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, 40).astype(F32)
+    y = FS.w8a8_matmul(to_dev(x), to_dev(W8), to_dev(ws))          # fp32 in, fp32 out, no rounding
+    assert y.shape == (2, 3, 40) and y.dtype == torch.float32
+    ref = C.w8a8_matmul(x.reshape(6, 256), W8, ws, None, "f32")
+    assert np.array_equal(bits(y).reshape(6, 40), f32_bits(ref))
+    z = FS.w8a8_matmul(to_dev(np.zeros((0, 256), F32)), to_dev(W8), to_dev(ws), out_dtype=torch.bfloat16)
+    assert z.shape == (0, 40) and z.dtype == torch.bfloat16
+
+
+def test_w8a8_linear_v2_order():
+    from lockstep_amd import contract_common as CC
+    r = _rng(6)
+    lin = torch.nn.Linear(384, 72, bias=True).to(dev()).to(torch.bfloat16)
+    Wf = lin.weight.data.float().cpu().numpy()
+    bias = lin.bias.data.float().cpu().numpy()
+    x = C.bfr((r.standard_normal((9, 384)) * 2).astype(F32))
+    CC.w8a8_linear(lin)
+    y = lin(bf16_dev(x))
+    W8, ws = C.w8a8_linear_prepare(Wf)
+    ref = C.w8a8_linear_fwd(x, W8, ws, bias, "bf16")
+    assert y.dtype == torch.bfloat16
+    assert np.array_equal(bits(y), ref)
+
+
+# ------------------------------------------------------------------ pow2 (ref_block_v1)
+def test_pow2_quant_and_gemm_parity():
+    from lockstep_amd import ref_block_v1 as RB
+    r = _rng(7)
+    x = (r.standard_normal((64, 512)) * 3).astype(F32)
+    Wt = (r.standard_normal((512, 192)) * 0.05).astype(F32)   # [K, N] as the block's weights
+    qx, ex = RB.quant8_dyn(x)
+    qo, eo = C.quant8_dyn(x)
+    assert ex == eo and np.array_equal(qx, qo)
+    qw, ew = RB.quant8_dyn(Wt)
+    qwo, ewo = C.quant8_dyn(Wt)
+    assert ew == ewo and np.array_equal(qw, qwo)
+    acc = RB.gemm_int(qx, qw)
+    assert np.array_equal(acc, C.gemm_int(qo, qwo))
+    y = RB.gemm_pow2(qx, ex, qw, ew)
+    assert np.array_equal(f32_bits(y), f32_bits(C.dequant_pow2(C.gemm_int(qo, qwo), eo + ewo)))
+    qr, er = RB.quant8_rows(x)
+    qro, ero = C.quant8_rows(x)
+    assert np.array_equal(qr, qro) and np.array_equal(er, ero)
+    qc, ec = RB.quant8_cols(Wt)
+    qco, eco = C.quant8_cols(Wt)
+    assert np.array_equal(qc, qco) and np.array_equal(ec, eco)
+    y2 = RB.gemm_pow2(qr, er, qc, ec)
+    ref2 = C.dequant_pow2(C.gemm_int(qro, qco), ero[:, None] + eco[None, :])
+    assert np.array_equal(f32_bits(y2), f32_bits(ref2))
+    assert RB.quant8_dyn(np.zeros((3, 4), F32))[1] == 0
+    em = np.array([0.0, 127.0, 127.5, 1e-30, 3e38, 1e-40, 64.0], F32)
+    assert np.array_equal(RB._e_from_max(em), C._e_from_max(em))
+
+
+# ------------------------------------------------------------------ the dense configurations
+def test_config1_o_proj_m16_bit_exact():
+    """M=16 tokens, K=N=3584: x N(0,1) seed 0 quantised by the contract quantiser, W8 uniform
+    [-127, 127], ws U(1e-3, 1e-2), bf16 output."""
+    from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import workloads as WL
+    x, W8, ws = WL.dense_inputs(16, 3584, 3584, seed=0)
+    y = FS.w8a8_matmul(to_dev(x), to_dev(W8), to_dev(ws), out_dtype=torch.bfloat16)
+    assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, None, "bf16"))
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+@pytest.mark.parametrize("which", ["gate_up", "down"])
+def test_config2_decode_bit_exact(M, which):
+    from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import workloads as WL
+    N, K = WL.LLAMA8B[which]
+    say("config2 decode", which, M, N, K)
+    x, W8, ws = WL.dense_inputs(M, N, K, seed=1, outliers=True)
+    y = FS.w8a8_matmul(to_dev(x), to_dev(W8), to_dev(ws), out_dtype=torch.bfloat16)
+    assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, None, "bf16"))
+
+
+@pytest.mark.parametrize("which", ["gate_up", "down"])
+def test_config2_prefill_rows_and_chunk_invariance(which):
+    """M=2048: a seeded subset of rows against the oracle, and the whole result equal to the
+    same rows computed in 64-row chunks (row independence: per-token scales, exact sums)."""
+    from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import workloads as WL
+    N, K = WL.LLAMA8B[which]
+    M = 2048
+    say("config2 prefill", which, M, N, K)
+    x, W8, ws = WL.dense_inputs(M, N, K, seed=2, outliers=True)
+    xd, Wd, wsd = to_dev(x), to_dev(W8), to_dev(ws)
+    y = FS.w8a8_matmul(xd, Wd, wsd, out_dtype=torch.bfloat16)
+    rows = np.sort(_rng(3).choice(M, 24, replace=False))
+    ref = C.w8a8_matmul(x[rows], W8, ws, None, "bf16")
+    assert np.array_equal(bits(y)[rows], ref)
+    chunks = torch.cat([FS.w8a8_matmul(xd[i:i + 64], Wd, wsd, out_dtype=torch.bfloat16) for i in range(0, M, 64)])
+    assert torch.equal(chunks.view(torch.int16), y.view(torch.int16))
