@@ -97,6 +97,13 @@ int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
                     int order, void* out, int out_dtype, int64_t ldo,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Tuning control with no counterpart in the reference: force the dense prefill tile
+ * (0: 256x256 tile, 4 waves of 128x128; 1: 256x128, 4 waves of 128x64; 2: 128x128, 4 waves
+ * of 64x64; 3: 256x256, 8 waves of 64x128; 4: 128x256, 4 waves of 64x128) or -1 to choose by
+ * shape (the default).  Results are identical for every choice; only speed differs.
+ * Process-wide, not thread-safe against concurrent launches. */
+int lsk_gemm_select(int tile_id);
+
 /* Power-of-two int8 quantisation of ref_block_v1 (reference/ref_block_v1.py:56-72,122-130).
  * mode 0 = per tensor (quant8_dyn: one exponent e_out[0]); 1 = per row (quant8_rows: e_out[M]);
  * 2 = per column (quant8_cols: e_out[K]).  e = 6 - (biased_exp(m) - 127), minus 1 when

@@ -34,6 +34,7 @@ SIGNATURES = {
     "lsk_epilogue_apply": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I64, _P]),
     "lsk_w8a8_matmul_workspace": (_I64, [_I64, _I64]),
     "lsk_w8a8_matmul": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P, _I64, _P]),
+    "lsk_gemm_select": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
 }
 

@@ -8,136 +8,69 @@
 //
 // Integer accumulation is exact in any order (|acc| <= K * 127^2 < 2^31 for K <= 133144), so
 // tiling and K-splits never change a bit; the epilogue is applied once per output element.
-#include "lsk_common.h"
+#include "mfma_tile.h"
 
 namespace {
 
-constexpr int kBK = 128;  // bytes of K per LDS stage (8 chunks of 16 B per row)
+using lsk::zero4;
 
-LSK_DEV v4i mfma16(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
-
-LSK_DEV v4i zero4() { return v4i{0, 0, 0, 0}; }
-
-// Map a hardware block id to a logical tile id so that the blocks one XCD runs (hardware ids
-// congruent mod 8) form one contiguous run of logical ids, then walk logical ids M-fastest
-// inside groups of `gm` M-tiles: tiles that run together share weight and activation panels
-// in the XCD's own L2.
-LSK_DEV void tile_coords(int nblocks, int mtiles, int ntiles, int gm, int& mt, int& nt) {
-  const int b = blockIdx.x;
-  const int per = nblocks / 8, rem = nblocks % 8;
-  const int x = b % 8, i = b / 8;
-  const int L = x * per + (x < rem ? x : rem) + i;
-  const int group = L / (gm * ntiles);
-  const int first_m = group * gm;
-  const int gsize = (mtiles - first_m) < gm ? (mtiles - first_m) : gm;
-  const int r = L - group * gm * ntiles;
-  mt = first_m + r % gsize;
-  nt = r / gsize;
-}
-
-template <int BM, int BN, int WM, int WN>
-struct Cfg {
-  static constexpr int kThreads = WM * WN * 64;
-  static constexpr int WTM = BM / WM, WTN = BN / WN;
-  static constexpr int TM = WTM / 16, TN = WTN / 16;
-  static constexpr int kAChunks = BM * kBK / 16, kBChunks = BN * kBK / 16;
-  static constexpr int kAPer = kAChunks / kThreads, kBPer = kBChunks / kThreads;
-  static_assert(kAChunks % kThreads == 0 && kBChunks % kThreads == 0, "tile/threads mismatch");
-  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be a multiple of 16");
-};
-
-// C[m, n] = sum_k A[m, k] * W[n, k]; A and W K-contiguous, K % 16 == 0, 16-byte aligned rows.
+// Dense tile kernel: C[m, n] = sum_k A[m, k] * W[n, k] with the epilogue applied per element.
+// A and W are K-contiguous with 16-byte aligned rows and K % 16 == 0.  Logical tile ids walk
+// M-fastest inside groups of 16 M-tiles after the XCD remap.
 template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
     const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ W, int64_t ldw, int M, int N, int K,
-    EpiParams ep) {
-  using C = Cfg<BM, BN, WM, WN>;
-  __shared__ v4i sA[2][BM * 8];
-  __shared__ v4i sB[2][BN * 8];
-
+    EpiParams ep, int vec_ok) {
+  using C = lsk::TileCfg<BM, BN, WM, WN>;
+  extern __shared__ v4i smem[];
   const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN;
-  int mt, nt;
-  tile_coords(mtiles * ntiles, mtiles, ntiles, 16, mt, nt);
-  const int m0 = mt * BM, n0 = nt * BN;
+  const int L = lsk::xcd_logical_id(blockIdx.x, mtiles * ntiles);
+  constexpr int GM = 16;
+  const int group = L / (GM * ntiles);
+  const int first_m = group * GM;
+  const int gsize = (mtiles - first_m) < GM ? (mtiles - first_m) : GM;
+  const int r = L - group * GM * ntiles;
+  const int m0 = (first_m + r % gsize) * BM, n0 = (r / gsize) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-
-  v4i acc[C::TM][C::TN];
+  typename C::RowsA pa;
+  typename C::RowsB pb;
+#pragma unroll
+  for (int j = 0; j < C::kAPer; ++j) {
+    int row, c;
+    lsk::chunk_of<C::kThreads>(tid, j, row, c);
+    pa[j] = (m0 + row < M) ? A + (int64_t)(m0 + row) * lda : nullptr;
+  }
+#pragma unroll
+  for (int j = 0; j < C::kBPer; ++j) {
+    int row, c;
+    lsk::chunk_of<C::kThreads>(tid, j, row, c);
+    pb[j] = (n0 + row < N) ? W + (int64_t)(n0 + row) * ldw : nullptr;
+  }
+  typename C::Acc acc;
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = zero4();
 
-  v4i ra[C::kAPer], rb[C::kBPer];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int j = 0; j < C::kAPer; ++j) {
-      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
-      const int gm = m0 + row, gk = k0 + c * 16;
-      ra[j] = (gm < M && gk < K) ? *(const v4i*)(A + (int64_t)gm * lda + gk) : zero4();
-    }
-#pragma unroll
-    for (int j = 0; j < C::kBPer; ++j) {
-      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
-      const int gn = n0 + row, gk = k0 + c * 16;
-      rb[j] = (gn < N && gk < K) ? *(const v4i*)(W + (int64_t)gn * ldw + gk) : zero4();
-    }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < C::kAPer; ++j) {
-      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
-      sA[buf][row * 8 + (c ^ (row & 7))] = ra[j];
-    }
-#pragma unroll
-    for (int j = 0; j < C::kBPer; ++j) {
-      const int i = tid + j * C::kThreads, row = i >> 3, c = i & 7;
-      sB[buf][row * 8 + (c ^ (row & 7))] = rb[j];
-    }
-  };
+  lsk::mfma_mainloop<BM, BN, WM, WN>(acc, pa, pb, K, smem);
 
-  const int nk = (K + kBK - 1) / kBK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
+  int32_t* region = (int32_t*)smem + wave * C::kStripInts;
+  constexpr int kQuads = C::WTN / 4;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int c = ks * 4 + (lane >> 4);
-      v4i af[C::TM], bf[C::TN];
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i) {
-        const int r = wm * C::WTM + i * 16 + (lane & 15);
-        af[i] = sA[buf][r * 8 + (c ^ (r & 7))];
-      }
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j) {
-        const int r = wn * C::WTN + j * 16 + (lane & 15);
-        bf[j] = sB[buf][r * 8 + (c ^ (r & 7))];
-      }
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+  for (int i = 0; i < C::TM; ++i) {
+    lsk::stage_strip<C::TN, C::kLdc>(acc[i], region);
+    __syncthreads();
+    for (int q = lane; q < 16 * kQuads; q += 64) {
+      const int row = q / kQuads, c4 = q - row * kQuads;
+      const v4i v = *(const v4i*)(region + row * C::kLdc + c4 * 4);
+      const int m = m0 + wm * C::WTM + i * 16 + row;
+      const int n = n0 + wn * C::WTN + c4 * 4;
+      if (m < M && n < N) epilogue_store4(ep, m, n, N, v, vec_ok && n + 4 <= N);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
     __syncthreads();
   }
-
-  // D[i][j] of one 16x16 MFMA tile lives in lane (j + 16 * (i / 4)), register i % 4.
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * C::WTM + i * 16 + (lane >> 4) * 4 + r;
-        const int n = n0 + wn * C::WTN + j * 16 + (lane & 15);
-        if (m < M && n < N) epilogue_store(ep, m, n, acc[i][j][r]);
-      }
 }
 
 // Decode GEMV: one block per 16 output columns; its 4 waves take interleaved 256-byte K slabs;
@@ -169,7 +102,7 @@ __global__ __launch_bounds__(256) void gemv_i8_mfma_kernel(const int8_t* __restr
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const v4i a = (m < M && k + j * 16 < K) ? *(const v4i*)(A + (int64_t)m * lda + k + j * 16) : zero4();
-        acc[t] = mfma16(a, w4[j], acc[t]);
+        acc[t] = lsk::mfma_i8(a, w4[j], acc[t]);
       }
     }
   }
@@ -238,6 +171,39 @@ int validate_epilogue(int order, int out_dtype, const float* asc, const float* w
   return LSK_OK;
 }
 
+// Tile configurations of the dense kernel; id -1 lets the shape decide.
+static int g_force_tile = -1;
+
+template <int BM, int BN, int WM, int WN>
+static int launch_tile(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int M, int N, int K,
+                       const EpiParams& ep, int vec_ok, hipStream_t s, const char* name) {
+  using C = TileCfg<BM, BN, WM, WN>;
+  static bool attr_set = false;
+  auto kern = gemm_i8_mfma_kernel<BM, BN, WM, WN>;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmemBytes) !=
+        hipSuccess) {
+      set_error("%s: cannot reserve %d bytes of LDS", name, C::kSmemBytes);
+      return LSK_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  LSK_REQUIRE(tiles <= 0x7fffffff, "gemm: too many tiles");
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C::kThreads), C::kSmemBytes, s, a, lda, w, ldw, M, N, K, ep,
+                     vec_ok);
+  return check_launch(name);
+}
+
+static int pick_tile(int64_t M, int64_t N) {
+  if (g_force_tile >= 0) return g_force_tile;
+  // Measured on MI355X (Llama-3.1-8B / Qwen2.5-7B prefill shapes): the 256x256 tile of 8 waves
+  // wins once there are at least two full rounds of such tiles for the 256 CUs; below that the
+  // 128x128 tile (two blocks per CU) keeps every CU busy.
+  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+  return t256 >= 512 ? 3 : 2;
+}
+
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiParams& ep, hipStream_t s) {
   if (M == 0 || N == 0) return LSK_OK;
@@ -261,11 +227,14 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
                        iN, iK, ep);
     return check_launch("gemv_i8_mfma_kernel<2>");
   }
-  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
-  LSK_REQUIRE(tiles <= 0x7fffffff, "gemm: too many tiles");
-  hipLaunchKernelGGL((gemm_i8_mfma_kernel<128, 128, 2, 2>), dim3((unsigned)tiles), dim3(256), 0, s, a, lda, w, ldw,
-                     iM, iN, iK, ep);
-  return check_launch("gemm_i8_mfma_kernel<128,128,2,2>");
+  const int vec_ok = out_vec_ok(ep.out, ep.out_dtype, ep.ldo) ? 1 : 0;
+  switch (pick_tile(M, N)) {
+    case 0: return launch_tile<256, 256, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,2x2>");
+    case 1: return launch_tile<256, 128, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x128,2x2>");
+    case 3: return launch_tile<256, 256, 4, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,4x2>");
+    case 4: return launch_tile<128, 256, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x256,2x2>");
+    default: return launch_tile<128, 128, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2>");
+  }
 }
 
 }  // namespace lsk
@@ -329,4 +298,10 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
   hipLaunchKernelGGL(epilogue_apply_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, acc, ldc, M,
                      N, ep);
   return lsk::check_launch("epilogue_apply_kernel");
+}
+
+extern "C" int lsk_gemm_select(int tile_id) {
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 4, "lsk_gemm_select: tile id %d not in [-1, 4]", tile_id);
+  lsk::g_force_tile = tile_id;
+  return LSK_OK;
 }

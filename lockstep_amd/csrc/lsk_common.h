@@ -125,9 +125,77 @@ LSK_DEV void epilogue_store(const EpiParams& p, int64_t m, int64_t n, int32_t ac
     int s = p.shift;
     if (p.erow) s += p.erow[m];
     if (p.ecol) s += p.ecol[n];
-    float y = f32_mul(v, pow2f(-s));
-    store_out(p.out, p.out_dtype, o, y);
+    float sc = (s > 149) ? 0.0f : (s < -127 ? __uint_as_float(0x7f800000u) : pow2f(-s));
+    store_out(p.out, p.out_dtype, o, f32_mul(v, sc));
   }
+}
+
+// Epilogue value of one element, before the final rounding to the output type.
+LSK_DEV float epi_value(const EpiParams& p, int64_t m, int64_t n, int32_t acc) {
+  const float v = (float)acc;  // int32 -> binary32, round to nearest even
+  if (p.order == LSK_EPI_V21) {
+    float y = f32_mul(f32_mul(v, p.ws[n]), p.asc[m]);
+    if (p.bias) y = f32_add(round_out(p.out_dtype, y), p.bias[n]);
+    return y;
+  }
+  if (p.order == LSK_EPI_V2) {
+    float y = f32_mul(f32_mul(v, p.asc[m]), p.ws[n]);
+    if (p.bias) y = f32_add(y, p.bias[n]);
+    return y;
+  }
+  int s = p.shift;
+  if (p.erow) s += p.erow[m];
+  if (p.ecol) s += p.ecol[n];
+  float sc = (s > 149) ? 0.0f : (s < -127 ? __uint_as_float(0x7f800000u) : pow2f(-s));
+  return f32_mul(v, sc);
+}
+
+// Four consecutive columns n..n+3 of row m: epilogue, rounding and one vector store when
+// `vec` (the row segment is aligned and in range), else element stores up to column N.
+LSK_DEV void epilogue_store4(const EpiParams& p, int64_t m, int64_t n, int64_t N, v4i acc, bool vec) {
+  if (!vec) {
+    for (int t = 0; t < 4; ++t)
+      if (n + t < N) epilogue_store(p, m, n + t, acc[t]);
+    return;
+  }
+  const int64_t o = m * p.ldo + n;
+  if (p.order == LSK_EPI_RAW) {
+    *(v4i*)((int32_t*)p.out + o) = acc;
+    return;
+  }
+  float y[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) y[t] = epi_value(p, m, n + t, acc[t]);
+  switch (p.out_dtype) {
+    case LSK_BF16: {
+      uint2 u;
+      u.x = (uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16);
+      u.y = (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16);
+      *(uint2*)((uint16_t*)p.out + o) = u;
+      break;
+    }
+    case LSK_F16: {
+      uint2 u;
+      u.x = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y[0]) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y[1]) << 16);
+      u.y = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y[2]) |
+            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y[3]) << 16);
+      *(uint2*)((uint16_t*)p.out + o) = u;
+      break;
+    }
+    case LSK_BF16_AS_F32:
+      *(float4*)((float*)p.out + o) = make_float4(bfr(y[0]), bfr(y[1]), bfr(y[2]), bfr(y[3]));
+      break;
+    default:
+      *(float4*)((float*)p.out + o) = make_float4(y[0], y[1], y[2], y[3]);
+  }
+}
+
+// Whether rows of the output allow 4-wide vector stores (16-byte rows for 4-byte types,
+// 8-byte for 2-byte types).
+inline bool out_vec_ok(const void* out, int out_dtype, int64_t ldo) {
+  const int esz = (out_dtype == LSK_BF16 || out_dtype == LSK_F16) ? 2 : 4;
+  return ((uintptr_t)out % (4 * esz) == 0) && ((ldo * esz) % (4 * esz) == 0);
 }
 
 // Thread-local last-error string shared by every entry point.

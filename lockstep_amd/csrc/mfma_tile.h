@@ -11,6 +11,10 @@
 // A operand and of the W operand alike; D[i][j] lands in lane j + 16 * (i / 4), register i % 4.
 // Integer accumulation is exact in any order (|acc| <= K * 127^2 < 2^31), so the K blocking
 // never changes a result.
+//
+// Results leave the registers through LDS one 16-row strip at a time (per wave, static
+// register indices), and are read back four consecutive columns per lane so the epilogue
+// issues full-width, coalesced stores.
 #pragma once
 #include "lsk_common.h"
 
@@ -29,8 +33,16 @@ struct TileCfg {
   static constexpr int kAPer = BM * kBK / 16 / kThreads;  // 16-byte chunks per thread per stage
   static constexpr int kBPer = BN * kBK / 16 / kThreads;
   static constexpr int kSmemA = BM * 8, kSmemB = BN * 8;  // v4i chunks per stage
+  static constexpr int kLdc = WTN + 4;                     // int32 row stride of a staged strip
+  static constexpr int kStripInts = 16 * kLdc;             // per wave
+  static constexpr int kMainBytes = 2 * (kSmemA + kSmemB) * 16;
+  static constexpr int kEpiBytes = WM * WN * kStripInts * 4;
+  static constexpr int kSmemBytes = kMainBytes > kEpiBytes ? kMainBytes : kEpiBytes;
   static_assert((BM * kBK / 16) % kThreads == 0 && (BN * kBK / 16) % kThreads == 0, "tile/threads");
   static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be a multiple of 16");
+  typedef v4i Acc[TM][TN];
+  typedef const int8_t* RowsA[kAPer];
+  typedef const int8_t* RowsB[kBPer];
 };
 
 // Row index (within the tile) and 16-byte chunk index that thread `tid` loads in slot j.
@@ -44,11 +56,11 @@ LSK_DEV void chunk_of(int tid, int j, int& row, int& c) {
 // acc[TM][TN] += A_tile * W_tile^T over K (K % 16 == 0; row pointers 16-byte aligned).
 // pa / pb: the global row pointers of this thread's load slots (null = zero row).
 template <int BM, int BN, int WM, int WN>
-LSK_DEV void mfma_mainloop(v4i (&acc)[TileCfg<BM, BN, WM, WN>::TM][TileCfg<BM, BN, WM, WN>::TN],
-                           const int8_t* const (&pa)[TileCfg<BM, BN, WM, WN>::kAPer],
-                           const int8_t* const (&pb)[TileCfg<BM, BN, WM, WN>::kBPer], int K, v4i* sA,
-                           v4i* sB) {
+LSK_DEV void mfma_mainloop(typename TileCfg<BM, BN, WM, WN>::Acc& acc, const typename TileCfg<BM, BN, WM, WN>::RowsA& pa,
+                           const typename TileCfg<BM, BN, WM, WN>::RowsB& pb, int K, v4i* smem) {
   using C = TileCfg<BM, BN, WM, WN>;
+  v4i* sA = smem;
+  v4i* sB = smem + 2 * C::kSmemA;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
@@ -115,6 +127,18 @@ LSK_DEV void mfma_mainloop(v4i (&acc)[TileCfg<BM, BN, WM, WN>::TM][TileCfg<BM, B
     if (kt + 1 < nk) sstore(buf ^ 1);
     __syncthreads();
   }
+}
+
+// Write the 16-row strip `strip` of this wave's accumulators into the wave's LDS region
+// (row stride TileCfg::kLdc int32).  Called after the main loop's final barrier; the region
+// is private to the wave, and a wave's LDS accesses complete in program order.
+template <int TN, int LDC>
+LSK_DEV void stage_strip(const v4i* strip, int32_t* region) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) region[((lane >> 4) * 4 + r) * LDC + j * 16 + (lane & 15)] = strip[j][r];
 }
 
 // Map a hardware block id to a logical tile id so the blocks one XCD runs (hardware ids

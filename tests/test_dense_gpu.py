@@ -243,3 +243,25 @@ def test_config2_prefill_rows_and_chunk_invariance(which):
     assert np.array_equal(bits(y)[rows], ref)
     chunks = torch.cat([FS.w8a8_matmul(xd[i:i + 64], Wd, wsd, out_dtype=torch.bfloat16) for i in range(0, M, 64)])
     assert torch.equal(chunks.view(torch.int16), y.view(torch.int16))
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 257, 640), (512, 520, 2880), (64, 64, 16)])
+def test_every_tile_config_is_exact(tile, M, N, K):
+    """The forced tile configurations produce the same bits (exact integer sums, any tiling)."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import lockstep_fullstack as FS
+    say("tile", tile, M, N, K)
+    r = _rng(M + 3 * N + 7 * K + tile)
+    x = (r.standard_normal((M, K)) * 2).astype(F32)
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    bias = (r.standard_normal(N) * 0.1).astype(F32)
+    L.call("lsk_gemm_select", tile)
+    try:
+        y = FS.w8a8_matmul(to_dev(x), to_dev(W8), to_dev(ws), to_dev(bias), out_dtype=torch.bfloat16)
+        acc = FS._int_mm_exact(to_dev(C.rowquant(x)[0]), to_dev(W8).t())
+    finally:
+        L.call("lsk_gemm_select", -1)
+    assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, bias, "bf16"))
+    assert np.array_equal(bits(acc), C.int_mm(C.rowquant(x)[0], W8.T))
