@@ -113,6 +113,97 @@ int lsk_gemm_select(int tile_id);
 int lsk_quant8_pow2(const float* x, int64_t M, int64_t K, int64_t ldx, int mode,
                     int8_t* q, int64_t ldq, int32_t* e_out, void* workspace, void* stream);
 
+/* ---------------------------------------------------------------- mixture of experts (v3) */
+
+/* Activation of the gate/up pair in the expert block. */
+typedef enum {
+  LSK_ACT_SILU = 0,      /* moe_ref.act_silu: bfr(silu_contract(g) * u) (reference/moe_ref.py:183-186) */
+  LSK_ACT_SWIGLUOAI = 1  /* moe_ref.act_swigluoai (reference/moe_ref.py:172-180) */
+} lsk_act;
+
+/* Router scores and top-k from gate logits.
+ * Replaces moe_ref.router_from_logits + table_scores (reference/moe_ref.py:64-74,85-97):
+ *   d = max(rint(fl32(fl32(max_e g - g) * fl32(2^26 / ln 2))), 0);
+ *   s = tab[(d >> 13) & 8191] >> min(d >> 26, 63), 0 when d >= 16 << 26;
+ *   top-k by s * E + (E - 1 - e) (ties to the lower index), in rank order;
+ *   w = bf16(fl32(s_sel) / fl32(S)), S = sum of the selected (renormalize) or of all scores, >= 1.
+ * g: [T, E] of g_dtype (LSK_F32 holding bf16 values, or LSK_BF16), row stride ldg;
+ * tab: [8192] int32 (the FRAC table); idx: [T, k] int64; w_bf16: [T, k] bf16 bits.
+ * E <= 1024, k <= min(E, 32). */
+int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t T, int64_t E, int k, int renormalize,
+                    const int32_t* tab, int64_t* idx, uint16_t* w_bf16, void* stream);
+
+/* Elementwise table activations over n binary32 elements (no libm; one IEEE operation per
+ * declared step).  op LSK_OP_SILU: lockstep_fullstack.silu_contract(g)
+ * (reference/lockstep_fullstack.py:590-604); LSK_OP_SIGMOID: moe_ref.sigmoid_contract(g)
+ * (reference/moe_ref.py:150-161); LSK_OP_ACT_SILU: moe_ref.act_silu(g, u) (:183-186);
+ * LSK_OP_ACT_SWIGLUOAI: moe_ref.act_swigluoai(g, u) (:172-180).  frac: the [8192] int32
+ * FRAC table.  u is unused (may be NULL) for the one-input ops. */
+#define LSK_OP_SILU 0
+#define LSK_OP_SIGMOID 1
+#define LSK_OP_ACT_SILU 2
+#define LSK_OP_ACT_SWIGLUOAI 3
+int lsk_act_elementwise(const float* g, const float* u, int64_t n, int op, const int32_t* frac, float* out,
+                        void* stream);
+
+/* Router table scores of n gaps (replaces moe_ref.table_scores, reference/moe_ref.py:64-74):
+ * out = tab[(d >> 13) & 8191] >> min(d >> 26, 63) for d = max(rint(fl32(dgap * C)), 0) below
+ * 16 << 26, else 0.  dgap: binary32; tab: [8192] int32; out: int64. */
+int lsk_table_scores(const float* dgap, int64_t n, const int32_t* tab, int64_t* out, void* stream);
+
+/* The R1 / R4 block butterfly (replaces lockstep_fullstack.fwht_blocks,
+ * reference/lockstep_fullstack.py:533-546): on every blk-wide block of each row, pairs (i, i+h)
+ * -> (a+b, a-b) for h = 1, 2, ..., blk/2 in binary32, then one multiply by `scale`.
+ * x, y: [rows, D] binary32 (row strides ldx, ldy; y may equal x); blk a power of two <= 1024
+ * dividing D. */
+int lsk_fwht_blocks(const float* x, int64_t rows, int64_t D, int64_t ldx, int blk, float scale, float* y,
+                    int64_t ldy, void* stream);
+
+/* The whole contract v3 MoE layer with int8 experts and injected routing.
+ * Replaces moe_ref.moe_forward / moe_forward_b with routing=(idx, w), rot off
+ * (reference/moe_ref.py:117-140, 189-200, 213-230):
+ *   for each expert e ascending and the tokens that chose it: rowquant(x) -> exact GEMM with
+ *   w13[e] -> bfr(V21 epilogue) (+ bfr(+ b13)) -> act(gate, up) -> rowquant -> exact GEMM with
+ *   w2[e] -> bfr(V21) (+ bfr(+ b2)); y[t] = bf16(sum over t's experts ascending of
+ *   bfr(w * out), binary32 adds from +0) (+ bfr(shared[t]) last).
+ * Expert weights are given as device tables of E device addresses (int64): w13_ptrs -> int8
+ * [2I, H] (row stride ldw13), ws13_ptrs -> f32 [2I], w2_ptrs -> int8 [H, I] (row stride ldw2),
+ * ws2_ptrs -> f32 [H], b13_ptrs / b2_ptrs -> f32 [2I] / [H] (the tables may be NULL for no
+ * bias).  x: [T, H] bf16; idx: [T, k] int64 (experts outside [0, E) are skipped, as the
+ * reference's loop over range(E) skips them; a token's experts must be distinct);
+ * w: [T, k] bf16 bits; shared: [T, H] f32 or NULL; y: [T, H] bf16.
+ * frac: the [8192] int32 FRAC table of the activation.  rot_blk > 0 applies the block
+ * rotation of moe_ref's rot / rot_blk options (H and I multiples of rot_blk, I <= 16384).
+ * workspace: lsk_moe_workspace bytes, 256-byte aligned.  H % 16 == 0 and I % 16 == 0. */
+typedef struct {
+  int64_t T, H, I, E;
+  int k;
+  int act;                       /* lsk_act */
+  const uint16_t* x;             /* [T, H] bf16 */
+  const int64_t* idx;            /* [T, k] */
+  const uint16_t* w;             /* [T, k] bf16 */
+  const int64_t* w13_ptrs;       /* [E] */
+  int64_t ldw13;
+  const int64_t* ws13_ptrs;      /* [E] */
+  const int64_t* b13_ptrs;       /* [E] or NULL */
+  const int64_t* w2_ptrs;        /* [E] */
+  int64_t ldw2;
+  const int64_t* ws2_ptrs;       /* [E] */
+  const int64_t* b2_ptrs;        /* [E] or NULL */
+  const int32_t* frac;           /* [8192] */
+  int rot_blk;                   /* 0: no rotation; else the R1 / R4 block (fwht_blocks) applied to
+                                    x before its row quant and to h before its requant */
+  float rot_scale;               /* the butterfly's final scale (1 / sqrt(rot_blk)) */
+  const float* shared;           /* [T, H] or NULL */
+  uint16_t* y;                   /* [T, H] bf16 */
+  void* workspace;
+  int64_t workspace_bytes;
+} lsk_moe_args;
+
+int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk);
+
+int lsk_moe_forward(const lsk_moe_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "liblockstep_amd.so")
 
 LSK_F32, LSK_BF16, LSK_F16, LSK_I32, LSK_I8, LSK_BF16_AS_F32 = 0, 1, 2, 3, 4, 5
 EPI_V21, EPI_V2, EPI_POW2, EPI_RAW = 0, 1, 2, 3
+LSK_ACT_SILU, LSK_ACT_SWIGLUOAI = 0, 1
 
 _DTYPE = {torch.float32: LSK_F32, torch.bfloat16: LSK_BF16, torch.float16: LSK_F16,
           torch.int32: LSK_I32, torch.int8: LSK_I8}
@@ -36,7 +37,21 @@ SIGNATURES = {
     "lsk_w8a8_matmul": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P, _I64, _P]),
     "lsk_gemm_select": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
+    "lsk_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
+    "lsk_act_elementwise": (_I, [_P, _P, _I64, _I, _P, _P, _P]),
+    "lsk_table_scores": (_I, [_P, _I64, _P, _P, _P]),
+    "lsk_fwht_blocks": (_I, [_P, _I64, _I64, _I64, _I, ctypes.c_float, _P, _I64, _P]),
+    "lsk_moe_workspace": (_I64, [_I64, _I, _I64, _I64, _I64, _I]),
+    "lsk_moe_forward": (_I, [_P, _P]),
 }
+
+
+class MoeArgs(ctypes.Structure):
+    """Mirror of lsk_moe_args (include/lockstep_amd.h)."""
+    _fields_ = [("T", _I64), ("H", _I64), ("I", _I64), ("E", _I64), ("k", _I), ("act", _I),
+                ("x", _P), ("idx", _P), ("w", _P), ("w13_ptrs", _P), ("ldw13", _I64), ("ws13_ptrs", _P),
+                ("b13_ptrs", _P), ("w2_ptrs", _P), ("ldw2", _I64), ("ws2_ptrs", _P), ("b2_ptrs", _P),
+                ("frac", _P), ("rot_blk", _I), ("rot_scale", ctypes.c_float), ("shared", _P), ("y", _P), ("workspace", _P), ("workspace_bytes", _I64)]
 
 _lock = threading.Lock()
 _lib = None

@@ -59,6 +59,17 @@ def frac_on(dev):
     return table_on(dev, 13, 15)
 
 
+_frac_i32 = {}
+
+
+def table_i32_on(dev, n=13, w=15):
+    """The table as int32 (every entry is below 2^16), the form the kernels read."""
+    k = (str(dev), n, w)
+    if k not in _frac_i32:
+        _frac_i32[k] = torch.tensor(table_np(n, w).astype(np.int32), dtype=torch.int32, device=dev)
+    return _frac_i32[k]
+
+
 def frac_check():
     d = hashlib.sha256(np.asarray(table_np(13, 15), dtype="<u2").tobytes()).hexdigest()
     assert d == FRAC_DIGEST, "FRAC digest mismatch: " + d

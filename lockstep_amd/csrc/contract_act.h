@@ -1,0 +1,48 @@
+// The contract's table activations (no libm): silu_contract, sigmoid_contract, act_silu and
+// act_swigluoai, one binary32 operation per declared step.
+#pragma once
+#include "lsk_common.h"
+
+namespace lsk {
+
+constexpr float kSiluC = -0x1.715476p+0f;   // binary32 nearest -log2(e) (lockstep_fullstack.py:175)
+constexpr float kAlpha = 0x1.b3b646p+0f;    // fl32(1.702) (moe_ref.py:146)
+constexpr float kMinNormal = 0x1p-126f;
+
+// Steps (2)-(9) of silu_contract / sigmoid_contract (lockstep_fullstack.py:590-604,
+// moe_ref.py:150-161) on the flushed input xc: 1 / (1 + FRAC[k] * 2^-15 * 2^i).
+LSK_DEV float sigmoid_steps(float xc, const int32_t* __restrict__ frac) {
+  float t = f32_mul(xc, kSiluC);
+  t = fminf(fmaxf(t, -30.0f), 30.0f);
+  const float i = ceilf(t);
+  const float g = i - t;
+  const float kf = fminf(truncf(f32_mul(g, 8192.0f)), 8191.0f);
+  const float f = f32_mul((float)frac[(int)kf], 0x1p-15f);
+  const float e2 = f32_mul(f, pow2f((int)i));
+  return f32_div(1.0f, f32_add(1.0f, e2));
+}
+
+// Step (0): subnormal inputs are flushed to +0.
+LSK_DEV float flush_sub(float x) { return fabsf(x) < kMinNormal ? 0.0f : x; }
+
+LSK_DEV float silu_contract(float x, const int32_t* frac) {
+  const float xc = flush_sub(x);
+  return f32_mul(xc, sigmoid_steps(xc, frac));
+}
+
+LSK_DEV float sigmoid_contract(float x, const int32_t* frac) { return sigmoid_steps(flush_sub(x), frac); }
+
+// moe_ref.py:183-186: bfr(fl32(silu(g)) * u)
+LSK_DEV float act_silu(float g, float u, const int32_t* frac) { return bfr(f32_mul(silu_contract(g, frac), u)); }
+
+// moe_ref.py:172-180: gc = min(g, 7); uc = clamp(u, -7, 7); arg = bfr(gc * 1.702);
+// glu = bfr(gc * sig(arg)); h = bfr((uc + 1) * glu)
+LSK_DEV float act_swigluoai(float g, float u, const int32_t* frac) {
+  const float gc = fminf(g, 7.0f);
+  const float uc = fminf(fmaxf(u, -7.0f), 7.0f);
+  const float arg = bfr(f32_mul(gc, kAlpha));
+  const float glu = bfr(f32_mul(gc, sigmoid_contract(arg, frac)));
+  return bfr(f32_mul(f32_add(uc, 1.0f), glu));
+}
+
+}  // namespace lsk

@@ -1,0 +1,636 @@
+// Contract v3 mixture-of-experts layer on gfx950, int8 experts (reference/moe_ref.py:117-230).
+//
+// Stages, all stream-ordered with no host synchronisation:
+//   1. row quant of x once per token (an expert's rows are a subset of tokens; the per-row
+//      quant does not depend on which other rows an expert sees);
+//   2. dispatch: per-expert row counts, offsets and an M-tile table built on the device; rows
+//      placed expert-major and token-ascending inside each expert (a counting sort whose
+//      in-chunk ranks come from per-expert token bitmasks: deterministic);
+//   3. grouped gate/up GEMM over variable-size expert tiles (token rows gathered), v2.1 epilogue
+//      (+ bias) and the activation fused; each row's |h| maximum gathered by integer atomics on
+//      the non-negative float bits (exact and order-free);
+//   4. row requant of h;
+//   5. grouped down GEMM, v2.1 epilogue (+ bias), times the routing weight, bf16 into a
+//      token-major slot r = rank of the expert among the token's experts;
+//   6. combine: per token, binary32 adds of its slots in ascending expert order from +0.
+#include "contract_act.h"
+#include "mfma_tile.h"
+
+namespace {
+
+constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
+constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
+constexpr int kBM = 128;
+
+// ---------------------------------------------------------------- router
+LSK_DEV long long wave_max_ll(long long v) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const long long w = __shfl_xor(v, o, 64);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// One wave per token; lane l owns experts l, l + 64, ...
+__global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ g, int gdt, int64_t ldg, int T,
+                                                          int E, int k, int renorm, const int32_t* __restrict__ tab,
+                                                          int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  constexpr int EPL = 16;  // experts per lane, E <= 1024
+  float gv[EPL];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    gv[j] = 0.0f;
+    if (e < E) {
+      gv[j] = gdt == LSK_BF16 ? bf16_to_f32(((const uint16_t*)g)[(int64_t)t * ldg + e])
+                              : ((const float*)g)[(int64_t)t * ldg + e];
+      m = fmaxf(m, gv[j]);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  long long key[EPL];
+  int sc[EPL];
+  int s_all = 0;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    key[j] = -1;
+    sc[j] = 0;
+    if (e < E) {
+      const float v = rintf(f32_mul(m - gv[j], kRouterC));
+      int s = 0;
+      if (v < 1073741824.0f) {  // d < 16 << 26 (also false for NaN / inf)
+        const int d = v > 0.0f ? (int)v : 0;
+        s = tab[(d >> 13) & 8191] >> (d >> 26);
+      }
+      sc[j] = s;
+      s_all += s;
+      key[j] = (long long)s * E + (E - 1 - e);
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) s_all += __shfl_xor(s_all, o, 64);
+  int s_sel_mine = 0;  // lane r keeps the score of rank r
+  int s_sum = 0;
+  for (int r = 0; r < k; ++r) {
+    long long best = -1;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
+    best = wave_max_ll(best);
+    const int e = (E - 1) - (int)(best % E);
+    const int s = (int)(best / E);
+    s_sum += s;
+    if (lane == r) s_sel_mine = s;
+    if (lane == 0) idx_out[(int64_t)t * k + r] = e;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+      if (lane + 64 * j == e) key[j] = -1;
+  }
+  if (lane < k) {
+    int S = renorm ? s_sum : s_all;
+    S = S < 1 ? 1 : S;
+    w_out[(int64_t)t * k + lane] = f32_to_bf16(f32_div((float)s_sel_mine, (float)S));
+  }
+}
+
+// ---------------------------------------------------------------- dispatch (one block)
+__global__ __launch_bounds__(256) void moe_dispatch_kernel(const int64_t* __restrict__ idx,
+                                                           const uint16_t* __restrict__ w, int T, int k, int E,
+                                                           int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
+                                                           int32_t* __restrict__ row_tok,
+                                                           int32_t* __restrict__ row_dst, float* __restrict__ row_w,
+                                                           int32_t* __restrict__ tok_cnt) {
+  extern __shared__ int32_t dsm[];
+  int32_t* cnt = dsm;
+  int32_t* cursor = dsm + E;
+  uint32_t* mask = (uint32_t*)(dsm + 2 * E);  // [E][8]: one bit per token of a 256-token chunk
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 256) cnt[e] = 0;
+  __syncthreads();
+  for (int t = tid; t < T; t += 256) {
+    int nv = 0;
+    for (int j = 0; j < k; ++j) {
+      const int64_t e = idx[(int64_t)t * k + j];
+      if (e >= 0 && e < E) {
+        atomicAdd(&cnt[e], 1);
+        ++nv;
+      }
+    }
+    tok_cnt[t] = nv;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0, nt = 0;
+    for (int e = 0; e < E; ++e) {
+      offs[e] = run;
+      cursor[e] = run;
+      const int c = cnt[e];
+      for (int r0 = run; r0 < run + c; r0 += kBM) {
+        tiles[1 + 2 * nt] = e;
+        tiles[2 + 2 * nt] = r0;
+        ++nt;
+      }
+      run += c;
+    }
+    offs[E] = run;
+    tiles[0] = nt;
+  }
+  __syncthreads();
+  for (int c0 = 0; c0 < T; c0 += 256) {
+    for (int i = tid; i < E * 8; i += 256) mask[i] = 0;
+    __syncthreads();
+    const int t = c0 + tid;
+    if (t < T) {
+      for (int j = 0; j < k; ++j) {
+        const int64_t e = idx[(int64_t)t * k + j];
+        if (e >= 0 && e < E) atomicOr(&mask[e * 8 + (tid >> 5)], 1u << (tid & 31));
+      }
+    }
+    __syncthreads();
+    if (t < T) {
+      for (int j = 0; j < k; ++j) {
+        const int64_t e = idx[(int64_t)t * k + j];
+        if (!(e >= 0 && e < E)) continue;
+        int rank = __popc(mask[e * 8 + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
+        for (int wd = 0; wd < (tid >> 5); ++wd) rank += __popc(mask[e * 8 + wd]);
+        const int p = cursor[e] + rank;
+        int slot = 0;  // rank of e among the token's experts, ascending
+        for (int j2 = 0; j2 < k; ++j2) {
+          const int64_t e2 = idx[(int64_t)t * k + j2];
+          if (e2 >= 0 && e2 < E && e2 < e) ++slot;
+        }
+        row_tok[p] = t;
+        row_dst[p] = t * k + slot;
+        row_w[p] = bf16_to_f32(w[(int64_t)t * k + j]);
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) {
+      int c = 0;
+#pragma unroll
+      for (int wd = 0; wd < 8; ++wd) c += __popc(mask[e * 8 + wd]);
+      cursor[e] += c;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x, int64_t n, float* __restrict__ y) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) y[i] = bf16_to_f32(x[i]);
+}
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+// ---------------------------------------------------------------- grouped GEMM
+struct MoeGemmArgs {
+  const int8_t* A;
+  int64_t lda;
+  const float* a_scale;     // per A row
+  const int32_t* row_tok;   // gate/up: permuted row -> token (A row); down: unused
+  const int32_t* offs;      // [E + 1]
+  const int32_t* tiles;     // [0] count, then (expert, first row) pairs
+  const int64_t* w_ptrs;    // [E]
+  int64_t ldw;
+  const int64_t* ws_ptrs;   // [E]
+  const int64_t* b_ptrs;    // [E] or null
+  int K;
+  int N;                    // gate/up: I (h columns); down: H
+  int act;
+  const int32_t* frac;
+  uint16_t* h;              // gate/up out [R, I]
+  uint32_t* h_amax;         // [R]
+  const float* row_w;       // down: routing weight per row
+  const int32_t* row_dst;   // down: destination slot row
+  uint16_t* y;              // down out [T * k, N]
+};
+
+// MODE 0: gate/up + activation; MODE 1: down + routing weight.
+template <int MODE>
+__global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
+  using C = lsk::TileCfg<128, 128, 2, 2>;
+  extern __shared__ v4i smem[];
+  const int ntiles = MODE == 0 ? (a.N + 63) / 64 : (a.N + 127) / 128;
+  const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
+  const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
+  if (mt >= a.tiles[0]) return;
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + kBM);
+  const int8_t* wb = (const int8_t*)a.w_ptrs[e];
+  const float* ws = (const float*)a.ws_ptrs[e];
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / 2, wn = wave % 2;
+  typename C::RowsA pa;
+  typename C::RowsB pb;
+#pragma unroll
+  for (int j = 0; j < C::kAPer; ++j) {
+    int row, c;
+    lsk::chunk_of<C::kThreads>(tid, j, row, c);
+    const int p = p0 + row;
+    const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
+    pa[j] = src >= 0 ? a.A + (int64_t)src * a.lda : nullptr;
+  }
+#pragma unroll
+  for (int j = 0; j < C::kBPer; ++j) {
+    int row, c;
+    lsk::chunk_of<C::kThreads>(tid, j, row, c);
+    if (MODE == 0) {
+      const int blk = row >> 4;
+      const int hc = nt * 64 + (blk >> 1) * 16 + (row & 15);
+      pb[j] = hc < a.N ? wb + (int64_t)((blk & 1) ? a.N + hc : hc) * a.ldw : nullptr;
+    } else {
+      const int n = nt * 128 + row;
+      pb[j] = n < a.N ? wb + (int64_t)n * a.ldw : nullptr;
+    }
+  }
+  typename C::Acc acc;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero4();
+
+  lsk::mfma_mainloop<128, 128, 2, 2>(acc, pa, pb, a.K, smem);
+
+  int32_t* region = (int32_t*)smem + wave * C::kStripInts;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) {
+    lsk::stage_strip<C::TN, C::kLdc>(acc[i], region);
+    __syncthreads();
+    if (MODE == 0) {
+      // strip columns: [gate pair 0 | up pair 0 | gate pair 1 | up pair 1], 16 each
+#pragma unroll
+      for (int pass = 0; pass < 2; ++pass) {
+        const int q = pass * 64 + lane;
+        const int row = q >> 3, hq = q & 7, pair = hq >> 2, c4 = (hq & 3) * 4;
+        const v4i vg = *(const v4i*)(region + row * C::kLdc + pair * 32 + c4);
+        const v4i vu = *(const v4i*)(region + row * C::kLdc + pair * 32 + 16 + c4);
+        const int p = p0 + wm * 64 + i * 16 + row;
+        const int hc0 = nt * 64 + wn * 32 + pair * 16 + c4;
+        float am = 0.0f;
+        if (p < p1) {
+          const float asc = a.a_scale[a.row_tok[p]];
+          uint16_t hb[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int hc = hc0 + t;
+            hb[t] = 0;
+            if (hc < a.N) {
+              float yg = bfr(f32_mul(f32_mul((float)vg[t], ws[hc]), asc));
+              float yu = bfr(f32_mul(f32_mul((float)vu[t], ws[a.N + hc]), asc));
+              if (bias) {
+                yg = bfr(f32_add(yg, bias[hc]));
+                yu = bfr(f32_add(yu, bias[a.N + hc]));
+              }
+              const float hv = a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
+              hb[t] = f32_to_bf16(hv);
+              am = fmaxf(am, fabsf(hv));
+            }
+          }
+          uint16_t* dst = a.h + (int64_t)p * a.N + hc0;
+          if (hc0 + 4 <= a.N) {
+            *(uint2*)dst = make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
+          } else {
+            for (int t = 0; t < 4; ++t)
+              if (hc0 + t < a.N) dst[t] = hb[t];
+          }
+        }
+        am = fmaxf(am, __shfl_xor(am, 1, 64));
+        am = fmaxf(am, __shfl_xor(am, 2, 64));
+        am = fmaxf(am, __shfl_xor(am, 4, 64));
+        if ((lane & 7) == 0 && p < p1) atomicMax(&a.h_amax[p], __float_as_uint(am));
+      }
+    } else {
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const int q = pass * 64 + lane;
+        const int row = q >> 4, c4 = (q & 15) * 4;
+        const v4i v = *(const v4i*)(region + row * C::kLdc + c4);
+        const int p = p0 + wm * 64 + i * 16 + row;
+        const int n0 = nt * 128 + wn * 64 + c4;
+        if (p < p1 && n0 < a.N) {
+          const float asc = a.a_scale[p];
+          const float wt = a.row_w[p];
+          uint16_t ob[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int n = n0 + t;
+            ob[t] = 0;
+            if (n < a.N) {
+              float yv = bfr(f32_mul(f32_mul((float)v[t], ws[n]), asc));
+              if (bias) yv = bfr(f32_add(yv, bias[n]));
+              ob[t] = f32_to_bf16(f32_mul(wt, yv));
+            }
+          }
+          uint16_t* dst = a.y + (int64_t)a.row_dst[p] * a.N + n0;
+          if (n0 + 4 <= a.N) {
+            *(uint2*)dst = make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+          } else {
+            for (int t = 0; t < 4; ++t)
+              if (n0 + t < a.N) dst[t] = ob[t];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- requant and combine
+// rowquant of the activation output h (bf16 values), with the row maxima from the GEMM.
+__global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __restrict__ h, const uint32_t* __restrict__ amax,
+                                                          const int32_t* __restrict__ nrows, int I,
+                                                          int8_t* __restrict__ q, float* __restrict__ asc) {
+  const int R = *nrows;
+  const int chunks = I / 8;
+  const int64_t total = (int64_t)R * chunks;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t p = i / chunks;
+    const int c = (int)(i - p * chunks);
+    const float s = f32_div(fmaxf(__uint_as_float(amax[p]), kAmaxFloor), 127.0f);
+    if (c == 0) asc[p] = s;
+    const uint4 u = *(const uint4*)(h + p * I + c * 8);
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v0 = bf16_to_f32((uint16_t)(wd[j] & 0xffff));
+      const float v1 = bf16_to_f32((uint16_t)(wd[j] >> 16));
+      float q0 = fminf(fmaxf(rintf(f32_div(v0, s)), -127.0f), 127.0f);
+      float q1 = fminf(fmaxf(rintf(f32_div(v1, s)), -127.0f), 127.0f);
+      const uint32_t b = ((uint32_t)(uint8_t)(int8_t)(int)q0) | (((uint32_t)(uint8_t)(int8_t)(int)q1) << 8);
+      if (j < 2) lo |= b << (16 * j);
+      else hi |= b << (16 * (j - 2));
+    }
+    *(uint2*)(q + p * I + c * 8) = make_uint2(lo, hi);
+  }
+}
+
+// The R4 rotation of h followed by its row quant (moe_ref.py:112-113, 195-199 with rotation):
+// one block per row; the row's bf16 values are widened into LDS, butterflied per blk-wide
+// block in binary32, scaled, and quantised with the row's own maximum.
+__global__ __launch_bounds__(256) void moe_rot_requant_kernel(const uint16_t* __restrict__ h,
+                                                              const int32_t* __restrict__ nrows, int I, int blk,
+                                                              float scale, int8_t* __restrict__ q,
+                                                              float* __restrict__ asc) {
+  extern __shared__ float rv[];
+  __shared__ float red[4];
+  const int64_t p = blockIdx.x;
+  if (p >= *nrows) return;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < I; i += 256) rv[i] = bf16_to_f32(h[p * I + i]);
+  __syncthreads();
+  const int half = blk / 2;
+  for (int hh = 1; hh < blk; hh <<= 1) {
+    for (int i = tid; i < I / 2; i += 256) {
+      const int b = i / half, w = i - b * half;
+      const int grp = w / hh, off = w - grp * hh;
+      const int i0 = b * blk + grp * 2 * hh + off, i1 = i0 + hh;
+      const float x0 = rv[i0], x1 = rv[i1];
+      rv[i0] = f32_add(x0, x1);
+      rv[i1] = x0 - x1;
+    }
+    __syncthreads();
+  }
+  float am = 0.0f;
+  for (int i = tid; i < I; i += 256) {
+    const float v = f32_mul(rv[i], scale);
+    rv[i] = v;
+    am = fmaxf(am, fabsf(v));
+  }
+  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f);
+  if (tid == 0) asc[p] = s;
+  for (int i = tid; i < I; i += 256) {
+    const float t = fminf(fmaxf(rintf(f32_div(rv[i], s)), -127.0f), 127.0f);
+    q[p * I + i] = (int8_t)(int)t;
+  }
+}
+
+// y[t] = bf16( sum_r fl32(slot r of t) in ascending expert order, from +0 ) (+ bfr(shared[t]) last)
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ slots, int64_t H, int k,
+                                                          const int32_t* __restrict__ tok_cnt,
+                                                          const float* __restrict__ shared, int64_t T,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t chunks = H / 8;
+  const int64_t total = T * chunks;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t t = i / chunks;
+    const int64_t c = (i - t * chunks) * 8;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    const int n = tok_cnt[t];
+    for (int r = 0; r < n; ++r) {
+      const uint4 u = *(const uint4*)(slots + (t * k + r) * H + c);
+      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] = f32_add(acc[2 * j], bf16_to_f32((uint16_t)(wd[j] & 0xffff)));
+        acc[2 * j + 1] = f32_add(acc[2 * j + 1], bf16_to_f32((uint16_t)(wd[j] >> 16)));
+      }
+    }
+    if (shared) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = f32_add(acc[j], bfr(shared[t * H + c + j]));
+    }
+    uint4 o;
+    o.x = (uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+    o.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+    o.z = (uint32_t)f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
+    o.w = (uint32_t)f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+    *(uint4*)(out + t * H + c) = o;
+  }
+}
+
+// ---------------------------------------------------------------- workspace layout
+struct MoeWs {
+  int8_t* qx;
+  float* ascx;
+  int32_t* offs;
+  int32_t* tiles;
+  int32_t* row_tok;
+  int32_t* row_dst;
+  float* row_w;
+  int32_t* tok_cnt;
+  uint16_t* h;
+  uint32_t* h_amax;
+  int8_t* qh;
+  float* asch;
+  uint16_t* slots;
+  float* xrot;
+  int64_t bytes;
+  int64_t max_tiles;
+};
+
+inline int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
+
+MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk) {
+  MoeWs w{};
+  const int64_t R = T * k;
+  w.max_tiles = R / kBM + (E < R ? E : R);
+  int64_t off = 0;
+  auto take = [&](int64_t nbytes) {
+    char* p = base ? base + off : nullptr;
+    off += up256(nbytes);
+    return p;
+  };
+  w.qx = (int8_t*)take(T * H);
+  w.ascx = (float*)take(T * 4);
+  w.offs = (int32_t*)take((E + 1) * 4);
+  w.tiles = (int32_t*)take((1 + 2 * w.max_tiles) * 4);
+  w.row_tok = (int32_t*)take(R * 4);
+  w.row_dst = (int32_t*)take(R * 4);
+  w.row_w = (float*)take(R * 4);
+  w.tok_cnt = (int32_t*)take(T * 4);
+  w.h = (uint16_t*)take(R * I * 2);
+  w.h_amax = (uint32_t*)take(R * 4);
+  w.qh = (int8_t*)take(R * I);
+  w.asch = (float*)take(R * 4);
+  w.slots = (uint16_t*)take(R * H * 2);
+  w.xrot = rot_blk > 0 ? (float*)take(T * H * 4) : nullptr;
+  w.bytes = off;
+  return w;
+}
+
+template <int MODE>
+int launch_moe_gemm(const MoeGemmArgs& ga, int64_t max_tiles, int ntiles, hipStream_t s, const char* name) {
+  using C = lsk::TileCfg<128, 128, 2, 2>;
+  const int64_t blocks = max_tiles * ntiles;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  hipLaunchKernelGGL(moe_gemm_kernel<MODE>, dim3((unsigned)blocks), dim3(256), C::kSmemBytes, s, ga);
+  return lsk::check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t T, int64_t E, int k, int renormalize,
+                               const int32_t* tab, int64_t* idx, uint16_t* w_bf16, void* stream) {
+  LSK_REQUIRE(T >= 0 && E >= 1 && E <= 1024, "lsk_router_topk: E=%lld not in [1, 1024]", (long long)E);
+  LSK_REQUIRE(k >= 1 && k <= 32 && k <= E, "lsk_router_topk: k=%d not in [1, min(E, 32)]", k);
+  LSK_REQUIRE(g_dtype == LSK_F32 || g_dtype == LSK_BF16, "lsk_router_topk: g_dtype must be f32 or bf16");
+  LSK_REQUIRE(ldg >= E, "lsk_router_topk: ldg below E");
+  if (T == 0) return LSK_OK;
+  LSK_REQUIRE(g && tab && idx && w_bf16, "lsk_router_topk: null pointer");
+  LSK_REQUIRE(T <= 0x7fffffffLL * 4, "lsk_router_topk: T too large");
+  hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, (hipStream_t)stream, g, g_dtype,
+                     ldg, (int)T, (int)E, k, renormalize, tab, idx, w_bf16);
+  return lsk::check_launch("router_topk_kernel");
+}
+
+extern "C" int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk) {
+  return moe_layout(nullptr, T, k, E, H, I, rot_blk).bytes;
+}
+
+extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
+  LSK_REQUIRE(a, "lsk_moe_forward: null args");
+  const int64_t T = a->T, H = a->H, I = a->I, E = a->E;
+  const int k = a->k;
+  LSK_REQUIRE(T >= 0 && H > 0 && I > 0 && E >= 1 && E <= 1024, "lsk_moe_forward: bad sizes T=%lld H=%lld I=%lld E=%lld",
+              (long long)T, (long long)H, (long long)I, (long long)E);
+  LSK_REQUIRE(k >= 1 && k <= 32, "lsk_moe_forward: k=%d not in [1, 32]", k);
+  LSK_REQUIRE(H % 16 == 0 && I % 16 == 0, "lsk_moe_forward: H and I must be multiples of 16");
+  LSK_REQUIRE(H <= 133144 && I <= 133144, "lsk_moe_forward: K above the int32-exact bound");
+  LSK_REQUIRE(a->act == LSK_ACT_SILU || a->act == LSK_ACT_SWIGLUOAI, "lsk_moe_forward: unknown act %d", a->act);
+  LSK_REQUIRE(T * k <= 0x7fffffff && T * H <= ((int64_t)1 << 40), "lsk_moe_forward: T too large");
+  if (T == 0) return LSK_OK;
+  LSK_REQUIRE(a->x && a->idx && a->w && a->w13_ptrs && a->ws13_ptrs && a->w2_ptrs && a->ws2_ptrs && a->frac && a->y,
+              "lsk_moe_forward: null pointer");
+  LSK_REQUIRE(a->ldw13 >= H && a->ldw13 % 16 == 0 && a->ldw2 >= I && a->ldw2 % 16 == 0,
+              "lsk_moe_forward: weight row strides must cover K and be multiples of 16");
+  const int rb = a->rot_blk;
+  LSK_REQUIRE(rb == 0 || (rb >= 2 && rb <= 1024 && (rb & (rb - 1)) == 0 && H % rb == 0 && I % rb == 0 && I <= 16384),
+              "lsk_moe_forward: rot_blk=%d must be 0 or a power of two dividing H and I (I <= 16384)", rb);
+  const MoeWs w = moe_layout((char*)a->workspace, T, k, E, H, I, rb);
+  LSK_REQUIRE(a->workspace && a->workspace_bytes >= w.bytes && ((uintptr_t)a->workspace & 255) == 0,
+              "lsk_moe_forward: workspace of %lld bytes (256-byte aligned) needed", (long long)w.bytes);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t R = T * k;
+
+  int rc;
+  if (rb > 0) {
+    // xrot = fwht_blocks(fl32(x)): widen, then butterfly in place
+    int64_t blocks = (T * H + 255) / 256;
+    blocks = blocks > 8192 ? 8192 : blocks;
+    hipLaunchKernelGGL(widen_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a->x, T * H, w.xrot);
+    if ((rc = lsk::check_launch("widen_bf16_kernel"))) return rc;
+    if ((rc = lsk_fwht_blocks(w.xrot, T, H, H, rb, a->rot_scale, w.xrot, H, stream))) return rc;
+    rc = lsk_rowquant(w.xrot, LSK_F32, T, H, H, w.qx, H, w.ascx, stream);
+  } else {
+    rc = lsk_rowquant(a->x, LSK_BF16, T, H, H, w.qx, H, w.ascx, stream);
+  }
+  if (rc) return rc;
+  const size_t dsm = (size_t)(2 * E + 8 * E) * 4;
+  hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(256), dsm, s, a->idx, a->w, (int)T, k, (int)E, w.offs, w.tiles,
+                     w.row_tok, w.row_dst, w.row_w, w.tok_cnt);
+  if ((rc = lsk::check_launch("moe_dispatch_kernel"))) return rc;
+  {
+    int64_t blocks = (R + 255) / 256;
+    blocks = blocks > 1024 ? 1024 : (blocks < 1 ? 1 : blocks);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w.h_amax, R, 0u);
+    if ((rc = lsk::check_launch("fill_u32_kernel"))) return rc;
+  }
+  MoeGemmArgs g1{};
+  g1.A = w.qx;
+  g1.lda = H;
+  g1.a_scale = w.ascx;
+  g1.row_tok = w.row_tok;
+  g1.offs = w.offs;
+  g1.tiles = w.tiles;
+  g1.w_ptrs = a->w13_ptrs;
+  g1.ldw = a->ldw13;
+  g1.ws_ptrs = a->ws13_ptrs;
+  g1.b_ptrs = a->b13_ptrs;
+  g1.K = (int)H;
+  g1.N = (int)I;
+  g1.act = a->act;
+  g1.frac = a->frac;
+  g1.h = w.h;
+  g1.h_amax = w.h_amax;
+  if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) return rc;
+  if (rb > 0) {
+    hipLaunchKernelGGL(moe_rot_requant_kernel, dim3((unsigned)R), dim3(256), (size_t)I * 4, s, w.h, w.offs + E, (int)I,
+                       rb, a->rot_scale, w.qh, w.asch);
+    if ((rc = lsk::check_launch("moe_rot_requant_kernel"))) return rc;
+  } else {
+    int64_t blocks = (R * (I / 8) + 255) / 256;
+    blocks = blocks > 8192 ? 8192 : (blocks < 1 ? 1 : blocks);
+    hipLaunchKernelGGL(moe_requant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w.h, w.h_amax, w.offs + E, (int)I,
+                       w.qh, w.asch);
+    if ((rc = lsk::check_launch("moe_requant_kernel"))) return rc;
+  }
+  MoeGemmArgs g2{};
+  g2.A = w.qh;
+  g2.lda = I;
+  g2.a_scale = w.asch;
+  g2.offs = w.offs;
+  g2.tiles = w.tiles;
+  g2.w_ptrs = a->w2_ptrs;
+  g2.ldw = a->ldw2;
+  g2.ws_ptrs = a->ws2_ptrs;
+  g2.b_ptrs = a->b2_ptrs;
+  g2.K = (int)I;
+  g2.N = (int)H;
+  g2.row_w = w.row_w;
+  g2.row_dst = w.row_dst;
+  g2.y = w.slots;
+  if ((rc = launch_moe_gemm<1>(g2, w.max_tiles, (int)((H + 127) / 128), s, "moe_gemm_kernel<down>"))) return rc;
+  {
+    int64_t blocks = (T * (H / 8) + 255) / 256;
+    blocks = blocks > 8192 ? 8192 : (blocks < 1 ? 1 : blocks);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w.slots, H, k, w.tok_cnt, a->shared,
+                       T, a->y);
+    if ((rc = lsk::check_launch("moe_combine_kernel"))) return rc;
+  }
+  return LSK_OK;
+}

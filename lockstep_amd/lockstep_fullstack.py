@@ -65,6 +65,16 @@ def quantize_weight_int8(W):
     return W8.contiguous(), ws.contiguous()
 
 
+def silu_contract(x):
+    """The invariant SiLU: ten declared binary32 steps with the 8192-entry FRAC table."""
+    return ops.act(x, None, ops.OP_SILU)
+
+
+def fwht_blocks(x2, blk=256, scale=1.0 / 16.0):
+    """The R4 / online-R1 butterfly on every blk-wide block of the last dim, then * scale."""
+    return ops.fwht_blocks(x2, blk, scale)
+
+
 def pow2_f32(e):
     """Exact 2^e as float32 from the exponent field, e in [-126, 127]."""
     return ((e.to(torch.int32) + 127) << 23).view(torch.float32)

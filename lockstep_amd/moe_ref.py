@@ -7,8 +7,14 @@ Same names and signatures; GPU tensors only; results bit-identical to the refere
     lin_epilogue(acc, ws, asc)            moe_ref.py:40-42
     int_mm(a8, b8)                        moe_ref.py:48-55
     lin_epilogue_b(acc, ws, asc, bias)    moe_ref.py:164-169
+    table_scores, router_from_logits, router, router_b     moe_ref.py:64-97, 203-210
+    sigmoid_contract, act_swigluoai, act_silu              moe_ref.py:150-186
+    expert_swiglu, expert_block                            moe_ref.py:100-114, 189-200
+    moe_forward, moe_forward_b                             moe_ref.py:117-140, 213-230
 """
 from __future__ import annotations
+
+import ctypes
 
 import torch
 
@@ -49,3 +55,226 @@ def int_mm(a8: torch.Tensor, b8: torch.Tensor) -> torch.Tensor:
 def linear(q: torch.Tensor, asc: torch.Tensor, b8: torch.Tensor, ws: torch.Tensor, bias=None) -> torch.Tensor:
     """lin_epilogue_b(int_mm(q, b8), ws, asc, bias) in one launch (the fused form)."""
     return ops.gemm(q, ops.weight_nk(b8), L.EPI_V21, L.LSK_BF16_AS_F32, asc=asc, ws=ws, bias=bias)
+
+
+# ============================================================================ router (moe_ref.py:58-97, 203-210)
+BHI, TAB_N, TAB_W = 26, 13, 15
+ROUTER_C = float(2.0 ** BHI / 0.6931471805599453)   # rounded once to binary32 by the kernels
+SWIGLU_ALPHA = torch.tensor(1.702, dtype=F32)
+SWIGLU_LIMIT = 7.0
+
+
+def table_scores(dgap: torch.Tensor, tab: torch.Tensor) -> torch.Tensor:
+    """Integer router scores of the gaps dgap >= 0: the attention rule's table exponential."""
+    return ops.table_scores(dgap, tab)
+
+
+def router_from_logits(g: torch.Tensor, k: int, renormalize: bool, tab: torch.Tensor, win: int = 0):
+    """Top-k by table score (ties to the lower expert index) and w = bf16(s / S).
+    Returns (idx int64 [T, k] by rank, w bf16 [T, k], g bf16 [T, E])."""
+    idx, w = ops.router_topk(g, k, renormalize, tab)
+    return idx, w, g.to(BF)
+
+
+def router(x: torch.Tensor, gate_w8: torch.Tensor, gate_ws: torch.Tensor, k: int, renormalize: bool,
+           tab: torch.Tensor, win: int = 0):
+    """rowquant -> exact GEMM with the [H, E] gate -> v2.1 epilogue -> router_from_logits."""
+    q, asc = rowquant(x)
+    g = linear(q, asc, gate_w8, gate_ws)
+    return router_from_logits(g, k, renormalize, tab, win)
+
+
+def router_b(x, gate_w8, gate_ws, k, renormalize, tab, win, gate_bias=None):
+    """The router with an optional bias on the gate logits (a second bf16 rounding)."""
+    if gate_bias is None:
+        return router(x, gate_w8, gate_ws, k, renormalize, tab, win)
+    q, asc = rowquant(x)
+    g = linear(q, asc, gate_w8, gate_ws, gate_bias).to(BF)
+    return router_from_logits(g, k, renormalize, tab, win)
+
+
+# ============================================================================ activations (moe_ref.py:150-186)
+def sigmoid_contract(x: torch.Tensor) -> torch.Tensor:
+    """Steps (1)-(9) of the invariant SiLU: the table sigmoid, binary32 in and out."""
+    return ops.act(x, None, ops.OP_SIGMOID)
+
+
+def act_swigluoai(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """GPT-OSS clamped SwiGLU with the alpha-scaled table sigmoid; bf16 values in binary32."""
+    return ops.act(gate, up, ops.OP_ACT_SWIGLUOAI)
+
+
+def act_silu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """bfr(silu_table(g) * u)."""
+    return ops.act(gate, up, ops.OP_ACT_SILU)
+
+
+def _act_code(fn) -> int:
+    name = getattr(fn, "__name__", "")
+    if fn is act_silu or name == "act_silu":
+        return L.LSK_ACT_SILU
+    if fn is act_swigluoai or name == "act_swigluoai":
+        return L.LSK_ACT_SWIGLUOAI
+    raise NotImplementedError("the fused MoE layer runs the contract activations act_silu / act_swigluoai; "
+                              "got %r" % (fn,))
+
+
+# ============================================================================ expert blocks (moe_ref.py:100-114, 189-200)
+def _fwht(v, blk, scale):
+    return ops.fwht_blocks(v.to(F32), blk, scale)
+
+
+def expert_swiglu(x_rows, w13_8, ws13, w2_8, ws2, silu_fn, rot: bool = False):
+    """The v2.5 SwiGLU block on one expert's rows (w13_8 [H, 2I], w2_8 [I, H] column-major)."""
+    xin = _fwht(x_rows, 256, 1.0 / 16.0) if rot else x_rows
+    q, asc = rowquant(xin)
+    y = linear(q, asc, w13_8, ws13)
+    I = y.shape[-1] // 2
+    h = silu_fn(y[:, :I], y[:, I:])
+    hin = _fwht(h, 256, 1.0 / 16.0) if rot else h
+    q2, asc2 = rowquant(hin)
+    return linear(q2, asc2, w2_8, ws2)
+
+
+def expert_block(x_rows, w13_8, ws13, w2_8, ws2, act, b13=None, b2=None, rot_blk: int = 256):
+    """The expert block with biases and a parametrised R1 / R4 block (0 = no rotation)."""
+    def rot(v):
+        if not rot_blk:
+            return v
+        return _fwht(v, rot_blk, 1.0 / (rot_blk ** 0.5))
+    q, asc = rowquant(rot(x_rows))
+    y = linear(q, asc, w13_8, ws13, b13)
+    I = y.shape[-1] // 2
+    h = act(y[:, :I], y[:, I:])
+    q2, asc2 = rowquant(rot(h))
+    return linear(q2, asc2, w2_8, ws2, b2)
+
+
+# ============================================================================ the fused layer (moe_ref.py:117-140, 213-230)
+class ExpertTables:
+    """Device address tables of the experts' int8 weights, scales and biases, as the fused
+    layer reads them.  experts[e] = (w13col [H, 2I], ws13 [2I], w2col [I, H], ws2 [H][, b13, b2]),
+    each w*col the transpose view of a row-major [N, K] int8 matrix (else it is copied once)."""
+
+    def __init__(self, experts):
+        if not experts:
+            raise ValueError("no experts")
+        ex0 = experts[0]
+        L.require_cuda(ex0[0], what="experts")
+        self.device = ex0[0].device
+        self.E = len(experts)
+        self.H = int(ex0[0].shape[0])
+        self.I = int(ex0[0].shape[1]) // 2
+        keep = []
+        w13, ws13, w2, ws2, b13, b2 = [], [], [], [], [], []
+        for ex in experts:
+            W13 = ops.weight_nk(ex[0])
+            W2 = ops.weight_nk(ex[2])
+            if W13.dtype != torch.int8 or W2.dtype != torch.int8:
+                raise TypeError("expert weights must be int8")
+            if tuple(W13.shape) != (2 * self.I, self.H) or tuple(W2.shape) != (self.H, self.I):
+                raise ValueError("expert shapes differ: %s / %s" % (tuple(W13.shape), tuple(W2.shape)))
+            s13 = ex[1].to(F32).contiguous()
+            s2 = ex[3].to(F32).contiguous()
+            c13 = ex[4].to(F32).contiguous() if len(ex) > 4 and ex[4] is not None else None
+            c2 = ex[5].to(F32).contiguous() if len(ex) > 5 and ex[5] is not None else None
+            keep += [W13, W2, s13, s2, c13, c2]
+            w13.append(W13)
+            w2.append(W2)
+            ws13.append(s13.data_ptr())
+            ws2.append(s2.data_ptr())
+            b13.append(c13.data_ptr() if c13 is not None else 0)
+            b2.append(c2.data_ptr() if c2 is not None else 0)
+        ld13 = {t.stride(0) for t in w13}
+        ld2 = {t.stride(0) for t in w2}
+        if len(ld13) != 1 or ld13.pop() % 16 or any(t.stride(0) != w13[0].stride(0) for t in w13):
+            w13 = [t.contiguous() for t in w13]
+            keep += w13
+        if len(ld2) != 1 or w2[0].stride(0) % 16:
+            w2 = [t.contiguous() for t in w2]
+            keep += w2
+        self.ldw13 = int(w13[0].stride(0))
+        self.ldw2 = int(w2[0].stride(0))
+        dev = self.device
+
+        def table(vals):
+            return torch.tensor(vals, dtype=torch.int64).to(dev)
+        self.w13 = table([t.data_ptr() for t in w13])
+        self.w2 = table([t.data_ptr() for t in w2])
+        self.ws13 = table(ws13)
+        self.ws2 = table(ws2)
+        self.b13 = table(b13) if any(b13) else None
+        self.b2 = table(b2) if any(b2) else None
+        self._keep = keep
+
+
+_TABLES = {}
+
+
+def expert_tables(experts) -> ExpertTables:
+    """Cached ExpertTables for an experts list (keyed by every tensor's address and version)."""
+    if isinstance(experts, ExpertTables):
+        return experts
+    key = (id(experts),) + tuple((t.data_ptr(), t._version) for ex in experts for t in ex if t is not None)
+    hit = _TABLES.get(key)
+    if hit is None:
+        if len(_TABLES) >= 8:
+            _TABLES.pop(next(iter(_TABLES)))
+        hit = _TABLES[key] = ExpertTables(experts)
+    return hit
+
+
+def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_out=None):
+    L.require_cuda(x, idx, w, what="moe_forward")
+    if x.dtype != BF:
+        raise TypeError("moe_forward: x must be bf16 [T, H] (got %s)" % x.dtype)
+    x = x.contiguous()
+    T, H = x.shape
+    k = int(idx.shape[1])
+    if H != tables.H:
+        raise ValueError("moe_forward: x width %d != expert H %d" % (H, tables.H))
+    idx = idx.to(torch.int64).contiguous()
+    w = w.to(BF).contiguous()
+    y = torch.empty((T, H), dtype=BF, device=x.device)
+    if T == 0:
+        return y
+    nbytes = L.load().lsk_moe_workspace(T, k, tables.E, H, tables.I, rot_blk)
+    work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
+    sh = None if shared_out is None else shared_out.to(F32).contiguous()
+    a = L.MoeArgs(T=T, H=H, I=tables.I, E=tables.E, k=k, act=act, x=x.data_ptr(), idx=idx.data_ptr(),
+                  w=w.data_ptr(), w13_ptrs=tables.w13.data_ptr(), ldw13=tables.ldw13,
+                  ws13_ptrs=tables.ws13.data_ptr(),
+                  b13_ptrs=tables.b13.data_ptr() if tables.b13 is not None else None,
+                  w2_ptrs=tables.w2.data_ptr(), ldw2=tables.ldw2, ws2_ptrs=tables.ws2.data_ptr(),
+                  b2_ptrs=tables.b2.data_ptr() if tables.b2 is not None else None,
+                  frac=ops.frac_i32(x.device).data_ptr(), rot_blk=int(rot_blk),
+                  rot_scale=(1.0 / (rot_blk ** 0.5)) if rot_blk else 0.0,
+                  shared=sh.data_ptr() if sh is not None else None, y=y.data_ptr(),
+                  workspace=work.data_ptr(), workspace_bytes=nbytes)
+    L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
+    return y
+
+
+def moe_forward(x: torch.Tensor, gate, experts, k: int, renormalize: bool, tab: torch.Tensor, win: int, silu_fn,
+                shared=None, routing=None, rot: bool = False):
+    """x bf16 [T, H] -> (y bf16 [T, H], idx, w).  routing=(idx, w) injects a routing; the
+    declared router runs otherwise.  experts: the reference's list, or an ExpertTables."""
+    if routing is None:
+        idx, w, _ = router(x, gate[0], gate[1], k, renormalize, tab, win)
+    else:
+        idx, w = routing[0].to(torch.int64), routing[1].to(BF)
+    tables = expert_tables(experts)
+    sh = shared(x) if shared is not None else None
+    y = _moe_layer(x, idx, w, tables, _act_code(silu_fn), 256 if rot else 0, sh)
+    return y, idx, w
+
+
+def moe_forward_b(x, gate, experts, k, renormalize, tab, win, act, rot_blk=256, routing=None):
+    """moe_forward for the GPT-OSS addendum: biased gate and experts, act_silu or
+    act_swigluoai, rot_blk the R1 / R4 block (0 = none)."""
+    if routing is None:
+        idx, w, _ = router_b(x, gate[0], gate[1], k, renormalize, tab, win, gate[2] if len(gate) > 2 else None)
+    else:
+        idx, w = routing[0].to(torch.int64), routing[1].to(BF)
+    y = _moe_layer(x, idx, w, expert_tables(experts), _act_code(act), int(rot_blk or 0))
+    return y, idx, w

@@ -133,3 +133,70 @@ def quant8_pow2(x: torch.Tensor, mode: int):
     L.call("lsk_quant8_pow2", L.ptr(x), M, K, max(K, 1), mode, L.ptr(q), max(K, 1), L.ptr(e), L.ptr(work),
            L.stream_of(x))
     return q, e[:ne]
+
+
+OP_SILU, OP_SIGMOID, OP_ACT_SILU, OP_ACT_SWIGLUOAI = 0, 1, 2, 3
+
+
+def frac_i32(dev) -> torch.Tensor:
+    """The FRAC (13, 15) table as int32 on `dev` (values < 2^16), built once per device."""
+    from . import contract_common as CC
+    return CC.table_i32_on(dev)
+
+
+def tab_i32(tab: torch.Tensor) -> torch.Tensor:
+    """A caller's router table (int64 in the reference) as the int32 table the kernels read."""
+    L.require_cuda(tab, what="table")
+    if tab.numel() != 8192:
+        raise ValueError("the router table must have 8192 entries (TAB_N = 13), got %d" % tab.numel())
+    return tab.to(torch.int32).contiguous()
+
+
+def act(g: torch.Tensor, u, op: int) -> torch.Tensor:
+    """Elementwise table activation in binary32 (shape of g)."""
+    L.require_cuda(g, u, what="activation")
+    gf = g.to(torch.float32).contiguous()
+    uf = None
+    if u is not None:
+        uf = u.to(torch.float32)
+        if uf.shape != gf.shape:
+            uf = uf.expand(gf.shape)
+        uf = uf.contiguous()
+    out = torch.empty_like(gf)
+    L.call("lsk_act_elementwise", L.ptr(gf), L.ptr(uf), gf.numel(), op, L.ptr(frac_i32(g.device)), L.ptr(out),
+           L.stream_of(g))
+    return out
+
+
+def table_scores(dgap: torch.Tensor, tab: torch.Tensor) -> torch.Tensor:
+    L.require_cuda(dgap, tab, what="table_scores")
+    d = dgap.to(torch.float32).contiguous()
+    out = torch.empty(d.shape, dtype=torch.int64, device=d.device)
+    L.call("lsk_table_scores", L.ptr(d), d.numel(), L.ptr(tab_i32(tab)), L.ptr(out), L.stream_of(d))
+    return out
+
+
+def fwht_blocks(x: torch.Tensor, blk: int = 256, scale: float = 1.0 / 16.0) -> torch.Tensor:
+    L.require_cuda(x, what="fwht_blocks")
+    sh = x.shape
+    x2 = x.to(torch.float32).reshape(-1, sh[-1]).contiguous()
+    y = torch.empty_like(x2)
+    L.call("lsk_fwht_blocks", L.ptr(x2), x2.shape[0], x2.shape[1], x2.shape[1], int(blk), float(scale), L.ptr(y),
+           x2.shape[1], L.stream_of(x))
+    return y.reshape(sh)
+
+
+def router_topk(g: torch.Tensor, k: int, renormalize: bool, tab: torch.Tensor):
+    """Top-k routing from logits g [T, E] (bf16 values): (idx int64 [T, k], w bf16 [T, k])."""
+    L.require_cuda(g, tab, what="router")
+    T, E = g.shape
+    if g.dtype == torch.bfloat16:
+        gd, code = g.contiguous(), L.LSK_BF16
+    else:
+        gd, code = g.to(torch.float32).contiguous(), L.LSK_F32
+    idx = torch.empty((T, k), dtype=torch.int64, device=g.device)
+    w = torch.empty((T, k), dtype=torch.bfloat16, device=g.device)
+    if T:
+        L.call("lsk_router_topk", L.ptr(gd), code, E, T, E, int(k), 1 if renormalize else 0, L.ptr(tab_i32(tab)),
+               L.ptr(idx), L.ptr(w), L.stream_of(g))
+    return idx, w

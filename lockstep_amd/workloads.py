@@ -41,3 +41,43 @@ def dense_inputs(M, N, K, seed=0, outliers=False):
     x = activations(g, M, K, outliers)
     W8, ws = int8_weight(g, N, K)
     return x, W8, ws
+
+
+# ---------------------------------------------------------------- MoE
+QWEN3_30B_A3B = dict(E=128, k=8, H=2048, I=768)     # per-expert SwiGLU
+GPT_OSS_20B = dict(E=32, k=4, H=2880, I=2880)
+
+
+def _bf16_round(x):
+    u = np.ascontiguousarray(x, dtype=F32).view(np.uint32).astype(np.uint64)
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    return (b << 16).view(F32)
+
+
+def zipf_logits(g, T, E, s=1.1):
+    """Router logits N(0,1) plus an expert-popularity bias -s * ln(1 + rank_e) over a random
+    rank permutation: routing probabilities follow a Zipf(s) law, so loads are skewed."""
+    rank = g.permutation(E)
+    bias = (-s * np.log1p(rank)).astype(F32)
+    return _bf16_round(g.standard_normal((T, E), dtype=np.float64).astype(F32) + bias[None, :])
+
+
+def moe_int8_experts(g, E, H, I, bias=False):
+    """experts[e] = (w13 [2I, H] int8, ws13 [2I], w2 [H, I] int8, ws2 [H], b13 | None, b2 | None)."""
+    out = []
+    for _ in range(E):
+        w13, ws13 = int8_weight(g, 2 * I, H)
+        w2, ws2 = int8_weight(g, H, I)
+        b13 = (g.standard_normal(2 * I) * 0.1).astype(F32) if bias else None
+        b2 = (g.standard_normal(H) * 0.1).astype(F32) if bias else None
+        out.append((w13, ws13, w2, ws2, b13, b2))
+    return out
+
+
+def moe_inputs(T, E, k, H, I, seed=0, bias=False, zipf=True):
+    """x [T, H] (bf16 values as f32), experts (moe_int8_experts), logits [T, E] (bf16 values)."""
+    g = rng(seed)
+    x = _bf16_round(g.standard_normal((T, H), dtype=np.float64).astype(F32))
+    logits = zipf_logits(g, T, E) if zipf else _bf16_round(g.standard_normal((T, E), dtype=np.float64).astype(F32))
+    experts = moe_int8_experts(g, E, H, I, bias)
+    return x, experts, logits

@@ -478,12 +478,12 @@ def expert_block_mx(x_rows, w13, w2, act, b13=None, b2=None):
 
 
 # ----------------------------------------------------------------------------- A11 MoE layers
-def _combine(T, H, idx, w, expert_out):
-    """moe_ref.py:127-140: for e ascending, acc[tok] += bfr(w_e * out) in binary32 from +0."""
+def _combine(T, H, idx, w, expert_out, E):
+    """moe_ref.py:127-140: for e in range(E) ascending, acc[tok] += bfr(w_e * out) in binary32
+    from +0 (routing entries outside [0, E) are never visited)."""
     idx = np.asarray(idx, np.int64)
     wf = bf16_to_f32(w)
     acc = np.zeros((T, H), F32)
-    E = int(idx.max()) + 1 if idx.size else 0
     for e in range(E):
         hit = idx == e
         if not hit.any():
@@ -495,12 +495,16 @@ def _combine(T, H, idx, w, expert_out):
     return acc
 
 
-def moe_forward(x, experts, idx, w, act=act_silu, rot=False):
+def moe_forward(x, experts, idx, w, act=act_silu, rot=False, shared_out=None):
     """moe_ref.py:117-140 with routing=(idx, w) injected; x [T, H] binary32 values (bf16 in
-    the reference); experts[e] = (w13col, ws13, w2col, ws2).  Returns y as bf16 bits."""
+    the reference); experts[e] = (w13col, ws13, w2col, ws2); shared_out: the shared expert's
+    output [T, H] (added as bfr(shared) after every routed expert).  Returns y as bf16 bits."""
     x = np.asarray(x, F32)
     T, H = x.shape
-    acc = _combine(T, H, idx, w, lambda e, tok: expert_swiglu(x[tok], *experts[e][:4], act=act, rot=rot))
+    acc = _combine(T, H, idx, w, lambda e, tok: expert_swiglu(x[tok], *experts[e][:4], act=act, rot=rot),
+                   len(experts))
+    if shared_out is not None:
+        acc = (acc + bfr(np.asarray(shared_out, F32))).astype(F32)
     return bf16_bits(acc)
 
 
@@ -513,7 +517,7 @@ def moe_forward_b(x, experts, idx, w, act, rot_blk=256):
         ex = experts[e]
         return expert_block(x[tok], ex[0], ex[1], ex[2], ex[3], act,
                             ex[4] if len(ex) > 4 else None, ex[5] if len(ex) > 5 else None, rot_blk)
-    return bf16_bits(_combine(T, H, idx, w, run))
+    return bf16_bits(_combine(T, H, idx, w, run, len(experts)))
 
 
 def moe_forward_mx(x, experts, idx, w, act):
@@ -525,7 +529,7 @@ def moe_forward_mx(x, experts, idx, w, act):
         ex = experts[e]
         return expert_block_mx(x[tok], ex[0], ex[1], act,
                                ex[2] if len(ex) > 2 else None, ex[3] if len(ex) > 3 else None)
-    return bf16_bits(_combine(T, H, idx, w, run))
+    return bf16_bits(_combine(T, H, idx, w, run, len(experts)))
 
 
 # ----------------------------------------------------------------------------- digest (tools/contract_vectors.py:40-49)

@@ -1,0 +1,212 @@
+"""GPU parity of the contract v3 MoE path (router, activations, rotation, fused int8 layer)
+against the oracle, bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_dev, bits, dev, f32_bits, say, to_dev
+from moe_util import device_experts, oracle_experts, routing_device, routing_from_logits, u16
+from oracle import contract as C
+from vector_inputs import load_vectors, silu_r4_inputs
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _tab():
+    from lockstep_amd import contract_common as CC
+    return CC.table_on(dev())
+
+
+# ------------------------------------------------------------------ elementwise operators
+def test_silu_and_r4_digests_on_gpu():
+    from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import moe_ref as MR
+    V = load_vectors()
+    gate, up, v = silu_r4_inputs()
+    s = FS.silu_contract(to_dev(gate))
+    assert C.digest(bits(s).view(F32), "float32") == V["silu"]["sha256"]
+    sm = (s * to_dev(up)).to(torch.bfloat16)
+    assert C.digest(u16(sm), "bfloat16") == V["silu_mul"]["sha256"]
+    am = MR.act_silu(to_dev(gate), to_dev(up)).to(torch.bfloat16)
+    assert C.digest(u16(am), "bfloat16") == V["silu_mul"]["sha256"]
+    r4 = FS.fwht_blocks(to_dev(v))
+    assert C.digest(bits(r4).view(F32), "float32") == V["r4.block256"]["sha256"]
+
+
+def test_activations_parity_wide_range():
+    from lockstep_amd import moe_ref as MR
+    r = np.random.default_rng(1)
+    x = np.concatenate([r.standard_normal(20000) * 8, np.linspace(-40, 40, 4001),
+                        [0.0, -0.0, 1e-39, -1e-39, 1e-30, 30.0, -30.0, 1e30, -1e30]]).astype(F32)
+    u = C.bfr(r.standard_normal(x.size).astype(F32) * 5)
+    xb = C.bfr(x)
+    assert np.array_equal(bits(MR.sigmoid_contract(to_dev(x))), f32_bits(C.sigmoid_contract(x)))
+    from lockstep_amd import lockstep_fullstack as FS
+    assert np.array_equal(bits(FS.silu_contract(to_dev(x))), f32_bits(C.silu_contract(x)))
+    assert np.array_equal(bits(MR.act_silu(to_dev(xb), to_dev(u))), f32_bits(C.act_silu(xb, u)))
+    assert np.array_equal(bits(MR.act_swigluoai(to_dev(xb), to_dev(u))), f32_bits(C.act_swigluoai(xb, u)))
+
+
+@pytest.mark.parametrize("blk", [64, 256])
+def test_fwht_parity(blk):
+    from lockstep_amd import lockstep_fullstack as FS
+    r = np.random.default_rng(blk)
+    x = (r.standard_normal((7, 768)) * 3).astype(F32)
+    y = FS.fwht_blocks(to_dev(x), blk=blk, scale=1.0 / blk ** 0.5)
+    assert np.array_equal(bits(y), f32_bits(C.fwht_blocks(x, blk, 1.0 / blk ** 0.5)))
+
+
+# ------------------------------------------------------------------ router
+@pytest.mark.parametrize("E,k", [(8, 2), (32, 4), (128, 8), (1000, 7)])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_router_parity(E, k, renorm):
+    from lockstep_amd import moe_ref as MR
+    r = np.random.default_rng(E * 10 + k)
+    T = 257
+    g = C.bfr((r.standard_normal((T, E)) * 2).astype(F32))
+    g[:40] = C.bfr((r.integers(-6, 6, (40, E)) / 4.0).astype(F32))     # tie-dense rows
+    g[40] = 0.0                                                          # all tied
+    idx, w, gb = MR.router_from_logits(to_dev(g), k, renorm, _tab())
+    ridx, rw, rg = C.router_from_logits(g, k, renorm)
+    assert np.array_equal(bits(idx), ridx)
+    assert np.array_equal(u16(w), rw)
+    assert np.array_equal(u16(gb), rg)
+    dg = np.abs(r.standard_normal(5000) * 6).astype(F32)
+    assert np.array_equal(bits(MR.table_scores(to_dev(dg), _tab())), C.table_scores(dg))
+
+
+def test_router_from_hidden_states():
+    from lockstep_amd import moe_ref as MR
+    r = np.random.default_rng(3)
+    T, H, E, k = 40, 256, 16, 4
+    x = C.bfr(r.standard_normal((T, H)).astype(F32))
+    gw = r.integers(-127, 128, (E, H), dtype=np.int8)
+    gws = r.uniform(1e-3, 1e-2, E).astype(F32)
+    gb = (r.standard_normal(E) * 0.1).astype(F32)
+    idx, w, _ = MR.router(bf16_dev(x), to_dev(gw).t(), to_dev(gws), k, True, _tab())
+    ridx, rw, _ = C.router(x, gw.T, gws, k, True)
+    assert np.array_equal(bits(idx), ridx) and np.array_equal(u16(w), rw)
+    idx, w, _ = MR.router_b(bf16_dev(x), to_dev(gw).t(), to_dev(gws), k, True, _tab(), 0, to_dev(gb))
+    ridx, rw, _ = C.router(x, gw.T, gws, k, True, gate_bias=gb)
+    assert np.array_equal(bits(idx), ridx) and np.array_equal(u16(w), rw)
+
+
+# ------------------------------------------------------------------ the fused int8 layer
+def _run_case(T, E, k, H, I, seed, bias=False, act="silu", rot_blk=0, zipf=True, shared=False,
+              routing_override=None):
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("moe case", dict(T=T, E=E, k=k, H=H, I=I, seed=seed, bias=bias, act=act, rot_blk=rot_blk))
+    x, experts, logits = WL.moe_inputs(T, E, k, H, I, seed=seed, bias=bias, zipf=zipf)
+    idx, w = routing_from_logits(logits, k) if routing_override is None else routing_override
+    dx = bf16_dev(x)
+    dexp = device_experts(experts)
+    ridx, rw = routing_device(idx, w)
+    oact = C.act_silu if act == "silu" else C.act_swigluoai
+    dact = MR.act_silu if act == "silu" else MR.act_swigluoai
+    sh_np = None
+    if shared:
+        sh_np = (np.random.default_rng(seed).standard_normal((T, H)) * 0.3).astype(F32)
+    if bias or act != "silu" or rot_blk not in (0, 256):
+        y, _, _ = MR.moe_forward_b(dx, None, dexp, k, True, _tab(), 0, dact, rot_blk=rot_blk, routing=(ridx, rw))
+        ref = C.moe_forward_b(x, oracle_experts(experts, True), idx, w, oact, rot_blk=rot_blk)
+    else:
+        sfn = (lambda xx: to_dev(sh_np)) if shared else None
+        y, _, _ = MR.moe_forward(dx, None, dexp, k, True, _tab(), 0, dact, shared=sfn, routing=(ridx, rw),
+                                 rot=rot_blk == 256)
+        ref = C.moe_forward(x, oracle_experts(experts), idx, w, act=oact, rot=rot_blk == 256, shared_out=sh_np)
+    got = u16(y)
+    assert got.shape == ref.shape
+    bad = int((got != ref).sum())
+    assert bad == 0, "%d of %d outputs differ" % (bad, got.size)
+
+
+def test_moe_small():
+    _run_case(24, 8, 2, 256, 128, seed=3)
+
+
+def test_moe_single_token_and_zero_load_experts():
+    _run_case(1, 16, 4, 256, 128, seed=4)
+
+
+def test_moe_skewed_multi_tile_expert():
+    """Every token routed to experts {0, 1}: expert tiles of up to 300 rows (3 M-tiles)."""
+    T, E, k = 300, 6, 2
+    idx = np.tile(np.array([[1, 0]]), (T, 1)).astype(np.int64)
+    w = C.bf16_bits(np.tile(np.array([[0.75, 0.25]], F32), (T, 1)))
+    _run_case(T, E, k, 128, 64, seed=5, routing_override=(idx, w))
+
+
+def test_moe_skipped_experts_out_of_range():
+    """Routing entries outside [0, E) are skipped, as the reference's loop over range(E) does."""
+    T, E, k = 20, 4, 3
+    r = np.random.default_rng(6)
+    idx = np.stack([r.permutation(6)[:k] for _ in range(T)]).astype(np.int64)   # some >= E
+    w = C.bf16_bits(r.uniform(0, 1, (T, k)).astype(F32))
+    _run_case(T, E, k, 128, 64, seed=6, routing_override=(idx, w))
+
+
+def test_moe_bias_swigluoai():
+    _run_case(40, 8, 3, 256, 192, seed=7, bias=True, act="swigluoai")
+
+
+def test_moe_shared_expert():
+    _run_case(30, 8, 2, 256, 128, seed=8, shared=True)
+
+
+@pytest.mark.parametrize("rot_blk", [256, 64])
+def test_moe_rotation(rot_blk):
+    _run_case(33, 8, 2, 512, 256, seed=9, rot_blk=rot_blk)
+
+
+def test_expert_swiglu_and_block_composed():
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    x, experts, _ = WL.moe_inputs(19, 1, 1, 256, 256, seed=10, bias=True)
+    w13, ws13, w2, ws2, b13, b2 = experts[0]
+    dx = bf16_dev(x)
+    d = device_experts(experts)[0]
+    for rot in (False, True):
+        y = MR.expert_swiglu(dx, d[0], d[1], d[2], d[3], MR.act_silu, rot=rot)
+        ref = C.expert_swiglu(x, w13.T, ws13, w2.T, ws2, act=C.act_silu, rot=rot)
+        assert np.array_equal(bits(y), f32_bits(ref))
+    y = MR.expert_block(dx, d[0], d[1], d[2], d[3], MR.act_swigluoai, d[4], d[5], rot_blk=64)
+    ref = C.expert_block(x, w13.T, ws13, w2.T, ws2, C.act_swigluoai, b13, b2, rot_blk=64)
+    assert np.array_equal(bits(y), f32_bits(ref))
+
+
+# ------------------------------------------------------------------ the Qwen3-30B-A3B shapes (E=128, k=8, H=2048, I=768)
+@pytest.mark.parametrize("T", [1, 32])
+def test_config4_full_bit_exact(T):
+    from lockstep_amd import workloads as WL
+    c = WL.QWEN3_30B_A3B
+    _run_case(T, c["E"], c["k"], c["H"], c["I"], seed=40 + T)
+
+
+def test_config4_t4096_token_subset():
+    """T=4096 on the device; a seeded subset of tokens against the oracle run on just those
+    tokens (a token's output depends only on its own row and routing)."""
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    c = WL.QWEN3_30B_A3B
+    T = 4096
+    say("config4 T=4096")
+    x, experts, logits = WL.moe_inputs(T, c["E"], c["k"], c["H"], c["I"], seed=44)
+    dx = bf16_dev(x)
+    dexp = device_experts(experts)
+    idx_d, w_d, _ = MR.router_from_logits(to_dev(logits), c["k"], True, _tab())
+    idx, w = routing_from_logits(logits, c["k"])
+    assert np.array_equal(bits(idx_d), idx) and np.array_equal(u16(w_d), w)
+    loads = np.bincount(idx.reshape(-1), minlength=c["E"])
+    say("expert loads: max %d, min %d, zero-load experts %d" % (loads.max(), loads.min(), (loads == 0).sum()))
+    y, _, _ = MR.moe_forward(dx, None, dexp, c["k"], True, _tab(), 0, MR.act_silu, routing=(idx_d, w_d))
+    rows = np.sort(np.random.default_rng(1).choice(T, 48, replace=False))
+    ref = C.moe_forward(x[rows], oracle_experts(experts), idx[rows], w[rows])
+    assert np.array_equal(u16(y)[rows], ref)
