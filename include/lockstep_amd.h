@@ -113,6 +113,39 @@ int lsk_gemm_select(int tile_id);
 int lsk_quant8_pow2(const float* x, int64_t M, int64_t K, int64_t ldx, int mode,
                     int8_t* q, int64_t ldq, int32_t* e_out, void* workspace, void* stream);
 
+/* ---------------------------------------------------------------- the MXFP4 operand */
+
+/* The MXFP4-consuming GEMM (contract addendum item 5).  Replaces moe_ref.int_mm_mx and,
+ * with epilogue = 1, lin_epilogue_mx (reference/moe_ref.py:243-261):
+ *   for each 32-wide K block b, ascending: s = sum_{j in b} a[m, j] * m2[n, j] (exact);
+ *   acc = fl32(acc + fl32(s) * 2^(kexp[n, b] - 128)), from +0;
+ *   epilogue 0: out = acc (binary32); 1: out = bfr(acc * asc[m]), then bfr(out + bias[n]).
+ * a: [M, K] int8 (row stride lda); weights either m2 int8 [N, K] (b_fmt 0, the reference's
+ * doubled mantissas in {0, +-1, +-2, +-3, +-4, +-6, +-8, +-12}) or packed E2M1 codes
+ * [N, K/2] (b_fmt 1, low nibble first), row stride ldb bytes; kexp: E8M0 bytes [N, K/32],
+ * row stride lds; out: [M, N] binary32 (row stride ldo).  K % 32 == 0. */
+int lsk_gemm_mx(const int8_t* a, int64_t lda, const void* b, int b_fmt, int64_t ldb, const uint8_t* kexp,
+                int64_t lds, int64_t M, int64_t N, int64_t K, int epilogue, const float* asc, const float* bias,
+                float* out, int64_t ldo, void* stream);
+
+/* The MX epilogue alone (replaces moe_ref.lin_epilogue_mx, reference/moe_ref.py:258-261):
+ * out = bfr(acc[m, n] * asc[m]), then bfr(out + bias[n]) when bias is given.  acc, out:
+ * [M, N] binary32 contiguous (out may equal acc). */
+int lsk_mx_epilogue(const float* acc, int64_t M, int64_t N, const float* asc, const float* bias, float* out,
+                    void* stream);
+
+/* Exact MXFP4 dequant (replaces moe_mxfp4.dequant_mxfp4, reference/moe_mxfp4.py:26-35):
+ * out[r, k] = fp4(code[r, k]) * 2^(scale[r, k / block] - 127), rounded to out_dtype (exact for
+ * every finite result; scale 255 gives 2^128 = inf as the reference's ldexp does).
+ * packed: [rows, K/2] uint8 (low nibble = even element); scale: [rows, K/block] uint8;
+ * out: [rows, K] of out_dtype (LSK_BF16 or LSK_F32), contiguous. */
+int lsk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t K, int block, void* out,
+                      int out_dtype, void* stream);
+
+/* Pack doubled mantissas m2 (int8 [n]) into E2M1 codes (uint8 [n / 2], low nibble first);
+ * *bad (device int32, caller-zeroed) receives 1 if some m2 is not 2 * an E2M1 value. */
+int lsk_mx_pack_m2(const int8_t* m2, int64_t n, uint8_t* packed, int32_t* bad, void* stream);
+
 /* ---------------------------------------------------------------- mixture of experts (v3) */
 
 /* Activation of the gate/up pair in the expert block. */
@@ -159,13 +192,15 @@ int lsk_table_scores(const float* dgap, int64_t n, const int32_t* tab, int64_t* 
 int lsk_fwht_blocks(const float* x, int64_t rows, int64_t D, int64_t ldx, int blk, float scale, float* y,
                     int64_t ldy, void* stream);
 
-/* The whole contract v3 MoE layer with int8 experts and injected routing.
- * Replaces moe_ref.moe_forward / moe_forward_b with routing=(idx, w), rot off
- * (reference/moe_ref.py:117-140, 189-200, 213-230):
+/* The whole contract v3 MoE layer with int8 or MXFP4 experts and injected routing.
+ * Replaces moe_ref.moe_forward / moe_forward_b / moe_forward_mx with routing=(idx, w)
+ * (reference/moe_ref.py:117-140, 189-200, 213-230, 264-290):
  *   for each expert e ascending and the tokens that chose it: rowquant(x) -> exact GEMM with
  *   w13[e] -> bfr(V21 epilogue) (+ bfr(+ b13)) -> act(gate, up) -> rowquant -> exact GEMM with
  *   w2[e] -> bfr(V21) (+ bfr(+ b2)); y[t] = bf16(sum over t's experts ascending of
- *   bfr(w * out), binary32 adds from +0) (+ bfr(shared[t]) last).
+ *   bfr(w * out), binary32 adds from +0) (+ bfr(shared[t]) last).  With MXFP4 experts each
+ *   GEMM is the MX operand (ordered binary32 block updates, see lsk_gemm_mx) and its epilogue
+ *   bfr(acc * asc[m]) (+ bfr(+ b)); no rotation.
  * Expert weights are given as device tables of E device addresses (int64): w13_ptrs -> int8
  * [2I, H] (row stride ldw13), ws13_ptrs -> f32 [2I], w2_ptrs -> int8 [H, I] (row stride ldw2),
  * ws2_ptrs -> f32 [H], b13_ptrs / b2_ptrs -> f32 [2I] / [H] (the tables may be NULL for no
@@ -179,6 +214,13 @@ typedef struct {
   int64_t T, H, I, E;
   int k;
   int act;                       /* lsk_act */
+  int wfmt;                      /* 0: int8 experts; 1: MXFP4 experts (moe_forward_mx): w13/w2 tables
+                                    point at packed E2M1 codes [N, K/2] (low nibble first, row stride
+                                    ldw* bytes) and ws13/ws2 tables at their E8M0 bytes [N, K/32]
+                                    (row stride lds* bytes); K % 32 == 0 */
+  int mx_safe;                   /* MXFP4: 1 when some E8M0 byte is >= 240 (exact multiply-then-add
+                                    block update instead of the fused one) */
+  int64_t lds13, lds2;           /* MXFP4: E8M0 row strides */
   const uint16_t* x;             /* [T, H] bf16 */
   const int64_t* idx;            /* [T, k] */
   const uint16_t* w;             /* [T, k] bf16 */
@@ -200,7 +242,7 @@ typedef struct {
   int64_t workspace_bytes;
 } lsk_moe_args;
 
-int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk);
+int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt);
 
 int lsk_moe_forward(const lsk_moe_args* args, void* stream);
 

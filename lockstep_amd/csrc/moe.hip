@@ -15,12 +15,13 @@
 //   6. combine: per token, binary32 adds of its slots in ascending expert order from +0.
 #include "contract_act.h"
 #include "mfma_tile.h"
+#include "moe_internal.h"
 
 namespace {
 
 constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
 constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
-constexpr int kBM = 128;
+constexpr int kBM = lsk::kMoeBM;
 
 // ---------------------------------------------------------------- router
 LSK_DEV long long wave_max_ll(long long v) {
@@ -187,27 +188,7 @@ __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p,
 }
 
 // ---------------------------------------------------------------- grouped GEMM
-struct MoeGemmArgs {
-  const int8_t* A;
-  int64_t lda;
-  const float* a_scale;     // per A row
-  const int32_t* row_tok;   // gate/up: permuted row -> token (A row); down: unused
-  const int32_t* offs;      // [E + 1]
-  const int32_t* tiles;     // [0] count, then (expert, first row) pairs
-  const int64_t* w_ptrs;    // [E]
-  int64_t ldw;
-  const int64_t* ws_ptrs;   // [E]
-  const int64_t* b_ptrs;    // [E] or null
-  int K;
-  int N;                    // gate/up: I (h columns); down: H
-  int act;
-  const int32_t* frac;
-  uint16_t* h;              // gate/up out [R, I]
-  uint32_t* h_amax;         // [R]
-  const float* row_w;       // down: routing weight per row
-  const int32_t* row_dst;   // down: destination slot row
-  uint16_t* y;              // down out [T * k, N]
-};
+using lsk::MoeGemmArgs;
 
 // MODE 0: gate/up + activation; MODE 1: down + routing weight.
 template <int MODE>
@@ -235,7 +216,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     lsk::chunk_of<C::kThreads>(tid, j, row, c);
     const int p = p0 + row;
     const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
-    pa[j] = src >= 0 ? a.A + (int64_t)src * a.lda : nullptr;
+    pa[j] = src >= 0 ? (const int8_t*)a.A + (int64_t)src * a.lda : nullptr;
   }
 #pragma unroll
   for (int j = 0; j < C::kBPer; ++j) {
@@ -474,7 +455,8 @@ struct MoeWs {
 
 inline int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
 
-MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk) {
+MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt) {
+  const int64_t qb = wfmt == 1 ? 2 : 1;  // bytes per quantised activation element
   MoeWs w{};
   const int64_t R = T * k;
   w.max_tiles = R / kBM + (E < R ? E : R);
@@ -484,7 +466,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
     off += up256(nbytes);
     return p;
   };
-  w.qx = (int8_t*)take(T * H);
+  w.qx = (int8_t*)take(T * H * qb);
   w.ascx = (float*)take(T * 4);
   w.offs = (int32_t*)take((E + 1) * 4);
   w.tiles = (int32_t*)take((1 + 2 * w.max_tiles) * 4);
@@ -494,7 +476,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.tok_cnt = (int32_t*)take(T * 4);
   w.h = (uint16_t*)take(R * I * 2);
   w.h_amax = (uint32_t*)take(R * 4);
-  w.qh = (int8_t*)take(R * I);
+  w.qh = (int8_t*)take(R * I * qb);
   w.asch = (float*)take(R * 4);
   w.slots = (uint16_t*)take(R * H * 2);
   w.xrot = rot_blk > 0 ? (float*)take(T * H * 4) : nullptr;
@@ -528,8 +510,8 @@ extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t 
   return lsk::check_launch("router_topk_kernel");
 }
 
-extern "C" int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk) {
-  return moe_layout(nullptr, T, k, E, H, I, rot_blk).bytes;
+extern "C" int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt) {
+  return moe_layout(nullptr, T, k, E, H, I, rot_blk, wfmt).bytes;
 }
 
 extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
@@ -546,12 +528,22 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   if (T == 0) return LSK_OK;
   LSK_REQUIRE(a->x && a->idx && a->w && a->w13_ptrs && a->ws13_ptrs && a->w2_ptrs && a->ws2_ptrs && a->frac && a->y,
               "lsk_moe_forward: null pointer");
-  LSK_REQUIRE(a->ldw13 >= H && a->ldw13 % 16 == 0 && a->ldw2 >= I && a->ldw2 % 16 == 0,
-              "lsk_moe_forward: weight row strides must cover K and be multiples of 16");
+  if (a->wfmt == 1) {
+    LSK_REQUIRE(a->ldw13 >= H / 2 && a->ldw13 % 16 == 0 && a->ldw2 >= I / 2 && a->ldw2 % 16 == 0 &&
+                    a->lds13 >= H / 32 && a->lds2 >= I / 32,
+                "lsk_moe_forward: MXFP4 row strides must cover K/2 (multiples of 16) and K/32");
+  } else {
+    LSK_REQUIRE(a->ldw13 >= H && a->ldw13 % 16 == 0 && a->ldw2 >= I && a->ldw2 % 16 == 0,
+                "lsk_moe_forward: weight row strides must cover K and be multiples of 16");
+  }
   const int rb = a->rot_blk;
   LSK_REQUIRE(rb == 0 || (rb >= 2 && rb <= 1024 && (rb & (rb - 1)) == 0 && H % rb == 0 && I % rb == 0 && I <= 16384),
               "lsk_moe_forward: rot_blk=%d must be 0 or a power of two dividing H and I (I <= 16384)", rb);
-  const MoeWs w = moe_layout((char*)a->workspace, T, k, E, H, I, rb);
+  const int mx = a->wfmt;
+  LSK_REQUIRE(mx == 0 || mx == 1, "lsk_moe_forward: unknown weight format %d", mx);
+  LSK_REQUIRE(!mx || (rb == 0 && H % 32 == 0 && I % 32 == 0), "lsk_moe_forward: MXFP4 experts need K %% 32 == 0 "
+              "and no rotation");
+  const MoeWs w = moe_layout((char*)a->workspace, T, k, E, H, I, rb, mx);
   LSK_REQUIRE(a->workspace && a->workspace_bytes >= w.bytes && ((uintptr_t)a->workspace & 255) == 0,
               "lsk_moe_forward: workspace of %lld bytes (256-byte aligned) needed", (long long)w.bytes);
   hipStream_t s = (hipStream_t)stream;
@@ -566,6 +558,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::check_launch("widen_bf16_kernel"))) return rc;
     if ((rc = lsk_fwht_blocks(w.xrot, T, H, H, rb, a->rot_scale, w.xrot, H, stream))) return rc;
     rc = lsk_rowquant(w.xrot, LSK_F32, T, H, H, w.qx, H, w.ascx, stream);
+  } else if (mx) {
+    rc = lsk::launch_rowquant_bf16(a->x, T, H, (uint16_t*)w.qx, w.ascx, s);
   } else {
     rc = lsk_rowquant(a->x, LSK_BF16, T, H, H, w.qx, H, w.ascx, stream);
   }
@@ -597,11 +591,18 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g1.frac = a->frac;
   g1.h = w.h;
   g1.h_amax = w.h_amax;
-  if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) return rc;
+  g1.lds = a->lds13;
+  if (mx) {
+    if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
+    return rc;
+  }
   if (rb > 0) {
     hipLaunchKernelGGL(moe_rot_requant_kernel, dim3((unsigned)R), dim3(256), (size_t)I * 4, s, w.h, w.offs + E, (int)I,
                        rb, a->rot_scale, w.qh, w.asch);
     if ((rc = lsk::check_launch("moe_rot_requant_kernel"))) return rc;
+  } else if (mx) {
+    if ((rc = lsk::launch_requant_bf16(w.h, w.h_amax, w.offs + E, R, (int)I, (uint16_t*)w.qh, w.asch, s))) return rc;
   } else {
     int64_t blocks = (R * (I / 8) + 255) / 256;
     blocks = blocks > 8192 ? 8192 : (blocks < 1 ? 1 : blocks);
@@ -624,7 +625,12 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g2.row_w = w.row_w;
   g2.row_dst = w.row_dst;
   g2.y = w.slots;
-  if ((rc = launch_moe_gemm<1>(g2, w.max_tiles, (int)((H + 127) / 128), s, "moe_gemm_kernel<down>"))) return rc;
+  g2.lds = a->lds2;
+  if (mx) {
+    if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if ((rc = launch_moe_gemm<1>(g2, w.max_tiles, (int)((H + 127) / 128), s, "moe_gemm_kernel<down>"))) {
+    return rc;
+  }
   {
     int64_t blocks = (T * (H / 8) + 255) / 256;
     blocks = blocks > 8192 ? 8192 : (blocks < 1 ? 1 : blocks);

@@ -1,0 +1,43 @@
+// Internal interface between the MoE layer driver (moe.hip) and the MXFP4 grouped GEMMs (mx.hip).
+#pragma once
+#include "lsk_common.h"
+
+namespace lsk {
+
+constexpr int kMoeBM = 128;  // rows per expert tile (the dispatch's tile table granularity)
+
+// Arguments of one grouped expert GEMM (gate/up with the activation, or down with the weight).
+struct MoeGemmArgs {
+  const void* A;            // int8 (int8 experts) or bf16 (MXFP4 experts) activation rows
+  int64_t lda;              // elements
+  const float* a_scale;     // per A row
+  const int32_t* row_tok;   // gate/up: permuted row -> token (A row); down: unused
+  const int32_t* offs;      // [E + 1]
+  const int32_t* tiles;     // [0] count, then (expert, first row) pairs
+  const int64_t* w_ptrs;    // [E]: int8 [N_w, K] or packed E2M1 [N_w, K / 2]
+  int64_t ldw;              // weight row stride in bytes
+  const int64_t* ws_ptrs;   // [E]: f32 scales [N_w] (int8) or E8M0 bytes [N_w, K / 32] (MXFP4)
+  int64_t lds;              // E8M0 row stride in bytes (MXFP4)
+  const int64_t* b_ptrs;    // [E] or null
+  int K;
+  int N;                    // gate/up: I (h columns); down: H
+  int act;
+  const int32_t* frac;
+  uint16_t* h;              // gate/up out [R, I] bf16
+  uint32_t* h_amax;         // [R]
+  const float* row_w;       // down: routing weight per row
+  const int32_t* row_dst;   // down: destination slot row
+  uint16_t* y;              // down out [T * k, N] bf16
+};
+
+// MXFP4 grouped GEMMs (mode 0: gate/up + activation; 1: down + routing weight).
+int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, hipStream_t s);
+
+// Row quant emitting the int8 values as bf16 (the MX GEMM's operand form).
+int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, float* asc, hipStream_t s);
+
+// Requant of h (bf16 values) with per-row maxima, emitting bf16 int8 values.
+int launch_requant_bf16(const uint16_t* h, const uint32_t* amax, const int32_t* nrows, int64_t R, int I, uint16_t* q,
+                        float* asc, hipStream_t s);
+
+}  // namespace lsk

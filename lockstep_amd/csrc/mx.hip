@@ -1,0 +1,428 @@
+// MXFP4 kernels on gfx950: the MX-operand GEMM (dense and grouped for the MoE layer), the exact
+// E2M1/E8M0 dequant, and the doubled-mantissa packer.  See mx_tile.h for the exactness argument.
+#include "contract_act.h"
+#include "moe_internal.h"
+#include "mx_tile.h"
+
+namespace {
+
+constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
+constexpr int NB = 2;                          // MX blocks per LDS stage (K = 64)
+using Cfg = lsk::MxCfg<128, 128, 2, 2, NB>;
+
+template <class K>
+int reserve_lds(K kern, int bytes, const char* name) {
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+    lsk::set_error("%s: cannot reserve %d bytes of LDS", name, bytes);
+    return LSK_ERR_HIP;
+  }
+  return LSK_OK;
+}
+
+// ---------------------------------------------------------------- quantisers emitting bf16 values
+LSK_DEV uint16_t q_bf16(float v, float s) {
+  const float t = fminf(fmaxf(rintf(f32_div(v, s)), -127.0f), 127.0f);
+  return (uint16_t)(__float_as_uint(t) >> 16);  // an integer of magnitude <= 127: exact in bf16
+}
+
+__global__ __launch_bounds__(256) void rowquant_bf16_kernel(const uint16_t* __restrict__ x, int64_t H,
+                                                            uint16_t* __restrict__ q, float* __restrict__ asc) {
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  const uint16_t* row = x + t * H;
+  float am = 0.0f;
+  for (int64_t i = threadIdx.x; i < H; i += 256) am = fmaxf(am, fabsf(bf16_to_f32(row[i])));
+  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f);
+  if (threadIdx.x == 0) asc[t] = s;
+  for (int64_t i = threadIdx.x; i < H; i += 256) q[t * H + i] = q_bf16(bf16_to_f32(row[i]), s);
+}
+
+__global__ __launch_bounds__(256) void requant_bf16_kernel(const uint16_t* __restrict__ h, const uint32_t* __restrict__ amax,
+                                                           const int32_t* __restrict__ nrows, int I,
+                                                           uint16_t* __restrict__ q, float* __restrict__ asc) {
+  const int R = *nrows;
+  const int chunks = I / 8;
+  const int64_t total = (int64_t)R * chunks;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t p = i / chunks;
+    const int c = (int)(i - p * chunks);
+    const float s = f32_div(fmaxf(__uint_as_float(amax[p]), kAmaxFloor), 127.0f);
+    if (c == 0) asc[p] = s;
+    const uint4 u = *(const uint4*)(h + p * I + c * 8);
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = (uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] & 0xffff)), s) |
+             ((uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] >> 16)), s) << 16);
+    *(uint4*)(q + p * I + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// ---------------------------------------------------------------- dense MX GEMM (int_mm_mx)
+template <bool B_FP4, bool SAFE>
+__global__ __launch_bounds__(256) void mx_gemm_kernel(const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B,
+                                                      int64_t ldb, const uint8_t* __restrict__ S, int64_t lds, int M, int N,
+                                                      int K, int epi, const float* __restrict__ asc,
+                                                      const float* __restrict__ bias, float* __restrict__ out,
+                                                      int64_t ldo) {
+  extern __shared__ char mx_smem[];
+  const int ntiles = (N + 127) / 128;
+  const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
+  const int m0 = (L / ntiles) * 128, n0 = (L % ntiles) * 128;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / 2, wn = wave % 2;
+  typename Cfg::Acc acc;
+#pragma unroll
+  for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  auto rowA = [&](int r) -> const void* { return m0 + r < M ? (const void*)(A + (int64_t)(m0 + r) * lda) : nullptr; };
+  auto rowB = [&](int r) -> const uint8_t* { return n0 + r < N ? B + (int64_t)(n0 + r) * ldb : nullptr; };
+  auto rowS = [&](int r) -> const uint8_t* { return n0 + r < N ? S + (int64_t)(n0 + r) * lds : nullptr; };
+  lsk::mx_mainloop<128, 128, 2, 2, NB, true, B_FP4, SAFE>(acc, rowA, rowB, rowS, K, mx_smem);
+
+  float* region = (float*)mx_smem + wave * Cfg::kStripFloats;
+#pragma unroll
+  for (int i = 0; i < Cfg::TM; ++i) {
+    lsk::stage_strip_f<Cfg::TN, Cfg::kLdc>(acc[i], region);
+    __syncthreads();
+    for (int q = lane; q < 16 * 16; q += 64) {
+      const int row = q >> 4, c4 = (q & 15) * 4;
+      const int m = m0 + wm * 64 + i * 16 + row;
+      const int n = n0 + wn * 64 + c4;
+      if (m < M) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (n + t >= N) break;
+          float v = region[row * Cfg::kLdc + c4 + t];
+          if (epi) {
+            v = bfr(f32_mul(v, asc[m]));
+            if (bias) v = bfr(f32_add(v, bias[n + t]));
+          }
+          out[(int64_t)m * ldo + n + t] = v;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- grouped MX GEMM (MoE)
+// MODE 0: gate/up + activation (tile columns interleave 16 gate / 16 up weight rows); MODE 1:
+// down + routing weight into the token-major slot rows.
+template <int MODE, bool SAFE>
+__global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
+  extern __shared__ char mx_smem[];
+  const int ntiles = MODE == 0 ? (a.N + 63) / 64 : (a.N + 127) / 128;
+  const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
+  const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
+  if (mt >= a.tiles[0]) return;
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  const uint8_t* wb = (const uint8_t*)a.w_ptrs[e];
+  const uint8_t* sb = (const uint8_t*)a.ws_ptrs[e];
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  const uint16_t* A = (const uint16_t*)a.A;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / 2, wn = wave % 2;
+
+  auto wrow = [&](int r) -> int {  // weight row of tile row r, or -1
+    if (MODE == 0) {
+      const int blk = r >> 4;
+      const int hc = nt * 64 + (blk >> 1) * 16 + (r & 15);
+      return hc < a.N ? ((blk & 1) ? a.N + hc : hc) : -1;
+    }
+    const int n = nt * 128 + r;
+    return n < a.N ? n : -1;
+  };
+  auto rowA = [&](int r) -> const void* {
+    const int p = p0 + r;
+    if (p >= p1) return nullptr;
+    const int src = MODE == 0 ? a.row_tok[p] : p;
+    return (const void*)(A + (int64_t)src * a.lda);
+  };
+  auto rowB = [&](int r) -> const uint8_t* {
+    const int w = wrow(r);
+    return w >= 0 ? wb + (int64_t)w * a.ldw : nullptr;
+  };
+  auto rowS = [&](int r) -> const uint8_t* {
+    const int w = wrow(r);
+    return w >= 0 ? sb + (int64_t)w * a.lds : nullptr;
+  };
+  typename Cfg::Acc acc;
+#pragma unroll
+  for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  lsk::mx_mainloop<128, 128, 2, 2, NB, false, true, SAFE>(acc, rowA, rowB, rowS, a.K, mx_smem);
+
+  float* region = (float*)mx_smem + wave * Cfg::kStripFloats;
+#pragma unroll
+  for (int i = 0; i < Cfg::TM; ++i) {
+    lsk::stage_strip_f<Cfg::TN, Cfg::kLdc>(acc[i], region);
+    __syncthreads();
+    if (MODE == 0) {
+#pragma unroll
+      for (int pass = 0; pass < 2; ++pass) {
+        const int q = pass * 64 + lane;
+        const int row = q >> 3, hq = q & 7, pair = hq >> 2, c4 = (hq & 3) * 4;
+        const int p = p0 + wm * 64 + i * 16 + row;
+        const int hc0 = nt * 64 + wn * 32 + pair * 16 + c4;
+        float am = 0.0f;
+        if (p < p1) {
+          const float asc = a.a_scale[a.row_tok[p]];
+          uint16_t hb[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int hc = hc0 + t;
+            hb[t] = 0;
+            if (hc < a.N) {
+              float yg = bfr(f32_mul(region[row * Cfg::kLdc + pair * 32 + c4 + t], asc));
+              float yu = bfr(f32_mul(region[row * Cfg::kLdc + pair * 32 + 16 + c4 + t], asc));
+              if (bias) {
+                yg = bfr(f32_add(yg, bias[hc]));
+                yu = bfr(f32_add(yu, bias[a.N + hc]));
+              }
+              const float hv = a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
+              hb[t] = f32_to_bf16(hv);
+              am = fmaxf(am, fabsf(hv));
+            }
+          }
+          uint16_t* dst = a.h + (int64_t)p * a.N + hc0;
+          if (hc0 + 4 <= a.N) {
+            *(uint2*)dst = make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
+          } else {
+            for (int t = 0; t < 4; ++t)
+              if (hc0 + t < a.N) dst[t] = hb[t];
+          }
+        }
+        am = fmaxf(am, __shfl_xor(am, 1, 64));
+        am = fmaxf(am, __shfl_xor(am, 2, 64));
+        am = fmaxf(am, __shfl_xor(am, 4, 64));
+        if ((lane & 7) == 0 && p < p1) atomicMax(&a.h_amax[p], __float_as_uint(am));
+      }
+    } else {
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const int q = pass * 64 + lane;
+        const int row = q >> 4, c4 = (q & 15) * 4;
+        const int p = p0 + wm * 64 + i * 16 + row;
+        const int n0 = nt * 128 + wn * 64 + c4;
+        if (p < p1 && n0 < a.N) {
+          const float asc = a.a_scale[p];
+          const float wt = a.row_w[p];
+          uint16_t ob[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int n = n0 + t;
+            ob[t] = 0;
+            if (n < a.N) {
+              float yv = bfr(f32_mul(region[row * Cfg::kLdc + c4 + t], asc));
+              if (bias) yv = bfr(f32_add(yv, bias[n]));
+              ob[t] = f32_to_bf16(f32_mul(wt, yv));
+            }
+          }
+          uint16_t* dst = a.y + (int64_t)a.row_dst[p] * a.N + n0;
+          if (n0 + 4 <= a.N) {
+            *(uint2*)dst = make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+          } else {
+            for (int t = 0; t < 4; ++t)
+              if (n0 + t < a.N) dst[t] = ob[t];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- dequant and packing
+__global__ __launch_bounds__(256) void dequant_mxfp4_kernel(const uint8_t* __restrict__ packed,
+                                                            const uint8_t* __restrict__ scale, int64_t rows, int64_t K,
+                                                            int block, void* __restrict__ out, int odt) {
+  const int64_t half = K / 2;
+  const int64_t total = rows * half;
+  const int64_t nsb = K / block;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / half, c = i - r * half;
+    const uint32_t byte = packed[i];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t k = 2 * c + t;
+      const uint32_t code = t ? (byte >> 4) : (byte & 15u);
+      const int e = (int)scale[r * nsb + k / block] - 127;
+      const float sc = e > 127 ? __builtin_inff() : pow2f(e);
+      // fp4 value = m2 / 2 (exact), times 2^e: one binary32 multiply, as the reference's vals * sc
+      const float v = f32_mul(f32_mul(__uint_as_float(lsk::m2_bf16(code) << 16), 0.5f), sc);
+      if (odt == LSK_BF16) ((uint16_t*)out)[r * K + k] = f32_to_bf16(v);
+      else ((float*)out)[r * K + k] = v;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void mx_pack_kernel(const int8_t* __restrict__ m2, int64_t n, uint8_t* __restrict__ packed,
+                                                      int32_t* __restrict__ bad) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n / 2; i += (int64_t)gridDim.x * 256) {
+    uint32_t codes[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int v = m2[2 * i + t];
+      const int a = v < 0 ? -v : v;
+      int mag = -1;
+      switch (a) {
+        case 0: mag = 0; break;
+        case 1: mag = 1; break;
+        case 2: mag = 2; break;
+        case 3: mag = 3; break;
+        case 4: mag = 4; break;
+        case 6: mag = 5; break;
+        case 8: mag = 6; break;
+        case 12: mag = 7; break;
+        default: break;
+      }
+      if (mag < 0) {
+        atomicOr(bad, 1);
+        mag = 0;
+      }
+      codes[t] = (uint32_t)mag | (v < 0 ? 8u : 0u);
+    }
+    packed[i] = (uint8_t)(codes[0] | (codes[1] << 4));
+  }
+}
+
+unsigned grid_for(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  return (unsigned)(b > 8192 ? 8192 : (b < 1 ? 1 : b));
+}
+
+template <int MODE, bool SAFE>
+int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s) {
+  static bool attr = false;
+  auto kern = moe_mx_gemm_kernel<MODE, SAFE>;
+  if (!attr) {
+    if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "moe_mx_gemm_kernel")) return rc;
+    attr = true;
+  }
+  const int ntiles = MODE == 0 ? (ga.N + 63) / 64 : (ga.N + 127) / 128;
+  const int64_t blocks = max_tiles * ntiles;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "moe_mx_gemm_kernel: grid too large");
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), Cfg::kSmemBytes, s, ga);
+  return lsk::check_launch(MODE == 0 ? "moe_mx_gemm_kernel<gate_up>" : "moe_mx_gemm_kernel<down>");
+}
+
+template <bool B_FP4, bool SAFE>
+int launch_dense(const int8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, const uint8_t* kexp, int64_t lds, int M,
+                 int N, int K, int epi, const float* asc, const float* bias, float* out, int64_t ldo, hipStream_t s) {
+  static bool attr = false;
+  auto kern = mx_gemm_kernel<B_FP4, SAFE>;
+  if (!attr) {
+    if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "mx_gemm_kernel")) return rc;
+    attr = true;
+  }
+  const int64_t blocks = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  LSK_REQUIRE(blocks <= 0x7fffffff, "mx_gemm_kernel: grid too large");
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), Cfg::kSmemBytes, s, a, lda, b, ldb, kexp, lds, M, N, K, epi,
+                     asc, bias, out, ldo);
+  return lsk::check_launch("mx_gemm_kernel");
+}
+
+}  // namespace
+
+namespace lsk {
+
+int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, hipStream_t s) {
+  if (mode == 0) return safe ? launch_grouped<0, true>(ga, max_tiles, s) : launch_grouped<0, false>(ga, max_tiles, s);
+  return safe ? launch_grouped<1, true>(ga, max_tiles, s) : launch_grouped<1, false>(ga, max_tiles, s);
+}
+
+int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, float* asc, hipStream_t s) {
+  if (T == 0) return LSK_OK;
+  LSK_REQUIRE(T <= 0x7fffffff, "rowquant_bf16: too many rows");
+  hipLaunchKernelGGL(rowquant_bf16_kernel, dim3((unsigned)T), dim3(256), 0, s, x, H, q, asc);
+  return check_launch("rowquant_bf16_kernel");
+}
+
+int launch_requant_bf16(const uint16_t* h, const uint32_t* amax, const int32_t* nrows, int64_t R, int I, uint16_t* q,
+                        float* asc, hipStream_t s) {
+  hipLaunchKernelGGL(requant_bf16_kernel, dim3(grid_for(R * (I / 8))), dim3(256), 0, s, h, amax, nrows, I, q, asc);
+  return check_launch("requant_bf16_kernel");
+}
+
+}  // namespace lsk
+
+extern "C" int lsk_gemm_mx(const int8_t* a, int64_t lda, const void* b, int b_fmt, int64_t ldb, const uint8_t* kexp,
+                           int64_t lds, int64_t M, int64_t N, int64_t K, int epilogue, const float* asc, const float* bias,
+                           float* out, int64_t ldo, void* stream) {
+  LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_gemm_mx: negative size");
+  LSK_REQUIRE(K % 32 == 0, "lsk_gemm_mx: K=%lld not a multiple of the 32-element block", (long long)K);
+  LSK_REQUIRE(b_fmt == 0 || b_fmt == 1, "lsk_gemm_mx: b_fmt %d not 0 (m2 int8) or 1 (packed E2M1)", b_fmt);
+  LSK_REQUIRE(epilogue == 0 || epilogue == 1, "lsk_gemm_mx: epilogue must be 0 or 1");
+  if (M == 0 || N == 0) return LSK_OK;
+  LSK_REQUIRE(a && b && kexp && out && (epilogue == 0 || asc), "lsk_gemm_mx: null pointer");
+  LSK_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, "lsk_gemm_mx: size too large");
+  const int64_t rowbytes = b_fmt == 1 ? K / 2 : K;
+  LSK_REQUIRE(lda >= K && lda % 16 == 0 && ((uintptr_t)a & 15) == 0, "lsk_gemm_mx: a rows must be 16-byte aligned");
+  LSK_REQUIRE(ldb >= rowbytes && ldb % 16 == 0 && ((uintptr_t)b & 15) == 0, "lsk_gemm_mx: weight rows must be 16-byte aligned");
+  LSK_REQUIRE(lds >= K / 32 && ldo >= N, "lsk_gemm_mx: leading dimension too small");
+  // the fused block update is exact unless an exponent byte >= 240 can overflow the product;
+  // the host cannot see device data, so the general entry point always takes the SAFE update
+  hipStream_t s = (hipStream_t)stream;
+  if (b_fmt == 1)
+    return launch_dense<true, true>(a, lda, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K, epilogue, asc,
+                                    bias, out, ldo, s);
+  return launch_dense<false, true>(a, lda, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K, epilogue, asc, bias,
+                                   out, ldo, s);
+}
+
+extern "C" int lsk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t K, int block,
+                                 void* out, int out_dtype, void* stream) {
+  LSK_REQUIRE(rows >= 0 && K >= 0 && block > 0, "lsk_dequant_mxfp4: bad sizes");
+  LSK_REQUIRE(K % 2 == 0 && K % block == 0, "lsk_dequant_mxfp4: K=%lld must be even and a multiple of block=%d",
+              (long long)K, block);
+  LSK_REQUIRE(out_dtype == LSK_BF16 || out_dtype == LSK_F32, "lsk_dequant_mxfp4: out_dtype must be bf16 or f32");
+  if (rows == 0 || K == 0) return LSK_OK;
+  LSK_REQUIRE(packed && scale && out, "lsk_dequant_mxfp4: null pointer");
+  hipLaunchKernelGGL(dequant_mxfp4_kernel, dim3(grid_for(rows * K / 2)), dim3(256), 0, (hipStream_t)stream, packed, scale,
+                     rows, K, block, out, out_dtype);
+  return lsk::check_launch("dequant_mxfp4_kernel");
+}
+
+extern "C" int lsk_mx_pack_m2(const int8_t* m2, int64_t n, uint8_t* packed, int32_t* bad, void* stream) {
+  LSK_REQUIRE(n >= 0 && n % 2 == 0, "lsk_mx_pack_m2: n=%lld must be even", (long long)n);
+  if (n == 0) return LSK_OK;
+  LSK_REQUIRE(m2 && packed && bad, "lsk_mx_pack_m2: null pointer");
+  hipLaunchKernelGGL(mx_pack_kernel, dim3(grid_for(n / 2)), dim3(256), 0, (hipStream_t)stream, m2, n, packed, bad);
+  return lsk::check_launch("mx_pack_kernel");
+}
+
+namespace {
+// moe_ref.py:258-261: y = bfr(acc * asc[m]); y = bfr(y + b[n])
+__global__ __launch_bounds__(256) void mx_epilogue_kernel(const float* __restrict__ acc, int64_t M, int64_t N,
+                                                          const float* __restrict__ asc, const float* __restrict__ bias,
+                                                          float* __restrict__ out) {
+  const int64_t total = M * N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / N, n = i - m * N;
+    float y = bfr(f32_mul(acc[i], asc[m]));
+    if (bias) y = bfr(f32_add(y, bias[n]));
+    out[i] = y;
+  }
+}
+}  // namespace
+
+extern "C" int lsk_mx_epilogue(const float* acc, int64_t M, int64_t N, const float* asc, const float* bias, float* out,
+                               void* stream) {
+  LSK_REQUIRE(M >= 0 && N >= 0, "lsk_mx_epilogue: negative size");
+  if (M == 0 || N == 0) return LSK_OK;
+  LSK_REQUIRE(acc && asc && out, "lsk_mx_epilogue: null pointer");
+  hipLaunchKernelGGL(mx_epilogue_kernel, dim3(grid_for(M * N)), dim3(256), 0, (hipStream_t)stream, acc, M, N, asc, bias,
+                     out);
+  return lsk::check_launch("mx_epilogue_kernel");
+}

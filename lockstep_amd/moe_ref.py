@@ -278,3 +278,128 @@ def moe_forward_b(x, gate, experts, k, renormalize, tab, win, act, rot_blk=256, 
         idx, w = routing[0].to(torch.int64), routing[1].to(BF)
     y = _moe_layer(x, idx, w, expert_tables(experts), _act_code(act), int(rot_blk or 0))
     return y, idx, w
+
+
+# ============================================================================ the MXFP4 operand (moe_ref.py:233-290)
+MX_BLOCK = 32
+
+
+def int_mm_mx(a8: torch.Tensor, m2: torch.Tensor, kexp: torch.Tensor) -> torch.Tensor:
+    """a8 int8 [T, K]; m2 int8 [N, K] doubled mantissas; kexp [N, K/32] E8M0 -> binary32 [T, N]:
+    per 32-block s (exact) then acc = fl32(acc + s * 2^(kexp - 128)) in ascending block order."""
+    return ops.gemm_mx(a8, m2, kexp, 0)
+
+
+def lin_epilogue_mx(acc: torch.Tensor, asc: torch.Tensor, bias=None) -> torch.Tensor:
+    """bfr(acc * asc[m]), then bfr(y + b)."""
+    return ops.mx_epilogue(acc, asc, bias)
+
+
+def expert_block_mx(x_rows, w13, w2, act, b13=None, b2=None):
+    """w13 = (m2 [2I, H], kexp [2I, H/32]); w2 = (m2 [H, I], kexp [H, I/32]).  No rotation."""
+    q, asc = rowquant(x_rows)
+    y = ops.gemm_mx(q, w13[0], w13[1], 0, asc=asc, bias=b13, epilogue=1)
+    I = y.shape[-1] // 2
+    h = act(y[:, :I], y[:, I:])
+    q2, asc2 = rowquant(h)
+    return ops.gemm_mx(q2, w2[0], w2[1], 0, asc=asc2, bias=b2, epilogue=1)
+
+
+class ExpertTablesMX:
+    """Device address tables of MXFP4 experts as the fused layer reads them: packed E2M1 codes
+    [N, K/2] and E8M0 bytes [N, K/32] per projection.  experts[e] = ((m2_13, kexp_13),
+    (m2_2, kexp_2), b13 | None, b2 | None) as moe_ref passes them (the m2 are packed once,
+    losslessly), or ((packed_13, scale_13), (packed_2, scale_2), ...) with packed=True."""
+
+    def __init__(self, experts, packed: bool = False):
+        if not experts:
+            raise ValueError("no experts")
+        first = experts[0][0][0]
+        L.require_cuda(first, what="experts")
+        self.device = first.device
+        self.E = len(experts)
+        keep = []
+        p13, s13, p2, s2, b13, b2 = [], [], [], [], [], []
+        safe = False
+        for ex in experts:
+            (m13, k13), (m2_, k2_) = ex[0], ex[1]
+            c13 = m13.to(torch.uint8).contiguous() if packed else ops.pack_m2(m13)
+            c2 = m2_.to(torch.uint8).contiguous() if packed else ops.pack_m2(m2_)
+            e13 = k13.to(torch.uint8).contiguous()
+            e2 = k2_.to(torch.uint8).contiguous()
+            bb13 = ex[2].to(F32).contiguous() if len(ex) > 2 and ex[2] is not None else None
+            bb2 = ex[3].to(F32).contiguous() if len(ex) > 3 and ex[3] is not None else None
+            keep += [c13, c2, e13, e2, bb13, bb2]
+            p13.append(c13.data_ptr())
+            p2.append(c2.data_ptr())
+            s13.append(e13.data_ptr())
+            s2.append(e2.data_ptr())
+            b13.append(bb13.data_ptr() if bb13 is not None else 0)
+            b2.append(bb2.data_ptr() if bb2 is not None else 0)
+            safe = safe or bool((e13.max() >= 240).item()) or bool((e2.max() >= 240).item())
+        two_i, hh = keep[0].shape
+        self.I = int(two_i) // 2
+        self.H = int(hh) * 2
+        self.ldw13, self.ldw2 = int(keep[0].stride(0)), int(keep[1].stride(0))
+        self.lds13, self.lds2 = int(keep[2].stride(0)), int(keep[3].stride(0))
+        self.mx_safe = 1 if safe else 0
+        dev = self.device
+
+        def table(vals):
+            return torch.tensor(vals, dtype=torch.int64).to(dev)
+        self.w13, self.w2, self.ws13, self.ws2 = table(p13), table(p2), table(s13), table(s2)
+        self.b13 = table(b13) if any(b13) else None
+        self.b2 = table(b2) if any(b2) else None
+        self._keep = keep
+
+
+def expert_tables_mx(experts) -> ExpertTablesMX:
+    if isinstance(experts, ExpertTablesMX):
+        return experts
+    key = ("mx", id(experts)) + tuple((t.data_ptr(), t._version) for ex in experts
+                                      for part in ex if part is not None
+                                      for t in (part if isinstance(part, tuple) else (part,)))
+    hit = _TABLES.get(key)
+    if hit is None:
+        if len(_TABLES) >= 8:
+            _TABLES.pop(next(iter(_TABLES)))
+        hit = _TABLES[key] = ExpertTablesMX(experts)
+    return hit
+
+
+def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int):
+    L.require_cuda(x, idx, w, what="moe_forward_mx")
+    if x.dtype != BF:
+        raise TypeError("moe_forward_mx: x must be bf16 [T, H] (got %s)" % x.dtype)
+    x = x.contiguous()
+    T, H = x.shape
+    k = int(idx.shape[1])
+    if H != t.H:
+        raise ValueError("moe_forward_mx: x width %d != expert H %d" % (H, t.H))
+    idx = idx.to(torch.int64).contiguous()
+    w = w.to(BF).contiguous()
+    y = torch.empty((T, H), dtype=BF, device=x.device)
+    if T == 0:
+        return y
+    nbytes = L.load().lsk_moe_workspace(T, k, t.E, H, t.I, 0, 1)
+    work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
+    a = L.MoeArgs(T=T, H=H, I=t.I, E=t.E, k=k, act=act, wfmt=1, mx_safe=t.mx_safe, lds13=t.lds13, lds2=t.lds2,
+                  x=x.data_ptr(), idx=idx.data_ptr(), w=w.data_ptr(), w13_ptrs=t.w13.data_ptr(), ldw13=t.ldw13,
+                  ws13_ptrs=t.ws13.data_ptr(), b13_ptrs=t.b13.data_ptr() if t.b13 is not None else None,
+                  w2_ptrs=t.w2.data_ptr(), ldw2=t.ldw2, ws2_ptrs=t.ws2.data_ptr(),
+                  b2_ptrs=t.b2.data_ptr() if t.b2 is not None else None, frac=ops.frac_i32(x.device).data_ptr(),
+                  rot_blk=0, rot_scale=0.0, shared=None, y=y.data_ptr(), workspace=work.data_ptr(),
+                  workspace_bytes=nbytes)
+    L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
+    return y
+
+
+def moe_forward_mx(x, gate, experts, k, renormalize, tab, win, act, routing=None):
+    """experts[e] = ((m2_13, kexp_13), (m2_2, kexp_2), b13 | None, b2 | None), or an
+    ExpertTablesMX; gate as moe_forward_b.  Returns (y bf16 [T, H], idx, w)."""
+    if routing is None:
+        idx, w, _ = router_b(x, gate[0], gate[1], k, renormalize, tab, win, gate[2] if len(gate) > 2 else None)
+    else:
+        idx, w = routing[0].to(torch.int64), routing[1].to(BF)
+    y = _moe_layer_mx(x, idx, w, expert_tables_mx(experts), _act_code(act))
+    return y, idx, w

@@ -200,3 +200,63 @@ def router_topk(g: torch.Tensor, k: int, renormalize: bool, tab: torch.Tensor):
         L.call("lsk_router_topk", L.ptr(gd), code, E, T, E, int(k), 1 if renormalize else 0, L.ptr(tab_i32(tab)),
                L.ptr(idx), L.ptr(w), L.stream_of(g))
     return idx, w
+
+
+def gemm_mx(a8: torch.Tensor, b: torch.Tensor, kexp: torch.Tensor, b_fmt: int, asc=None, bias=None,
+            epilogue: int = 0) -> torch.Tensor:
+    """MX-operand GEMM: a8 int8 [M, K] with m2 int8 [N, K] (b_fmt 0) or packed E2M1 [N, K/2]
+    (b_fmt 1) and E8M0 kexp [N, K/32] -> binary32 [M, N] (epilogue 1: bfr(acc * asc) + bias)."""
+    L.require_cuda(a8, b, kexp, asc, bias, what="gemm_mx")
+    if a8.dtype != torch.int8:
+        raise TypeError("gemm_mx: a8 must be int8")
+    a8 = a8 if (a8.stride(-1) == 1 and a8.stride(0) % 16 == 0) else a8.contiguous()
+    b = b.contiguous()
+    kexp = kexp.to(torch.uint8).contiguous()
+    M, K = a8.shape
+    N = b.shape[0]
+    out = torch.empty((M, N), dtype=torch.float32, device=a8.device)
+    if M and N:
+        ld_a = a8.stride(0) if M > 1 else K
+        asc, bias = _f32(asc), _f32(bias)
+        L.call("lsk_gemm_mx", L.ptr(a8), ld_a, L.ptr(b), int(b_fmt), b.stride(0), L.ptr(kexp), kexp.stride(0),
+               M, N, K, int(epilogue), L.ptr(asc), L.ptr(bias), L.ptr(out), N, L.stream_of(a8))
+    return out
+
+
+def mx_epilogue(acc: torch.Tensor, asc: torch.Tensor, bias=None) -> torch.Tensor:
+    L.require_cuda(acc, asc, bias, what="lin_epilogue_mx")
+    acc = acc.to(torch.float32).contiguous()
+    M, N = acc.shape
+    out = torch.empty_like(acc)
+    L.call("lsk_mx_epilogue", L.ptr(acc), M, N, L.ptr(_f32(asc)), L.ptr(_f32(bias)), L.ptr(out), L.stream_of(acc))
+    return out
+
+
+def dequant_mxfp4(packed: torch.Tensor, scale: torch.Tensor, out_dtype=torch.bfloat16, block: int = 32):
+    L.require_cuda(packed, scale, what="dequant_mxfp4")
+    lead = packed.shape[:-1]
+    K = packed.shape[-1] * 2
+    if scale.shape[-1] * block != K:
+        raise AssertionError((tuple(scale.shape), K))
+    p2 = packed.to(torch.uint8).reshape(-1, K // 2).contiguous()
+    s2 = scale.to(torch.uint8).reshape(-1, K // block).contiguous()
+    code = L.LSK_BF16 if out_dtype == torch.bfloat16 else L.LSK_F32
+    out = torch.empty((p2.shape[0], K), dtype=torch.bfloat16 if code == L.LSK_BF16 else torch.float32,
+                      device=packed.device)
+    L.call("lsk_dequant_mxfp4", L.ptr(p2), L.ptr(s2), p2.shape[0], K, int(block), L.ptr(out), code,
+           L.stream_of(packed))
+    out = out.reshape(*lead, K)
+    return out if out.dtype == out_dtype else out.to(out_dtype)
+
+
+def pack_m2(m2: torch.Tensor):
+    """Doubled mantissas m2 int8 [..., K] -> packed E2M1 codes uint8 [..., K/2]; raises if some
+    value is not twice an E2M1 value (one host synchronisation)."""
+    L.require_cuda(m2, what="pack_m2")
+    m = m2.to(torch.int8).contiguous()
+    packed = torch.empty((*m.shape[:-1], m.shape[-1] // 2), dtype=torch.uint8, device=m.device)
+    bad = torch.zeros((1,), dtype=torch.int32, device=m.device)
+    L.call("lsk_mx_pack_m2", L.ptr(m), m.numel(), L.ptr(packed), L.ptr(bad), L.stream_of(m))
+    if int(bad.item()):
+        raise ValueError("m2 holds a value that is not 2 * an E2M1 value {0, +-1, +-2, +-3, +-4, +-6, +-8, +-12}")
+    return packed

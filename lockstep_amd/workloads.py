@@ -81,3 +81,27 @@ def moe_inputs(T, E, k, H, I, seed=0, bias=False, zipf=True):
     logits = zipf_logits(g, T, E) if zipf else _bf16_round(g.standard_normal((T, E), dtype=np.float64).astype(F32))
     experts = moe_int8_experts(g, E, H, I, bias)
     return x, experts, logits
+
+
+def mx_expert_weights(g, N, K):
+    """Packed E2M1 codes [N, K/2] (uniform over all 16 codes) and E8M0 bytes [N, K/32] with
+    exponents uniform in [-8, 2] (127 + U{-8..2})."""
+    packed = g.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    scale = (127 + g.integers(-8, 3, (N, K // 32))).astype(np.uint8)
+    return packed, scale
+
+
+def moe_mx_inputs(T, E, k, H, I, seed=0, bias=False):
+    """x [T, H] (bf16 values as f32), experts [(packed13, scale13, packed2, scale2, b13, b2)],
+    logits [T, E] N(0,1) (bf16 values)."""
+    g = rng(seed)
+    x = _bf16_round(g.standard_normal((T, H), dtype=np.float64).astype(F32))
+    logits = _bf16_round(g.standard_normal((T, E), dtype=np.float64).astype(F32))
+    experts = []
+    for _ in range(E):
+        p13, s13 = mx_expert_weights(g, 2 * I, H)
+        p2, s2 = mx_expert_weights(g, H, I)
+        b13 = (g.standard_normal(2 * I) * 0.1).astype(F32) if bias else None
+        b2 = (g.standard_normal(H) * 0.1).astype(F32) if bias else None
+        experts.append((p13, s13, p2, s2, b13, b2))
+    return x, experts, logits

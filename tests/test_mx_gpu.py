@@ -1,0 +1,178 @@
+"""GPU parity of the MXFP4 path: the MX-operand GEMM (ordered binary32 block updates), the exact
+dequant, and the fused MoE layer with MXFP4 experts, against the oracle, bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bf16_dev, bits, dev, f32_bits, say, to_dev
+from moe_util import routing_device, routing_from_logits, u16
+from oracle import contract as C
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+M2_SET = np.array([0, 1, 2, 3, 4, 6, 8, 12, -1, -2, -3, -4, -6, -8, -12], np.int8)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _tab():
+    from lockstep_amd import contract_common as CC
+    return CC.table_on(dev())
+
+
+def _pack(m2):
+    """m2 int8 [..., K] -> packed codes (the oracle's inverse of mx_to_m2)."""
+    a = np.abs(m2.astype(np.int64))
+    mag = np.select([a == 0, a == 1, a == 2, a == 3, a == 4, a == 6, a == 8, a == 12], list(range(8)), -1)
+    assert (mag >= 0).all()
+    codes = (mag | np.where(m2 < 0, 8, 0)).astype(np.uint8)
+    return (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 32), (3, 256, 64), (17, 100, 2880), (64, 520, 128), (130, 130, 320)])
+@pytest.mark.parametrize("fmt", [0, 1])
+def test_int_mm_mx_parity(M, N, K, fmt):
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import ops
+    say("int_mm_mx", M, N, K, fmt)
+    r = np.random.default_rng(M * 7 + N + K + fmt)
+    a = r.integers(-127, 128, (M, K), dtype=np.int8)
+    m2 = r.choice(M2_SET, (N, K))
+    kexp = r.integers(100, 150, (N, K // 32), dtype=np.uint8)
+    ref = C.int_mm_mx(a, m2, kexp)
+    if fmt == 0:
+        acc = MR.int_mm_mx(to_dev(a), to_dev(m2), to_dev(kexp))
+    else:
+        acc = ops.gemm_mx(to_dev(a), to_dev(_pack(m2)), to_dev(kexp), 1)
+    assert np.array_equal(bits(acc), f32_bits(ref))
+    asc = r.uniform(1e-3, 1e-1, M).astype(F32)
+    bias = (r.standard_normal(N) * 0.1).astype(F32)
+    y = MR.lin_epilogue_mx(acc, to_dev(asc), to_dev(bias))
+    assert np.array_equal(bits(y), f32_bits(C.lin_epilogue_mx(ref, asc, bias)))
+    y2 = ops.gemm_mx(to_dev(a), to_dev(m2), to_dev(kexp), 0, asc=to_dev(asc), bias=to_dev(bias), epilogue=1)
+    assert np.array_equal(bits(y2), f32_bits(C.lin_epilogue_mx(ref, asc, bias)))
+
+
+def test_int_mm_mx_extreme_exponents():
+    """Exponent bytes across the whole range: subnormal block scales (0, 1), ordinary ones, and
+    bytes >= 240 whose products overflow to infinity exactly as the reference's."""
+    from lockstep_amd import moe_ref as MR
+    r = np.random.default_rng(5)
+    M, N, K = 9, 40, 32 * 12
+    a = r.integers(-127, 128, (M, K), dtype=np.int8)
+    m2 = r.choice(M2_SET, (N, K))
+    kexp = r.integers(0, 256, (N, K // 32), dtype=np.uint8)
+    kexp[:, 0] = 0
+    kexp[:, 1] = 1
+    kexp[0, :] = 250
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.int_mm_mx(a, m2, kexp)
+    acc = MR.int_mm_mx(to_dev(a), to_dev(m2), to_dev(kexp))
+    got = bits(acc)
+    refb = f32_bits(ref)
+    nan_g = np.isnan(acc.cpu().numpy())
+    assert np.array_equal(nan_g, np.isnan(ref))
+    assert np.array_equal(got[~nan_g], refb[~nan_g])
+
+
+def test_int_mm_mx_block_order_is_ascending():
+    """The crafted negative control of the oracle: 2^24 + 1 - 2^24 in block order gives 0."""
+    from lockstep_amd import moe_ref as MR
+    a = np.zeros((1, 96), np.int8)
+    a[0, [0, 32, 64]] = 1
+    m2 = np.zeros((1, 96), np.int8)
+    m2[0, 0], m2[0, 32], m2[0, 64] = 1, 1, -1
+    kk = np.array([[152, 128, 152]], np.uint8)
+    acc = MR.int_mm_mx(to_dev(a), to_dev(m2), to_dev(kk))
+    assert float(acc.cpu()[0, 0]) == 0.0
+
+
+def test_dequant_mxfp4_all_codes_and_exponents():
+    from lockstep_amd import moe_mxfp4 as MX
+    codes = np.tile(np.arange(16, dtype=np.uint8), 256 * 2)            # [8192]
+    packed = (codes[0::2] | (codes[1::2] << 4)).astype(np.uint8).reshape(256, 16)
+    scale = np.arange(256, dtype=np.uint8).reshape(256, 1)             # one block of 32 per row
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref_bf = C.dequant_mxfp4(packed, scale)
+        ref_f = C.dequant_mxfp4(packed, scale, out="f32")
+    y = MX.dequant_mxfp4(to_dev(packed), to_dev(scale))
+    assert np.array_equal(u16(y), ref_bf)
+    yf = MX.dequant_mxfp4(to_dev(packed), to_dev(scale), out_dtype=torch.float32)
+    got = yf.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref_f))
+    ok = ~np.isnan(got)
+    assert np.array_equal(got.view(np.uint32)[ok], ref_f.view(np.uint32)[ok])
+    vals = MX.fp4_values(to_dev(np.arange(16, dtype=np.uint8)))
+    assert np.array_equal(bits(vals), f32_bits(C.fp4_values(np.arange(16))))
+    assert MX.self_test(dev())
+
+
+def _mx_case(T, E, k, H, I, seed, bias=False, act="silu", from_m2=True):
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("mx moe case", dict(T=T, E=E, k=k, H=H, I=I, seed=seed, bias=bias, act=act, from_m2=from_m2))
+    x, experts, logits = WL.moe_mx_inputs(T, E, k, H, I, seed=seed, bias=bias)
+    idx, w = routing_from_logits(logits, k)
+    oexp = []
+    dexp = []
+    for (p13, s13, p2, s2, b13, b2) in experts:
+        m13, _ = C.mx_to_m2(p13, s13)
+        m2_, _ = C.mx_to_m2(p2, s2)
+        oexp.append(((m13, s13), (m2_, s2), b13, b2))
+        d13 = to_dev(m13) if from_m2 else to_dev(p13)
+        d2 = to_dev(m2_) if from_m2 else to_dev(p2)
+        dexp.append(((d13, to_dev(s13)), (d2, to_dev(s2)), None if b13 is None else to_dev(b13),
+                     None if b2 is None else to_dev(b2)))
+    if not from_m2:
+        dexp = MR.ExpertTablesMX(dexp, packed=True)
+    oact = C.act_silu if act == "silu" else C.act_swigluoai
+    dact = MR.act_silu if act == "silu" else MR.act_swigluoai
+    ridx, rw = routing_device(idx, w)
+    y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, dact, routing=(ridx, rw))
+    return x, oexp, idx, w, oact, u16(y)
+
+
+def test_moe_mx_small():
+    x, oexp, idx, w, oact, got = _mx_case(24, 8, 2, 256, 128, seed=1)
+    assert np.array_equal(got, C.moe_forward_mx(x, oexp, idx, w, oact))
+
+
+def test_moe_mx_bias_swigluoai_packed_tables():
+    x, oexp, idx, w, oact, got = _mx_case(40, 6, 3, 320, 192, seed=2, bias=True, act="swigluoai", from_m2=False)
+    assert np.array_equal(got, C.moe_forward_mx(x, oexp, idx, w, oact))
+
+
+def test_expert_block_mx_composed():
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    x, experts, _ = WL.moe_mx_inputs(13, 1, 1, 256, 160, seed=3, bias=True)
+    p13, s13, p2, s2, b13, b2 = experts[0]
+    m13, _ = C.mx_to_m2(p13, s13)
+    m2_, _ = C.mx_to_m2(p2, s2)
+    y = MR.expert_block_mx(bf16_dev(x), (to_dev(m13), to_dev(s13)), (to_dev(m2_), to_dev(s2)), MR.act_swigluoai,
+                           to_dev(b13), to_dev(b2))
+    ref = C.expert_block_mx(x, (m13, s13), (m2_, s2), C.act_swigluoai, b13, b2)
+    assert np.array_equal(bits(y), f32_bits(ref))
+
+
+@pytest.mark.parametrize("T", [1, 32])
+def test_config5_gpt_oss_full(T):
+    from lockstep_amd import workloads as WL
+    c = WL.GPT_OSS_20B
+    x, oexp, idx, w, oact, got = _mx_case(T, c["E"], c["k"], c["H"], c["I"], seed=50 + T, act="swigluoai",
+                                          from_m2=False)
+    assert np.array_equal(got, C.moe_forward_mx(x, oexp, idx, w, oact))
+
+
+def test_config5_t4096_token_subset():
+    from lockstep_amd import workloads as WL
+    c = WL.GPT_OSS_20B
+    x, oexp, idx, w, oact, got = _mx_case(4096, c["E"], c["k"], c["H"], c["I"], seed=54, act="swigluoai",
+                                          from_m2=False)
+    rows = np.sort(np.random.default_rng(2).choice(4096, 24, replace=False))
+    ref = C.moe_forward_mx(x[rows], oexp, idx[rows], w[rows], oact)
+    assert np.array_equal(got[rows], ref)
