@@ -134,6 +134,112 @@ def decode_section(torch, args):
     return res
 
 
+def _int8_expert_tables(torch, MR, g, dev, E, H, I):
+    experts = []
+    for _ in range(E):
+        w13 = torch.randint(-127, 128, (2 * I, H), generator=g, device=dev, dtype=torch.int8)
+        w2 = torch.randint(-127, 128, (H, I), generator=g, device=dev, dtype=torch.int8)
+        ws13 = torch.empty(2 * I, device=dev).uniform_(1e-3, 1e-2, generator=g)
+        ws2 = torch.empty(H, device=dev).uniform_(1e-3, 1e-2, generator=g)
+        experts.append((w13.t(), ws13, w2.t(), ws2))
+    return MR.ExpertTables(experts)
+
+
+def _mx_expert_tables(torch, MR, g, dev, E, H, I):
+    experts = []
+    for _ in range(E):
+        p13 = torch.randint(0, 256, (2 * I, H // 2), generator=g, device=dev, dtype=torch.uint8)
+        s13 = 127 + torch.randint(-8, 3, (2 * I, H // 32), generator=g, device=dev, dtype=torch.int16)
+        p2 = torch.randint(0, 256, (H, I // 2), generator=g, device=dev, dtype=torch.uint8)
+        s2 = 127 + torch.randint(-8, 3, (H, I // 32), generator=g, device=dev, dtype=torch.int16)
+        experts.append(((p13, s13.to(torch.uint8)), (p2, s2.to(torch.uint8)), None, None))
+    return MR.ExpertTablesMX(experts, packed=True)
+
+
+def moe_section(torch, args):
+    """Config 4 (Qwen3-30B-A3B int8 experts, E=128, k=8, H=2048, I=768) and config 5 (GPT-OSS-20B
+    MXFP4 experts, E=32, k=4, H=I=2880) at T in {1, 32, 4096}: one step = the router from the given
+    logits (N(0,1), plus a Zipf(1.1) popularity bias for config 4) and the fused layer.  Two weight
+    copies alternate so a step's experts were evicted from the Infinity Cache by the other copy."""
+    from lockstep_amd import contract_common as CC
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    tab = CC.table_on(dev)
+    res = {}
+    cases = [("qwen3_30b_a3b_int8", WL.QWEN3_30B_A3B, False, 75497472, 4718592 + 4 * (2 * 768 + 2048)),
+             ("gpt_oss_20b_mxfp4", WL.GPT_OSS_20B, True, 199065600, 13219200)]
+    for name, c, mx, ops_tok, bytes_expert in cases:
+        E, k, H, I = c["E"], c["k"], c["H"], c["I"]
+        mk = _mx_expert_tables if mx else _int8_expert_tables
+        copies = [mk(torch, MR, g, dev, E, H, I) for _ in range(2)]
+        act = MR.act_swigluoai if mx else MR.act_silu
+        fwd = MR.moe_forward_mx if mx else MR.moe_forward
+        for T in (1, 32, 4096):
+            x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+            logits = torch.randn((T, E), generator=g, device=dev)
+            if not mx:
+                rank = torch.randperm(E, generator=g, device=dev).to(torch.float32)
+                logits = logits - 1.1 * torch.log1p(rank)[None, :]
+            logits = logits.to(torch.bfloat16)
+            it = [0]
+
+            def step():
+                idx, w, _ = MR.router_from_logits(logits, k, True, tab)
+                fwd(x, None, copies[it[0] % 2], k, True, tab, 0, act, routing=(idx, w))
+                it[0] += 1
+            for _ in range(3):
+                step()
+            reps = 20 if T < 4096 else 10
+            ms = _events_time(torch, step, reps)
+            idx, _, _ = MR.router_from_logits(logits, k, True, tab)
+            active = int(torch.unique(idx).numel())
+            gbs = active * bytes_expert / (ms * 1e-3) / 1e9
+            tops = ops_tok * T / (ms * 1e-3) / 1e12
+            peak_t = 2500.0 if mx else PEAK_INT8_TOPS
+            res["%s_T%d" % (name, T)] = {
+                "us": round(ms * 1e3, 2), "tokens_per_s": round(T / (ms * 1e-3), 1), "active_experts": active,
+                "weight_GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "TOPS": round(tops, 2),
+                "frac_mfma": round(tops / peak_t, 4)}
+            log("bench: %s T=%d: %.1f us, %.0f tokens/s" % (name, T, ms * 1e3, T / (ms * 1e-3)))
+        del copies
+        torch.cuda.empty_cache()
+    res["note"] = ("tokens/s of one MoE layer (router from logits + fused layer); weight_GB/s counts the active "
+                   "experts' weight bytes (int8 + f32 scales, or 4-bit codes + E8M0 bytes); TOPS counts "
+                   "2 * k * (2I*H + I*H) ops per token; MXFP4 fractions are of the bf16 MFMA peak (2.5 PF) the "
+                   "exact block contraction runs on")
+    return res
+
+
+def cpu_baseline_moe(args):
+    """The reference's moe_forward op sequence on the host (per-expert loop, int64 matmuls), on a
+    token sample of the config-4 layer."""
+    import numpy as np
+    import torch
+
+    from lockstep_amd import workloads as WL
+    from oracle import contract as C
+    from oracle import cpu_baseline as B
+
+    c = WL.QWEN3_30B_A3B
+    T = 16
+    x, experts, logits = WL.moe_inputs(T, c["E"], c["k"], c["H"], c["I"], seed=9)
+    idx, w, _ = C.router_from_logits(logits, c["k"], True)
+    ex = [(torch.from_numpy(w13).t(), torch.from_numpy(ws13), torch.from_numpy(w2).t(), torch.from_numpy(ws2))
+          for (w13, ws13, w2, ws2, _, _) in experts]
+    xt = torch.from_numpy(x).to(torch.bfloat16)
+    wt = torch.from_numpy(C.bf16_to_f32(w)).to(torch.bfloat16)
+    t0 = time.perf_counter()
+    B.moe_int8(xt, ex, torch.from_numpy(idx), wt)
+    dt = time.perf_counter() - t0
+    return {"value": round(T / dt, 2), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "%d tokens of the Qwen3-30B-A3B layer (E=128, k=8, H=2048, I=768) through the torch CPU op "
+                      "sequence of moe_ref.moe_forward (per-expert loop, int64 matmuls)" % T}
+
+
 def cpu_baseline_dense(args):
     """The reference's CPU op sequence for w8a8_matmul on a row sample of both step shapes."""
     import numpy as np
@@ -198,16 +304,13 @@ def main():
         log("bench: decode rows M in {1, 8, 32}")
         out["decode"] = decode_section(torch, args)
     if "moe" in sections:
-        try:
-            from bench_moe import moe_section
-        except ImportError:
-            moe_section = None
-        if moe_section is not None:
-            log("bench: MoE layers")
-            out["moe"] = moe_section(torch, args)
+        log("bench: MoE layers")
+        out["moe"] = moe_section(torch, args)
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (reference op sequence, row sample)")
         out["cpu_baseline"] = cpu_baseline_dense(args)
+        if "moe" in sections:
+            out["moe"]["cpu_baseline"] = cpu_baseline_moe(args)
     print(json.dumps(out), flush=True)
 
 

@@ -238,7 +238,7 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
     y = torch.empty((T, H), dtype=BF, device=x.device)
     if T == 0:
         return y
-    nbytes = L.load().lsk_moe_workspace(T, k, tables.E, H, tables.I, rot_blk)
+    nbytes = L.load().lsk_moe_workspace(T, k, tables.E, H, tables.I, rot_blk, 0)
     work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     sh = None if shared_out is None else shared_out.to(F32).contiguous()
     a = L.MoeArgs(T=T, H=H, I=tables.I, E=tables.E, k=k, act=act, x=x.data_ptr(), idx=idx.data_ptr(),
