@@ -98,9 +98,9 @@ int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Tuning control with no counterpart in the reference: force the dense prefill tile
- * (0: 256x256 tile, 4 waves of 128x128; 1: 256x128, 4 waves of 128x64; 2: 128x128, 4 waves
- * of 64x64; 3: 256x256, 8 waves of 64x128; 4: 128x256, 4 waves of 64x128) or -1 to choose by
- * shape (the default).  Results are identical for every choice; only speed differs.
+ * (0: 256x256 tile, 4 waves of 128x128; 1: 256x128, 8 waves of 64x64; 2: 128x128, 4 waves
+ * of 64x64; 3: 256x256, 8 waves of 64x128; 4: 128x256, 8 waves of 64x64; 5-8: tiles 2, 1, 3, 4
+ * with global loads issued two K stages ahead) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
  * Process-wide, not thread-safe against concurrent launches. */
 int lsk_gemm_select(int tile_id);
 

@@ -17,9 +17,9 @@ using lsk::zero4;
 // Dense tile kernel: C[m, n] = sum_k A[m, k] * W[n, k] with the epilogue applied per element.
 // A and W are K-contiguous with 16-byte aligned rows and K % 16 == 0.  Logical tile ids walk
 // M-fastest inside groups of 16 M-tiles after the XCD remap.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int PF>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
-    const int8_t* __restrict__ A, int64_t lda, const int8_t* __restrict__ W, int64_t ldw, int M, int N, int K,
+    const int8_t* __restrict__ A, int lda, const int8_t* __restrict__ W, int ldw, int M, int N, int K,
     EpiParams ep, int vec_ok) {
   using C = lsk::TileCfg<BM, BN, WM, WN>;
   extern __shared__ v4i smem[];
@@ -34,43 +34,48 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  // resources start at the tile's first row: offsets stay below BM * lda
+  const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(A + (int64_t)m0 * lda, (int64_t)(M - m0) * lda);
+  const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)(N - n0) * ldw);
   typename C::RowsA pa;
   typename C::RowsB pb;
 #pragma unroll
   for (int j = 0; j < C::kAPer; ++j) {
     int row, c;
     lsk::chunk_of<C::kThreads>(tid, j, row, c);
-    pa[j] = (m0 + row < M) ? A + (int64_t)(m0 + row) * lda : nullptr;
+    pa[j] = (m0 + row < M) ? (uint32_t)(row * lda) : lsk::kOob;
   }
 #pragma unroll
   for (int j = 0; j < C::kBPer; ++j) {
     int row, c;
     lsk::chunk_of<C::kThreads>(tid, j, row, c);
-    pb[j] = (n0 + row < N) ? W + (int64_t)(n0 + row) * ldw : nullptr;
+    pb[j] = (n0 + row < N) ? (uint32_t)(row * ldw) : lsk::kOob;
   }
   typename C::Acc acc;
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) acc[i][j] = zero4();
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  lsk::mfma_mainloop<BM, BN, WM, WN>(acc, pa, pb, K, smem);
+  lsk::mfma_mainloop<BM, BN, WM, WN, PF>(acc, ra_res, pa, rb_res, pb, K, smem);
 
   int32_t* region = (int32_t*)smem + wave * C::kStripInts;
   constexpr int kQuads = C::WTN / 4;
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i) {
-    lsk::stage_strip<C::TN, C::kLdc>(acc[i], region);
-    __syncthreads();
-    for (int q = lane; q < 16 * kQuads; q += 64) {
-      const int row = q / kQuads, c4 = q - row * kQuads;
-      const v4i v = *(const v4i*)(region + row * C::kLdc + c4 * 4);
-      const int m = m0 + wm * C::WTM + i * 16 + row;
-      const int n = n0 + wn * C::WTN + c4 * 4;
-      if (m < M && n < N) epilogue_store4(ep, m, n, N, v, vec_ok && n + 4 <= N);
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      lsk::stage_half<C::TN, C::kLdc>(acc[i], h, region);
+      __syncthreads();
+      for (int q = lane; q < 16 * kQuads; q += 64) {
+        const int row = q / kQuads, c4 = q - row * kQuads;
+        const v4i v = *(const v4i*)(region + row * C::kLdc + c4 * 4);
+        const int m = m0 + wm * C::WTM + i * 32 + h * 16 + row;
+        const int n = n0 + wn * C::WTN + c4 * 4;
+        if (m < M && n < N) epilogue_store4(ep, m, n, N, v, vec_ok && n + 4 <= N);
+      }
+      __syncthreads();
     }
-    __syncthreads();
-  }
 }
 
 // Decode GEMV: one block per 16 output columns; its 4 waves take interleaved 256-byte K slabs;
@@ -174,12 +179,12 @@ int validate_epilogue(int order, int out_dtype, const float* asc, const float* w
 // Tile configurations of the dense kernel; id -1 lets the shape decide.
 static int g_force_tile = -1;
 
-template <int BM, int BN, int WM, int WN>
-static int launch_tile(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int M, int N, int K,
+template <int BM, int BN, int WM, int WN, int PF = 1>
+static int launch_tile(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K,
                        const EpiParams& ep, int vec_ok, hipStream_t s, const char* name) {
   using C = TileCfg<BM, BN, WM, WN>;
   static bool attr_set = false;
-  auto kern = gemm_i8_mfma_kernel<BM, BN, WM, WN>;
+  auto kern = gemm_i8_mfma_kernel<BM, BN, WM, WN, PF>;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmemBytes) !=
         hipSuccess) {
@@ -207,8 +212,9 @@ static int pick_tile(int64_t M, int64_t N) {
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiParams& ep, hipStream_t s) {
   if (M == 0 || N == 0) return LSK_OK;
+  // the tile kernels address rows by 32-bit offsets inside a 256-row tile
   const bool fast = (K % 16 == 0) && (lda % 16 == 0) && (ldw % 16 == 0) && aligned16(a) && aligned16(w) &&
-                    M <= 0x7fffffff && N <= 0x7fffffff && K > 0;
+                    M <= 0x7fffffff && N <= 0x7fffffff && K > 0 && lda * 256 < 0x7fffffff && ldw * 256 < 0x7fffffff;
   if (!fast) {
     const int64_t total = M * N;
     const int64_t blocks = (total + 255) / 256;
@@ -228,12 +234,17 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     return check_launch("gemv_i8_mfma_kernel<2>");
   }
   const int vec_ok = out_vec_ok(ep.out, ep.out_dtype, ep.ldo) ? 1 : 0;
+  const int ilda = (int)lda, ildw = (int)ldw;
   switch (pick_tile(M, N)) {
-    case 0: return launch_tile<256, 256, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,2x2>");
-    case 1: return launch_tile<256, 128, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x128,2x2>");
-    case 3: return launch_tile<256, 256, 4, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,4x2>");
-    case 4: return launch_tile<128, 256, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x256,2x2>");
-    default: return launch_tile<128, 128, 2, 2>(a, lda, w, ldw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2>");
+    case 0: return launch_tile<256, 256, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,2x2>");
+    case 1: return launch_tile<256, 128, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x128,4x2>");
+    case 3: return launch_tile<256, 256, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,4x2>");
+    case 4: return launch_tile<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x256,2x4>");
+    case 5: return launch_tile<128, 128, 2, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2,pf2>");
+    case 6: return launch_tile<256, 128, 4, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x128,4x2,pf2>");
+    case 7: return launch_tile<256, 256, 4, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,4x2,pf2>");
+    case 8: return launch_tile<128, 256, 2, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x256,2x4,pf2>");
+    default: return launch_tile<128, 128, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2>");
   }
 }
 
@@ -301,7 +312,7 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 4, "lsk_gemm_select: tile id %d not in [-1, 4]", tile_id);
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 8, "lsk_gemm_select: tile id %d not in [-1, 8]", tile_id);
   lsk::g_force_tile = tile_id;
   return LSK_OK;
 }

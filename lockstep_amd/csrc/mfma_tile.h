@@ -4,17 +4,19 @@
 // are addressed through per-thread row pointers fixed before the K loop, so a caller can
 // gather rows (MoE token rows), interleave weight rows (gate/up pairs) or clip at the matrix
 // edge (a null pointer loads zeros).  K stages of 128 bytes are double-buffered in LDS as
-// 16-byte chunks whose position within a row is XOR-swizzled by the row index, so the
-// 16 lanes that read one MFMA operand column hit 16 distinct bank groups.
+// 16-byte chunks; chunk c of row r sits at position c ^ ((r >> 1) & 7), so any 16 consecutive
+// rows reading one logical chunk hit 16 distinct 16-byte bank groups (two 128-byte rows span
+// the 64 four-byte banks).
 //
-// v_mfma_i32_16x16x64_i8: lane l supplies 16 bytes of row (l % 16) at K-group (l / 16) of the
-// A operand and of the W operand alike; D[i][j] lands in lane j + 16 * (i / 4), register i % 4.
-// Integer accumulation is exact in any order (|acc| <= K * 127^2 < 2^31), so the K blocking
-// never changes a result.
+// v_mfma_i32_32x32x32_i8 (measured at 97% of the 5.0 POPS int8 peak in a register-only loop;
+// the 16x16x64 form stalls near 55-70%): lane l supplies 16 bytes of row (l % 32) at K-group
+// (l / 32) of the A operand and of the W operand alike; D[i][j] lands in lane j + 32 * ((i / 4) % 2),
+// register 4 * (i / 8) + i % 4.  Integer accumulation is exact in any order (|acc| <= K * 127^2
+// < 2^31), so the K blocking never changes a result.
 //
-// Results leave the registers through LDS one 16-row strip at a time (per wave, static
-// register indices), and are read back four consecutive columns per lane so the epilogue
-// issues full-width, coalesced stores.
+// Results leave the registers through LDS 16 rows at a time (per wave, static register indices)
+// and are read back four consecutive columns per lane, so the epilogue issues full-width,
+// coalesced stores.
 #pragma once
 #include "lsk_common.h"
 
@@ -22,27 +24,46 @@ namespace lsk {
 
 constexpr int kBK = 128;  // bytes of K per LDS stage
 
+LSK_DEV v16i mfma_i8_32(v4i a, v4i b, v16i c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
 LSK_DEV v4i mfma_i8(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
 LSK_DEV v4i zero4() { return v4i{0, 0, 0, 0}; }
+LSK_DEV v16i zero16() { return v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}; }
+
+// Raw buffer loads: an access at or beyond the resource's byte range returns zero in hardware,
+// so edge rows and the K tail need no branch around the load (branches around loads also stop
+// the compiler from counting outstanding loads, which serialises the prefetch).
+constexpr uint32_t kOob = 0x80000000u;  // an offset beyond any resource range used here
+
+LSK_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+LSK_DEV v4i buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// Position of 16-byte chunk c (0..7) of row r in a tile of 128-byte rows.
+LSK_DEV int swz8(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
 
 template <int BM, int BN, int WM, int WN>
 struct TileCfg {
   static constexpr int kThreads = WM * WN * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
-  static constexpr int TM = WTM / 16, TN = WTN / 16;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;       // 32x32 MFMA tiles per wave
   static constexpr int kAPer = BM * kBK / 16 / kThreads;  // 16-byte chunks per thread per stage
   static constexpr int kBPer = BN * kBK / 16 / kThreads;
   static constexpr int kSmemA = BM * 8, kSmemB = BN * 8;  // v4i chunks per stage
-  static constexpr int kLdc = WTN + 4;                     // int32 row stride of a staged strip
+  static constexpr int kLdc = WTN + 8;                     // int32 row stride of a staged half strip
   static constexpr int kStripInts = 16 * kLdc;             // per wave
   static constexpr int kMainBytes = 2 * (kSmemA + kSmemB) * 16;
   static constexpr int kEpiBytes = WM * WN * kStripInts * 4;
   static constexpr int kSmemBytes = kMainBytes > kEpiBytes ? kMainBytes : kEpiBytes;
   static_assert((BM * kBK / 16) % kThreads == 0 && (BN * kBK / 16) % kThreads == 0, "tile/threads");
-  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be a multiple of 16");
-  typedef v4i Acc[TM][TN];
-  typedef const int8_t* RowsA[kAPer];
-  typedef const int8_t* RowsB[kBPer];
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
+  typedef v16i Acc[TM][TN];
+  typedef uint32_t RowsA[kAPer];  // byte offset of each load slot's row in its resource (kOob: zero row)
+  typedef uint32_t RowsB[kBPer];
 };
 
 // Row index (within the tile) and 16-byte chunk index that thread `tid` loads in slot j.
@@ -53,92 +74,117 @@ LSK_DEV void chunk_of(int tid, int j, int& row, int& c) {
   c = i & 7;
 }
 
-// acc[TM][TN] += A_tile * W_tile^T over K (K % 16 == 0; row pointers 16-byte aligned).
-// pa / pb: the global row pointers of this thread's load slots (null = zero row).
-template <int BM, int BN, int WM, int WN>
-LSK_DEV void mfma_mainloop(typename TileCfg<BM, BN, WM, WN>::Acc& acc, const typename TileCfg<BM, BN, WM, WN>::RowsA& pa,
+// acc[TM][TN] += A_tile * W_tile^T over K (K % 16 == 0; rows 16-byte aligned).
+// ra_res / rb_res: buffer resources over the operands; pa / pb: the byte offsets of this thread's
+// load-slot rows in them (kOob = zero row).
+// PF: global prefetch depth in K stages (1: the next stage's loads are issued while the current
+// one is computed; 2: two stages ahead, through two register sets), to cover HBM latency when
+// one block per CU leaves no other block to overlap with.
+template <int BM, int BN, int WM, int WN, int PF = 1>
+LSK_DEV void mfma_mainloop(typename TileCfg<BM, BN, WM, WN>::Acc& acc, __amdgpu_buffer_rsrc_t ra_res,
+                           const typename TileCfg<BM, BN, WM, WN>::RowsA& pa, __amdgpu_buffer_rsrc_t rb_res,
                            const typename TileCfg<BM, BN, WM, WN>::RowsB& pb, int K, v4i* smem) {
   using C = TileCfg<BM, BN, WM, WN>;
+  static_assert(PF == 1 || PF == 2, "prefetch depth 1 or 2");
   v4i* sA = smem;
   v4i* sB = smem + 2 * C::kSmemA;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  v4i ra[C::kAPer], rb[C::kBPer];
-  auto gload = [&](int k0) {
+  v4i ra[PF][C::kAPer], rb[PF][C::kBPer];
+  auto gload = [&](int set, int k0) {
 #pragma unroll
     for (int j = 0; j < C::kAPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
       const int gk = k0 + c * 16;
-      ra[j] = (pa[j] && gk < K) ? *(const v4i*)(pa[j] + gk) : zero4();
+      ra[set][j] = buf_load16(ra_res, gk < K ? pa[j] + (uint32_t)gk : kOob);
     }
 #pragma unroll
     for (int j = 0; j < C::kBPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
       const int gk = k0 + c * 16;
-      rb[j] = (pb[j] && gk < K) ? *(const v4i*)(pb[j] + gk) : zero4();
+      rb[set][j] = buf_load16(rb_res, gk < K ? pb[j] + (uint32_t)gk : kOob);
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int set, int buf) {
 #pragma unroll
     for (int j = 0; j < C::kAPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
-      sA[buf * C::kSmemA + row * 8 + (c ^ (row & 7))] = ra[j];
+      sA[buf * C::kSmemA + swz8(row, c)] = ra[set][j];
     }
 #pragma unroll
     for (int j = 0; j < C::kBPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
-      sB[buf * C::kSmemB + row * 8 + (c ^ (row & 7))] = rb[j];
+      sB[buf * C::kSmemB + swz8(row, c)] = rb[set][j];
+    }
+  };
+  auto compute = [&](int buf) {
+    const v4i* a_s = sA + buf * C::kSmemA;
+    const v4i* b_s = sB + buf * C::kSmemB;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int c = ks * 2 + (lane >> 5);
+      v4i af[C::TM], bf[C::TN];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) af[i] = a_s[swz8(wm * C::WTM + i * 32 + (lane & 31), c)];
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) bf[j] = b_s[swz8(wn * C::WTN + j * 32 + (lane & 31), c)];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma_i8_32(af[i], bf[j], acc[i][j]);
     }
   };
 
   const int nk = (K + kBK - 1) / kBK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
-    const v4i* a_s = sA + buf * C::kSmemA;
-    const v4i* b_s = sB + buf * C::kSmemB;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int c = ks * 4 + (lane >> 4);
-      v4i af[C::TM], bf[C::TN];
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i) {
-        const int r = wm * C::WTM + i * 16 + (lane & 15);
-        af[i] = a_s[r * 8 + (c ^ (r & 7))];
-      }
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j) {
-        const int r = wn * C::WTN + j * 16 + (lane & 15);
-        bf[j] = b_s[r * 8 + (c ^ (r & 7))];
-      }
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
-    }
-    if (kt + 1 < nk) sstore(buf ^ 1);
+  if (PF == 1) {
+    gload(0, 0);
+    sstore(0, 0);
     __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      if (kt + 1 < nk) gload(0, (kt + 1) * kBK);
+      compute(buf);
+      if (kt + 1 < nk) sstore(0, buf ^ 1);
+      __syncthreads();
+    }
+  } else {
+    // stage s is loaded into register set s & 1, two iterations before it is computed
+    gload(0, 0);
+    if (nk > 1) gload(1, kBK);
+    sstore(0, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+      // even stage kt in LDS buffer 0, registers of set 1 hold stage kt + 1
+      if (kt + 2 < nk) gload(0, (kt + 2) * kBK);
+      compute(0);
+      if (kt + 1 < nk) sstore(1, 1);
+      __syncthreads();
+      if (kt + 1 >= nk) break;
+      if (kt + 3 < nk) gload(1, (kt + 3) * kBK);
+      compute(1);
+      if (kt + 2 < nk) sstore(0, 0);
+      __syncthreads();
+    }
   }
 }
 
-// Write the 16-row strip `strip` of this wave's accumulators into the wave's LDS region
-// (row stride TileCfg::kLdc int32).  Called after the main loop's final barrier; the region
-// is private to the wave, and a wave's LDS accesses complete in program order.
+// Write half h (rows 16h .. 16h+15) of the wave's 32-row strip `strip` into the wave's LDS
+// region (row stride LDC int32).  Called after the main loop's final barrier.
 template <int TN, int LDC>
-LSK_DEV void stage_strip(const v4i* strip, int32_t* region) {
+LSK_DEV void stage_half(const v16i* strip, int h, int32_t* region) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < TN; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) region[((lane >> 4) * 4 + r) * LDC + j * 16 + (lane & 15)] = strip[j][r];
+    for (int rr = 0; rr < 8; ++rr) {
+      const int row = 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+      region[row * LDC + j * 32 + (lane & 31)] = strip[j][8 * h + rr];
+    }
 }
 
 // Map a hardware block id to a logical tile id so the blocks one XCD runs (hardware ids

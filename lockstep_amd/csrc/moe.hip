@@ -208,6 +208,10 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / 2, wn = wave % 2;
+  // one resource over the whole activation matrix (gathered rows) and one over this expert's
+  // weight; the host guarantees both spans fit 31-bit offsets
+  const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(a.A, a.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(wb, a.w_bytes);
   typename C::RowsA pa;
   typename C::RowsB pb;
 #pragma unroll
@@ -216,111 +220,117 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     lsk::chunk_of<C::kThreads>(tid, j, row, c);
     const int p = p0 + row;
     const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
-    pa[j] = src >= 0 ? (const int8_t*)a.A + (int64_t)src * a.lda : nullptr;
+    pa[j] = src >= 0 ? (uint32_t)(src * a.lda) : lsk::kOob;
   }
 #pragma unroll
   for (int j = 0; j < C::kBPer; ++j) {
     int row, c;
     lsk::chunk_of<C::kThreads>(tid, j, row, c);
     if (MODE == 0) {
-      const int blk = row >> 4;
-      const int hc = nt * 64 + (blk >> 1) * 16 + (row & 15);
-      pb[j] = hc < a.N ? wb + (int64_t)((blk & 1) ? a.N + hc : hc) * a.ldw : nullptr;
+      const int blk = row >> 5;  // 32-row blocks alternate gate / up weight rows
+      const int hc = nt * 64 + (blk >> 1) * 32 + (row & 31);
+      pb[j] = hc < a.N ? (uint32_t)(((blk & 1) ? a.N + hc : hc) * a.ldw) : lsk::kOob;
     } else {
       const int n = nt * 128 + row;
-      pb[j] = n < a.N ? wb + (int64_t)n * a.ldw : nullptr;
+      pb[j] = n < a.N ? (uint32_t)(n * a.ldw) : lsk::kOob;
     }
   }
   typename C::Acc acc;
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero4();
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  lsk::mfma_mainloop<128, 128, 2, 2>(acc, pa, pb, a.K, smem);
+  lsk::mfma_mainloop<128, 128, 2, 2>(acc, ra_res, pa, rb_res, pb, a.K, smem);
 
   int32_t* region = (int32_t*)smem + wave * C::kStripInts;
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i) {
-    lsk::stage_strip<C::TN, C::kLdc>(acc[i], region);
-    __syncthreads();
-    if (MODE == 0) {
-      // strip columns: [gate pair 0 | up pair 0 | gate pair 1 | up pair 1], 16 each
+  for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-      for (int pass = 0; pass < 2; ++pass) {
-        const int q = pass * 64 + lane;
-        const int row = q >> 3, hq = q & 7, pair = hq >> 2, c4 = (hq & 3) * 4;
-        const v4i vg = *(const v4i*)(region + row * C::kLdc + pair * 32 + c4);
-        const v4i vu = *(const v4i*)(region + row * C::kLdc + pair * 32 + 16 + c4);
-        const int p = p0 + wm * 64 + i * 16 + row;
-        const int hc0 = nt * 64 + wn * 32 + pair * 16 + c4;
-        float am = 0.0f;
-        if (p < p1) {
-          const float asc = a.a_scale[a.row_tok[p]];
-          uint16_t hb[4];
+    for (int hh = 0; hh < 2; ++hh) {
+      lsk::stage_half<C::TN, C::kLdc>(acc[i], hh, region);
+      __syncthreads();
+      const int rbase = p0 + wm * 64 + i * 32 + hh * 16;
+      if (MODE == 0) {
+        // half-strip columns: [gate 32 | up 32] for h columns nt*64 + wn*32 + [0, 32)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int hc = hc0 + t;
-            hb[t] = 0;
-            if (hc < a.N) {
-              float yg = bfr(f32_mul(f32_mul((float)vg[t], ws[hc]), asc));
-              float yu = bfr(f32_mul(f32_mul((float)vu[t], ws[a.N + hc]), asc));
-              if (bias) {
-                yg = bfr(f32_add(yg, bias[hc]));
-                yu = bfr(f32_add(yu, bias[a.N + hc]));
+        for (int pass = 0; pass < 2; ++pass) {
+          const int q = pass * 64 + lane;
+          const int row = q >> 3, c4 = (q & 7) * 4;
+          const v4i vg = *(const v4i*)(region + row * C::kLdc + c4);
+          const v4i vu = *(const v4i*)(region + row * C::kLdc + 32 + c4);
+          const int p = rbase + row;
+          const int hc0 = nt * 64 + wn * 32 + c4;
+          float am = 0.0f;
+          if (p < p1) {
+            const float asc = a.a_scale[a.row_tok[p]];
+            uint16_t hb[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int hc = hc0 + t;
+              hb[t] = 0;
+              if (hc < a.N) {
+                float yg = bfr(f32_mul(f32_mul((float)vg[t], ws[hc]), asc));
+                float yu = bfr(f32_mul(f32_mul((float)vu[t], ws[a.N + hc]), asc));
+                if (bias) {
+                  yg = bfr(f32_add(yg, bias[hc]));
+                  yu = bfr(f32_add(yu, bias[a.N + hc]));
+                }
+                const float hv =
+                    a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
+                hb[t] = f32_to_bf16(hv);
+                am = fmaxf(am, fabsf(hv));
               }
-              const float hv = a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
-              hb[t] = f32_to_bf16(hv);
-              am = fmaxf(am, fabsf(hv));
+            }
+            uint16_t* dst = a.h + (int64_t)p * a.N + hc0;
+            if (hc0 + 4 <= a.N) {
+              *(uint2*)dst =
+                  make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
+            } else {
+              for (int t = 0; t < 4; ++t)
+                if (hc0 + t < a.N) dst[t] = hb[t];
             }
           }
-          uint16_t* dst = a.h + (int64_t)p * a.N + hc0;
-          if (hc0 + 4 <= a.N) {
-            *(uint2*)dst = make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
-          } else {
-            for (int t = 0; t < 4; ++t)
-              if (hc0 + t < a.N) dst[t] = hb[t];
-          }
+          am = fmaxf(am, __shfl_xor(am, 1, 64));
+          am = fmaxf(am, __shfl_xor(am, 2, 64));
+          am = fmaxf(am, __shfl_xor(am, 4, 64));
+          if ((lane & 7) == 0 && p < p1) atomicMax(&a.h_amax[p], __float_as_uint(am));
         }
-        am = fmaxf(am, __shfl_xor(am, 1, 64));
-        am = fmaxf(am, __shfl_xor(am, 2, 64));
-        am = fmaxf(am, __shfl_xor(am, 4, 64));
-        if ((lane & 7) == 0 && p < p1) atomicMax(&a.h_amax[p], __float_as_uint(am));
-      }
-    } else {
+      } else {
 #pragma unroll
-      for (int pass = 0; pass < 4; ++pass) {
-        const int q = pass * 64 + lane;
-        const int row = q >> 4, c4 = (q & 15) * 4;
-        const v4i v = *(const v4i*)(region + row * C::kLdc + c4);
-        const int p = p0 + wm * 64 + i * 16 + row;
-        const int n0 = nt * 128 + wn * 64 + c4;
-        if (p < p1 && n0 < a.N) {
-          const float asc = a.a_scale[p];
-          const float wt = a.row_w[p];
-          uint16_t ob[4];
+        for (int pass = 0; pass < 4; ++pass) {
+          const int q = pass * 64 + lane;
+          const int row = q >> 4, c4 = (q & 15) * 4;
+          const v4i v = *(const v4i*)(region + row * C::kLdc + c4);
+          const int p = rbase + row;
+          const int n0 = nt * 128 + wn * 64 + c4;
+          if (p < p1 && n0 < a.N) {
+            const float asc = a.a_scale[p];
+            const float wt = a.row_w[p];
+            uint16_t ob[4];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int n = n0 + t;
-            ob[t] = 0;
-            if (n < a.N) {
-              float yv = bfr(f32_mul(f32_mul((float)v[t], ws[n]), asc));
-              if (bias) yv = bfr(f32_add(yv, bias[n]));
-              ob[t] = f32_to_bf16(f32_mul(wt, yv));
+            for (int t = 0; t < 4; ++t) {
+              const int n = n0 + t;
+              ob[t] = 0;
+              if (n < a.N) {
+                float yv = bfr(f32_mul(f32_mul((float)v[t], ws[n]), asc));
+                if (bias) yv = bfr(f32_add(yv, bias[n]));
+                ob[t] = f32_to_bf16(f32_mul(wt, yv));
+              }
+            }
+            uint16_t* dst = a.y + (int64_t)a.row_dst[p] * a.N + n0;
+            if (n0 + 4 <= a.N) {
+              *(uint2*)dst =
+                  make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+            } else {
+              for (int t = 0; t < 4; ++t)
+                if (n0 + t < a.N) dst[t] = ob[t];
             }
           }
-          uint16_t* dst = a.y + (int64_t)a.row_dst[p] * a.N + n0;
-          if (n0 + 4 <= a.N) {
-            *(uint2*)dst = make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
-          } else {
-            for (int t = 0; t < 4; ++t)
-              if (n0 + t < a.N) dst[t] = ob[t];
-          }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
-  }
 }
 
 // ---------------------------------------------------------------- requant and combine
@@ -524,7 +534,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(H % 16 == 0 && I % 16 == 0, "lsk_moe_forward: H and I must be multiples of 16");
   LSK_REQUIRE(H <= 133144 && I <= 133144, "lsk_moe_forward: K above the int32-exact bound");
   LSK_REQUIRE(a->act == LSK_ACT_SILU || a->act == LSK_ACT_SWIGLUOAI, "lsk_moe_forward: unknown act %d", a->act);
-  LSK_REQUIRE(T * k <= 0x7fffffff && T * H <= ((int64_t)1 << 40), "lsk_moe_forward: T too large");
+  LSK_REQUIRE(T * k <= 0x7fffffff && T * H * 2 < 0x7fffffff && T * k * I * 2 < 0x7fffffff,
+              "lsk_moe_forward: activations beyond 2 GB (31-bit buffer offsets)");
   if (T == 0) return LSK_OK;
   LSK_REQUIRE(a->x && a->idx && a->w && a->w13_ptrs && a->ws13_ptrs && a->w2_ptrs && a->ws2_ptrs && a->frac && a->y,
               "lsk_moe_forward: null pointer");
@@ -535,6 +546,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   } else {
     LSK_REQUIRE(a->ldw13 >= H && a->ldw13 % 16 == 0 && a->ldw2 >= I && a->ldw2 % 16 == 0,
                 "lsk_moe_forward: weight row strides must cover K and be multiples of 16");
+    LSK_REQUIRE(2 * I * a->ldw13 < 0x7fffffff && H * a->ldw2 < 0x7fffffff,
+                "lsk_moe_forward: an expert's weight beyond 2 GB (31-bit buffer offsets)");
   }
   const int rb = a->rot_blk;
   LSK_REQUIRE(rb == 0 || (rb >= 2 && rb <= 1024 && (rb & (rb - 1)) == 0 && H % rb == 0 && I % rb == 0 && I <= 16384),
@@ -577,6 +590,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   MoeGemmArgs g1{};
   g1.A = w.qx;
   g1.lda = H;
+  g1.a_bytes = T * H;
+  g1.w_bytes = 2 * I * a->ldw13;
   g1.a_scale = w.ascx;
   g1.row_tok = w.row_tok;
   g1.offs = w.offs;
@@ -613,6 +628,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   MoeGemmArgs g2{};
   g2.A = w.qh;
   g2.lda = I;
+  g2.a_bytes = R * I;
+  g2.w_bytes = H * a->ldw2;
   g2.a_scale = w.asch;
   g2.offs = w.offs;
   g2.tiles = w.tiles;

@@ -10,6 +10,8 @@ constexpr int kMoeBM = 128;  // rows per expert tile (the dispatch's tile table 
 struct MoeGemmArgs {
   const void* A;            // int8 (int8 experts) or bf16 (MXFP4 experts) activation rows
   int64_t lda;              // elements
+  int64_t a_bytes;          // bytes of A (its buffer resource range)
+  int64_t w_bytes;          // bytes of one expert's weight (its buffer resource range)
   const float* a_scale;     // per A row
   const int32_t* row_tok;   // gate/up: permuted row -> token (A row); down: unused
   const int32_t* offs;      // [E + 1]
