@@ -95,7 +95,7 @@ def dense_section(torch, args):
         "ms_per_step": ms, "value": tops, "wall_s": wall, "ops_step": ops_step,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                     "kernel": "gemm_i8_mfma_kernel", "per_shape": per_shape,
+                     "kernel": "gemm_i8_pp_kernel", "per_shape": per_shape,
                      "note": "int8 ops (2 per MAC) per launch / average launch time, HIP events"},
     }
 

@@ -1,7 +1,9 @@
 // Dense contract GEMM on gfx950: exact int8 x int8 -> int32 on MFMA, fused binary32 epilogue.
 //
-//   prefill (M > 32): LDS-staged MFMA tiles, v_mfma_i32_16x16x64_i8, double-buffered 128-byte
-//                     K stages, XOR-swizzled 16-byte LDS chunks, XCD-aware tile order.
+//   prefill (M > 128): eight-wave ping-pong MFMA tiles (pp_tile.h), v_mfma_i32_32x32x32_i8,
+//                     four 64-byte K stages in flight through direct-to-LDS loads, XCD-aware
+//                     tile order, epilogue operands staged in LDS.
+//   small   (32 < M <= 128): register-staged 128x128 MFMA tiles (mfma_tile.h).
 //   decode  (M <= 32): weight-streaming GEMV on the same MFMA (rows padded to 16 in registers),
 //                     K split over the block's waves and reduced exactly in LDS.
 //   generic:          any stride / alignment / K, one thread per output (correctness path).
@@ -9,6 +11,7 @@
 // Integer accumulation is exact in any order (|acc| <= K * 127^2 < 2^31 for K <= 133144), so
 // tiling and K-splits never change a bit; the epilogue is applied once per output element.
 #include "mfma_tile.h"
+#include "pp_tile.h"
 
 namespace {
 
@@ -76,6 +79,152 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
       }
       __syncthreads();
     }
+}
+
+// Epilogue of the ping-pong kernel, one staged 32-row strip (strip i of the wave's tile, in the
+// wave's LDS region): the contract epilogue over four consecutive columns per lane (a lane
+// always covers the same four columns), with the tile's operands read from LDS.  ORDER / ODT /
+// BIAS specialise the common cases; -1 evaluates them at run time.
+template <class C, int ORDER, int ODT, bool BIAS>
+__device__ __forceinline__ void pp_strip_store(int i, const int32_t* region, const EpiParams& ep, int m0, int n0,
+                                               int M, int N, int vec_ok, const char* smem) {
+  const int order = ORDER >= 0 ? ORDER : ep.order;
+  const int odt = ODT >= 0 ? ODT : ep.out_dtype;
+  const bool has_bias = ORDER >= 0 ? BIAS : ep.bias != nullptr;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / C::kWN, wn = wave % C::kWN;
+  const float* sc_row = (const float*)(smem + C::kScaleOff);
+  const float* sc_ws = sc_row + C::kBM;
+  const float* sc_b = sc_ws + C::kBN;
+  const int* sc_ec = (const int*)(sc_b + C::kBN);
+  constexpr int kQuads = C::WTN / 4;
+  static_assert(64 % kQuads == 0, "a lane keeps one column quad");
+  const int c4 = lane % kQuads;
+  const int nl = wn * C::WTN + c4 * 4;  // tile-local first column of the lane's quad
+  const int n = n0 + nl;
+  const v4f wsq = *(const v4f*)(sc_ws + nl);
+  const v4f bq = *(const v4f*)(sc_b + nl);
+  const v4i ecq = *(const v4i*)(sc_ec + nl);
+  const float wsv[4] = {wsq[0], wsq[1], wsq[2], wsq[3]}, bv[4] = {bq[0], bq[1], bq[2], bq[3]};
+  const int ecv[4] = {ecq[0], ecq[1], ecq[2], ecq[3]};
+  const bool pow2 = order == LSK_EPI_POW2;
+  const bool vec = vec_ok && n + 4 <= N;
+#pragma unroll
+  for (int t = 0; t < 32 * kQuads / 64; ++t) {
+    const int row = (lane + 64 * t) / kQuads;
+    const v4i v = *(const v4i*)(region + row * C::kLdc + c4 * 4);
+    const int ml = wm * C::WTM + i * 32 + row;
+    const int m = m0 + ml;
+    const float rv = sc_row[ml];
+    if (m < M && n < N)
+      epilogue_store4_pre(ep.out, ep.ldo, order, odt, has_bias, ep.shift, m, n, N, v, rv, wsv, bv,
+                          pow2 ? __float_as_int(rv) : 0, ecv, vec);
+  }
+}
+
+// All strips of the wave's tile, strip index a compile-time constant (the accumulators stay in
+// registers): stage strip I in the wave's LDS region, store it, recurse.
+template <class C, int ORDER, int ODT, bool BIAS, int I>
+__device__ __forceinline__ void pp_epilogue(const typename C::Acc& acc, const EpiParams& ep, int m0, int n0, int M,
+                                            int N, int vec_ok, char* smem) {
+  if constexpr (I < C::TM) {
+    int32_t* region = (int32_t*)(smem + (threadIdx.x >> 6) * C::kStripBytes);
+    lsk::pp_stage_strip<C::TN, C::kLdc>(acc[I], region);
+    pp_strip_store<C, ORDER, ODT, BIAS>(I, region, ep, m0, n0, M, N, vec_ok, smem);
+    pp_epilogue<C, ORDER, ODT, BIAS, I + 1>(acc, ep, m0, n0, M, N, vec_ok, smem);
+  }
+}
+
+// Dense ping-pong tile kernel (512 threads, eight waves in two alternating groups); same
+// operand contract and tile order as gemm_i8_mfma_kernel.  The epilogue operands of the tile
+// (asc / row exponents, ws, bias, column exponents) are loaded into registers before the main
+// loop and parked in LDS after it, so the epilogue itself touches global memory only to store.
+template <int BM, int BN, int WM, int WN, int RING>
+__global__ __launch_bounds__(512) void gemm_i8_pp_kernel(const int8_t* __restrict__ A, int lda,
+                                                         const int8_t* __restrict__ W, int ldw, int M, int N, int K,
+                                                         EpiParams ep, int vec_ok) {
+  using C = lsk::PPCfg<BM, BN, WM, WN, RING>;
+  extern __shared__ __attribute__((aligned(16))) char smem_pp[];
+  const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN;
+  const int L = lsk::xcd_logical_id(blockIdx.x, mtiles * ntiles);
+  constexpr int GM = 16;
+  const int group = L / (GM * ntiles);
+  const int first_m = group * GM;
+  const int gsize = (mtiles - first_m) < GM ? (mtiles - first_m) : GM;
+  const int r = L - group * GM * ntiles;
+  const int m0 = (first_m + r % gsize) * BM, n0 = (r / gsize) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  // epilogue operands: thread t holds row m0 + t and column n0 + t
+  float s_row = 0.0f, s_ws = 0.0f, s_b = 0.0f;
+  int s_ec = 0;
+  if (tid < BM && m0 + tid < M) {
+    if (ep.order == LSK_EPI_POW2) s_row = __int_as_float(ep.erow ? ep.erow[m0 + tid] : 0);
+    else if (ep.order != LSK_EPI_RAW) s_row = ep.asc[m0 + tid];
+  }
+  if (tid < BN && n0 + tid < N) {
+    if (ep.order == LSK_EPI_POW2) {
+      s_ec = ep.ecol ? ep.ecol[n0 + tid] : 0;
+    } else if (ep.order != LSK_EPI_RAW) {
+      s_ws = ep.ws[n0 + tid];
+      if (ep.bias) s_b = ep.bias[n0 + tid];
+    }
+  }
+
+  const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(A + (int64_t)m0 * lda, (int64_t)(M - m0) * lda);
+  const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)(N - n0) * ldw);
+  typename C::RowsA pa;
+  typename C::RowsB pb;
+#pragma unroll
+  for (int j = 0; j < C::kLA; ++j) {
+    int row, kb;
+    lsk::pp_slot<C::kThreads>(tid, j, row, kb);
+    pa[j] = (m0 + row < M) ? (uint32_t)(row * lda) : lsk::kOob;
+  }
+#pragma unroll
+  for (int j = 0; j < C::kLB; ++j) {
+    int row, kb;
+    lsk::pp_slot<C::kThreads>(tid, j, row, kb);
+    pb[j] = (n0 + row < N) ? (uint32_t)(row * ldw) : lsk::kOob;
+  }
+  typename C::Acc acc;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
+
+  lsk::pp_mainloop<BM, BN, WM, WN, RING>(acc, ra_res, pa, rb_res, pb, K, smem_pp);
+
+  // every wave is past its last read of the LDS ring
+  float* sc_row = (float*)(smem_pp + C::kScaleOff);
+  float* sc_ws = sc_row + BM;
+  float* sc_b = sc_ws + BN;
+  int* sc_ec = (int*)(sc_b + BN);
+  if (tid < BM) sc_row[tid] = s_row;
+  if (tid < BN) {
+    sc_ws[tid] = s_ws;
+    sc_b[tid] = s_b;
+    sc_ec[tid] = s_ec;
+  }
+  __syncthreads();
+  // each wave stages its own 32-row strips, then stores them through the epilogue
+  const bool bias = ep.bias != nullptr;
+#define LSK_PP_EPI(O, D, B)                                                        \
+  if (ep.order == O && ep.out_dtype == D && bias == B) {                           \
+    pp_epilogue<C, O, D, B, 0>(acc, ep, m0, n0, M, N, vec_ok, smem_pp);            \
+    return;                                                                        \
+  }
+  LSK_PP_EPI(LSK_EPI_V21, LSK_BF16, false)
+  LSK_PP_EPI(LSK_EPI_V21, LSK_BF16, true)
+  LSK_PP_EPI(LSK_EPI_V21, LSK_F32, false)
+  LSK_PP_EPI(LSK_EPI_V21, LSK_BF16_AS_F32, false)
+  LSK_PP_EPI(LSK_EPI_V2, LSK_BF16, false)
+  LSK_PP_EPI(LSK_EPI_POW2, LSK_F32, false)
+  LSK_PP_EPI(LSK_EPI_RAW, LSK_I32, false)
+#undef LSK_PP_EPI
+  pp_epilogue<C, -1, -1, false, 0>(acc, ep, m0, n0, M, N, vec_ok, smem_pp);  // any other combination
 }
 
 // Decode GEMV: one block per 16 output columns; its 4 waves take interleaved 256-byte K slabs;
@@ -200,13 +349,36 @@ static int launch_tile(const int8_t* a, int lda, const int8_t* w, int ldw, int M
   return check_launch(name);
 }
 
+template <int BM, int BN, int WM, int WN, int RING = 4>
+static int launch_pp(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K, const EpiParams& ep,
+                     int vec_ok, hipStream_t s, const char* name) {
+  using C = PPCfg<BM, BN, WM, WN, RING>;
+  static bool attr_set = false;
+  auto kern = gemm_i8_pp_kernel<BM, BN, WM, WN, RING>;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmemBytes) !=
+        hipSuccess) {
+      set_error("%s: cannot reserve %d bytes of LDS", name, C::kSmemBytes);
+      return LSK_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  LSK_REQUIRE(tiles <= 0x7fffffff, "gemm: too many tiles");
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C::kThreads), C::kSmemBytes, s, a, lda, w, ldw, M, N, K, ep,
+                     vec_ok);
+  return check_launch(name);
+}
+
 static int pick_tile(int64_t M, int64_t N) {
   if (g_force_tile >= 0) return g_force_tile;
-  // Measured on MI355X (Llama-3.1-8B / Qwen2.5-7B prefill shapes): the 256x256 tile of 8 waves
-  // wins once there are at least two full rounds of such tiles for the 256 CUs; below that the
-  // 128x128 tile (two blocks per CU) keeps every CU busy.
-  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-  return t256 >= 512 ? 3 : 2;
+  if (M <= 128) return 2;  // few rows: the 128x128 register-staged tile wastes least
+  // Ping-pong tiles: whole rounds of 256 blocks (one per CU) are what a launch costs.  A
+  // 256x128 tile takes 0.68 of a 256x256 tile's time (measured on MI355X at the Llama-3.1-8B /
+  // Qwen2.5-7B prefill shapes), so pick the shape with the smaller rounds x tile cost.
+  const int64_t r256 = ((M + 255) / 256 * ((N + 255) / 256) + 255) / 256;
+  const int64_t r128 = ((M + 255) / 256 * ((N + 127) / 128) + 255) / 256;
+  return (double)r128 * 0.68 < (double)r256 ? 11 : 10;
 }
 
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
@@ -244,6 +416,10 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     case 6: return launch_tile<256, 128, 4, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x128,4x2,pf2>");
     case 7: return launch_tile<256, 256, 4, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,4x2,pf2>");
     case 8: return launch_tile<128, 256, 2, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x256,2x4,pf2>");
+    case 9: return launch_pp<256, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,2x4>");
+    case 10: return launch_pp<256, 256, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,4x2>");
+    case 11: return launch_pp<256, 128, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x128,4x2>");
+    case 12: return launch_pp<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4>");
     default: return launch_tile<128, 128, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2>");
   }
 }
@@ -312,7 +488,7 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 8, "lsk_gemm_select: tile id %d not in [-1, 8]", tile_id);
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 12, "lsk_gemm_select: tile id %d not in [-1, 12]", tile_id);
   lsk::g_force_tile = tile_id;
   return LSK_OK;
 }

@@ -150,28 +150,39 @@ LSK_DEV float epi_value(const EpiParams& p, int64_t m, int64_t n, int32_t acc) {
   return f32_mul(v, sc);
 }
 
-// Four consecutive columns n..n+3 of row m: epilogue, rounding and one vector store when
-// `vec` (the row segment is aligned and in range), else element stores up to column N.
-LSK_DEV void epilogue_store4(const EpiParams& p, int64_t m, int64_t n, int64_t N, v4i acc, bool vec) {
-  if (!vec) {
-    for (int t = 0; t < 4; ++t)
-      if (n + t < N) epilogue_store(p, m, n + t, acc[t]);
+// Epilogue value of one element from operands already in registers: the row operand (asc[m],
+// or the POW2 row exponent), the column operands (ws[n], bias[n] or 0) and, for POW2, the
+// total exponent shift + erow[m] + ecol[n].  The same binary32 operations as epi_value.
+LSK_DEV float epi_value_pre(int order, int out_dtype, bool has_bias, int32_t acc, float ascm, float wsn, float bn,
+                            int pshift) {
+  const float v = (float)acc;  // int32 -> binary32, round to nearest even
+  if (order == LSK_EPI_V21) {
+    float y = f32_mul(f32_mul(v, wsn), ascm);
+    if (has_bias) y = f32_add(round_out(out_dtype, y), bn);
+    return y;
+  }
+  if (order == LSK_EPI_V2) {
+    float y = f32_mul(f32_mul(v, ascm), wsn);
+    if (has_bias) y = f32_add(y, bn);
+    return y;
+  }
+  float sc = (pshift > 149) ? 0.0f : (pshift < -127 ? __uint_as_float(0x7f800000u) : pow2f(-pshift));
+  return f32_mul(v, sc);
+}
+
+// Round four epilogue values to the output type and store them at element offset o with one
+// vector store (the row segment is aligned and in range).  RAW stores the accumulators.
+LSK_DEV void store4_out(void* out, int order, int out_dtype, int64_t o, const float* y, v4i acc) {
+  if (order == LSK_EPI_RAW) {
+    *(v4i*)((int32_t*)out + o) = acc;
     return;
   }
-  const int64_t o = m * p.ldo + n;
-  if (p.order == LSK_EPI_RAW) {
-    *(v4i*)((int32_t*)p.out + o) = acc;
-    return;
-  }
-  float y[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) y[t] = epi_value(p, m, n + t, acc[t]);
-  switch (p.out_dtype) {
+  switch (out_dtype) {
     case LSK_BF16: {
       uint2 u;
       u.x = (uint32_t)f32_to_bf16(y[0]) | ((uint32_t)f32_to_bf16(y[1]) << 16);
       u.y = (uint32_t)f32_to_bf16(y[2]) | ((uint32_t)f32_to_bf16(y[3]) << 16);
-      *(uint2*)((uint16_t*)p.out + o) = u;
+      *(uint2*)((uint16_t*)out + o) = u;
       break;
     }
     case LSK_F16: {
@@ -180,14 +191,53 @@ LSK_DEV void epilogue_store4(const EpiParams& p, int64_t m, int64_t n, int64_t N
             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y[1]) << 16);
       u.y = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y[2]) |
             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y[3]) << 16);
-      *(uint2*)((uint16_t*)p.out + o) = u;
+      *(uint2*)((uint16_t*)out + o) = u;
       break;
     }
     case LSK_BF16_AS_F32:
-      *(float4*)((float*)p.out + o) = make_float4(bfr(y[0]), bfr(y[1]), bfr(y[2]), bfr(y[3]));
+      *(float4*)((float*)out + o) = make_float4(bfr(y[0]), bfr(y[1]), bfr(y[2]), bfr(y[3]));
       break;
     default:
-      *(float4*)((float*)p.out + o) = make_float4(y[0], y[1], y[2], y[3]);
+      *(float4*)((float*)out + o) = make_float4(y[0], y[1], y[2], y[3]);
+  }
+}
+
+// Four consecutive columns n..n+3 of row m: epilogue, rounding and one vector store when
+// `vec` (the row segment is aligned and in range), else element stores up to column N.
+LSK_DEV void epilogue_store4(const EpiParams& p, int64_t m, int64_t n, int64_t N, v4i acc, bool vec) {
+  if (!vec) {
+    for (int t = 0; t < 4; ++t)
+      if (n + t < N) epilogue_store(p, m, n + t, acc[t]);
+    return;
+  }
+  float y[4];
+  if (p.order != LSK_EPI_RAW) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) y[t] = epi_value(p, m, n + t, acc[t]);
+  }
+  store4_out(p.out, p.order, p.out_dtype, m * p.ldo + n, y, acc);
+}
+
+// The same with the row and column operands already loaded (see epi_value_pre), the
+// epilogue given as plain values so the common cases fold to constants; stores element-wise
+// up to column N when not `vec`.
+LSK_DEV void epilogue_store4_pre(void* out, int64_t ldo, int order, int out_dtype, bool has_bias, int shift,
+                                 int64_t m, int64_t n, int64_t N, v4i acc, float ascm, const float* wsn,
+                                 const float* bn, int rshift, const int* cshift, bool vec) {
+  float y[4];
+  if (order != LSK_EPI_RAW) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      y[t] = epi_value_pre(order, out_dtype, has_bias, acc[t], ascm, wsn[t], bn[t], shift + rshift + cshift[t]);
+  }
+  if (vec) {
+    store4_out(out, order, out_dtype, m * ldo + n, y, acc);
+    return;
+  }
+  for (int t = 0; t < 4; ++t) {
+    if (n + t >= N) break;
+    if (order == LSK_EPI_RAW) ((int32_t*)out)[m * ldo + n + t] = acc[t];
+    else store_out(out, out_dtype, m * ldo + n + t, y[t]);
   }
 }
 

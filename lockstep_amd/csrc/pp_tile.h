@@ -1,0 +1,192 @@
+// Eight-wave ping-pong int8 MFMA main loop for gfx950 (dense and grouped contract GEMMs).
+//
+// A block of 512 threads computes a BM x BN tile of C = A * W^T over all of K.  Its eight
+// waves form two groups of four, one wave of each group per SIMD; the groups run half a
+// period apart, so while one group issues its MFMAs the other reads its operand fragments
+// from LDS and issues the next global loads.  Each SIMD's matrix core therefore always has a
+// wave with operands ready, and the LDS port is used by one group at a time.
+//
+// K is staged 64 bytes at a time through a ring of four LDS stages filled by direct
+// global -> LDS loads (buffer_load_dwordx4 ... lds: no registers, no LDS write instructions).
+// Loads run three stages ahead of the stage being multiplied.  A stage holds BM + BN rows of
+// 64 bytes as four 16-byte chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the
+// 16 lanes one LDS cycle serves (16 consecutive rows, one logical chunk) touch 16 distinct
+// 16-byte bank groups of the 256-byte bank row.
+//
+// v_mfma_i32_32x32x32_i8: lane l supplies 16 bytes of row l % 32 at K-group l / 32 of both
+// operands; the 64-byte stage is two such K-steps.  Integer accumulation is exact in any
+// order (|acc| <= K * 127^2 < 2^31), so staging and the chunk permutation never change a bit.
+#pragma once
+#include "mfma_tile.h"
+
+namespace lsk {
+
+typedef __attribute__((address_space(3))) void* lds_void_t;
+
+template <int BM, int BN, int WM, int WN, int RING = 4>
+struct PPCfg {
+  static_assert(WM * WN == 8, "eight waves");
+  static_assert(RING >= 2 && RING <= 5, "ring of 2..5 stages");
+  static constexpr int kThreads = 512;
+  static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN;
+  static constexpr int kBK = 64;          // bytes of K per stage
+  static constexpr int kRing = RING;      // LDS stages
+  static constexpr int kAhead = RING - 1; // stages loaded ahead of the one being multiplied
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int TM = WTM / 32, TN = WTN / 32;
+  static constexpr int kStageA = BM * kBK, kStageB = BN * kBK, kStage = kStageA + kStageB;  // bytes
+  static constexpr int kLA = kStageA / 16 / kThreads;  // 16-byte loads per thread per stage
+  static constexpr int kLB = kStageB / 16 / kThreads;
+  static constexpr int kMainBytes = kRing * kStage;
+  static constexpr int kLdc = WTN + 4;                 // int32 row stride of a staged 32-row strip
+  static constexpr int kStripBytes = 32 * kLdc * 4;
+  static constexpr int kEpiBytes = 8 * kStripBytes;
+  // epilogue operands of the tile: row operand [BM], ws / bias / column exponent [BN] each
+  static constexpr int kScaleOff = kMainBytes > kEpiBytes ? kMainBytes : kEpiBytes;
+  static constexpr int kSmemBytes = kScaleOff + (BM + 3 * BN) * 4;
+  static_assert(BM <= kThreads && BN <= kThreads, "one epilogue operand per thread");
+  static_assert(kStageA % (16 * kThreads) == 0 && kStageB % (16 * kThreads) == 0, "tile / threads");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");
+  typedef v16i Acc[TM][TN];
+  typedef uint32_t RowsA[kLA];  // byte offset of each load slot's row in its resource (kOob: zero row)
+  typedef uint32_t RowsB[kLB];
+};
+
+// Tile row loaded by thread `tid` in load slot j, and the byte offset within the 64-byte row
+// segment it fetches (the logical chunk that its LDS slot holds).
+template <int THREADS>
+LSK_DEV void pp_slot(int tid, int j, int& row, int& kbyte) {
+  const int p = j * THREADS + tid;  // 16-byte LDS slot index inside the operand's stage
+  row = p >> 2;
+  kbyte = 16 * ((p & 3) ^ ((row >> 2) & 3));
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+LSK_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+LSK_DEV void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0), vmcnt/expcnt max
+
+// s_barrier that the instruction scheduler may not move anything across (the phases of the
+// ping-pong are defined by where the MFMAs and LDS reads sit relative to the barriers).
+LSK_DEV void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BM, int BN, int WM, int WN, int RING>
+LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING>::Acc& acc, __amdgpu_buffer_rsrc_t ra,
+                         const typename PPCfg<BM, BN, WM, WN, RING>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
+                         const typename PPCfg<BM, BN, WM, WN, RING>::RowsB& pb, int K, char* smem) {
+  using C = PPCfg<BM, BN, WM, WN, RING>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int group = wave >> 2;
+  const int wm = wave / WN, wn = wave % WN;
+  const int nk = (K + C::kBK - 1) / C::kBK;
+
+  // per-slot chunk byte offsets (the LDS side of each load is fixed by the lane)
+  int ka[C::kLA], kb[C::kLB];
+#pragma unroll
+  for (int j = 0; j < C::kLA; ++j) {
+    int r;
+    pp_slot<C::kThreads>(tid, j, r, ka[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < C::kLB; ++j) {
+    int r;
+    pp_slot<C::kThreads>(tid, j, r, kb[j]);
+  }
+
+  // issue this thread's direct-to-LDS loads of stage s
+  auto issue = [&](int s) {
+    char* st = smem + (s % C::kRing) * C::kStage;
+    const int k0 = s * C::kBK;
+#pragma unroll
+    for (int j = 0; j < C::kLA; ++j) {
+      const int kk = k0 + ka[j];
+      const uint32_t off = kk < K ? pa[j] + (uint32_t)kk : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t)(st + (j * C::kThreads + wave * 64) * 16), 16, off, 0,
+                                               0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < C::kLB; ++j) {
+      const int kk = k0 + kb[j];
+      const uint32_t off = kk < K ? pb[j] + (uint32_t)kk : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, (lds_void_t)(st + C::kStageA + (j * C::kThreads + wave * 64) * 16), 16, off, 0, 0, 0);
+    }
+  };
+  constexpr int kPer = C::kLA + C::kLB;  // loads per thread per stage
+
+  // fragment addresses: row r = base + (lane & 31), logical chunk 2*ks + (lane >> 5)
+  const int lr = lane & 31, sw = (lr >> 2) & 3, kg = lane >> 5;
+  const int offA = (wm * C::WTM + lr) * C::kBK, offB = C::kStageA + (wn * C::WTN + lr) * C::kBK;
+  const int slot0 = 16 * ((0 + kg) ^ sw), slot1 = 16 * ((2 + kg) ^ sw);
+
+  // wait until at most n stages of this thread's loads are outstanding
+  auto wait_stages = [&](int n) {
+    if (n >= 3) wait_vm<3 * kPer>();
+    else if (n == 2) wait_vm<2 * kPer>();
+    else if (n == 1) wait_vm<kPer>();
+    else wait_vm<0>();
+  };
+  static_assert(C::kAhead - 1 <= 3, "wait_stages covers up to three younger stages");
+
+  // prologue: stages 0 .. kAhead-1 in flight, stage 0 complete everywhere
+#pragma unroll
+  for (int s = 0; s < C::kAhead; ++s)
+    if (s < nk) issue(s);
+  wait_stages((nk < C::kAhead ? nk : C::kAhead) - 1);
+  phase_barrier();
+  if (group == 1) phase_barrier();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    // ---- memory phase: next loads, fragments of stage kt, own part of stage kt+1 complete
+    if (kt + C::kAhead < nk) issue(kt + C::kAhead);
+    const char* st = smem + (kt % C::kRing) * C::kStage;
+    v4i fa[2][C::TM], fb[2][C::TN];
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      fa[0][i] = *(const v4i*)(st + offA + i * 32 * C::kBK + slot0);
+      fa[1][i] = *(const v4i*)(st + offA + i * 32 * C::kBK + slot1);
+    }
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      fb[0][j] = *(const v4i*)(st + offB + j * 32 * C::kBK + slot0);
+      fb[1][j] = *(const v4i*)(st + offB + j * 32 * C::kBK + slot1);
+    }
+    // loads issued after stage kt+1: stages kt+2 .. min(nk-1, kt+kAhead)
+    wait_stages((kt + C::kAhead < nk ? C::kAhead : nk - 1 - kt) - 1);
+    wait_lgkm0();
+    phase_barrier();
+    // ---- compute phase
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma_i8_32(fa[ks][i], fb[ks][j], acc[i][j]);
+    phase_barrier();
+  }
+  if (group == 0) phase_barrier();
+}
+
+// Stage 32-row strip i of the wave's accumulators (rows 32i .. 32i+31 of the wave tile) into
+// the wave's LDS region, row stride LDC int32.  MFMA layout: register r of lane l holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 of each 32 x 32 block.
+template <int TN, int LDC>
+LSK_DEV void pp_stage_strip(const v16i* strip, int32_t* region) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      region[row * LDC + j * 32 + (lane & 31)] = strip[j][r];
+    }
+}
+
+}  // namespace lsk
