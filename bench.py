@@ -100,11 +100,42 @@ def dense_section(torch, args):
     }
 
 
+def _graph_time(torch, calls, reps):
+    """Average milliseconds per call of the callables in `calls`, captured once into a HIP graph
+    (so host overhead between launches is not timed) and replayed `reps` times; HIP events on
+    the replay stream."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for fn in calls:          # first calls outside capture (one-time setup, allocator warm-up)
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in calls:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        g.replay()
+    e1.record(s)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / (reps * len(calls))
+
+
 def decode_section(torch, args):
-    """Batch-1/8/32 decode rows through w8a8_matmul; weights rotated over > 512 MB of copies so
-    the 256 MB Infinity Cache cannot serve them.  GB/s counts the algorithmic bytes
-    N*K + 4N + 4MK + 2MN of one call."""
+    """Batch-1/8/32 decode rows through w8a8_matmul (row quant + GEMV) and the GEMV alone on
+    pre-quantised rows.  Each is timed as HIP-graph replays of one call per weight copy, the
+    copies totalling > 768 MB so the 256 MB Infinity Cache cannot serve the weights.  GB/s counts
+    the algorithmic bytes N*K + 4N + 4MK + 2MN of one call (int8 weights, f32 scales and
+    activations, bf16 out)."""
+    from lockstep_amd import _lib as L
     from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import ops
     from lockstep_amd import workloads as WL
 
     dev = torch.device("cuda", 0)
@@ -118,19 +149,21 @@ def decode_section(torch, args):
         ws = torch.empty(N, device=dev).uniform_(1e-3, 1e-2, generator=g)
         for M in (1, 8, 32):
             x = torch.randn((M, K), generator=g, device=dev)
-            it = [0]
-
-            def fn():
-                FS.w8a8_matmul(x, Ws[it[0] % copies], ws, out_dtype=torch.bfloat16)
-                it[0] += 1
-            for _ in range(copies):
-                fn()
-            ms = _events_time(torch, fn, 6 * copies)
+            q, asc = ops.rowquant(x)
+            out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            full = [(lambda W=W: FS.w8a8_matmul(x, W, ws, out_dtype=torch.bfloat16)) for W in Ws]
+            gemv = [(lambda W=W: ops.gemm(q, W, L.EPI_V21, L.LSK_BF16, asc=asc, ws=ws, out=out)) for W in Ws]
+            ms = _graph_time(torch, full, 8)
+            ms_k = _graph_time(torch, gemv, 8)
             nbytes = N * K + 4 * N + 4 * M * K + 2 * M * N
-            gbs = nbytes / (ms * 1e-3) / 1e9
+            gbs, gbs_k = nbytes / (ms * 1e-3) / 1e9, nbytes / (ms_k * 1e-3) / 1e9
             res["%s_M%d" % (name, M)] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-                                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)}
+                                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                         "gemv_us": round(ms_k * 1e3, 2), "gemv_GB/s": round(gbs_k, 1),
+                                         "gemv_frac_hbm": round(gbs_k / PEAK_HBM_GBS, 4)}
         del Ws
+    res["note"] = ("us / GB/s: one w8a8_matmul call (row quant + GEMV kernels); gemv_*: the GEMV kernel alone on "
+                   "pre-quantised rows; both from HIP-graph replays over > 768 MB of weight copies")
     return res
 
 

@@ -97,11 +97,14 @@ int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
                     int order, void* out, int out_dtype, int64_t ldo,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Tuning control with no counterpart in the reference: force the dense prefill tile
- * (0: 256x256 tile, 4 waves of 128x128; 1: 256x128, 8 waves of 64x64; 2: 128x128, 4 waves
- * of 64x64; 3: 256x256, 8 waves of 64x128; 4: 128x256, 8 waves of 64x64; 5-8: tiles 2, 1, 3, 4
- * with global loads issued two K stages ahead) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
- * Process-wide, not thread-safe against concurrent launches. */
+/* Tuning control with no counterpart in the reference: force the dense kernel
+ * (0: 128x128 register-staged tile, 4 waves of 64x64; 1: ping-pong 256x256, 8 waves of 64x128;
+ * 2: ping-pong 256x256, 8 waves of 128x64; 3: ping-pong 256x128, 8 waves of 64x64;
+ * 4: ping-pong 128x256, 8 waves of 64x64; 5: the decode GEMV when M <= 32, else tile 0;
+ * 6, 7: for M <= 4 the 8-row register-buffered / LDS-ring GEMV instead of the whole-row GEMV;
+ * 8..11: the whole-row GEMV with 1 / 2 / 4 / 8 rows per wave) or -1 to choose by shape (the
+ * default).  Results are identical for every choice; only speed
+ * differs.  Process-wide, not thread-safe against concurrent launches. */
 int lsk_gemm_select(int tile_id);
 
 /* Power-of-two int8 quantisation of ref_block_v1 (reference/ref_block_v1.py:56-72,122-130).

@@ -20,7 +20,7 @@ using lsk::zero4;
 // Dense tile kernel: C[m, n] = sum_k A[m, k] * W[n, k] with the epilogue applied per element.
 // A and W are K-contiguous with 16-byte aligned rows and K % 16 == 0.  Logical tile ids walk
 // M-fastest inside groups of 16 M-tiles after the XCD remap.
-template <int BM, int BN, int WM, int WN, int PF>
+template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
     const int8_t* __restrict__ A, int lda, const int8_t* __restrict__ W, int ldw, int M, int N, int K,
     EpiParams ep, int vec_ok) {
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
   const int r = L - group * GM * ntiles;
   const int m0 = (first_m + r % gsize) * BM, n0 = (r / gsize) * BN;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / WN, wn = wave % WN;
   // resources start at the tile's first row: offsets stay below BM * lda
   const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(A + (int64_t)m0 * lda, (int64_t)(M - m0) * lda);
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_i8_mfma_kernel(
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  lsk::mfma_mainloop<BM, BN, WM, WN, PF>(acc, ra_res, pa, rb_res, pb, K, smem);
+  lsk::mfma_mainloop<BM, BN, WM, WN>(acc, ra_res, pa, rb_res, pb, K, smem);
 
   int32_t* region = (int32_t*)smem + wave * C::kStripInts;
   constexpr int kQuads = C::WTN / 4;
@@ -91,7 +91,7 @@ __device__ __forceinline__ void pp_strip_store(int i, const int32_t* region, con
   const int order = ORDER >= 0 ? ORDER : ep.order;
   const int odt = ODT >= 0 ? ODT : ep.out_dtype;
   const bool has_bias = ORDER >= 0 ? BIAS : ep.bias != nullptr;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / C::kWN, wn = wave % C::kWN;
   const float* sc_row = (const float*)(smem + C::kScaleOff);
   const float* sc_ws = sc_row + C::kBM;
@@ -128,7 +128,7 @@ template <class C, int ORDER, int ODT, bool BIAS, int I>
 __device__ __forceinline__ void pp_epilogue(const typename C::Acc& acc, const EpiParams& ep, int m0, int n0, int M,
                                             int N, int vec_ok, char* smem) {
   if constexpr (I < C::TM) {
-    int32_t* region = (int32_t*)(smem + (threadIdx.x >> 6) * C::kStripBytes);
+    int32_t* region = (int32_t*)(smem + wave_id() * C::kStripBytes);
     lsk::pp_stage_strip<C::TN, C::kLdc>(acc[I], region);
     pp_strip_store<C, ORDER, ODT, BIAS>(I, region, ep, m0, n0, M, N, vec_ok, smem);
     pp_epilogue<C, ORDER, ODT, BIAS, I + 1>(acc, ep, m0, n0, M, N, vec_ok, smem);
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(512) void gemm_i8_pp_kernel(const int8_t* __restric
   const int r = L - group * GM * ntiles;
   const int m0 = (first_m + r % gsize) * BM, n0 = (r / gsize) * BN;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / WN, wn = wave % WN;
 
   // epilogue operands: thread t holds row m0 + t and column n0 + t
@@ -227,55 +227,437 @@ __global__ __launch_bounds__(512) void gemm_i8_pp_kernel(const int8_t* __restric
   pp_epilogue<C, -1, -1, false, 0>(acc, ep, m0, n0, M, N, vec_ok, smem_pp);  // any other combination
 }
 
-// Decode GEMV: one block per 16 output columns; its 4 waves take interleaved 256-byte K slabs;
-// each lane streams 64 contiguous weight bytes per slab (4 MFMAs).  MT 16-row tiles cover M.
-template <int MT>
-__global__ __launch_bounds__(256) void gemv_i8_mfma_kernel(const int8_t* __restrict__ A, int64_t lda,
-                                                           const int8_t* __restrict__ W, int64_t ldw, int M,
-                                                           int N, int K, EpiParams ep) {
-  __shared__ v4i red[3][MT][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Decode GEMV (M <= 32), bandwidth-bound on the weight stream: one block per 16 output
+// columns, its KW waves splitting K into 64-byte-aligned slices.  Lane l streams 16 bytes of
+// weight row n0 + l % 16 at K-group l / 16 of each 64-byte step (one v_mfma_i32_16x16x64_i8
+// per step and 16-row tile of activations); batches of U steps are loaded one batch ahead of
+// their MFMAs.  The waves' partial sums are added exactly in LDS; wave 0 applies the
+// epilogue.  Edge rows, the K tail and slice ends load zeros through the buffer range.
+template <int MT, int U>
+__global__ __launch_bounds__(1024) void gemv_i8_stream_kernel(const int8_t* __restrict__ A, int lda,
+                                                              const int8_t* __restrict__ W, int ldw, int M, int N,
+                                                              int K, int kslice, EpiParams ep) {
+  extern __shared__ v4i red_gemv[];  // [(KW - 1) * MT][64]
+  const int lane = threadIdx.x & 63, wave = wave_id(), KW = blockDim.x >> 6;
   const int col = lane & 15, kg = lane >> 4;
   const int n0 = blockIdx.x * 16;
-  const int n = n0 + col;
-  const bool nvalid = n < N;
-  const int8_t* wrow = W + (int64_t)(nvalid ? n : 0) * ldw;
+  const int nrows = (N - n0) < 16 ? (N - n0) : 16;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)nrows * ldw);
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(A, (int64_t)M * lda);
+  const uint32_t wrow = (col < nrows) ? (uint32_t)(col * ldw) : lsk::kOob;
+  uint32_t arow[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) arow[t] = (t * 16 + col < M) ? (uint32_t)((t * 16 + col) * lda) : lsk::kOob;
+  const int kb = wave * kslice;
+  const int ke = (kb + kslice) < K ? (kb + kslice) : K;
 
+  // one batch = U 64-byte steps: weights (non-temporal) and activations, loaded one batch
+  // ahead of the MFMAs that consume them (register double buffer)
+  auto load_batch = [&](v4i* w, v4i (*a)[MT], int k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + u * 64 + kg * 16;
+      const bool in = kk < ke;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) a[u][t] = lsk::buf_load16(ra, in ? arow[t] + (uint32_t)kk : lsk::kOob);
+      w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, in ? wrow + (uint32_t)kk : lsk::kOob,
+                                                                           0, 2 /* non-temporal */));
+    }
+  };
   v4i acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = zero4();
-
-  for (int kb = wave * 256; kb < K; kb += 4 * 256) {
-    const int k = kb + kg * 64;
-    v4i w4[4];
+  auto mma_batch = [&](const v4i* w, const v4i (*a)[MT]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w4[j] = (nvalid && k + j * 16 < K) ? *(const v4i*)(wrow + k + j * 16) : zero4();
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int m = t * 16 + col;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v4i a = (m < M && k + j * 16 < K) ? *(const v4i*)(A + (int64_t)m * lda + k + j * 16) : zero4();
-        acc[t] = lsk::mfma_i8(a, w4[j], acc[t]);
-      }
-    }
+      for (int t = 0; t < MT; ++t) acc[t] = lsk::mfma_i8(a[u][t], w[u], acc[t]);
+  };
+  // two register sets in turn (no copies between them, so no wait on the newer loads)
+  v4i w0[U], a0[U][MT], w1[U], a1[U][MT];
+  load_batch(w0, a0, kb);
+  lsk::compiler_fence();
+  for (int k = kb; k < ke; k += 128 * U) {
+    load_batch(w1, a1, k + 64 * U);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_batch(w0, a0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + 64 * U >= ke) break;
+    load_batch(w0, a0, k + 128 * U);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_batch(w1, a1);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (wave > 0) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t) red[wave - 1][t][lane] = acc[t];
+    for (int t = 0; t < MT; ++t) red_gemv[((wave - 1) * MT + t) * 64 + lane] = acc[t];
   }
   __syncthreads();
   if (wave != 0) return;
+  for (int w2 = 1; w2 < KW; ++w2)
 #pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    v4i s = acc[t];
+    for (int t = 0; t < MT; ++t) acc[t] += red_gemv[((w2 - 1) * MT + t) * 64 + lane];
+  const int n = n0 + col;
 #pragma unroll
-    for (int w = 0; w < 3; ++w) s += red[w][t][lane];
+  for (int t = 0; t < MT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = t * 16 + (lane >> 4) * 4 + r;
-      if (m < M && nvalid) epilogue_store(ep, m, n, s[r]);
+      const int m = t * 16 + kg * 4 + r;
+      if (m < M && n < N) epilogue_store(ep, m, n, acc[t][r]);
     }
+}
+
+// Batch-few decode GEMV (M <= MR <= 8) on the VALU (v_dot4c_i32_i8), bandwidth-bound on the
+// weight stream.  A block is four waves; each wave owns 8 weight rows and one of WK K-slices
+// (WK = 1, 2 or 4 waves per row group).  Lane l reads 16 bytes of row l / 8 at chunk l % 8 of
+// every 128-byte step, so each load instruction covers 8 whole 128-byte row segments; U steps
+// of loads are in flight while the previous U are multiplied (register double buffer).  The
+// activation rows sit in LDS (zero-padded to 128 bytes).  Partial sums are exact int32 and
+// reduced across the 8 lanes of a row, then across the K-slices, in any order.
+template <int MR, int U>
+__global__ __launch_bounds__(256) void gemv_i8_dot_kernel(const int8_t* __restrict__ A, int lda,
+                                                          const int8_t* __restrict__ W, int ldw, int M, int N, int K,
+                                                          int wk, int kslice, EpiParams ep) {
+  extern __shared__ __attribute__((aligned(16))) char smem_dot[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int Kp = (K + 127) & ~127;
+  v4i* sa = (v4i*)smem_dot;                           // [MR][Kp / 16]
+  int* red = (int*)(smem_dot + MR * Kp);              // [4 waves][8 rows][MR]
+  const int rg = wave / wk, ks = wave % wk;
+  const int rows_blk = 8 * (4 / wk);
+  const int n0 = blockIdx.x * rows_blk;
+  const int rl = rg * 8 + (lane >> 3), c = lane & 7;
+  const int nrows = (N - n0) < rows_blk ? (N - n0) : rows_blk;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)nrows * ldw);
+  const uint32_t wrow = rl < nrows ? (uint32_t)(rl * ldw) : lsk::kOob;
+  const int kb = ks * kslice;
+  const int ke = (kb + kslice) < K ? (kb + kslice) : K;
+
+  // epilogue operands of the lanes that store (first K-slice, first lane of each row), loaded
+  // before the stream so the tail does not wait on them
+  const int n = n0 + rl;
+  EpiOps eo[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) eo[m] = EpiOps{0.0f, 0.0f, 0.0f, 0};
+  if (ks == 0 && c == 0 && n < N) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (m < M) eo[m] = epi_ops_load(ep, m, n);
+  }
+
+  // activation rows -> LDS by direct-to-LDS loads, issued before the weight stream (loads
+  // complete in order, so waiting for these never waits for the weights behind them)
+  const int kc16 = Kp / 16;
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(A, (int64_t)M * lda);
+  int na = 0;  // this thread's activation loads
+  for (int i0 = wave * 64; i0 < MR * kc16; i0 += 256, ++na) {
+    const int i = i0 + lane;
+    const int m = i / kc16, kc = i - m * kc16;
+    const uint32_t off = (m < M && kc * 16 < K) ? (uint32_t)(m * lda + kc * 16) : lsk::kOob;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(smem_dot + i0 * 16), 16, off, 0, 0, 0);
+  }
+  auto load_batch = [&](v4i* w, int s) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = s + u * 128 + c * 16;
+      w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rw, kk < ke ? wrow + (uint32_t)kk : lsk::kOob, 0, 2 /* non-temporal */));
+    }
+  };
+  int acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0;
+  auto dot_batch = [&](const v4i* w, int s) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = s + u * 128 + c * 16;
+      if (s + u * 128 < ke) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const v4i a = sa[m * kc16 + kk / 16];
+          acc[m] = __builtin_amdgcn_sdot4(a[0], w[u][0], acc[m], false);
+          acc[m] = __builtin_amdgcn_sdot4(a[1], w[u][1], acc[m], false);
+          acc[m] = __builtin_amdgcn_sdot4(a[2], w[u][2], acc[m], false);
+          acc[m] = __builtin_amdgcn_sdot4(a[3], w[u][3], acc[m], false);
+        }
+      }
+    }
+  };
+  // two register sets in turn (no copies between them, so no wait on the newer loads)
+  v4i w0[U], w1[U];
+  load_batch(w0, kb);
+  // The activation loads must have landed before the barrier.  The compiler may place the
+  // first weight batch on either side of this wait, so it cannot be counted on to be
+  // outstanding: wait for everything.
+  lsk::wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  for (int s = kb; s < ke; s += 256 * U) {
+    load_batch(w1, s + 128 * U);
+    __builtin_amdgcn_sched_barrier(0);
+    dot_batch(w0, s);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 128 * U >= ke) break;
+    load_batch(w0, s + 256 * U);
+    __builtin_amdgcn_sched_barrier(0);
+    dot_batch(w1, s + 128 * U);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the 8 lanes of a row, then the K-slices of the row group
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    acc[m] += __shfl_xor(acc[m], 1, 64);
+    acc[m] += __shfl_xor(acc[m], 2, 64);
+    acc[m] += __shfl_xor(acc[m], 4, 64);
+  }
+  if (c == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[(wave * 8 + (lane >> 3)) * MR + m] = acc[m];
+  }
+  __syncthreads();
+  if (ks != 0 || c != 0) return;
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    int sum = 0;
+    for (int k2 = 0; k2 < wk; ++k2) sum += red[((rg * wk + k2) * 8 + (lane >> 3)) * MR + m];
+    if (m < M && n < N) epilogue_store_ops(ep, m, n, sum, eo[m]);
+  }
+}
+
+// s_waitcnt vmcnt(n) for a run-time n in [0, 15] (larger n waits for 15).
+__device__ __forceinline__ void wait_vm_upto15(int n) {
+  switch (n < 0 ? 0 : (n > 15 ? 15 : n)) {
+    case 0: lsk::wait_vm<0>(); break;
+    case 1: lsk::wait_vm<1>(); break;
+    case 2: lsk::wait_vm<2>(); break;
+    case 3: lsk::wait_vm<3>(); break;
+    case 4: lsk::wait_vm<4>(); break;
+    case 5: lsk::wait_vm<5>(); break;
+    case 6: lsk::wait_vm<6>(); break;
+    case 7: lsk::wait_vm<7>(); break;
+    case 8: lsk::wait_vm<8>(); break;
+    case 9: lsk::wait_vm<9>(); break;
+    case 10: lsk::wait_vm<10>(); break;
+    case 11: lsk::wait_vm<11>(); break;
+    case 12: lsk::wait_vm<12>(); break;
+    case 13: lsk::wait_vm<13>(); break;
+    case 14: lsk::wait_vm<14>(); break;
+    default: lsk::wait_vm<15>(); break;
+  }
+}
+
+// Batch-few decode GEMV (M <= MR <= 4), weights streamed through per-wave LDS rings.  A block
+// is four waves; each wave owns 8 weight rows and one of WK K-slices.  A step is 128 bytes of
+// K of the wave's 8 rows: one direct-to-LDS load (lane l: row l / 8, 16-byte chunk l % 8), so
+// every load instruction covers 8 whole 128-byte row segments.  Steps travel in batches of U;
+// the wave keeps R batches in flight in its private ring (R * U slots of 1 KB) and waits on its
+// own loads only (exact counts: no other vector-memory load is issued in the loop), so the
+// stream needs no barrier and no registers.  The activation rows (zero-padded to 128 bytes)
+// are staged once per block.  Each lane multiplies its 16-byte chunks on the VALU
+// (v_dot4c_i32_i8); the exact int32 sums are reduced across the 8 lanes of a row, then across
+// the K-slices, in any order.
+template <int MR, int U, int R>
+__global__ __launch_bounds__(256) void gemv_i8_ring_kernel(const int8_t* __restrict__ A, int lda,
+                                                           const int8_t* __restrict__ W, int ldw, int M, int N, int K,
+                                                           int wk, int kslice, EpiParams ep) {
+  extern __shared__ __attribute__((aligned(16))) char smem_ring[];
+  constexpr int kSlots = U * R;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int Kp = (K + 127) & ~127;
+  const int kc16 = Kp / 16;
+  char* sa = smem_ring;                                         // [MR][Kp] activations
+  char* ring = smem_ring + MR * Kp + wave * kSlots * 1024;      // this wave's slots
+  int* red = (int*)(smem_ring + MR * Kp + 4 * kSlots * 1024);   // [4 waves][8 rows][MR]
+  const int rg = wave / wk, ks = wave % wk;
+  const int rows_blk = 8 * (4 / wk);
+  const int n0 = blockIdx.x * rows_blk;
+  const int rl = rg * 8 + (lane >> 3), c = lane & 7;
+  const int nrows = (N - n0) < rows_blk ? (N - n0) : rows_blk;
+  const int n = n0 + rl;
+  const int kb = ks * kslice;
+  const int ke = (kb + kslice) < K ? (kb + kslice) : K;
+  const int nbatch = ke > kb ? (ke - kb + 128 * U - 1) / (128 * U) : 0;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)nrows * ldw);
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(A, (int64_t)M * lda);
+  const uint32_t wrow = rl < nrows ? (uint32_t)(rl * ldw) : lsk::kOob;
+
+  // activations -> LDS (every wave a share), then the first R weight batches of this wave
+  for (int i0 = wave * 64; i0 < MR * kc16; i0 += 256) {
+    const int i = i0 + lane;
+    const int m = i / kc16, kc = i - m * kc16;
+    const uint32_t off = (m < M && kc * 16 < K) ? (uint32_t)(m * lda + kc * 16) : lsk::kOob;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(sa + i0 * 16), 16, off, 0, 0, 0);
+  }
+  auto issue = [&](int bt) {
+    char* slot = ring + (bt % R) * U * 1024;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = kb + (bt * U + u) * 128 + c * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lsk::lds_void_t)(slot + u * 1024), 16,
+                                               kk < ke ? wrow + (uint32_t)kk : lsk::kOob, 0, 0, 2 /* non-temporal */);
+    }
+  };
+#pragma unroll
+  for (int bt = 0; bt < R; ++bt)
+    if (bt < nbatch) issue(bt);
+  // everything issued so far has landed (one latency for all of it); the activations are
+  // visible to the block after the barrier
+  lsk::wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+
+  int acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0;
+  for (int bt = 0; bt < nbatch; ++bt) {
+    // batches issued after batch bt: min(nbatch, bt + R) - bt - 1 (those before R landed already)
+    if (bt >= R) {
+      if (nbatch - bt - 1 >= R - 1) lsk::wait_vm<U * (R - 1)>();
+      else wait_vm_upto15(U * (nbatch - bt - 1));
+    }
+    const char* slot = ring + (bt % R) * U * 1024;
+    v4i w[U], a[U][MR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      w[u] = *(const v4i*)(slot + u * 1024 + lane * 16);
+      const int kl = (kb + (bt * U + u) * 128) / 16 + c;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) a[u][m] = *(const v4i*)(sa + m * Kp + (kl < kc16 ? kl : 0) * 16);
+    }
+    lsk::wait_lgkm0();  // the batch is in registers: its slots can be refilled
+    if (bt + R < nbatch) issue(bt + R);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        acc[m] = __builtin_amdgcn_sdot4(a[u][m][0], w[u][0], acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(a[u][m][1], w[u][1], acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(a[u][m][2], w[u][2], acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(a[u][m][3], w[u][3], acc[m], false);
+      }
+  }
+  EpiOps eo[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) eo[m] = EpiOps{0.0f, 0.0f, 0.0f, 0};
+  if (ks == 0 && c == 0 && n < N) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (m < M) eo[m] = epi_ops_load(ep, m, n);
+  }
+  // the 8 lanes of a row, then the K-slices of the row group
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    acc[m] += __shfl_xor(acc[m], 1, 64);
+    acc[m] += __shfl_xor(acc[m], 2, 64);
+    acc[m] += __shfl_xor(acc[m], 4, 64);
+  }
+  if (c == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[(wave * 8 + (lane >> 3)) * MR + m] = acc[m];
+  }
+  __syncthreads();
+  if (ks != 0 || c != 0) return;
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    int sum = 0;
+    for (int k2 = 0; k2 < wk; ++k2) sum += red[((rg * wk + k2) * 8 + (lane >> 3)) * MR + m];
+    if (m < M && n < N) epilogue_store_ops(ep, m, n, sum, eo[m]);
+  }
+}
+
+// Batch-few decode GEMV (M <= MR <= 4) streaming whole weight rows.  Each load instruction of
+// a wave reads 1 KB of one row (lane l: bytes 16 l .. 16 l + 15 of a 1 KB chunk): contiguous
+// streams reach a higher HBM rate than several rows per instruction.  A wave owns RPW rows
+// and one of WK K-slices of NC chunks; the activations of its K-slice sit in registers
+// (loaded once), the next row is loaded while the current one is multiplied on the VALU
+// (v_dot4c_i32_i8), and each row's exact int32 sum is reduced across the wave; the K-slices
+// of a row are added in LDS.  Everything outside [0, K) and past the last row loads zero
+// through the buffer range.
+template <int MR, int NC>
+__global__ __launch_bounds__(256) void gemv_i8_row_kernel(const int8_t* __restrict__ A, int lda,
+                                                          const int8_t* __restrict__ W, int ldw, int M, int N, int K,
+                                                          int wk, int rpw, EpiParams ep) {
+  __shared__ int red[4][16][MR];  // [wave][row of the wave][m], rpw <= 16
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int rg = wave / wk, ks = wave % wk;
+  const int rows_blk = rpw * (4 / wk);
+  const int n0 = blockIdx.x * rows_blk;
+  const int nrows = (N - n0) < rows_blk ? (N - n0) : rows_blk;
+  const int kb = ks * NC * 1024;
+  const int ke = (kb + NC * 1024) < K ? (kb + NC * 1024) : K;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)nrows * ldw);
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(A, (int64_t)M * lda);
+
+  // this lane's byte offsets within the K-slice (kOob past its end)
+  uint32_t koff[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int kk = kb + j * 1024 + lane * 16;
+    koff[j] = kk < ke ? (uint32_t)kk : lsk::kOob;
+  }
+  v4i a[MR][NC];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+      a[m][j] = lsk::buf_load16(ra, (m < M && koff[j] != lsk::kOob) ? (uint32_t)(m * lda) + koff[j] : lsk::kOob);
+
+  const int r0 = rg * rpw;  // first row of this wave within the block
+  auto load_row = [&](v4i* w, int i) {
+    const int rl = r0 + i;
+    const uint32_t rowoff = rl < nrows ? (uint32_t)(rl * ldw) : lsk::kOob;
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+      w[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rw, (rowoff == lsk::kOob || koff[j] == lsk::kOob) ? lsk::kOob : rowoff + koff[j],
+                                         0, 2 /* non-temporal */));
+  };
+  auto row_sum = [&](const v4i* w, int i) {
+    int acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      acc[m] = 0;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        acc[m] = __builtin_amdgcn_sdot4(a[m][j][0], w[j][0], acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(a[m][j][1], w[j][1], acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(a[m][j][2], w[j][2], acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(a[m][j][3], w[j][3], acc[m], false);
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MR; ++m) red[wave][i][m] = acc[m];
+    }
+  };
+  // two register sets in turn (no copies between them, so no wait on the newer loads)
+  v4i w0[NC], w1[NC];
+  load_row(w0, 0);
+  for (int i = 0; i < rpw; i += 2) {
+    if (i + 1 < rpw) load_row(w1, i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    row_sum(w0, i);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 1 >= rpw) break;
+    if (i + 2 < rpw) load_row(w0, i + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    row_sum(w1, i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();
+  // the K-slices of each row: one lane per (row of the row group)
+  if (ks != 0 || lane >= rpw) return;
+  const int rl = r0 + lane;
+  const int n = n0 + rl;
+  if (rl >= nrows) return;
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m >= M) break;
+    int sum = 0;
+    for (int k2 = 0; k2 < wk; ++k2) sum += red[rg * wk + k2][lane][m];
+    epilogue_store(ep, m, n, sum);
   }
 }
 
@@ -327,13 +709,15 @@ int validate_epilogue(int order, int out_dtype, const float* asc, const float* w
 
 // Tile configurations of the dense kernel; id -1 lets the shape decide.
 static int g_force_tile = -1;
+static int g_row_rpw = 0;       // rows per wave of the whole-row GEMV (0: by shape)
+static int g_gemv_variant = 0;  // M <= 4: 0 whole-row GEMV, 1 register double-buffered 8-row GEMV, 2 LDS-ring 8-row GEMV
 
-template <int BM, int BN, int WM, int WN, int PF = 1>
+template <int BM, int BN, int WM, int WN>
 static int launch_tile(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K,
                        const EpiParams& ep, int vec_ok, hipStream_t s, const char* name) {
   using C = TileCfg<BM, BN, WM, WN>;
   static bool attr_set = false;
-  auto kern = gemm_i8_mfma_kernel<BM, BN, WM, WN, PF>;
+  auto kern = gemm_i8_mfma_kernel<BM, BN, WM, WN>;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmemBytes) !=
         hipSuccess) {
@@ -372,13 +756,106 @@ static int launch_pp(const int8_t* a, int lda, const int8_t* w, int ldw, int M, 
 
 static int pick_tile(int64_t M, int64_t N) {
   if (g_force_tile >= 0) return g_force_tile;
-  if (M <= 128) return 2;  // few rows: the 128x128 register-staged tile wastes least
+  if (g_force_tile == 5) return 0;  // the GEMV takes M <= 32 only
+  if (M <= 128) return 0;  // few rows: the 128x128 register-staged tile wastes least
   // Ping-pong tiles: whole rounds of 256 blocks (one per CU) are what a launch costs.  A
   // 256x128 tile takes 0.68 of a 256x256 tile's time (measured on MI355X at the Llama-3.1-8B /
   // Qwen2.5-7B prefill shapes), so pick the shape with the smaller rounds x tile cost.
   const int64_t r256 = ((M + 255) / 256 * ((N + 255) / 256) + 255) / 256;
   const int64_t r128 = ((M + 255) / 256 * ((N + 127) / 128) + 255) / 256;
-  return (double)r128 * 0.68 < (double)r256 ? 11 : 10;
+  return (double)r128 * 0.68 < (double)r256 ? 3 : 1;
+}
+
+// Waves per block of the decode GEMV: enough blocks x waves (about 8192) to keep every CU's
+// memory pipeline full, K split into 64-byte-aligned slices.
+static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K, const EpiParams& ep,
+                       hipStream_t s) {
+  const int64_t Kp = (K + 127) / 128 * 128;
+  if (M <= 4 && g_gemv_variant == 0 && K <= 4 * 8 * 1024) {
+    // whole-row streaming: K-slices of NC <= 8 chunks (WK <= 4 waves per row)
+    const int nch = (K + 1023) / 1024;
+    int wk = 1;
+    while (wk < 4 && (nch + wk - 1) / wk > 4) wk *= 2;
+    const int nc = (nch + wk - 1) / wk;
+    // rows per wave (measured on MI355X, Llama-3.1-8B decode shapes): one row per wave streams
+    // best for a single activation row; more activation rows amortise their registers over
+    // more weight rows.  Fewer when N leaves under about 2048 waves.
+    const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    int rpw = mr == 1 ? (wk == 1 ? 1 : 2) : (mr == 2 ? 4 : 8);
+    while (rpw > 1 && (int64_t)((N + rpw * (4 / wk) - 1) / (rpw * (4 / wk))) * 4 < 2048) rpw /= 2;
+    if (g_row_rpw > 0) rpw = g_row_rpw;
+    const int rows_blk = rpw * (4 / wk);
+    const int rblocks = (N + rows_blk - 1) / rows_blk;
+#define LSK_ROW(MRV, NCV)                                                                                  \
+  {                                                                                                        \
+    hipLaunchKernelGGL((gemv_i8_row_kernel<MRV, NCV>), dim3((unsigned)rblocks), dim3(256), 0, s, a, lda, w, ldw, M, N, \
+                       K, wk, rpw, ep);                                                                    \
+    return check_launch("gemv_i8_row_kernel");                                                             \
+  }
+#define LSK_ROW_NC(MRV) \
+  if (nc <= 1) LSK_ROW(MRV, 1) else if (nc <= 2) LSK_ROW(MRV, 2) else if (nc <= 4) LSK_ROW(MRV, 4) else LSK_ROW(MRV, 8)
+    if (mr == 1) LSK_ROW_NC(1) else if (mr == 2) LSK_ROW_NC(2) else LSK_ROW_NC(4)
+#undef LSK_ROW_NC
+#undef LSK_ROW
+  }
+  if (M <= 4 && 4 * Kp <= 65536) {
+    // WK waves per 8-row group so that about 2048 waves stream the weights
+    int wk = 1;
+    while (wk < 4 && (int64_t)((N + 8 * (4 / wk) - 1) / (8 * (4 / wk))) * 4 < 2048) wk *= 2;
+    const int rows_blk = 8 * (4 / wk);
+    const int dblocks = (N + rows_blk - 1) / rows_blk;
+    const int kslice = (int)(((K + wk - 1) / wk + 127) / 128 * 128);
+    const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    if (g_gemv_variant == 1) {
+      const size_t smem = (size_t)mr * Kp + 4 * 8 * mr * sizeof(int);
+      if (mr == 1)
+        hipLaunchKernelGGL((gemv_i8_dot_kernel<1, 8>), dim3((unsigned)dblocks), dim3(256), smem, s, a, lda, w, ldw, M,
+                           N, K, wk, kslice, ep);
+      else if (mr == 2)
+        hipLaunchKernelGGL((gemv_i8_dot_kernel<2, 8>), dim3((unsigned)dblocks), dim3(256), smem, s, a, lda, w, ldw, M,
+                           N, K, wk, kslice, ep);
+      else
+        hipLaunchKernelGGL((gemv_i8_dot_kernel<4, 8>), dim3((unsigned)dblocks), dim3(256), smem, s, a, lda, w, ldw, M,
+                           N, K, wk, kslice, ep);
+      return check_launch("gemv_i8_dot_kernel");
+    }
+    // ring: batches of 4 steps, 3 or 2 batches deep as the LDS share of the blocks one CU
+    // must hold allows
+    const int64_t per_cu = (dblocks + 255) / 256;
+    const int64_t budget = (160 * 1024) / (per_cu < 1 ? 1 : per_cu) - mr * Kp - 4 * 8 * mr * 4;
+    const int R = budget >= 4 * 12 * 1024 ? 3 : 2;
+    const size_t smem = (size_t)mr * Kp + (size_t)4 * 4 * R * 1024 + 4 * 8 * mr * sizeof(int);
+    if (smem > 160 * 1024) return set_error("gemv: %zu bytes of LDS exceed the 160 KB limit", smem), LSK_ERR_ARG;
+#define LSK_RING(MRV, RV)                                                                                         \
+  {                                                                                                               \
+    auto kern = gemv_i8_ring_kernel<MRV, 4, RV>;                                                                  \
+    if (smem > 65536 &&                                                                                           \
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) \
+      return set_error("gemv: cannot reserve LDS"), LSK_ERR_HIP;                                                  \
+    hipLaunchKernelGGL(kern, dim3((unsigned)dblocks), dim3(256), smem, s, a, lda, w, ldw, M, N, K, wk, kslice, ep); \
+    return check_launch("gemv_i8_ring_kernel");                                                                   \
+  }
+    if (mr == 1) {
+      if (R == 3) LSK_RING(1, 3) else LSK_RING(1, 2)
+    } else if (mr == 2) {
+      if (R == 3) LSK_RING(2, 3) else LSK_RING(2, 2)
+    } else {
+      if (R == 3) LSK_RING(4, 3) else LSK_RING(4, 2)
+    }
+#undef LSK_RING
+  }
+  const int blocks = (N + 15) / 16;
+  int kw = 1;
+  while (kw < 16 && (int64_t)blocks * kw < 2048 && (int64_t)(kw * 2) * 64 * 4 * 2 <= K) kw *= 2;
+  const int kslice = ((K + kw * 64 - 1) / (kw * 64)) * 64;
+  const size_t smem = (size_t)(kw - 1) * (M <= 16 ? 1 : 2) * 64 * sizeof(v4i);
+  if (M <= 16)
+    hipLaunchKernelGGL((gemv_i8_stream_kernel<1, 4>), dim3((unsigned)blocks), dim3(64 * kw), smem, s, a, lda, w, ldw, M,
+                       N, K, kslice, ep);
+  else
+    hipLaunchKernelGGL((gemv_i8_stream_kernel<2, 4>), dim3((unsigned)blocks), dim3(64 * kw), smem, s, a, lda, w, ldw, M,
+                       N, K, kslice, ep);
+  return check_launch("gemv_i8_stream_kernel");
 }
 
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
@@ -395,31 +872,14 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     return check_launch("gemm_i8_generic_kernel");
   }
   const int iM = (int)M, iN = (int)N, iK = (int)K;
-  if (M <= 16) {
-    hipLaunchKernelGGL(gemv_i8_mfma_kernel<1>, dim3((unsigned)((N + 15) / 16)), dim3(256), 0, s, a, lda, w, ldw, iM,
-                       iN, iK, ep);
-    return check_launch("gemv_i8_mfma_kernel<1>");
-  }
-  if (M <= 32) {
-    hipLaunchKernelGGL(gemv_i8_mfma_kernel<2>, dim3((unsigned)((N + 15) / 16)), dim3(256), 0, s, a, lda, w, ldw, iM,
-                       iN, iK, ep);
-    return check_launch("gemv_i8_mfma_kernel<2>");
-  }
+  if (M <= 32 && (g_force_tile < 0 || g_force_tile == 5)) return launch_gemv(a, (int)lda, w, (int)ldw, iM, iN, iK, ep, s);
   const int vec_ok = out_vec_ok(ep.out, ep.out_dtype, ep.ldo) ? 1 : 0;
   const int ilda = (int)lda, ildw = (int)ldw;
   switch (pick_tile(M, N)) {
-    case 0: return launch_tile<256, 256, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,2x2>");
-    case 1: return launch_tile<256, 128, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x128,4x2>");
-    case 3: return launch_tile<256, 256, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,4x2>");
-    case 4: return launch_tile<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x256,2x4>");
-    case 5: return launch_tile<128, 128, 2, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2,pf2>");
-    case 6: return launch_tile<256, 128, 4, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x128,4x2,pf2>");
-    case 7: return launch_tile<256, 256, 4, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<256x256,4x2,pf2>");
-    case 8: return launch_tile<128, 256, 2, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x256,2x4,pf2>");
-    case 9: return launch_pp<256, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,2x4>");
-    case 10: return launch_pp<256, 256, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,4x2>");
-    case 11: return launch_pp<256, 128, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x128,4x2>");
-    case 12: return launch_pp<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4>");
+    case 1: return launch_pp<256, 256, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,4x2>");
+    case 2: return launch_pp<256, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,2x4>");
+    case 3: return launch_pp<256, 128, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x128,4x2>");
+    case 4: return launch_pp<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4>");
     default: return launch_tile<128, 128, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2>");
   }
 }
@@ -488,7 +948,9 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 12, "lsk_gemm_select: tile id %d not in [-1, 12]", tile_id);
-  lsk::g_force_tile = tile_id;
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 11, "lsk_gemm_select: tile id %d not in [-1, 11]", tile_id);
+  lsk::g_force_tile = tile_id >= 6 ? 5 : tile_id;
+  lsk::g_gemv_variant = (tile_id == 6 || tile_id == 7) ? tile_id - 5 : 0;
+  lsk::g_row_rpw = tile_id >= 8 ? (1 << (tile_id - 8)) : 0;
   return LSK_OK;
 }

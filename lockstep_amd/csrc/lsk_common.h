@@ -18,6 +18,10 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
+// Index of the calling wave in its block, as a wave-uniform (scalar) value: the compiler cannot
+// prove threadIdx.x / 64 uniform by itself, and treats code that depends on it as divergent.
+LSK_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // binary32 -> bf16, round to nearest even; every NaN becomes 0x7FC0 (the conversion torch's
 // c10::BFloat16 performs, which is what the reference's `.to(torch.bfloat16)` runs).
 LSK_DEV uint16_t f32_to_bf16(float f) {
@@ -168,6 +172,36 @@ LSK_DEV float epi_value_pre(int order, int out_dtype, bool has_bias, int32_t acc
   }
   float sc = (pshift > 149) ? 0.0f : (pshift < -127 ? __uint_as_float(0x7f800000u) : pow2f(-pshift));
   return f32_mul(v, sc);
+}
+
+// The per-element epilogue operands of output (m, n), loaded ahead of the accumulator so a
+// kernel's tail does not wait on them: the row operand (asc[m]), ws[n], bias[n] (0 if none),
+// and for POW2 the total exponent shift + erow[m] + ecol[n].
+struct EpiOps {
+  float row, ws, b;
+  int sh;
+};
+
+LSK_DEV EpiOps epi_ops_load(const EpiParams& p, int64_t m, int64_t n) {
+  EpiOps o{0.0f, 0.0f, 0.0f, 0};
+  if (p.order == LSK_EPI_V21 || p.order == LSK_EPI_V2) {
+    o.row = p.asc[m];
+    o.ws = p.ws[n];
+    if (p.bias) o.b = p.bias[n];
+  } else if (p.order == LSK_EPI_POW2) {
+    o.sh = p.shift + (p.erow ? p.erow[m] : 0) + (p.ecol ? p.ecol[n] : 0);
+  }
+  return o;
+}
+
+// epilogue_store with the operands from epi_ops_load.
+LSK_DEV void epilogue_store_ops(const EpiParams& p, int64_t m, int64_t n, int32_t acc, const EpiOps& o) {
+  const int64_t off = m * p.ldo + n;
+  if (p.order == LSK_EPI_RAW) {
+    ((int32_t*)p.out)[off] = acc;
+    return;
+  }
+  store_out(p.out, p.out_dtype, off, epi_value_pre(p.order, p.out_dtype, p.bias != nullptr, acc, o.row, o.ws, o.b, o.sh));
 }
 
 // Round four epilogue values to the output type and store them at element offset o with one

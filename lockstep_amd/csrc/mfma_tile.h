@@ -8,8 +8,8 @@
 // rows reading one logical chunk hit 16 distinct 16-byte bank groups (two 128-byte rows span
 // the 64 four-byte banks).
 //
-// v_mfma_i32_32x32x32_i8 (measured at 97% of the 5.0 POPS int8 peak in a register-only loop;
-// the 16x16x64 form stalls near 55-70%): lane l supplies 16 bytes of row (l % 32) at K-group
+// v_mfma_i32_32x32x32_i8 (measured at 97% of the 5.0 POPS int8 peak in a register-only loop
+// with constant operands; the 16x16x64 form stalls near 55-70%): lane l supplies 16 bytes of row (l % 32) at K-group
 // (l / 32) of the A operand and of the W operand alike; D[i][j] lands in lane j + 32 * ((i / 4) % 2),
 // register 4 * (i / 8) + i % 4.  Integer accumulation is exact in any order (|acc| <= K * 127^2
 // < 2^31), so the K blocking never changes a result.
@@ -77,49 +77,45 @@ LSK_DEV void chunk_of(int tid, int j, int& row, int& c) {
 // acc[TM][TN] += A_tile * W_tile^T over K (K % 16 == 0; rows 16-byte aligned).
 // ra_res / rb_res: buffer resources over the operands; pa / pb: the byte offsets of this thread's
 // load-slot rows in them (kOob = zero row).
-// PF: global prefetch depth in K stages (1: the next stage's loads are issued while the current
-// one is computed; 2: two stages ahead, through two register sets), to cover HBM latency when
-// one block per CU leaves no other block to overlap with.
-template <int BM, int BN, int WM, int WN, int PF = 1>
+template <int BM, int BN, int WM, int WN>
 LSK_DEV void mfma_mainloop(typename TileCfg<BM, BN, WM, WN>::Acc& acc, __amdgpu_buffer_rsrc_t ra_res,
                            const typename TileCfg<BM, BN, WM, WN>::RowsA& pa, __amdgpu_buffer_rsrc_t rb_res,
                            const typename TileCfg<BM, BN, WM, WN>::RowsB& pb, int K, v4i* smem) {
   using C = TileCfg<BM, BN, WM, WN>;
-  static_assert(PF == 1 || PF == 2, "prefetch depth 1 or 2");
   v4i* sA = smem;
   v4i* sB = smem + 2 * C::kSmemA;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / WN, wn = wave % WN;
 
-  v4i ra[PF][C::kAPer], rb[PF][C::kBPer];
-  auto gload = [&](int set, int k0) {
+  v4i ra[C::kAPer], rb[C::kBPer];
+  auto gload = [&](int k0) {
 #pragma unroll
     for (int j = 0; j < C::kAPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
       const int gk = k0 + c * 16;
-      ra[set][j] = buf_load16(ra_res, gk < K ? pa[j] + (uint32_t)gk : kOob);
+      ra[j] = buf_load16(ra_res, gk < K ? pa[j] + (uint32_t)gk : kOob);
     }
 #pragma unroll
     for (int j = 0; j < C::kBPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
       const int gk = k0 + c * 16;
-      rb[set][j] = buf_load16(rb_res, gk < K ? pb[j] + (uint32_t)gk : kOob);
+      rb[j] = buf_load16(rb_res, gk < K ? pb[j] + (uint32_t)gk : kOob);
     }
   };
-  auto sstore = [&](int set, int buf) {
+  auto sstore = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < C::kAPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
-      sA[buf * C::kSmemA + swz8(row, c)] = ra[set][j];
+      sA[buf * C::kSmemA + swz8(row, c)] = ra[j];
     }
 #pragma unroll
     for (int j = 0; j < C::kBPer; ++j) {
       int row, c;
       chunk_of<C::kThreads>(tid, j, row, c);
-      sB[buf * C::kSmemB + swz8(row, c)] = rb[set][j];
+      sB[buf * C::kSmemB + swz8(row, c)] = rb[j];
     }
   };
   auto compute = [&](int buf) {
@@ -141,35 +137,15 @@ LSK_DEV void mfma_mainloop(typename TileCfg<BM, BN, WM, WN>::Acc& acc, __amdgpu_
   };
 
   const int nk = (K + kBK - 1) / kBK;
-  if (PF == 1) {
-    gload(0, 0);
-    sstore(0, 0);
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * kBK);
+    compute(buf);
+    if (kt + 1 < nk) sstore(buf ^ 1);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int buf = kt & 1;
-      if (kt + 1 < nk) gload(0, (kt + 1) * kBK);
-      compute(buf);
-      if (kt + 1 < nk) sstore(0, buf ^ 1);
-      __syncthreads();
-    }
-  } else {
-    // stage s is loaded into register set s & 1, two iterations before it is computed
-    gload(0, 0);
-    if (nk > 1) gload(1, kBK);
-    sstore(0, 0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
-      // even stage kt in LDS buffer 0, registers of set 1 hold stage kt + 1
-      if (kt + 2 < nk) gload(0, (kt + 2) * kBK);
-      compute(0);
-      if (kt + 1 < nk) sstore(1, 1);
-      __syncthreads();
-      if (kt + 1 >= nk) break;
-      if (kt + 3 < nk) gload(1, (kt + 3) * kBK);
-      compute(1);
-      if (kt + 2 < nk) sstore(0, 0);
-      __syncthreads();
-    }
   }
 }
 

@@ -206,7 +206,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
   const float* ws = (const float*)a.ws_ptrs[e];
   const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / 2, wn = wave % 2;
   // one resource over the whole activation matrix (gathered rows) and one over this expert's
   // weight; the host guarantees both spans fit 31-bit offsets

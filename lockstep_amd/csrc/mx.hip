@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(const int8_t* __restrict__
   const int ntiles = (N + 127) / 128;
   const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
   const int m0 = (L / ntiles) * 128, n0 = (L % ntiles) * 128;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / 2, wn = wave % 2;
   typename Cfg::Acc acc;
 #pragma unroll
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
   const uint8_t* sb = (const uint8_t*)a.ws_ptrs[e];
   const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
   const uint16_t* A = (const uint16_t*)a.A;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / 2, wn = wave % 2;
 
   auto wrow = [&](int r) -> int {  // weight row of tile row r, or -1

@@ -108,7 +108,7 @@ LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, 
   constexpr int kAChunksPerRow = A_I8 ? RC / 2 : RC;
   constexpr int kBChunksPerRow = B_FP4 ? RC / 4 : RC / 2;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / WN, wn = wave % WN;
 
   constexpr int kSPer = (BN * NB + T - 1) / T;  // scale bytes per thread per stage

@@ -69,6 +69,11 @@ LSK_DEV void wait_vm() {
 }
 LSK_DEV void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0), vmcnt/expcnt max
 
+// Keeps the compiler from moving memory operations across this point (a plain load is
+// otherwise free to sink to its first use, past a barrier or a counted wait that assumes it
+// was issued).
+LSK_DEV void compiler_fence() { asm volatile("" ::: "memory"); }
+
 // s_barrier that the instruction scheduler may not move anything across (the phases of the
 // ping-pong are defined by where the MFMAs and LDS reads sit relative to the barriers).
 LSK_DEV void phase_barrier() {
@@ -82,7 +87,7 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING>::Acc& acc, __amdgp
                          const typename PPCfg<BM, BN, WM, WN, RING>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
                          const typename PPCfg<BM, BN, WM, WN, RING>::RowsB& pb, int K, char* smem) {
   using C = PPCfg<BM, BN, WM, WN, RING>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int group = wave >> 2;
   const int wm = wave / WN, wn = wave % WN;
   const int nk = (K + C::kBK - 1) / C::kBK;
@@ -135,11 +140,14 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING>::Acc& acc, __amdgp
   };
   static_assert(C::kAhead - 1 <= 3, "wait_stages covers up to three younger stages");
 
-  // prologue: stages 0 .. kAhead-1 in flight, stage 0 complete everywhere
+  // prologue: stages 0 .. kAhead-1 issued together and all waited for (about one latency,
+  // like waiting for stage 0 alone).  A counted wait here could also count a caller's plain
+  // loads that the compiler placed among these; inside the loop only ring loads are issued,
+  // so the counted waits there are exact.
 #pragma unroll
   for (int s = 0; s < C::kAhead; ++s)
     if (s < nk) issue(s);
-  wait_stages((nk < C::kAhead ? nk : C::kAhead) - 1);
+  wait_vm<0>();
   phase_barrier();
   if (group == 1) phase_barrier();
 

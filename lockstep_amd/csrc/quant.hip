@@ -105,6 +105,87 @@ __global__ __launch_bounds__(THREADS) void rowquant_kernel(const void* __restric
   }
 }
 
+// Load 8 consecutive elements of dtype DT (16-byte aligned) as binary32.
+template <int DT>
+LSK_DEV void load8(const void* x, int64_t i8, float* v) {
+  if (DT == LSK_F32) {
+    const float4* p = (const float4*)x + 2 * i8;
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 u = ((const uint4*)x)[i8];
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (DT == LSK_BF16) {
+        v[2 * j] = bf16_to_f32((uint16_t)(w[j] & 0xffff));
+        v[2 * j + 1] = bf16_to_f32((uint16_t)(w[j] >> 16));
+      } else {
+        v[2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffff));
+        v[2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+      }
+    }
+  }
+}
+
+// Single-pass row quant: one block per row, the row held in registers (NV chunks of 8
+// elements per thread, K <= 8 * NV * THREADS), so x is read from memory once.  Same
+// arithmetic as rowquant_kernel: exact amax, asc = fl32(max(amax, 1e-8) / 127), q = clamp(rint(x / asc)).
+template <int THREADS, int NV, int DT>
+__global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __restrict__ x, int64_t K, int64_t ldx,
+                                                               int8_t* __restrict__ q, int64_t ldq,
+                                                               float* __restrict__ asc) {
+  __shared__ float red[THREADS / 64];
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t K8 = K >> 3;
+  const void* row = (const char*)x + m * ldx * (DT == LSK_F32 ? 4 : 2);
+  float v[NV][8];
+  float am = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = tid + (int64_t)j * THREADS;
+    if (c < K8) {
+      load8<DT>(row, c, v[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(v[j][e]));
+    }
+  }
+  am = block_max<THREADS>(am, red);
+  am = fmaxf(am, kAmaxFloor);
+  const float s = f32_div(am, 127.0f);
+  if (tid == 0) asc[m] = s;
+  int8_t* qrow = q + m * ldq;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = tid + (int64_t)j * THREADS;
+    if (c < K8) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lo |= ((uint32_t)(uint8_t)quant_one(v[j][e], s)) << (8 * e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hi |= ((uint32_t)(uint8_t)quant_one(v[j][4 + e], s)) << (8 * e);
+      ((uint2*)qrow)[c] = make_uint2(lo, hi);
+    }
+  }
+}
+
+template <int THREADS, int NV>
+int launch_rowquant_reg(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* asc,
+                        hipStream_t s) {
+  if (dt == LSK_F32)
+    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_F32>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K, ldx,
+                       q, ldq, asc);
+  else if (dt == LSK_BF16)
+    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_BF16>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K,
+                       ldx, q, ldq, asc);
+  else
+    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_F16>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K, ldx,
+                       q, ldq, asc);
+  return lsk::check_launch("rowquant_reg_kernel");
+}
+
 // ---------------------------------------------------------------- power-of-two quantisers
 // e = 6 - (biased_exp(m) - 127); e -= 1 if fl32(m * 2^e) > 127; e = 0 where m == 0; clip [-32, 40]
 LSK_DEV int pow2_exponent(float m) {
@@ -197,8 +278,17 @@ extern "C" int lsk_rowquant(const void* x, int x_dtype, int64_t M, int64_t K, in
   const int esz = x_dtype == LSK_F32 ? 4 : 2;
   const int vec = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) && ((uintptr_t)x % 16 == 0) &&
                   ((uintptr_t)q % 8 == 0) && ((ldx * esz) % 16 == 0);
-  hipLaunchKernelGGL(rowquant_kernel<256>, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, x, x_dtype, K,
-                     ldx, q, ldq, asc, vec);
+  hipStream_t s = (hipStream_t)stream;
+  if (vec) {
+    // single pass with the row in registers: chunks of 8 elements per thread
+    const int64_t K8 = K >> 3;
+    if (K8 <= 256) return launch_rowquant_reg<256, 1>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+    if (K8 <= 512) return launch_rowquant_reg<256, 2>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+    if (K8 <= 1024) return launch_rowquant_reg<256, 4>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+    if (K8 <= 2048) return launch_rowquant_reg<512, 4>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+    if (K8 <= 4096) return launch_rowquant_reg<512, 8>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+  }
+  hipLaunchKernelGGL(rowquant_kernel<256>, dim3((unsigned)M), dim3(256), 0, s, x, x_dtype, K, ldx, q, ldq, asc, vec);
   return lsk::check_launch("rowquant_kernel");
 }
 
