@@ -167,6 +167,34 @@ def decode_section(torch, args):
     return res
 
 
+def copy_section(torch, args):
+    """A plain device copy of 1 GiB (read 1 GiB + write 1 GiB per launch): the calibration
+    kernel for the FETCH_SIZE / WRITE_SIZE counters (rocprofv3 --pmc) behind `traffic`."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(7)
+    dst = torch.empty_like(src)
+    for _ in range(max(args.steps, 1)):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"bytes_per_launch": n}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel at the two step shapes, from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, scaled by the 1 GiB copy's reading), or None."""
+    path = os.path.join(ROOT, "profiles", "dense_prefill_llama8b_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    kv = dict(t.split("=") for t in line.split(":", 1)[1].split())
+                    return {k2: int(v) for k2, v in kv.items()}
+    except (OSError, ValueError):
+        return None
+    return None
+
+
 def _int8_expert_tables(torch, MR, g, dev, E, H, I):
     experts = []
     for _ in range(E):
@@ -193,7 +221,9 @@ def moe_section(torch, args):
     """Config 4 (Qwen3-30B-A3B int8 experts, E=128, k=8, H=2048, I=768) and config 5 (GPT-OSS-20B
     MXFP4 experts, E=32, k=4, H=I=2880) at T in {1, 32, 4096}: one step = the router from the given
     logits (N(0,1), plus a Zipf(1.1) popularity bias for config 4) and the fused layer.  Two weight
-    copies alternate so a step's experts were evicted from the Infinity Cache by the other copy."""
+    copies alternate so a step's experts were evicted from the Infinity Cache by the other copy;
+    timed as HIP-graph replays (the layer has no host synchronisation), so host launch overhead
+    is not counted."""
     from lockstep_amd import contract_common as CC
     from lockstep_amd import moe_ref as MR
     from lockstep_amd import workloads as WL
@@ -218,16 +248,11 @@ def moe_section(torch, args):
                 rank = torch.randperm(E, generator=g, device=dev).to(torch.float32)
                 logits = logits - 1.1 * torch.log1p(rank)[None, :]
             logits = logits.to(torch.bfloat16)
-            it = [0]
-
-            def step():
+            def step(cp):
                 idx, w, _ = MR.router_from_logits(logits, k, True, tab)
-                fwd(x, None, copies[it[0] % 2], k, True, tab, 0, act, routing=(idx, w))
-                it[0] += 1
-            for _ in range(3):
-                step()
-            reps = 20 if T < 4096 else 10
-            ms = _events_time(torch, step, reps)
+                fwd(x, None, cp, k, True, tab, 0, act, routing=(idx, w))
+            reps = 20 if T < 4096 else 5
+            ms = _graph_time(torch, [(lambda cp=cp: step(cp)) for cp in copies], reps)
             idx, _, _ = MR.router_from_logits(logits, k, True, tab)
             active = int(torch.unique(idx).numel())
             gbs = active * bytes_expert / (ms * 1e-3) / 1e9
@@ -333,6 +358,14 @@ def main():
                    "out": "bf16", "parallelism": "single GPU"},
         "roofline": d["roofline"],
     }
+    tr = measured_traffic()
+    if tr and "gate_up" in tr and "down" in tr:
+        out["roofline"]["traffic"] = (tr["gate_up"] + tr["down"]) // 2
+        out["roofline"]["traffic_per_shape"] = {"gate_up": tr["gate_up"], "down": tr["down"]}
+        out["roofline"]["traffic_note"] = ("HBM bytes per launch (mean of the two shapes) from rocprofv3 FETCH_SIZE + "
+                                           "WRITE_SIZE, profiles/dense_prefill_llama8b_pmc.md")
+    if "copy" in sections:
+        out["copy"] = copy_section(torch, args)
     if "decode" in sections:
         log("bench: decode rows M in {1, 8, 32}")
         out["decode"] = decode_section(torch, args)
