@@ -97,21 +97,109 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
   }
 }
 
-// ---------------------------------------------------------------- dispatch (one block)
-__global__ __launch_bounds__(256) void moe_dispatch_kernel(const int64_t* __restrict__ idx,
-                                                           const uint16_t* __restrict__ w, int T, int k, int E,
-                                                           int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
-                                                           int32_t* __restrict__ row_tok,
-                                                           int32_t* __restrict__ row_dst, float* __restrict__ row_w,
-                                                           int32_t* __restrict__ tok_cnt) {
-  extern __shared__ int32_t dsm[];
-  int32_t* cnt = dsm;
-  int32_t* cursor = dsm + E;
-  uint32_t* mask = (uint32_t*)(dsm + 2 * E);  // [E][8]: one bit per token of a 256-token chunk
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += 256) cnt[e] = 0;
+// ---------------------------------------------------------------- dispatch
+// Rows are placed expert-major, token-ascending inside each expert: a counting sort over
+// chunks of 256 tokens whose in-chunk ranks come from per-expert token bitmasks (no atomics
+// decide a position, so the placement is deterministic).
+
+// Exclusive scan of one int per thread across a block of THREADS threads; `total` gets the sum.
+template <int THREADS>
+LSK_DEV int block_excl_scan(int v, int* tmp, int& total) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
   __syncthreads();
-  for (int t = tid; t < T; t += 256) {
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < THREADS / 64; ++w2) {
+    const int t = tmp[w2];
+    if (w2 < wave) base += t;
+    tot += t;
+  }
+  __syncthreads();
+  total = tot;
+  return base + x - v;
+}
+
+// Expert offsets and the M-tile table from per-expert row counts cnt[E] (any memory the block
+// reads): offs[e] = rows of experts < e, offs[E] = all rows; tiles[0] = number of kBM-row tiles,
+// then (expert, first row) per tile, experts ascending.  Each thread owns a contiguous run of
+// experts.
+template <int THREADS>
+LSK_DEV void expert_offsets_and_tiles(const int32_t* cnt, int E, int32_t* offs, int32_t* tiles, int* tmp) {
+  const int per = (E + THREADS - 1) / THREADS;
+  const int e0 = threadIdx.x * per;
+  int rows = 0, ntl = 0;
+  for (int e = e0; e < e0 + per && e < E; ++e) {
+    rows += cnt[e];
+    ntl += (cnt[e] + kBM - 1) / kBM;
+  }
+  int rows_all, tiles_all;
+  int rbase = block_excl_scan<THREADS>(rows, tmp, rows_all);
+  int tbase = block_excl_scan<THREADS>(ntl, tmp, tiles_all);
+  for (int e = e0; e < e0 + per && e < E; ++e) {
+    offs[e] = rbase;
+    const int c = cnt[e];
+    for (int r0 = 0; r0 < c; r0 += kBM, ++tbase) {
+      tiles[1 + 2 * tbase] = e;
+      tiles[2 + 2 * tbase] = rbase + r0;
+    }
+    rbase += c;
+  }
+  if (threadIdx.x == 0) {
+    offs[E] = rows_all;
+    tiles[0] = tiles_all;
+  }
+}
+
+// Place the rows of the 256-token chunk c0 .. c0+255: p = base[e] + (rank of the token among the
+// chunk's tokens routed to e); base (LDS or global) is advanced by the caller.  mask: E x 8 words.
+LSK_DEV void place_chunk(const int64_t* __restrict__ idx, const uint16_t* __restrict__ w, int T, int k, int E, int c0,
+                         const int32_t* base, uint32_t* mask, int32_t* __restrict__ row_tok,
+                         int32_t* __restrict__ row_dst, float* __restrict__ row_w) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E * 8; i += 256) mask[i] = 0;
+  __syncthreads();
+  const int t = c0 + tid;
+  if (t < T) {
+    for (int j = 0; j < k; ++j) {
+      const int64_t e = idx[(int64_t)t * k + j];
+      if (e >= 0 && e < E) atomicOr(&mask[e * 8 + (tid >> 5)], 1u << (tid & 31));
+    }
+  }
+  __syncthreads();
+  if (t < T) {
+    for (int j = 0; j < k; ++j) {
+      const int64_t e = idx[(int64_t)t * k + j];
+      if (!(e >= 0 && e < E)) continue;
+      int rank = __popc(mask[e * 8 + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
+      for (int wd = 0; wd < (tid >> 5); ++wd) rank += __popc(mask[e * 8 + wd]);
+      const int p = base[e] + rank;
+      int slot = 0;  // rank of e among the token's experts, ascending
+      for (int j2 = 0; j2 < k; ++j2) {
+        const int64_t e2 = idx[(int64_t)t * k + j2];
+        if (e2 >= 0 && e2 < E && e2 < e) ++slot;
+      }
+      row_tok[p] = t;
+      row_dst[p] = t * k + slot;
+      row_w[p] = bf16_to_f32(w[(int64_t)t * k + j]);
+    }
+  }
+  __syncthreads();
+}
+
+// Tokens routed to each expert in a 256-token chunk (LDS cnt[E]), and each token's number of
+// valid routes; also zeroes zero_n words of zero_buf (the per-row |h| maxima) grid-wide.
+LSK_DEV void count_chunk(const int64_t* __restrict__ idx, int T, int k, int E, int c0, int32_t* cnt,
+                         int32_t* __restrict__ tok_cnt) {
+  const int tid = threadIdx.x;
+  const int t = c0 + tid;
+  if (t < T) {
     int nv = 0;
     for (int j = 0; j < k; ++j) {
       const int64_t e = idx[(int64_t)t * k + j];
@@ -122,70 +210,86 @@ __global__ __launch_bounds__(256) void moe_dispatch_kernel(const int64_t* __rest
     }
     tok_cnt[t] = nv;
   }
+}
+
+// T <= 256: the whole dispatch in one block.
+__global__ __launch_bounds__(256) void moe_dispatch_small_kernel(const int64_t* __restrict__ idx,
+                                                                 const uint16_t* __restrict__ w, int T, int k, int E,
+                                                                 int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
+                                                                 int32_t* __restrict__ row_tok,
+                                                                 int32_t* __restrict__ row_dst,
+                                                                 float* __restrict__ row_w,
+                                                                 int32_t* __restrict__ tok_cnt,
+                                                                 uint32_t* __restrict__ zero_buf, int64_t zero_n) {
+  extern __shared__ int32_t dsm[];
+  __shared__ int tmp[4];
+  int32_t* cnt = dsm;
+  int32_t* base = dsm + E;
+  uint32_t* mask = (uint32_t*)(dsm + 2 * E);
+  const int tid = threadIdx.x;
+  for (int64_t i = tid; i < zero_n; i += 256) zero_buf[i] = 0u;
+  for (int e = tid; e < E; e += 256) cnt[e] = 0;
   __syncthreads();
-  if (tid == 0) {
-    int run = 0, nt = 0;
-    for (int e = 0; e < E; ++e) {
-      offs[e] = run;
-      cursor[e] = run;
-      const int c = cnt[e];
-      for (int r0 = run; r0 < run + c; r0 += kBM) {
-        tiles[1 + 2 * nt] = e;
-        tiles[2 + 2 * nt] = r0;
-        ++nt;
-      }
-      run += c;
-    }
-    offs[E] = run;
-    tiles[0] = nt;
+  count_chunk(idx, T, k, E, 0, cnt, tok_cnt);
+  __syncthreads();
+  expert_offsets_and_tiles<256>(cnt, E, base, tiles, tmp);
+  __syncthreads();
+  for (int e = tid; e <= E; e += 256) offs[e] = base[e];  // base[E] = all rows
+  __syncthreads();
+  place_chunk(idx, w, T, k, E, 0, base, mask, row_tok, row_dst, row_w);
+}
+
+// Large T, step 1: per-chunk expert counts ccnt[chunk][E].
+__global__ __launch_bounds__(256) void moe_count_kernel(const int64_t* __restrict__ idx, int T, int k, int E,
+                                                        int32_t* __restrict__ ccnt, int32_t* __restrict__ tok_cnt,
+                                                        uint32_t* __restrict__ zero_buf, int64_t zero_n) {
+  extern __shared__ int32_t cnt[];
+  const int tid = threadIdx.x;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < zero_n; i += (int64_t)gridDim.x * 256) zero_buf[i] = 0u;
+  for (int e = tid; e < E; e += 256) cnt[e] = 0;
+  __syncthreads();
+  count_chunk(idx, T, k, E, blockIdx.x * 256, cnt, tok_cnt);
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) ccnt[(int64_t)blockIdx.x * E + e] = cnt[e];
+}
+
+// Large T, step 2 (one block): expert offsets, tile table, and each chunk's first row per
+// expert cbase[chunk][E] (chunks ascending inside each expert: token order).
+__global__ __launch_bounds__(1024) void moe_scan_kernel(const int32_t* __restrict__ ccnt, int nchunks, int E,
+                                                        int32_t* __restrict__ cbase, int32_t* __restrict__ offs,
+                                                        int32_t* __restrict__ tiles) {
+  extern __shared__ int32_t tot[];  // [E]
+  __shared__ int tmp[16];
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    int s2 = 0;
+    for (int c = 0; c < nchunks; ++c) s2 += ccnt[(int64_t)c * E + e];
+    tot[e] = s2;
   }
   __syncthreads();
-  for (int c0 = 0; c0 < T; c0 += 256) {
-    for (int i = tid; i < E * 8; i += 256) mask[i] = 0;
-    __syncthreads();
-    const int t = c0 + tid;
-    if (t < T) {
-      for (int j = 0; j < k; ++j) {
-        const int64_t e = idx[(int64_t)t * k + j];
-        if (e >= 0 && e < E) atomicOr(&mask[e * 8 + (tid >> 5)], 1u << (tid & 31));
-      }
+  expert_offsets_and_tiles<1024>(tot, E, offs, tiles, tmp);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    int run = offs[e];
+    for (int c = 0; c < nchunks; ++c) {
+      cbase[(int64_t)c * E + e] = run;
+      run += ccnt[(int64_t)c * E + e];
     }
-    __syncthreads();
-    if (t < T) {
-      for (int j = 0; j < k; ++j) {
-        const int64_t e = idx[(int64_t)t * k + j];
-        if (!(e >= 0 && e < E)) continue;
-        int rank = __popc(mask[e * 8 + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
-        for (int wd = 0; wd < (tid >> 5); ++wd) rank += __popc(mask[e * 8 + wd]);
-        const int p = cursor[e] + rank;
-        int slot = 0;  // rank of e among the token's experts, ascending
-        for (int j2 = 0; j2 < k; ++j2) {
-          const int64_t e2 = idx[(int64_t)t * k + j2];
-          if (e2 >= 0 && e2 < E && e2 < e) ++slot;
-        }
-        row_tok[p] = t;
-        row_dst[p] = t * k + slot;
-        row_w[p] = bf16_to_f32(w[(int64_t)t * k + j]);
-      }
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += 256) {
-      int c = 0;
-#pragma unroll
-      for (int wd = 0; wd < 8; ++wd) c += __popc(mask[e * 8 + wd]);
-      cursor[e] += c;
-    }
-    __syncthreads();
   }
+}
+
+// Large T, step 3: place each chunk's rows.
+__global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restrict__ idx, const uint16_t* __restrict__ w,
+                                                        int T, int k, int E, const int32_t* __restrict__ cbase,
+                                                        int32_t* __restrict__ row_tok, int32_t* __restrict__ row_dst,
+                                                        float* __restrict__ row_w) {
+  extern __shared__ uint32_t mask[];  // [E][8]
+  place_chunk(idx, w, T, k, E, blockIdx.x * 256, cbase + (int64_t)blockIdx.x * E, mask, row_tok, row_dst, row_w);
 }
 
 __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x, int64_t n, float* __restrict__ y) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) y[i] = bf16_to_f32(x[i]);
 }
 
-__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
-}
 
 // ---------------------------------------------------------------- grouped GEMM
 using lsk::MoeGemmArgs;
@@ -453,6 +557,8 @@ struct MoeWs {
   int32_t* row_dst;
   float* row_w;
   int32_t* tok_cnt;
+  int32_t* ccnt;   // [chunks][E] per-chunk expert counts (T > 256)
+  int32_t* cbase;  // [chunks][E] first row of each chunk's rows per expert
   uint16_t* h;
   uint32_t* h_amax;
   int8_t* qh;
@@ -484,6 +590,9 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.row_dst = (int32_t*)take(R * 4);
   w.row_w = (float*)take(R * 4);
   w.tok_cnt = (int32_t*)take(T * 4);
+  const int64_t nchunks = (T + 255) / 256;
+  w.ccnt = (int32_t*)take(nchunks * E * 4);
+  w.cbase = (int32_t*)take(nchunks * E * 4);
   w.h = (uint16_t*)take(R * I * 2);
   w.h_amax = (uint32_t*)take(R * 4);
   w.qh = (int8_t*)take(R * I * qb);
@@ -577,15 +686,23 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     rc = lsk_rowquant(a->x, LSK_BF16, T, H, H, w.qx, H, w.ascx, stream);
   }
   if (rc) return rc;
-  const size_t dsm = (size_t)(2 * E + 8 * E) * 4;
-  hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(256), dsm, s, a->idx, a->w, (int)T, k, (int)E, w.offs, w.tiles,
-                     w.row_tok, w.row_dst, w.row_w, w.tok_cnt);
-  if ((rc = lsk::check_launch("moe_dispatch_kernel"))) return rc;
-  {
-    int64_t blocks = (R + 255) / 256;
-    blocks = blocks > 1024 ? 1024 : (blocks < 1 ? 1 : blocks);
-    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w.h_amax, R, 0u);
-    if ((rc = lsk::check_launch("fill_u32_kernel"))) return rc;
+  // dispatch (and the zeroing of the per-row |h| maxima, which the gate/up GEMM raises)
+  const int64_t nchunks = (T + 255) / 256;
+  if (nchunks == 1) {
+    const size_t dsm = (size_t)(2 * E + 8 * E) * 4;
+    hipLaunchKernelGGL(moe_dispatch_small_kernel, dim3(1), dim3(256), dsm, s, a->idx, a->w, (int)T, k, (int)E, w.offs,
+                       w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, R);
+    if ((rc = lsk::check_launch("moe_dispatch_small_kernel"))) return rc;
+  } else {
+    hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 4, s, a->idx, (int)T, k,
+                       (int)E, w.ccnt, w.tok_cnt, w.h_amax, R);
+    if ((rc = lsk::check_launch("moe_count_kernel"))) return rc;
+    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), (size_t)E * 4, s, w.ccnt, (int)nchunks, (int)E, w.cbase,
+                       w.offs, w.tiles);
+    if ((rc = lsk::check_launch("moe_scan_kernel"))) return rc;
+    hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 8 * 4, s, a->idx, a->w,
+                       (int)T, k, (int)E, w.cbase, w.row_tok, w.row_dst, w.row_w);
+    if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
   }
   MoeGemmArgs g1{};
   g1.A = w.qx;

@@ -153,6 +153,22 @@ def test_moe_skipped_experts_out_of_range():
     _run_case(T, E, k, 128, 64, seed=6, routing_override=(idx, w))
 
 
+@pytest.mark.parametrize("T,E,k", [(700, 16, 4), (513, 9, 3)])
+def test_moe_multi_chunk_dispatch(T, E, k):
+    """T > 256: per-chunk counts, the expert scan and per-chunk placement; every output against
+    the oracle (Zipf-skewed routing, some experts never chosen)."""
+    _run_case(T, E, k, 128, 64, seed=11 + T)
+
+
+def test_moe_multi_chunk_out_of_range_entries():
+    """Routing entries outside [0, E) spread over several 256-token chunks are skipped."""
+    T, E, k = 600, 5, 3
+    r = np.random.default_rng(12)
+    idx = np.stack([r.permutation(8)[:k] for _ in range(T)]).astype(np.int64)   # some >= E
+    w = C.bf16_bits(r.uniform(0, 1, (T, k)).astype(F32))
+    _run_case(T, E, k, 128, 64, seed=12, routing_override=(idx, w))
+
+
 def test_moe_bias_swigluoai():
     _run_case(40, 8, 3, 256, 192, seed=7, bias=True, act="swigluoai")
 
