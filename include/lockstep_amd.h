@@ -249,6 +249,12 @@ int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int
 
 int lsk_moe_forward(const lsk_moe_args* args, void* stream);
 
+/* Tuning control with no counterpart in the reference: the int8 grouped expert GEMMs of
+ * lsk_moe_forward on the 128x128 register-staged tile (0), on the eight-wave ping-pong
+ * 128x256 tile (1), or chosen by size (-1, the default: ping-pong once the routed rows reach
+ * E x 128).  Results are identical for every choice.  Process-wide. */
+int lsk_moe_select(int variant);
+
 #ifdef __cplusplus
 }
 #endif

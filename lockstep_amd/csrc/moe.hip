@@ -16,12 +16,14 @@
 #include "contract_act.h"
 #include "mfma_tile.h"
 #include "moe_internal.h"
+#include "pp_tile.h"
 
 namespace {
 
 constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
 constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
 constexpr int kBM = lsk::kMoeBM;
+int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile
 
 // ---------------------------------------------------------------- router
 LSK_DEV long long wave_max_ll(long long v) {
@@ -437,6 +439,199 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     }
 }
 
+// Grouped GEMM on the eight-wave ping-pong main loop: a 128-row expert tile (the dispatch's tile
+// granularity) by 256 weight rows.  MODE 0 (gate/up): the 256 weight rows are 128 h-columns'
+// gate and up rows interleaved per 32, so each wave's 64-column strip holds a [gate 32 | up 32]
+// pair and the activation is thread-local; MODE 1 (down): 256 output columns.  The epilogue
+// operands of the tile (row scales, routing weights and slots, column scales and biases) are
+// loaded before the main loop and parked in LDS after it.
+using PPM = lsk::PPCfg<128, 256, 2, 4, 4>;
+static_assert(PPM::kSmemBytes - PPM::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
+
+template <int MODE>
+__global__ __launch_bounds__(512) void moe_pp_kernel(MoeGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_moe[];
+  const int ntiles = MODE == 0 ? (a.N + 127) / 128 : (a.N + 255) / 256;
+  const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
+  const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
+  if (mt >= a.tiles[0]) return;  // the whole block leaves: no barrier is left waiting
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + kBM);
+  const int8_t* wb = (const int8_t*)a.w_ptrs[e];
+  const float* ws = (const float*)a.ws_ptrs[e];
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm = wave / PPM::kWN, wn = wave % PPM::kWN;
+
+  // weight row of local column c (gate/up interleave) and whether it exists
+  auto wrow_of = [&](int c, int& hc) {
+    if (MODE == 0) {
+      const int blk = c >> 5;
+      hc = nt * 128 + (blk >> 1) * 32 + (c & 31);
+      return (blk & 1) ? a.N + hc : hc;
+    }
+    hc = nt * 256 + c;
+    return hc;
+  };
+
+  // epilogue operands, held in registers across the main loop
+  float r_asc = 0.0f, r_w = 0.0f, c_ws = 0.0f, c_b = 0.0f;
+  int r_dst = 0;
+  if (tid < 128 && p0 + tid < p1) {
+    const int p = p0 + tid;
+    if (MODE == 0) {
+      r_asc = a.a_scale[a.row_tok[p]];
+    } else {
+      r_asc = a.a_scale[p];
+      r_w = a.row_w[p];
+      r_dst = a.row_dst[p];
+    }
+  }
+  if (tid < 256) {
+    int hc;
+    const int wr = wrow_of(tid, hc);
+    if (hc < a.N) {
+      c_ws = ws[wr];
+      if (bias) c_b = bias[wr];
+    }
+  }
+
+  const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(a.A, a.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(wb, a.w_bytes);
+  typename PPM::RowsA pa;
+  typename PPM::RowsB pb;
+#pragma unroll
+  for (int j = 0; j < PPM::kLA; ++j) {
+    int row, kb;
+    lsk::pp_slot<PPM::kThreads>(tid, j, row, kb);
+    const int p = p0 + row;
+    const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
+    pa[j] = src >= 0 ? (uint32_t)(src * a.lda) : lsk::kOob;
+  }
+#pragma unroll
+  for (int j = 0; j < PPM::kLB; ++j) {
+    int row, kb, hc;
+    lsk::pp_slot<PPM::kThreads>(tid, j, row, kb);
+    const int wr = wrow_of(row, hc);
+    pb[j] = hc < a.N ? (uint32_t)(wr * a.ldw) : lsk::kOob;
+  }
+  typename PPM::Acc acc;
+#pragma unroll
+  for (int i = 0; i < PPM::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < PPM::TN; ++j) acc[i][j] = lsk::zero16();
+
+  lsk::pp_mainloop<128, 256, 2, 4, 4>(acc, ra_res, pa, rb_res, pb, a.K, smem_moe);
+
+  // park the operands in LDS (past every wave's last ring read)
+  float* sc_asc = (float*)(smem_moe + PPM::kScaleOff);
+  float* sc_w = sc_asc + 128;
+  int* sc_dst = (int*)(sc_w + 128);
+  float* sc_ws = (float*)(sc_dst + 128);
+  float* sc_b = sc_ws + 256;
+  if (tid < 128) {
+    sc_asc[tid] = r_asc;
+    sc_w[tid] = r_w;
+    sc_dst[tid] = r_dst;
+  }
+  if (tid < 256) {
+    sc_ws[tid] = c_ws;
+    sc_b[tid] = c_b;
+  }
+  __syncthreads();
+
+  int32_t* region = (int32_t*)(smem_moe + wave * PPM::kStripBytes);
+  auto strip = [&](int i) {
+    if (MODE == 0) {
+      // 32 rows x 8 column quads of [gate | up]; a lane keeps one quad (lane & 7)
+      const int c4 = (lane & 7) * 4;
+      const int hc0 = nt * 128 + wn * 32 + c4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int row = (lane >> 3) + 8 * t;
+        const int ml = wm * PPM::WTM + i * 32 + row;
+        const int p = p0 + ml;
+        const v4i vg = *(const v4i*)(region + row * PPM::kLdc + c4);
+        const v4i vu = *(const v4i*)(region + row * PPM::kLdc + 32 + c4);
+        float am = 0.0f;
+        if (p < p1) {
+          const float asc = sc_asc[ml];
+          uint16_t hb[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int hc = hc0 + q;
+            hb[q] = 0;
+            if (hc < a.N) {
+              const int cg = wn * 64 + c4 + q, cu = cg + 32;
+              float yg = bfr(f32_mul(f32_mul((float)vg[q], sc_ws[cg]), asc));
+              float yu = bfr(f32_mul(f32_mul((float)vu[q], sc_ws[cu]), asc));
+              if (bias) {
+                yg = bfr(f32_add(yg, sc_b[cg]));
+                yu = bfr(f32_add(yu, sc_b[cu]));
+              }
+              const float hv =
+                  a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
+              hb[q] = f32_to_bf16(hv);
+              am = fmaxf(am, fabsf(hv));
+            }
+          }
+          uint16_t* dst = a.h + (int64_t)p * a.N + hc0;
+          if (hc0 + 4 <= a.N) {
+            *(uint2*)dst =
+                make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
+          } else {
+            for (int q = 0; q < 4; ++q)
+              if (hc0 + q < a.N) dst[q] = hb[q];
+          }
+        }
+        am = fmaxf(am, __shfl_xor(am, 1, 64));
+        am = fmaxf(am, __shfl_xor(am, 2, 64));
+        am = fmaxf(am, __shfl_xor(am, 4, 64));
+        if ((lane & 7) == 0 && p < p1) atomicMax(&a.h_amax[p], __float_as_uint(am));
+      }
+    } else {
+      // 32 rows x 16 column quads; a lane keeps one quad (lane & 15)
+      const int c4 = (lane & 15) * 4;
+      const int n0 = nt * 256 + wn * 64 + c4;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int row = (lane >> 4) + 4 * t;
+        const int ml = wm * PPM::WTM + i * 32 + row;
+        const int p = p0 + ml;
+        const v4i v = *(const v4i*)(region + row * PPM::kLdc + c4);
+        if (p < p1 && n0 < a.N) {
+          const float asc = sc_asc[ml];
+          const float wt = sc_w[ml];
+          uint16_t ob[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int cl = wn * 64 + c4 + q;
+            ob[q] = 0;
+            if (n0 + q < a.N) {
+              float yv = bfr(f32_mul(f32_mul((float)v[q], sc_ws[cl]), asc));
+              if (bias) yv = bfr(f32_add(yv, sc_b[cl]));
+              ob[q] = f32_to_bf16(f32_mul(wt, yv));
+            }
+          }
+          uint16_t* dst = a.y + (int64_t)sc_dst[ml] * a.N + n0;
+          if (n0 + 4 <= a.N) {
+            *(uint2*)dst =
+                make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+          } else {
+            for (int q = 0; q < 4; ++q)
+              if (n0 + q < a.N) dst[q] = ob[q];
+          }
+        }
+      }
+    }
+  };
+  lsk::pp_stage_strip<PPM::TN, PPM::kLdc>(acc[0], region);
+  strip(0);
+  lsk::pp_stage_strip<PPM::TN, PPM::kLdc>(acc[1], region);
+  strip(1);
+}
+
 // ---------------------------------------------------------------- requant and combine
 // rowquant of the activation output h (bf16 values), with the row maxima from the GEMM.
 __global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __restrict__ h, const uint32_t* __restrict__ amax,
@@ -604,6 +799,26 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
 }
 
 template <int MODE>
+int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const char* name) {
+  static_assert(PPM::TM == 2, "the epilogue stages two 32-row strips");
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)moe_pp_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            PPM::kSmemBytes) != hipSuccess) {
+      lsk::set_error("%s: cannot reserve %d bytes of LDS", name, PPM::kSmemBytes);
+      return LSK_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  const int ntiles = MODE == 0 ? (ga.N + 127) / 128 : (ga.N + 255) / 256;
+  const int64_t blocks = max_tiles * ntiles;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  hipLaunchKernelGGL(moe_pp_kernel<MODE>, dim3((unsigned)blocks), dim3(512), PPM::kSmemBytes, s, ga);
+  return lsk::check_launch(name);
+}
+
+template <int MODE>
 int launch_moe_gemm(const MoeGemmArgs& ga, int64_t max_tiles, int ntiles, hipStream_t s, const char* name) {
   using C = lsk::TileCfg<128, 128, 2, 2>;
   const int64_t blocks = max_tiles * ntiles;
@@ -627,6 +842,12 @@ extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t 
   hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, (hipStream_t)stream, g, g_dtype,
                      ldg, (int)T, (int)E, k, renormalize, tab, idx, w_bf16);
   return lsk::check_launch("router_topk_kernel");
+}
+
+extern "C" int lsk_moe_select(int variant) {
+  LSK_REQUIRE(variant >= -1 && variant <= 1, "lsk_moe_select: variant %d not in [-1, 1]", variant);
+  g_moe_force = variant;
+  return LSK_OK;
 }
 
 extern "C" int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt) {
@@ -670,6 +891,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
               "lsk_moe_forward: workspace of %lld bytes (256-byte aligned) needed", (long long)w.bytes);
   hipStream_t s = (hipStream_t)stream;
   const int64_t R = T * k;
+  // the ping-pong grouped GEMM once experts average a full 128-row tile or more; the 128x128
+  // register-staged tile below that (decode-sized token counts)
+  const bool use_pp = g_moe_force >= 0 ? g_moe_force == 1 : R >= (int64_t)E * kBM;
 
   int rc;
   if (rb > 0) {
@@ -726,6 +950,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g1.lds = a->lds13;
   if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (use_pp) {
+    if ((rc = launch_moe_pp<0>(g1, w.max_tiles, s, "moe_pp_kernel<gate_up>"))) return rc;
   } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
     return rc;
   }
@@ -762,6 +988,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g2.lds = a->lds2;
   if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (use_pp) {
+    if ((rc = launch_moe_pp<1>(g2, w.max_tiles, s, "moe_pp_kernel<down>"))) return rc;
   } else if ((rc = launch_moe_gemm<1>(g2, w.max_tiles, (int)((H + 127) / 128), s, "moe_gemm_kernel<down>"))) {
     return rc;
   }

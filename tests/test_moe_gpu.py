@@ -160,6 +160,20 @@ def test_moe_multi_chunk_dispatch(T, E, k):
     _run_case(T, E, k, 128, 64, seed=11 + T)
 
 
+@pytest.mark.parametrize("variant", [0, 1])
+def test_moe_grouped_gemm_variants(variant):
+    """Both grouped-GEMM tiles (register-staged 128x128, ping-pong 128x256) give the oracle's bits:
+    skewed routing with multi-tile experts, empty experts, a bias and SwiGLU-OAI."""
+    from lockstep_amd import _lib as L
+    L.call("lsk_moe_select", variant)
+    try:
+        _run_case(300, 12, 4, 256, 192, seed=13)
+        _run_case(150, 6, 2, 320, 96, seed=14, bias=True, act="swigluoai")
+        _run_case(5, 16, 4, 256, 128, seed=15)
+    finally:
+        L.call("lsk_moe_select", -1)
+
+
 def test_moe_multi_chunk_out_of_range_entries():
     """Routing entries outside [0, E) spread over several 256-token chunks are skipped."""
     T, E, k = 600, 5, 3
