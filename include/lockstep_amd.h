@@ -102,8 +102,8 @@ int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
  * 2: ping-pong 256x256, 8 waves of 128x64; 3: ping-pong 256x128, 8 waves of 64x64;
  * 4: ping-pong 128x256, 8 waves of 64x64; 5: the decode GEMV when M <= 32, else tile 0;
  * 6, 7: for M <= 4 the 8-row register-buffered / LDS-ring GEMV instead of the whole-row GEMV;
- * 8..11: the whole-row GEMV with 1 / 2 / 4 / 8 rows per wave) or -1 to choose by shape (the
- * default).  Results are identical for every choice; only speed
+ * 8..11: the whole-row GEMV with 1 / 2 / 4 / 8 rows per wave; 12, 13: tiles 3, 4 with a
+ * three-stage LDS ring, two blocks per CU) or -1 to choose by shape (the default).  Results are identical for every choice; only speed
  * differs.  Process-wide, not thread-safe against concurrent launches. */
 int lsk_gemm_select(int tile_id);
 

@@ -140,7 +140,7 @@ __device__ __forceinline__ void pp_epilogue(const typename C::Acc& acc, const Ep
 // (asc / row exponents, ws, bias, column exponents) are loaded into registers before the main
 // loop and parked in LDS after it, so the epilogue itself touches global memory only to store.
 template <int BM, int BN, int WM, int WN, int RING>
-__global__ __launch_bounds__(512) void gemm_i8_pp_kernel(const int8_t* __restrict__ A, int lda,
+__global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(const int8_t* __restrict__ A, int lda,
                                                          const int8_t* __restrict__ W, int ldw, int M, int N, int K,
                                                          EpiParams ep, int vec_ok) {
   using C = lsk::PPCfg<BM, BN, WM, WN, RING>;
@@ -880,6 +880,8 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     case 2: return launch_pp<256, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,2x4>");
     case 3: return launch_pp<256, 128, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x128,4x2>");
     case 4: return launch_pp<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4>");
+    case 12: return launch_pp<256, 128, 4, 2, 3>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x128,4x2,r3>");
+    case 13: return launch_pp<128, 256, 2, 4, 3>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4,r3>");
     default: return launch_tile<128, 128, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2>");
   }
 }
@@ -948,9 +950,9 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 11, "lsk_gemm_select: tile id %d not in [-1, 11]", tile_id);
-  lsk::g_force_tile = tile_id >= 6 ? 5 : tile_id;
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 13, "lsk_gemm_select: tile id %d not in [-1, 13]", tile_id);
+  lsk::g_force_tile = (tile_id >= 6 && tile_id <= 11) ? 5 : tile_id;
   lsk::g_gemv_variant = (tile_id == 6 || tile_id == 7) ? tile_id - 5 : 0;
-  lsk::g_row_rpw = tile_id >= 8 ? (1 << (tile_id - 8)) : 0;
+  lsk::g_row_rpw = (tile_id >= 8 && tile_id <= 11) ? (1 << (tile_id - 8)) : 0;
   return LSK_OK;
 }

@@ -440,16 +440,17 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
 }
 
 // Grouped GEMM on the eight-wave ping-pong main loop: a 128-row expert tile (the dispatch's tile
-// granularity) by 256 weight rows.  MODE 0 (gate/up): the 256 weight rows are 128 h-columns'
+// granularity) by 256 weight rows; a three-stage LDS ring keeps a block under 80 KB so two
+// blocks share a CU and one's epilogue overlaps the other's main loop.  MODE 0 (gate/up): the 256 weight rows are 128 h-columns'
 // gate and up rows interleaved per 32, so each wave's 64-column strip holds a [gate 32 | up 32]
 // pair and the activation is thread-local; MODE 1 (down): 256 output columns.  The epilogue
 // operands of the tile (row scales, routing weights and slots, column scales and biases) are
 // loaded before the main loop and parked in LDS after it.
-using PPM = lsk::PPCfg<128, 256, 2, 4, 4>;
+using PPM = lsk::PPCfg<128, 256, 2, 4, 3>;  // three-stage ring: two blocks per CU
 static_assert(PPM::kSmemBytes - PPM::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
 
 template <int MODE>
-__global__ __launch_bounds__(512) void moe_pp_kernel(MoeGemmArgs a) {
+__global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
   const int ntiles = MODE == 0 ? (a.N + 127) / 128 : (a.N + 255) / 256;
   const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
@@ -522,7 +523,7 @@ __global__ __launch_bounds__(512) void moe_pp_kernel(MoeGemmArgs a) {
 #pragma unroll
     for (int j = 0; j < PPM::TN; ++j) acc[i][j] = lsk::zero16();
 
-  lsk::pp_mainloop<128, 256, 2, 4, 4>(acc, ra_res, pa, rb_res, pb, a.K, smem_moe);
+  lsk::pp_mainloop<128, 256, 2, 4, 3>(acc, ra_res, pa, rb_res, pb, a.K, smem_moe);
 
   // park the operands in LDS (past every wave's last ring read)
   float* sc_asc = (float*)(smem_moe + PPM::kScaleOff);
