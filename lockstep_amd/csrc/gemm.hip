@@ -139,11 +139,11 @@ __device__ __forceinline__ void pp_epilogue(const typename C::Acc& acc, const Ep
 // operand contract and tile order as gemm_i8_mfma_kernel.  The epilogue operands of the tile
 // (asc / row exponents, ws, bias, column exponents) are loaded into registers before the main
 // loop and parked in LDS after it, so the epilogue itself touches global memory only to store.
-template <int BM, int BN, int WM, int WN, int RING>
+template <int BM, int BN, int WM, int WN, int RING, int BKB>
 __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(const int8_t* __restrict__ A, int lda,
                                                          const int8_t* __restrict__ W, int ldw, int M, int N, int K,
                                                          EpiParams ep, int vec_ok) {
-  using C = lsk::PPCfg<BM, BN, WM, WN, RING>;
+  using C = lsk::PPCfg<BM, BN, WM, WN, RING, BKB>;
   extern __shared__ __attribute__((aligned(16))) char smem_pp[];
   const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN;
   const int L = lsk::xcd_logical_id(blockIdx.x, mtiles * ntiles);
@@ -180,13 +180,13 @@ __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(co
 #pragma unroll
   for (int j = 0; j < C::kLA; ++j) {
     int row, kb;
-    lsk::pp_slot<C::kThreads>(tid, j, row, kb);
+    lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
     pa[j] = (m0 + row < M) ? (uint32_t)(row * lda) : lsk::kOob;
   }
 #pragma unroll
   for (int j = 0; j < C::kLB; ++j) {
     int row, kb;
-    lsk::pp_slot<C::kThreads>(tid, j, row, kb);
+    lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
     pb[j] = (n0 + row < N) ? (uint32_t)(row * ldw) : lsk::kOob;
   }
   typename C::Acc acc;
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(co
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  lsk::pp_mainloop<BM, BN, WM, WN, RING>(acc, ra_res, pa, rb_res, pb, K, smem_pp);
+  lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra_res, pa, rb_res, pb, K, smem_pp);
 
   // every wave is past its last read of the LDS ring
   float* sc_row = (float*)(smem_pp + C::kScaleOff);
@@ -733,12 +733,12 @@ static int launch_tile(const int8_t* a, int lda, const int8_t* w, int ldw, int M
   return check_launch(name);
 }
 
-template <int BM, int BN, int WM, int WN, int RING = 4>
+template <int BM, int BN, int WM, int WN, int RING = 4, int BKB = 64>
 static int launch_pp(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K, const EpiParams& ep,
                      int vec_ok, hipStream_t s, const char* name) {
-  using C = PPCfg<BM, BN, WM, WN, RING>;
+  using C = PPCfg<BM, BN, WM, WN, RING, BKB>;
   static bool attr_set = false;
-  auto kern = gemm_i8_pp_kernel<BM, BN, WM, WN, RING>;
+  auto kern = gemm_i8_pp_kernel<BM, BN, WM, WN, RING, BKB>;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmemBytes) !=
         hipSuccess) {

@@ -505,7 +505,7 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
 #pragma unroll
   for (int j = 0; j < PPM::kLA; ++j) {
     int row, kb;
-    lsk::pp_slot<PPM::kThreads>(tid, j, row, kb);
+    lsk::pp_slot<PPM::kThreads, PPM::kChunks>(tid, j, row, kb);
     const int p = p0 + row;
     const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
     pa[j] = src >= 0 ? (uint32_t)(src * a.lda) : lsk::kOob;
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
 #pragma unroll
   for (int j = 0; j < PPM::kLB; ++j) {
     int row, kb, hc;
-    lsk::pp_slot<PPM::kThreads>(tid, j, row, kb);
+    lsk::pp_slot<PPM::kThreads, PPM::kChunks>(tid, j, row, kb);
     const int wr = wrow_of(row, hc);
     pb[j] = hc < a.N ? (uint32_t)(wr * a.ldw) : lsk::kOob;
   }

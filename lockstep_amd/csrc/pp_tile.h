@@ -6,30 +6,35 @@
 // from LDS and issues the next global loads.  Each SIMD's matrix core therefore always has a
 // wave with operands ready, and the LDS port is used by one group at a time.
 //
-// K is staged 64 bytes at a time through a ring of four LDS stages filled by direct
+// K is staged 64 (or 128) bytes at a time through a ring of LDS stages filled by direct
 // global -> LDS loads (buffer_load_dwordx4 ... lds: no registers, no LDS write instructions).
-// Loads run three stages ahead of the stage being multiplied.  A stage holds BM + BN rows of
-// 64 bytes as four 16-byte chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the
-// 16 lanes one LDS cycle serves (16 consecutive rows, one logical chunk) touch 16 distinct
-// 16-byte bank groups of the 256-byte bank row.
+// Loads run RING - 1 stages ahead of the stage being multiplied.  A stage holds BM + BN rows
+// of 16-byte chunks, XOR-swizzled per row (pp_swz) so that the 16 lanes one LDS cycle serves
+// (16 consecutive rows, one logical chunk) touch 16 distinct 16-byte bank groups of the
+// 256-byte bank row.
 //
 // v_mfma_i32_32x32x32_i8: lane l supplies 16 bytes of row l % 32 at K-group l / 32 of both
 // operands; the 64-byte stage is two such K-steps.  Integer accumulation is exact in any
 // order (|acc| <= K * 127^2 < 2^31), so staging and the chunk permutation never change a bit.
 #pragma once
+#include <type_traits>
+
 #include "mfma_tile.h"
 
 namespace lsk {
 
 typedef __attribute__((address_space(3))) void* lds_void_t;
 
-template <int BM, int BN, int WM, int WN, int RING = 4>
+template <int BM, int BN, int WM, int WN, int RING = 4, int BKB = 64>
 struct PPCfg {
   static_assert(WM * WN == 8, "eight waves");
-  static_assert(RING >= 2 && RING <= 5, "ring of 2..5 stages");
+  static_assert(RING >= 3 && RING <= 5, "ring of 3..5 stages (the ping-pong waits one phase after issue)");
   static constexpr int kThreads = 512;
   static constexpr int kBM = BM, kBN = BN, kWM = WM, kWN = WN;
-  static constexpr int kBK = 64;          // bytes of K per stage
+  static_assert(BKB == 64 || BKB == 128, "64- or 128-byte K stages");
+  static constexpr int kBK = BKB;         // bytes of K per stage
+  static constexpr int kChunks = BKB / 16;  // 16-byte chunks per row per stage
+  static constexpr int kKS = BKB / 32;      // 32-byte MFMA K-steps per stage
   static constexpr int kRing = RING;      // LDS stages
   static constexpr int kAhead = RING - 1; // stages loaded ahead of the one being multiplied
   static constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -52,13 +57,21 @@ struct PPCfg {
   typedef uint32_t RowsB[kLB];
 };
 
-// Tile row loaded by thread `tid` in load slot j, and the byte offset within the 64-byte row
-// segment it fetches (the logical chunk that its LDS slot holds).
-template <int THREADS>
+// Tile row loaded by thread `tid` in load slot j of a stage with CHUNKS 16-byte chunks per row,
+// and the byte offset within the row's stage segment that it fetches: the logical chunk that
+// its LDS slot holds.  Chunk c of row r sits in slot c ^ ((r >> SHIFT) & (CHUNKS - 1)), SHIFT
+// chosen so that 16 consecutive rows reading one logical chunk fall in 16 distinct 16-byte
+// bank groups of the 256-byte bank row.
+template <int CHUNKS>
+LSK_DEV int pp_swz(int r) {
+  constexpr int kShift = CHUNKS == 4 ? 2 : 1;
+  return (r >> kShift) & (CHUNKS - 1);
+}
+template <int THREADS, int CHUNKS = 4>
 LSK_DEV void pp_slot(int tid, int j, int& row, int& kbyte) {
   const int p = j * THREADS + tid;  // 16-byte LDS slot index inside the operand's stage
-  row = p >> 2;
-  kbyte = 16 * ((p & 3) ^ ((row >> 2) & 3));
+  row = p / CHUNKS;
+  kbyte = 16 * ((p % CHUNKS) ^ pp_swz<CHUNKS>(row));
 }
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
@@ -82,11 +95,11 @@ LSK_DEV void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BM, int BN, int WM, int WN, int RING>
-LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING>::Acc& acc, __amdgpu_buffer_rsrc_t ra,
-                         const typename PPCfg<BM, BN, WM, WN, RING>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
-                         const typename PPCfg<BM, BN, WM, WN, RING>::RowsB& pb, int K, char* smem) {
-  using C = PPCfg<BM, BN, WM, WN, RING>;
+template <int BM, int BN, int WM, int WN, int RING, int BKB = 64>
+LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __amdgpu_buffer_rsrc_t ra,
+                         const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
+                         const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb, int K, char* smem) {
+  using C = PPCfg<BM, BN, WM, WN, RING, BKB>;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int group = wave >> 2;
   const int wm = wave / WN, wn = wave % WN;
@@ -97,29 +110,31 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING>::Acc& acc, __amdgp
 #pragma unroll
   for (int j = 0; j < C::kLA; ++j) {
     int r;
-    pp_slot<C::kThreads>(tid, j, r, ka[j]);
+    pp_slot<C::kThreads, C::kChunks>(tid, j, r, ka[j]);
   }
 #pragma unroll
   for (int j = 0; j < C::kLB; ++j) {
     int r;
-    pp_slot<C::kThreads>(tid, j, r, kb[j]);
+    pp_slot<C::kThreads, C::kChunks>(tid, j, r, kb[j]);
   }
 
-  // issue this thread's direct-to-LDS loads of stage s
-  auto issue = [&](int s) {
+  // issue this thread's direct-to-LDS loads of stage s; CHECK: the stage may reach past K
+  // (chunks there read zeros), otherwise it lies wholly inside K and needs no test
+  auto issue = [&](int s, auto check) {
+    constexpr bool kCheck = decltype(check)::value;
     char* st = smem + (s % C::kRing) * C::kStage;
     const int k0 = s * C::kBK;
 #pragma unroll
     for (int j = 0; j < C::kLA; ++j) {
       const int kk = k0 + ka[j];
-      const uint32_t off = kk < K ? pa[j] + (uint32_t)kk : kOob;
+      const uint32_t off = (!kCheck || kk < K) ? pa[j] + (uint32_t)kk : kOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t)(st + (j * C::kThreads + wave * 64) * 16), 16, off, 0,
                                                0, 0);
     }
 #pragma unroll
     for (int j = 0; j < C::kLB; ++j) {
       const int kk = k0 + kb[j];
-      const uint32_t off = kk < K ? pb[j] + (uint32_t)kk : kOob;
+      const uint32_t off = (!kCheck || kk < K) ? pb[j] + (uint32_t)kk : kOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rb, (lds_void_t)(st + C::kStageA + (j * C::kThreads + wave * 64) * 16), 16, off, 0, 0, 0);
     }
@@ -127,18 +142,41 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING>::Acc& acc, __amdgp
   constexpr int kPer = C::kLA + C::kLB;  // loads per thread per stage
 
   // fragment addresses: row r = base + (lane & 31), logical chunk 2*ks + (lane >> 5)
-  const int lr = lane & 31, sw = (lr >> 2) & 3, kg = lane >> 5;
+  const int lr = lane & 31, sw = pp_swz<C::kChunks>(lr), kg = lane >> 5;
   const int offA = (wm * C::WTM + lr) * C::kBK, offB = C::kStageA + (wn * C::WTN + lr) * C::kBK;
-  const int slot0 = 16 * ((0 + kg) ^ sw), slot1 = 16 * ((2 + kg) ^ sw);
+  int slot[C::kKS];
+#pragma unroll
+  for (int ks = 0; ks < C::kKS; ++ks) slot[ks] = 16 * ((2 * ks + kg) ^ sw);
 
-  // wait until at most n stages of this thread's loads are outstanding
-  auto wait_stages = [&](int n) {
-    if (n >= 3) wait_vm<3 * kPer>();
-    else if (n == 2) wait_vm<2 * kPer>();
-    else if (n == 1) wait_vm<kPer>();
-    else wait_vm<0>();
+  // one iteration: [next loads] fragments of stage kt; own part of stage kt+1 complete (at
+  // most WAIT younger loads outstanding); barrier; MFMAs; barrier.  WAIT is a compile-time
+  // count: the steady state and each step of the drain get their own copy (no branches).
+  using Chk = std::true_type;
+  using NoChk = std::false_type;
+  auto step = [&](int kt, auto wait_n, bool do_issue, auto check) {
+    constexpr int kWait = decltype(wait_n)::value;
+    if (do_issue) issue(kt + C::kAhead, check);
+    const char* st = smem + (kt % C::kRing) * C::kStage;
+    v4i fa[C::kKS][C::TM], fb[C::kKS][C::TN];
+#pragma unroll
+    for (int ks = 0; ks < C::kKS; ++ks) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) fa[ks][i] = *(const v4i*)(st + offA + i * 32 * C::kBK + slot[ks]);
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) fb[ks][j] = *(const v4i*)(st + offB + j * 32 * C::kBK + slot[ks]);
+    }
+    wait_vm<kWait>();
+    wait_lgkm0();
+    phase_barrier();
+#pragma unroll
+    for (int ks = 0; ks < C::kKS; ++ks)
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma_i8_32(fa[ks][i], fb[ks][j], acc[i][j]);
+    phase_barrier();
   };
-  static_assert(C::kAhead - 1 <= 3, "wait_stages covers up to three younger stages");
+  using W0 = std::integral_constant<int, 0>;
 
   // prologue: stages 0 .. kAhead-1 issued together and all waited for (about one latency,
   // like waiting for stage 0 alone).  A counted wait here could also count a caller's plain
@@ -146,38 +184,29 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING>::Acc& acc, __amdgp
   // so the counted waits there are exact.
 #pragma unroll
   for (int s = 0; s < C::kAhead; ++s)
-    if (s < nk) issue(s);
+    if (s < nk) issue(s, Chk{});
   wait_vm<0>();
   phase_barrier();
   if (group == 1) phase_barrier();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    // ---- memory phase: next loads, fragments of stage kt, own part of stage kt+1 complete
-    if (kt + C::kAhead < nk) issue(kt + C::kAhead);
-    const char* st = smem + (kt % C::kRing) * C::kStage;
-    v4i fa[2][C::TM], fb[2][C::TN];
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
-      fa[0][i] = *(const v4i*)(st + offA + i * 32 * C::kBK + slot0);
-      fa[1][i] = *(const v4i*)(st + offA + i * 32 * C::kBK + slot1);
-    }
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      fb[0][j] = *(const v4i*)(st + offB + j * 32 * C::kBK + slot0);
-      fb[1][j] = *(const v4i*)(st + offB + j * 32 * C::kBK + slot1);
-    }
-    // loads issued after stage kt+1: stages kt+2 .. min(nk-1, kt+kAhead)
-    wait_stages((kt + C::kAhead < nk ? C::kAhead : nk - 1 - kt) - 1);
-    wait_lgkm0();
-    phase_barrier();
-    // ---- compute phase
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma_i8_32(fa[ks][i], fb[ks][j], acc[i][j]);
-    phase_barrier();
+  if (nk >= C::kAhead) {
+    // steady state: every iteration issues a whole stage; kAhead - 1 stages stay younger
+    // (stages below K / kBK lie wholly inside K; only a last partial stage needs the test)
+    using WSteady = std::integral_constant<int, (C::kAhead - 1) * kPer>;
+    const int nfull = K / C::kBK;
+    int kt = 0;
+    for (; kt + C::kAhead < nfull; ++kt) step(kt, WSteady{}, true, NoChk{});
+    for (; kt + C::kAhead < nk; ++kt) step(kt, WSteady{}, true, Chk{});
+    // drain: the last kAhead stages, nothing more to issue
+    step(kt, std::integral_constant<int, (C::kAhead >= 2 ? C::kAhead - 2 : 0) * kPer>{}, false, NoChk{});
+    if (C::kAhead >= 2)
+      step(kt + 1, std::integral_constant<int, (C::kAhead >= 3 ? C::kAhead - 3 : 0) * kPer>{}, false, NoChk{});
+    if (C::kAhead >= 3)
+      step(kt + 2, std::integral_constant<int, (C::kAhead >= 4 ? C::kAhead - 4 : 0) * kPer>{}, false, NoChk{});
+    if (C::kAhead >= 4) step(kt + 3, W0{}, false, NoChk{});
+  } else {
+    // fewer stages than the ring holds: all were issued and waited for in the prologue
+    for (int kt = 0; kt < nk; ++kt) step(kt, W0{}, false, NoChk{});
   }
   if (group == 0) phase_barrier();
 }
