@@ -122,6 +122,51 @@ __device__ __forceinline__ void pp_strip_store(int i, const int32_t* region, con
   }
 }
 
+// Fast epilogue of a whole tile under the v2.1 order, bf16 output, no bias, taken when no output
+// of the tile can be NaN: every ws of the tile finite with |ws| < 2^96 and every asc finite, so
+// fl32(acc) * ws is finite (|acc| < 2^31) and its product with a finite asc is finite or
+// infinite, never NaN.  Per four columns: the two binary32 products per element, gfx950's bf16
+// conversion (round to nearest even, equal to f32_to_bf16 away from NaN), and one 8-byte buffer
+// store at a 32-bit offset from the tile's first output (the host checks the tile span fits).
+// Stores stay 8 bytes wide: 16-byte buffer stores scheduled a few instructions ahead of VALU
+// writes to their data registers were measured on MI355X to store the newer values.
+template <class C>
+__device__ __forceinline__ void pp_strip_store_fast(int i, const int32_t* region, __amdgpu_buffer_rsrc_t ro,
+                                                    int ldo_bytes, const char* smem) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int wm = wave / C::kWN, wn = wave % C::kWN;
+  const float* sc_row = (const float*)(smem + C::kScaleOff);
+  const float* sc_ws = sc_row + C::kBM;
+  constexpr int kQuads = C::WTN / 4;
+  constexpr int kRowStep = 64 / kQuads;  // rows one pass of the wave covers
+  const int c4 = lane % kQuads, r0 = lane / kQuads;
+  const int nl = wn * C::WTN + c4 * 4;
+  const v4f wsq = *(const v4f*)(sc_ws + nl);
+  const int ml0 = wm * C::WTM + i * 32 + r0;
+  const uint32_t off = (uint32_t)(ml0 * ldo_bytes + nl * 2);
+#pragma unroll
+  for (int t = 0; t < 32 / kRowStep; ++t) {
+    const v4i v = *(const v4i*)(region + (r0 + kRowStep * t) * C::kLdc + c4 * 4);
+    const float rv = sc_row[ml0 + kRowStep * t];
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = f32_mul(f32_mul((float)v[k], wsq[k]), rv);
+    const v2u32 u = {pack_bf16x2_nonan(y[0], y[1]), pack_bf16x2_nonan(y[2], y[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(u, ro, off, kRowStep * t * ldo_bytes, 0);
+  }
+}
+
+template <class C, int I>
+__device__ __forceinline__ void pp_epilogue_fast(const typename C::Acc& acc, __amdgpu_buffer_rsrc_t ro, int ldo_bytes,
+                                                 char* smem) {
+  if constexpr (I < C::TM) {
+    int32_t* region = (int32_t*)(smem + wave_id() * C::kStripBytes);
+    lsk::pp_stage_strip<C::TN, C::kLdc>(acc[I], region);
+    pp_strip_store_fast<C>(I, region, ro, ldo_bytes, smem);
+    pp_epilogue_fast<C, I + 1>(acc, ro, ldo_bytes, smem);
+  }
+}
+
 // All strips of the wave's tile, strip index a compile-time constant (the accumulators stay in
 // registers): stage strip I in the wave's LDS region, store it, recurse.
 template <class C, int ORDER, int ODT, bool BIAS, int I>
@@ -208,9 +253,26 @@ __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(co
     sc_b[tid] = s_b;
     sc_ec[tid] = s_ec;
   }
+  // per wave: whether one of its operands rules out the fast epilogue (a NaN output possible)
+  int* sc_flag = (int*)(smem_pp + C::kFlagOff);
+  const bool odd = (tid < BM && !(__builtin_fabsf(s_row) < __builtin_inff())) ||
+                   (tid < BN && !(__builtin_fabsf(s_ws) < 0x1p96f));
+  const bool wave_odd = __builtin_amdgcn_ballot_w64(odd) != 0;
+  if (lane == 0) sc_flag[wave] = wave_odd ? 1 : 0;
   __syncthreads();
   // each wave stages its own 32-row strips, then stores them through the epilogue
   const bool bias = ep.bias != nullptr;
+  if (ep.order == LSK_EPI_V21 && !bias && vec_ok == 2 && m0 + BM <= M && n0 + BN <= N &&
+      ep.out_dtype == LSK_BF16) {
+    const v4i f0 = *(const v4i*)sc_flag, f1 = *(const v4i*)(sc_flag + 4);
+    if (((f0 | f1)[0] | (f0 | f1)[1] | (f0 | f1)[2] | (f0 | f1)[3]) == 0) {
+      const int ldo_bytes = (int)(ep.ldo * 2);
+      char* base = (char*)ep.out + ((int64_t)m0 * ep.ldo + n0) * 2;
+      const __amdgpu_buffer_rsrc_t ro = lsk::make_rsrc(base, (int64_t)(BM - 1) * ldo_bytes + BN * 2);
+      pp_epilogue_fast<C, 0>(acc, ro, ldo_bytes, smem_pp);
+      return;
+    }
+  }
 #define LSK_PP_EPI(O, D, B)                                                        \
   if (ep.order == O && ep.out_dtype == D && bias == B) {                           \
     pp_epilogue<C, O, D, B, 0>(acc, ep, m0, n0, M, N, vec_ok, smem_pp);            \
@@ -749,8 +811,12 @@ static int launch_pp(const int8_t* a, int lda, const int8_t* w, int ldw, int M, 
   }
   const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   LSK_REQUIRE(tiles <= 0x7fffffff, "gemm: too many tiles");
+  // 2: vector stores allowed and a whole tile's output span addressable by 32-bit offsets
+  // (the kernel's fast epilogue)
+  const int64_t esz = (ep.out_dtype == LSK_BF16 || ep.out_dtype == LSK_F16) ? 2 : 4;
+  const int vflag = (vec_ok && (int64_t)(BM - 1) * ep.ldo * esz + BN * esz < 0x7fffffff) ? 2 : vec_ok;
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C::kThreads), C::kSmemBytes, s, a, lda, w, ldw, M, N, K, ep,
-                     vec_ok);
+                     vflag);
   return check_launch(name);
 }
 

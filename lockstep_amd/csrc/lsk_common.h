@@ -17,6 +17,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef short v8s __attribute__((ext_vector_type(8)));
+typedef unsigned int v2u32 __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
 
 // Index of the calling wave in its block, as a wave-uniform (scalar) value: the compiler cannot
 // prove threadIdx.x / 64 uniform by itself, and treats code that depends on it as divergent.
@@ -32,6 +34,16 @@ LSK_DEV uint16_t f32_to_bf16(float f) {
 }
 
 LSK_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Two binary32 values to packed bf16 (a in the low half) with gfx950's conversion instruction:
+// round to nearest even, denormals kept; equal to f32_to_bf16 for every binary32 that is not a
+// NaN (checked exhaustively over all 2^32 patterns on MI355X).  NaN inputs are the caller's to
+// exclude.
+typedef float v2f_t __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf16_t __attribute__((ext_vector_type(2)));
+LSK_DEV uint32_t pack_bf16x2_nonan(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f_t){a, b}, v2bf16_t));
+}
 
 // fl32 -> bf16 -> fl32 (one bf16 rounding, kept in binary32)
 LSK_DEV float bfr(float f) { return bf16_to_f32(f32_to_bf16(f)); }

@@ -48,7 +48,9 @@ struct PPCfg {
   static constexpr int kEpiBytes = 8 * kStripBytes;
   // epilogue operands of the tile: row operand [BM], ws / bias / column exponent [BN] each
   static constexpr int kScaleOff = kMainBytes > kEpiBytes ? kMainBytes : kEpiBytes;
-  static constexpr int kSmemBytes = kScaleOff + (BM + 3 * BN) * 4;
+  // eight per-wave flags of the epilogue's fast-path test follow the operands
+  static constexpr int kFlagOff = kScaleOff + (BM + 3 * BN) * 4;
+  static constexpr int kSmemBytes = kFlagOff + 8 * 4;
   static_assert(BM <= kThreads && BN <= kThreads, "one epilogue operand per thread");
   static_assert(kStageA % (16 * kThreads) == 0 && kStageB % (16 * kThreads) == 0, "tile / threads");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be a multiple of 32");

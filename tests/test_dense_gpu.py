@@ -266,3 +266,59 @@ def test_every_tile_config_is_exact(tile, M, N, K):
         L.call("lsk_gemm_select", -1)
     assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, bias, "bf16"))
     assert np.array_equal(bits(acc), C.int_mm(C.rowquant(x)[0], W8.T))
+
+
+@pytest.mark.parametrize("tile", [1, 3, 4, 12, 13])
+@pytest.mark.parametrize("out", ["bf16", "f32"])
+def test_epilogue_special_scales(tile, out):
+    """Scales that can make outputs infinite or NaN, placed so that some tiles hold none of them
+    (those take the vectorised epilogue) and others do (the general one): every output equal to
+    the oracle's (bf16 NaN as 0x7FC0; binary32 NaN compared as NaN, its payload is the
+    platform's).  The clean tile also holds extreme but NaN-free scales: a subnormal ws and
+    asc, zeros of both signs, ws = 2^95 against asc = 2^100 (infinite outputs)."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import ops
+    say("epilogue special scales", tile, out)
+    r = _rng(11 + tile)
+    M = N = 512
+    K = 256
+    a8 = r.integers(-127, 128, (M, K), dtype=np.int8)
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    a8[7] = 0                                            # an all-zero accumulator row
+    asc = r.uniform(1e-3, 1e-2, M).astype(F32)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    # NaN-free extremes in rows / columns 0..127
+    ws[10] = F32(1e-40)
+    ws[20] = F32(2.0 ** 95)
+    ws[21] = F32(-3.0)
+    asc[30] = F32(2.0 ** 100)
+    asc[40] = F32(1e-41)
+    asc[50] = F32(0.0)
+    asc[51] = F32(-0.0)
+    # scales that rule the fast path out, in rows / columns 384..511
+    ws[400] = np.inf
+    ws[401] = np.nan
+    ws[402] = F32(2.0 ** 100)
+    ws[403] = F32(2.0 ** 96)
+    asc[450] = np.inf
+    asc[451] = np.nan
+    asc[452] = F32(0.0)
+    a8[452] = a8[0]
+    odt = {"bf16": L.LSK_BF16, "f32": L.LSK_F32}[out]
+    L.call("lsk_gemm_select", tile)
+    try:
+        y = ops.gemm(to_dev(a8), to_dev(W8), L.EPI_V21, odt, asc=to_dev(asc), ws=to_dev(ws))
+    finally:
+        L.call("lsk_gemm_select", -1)
+    acc = C.int_mm(a8, W8.T)
+    with np.errstate(invalid="ignore", over="ignore"):
+        ref = C.epilogue_v21(acc, ws, asc, None, out)
+    got = bits(y)
+    if out == "bf16":
+        assert np.array_equal(got, ref)
+    else:
+        gf = got.view(F32)
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(gf), nan)
+        assert np.array_equal(got[~nan], f32_bits(ref)[~nan])
+    assert acc[30, 20] != 0 and np.isinf(C.out_to_f32(ref, out)[30, 20])  # the case is present
