@@ -251,8 +251,11 @@ int lsk_moe_forward(const lsk_moe_args* args, void* stream);
 
 /* Tuning control with no counterpart in the reference: the int8 grouped expert GEMMs of
  * lsk_moe_forward on the 128x128 register-staged tile (0), on the eight-wave ping-pong
- * 128x256 tile (1), or chosen by size (-1, the default: ping-pong once the routed rows reach
- * E x 128).  Results are identical for every choice.  Process-wide. */
+ * 128x256 tile (1), on the grouped GEMV (2: whole weight rows streamed once against up to 8
+ * rows per expert at a time; taken only for int8 experts without rotation, T <= 64 and
+ * H, I <= 4096, the tiles otherwise), or chosen by size (-1, the default: the GEMV where it
+ * applies, ping-pong once the routed rows reach E x 128).  Results are identical for every
+ * choice.  Process-wide. */
 int lsk_moe_select(int variant);
 
 #ifdef __cplusplus

@@ -23,7 +23,7 @@ namespace {
 constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
 constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
 constexpr int kBM = lsk::kMoeBM;
-int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile
+int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV
 
 // ---------------------------------------------------------------- router
 LSK_DEV long long wave_max_ll(long long v) {
@@ -633,6 +633,194 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
   strip(1);
 }
 
+// ---------------------------------------------------------------- decode-sized grouped GEMV
+// One step of the transposing butterfly per level, sizes compile-time so the values stay in
+// registers: with N values left, a lane with bit O set keeps the upper half and adds the
+// partner's (lane ^ O) upper half; the other lane the lower halves.
+template <int N, int O>
+LSK_DEV void wave_xchg_sum(int* v, int lane) {
+  if constexpr (N > 1) {
+    const bool upper = (lane & O) != 0;
+#pragma unroll
+    for (int q = 0; q < N / 2; ++q) {
+      const int send = upper ? v[q] : v[q + N / 2];
+      const int keep = upper ? v[q + N / 2] : v[q];
+      v[q] = keep + __shfl_xor(send, O, 64);
+    }
+    wave_xchg_sum<N / 2, O / 2>(v, lane);
+  }
+}
+
+// Few rows per expert (decode token counts).  A wave owns RPW columns of one expert tile and
+// loads their weight rows whole, once (non-temporal 16-byte loads, all in flight together; MODE
+// 0 reads gate row c and up row N + c of h-column c), then multiplies them with the tile's
+// activation rows MR at a time (v_dot4 into exact int32; the weights stay in registers).  The
+// V = RPW x rows x MR partial sums of a lane are summed over the wave by a transposing
+// butterfly: at offset o a lane keeps half of its values and adds the partner's other half, so
+// after log2(V) steps lane l holds value l / (64 / V) (then plain steps over the rest).  Owner
+// lanes apply the tiled kernels' epilogue steps: MODE 0 writes the bias-added gate and up values
+// (bf16) for the activation-and-requant kernel; MODE 1 the routing-weighted output slot rows.
+template <int MODE, int MR, int NC, int RPW>
+__global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemmArgs a, uint16_t* __restrict__ gu) {
+  constexpr int kRows = MODE == 0 ? 2 : 1;  // weight rows per column
+  constexpr int V = RPW * kRows * MR;       // value index v = (i * MR + m) * kRows + r
+  static_assert(V >= 2 && V <= 64 && (V & (V - 1)) == 0, "a power of two of at most 64 values");
+  constexpr int kRep = 64 / V;  // lanes holding each value after the exchange steps
+  const int cols_blk = 4 * RPW;
+  const int nchunk = (a.N + cols_blk - 1) / cols_blk;
+  const int mt = blockIdx.x / nchunk, ch = blockIdx.x - mt * nchunk;
+  if (mt >= a.tiles[0]) return;
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + kBM);
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int c0 = ch * cols_blk + wave * RPW;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)a.w_ptrs[e], a.w_bytes);
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+  uint32_t koff[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int kk = j * 1024 + lane * 16;
+    koff[j] = kk < a.K ? (uint32_t)kk : lsk::kOob;
+  }
+  v4i w[RPW][kRows][NC];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const int c = c0 + i;
+      const uint32_t ro = c < a.N ? (uint32_t)((MODE == 0 && r ? a.N + c : c) * a.ldw) : lsk::kOob;
+#pragma unroll
+      for (int j = 0; j < NC; ++j)
+        w[i][r][j] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, (ro == lsk::kOob || koff[j] == lsk::kOob) ? lsk::kOob
+                                                                                                   : ro + koff[j],
+                                                       0, 2 /* non-temporal */));
+    }
+  // the value this lane ends with: column vi_i, row vi_m of the chunk, gate (0) or up (1)
+  const int vi = lane / kRep;
+  const int vi_i = vi / (MR * kRows), vi_m = (vi / kRows) % MR, vi_r = vi % kRows;
+  const int c = c0 + vi_i;
+  const bool owner = (lane % kRep) == 0 && vi_r == 0 && c < a.N;
+  const float* ws = (const float*)a.ws_ptrs[e];
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  float ws0 = 0.0f, ws1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+  if (owner) {
+    ws0 = ws[c];
+    if (bias) b0 = bias[c];
+    if (MODE == 0) {
+      ws1 = ws[a.N + c];
+      if (bias) b1 = bias[a.N + c];
+    }
+  }
+  for (int rb = p0; rb < p1; rb += MR) {
+    v4i act[MR][NC];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const int p = rb + m;
+      const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
+#pragma unroll
+      for (int j = 0; j < NC; ++j)
+        act[m][j] = lsk::buf_load16(ra, (src >= 0 && koff[j] != lsk::kOob) ? (uint32_t)(src * a.lda) + koff[j]
+                                                                           : lsk::kOob);
+    }
+    const int p = rb + vi_m;
+    const bool rowok = owner && p < p1;
+    float asc = 0.0f, wt = 0.0f;
+    int dst = 0;
+    if (rowok) {
+      asc = a.a_scale[MODE == 0 ? a.row_tok[p] : p];
+      if (MODE == 1) {
+        wt = a.row_w[p];
+        dst = a.row_dst[p];
+      }
+    }
+    int v[V];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+          int t = 0;
+#pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            t = __builtin_amdgcn_sdot4(act[m][j][0], w[i][r][j][0], t, false);
+            t = __builtin_amdgcn_sdot4(act[m][j][1], w[i][r][j][1], t, false);
+            t = __builtin_amdgcn_sdot4(act[m][j][2], w[i][r][j][2], t, false);
+            t = __builtin_amdgcn_sdot4(act[m][j][3], w[i][r][j][3], t, false);
+          }
+          v[(i * MR + m) * kRows + r] = t;
+        }
+    wave_xchg_sum<V, 32>(v, lane);
+    int tot = v[0];
+#pragma unroll
+    for (int o = kRep / 2; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    const int upv = MODE == 0 ? __shfl_xor(tot, kRep, 64) : 0;
+    if (rowok) {
+      if (MODE == 0) {
+        float yg = bfr(f32_mul(f32_mul((float)tot, ws0), asc));
+        float yu = bfr(f32_mul(f32_mul((float)upv, ws1), asc));
+        if (bias) {
+          yg = bfr(f32_add(yg, b0));
+          yu = bfr(f32_add(yu, b1));
+        }
+        uint16_t* row = gu + (int64_t)p * 2 * a.N;
+        row[c] = f32_to_bf16(yg);
+        row[a.N + c] = f32_to_bf16(yu);
+      } else {
+        float yv = bfr(f32_mul(f32_mul((float)tot, ws0), asc));
+        if (bias) yv = bfr(f32_add(yv, b0));
+        a.y[(int64_t)dst * a.N + c] = f32_to_bf16(f32_mul(wt, yv));
+      }
+    }
+  }
+}
+
+// Decode path after the gate/up GEMV: per row, h = act(gate, up) (the values the tiled kernels
+// store), its |h| maximum (fmaxf from +0, so a NaN is passed over as there), and the row quant
+// of h exactly as moe_requant_kernel does it.  One block per row; I <= 256 * PER.
+template <int PER>
+__global__ __launch_bounds__(256) void moe_act_requant_kernel(const uint16_t* __restrict__ gu,
+                                                              const int32_t* __restrict__ nrows, int I, int act,
+                                                              const int32_t* __restrict__ frac,
+                                                              int8_t* __restrict__ q, float* __restrict__ asc) {
+  __shared__ float red[4];
+  const int p = blockIdx.x;
+  if (p >= *nrows) return;
+  const int tid = threadIdx.x;
+  const uint16_t* g = gu + (int64_t)p * 2 * I;
+  const uint16_t* u = g + I;
+  float hv[PER];
+  float am = 0.0f;
+#pragma unroll
+  for (int t = 0; t < PER; ++t) {
+    const int c = tid + 256 * t;
+    hv[t] = 0.0f;
+    if (c < I) {
+      const float yg = bf16_to_f32(g[c]), yu = bf16_to_f32(u[c]);
+      hv[t] = act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, frac) : lsk::act_swigluoai(yg, yu, frac);
+      am = fmaxf(am, fabsf(hv[t]));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f);
+  if (tid == 0) asc[p] = s;
+#pragma unroll
+  for (int t = 0; t < PER; ++t) {
+    const int c = tid + 256 * t;
+    if (c < I) {
+      const float hb = bf16_to_f32(f32_to_bf16(hv[t]));  // h as the tiled kernels store it
+      const float qv = fminf(fmaxf(rintf(f32_div(hb, s)), -127.0f), 127.0f);
+      q[(int64_t)p * I + c] = (int8_t)(int)qv;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- requant and combine
 // rowquant of the activation output h (bf16 values), with the row maxima from the GEMM.
 __global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __restrict__ h, const uint32_t* __restrict__ amax,
@@ -761,11 +949,14 @@ struct MoeWs {
   float* asch;
   uint16_t* slots;
   float* xrot;
+  uint16_t* gu;  // decode path: bias-added gate and up values [R, 2I] bf16 (T <= kGemvMaxT)
   int64_t bytes;
   int64_t max_tiles;
 };
 
 inline int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
+
+constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
 
 MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt) {
   const int64_t qb = wfmt == 1 ? 2 : 1;  // bytes per quantised activation element
@@ -795,6 +986,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.asch = (float*)take(R * 4);
   w.slots = (uint16_t*)take(R * H * 2);
   w.xrot = rot_blk > 0 ? (float*)take(T * H * 4) : nullptr;
+  w.gu = T <= kGemvMaxT ? (uint16_t*)take(R * 2 * I * 2) : nullptr;
   w.bytes = off;
   return w;
 }
@@ -817,6 +1009,36 @@ int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const
   LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
   hipLaunchKernelGGL(moe_pp_kernel<MODE>, dim3((unsigned)blocks), dim3(512), PPM::kSmemBytes, s, ga);
   return lsk::check_launch(name);
+}
+
+// The grouped GEMV for decode token counts: MR = rows multiplied at once (a power of two >= the
+// token count, at most 8; 4 when K needs four 1 KB sweeps), RPW columns per wave.
+template <int MODE, int MR, int NC>
+int launch_moe_gemv_k(const MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
+  constexpr int RPW = MODE == 0 ? 2 : 4;
+  const int nchunk = (ga.N + 4 * RPW - 1) / (4 * RPW);
+  const int64_t blocks = max_tiles * nchunk;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  hipLaunchKernelGGL((moe_gemv_kernel<MODE, MR, NC, RPW>), dim3((unsigned)blocks), dim3(256), 0, s, ga, gu);
+  return lsk::check_launch(name);
+}
+
+template <int MODE, int MR>
+int launch_moe_gemv_mr(const MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
+  const int nc = (ga.K + 1023) / 1024;
+  if (nc <= 1) return launch_moe_gemv_k<MODE, MR, 1>(ga, max_tiles, gu, s, name);
+  if (nc <= 2) return launch_moe_gemv_k<MODE, MR, 2>(ga, max_tiles, gu, s, name);
+  return launch_moe_gemv_k<MODE, (MR > 4 ? 4 : MR), 4>(ga, max_tiles, gu, s, name);
+}
+
+template <int MODE>
+int launch_moe_gemv(const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint16_t* gu, hipStream_t s,
+                    const char* name) {
+  if (T <= 1) return launch_moe_gemv_mr<MODE, 1>(ga, max_tiles, gu, s, name);
+  if (T <= 2) return launch_moe_gemv_mr<MODE, 2>(ga, max_tiles, gu, s, name);
+  if (T <= 4) return launch_moe_gemv_mr<MODE, 4>(ga, max_tiles, gu, s, name);
+  return launch_moe_gemv_mr<MODE, 8>(ga, max_tiles, gu, s, name);
 }
 
 template <int MODE>
@@ -846,7 +1068,7 @@ extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t 
 }
 
 extern "C" int lsk_moe_select(int variant) {
-  LSK_REQUIRE(variant >= -1 && variant <= 1, "lsk_moe_select: variant %d not in [-1, 1]", variant);
+  LSK_REQUIRE(variant >= -1 && variant <= 2, "lsk_moe_select: variant %d not in [-1, 2]", variant);
   g_moe_force = variant;
   return LSK_OK;
 }
@@ -895,6 +1117,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   // the ping-pong grouped GEMM once experts average a full 128-row tile or more; the 128x128
   // register-staged tile below that (decode-sized token counts)
   const bool use_pp = g_moe_force >= 0 ? g_moe_force == 1 : R >= (int64_t)E * kBM;
+  // the grouped GEMV for decode token counts (whole weight rows streamed once per tile)
+  const bool use_gemv = !mx && rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true) &&
+                        H <= 4096 && I <= 4096;
 
   int rc;
   if (rb > 0) {
@@ -951,12 +1176,24 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g1.lds = a->lds13;
   if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (use_gemv) {
+    if ((rc = launch_moe_gemv<0>(g1, w.max_tiles, T, w.gu, s, "moe_gemv_kernel<gate_up>"))) return rc;
   } else if (use_pp) {
     if ((rc = launch_moe_pp<0>(g1, w.max_tiles, s, "moe_pp_kernel<gate_up>"))) return rc;
   } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
     return rc;
   }
-  if (rb > 0) {
+  if (use_gemv) {
+    const int per = (int)((I + 255) / 256);
+    const dim3 grid((unsigned)R), blk(256);
+    if (per <= 4) hipLaunchKernelGGL(moe_act_requant_kernel<4>, grid, blk, 0, s, w.gu, w.offs + E, (int)I, a->act,
+                                     a->frac, w.qh, w.asch);
+    else if (per <= 8) hipLaunchKernelGGL(moe_act_requant_kernel<8>, grid, blk, 0, s, w.gu, w.offs + E, (int)I,
+                                          a->act, a->frac, w.qh, w.asch);
+    else hipLaunchKernelGGL(moe_act_requant_kernel<16>, grid, blk, 0, s, w.gu, w.offs + E, (int)I, a->act, a->frac,
+                            w.qh, w.asch);
+    if ((rc = lsk::check_launch("moe_act_requant_kernel"))) return rc;
+  } else if (rb > 0) {
     hipLaunchKernelGGL(moe_rot_requant_kernel, dim3((unsigned)R), dim3(256), (size_t)I * 4, s, w.h, w.offs + E, (int)I,
                        rb, a->rot_scale, w.qh, w.asch);
     if ((rc = lsk::check_launch("moe_rot_requant_kernel"))) return rc;
@@ -989,6 +1226,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g2.lds = a->lds2;
   if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (use_gemv) {
+    if ((rc = launch_moe_gemv<1>(g2, w.max_tiles, T, nullptr, s, "moe_gemv_kernel<down>"))) return rc;
   } else if (use_pp) {
     if ((rc = launch_moe_pp<1>(g2, w.max_tiles, s, "moe_pp_kernel<down>"))) return rc;
   } else if ((rc = launch_moe_gemm<1>(g2, w.max_tiles, (int)((H + 127) / 128), s, "moe_gemm_kernel<down>"))) {

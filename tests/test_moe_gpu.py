@@ -160,10 +160,11 @@ def test_moe_multi_chunk_dispatch(T, E, k):
     _run_case(T, E, k, 128, 64, seed=11 + T)
 
 
-@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("variant", [0, 1, 2])
 def test_moe_grouped_gemm_variants(variant):
-    """Both grouped-GEMM tiles (register-staged 128x128, ping-pong 128x256) give the oracle's bits:
-    skewed routing with multi-tile experts, empty experts, a bias and SwiGLU-OAI."""
+    """Every grouped-GEMM kernel (register-staged 128x128 tile, ping-pong 128x256 tile, the
+    decode GEMV) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
+    their rows eight at a time), empty experts, a bias and SwiGLU-OAI."""
     from lockstep_amd import _lib as L
     L.call("lsk_moe_select", variant)
     try:
@@ -172,6 +173,14 @@ def test_moe_grouped_gemm_variants(variant):
         _run_case(5, 16, 4, 256, 128, seed=15)
     finally:
         L.call("lsk_moe_select", -1)
+
+
+@pytest.mark.parametrize("T", [1, 3, 12])
+def test_moe_gemv_wide_k(T):
+    """The decode GEMV with K beyond one 1 KB lane sweep and not a multiple of it (H = 2064:
+    three sweeps, the last partial; I = 1104: two), at one, up to four and up to eight rows per
+    expert at a time."""
+    _run_case(T, 8, 3, 2064, 1104, seed=21 + T)
 
 
 def test_moe_multi_chunk_out_of_range_entries():
