@@ -34,14 +34,16 @@ LSK_DEV long long wave_max_ll(long long v) {
   return v;
 }
 
-// One wave per token; lane l owns experts l, l + 64, ...
+// One wave per token; lane l owns experts l, l + 64, ... (EPL per lane, E <= 64 * EPL).  The
+// reference's ranking key s * E + (E - 1 - e) orders like the pair (s, E - 1 - e), so the key is
+// kept as s << 32 | (E - 1 - e) and decoded with shifts.
+template <int EPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ g, int gdt, int64_t ldg, int T,
                                                           int E, int k, int renorm, const int32_t* __restrict__ tab,
                                                           int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  constexpr int EPL = 16;  // experts per lane, E <= 1024
   float gv[EPL];
   float m = -__builtin_inff();
 #pragma unroll
@@ -56,13 +58,11 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
   }
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
   long long key[EPL];
-  int sc[EPL];
   int s_all = 0;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
     key[j] = -1;
-    sc[j] = 0;
     if (e < E) {
       const float v = rintf(f32_mul(m - gv[j], kRouterC));
       int s = 0;
@@ -70,9 +70,8 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
         const int d = v > 0.0f ? (int)v : 0;
         s = tab[(d >> 13) & 8191] >> (d >> 26);
       }
-      sc[j] = s;
       s_all += s;
-      key[j] = (long long)s * E + (E - 1 - e);
+      key[j] = ((long long)s << 32) | (long long)(unsigned)(E - 1 - e);
     }
   }
   for (int o = 32; o > 0; o >>= 1) s_all += __shfl_xor(s_all, o, 64);
@@ -83,10 +82,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
 #pragma unroll
     for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
     best = wave_max_ll(best);
-    const int e = (E - 1) - (int)(best % E);
-    const int s = (int)(best / E);
-    s_sum += s;
-    if (lane == r) s_sel_mine = s;
+    const int e = (E - 1) - (int)(unsigned)(best & 0xffffffffLL);
+    const int sc = (int)(best >> 32);
+    s_sum += sc;
+    if (lane == r) s_sel_mine = sc;
     if (lane == 0) idx_out[(int64_t)t * k + r] = e;
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
@@ -159,37 +158,53 @@ LSK_DEV void expert_offsets_and_tiles(const int32_t* cnt, int E, int32_t* offs, 
   }
 }
 
-// Place the rows of the 256-token chunk c0 .. c0+255: p = base[e] + (rank of the token among the
-// chunk's tokens routed to e); base (LDS or global) is advanced by the caller.  mask: E x 8 words.
-LSK_DEV void place_chunk(const int64_t* __restrict__ idx, const uint16_t* __restrict__ w, int T, int k, int E, int c0,
-                         const int32_t* base, uint32_t* mask, int32_t* __restrict__ row_tok,
-                         int32_t* __restrict__ row_dst, float* __restrict__ row_w) {
+// The routing entries of the 256-token chunk c0 .. c0+255 as expert ids in LDS (-1 outside
+// [0, E)), and their bf16 weights: one coalesced pass, so the steps below read LDS only.
+LSK_DEV void load_chunk_routes(const int64_t* __restrict__ idx, const uint16_t* __restrict__ w, int T, int k, int E,
+                               int c0, int32_t* ids, uint16_t* wts) {
+  const int n = (T - c0 < 256 ? T - c0 : 256) * k;
+  const int64_t* src = idx + (int64_t)c0 * k;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const int64_t e = src[i];
+    ids[i] = (e >= 0 && e < E) ? (int)e : -1;
+    if (wts) wts[i] = w[(int64_t)c0 * k + i];
+  }
+  __syncthreads();
+}
+
+// Place the rows of the 256-token chunk c0 .. c0+255 (its routes in ids / wts, as
+// load_chunk_routes leaves them): p = base[e] + (rank of the token among the chunk's tokens
+// routed to e); base (LDS or global) is advanced by the caller.  mask: E x 8 words.
+LSK_DEV void place_chunk(const int32_t* ids, const uint16_t* wts, int T, int k, int E, int c0, const int32_t* base,
+                         uint32_t* mask, int32_t* __restrict__ row_tok, int32_t* __restrict__ row_dst,
+                         float* __restrict__ row_w) {
   const int tid = threadIdx.x;
   for (int i = tid; i < E * 8; i += 256) mask[i] = 0;
   __syncthreads();
   const int t = c0 + tid;
+  const int32_t* my = ids + tid * k;
   if (t < T) {
     for (int j = 0; j < k; ++j) {
-      const int64_t e = idx[(int64_t)t * k + j];
-      if (e >= 0 && e < E) atomicOr(&mask[e * 8 + (tid >> 5)], 1u << (tid & 31));
+      const int e = my[j];
+      if (e >= 0) atomicOr(&mask[e * 8 + (tid >> 5)], 1u << (tid & 31));
     }
   }
   __syncthreads();
   if (t < T) {
     for (int j = 0; j < k; ++j) {
-      const int64_t e = idx[(int64_t)t * k + j];
-      if (!(e >= 0 && e < E)) continue;
+      const int e = my[j];
+      if (e < 0) continue;
       int rank = __popc(mask[e * 8 + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
       for (int wd = 0; wd < (tid >> 5); ++wd) rank += __popc(mask[e * 8 + wd]);
       const int p = base[e] + rank;
       int slot = 0;  // rank of e among the token's experts, ascending
       for (int j2 = 0; j2 < k; ++j2) {
-        const int64_t e2 = idx[(int64_t)t * k + j2];
-        if (e2 >= 0 && e2 < E && e2 < e) ++slot;
+        const int e2 = my[j2];
+        if (e2 >= 0 && e2 < e) ++slot;
       }
       row_tok[p] = t;
       row_dst[p] = t * k + slot;
-      row_w[p] = bf16_to_f32(w[(int64_t)t * k + j]);
+      row_w[p] = bf16_to_f32(wts[tid * k + j]);
     }
   }
   __syncthreads();
@@ -197,15 +212,14 @@ LSK_DEV void place_chunk(const int64_t* __restrict__ idx, const uint16_t* __rest
 
 // Tokens routed to each expert in a 256-token chunk (LDS cnt[E]), and each token's number of
 // valid routes; also zeroes zero_n words of zero_buf (the per-row |h| maxima) grid-wide.
-LSK_DEV void count_chunk(const int64_t* __restrict__ idx, int T, int k, int E, int c0, int32_t* cnt,
-                         int32_t* __restrict__ tok_cnt) {
+LSK_DEV void count_chunk(const int32_t* ids, int T, int k, int c0, int32_t* cnt, int32_t* __restrict__ tok_cnt) {
   const int tid = threadIdx.x;
   const int t = c0 + tid;
   if (t < T) {
     int nv = 0;
     for (int j = 0; j < k; ++j) {
-      const int64_t e = idx[(int64_t)t * k + j];
-      if (e >= 0 && e < E) {
+      const int e = ids[tid * k + j];
+      if (e >= 0) {
         atomicAdd(&cnt[e], 1);
         ++nv;
       }
@@ -223,34 +237,37 @@ __global__ __launch_bounds__(256) void moe_dispatch_small_kernel(const int64_t* 
                                                                  float* __restrict__ row_w,
                                                                  int32_t* __restrict__ tok_cnt,
                                                                  uint32_t* __restrict__ zero_buf, int64_t zero_n) {
-  extern __shared__ int32_t dsm[];
+  extern __shared__ int32_t dsm[];  // cnt [E], base [E + 1], mask [8 E], ids [256 k], wts [256 k] u16
   __shared__ int tmp[4];
   int32_t* cnt = dsm;
   int32_t* base = dsm + E;
-  uint32_t* mask = (uint32_t*)(dsm + 2 * E);
+  uint32_t* mask = (uint32_t*)(dsm + 2 * E + 1);
+  int32_t* ids = dsm + 10 * E + 1;
+  uint16_t* wts = (uint16_t*)(ids + 256 * k);
   const int tid = threadIdx.x;
   for (int64_t i = tid; i < zero_n; i += 256) zero_buf[i] = 0u;
   for (int e = tid; e < E; e += 256) cnt[e] = 0;
-  __syncthreads();
-  count_chunk(idx, T, k, E, 0, cnt, tok_cnt);
+  load_chunk_routes(idx, w, T, k, E, 0, ids, wts);  // ends with a barrier
+  count_chunk(ids, T, k, 0, cnt, tok_cnt);
   __syncthreads();
   expert_offsets_and_tiles<256>(cnt, E, base, tiles, tmp);
   __syncthreads();
   for (int e = tid; e <= E; e += 256) offs[e] = base[e];  // base[E] = all rows
   __syncthreads();
-  place_chunk(idx, w, T, k, E, 0, base, mask, row_tok, row_dst, row_w);
+  place_chunk(ids, wts, T, k, E, 0, base, mask, row_tok, row_dst, row_w);
 }
 
 // Large T, step 1: per-chunk expert counts ccnt[chunk][E].
 __global__ __launch_bounds__(256) void moe_count_kernel(const int64_t* __restrict__ idx, int T, int k, int E,
                                                         int32_t* __restrict__ ccnt, int32_t* __restrict__ tok_cnt,
                                                         uint32_t* __restrict__ zero_buf, int64_t zero_n) {
-  extern __shared__ int32_t cnt[];
+  extern __shared__ int32_t cnt[];  // [E], then the chunk's ids [256 k]
+  int32_t* ids = cnt + E;
   const int tid = threadIdx.x;
   for (int64_t i = (int64_t)blockIdx.x * 256 + tid; i < zero_n; i += (int64_t)gridDim.x * 256) zero_buf[i] = 0u;
   for (int e = tid; e < E; e += 256) cnt[e] = 0;
-  __syncthreads();
-  count_chunk(idx, T, k, E, blockIdx.x * 256, cnt, tok_cnt);
+  load_chunk_routes(idx, nullptr, T, k, E, blockIdx.x * 256, ids, nullptr);  // ends with a barrier
+  count_chunk(ids, T, k, blockIdx.x * 256, cnt, tok_cnt);
   __syncthreads();
   for (int e = tid; e < E; e += 256) ccnt[(int64_t)blockIdx.x * E + e] = cnt[e];
 }
@@ -284,8 +301,11 @@ __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restric
                                                         int T, int k, int E, const int32_t* __restrict__ cbase,
                                                         int32_t* __restrict__ row_tok, int32_t* __restrict__ row_dst,
                                                         float* __restrict__ row_w) {
-  extern __shared__ uint32_t mask[];  // [E][8]
-  place_chunk(idx, w, T, k, E, blockIdx.x * 256, cbase + (int64_t)blockIdx.x * E, mask, row_tok, row_dst, row_w);
+  extern __shared__ uint32_t mask[];  // [E][8], then the chunk's ids [256 k] and weights [256 k] u16
+  int32_t* ids = (int32_t*)(mask + 8 * E);
+  uint16_t* wts = (uint16_t*)(ids + 256 * k);
+  load_chunk_routes(idx, w, T, k, E, blockIdx.x * 256, ids, wts);
+  place_chunk(ids, wts, T, k, E, blockIdx.x * 256, cbase + (int64_t)blockIdx.x * E, mask, row_tok, row_dst, row_w);
 }
 
 __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x, int64_t n, float* __restrict__ y) {
@@ -1062,8 +1082,16 @@ extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t 
   if (T == 0) return LSK_OK;
   LSK_REQUIRE(g && tab && idx && w_bf16, "lsk_router_topk: null pointer");
   LSK_REQUIRE(T <= 0x7fffffffLL * 4, "lsk_router_topk: T too large");
-  hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, (hipStream_t)stream, g, g_dtype,
-                     ldg, (int)T, (int)E, k, renormalize, tab, idx, w_bf16);
+  const dim3 grid((unsigned)((T + 3) / 4)), blk(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (E <= 64) hipLaunchKernelGGL(router_topk_kernel<1>, grid, blk, 0, s, g, g_dtype, ldg, (int)T, (int)E, k,
+                                  renormalize, tab, idx, w_bf16);
+  else if (E <= 128) hipLaunchKernelGGL(router_topk_kernel<2>, grid, blk, 0, s, g, g_dtype, ldg, (int)T, (int)E, k,
+                                        renormalize, tab, idx, w_bf16);
+  else if (E <= 256) hipLaunchKernelGGL(router_topk_kernel<4>, grid, blk, 0, s, g, g_dtype, ldg, (int)T, (int)E, k,
+                                        renormalize, tab, idx, w_bf16);
+  else hipLaunchKernelGGL(router_topk_kernel<16>, grid, blk, 0, s, g, g_dtype, ldg, (int)T, (int)E, k, renormalize,
+                          tab, idx, w_bf16);
   return lsk::check_launch("router_topk_kernel");
 }
 
@@ -1136,21 +1164,34 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     rc = lsk_rowquant(a->x, LSK_BF16, T, H, H, w.qx, H, w.ascx, stream);
   }
   if (rc) return rc;
-  // dispatch (and the zeroing of the per-row |h| maxima, which the gate/up GEMM raises)
+  // dispatch (and the zeroing of the per-row |h| maxima, which the gate/up GEMM raises); the
+  // routes of a 256-token chunk are staged in LDS (up to 88 KB at E = 1024, k = 32)
+  static bool dispatch_lds = false;
+  if (!dispatch_lds) {
+    for (const void* f : {(const void*)moe_dispatch_small_kernel, (const void*)moe_count_kernel,
+                          (const void*)moe_place_kernel})
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess) {
+        lsk::set_error("lsk_moe_forward: cannot reserve LDS for the dispatch");
+        return LSK_ERR_HIP;
+      }
+    dispatch_lds = true;
+  }
   const int64_t nchunks = (T + 255) / 256;
   if (nchunks == 1) {
-    const size_t dsm = (size_t)(2 * E + 8 * E) * 4;
+    const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
     hipLaunchKernelGGL(moe_dispatch_small_kernel, dim3(1), dim3(256), dsm, s, a->idx, a->w, (int)T, k, (int)E, w.offs,
                        w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, R);
     if ((rc = lsk::check_launch("moe_dispatch_small_kernel"))) return rc;
   } else {
-    hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 4, s, a->idx, (int)T, k,
+    hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 4 + (size_t)256 * k * 4, s,
+                       a->idx, (int)T, k,
                        (int)E, w.ccnt, w.tok_cnt, w.h_amax, R);
     if ((rc = lsk::check_launch("moe_count_kernel"))) return rc;
     hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), (size_t)E * 4, s, w.ccnt, (int)nchunks, (int)E, w.cbase,
                        w.offs, w.tiles);
     if ((rc = lsk::check_launch("moe_scan_kernel"))) return rc;
-    hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 8 * 4, s, a->idx, a->w,
+    hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 8 * 4 + (size_t)256 * k * 6,
+                       s, a->idx, a->w,
                        (int)T, k, (int)E, w.cbase, w.row_tok, w.row_dst, w.row_w);
     if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
   }

@@ -64,7 +64,7 @@ def test_fwht_parity(blk):
 
 
 # ------------------------------------------------------------------ router
-@pytest.mark.parametrize("E,k", [(8, 2), (32, 4), (128, 8), (1000, 7)])
+@pytest.mark.parametrize("E,k", [(8, 2), (32, 4), (64, 6), (128, 8), (200, 8), (1000, 7)])
 @pytest.mark.parametrize("renorm", [True, False])
 def test_router_parity(E, k, renorm):
     from lockstep_amd import moe_ref as MR
