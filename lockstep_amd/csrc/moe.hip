@@ -1146,8 +1146,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   // register-staged tile below that (decode-sized token counts)
   const bool use_pp = g_moe_force >= 0 ? g_moe_force == 1 : R >= (int64_t)E * kBM;
   // the grouped GEMV for decode token counts (whole weight rows streamed once per tile)
-  const bool use_gemv = !mx && rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true) &&
-                        H <= 4096 && I <= 4096;
+  const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
+  const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096;
+  const bool use_mx_gemv = gemv_ok && mx && H <= 8192 && I <= 8192;
 
   int rc;
   if (rb > 0) {
@@ -1158,7 +1159,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::check_launch("widen_bf16_kernel"))) return rc;
     if ((rc = lsk_fwht_blocks(w.xrot, T, H, H, rb, a->rot_scale, w.xrot, H, stream))) return rc;
     rc = lsk_rowquant(w.xrot, LSK_F32, T, H, H, w.qx, H, w.ascx, stream);
-  } else if (mx) {
+  } else if (mx && !use_mx_gemv) {
     rc = lsk::launch_rowquant_bf16(a->x, T, H, (uint16_t*)w.qx, w.ascx, s);
   } else {
     rc = lsk_rowquant(a->x, LSK_BF16, T, H, H, w.qx, H, w.ascx, stream);
@@ -1215,7 +1216,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g1.h = w.h;
   g1.h_amax = w.h_amax;
   g1.lds = a->lds13;
-  if (mx) {
+  if (use_mx_gemv) {
+    if ((rc = lsk::launch_moe_mx_gemv(0, g1, w.max_tiles, T, a->mx_safe, w.gu, s))) return rc;
+  } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<0>(g1, w.max_tiles, T, w.gu, s, "moe_gemv_kernel<gate_up>"))) return rc;
@@ -1224,14 +1227,16 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
     return rc;
   }
-  if (use_gemv) {
+  if (use_gemv || use_mx_gemv) {
     const int per = (int)((I + 255) / 256);
     const dim3 grid((unsigned)R), blk(256);
     if (per <= 4) hipLaunchKernelGGL(moe_act_requant_kernel<4>, grid, blk, 0, s, w.gu, w.offs + E, (int)I, a->act,
                                      a->frac, w.qh, w.asch);
     else if (per <= 8) hipLaunchKernelGGL(moe_act_requant_kernel<8>, grid, blk, 0, s, w.gu, w.offs + E, (int)I,
                                           a->act, a->frac, w.qh, w.asch);
-    else hipLaunchKernelGGL(moe_act_requant_kernel<16>, grid, blk, 0, s, w.gu, w.offs + E, (int)I, a->act, a->frac,
+    else if (per <= 16) hipLaunchKernelGGL(moe_act_requant_kernel<16>, grid, blk, 0, s, w.gu, w.offs + E, (int)I,
+                                           a->act, a->frac, w.qh, w.asch);
+    else hipLaunchKernelGGL(moe_act_requant_kernel<32>, grid, blk, 0, s, w.gu, w.offs + E, (int)I, a->act, a->frac,
                             w.qh, w.asch);
     if ((rc = lsk::check_launch("moe_act_requant_kernel"))) return rc;
   } else if (rb > 0) {
@@ -1265,7 +1270,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g2.row_dst = w.row_dst;
   g2.y = w.slots;
   g2.lds = a->lds2;
-  if (mx) {
+  if (use_mx_gemv) {
+    if ((rc = lsk::launch_moe_mx_gemv(1, g2, w.max_tiles, T, a->mx_safe, nullptr, s))) return rc;
+  } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<1>(g2, w.max_tiles, T, nullptr, s, "moe_gemv_kernel<down>"))) return rc;

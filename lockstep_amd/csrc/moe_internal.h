@@ -35,6 +35,11 @@ struct MoeGemmArgs {
 // MXFP4 grouped GEMMs (mode 0: gate/up + activation; 1: down + routing weight).
 int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, hipStream_t s);
 
+// Decode-sized MX expert GEMV over int8 activation rows (mode 0: bias-added gate / up values into
+// gu [R, 2N] bf16; mode 1: the routing-weighted slot rows), for token counts up to 64.
+int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,
+                       hipStream_t s);
+
 // Row quant emitting the int8 values as bf16 (the MX GEMM's operand form).
 int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, float* asc, hipStream_t s);
 

@@ -333,6 +333,207 @@ int launch_dense(const int8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, co
   return lsk::check_launch("mx_gemm_kernel");
 }
 
+// ---------------------------------------------------------------- decode-sized grouped MX GEMV
+// Doubled E2M1 mantissas m2 (0, 1, 2, 3, 4, 6, 8, 12; codes 8..15 negated) as int8 for the four
+// codes (0..15) in the bytes of c: two byte-table lookups (v_perm_b32) and a sign select.
+LSK_DEV uint32_t m2x4_from_codes(uint32_t c) {
+  const uint32_t lo3 = c & 0x07070707u;
+  const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, lo3);
+  const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, lo3);
+  // selector 12 gives 0x00, 13 gives 0xFF: a byte mask from each code's sign bit
+  const uint32_t msk = __builtin_amdgcn_perm(0u, 0u, ((c >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
+  return (neg & msk) | (pos & ~msk);
+}
+
+// Decode-sized MX expert GEMV.  Lane l owns MX block b = l + 64 j (j < NCH) of every weight row
+// the wave streams: its 16 code bytes and its exponent byte, loaded coalesced.  The codes are
+// decoded once per row to int8 m2 (even / odd elements in separate words), and each block sum
+// s_b = sum a * m2 over the block's 32 elements is exact in int32 (v_dot4 against the
+// activation bytes split the same way).  The block sums go to LDS, and one lane per (row,
+// column) then runs the contract's ordered update acc = fl32(acc + s_b * 2^(k_b - 128)) over
+// the blocks in ascending order from +0 (one FMA, exact product; SAFE: multiply, then add).
+// MODE 0: gate row c and up row N + c, bias-added bfr values into gu for the activation-and-
+// requant kernel; MODE 1: bfr(w * y) into the token's slot row.  Activations are int8 rows.
+template <int MODE, int MR, int NCH, int RPW, bool SAFE>
+__global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu) {
+  constexpr int kRows = MODE == 0 ? 2 : 1;
+  constexpr int V = MR * RPW * kRows;  // chains per row chunk, q = (m * RPW + i) * kRows + r
+  static_assert(V <= 64, "one lane per chain");
+  constexpr int kB = 64 * NCH;          // blocks a wave covers
+  constexpr int kSbStride = kB + 4;     // int32 per chain row in LDS (16-byte aligned, skewed banks)
+  constexpr int kWaveBytes = V * kSbStride * 4 + RPW * kRows * kB;
+  extern __shared__ __attribute__((aligned(16))) char gemv_smem[];
+  const int cols_blk = 4 * RPW;
+  const int nchunk = (a.N + cols_blk - 1) / cols_blk;
+  const int mt = blockIdx.x / nchunk, ch = blockIdx.x - mt * nchunk;
+  if (mt >= a.tiles[0]) return;
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int nb = a.K / 32;
+  const int c0 = ch * cols_blk + wave * RPW;
+  const int nw = MODE == 0 ? 2 * a.N : a.N;  // weight rows of the expert
+  int32_t* sb = (int32_t*)(gemv_smem + wave * kWaveBytes);
+  uint8_t* ex = (uint8_t*)(sb + V * kSbStride);
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)a.w_ptrs[e], (int64_t)nw * a.ldw);
+  const __amdgpu_buffer_rsrc_t rsc = lsk::make_rsrc((const void*)a.ws_ptrs[e], (int64_t)nw * a.lds);
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+
+  // the wave's weight rows: codes decoded to m2 (even elements in lo[w], odd in hi[w] of each
+  // 8-element word w), exponents parked in LDS
+  uint32_t lo[RPW][kRows][NCH][4], hi[RPW][kRows][NCH][4];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const int c = c0 + i;
+      const int wr = MODE == 0 && r ? a.N + c : c;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int b = lane + 64 * j;
+        const bool in = c < a.N && b < nb;
+        const v4i codes = lsk::buf_load16(rw, in ? (uint32_t)(wr * a.ldw + b * 16) : lsk::kOob);
+        const uint32_t kx = __builtin_amdgcn_raw_buffer_load_b8(rsc, in ? (int)(wr * a.lds + b) : (int)lsk::kOob, 0, 0);
+        ex[(i * kRows + r) * kB + b] = (uint8_t)kx;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t x = (uint32_t)codes[w];
+          lo[i][r][j][w] = m2x4_from_codes(x & 0x0F0F0F0Fu);
+          hi[i][r][j][w] = m2x4_from_codes((x >> 4) & 0x0F0F0F0Fu);
+        }
+      }
+    }
+  // the chain this lane runs (lanes >= V idle in that phase)
+  const int q = lane;
+  const int q_m = q / (RPW * kRows), q_i = (q / kRows) % RPW, q_r = q % kRows;
+  const int c = c0 + q_i;
+  const bool chain = q < V;
+  const bool owner = chain && q_r == 0 && c < a.N;
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  float b0 = 0.0f, b1 = 0.0f;
+  if (owner && bias) {
+    b0 = bias[c];
+    if (MODE == 0) b1 = bias[a.N + c];
+  }
+  for (int rb = p0; rb < p1; rb += MR) {
+    // activation bytes of the lane's blocks, split into even / odd elements like the codes
+    uint32_t ae[MR][NCH][4], ao[MR][NCH][4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const int p = rb + m;
+      const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int b = lane + 64 * j;
+        const bool in = src >= 0 && b < nb;
+        const uint32_t off = in ? (uint32_t)(src * a.lda + b * 32) : lsk::kOob;
+        const v4i x0 = lsk::buf_load16(ra, off);
+        const v4i x1 = lsk::buf_load16(ra, in ? off + 16 : lsk::kOob);
+        const uint32_t d[8] = {(uint32_t)x0[0], (uint32_t)x0[1], (uint32_t)x0[2], (uint32_t)x0[3],
+                               (uint32_t)x1[0], (uint32_t)x1[1], (uint32_t)x1[2], (uint32_t)x1[3]};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          ae[m][j][w] = __builtin_amdgcn_perm(d[2 * w + 1], d[2 * w], 0x06040200u);
+          ao[m][j][w] = __builtin_amdgcn_perm(d[2 * w + 1], d[2 * w], 0x07050301u);
+        }
+      }
+    }
+    const int p = rb + q_m;
+    const bool rowok = owner && p < p1;
+    float asc = 0.0f, wt = 0.0f;
+    int dst = 0;
+    if (rowok) {
+      asc = a.a_scale[MODE == 0 ? a.row_tok[p] : p];
+      if (MODE == 1) {
+        wt = a.row_w[p];
+        dst = a.row_dst[p];
+      }
+    }
+    // exact block sums into LDS
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+          for (int j = 0; j < NCH; ++j) {
+            int t = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              t = __builtin_amdgcn_sdot4((int)ae[m][j][w], (int)lo[i][r][j][w], t, false);
+              t = __builtin_amdgcn_sdot4((int)ao[m][j][w], (int)hi[i][r][j][w], t, false);
+            }
+            sb[((m * RPW + i) * kRows + r) * kSbStride + lane + 64 * j] = t;
+          }
+    // the ordered update, one chain per lane (LDS written and read by this wave only: in order)
+    float acc = 0.0f;
+    if (chain) {
+      const int32_t* srow = sb + q * kSbStride;
+      const uint8_t* erow = ex + (q_i * kRows + q_r) * kB;
+      for (int b = 0; b < nb; ++b) {
+        const float sc = pow2f((int)erow[b] - 128);
+        acc = SAFE ? f32_add(acc, f32_mul((float)srow[b], sc)) : __builtin_fmaf((float)srow[b], sc, acc);
+      }
+    }
+    const float accu = MODE == 0 ? __shfl_down(acc, 1, 64) : 0.0f;  // the up chain sits in lane q + 1
+    if (rowok) {
+      if (MODE == 0) {
+        float yg = bfr(f32_mul(acc, asc));
+        float yu = bfr(f32_mul(accu, asc));
+        if (bias) {
+          yg = bfr(f32_add(yg, b0));
+          yu = bfr(f32_add(yu, b1));
+        }
+        uint16_t* row = gu + (int64_t)p * 2 * a.N;
+        row[c] = f32_to_bf16(yg);
+        row[a.N + c] = f32_to_bf16(yu);
+      } else {
+        float yv = bfr(f32_mul(acc, asc));
+        if (bias) yv = bfr(f32_add(yv, b0));
+        a.y[(int64_t)dst * a.N + c] = f32_to_bf16(f32_mul(wt, yv));
+      }
+    }
+  }
+}
+
+template <int MODE, int MR, int NCH, bool SAFE>
+int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
+  constexpr int RPW = MODE == 0 ? 2 : 4;
+  constexpr int kRows = MODE == 0 ? 2 : 1;
+  constexpr int V = MR * RPW * kRows;
+  constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH);
+  static bool attr = false;
+  auto kern = moe_mx_gemv_kernel<MODE, MR, NCH, RPW, SAFE>;
+  if (!attr) {
+    if (int rc = reserve_lds(kern, smem, name)) return rc;
+    attr = true;
+  }
+  const int nchunk = (ga.N + 4 * RPW - 1) / (4 * RPW);
+  const int64_t blocks = max_tiles * nchunk;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), smem, s, ga, gu);
+  return lsk::check_launch(name);
+}
+
+template <int MODE, int MR, bool SAFE>
+int launch_mx_gemv_mr(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
+  const int nch = (ga.K / 32 + 63) / 64;
+  if (nch <= 1) return launch_mx_gemv_k<MODE, MR, 1, SAFE>(ga, max_tiles, gu, s, name);
+  if (nch <= 2) return launch_mx_gemv_k<MODE, MR, 2, SAFE>(ga, max_tiles, gu, s, name);
+  return launch_mx_gemv_k<MODE, (MR > 2 ? 2 : MR), 4, SAFE>(ga, max_tiles, gu, s, name);
+}
+
+template <int MODE, bool SAFE>
+int launch_mx_gemv(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint16_t* gu, hipStream_t s,
+                   const char* name) {
+  if (T <= 1) return launch_mx_gemv_mr<MODE, 1, SAFE>(ga, max_tiles, gu, s, name);
+  if (T <= 2) return launch_mx_gemv_mr<MODE, 2, SAFE>(ga, max_tiles, gu, s, name);
+  return launch_mx_gemv_mr<MODE, 4, SAFE>(ga, max_tiles, gu, s, name);
+}
+
 }  // namespace
 
 namespace lsk {
@@ -340,6 +541,15 @@ namespace lsk {
 int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, hipStream_t s) {
   if (mode == 0) return safe ? launch_grouped<0, true>(ga, max_tiles, s) : launch_grouped<0, false>(ga, max_tiles, s);
   return safe ? launch_grouped<1, true>(ga, max_tiles, s) : launch_grouped<1, false>(ga, max_tiles, s);
+}
+
+int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,
+                       hipStream_t s) {
+  if (mode == 0)
+    return safe ? launch_mx_gemv<0, true>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<gate_up>")
+                : launch_mx_gemv<0, false>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<gate_up>");
+  return safe ? launch_mx_gemv<1, true>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<down>")
+              : launch_mx_gemv<1, false>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<down>");
 }
 
 int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, float* asc, hipStream_t s) {

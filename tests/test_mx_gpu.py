@@ -176,3 +176,45 @@ def test_config5_t4096_token_subset():
     rows = np.sort(np.random.default_rng(2).choice(4096, 24, replace=False))
     ref = C.moe_forward_mx(x[rows], oexp, idx[rows], w[rows], oact)
     assert np.array_equal(got[rows], ref)
+
+
+@pytest.mark.parametrize("variant", [0, 2])
+@pytest.mark.parametrize("big_exp", [False, True])
+def test_moe_mx_tiles_and_gemv(variant, big_exp):
+    """The MX layer on the tiled grouped GEMM (0) and on the decode GEMV (2), against the oracle:
+    up to 12 rows per expert (the GEMV's row chunks), a bias, and optionally exponent bytes >= 240
+    in some blocks of one expert's down projection (the separate multiply-then-add update; the
+    overflowing products give infinities, and their sums in the combine NaNs, compared as bf16
+    bits).  The gate/up stage stays finite: a NaN reaching the int8 requant has no defined
+    int8 value in the reference's torch casts."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    T, E, k, H, I = 12, 3, 2, 2112, 352
+    say("mx tiles / gemv", variant, big_exp)
+    x, experts, logits = WL.moe_mx_inputs(T, E, k, H, I, seed=61, bias=True)
+    if big_exp:
+        p13, s13, p2, s2, b13, b2 = experts[1]
+        s2 = s2.copy()
+        s2[::5, 2] = 241
+        s2[::9, 7] = 250
+        experts[1] = (p13, s13, p2, s2, b13, b2)
+    idx, w = routing_from_logits(logits, k)
+    oexp = []
+    dexp = []
+    for (p13, s13, p2, s2, b13, b2) in experts:
+        m13, _ = C.mx_to_m2(p13, s13)
+        m2_, _ = C.mx_to_m2(p2, s2)
+        oexp.append(((m13, s13), (m2_, s2), b13, b2))
+        dexp.append(((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2)))
+    dexp = MR.ExpertTablesMX(dexp, packed=True)
+    ridx, rw = routing_device(idx, w)
+    L.call("lsk_moe_select", variant)
+    try:
+        y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai,
+                                    routing=(ridx, rw))
+    finally:
+        L.call("lsk_moe_select", -1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx(x, oexp, idx, w, C.act_swigluoai)
+    assert np.array_equal(u16(y), ref)
