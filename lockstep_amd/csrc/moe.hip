@@ -799,13 +799,14 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemmArgs a, uint16_t* 
 
 // Decode path after the gate/up GEMV: per row, h = act(gate, up) (the values the tiled kernels
 // store), its |h| maximum (fmaxf from +0, so a NaN is passed over as there), and the row quant
-// of h exactly as moe_requant_kernel does it.  One block per row; I <= 256 * PER.
-template <int PER>
-__global__ __launch_bounds__(256) void moe_act_requant_kernel(const uint16_t* __restrict__ gu,
+// of h exactly as moe_requant_kernel does it (int8, or its values as bf16 for the MX GEMV).
+// One block of 1024 threads per row; I <= 1024 * PER.
+template <int PER, bool OUT_BF16>
+__global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* __restrict__ gu,
                                                               const int32_t* __restrict__ nrows, int I, int act,
                                                               const int32_t* __restrict__ frac,
-                                                              int8_t* __restrict__ q, float* __restrict__ asc) {
-  __shared__ float red[4];
+                                                              void* __restrict__ q, float* __restrict__ asc) {
+  __shared__ float red[16];
   const int p = blockIdx.x;
   if (p >= *nrows) return;
   const int tid = threadIdx.x;
@@ -815,7 +816,7 @@ __global__ __launch_bounds__(256) void moe_act_requant_kernel(const uint16_t* __
   float am = 0.0f;
 #pragma unroll
   for (int t = 0; t < PER; ++t) {
-    const int c = tid + 256 * t;
+    const int c = tid + 1024 * t;
     hv[t] = 0.0f;
     if (c < I) {
       const float yg = bf16_to_f32(g[c]), yu = bf16_to_f32(u[c]);
@@ -827,16 +828,19 @@ __global__ __launch_bounds__(256) void moe_act_requant_kernel(const uint16_t* __
   for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
   if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
-  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  am = red[0];
+#pragma unroll
+  for (int w2 = 1; w2 < 16; ++w2) am = fmaxf(am, red[w2]);
   const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f);
   if (tid == 0) asc[p] = s;
 #pragma unroll
   for (int t = 0; t < PER; ++t) {
-    const int c = tid + 256 * t;
+    const int c = tid + 1024 * t;
     if (c < I) {
       const float hb = bf16_to_f32(f32_to_bf16(hv[t]));  // h as the tiled kernels store it
       const float qv = fminf(fmaxf(rintf(f32_div(hb, s)), -127.0f), 127.0f);
-      q[(int64_t)p * I + c] = (int8_t)(int)qv;
+      if (OUT_BF16) ((uint16_t*)q)[(int64_t)p * I + c] = (uint16_t)(__float_as_uint(qv) >> 16);  // exact
+      else ((int8_t*)q)[(int64_t)p * I + c] = (int8_t)(int)qv;
     }
   }
 }
@@ -1159,7 +1163,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::check_launch("widen_bf16_kernel"))) return rc;
     if ((rc = lsk_fwht_blocks(w.xrot, T, H, H, rb, a->rot_scale, w.xrot, H, stream))) return rc;
     rc = lsk_rowquant(w.xrot, LSK_F32, T, H, H, w.qx, H, w.ascx, stream);
-  } else if (mx && !use_mx_gemv) {
+  } else if (mx) {
     rc = lsk::launch_rowquant_bf16(a->x, T, H, (uint16_t*)w.qx, w.ascx, s);
   } else {
     rc = lsk_rowquant(a->x, LSK_BF16, T, H, H, w.qx, H, w.ascx, stream);
@@ -1199,7 +1203,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   MoeGemmArgs g1{};
   g1.A = w.qx;
   g1.lda = H;
-  g1.a_bytes = T * H;
+  g1.a_bytes = T * H * (mx ? 2 : 1);
   g1.w_bytes = 2 * I * a->ldw13;
   g1.a_scale = w.ascx;
   g1.row_tok = w.row_tok;
@@ -1228,16 +1232,17 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     return rc;
   }
   if (use_gemv || use_mx_gemv) {
-    const int per = (int)((I + 255) / 256);
-    const dim3 grid((unsigned)R), blk(256);
-    if (per <= 4) hipLaunchKernelGGL(moe_act_requant_kernel<4>, grid, blk, 0, s, w.gu, w.offs + E, (int)I, a->act,
-                                     a->frac, w.qh, w.asch);
-    else if (per <= 8) hipLaunchKernelGGL(moe_act_requant_kernel<8>, grid, blk, 0, s, w.gu, w.offs + E, (int)I,
-                                          a->act, a->frac, w.qh, w.asch);
-    else if (per <= 16) hipLaunchKernelGGL(moe_act_requant_kernel<16>, grid, blk, 0, s, w.gu, w.offs + E, (int)I,
-                                           a->act, a->frac, w.qh, w.asch);
-    else hipLaunchKernelGGL(moe_act_requant_kernel<32>, grid, blk, 0, s, w.gu, w.offs + E, (int)I, a->act, a->frac,
-                            w.qh, w.asch);
+    const int per = (int)((I + 1023) / 1024);
+    const dim3 grid((unsigned)R), blk(1024);
+#define LSK_ACTQ(P)                                                                                             \
+  {                                                                                                             \
+    if (mx) hipLaunchKernelGGL((moe_act_requant_kernel<P, true>), grid, blk, 0, s, w.gu, w.offs + E, (int)I,    \
+                               a->act, a->frac, (void*)w.qh, w.asch);                                           \
+    else hipLaunchKernelGGL((moe_act_requant_kernel<P, false>), grid, blk, 0, s, w.gu, w.offs + E, (int)I,      \
+                            a->act, a->frac, (void*)w.qh, w.asch);                                              \
+  }
+    if (per <= 1) LSK_ACTQ(1) else if (per <= 2) LSK_ACTQ(2) else if (per <= 4) LSK_ACTQ(4) else LSK_ACTQ(8)
+#undef LSK_ACTQ
     if ((rc = lsk::check_launch("moe_act_requant_kernel"))) return rc;
   } else if (rb > 0) {
     hipLaunchKernelGGL(moe_rot_requant_kernel, dim3((unsigned)R), dim3(256), (size_t)I * 4, s, w.h, w.offs + E, (int)I,
@@ -1255,7 +1260,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   MoeGemmArgs g2{};
   g2.A = w.qh;
   g2.lda = I;
-  g2.a_bytes = R * I;
+  g2.a_bytes = R * I * (mx ? 2 : 1);
   g2.w_bytes = H * a->ldw2;
   g2.a_scale = w.asch;
   g2.offs = w.offs;

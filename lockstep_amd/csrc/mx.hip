@@ -334,34 +334,26 @@ int launch_dense(const int8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, co
 }
 
 // ---------------------------------------------------------------- decode-sized grouped MX GEMV
-// Doubled E2M1 mantissas m2 (0, 1, 2, 3, 4, 6, 8, 12; codes 8..15 negated) as int8 for the four
-// codes (0..15) in the bytes of c: two byte-table lookups (v_perm_b32) and a sign select.
-LSK_DEV uint32_t m2x4_from_codes(uint32_t c) {
-  const uint32_t lo3 = c & 0x07070707u;
-  const uint32_t pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, lo3);
-  const uint32_t neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, lo3);
-  // selector 12 gives 0x00, 13 gives 0xFF: a byte mask from each code's sign bit
-  const uint32_t msk = __builtin_amdgcn_perm(0u, 0u, ((c >> 3) & 0x01010101u) | 0x0C0C0C0Cu);
-  return (neg & msk) | (pos & ~msk);
-}
-
 // Decode-sized MX expert GEMV.  Lane l owns MX block b = l + 64 j (j < NCH) of every weight row
-// the wave streams: its 16 code bytes and its exponent byte, loaded coalesced.  The codes are
-// decoded once per row to int8 m2 (even / odd elements in separate words), and each block sum
-// s_b = sum a * m2 over the block's 32 elements is exact in int32 (v_dot4 against the
-// activation bytes split the same way).  The block sums go to LDS, and one lane per (row,
-// column) then runs the contract's ordered update acc = fl32(acc + s_b * 2^(k_b - 128)) over
-// the blocks in ascending order from +0 (one FMA, exact product; SAFE: multiply, then add).
-// MODE 0: gate row c and up row N + c, bias-added bfr values into gu for the activation-and-
-// requant kernel; MODE 1: bfr(w * y) into the token's slot row.  Activations are int8 rows.
+// the wave streams: its 16 code bytes and its exponent byte, loaded coalesced.  gfx950's
+// v_cvt_scalef32_pk_bf16_fp4 with scale 2 turns two codes into the bf16 doubled mantissas m2
+// (exact; checked over every code byte on MI355X), and v_dot2_f32_bf16 against the activation
+// (int8 values held as bf16) sums a block: every product and partial sum is an integer below
+// 2^16, so the block sum s_b is exact.  The block sums go to LDS, and one lane per (row, column)
+// then runs the contract's ordered update acc = fl32(acc + s_b * 2^(k_b - 128)) over the
+// blocks in ascending order from +0 (one FMA, exact product; SAFE: multiply, then add).  MODE
+// 0: gate row c and up row N + c, bias-added bfr values into gu for the activation-and-requant
+// kernel; MODE 1: bfr(w * y) into the token's slot row.
+typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+
 template <int MODE, int MR, int NCH, int RPW, bool SAFE>
 __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu) {
   constexpr int kRows = MODE == 0 ? 2 : 1;
   constexpr int V = MR * RPW * kRows;  // chains per row chunk, q = (m * RPW + i) * kRows + r
   static_assert(V <= 64, "one lane per chain");
   constexpr int kB = 64 * NCH;          // blocks a wave covers
-  constexpr int kSbStride = kB + 4;     // int32 per chain row in LDS (16-byte aligned, skewed banks)
-  constexpr int kWaveBytes = V * kSbStride * 4 + RPW * kRows * kB;
+  constexpr int kSbStride = kB + 4;     // floats per chain row in LDS (16-byte aligned, skewed banks)
+  constexpr int kWaveBytes = V * kSbStride * 4 + RPW * kRows * kB * 4;
   extern __shared__ __attribute__((aligned(16))) char gemv_smem[];
   const int cols_blk = 4 * RPW;
   const int nchunk = (a.N + cols_blk - 1) / cols_blk;
@@ -374,15 +366,15 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
   const int nb = a.K / 32;
   const int c0 = ch * cols_blk + wave * RPW;
   const int nw = MODE == 0 ? 2 * a.N : a.N;  // weight rows of the expert
-  int32_t* sb = (int32_t*)(gemv_smem + wave * kWaveBytes);
-  uint8_t* ex = (uint8_t*)(sb + V * kSbStride);
+  float* sb = (float*)(gemv_smem + wave * kWaveBytes);
+  float* scl = sb + V * kSbStride;  // 2^(k - 128) per (weight row, block)
   const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)a.w_ptrs[e], (int64_t)nw * a.ldw);
   const __amdgpu_buffer_rsrc_t rsc = lsk::make_rsrc((const void*)a.ws_ptrs[e], (int64_t)nw * a.lds);
   const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
 
-  // the wave's weight rows: codes decoded to m2 (even elements in lo[w], odd in hi[w] of each
-  // 8-element word w), exponents parked in LDS
-  uint32_t lo[RPW][kRows][NCH][4], hi[RPW][kRows][NCH][4];
+  // the wave's weight rows: the lane's code bytes and exponent bytes per (column, row, block)
+  v4i codes[RPW][kRows][NCH];
+  uint32_t kxs[RPW][kRows][NCH];
 #pragma unroll
   for (int i = 0; i < RPW; ++i)
 #pragma unroll
@@ -393,15 +385,8 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
       for (int j = 0; j < NCH; ++j) {
         const int b = lane + 64 * j;
         const bool in = c < a.N && b < nb;
-        const v4i codes = lsk::buf_load16(rw, in ? (uint32_t)(wr * a.ldw + b * 16) : lsk::kOob);
-        const uint32_t kx = __builtin_amdgcn_raw_buffer_load_b8(rsc, in ? (int)(wr * a.lds + b) : (int)lsk::kOob, 0, 0);
-        ex[(i * kRows + r) * kB + b] = (uint8_t)kx;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t x = (uint32_t)codes[w];
-          lo[i][r][j][w] = m2x4_from_codes(x & 0x0F0F0F0Fu);
-          hi[i][r][j][w] = m2x4_from_codes((x >> 4) & 0x0F0F0F0Fu);
-        }
+        codes[i][r][j] = lsk::buf_load16(rw, in ? (uint32_t)(wr * a.ldw + b * 16) : lsk::kOob);
+        kxs[i][r][j] = __builtin_amdgcn_raw_buffer_load_b8(rsc, in ? (int)(wr * a.lds + b) : (int)lsk::kOob, 0, 0);
       }
     }
   // the chain this lane runs (lanes >= V idle in that phase)
@@ -416,9 +401,10 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
     b0 = bias[c];
     if (MODE == 0) b1 = bias[a.N + c];
   }
+  const uint16_t* A = (const uint16_t*)a.A;
   for (int rb = p0; rb < p1; rb += MR) {
-    // activation bytes of the lane's blocks, split into even / odd elements like the codes
-    uint32_t ae[MR][NCH][4], ao[MR][NCH][4];
+    // the lane's blocks of the chunk's activation rows: 32 bf16 values each (16 pairs)
+    v4i act[MR][NCH][4];
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const int p = rb + m;
@@ -427,18 +413,12 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
       for (int j = 0; j < NCH; ++j) {
         const int b = lane + 64 * j;
         const bool in = src >= 0 && b < nb;
-        const uint32_t off = in ? (uint32_t)(src * a.lda + b * 32) : lsk::kOob;
-        const v4i x0 = lsk::buf_load16(ra, off);
-        const v4i x1 = lsk::buf_load16(ra, in ? off + 16 : lsk::kOob);
-        const uint32_t d[8] = {(uint32_t)x0[0], (uint32_t)x0[1], (uint32_t)x0[2], (uint32_t)x0[3],
-                               (uint32_t)x1[0], (uint32_t)x1[1], (uint32_t)x1[2], (uint32_t)x1[3]};
+        const uint32_t off = in ? (uint32_t)((src * a.lda + b * 32) * 2) : lsk::kOob;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          ae[m][j][w] = __builtin_amdgcn_perm(d[2 * w + 1], d[2 * w], 0x06040200u);
-          ao[m][j][w] = __builtin_amdgcn_perm(d[2 * w + 1], d[2 * w], 0x07050301u);
-        }
+        for (int h = 0; h < 4; ++h) act[m][j][h] = lsk::buf_load16(ra, in ? off + 16 * h : lsk::kOob);
       }
     }
+    (void)A;
     const int p = rb + q_m;
     const bool rowok = owner && p < p1;
     float asc = 0.0f, wt = 0.0f;
@@ -450,32 +430,68 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
         dst = a.row_dst[p];
       }
     }
-    // exact block sums into LDS
-#pragma unroll
-    for (int m = 0; m < MR; ++m)
+    if (rb == p0) {
+      // block scales into LDS, after the first chunk's loads are issued (its wait covers them)
 #pragma unroll
       for (int i = 0; i < RPW; ++i)
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
 #pragma unroll
-          for (int j = 0; j < NCH; ++j) {
-            int t = 0;
+          for (int j = 0; j < NCH; ++j)
+            scl[(i * kRows + r) * kB + lane + 64 * j] = pow2f((int)(kxs[i][r][j] & 0xffu) - 128);
+    }
+    // exact block sums into LDS: decode the codes of (i, r, j), dot with every row of the chunk
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              t = __builtin_amdgcn_sdot4((int)ae[m][j][w], (int)lo[i][r][j][w], t, false);
-              t = __builtin_amdgcn_sdot4((int)ao[m][j][w], (int)hi[i][r][j][w], t, false);
+    for (int i = 0; i < RPW; ++i)
+#pragma unroll
+      for (int r = 0; r < kRows; ++r)
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+          uint32_t m2[16];  // pair d = elements 2d, 2d + 1 of the block
+          // decoded per row chunk (kept out of registers between chunks: 16 words per row block)
+          v4i cw = codes[i][r][j];
+          asm volatile("" : "+v"(cw));
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t x = (uint32_t)cw[w];
+            m2[4 * w + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 0));
+            m2[4 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 1));
+            m2[4 * w + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 2));
+            m2[4 * w + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, 2.0f, 3));
+          }
+#pragma unroll
+          for (int m = 0; m < MR; ++m) {
+            float t = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 16; ++d) {
+              // through a plain int: a bit cast of a vector element lvalue read the vector's first
+              // element here
+              const int av = act[m][j][d >> 2][d & 3];
+              t = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2bf_t, av), __builtin_bit_cast(v2bf_t, m2[d]), t,
+                                                  false);
             }
             sb[((m * RPW + i) * kRows + r) * kSbStride + lane + 64 * j] = t;
           }
+        }
     // the ordered update, one chain per lane (LDS written and read by this wave only: in order)
     float acc = 0.0f;
     if (chain) {
-      const int32_t* srow = sb + q * kSbStride;
-      const uint8_t* erow = ex + (q_i * kRows + q_r) * kB;
-      for (int b = 0; b < nb; ++b) {
-        const float sc = pow2f((int)erow[b] - 128);
-        acc = SAFE ? f32_add(acc, f32_mul((float)srow[b], sc)) : __builtin_fmaf((float)srow[b], sc, acc);
+      const float* srow = sb + q * kSbStride;
+      const float* crow = scl + (q_i * kRows + q_r) * kB;
+      auto upd = [&](float sv, float sc) {
+        acc = SAFE ? f32_add(acc, f32_mul(sv, sc)) : __builtin_fmaf(sv, sc, acc);
+      };
+      int b = 0;
+#pragma unroll 2
+      for (; b + 4 <= nb; b += 4) {
+        const v4f s4 = *(const v4f*)(srow + b);
+        const v4f c4 = *(const v4f*)(crow + b);
+        upd(s4[0], c4[0]);
+        upd(s4[1], c4[1]);
+        upd(s4[2], c4[2]);
+        upd(s4[3], c4[3]);
       }
+      for (; b < nb; ++b) upd(srow[b], crow[b]);
     }
     const float accu = MODE == 0 ? __shfl_down(acc, 1, 64) : 0.0f;  // the up chain sits in lane q + 1
     if (rowok) {
@@ -503,7 +519,7 @@ int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu
   constexpr int RPW = MODE == 0 ? 2 : 4;
   constexpr int kRows = MODE == 0 ? 2 : 1;
   constexpr int V = MR * RPW * kRows;
-  constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH);
+  constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH * 4);
   static bool attr = false;
   auto kern = moe_mx_gemv_kernel<MODE, MR, NCH, RPW, SAFE>;
   if (!attr) {
@@ -518,12 +534,14 @@ int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu
   return lsk::check_launch(name);
 }
 
+// MR: activation rows per pass (their bf16 blocks live in registers: 16 words per row and block
+// sweep), fewer when K needs more sweeps.
 template <int MODE, int MR, bool SAFE>
 int launch_mx_gemv_mr(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
   const int nch = (ga.K / 32 + 63) / 64;
   if (nch <= 1) return launch_mx_gemv_k<MODE, MR, 1, SAFE>(ga, max_tiles, gu, s, name);
-  if (nch <= 2) return launch_mx_gemv_k<MODE, MR, 2, SAFE>(ga, max_tiles, gu, s, name);
-  return launch_mx_gemv_k<MODE, (MR > 2 ? 2 : MR), 4, SAFE>(ga, max_tiles, gu, s, name);
+  if (nch <= 2) return launch_mx_gemv_k<MODE, (MR > 2 ? 2 : MR), 2, SAFE>(ga, max_tiles, gu, s, name);
+  return launch_mx_gemv_k<MODE, 1, 4, SAFE>(ga, max_tiles, gu, s, name);
 }
 
 template <int MODE, bool SAFE>
