@@ -49,18 +49,19 @@ LSK_DEV void i8x16_to_bf16(v4i in, v4i& lo, v4i& hi) {
   hi = v4i{(int)o[4], (int)o[5], (int)o[6], (int)o[7]};
 }
 
-// 32 packed fp4 codes (element 2i in the low nibble of byte i) -> 32 bf16 m2 values (4 chunks)
+// 32 packed fp4 codes (element 2i in the low nibble of byte i) -> 32 bf16 m2 values (4 chunks).
+// gfx950's v_cvt_scalef32_pk_bf16_fp4 with scale 2 converts the two codes of one byte (low
+// nibble first) to bf16 2 * fp4 = m2, exactly (checked against m2_bf16 over every code byte on
+// MI355X).
 LSK_DEV void fp4x32_to_bf16(v4i in, v4i (&out)[4]) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const uint32_t u = (uint32_t)in[w];
-    uint32_t o[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const uint32_t byte = (u >> (8 * b)) & 0xffu;
-      o[b] = m2_bf16(byte & 0xfu) | (m2_bf16(byte >> 4) << 16);
-    }
-    out[w] = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+    const uint32_t o0 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(u, 2.0f, 0));
+    const uint32_t o1 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(u, 2.0f, 1));
+    const uint32_t o2 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(u, 2.0f, 2));
+    const uint32_t o3 = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(u, 2.0f, 3));
+    out[w] = v4i{(int)o0, (int)o1, (int)o2, (int)o3};
   }
 }
 
