@@ -33,9 +33,17 @@ FLAGS = [
 ]
 
 
+# Per-file code generation options.  mx.hip: the MX block update consumes every MFMA result
+# with VALU FMAs, so MFMA results go straight to VGPRs (no accumulation-register copies between
+# an MFMA and its FMAs).
+FILE_FLAGS = {
+    "mx.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed for %s:\n%s\n%s" % (src, " ".join(cmd), r.stderr))
