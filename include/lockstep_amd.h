@@ -39,7 +39,10 @@ typedef enum {
   LSK_EPI_V21 = 0,  /* out(fl32(fl32(acc)*ws[n])*asc[m]); bias: out(fl32(out) + b[n]) */
   LSK_EPI_V2 = 1,   /* out(fl32(fl32(fl32(acc)*asc[m])*ws[n]) + b[n]) (legacy order) */
   LSK_EPI_POW2 = 2, /* fl32(acc) * 2^-(shift + erow[m] + ecol[n]) (exact scaling) */
-  LSK_EPI_RAW = 3   /* the int32 accumulator itself */
+  LSK_EPI_RAW = 3,  /* the int32 accumulator itself */
+  LSK_EPI_V25 = 4   /* v2.5 outlier side path: y8 = bf16(fl32(fl32(acc)*ws[n])*asc[m]);
+                       y = bf16(fl32(y8) + side[m,n]), side[m,n] = sum_j fl32(ho[m,j]*wo[n,j]) in
+                       ascending j from +0; bias: bf16(fl32(y) + b[n]); then out(y) */
 } lsk_epilogue;
 
 /* The last error message of the calling thread ("" if none). */
@@ -96,6 +99,46 @@ int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
                     const int8_t* w, int64_t ldw, int64_t N, const float* ws, const float* bias,
                     int order, void* out, int out_dtype, int64_t ldo,
                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- the v2.5 outlier side path */
+
+/* The side term alone (replaces lockstep_fullstack.outlier_side, reference/lockstep_fullstack.py:549-557):
+ *   side[m, n] = sum_j fl32(ho[m, j]) * fl32(wo[n, j]), sequential in ascending j from +0, binary32.
+ * ho: [M, ko] of ho_dtype, wo: [N, ko] of wo_dtype (each LSK_F32 / LSK_BF16 / LSK_F16, contiguous);
+ * side: [M, N] binary32 contiguous.  ko = 0 gives +0 everywhere. */
+int lsk_outlier_side(const void* ho, int ho_dtype, int64_t M, int64_t ko, const void* wo, int wo_dtype, int64_t N,
+                     float* side, void* stream);
+
+/* The outlier split of w8a8_outlier_linear (reference/lockstep_fullstack.py:566-569):
+ * xm = binary32 copy of x [M, K] (row stride ldx, LSK_F32 / LSK_BF16 / LSK_F16) with the declared
+ * channels oidx [ko] (int32; negative values count from the end, as torch indexing does) set to
+ * +0; ho [M, ko] binary32 = x[:, oidx] (exact).  xm may be NULL (gather only).  A channel
+ * outside [-K, K) masks nothing and gathers NaN.  ko <= 4096. */
+int lsk_outlier_split(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, const int32_t* oidx, int64_t ko,
+                      float* xm, int64_t ldm, float* ho, void* stream);
+
+/* Exact GEMM with the V25 epilogue (lsk_epilogue) over pre-quantised rows: replaces the GEMM and
+ * epilogue lines of lockstep_fullstack.w8a8_outlier_linear (reference/lockstep_fullstack.py:571-577).
+ * a: [M, K] int8; w: [N, K] int8; asc [M], ws [N], bias [N] or NULL; ho: [M, ko] binary32;
+ * wo: [N, ko] of wo_dtype (LSK_BF16 or LSK_F32); out: [M, N] of out_dtype (f32 / bf16 / f16 /
+ * bf16-as-f32: the bf16 result cast like the reference's final `.to(out_dtype)`). */
+int lsk_gemm_w8a8_outlier(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                          const float* asc, const float* ws, const float* bias, const float* ho, int64_t ko,
+                          const void* wo, int wo_dtype, void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* Bytes of caller workspace lsk_w8a8_outlier_linear needs (M rows of width K, ko channels). */
+int64_t lsk_w8a8_outlier_linear_workspace(int64_t M, int64_t K, int64_t ko);
+
+/* The whole v2.5 norm-fed linear (replaces lockstep_fullstack.w8a8_outlier_linear,
+ * reference/lockstep_fullstack.py:560-578): split (lsk_outlier_split), the 256-block butterfly / 16
+ * when rot (v2.5; rot = 0 is the v2.5.1 o_proj form), row quant, exact GEMM, V25 epilogue.
+ * x: [M, K] (row stride ldx); oidx [ko] int32; wo [N, ko] (LSK_BF16 or LSK_F32); w [N, K] int8;
+ * ws [N]; bias [N] or NULL; out [M, N] of out_dtype.  rot needs K % 256 == 0.  workspace:
+ * lsk_w8a8_outlier_linear_workspace(M, K, ko) bytes, 256-byte aligned. */
+int lsk_w8a8_outlier_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, const int32_t* oidx,
+                            int64_t ko, const void* wo, int wo_dtype, const int8_t* w, int64_t ldw, int64_t N,
+                            const float* ws, const float* bias, int rot, void* out, int out_dtype, int64_t ldo,
+                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Tuning control with no counterpart in the reference: force the dense kernel
  * (0: 128x128 register-staged tile, 4 waves of 64x64; 1: ping-pong 256x256, 8 waves of 64x128;

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblockstep_amd.so")
 
 LSK_F32, LSK_BF16, LSK_F16, LSK_I32, LSK_I8, LSK_BF16_AS_F32 = 0, 1, 2, 3, 4, 5
-EPI_V21, EPI_V2, EPI_POW2, EPI_RAW = 0, 1, 2, 3
+EPI_V21, EPI_V2, EPI_POW2, EPI_RAW, EPI_V25 = 0, 1, 2, 3, 4
 LSK_ACT_SILU, LSK_ACT_SWIGLUOAI = 0, 1
 
 _DTYPE = {torch.float32: LSK_F32, torch.bfloat16: LSK_BF16, torch.float16: LSK_F16,
@@ -35,6 +35,13 @@ SIGNATURES = {
     "lsk_epilogue_apply": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I64, _P]),
     "lsk_w8a8_matmul_workspace": (_I64, [_I64, _I64]),
     "lsk_w8a8_matmul": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P, _I64, _P]),
+    "lsk_outlier_side": (_I, [_P, _I, _I64, _I64, _P, _I, _I64, _P, _P]),
+    "lsk_outlier_split": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P]),
+    "lsk_gemm_w8a8_outlier": (_I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P, _I, _P, _I, _I64,
+                                   _P]),
+    "lsk_w8a8_outlier_linear_workspace": (_I64, [_I64, _I64, _I64]),
+    "lsk_w8a8_outlier_linear": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I, _P, _I,
+                                     _I64, _P, _I64, _P]),
     "lsk_gemm_select": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
     "lsk_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),

@@ -116,6 +116,10 @@ __device__ __forceinline__ void pp_strip_store(int i, const int32_t* region, con
     const int ml = wm * C::WTM + i * 32 + row;
     const int m = m0 + ml;
     const float rv = sc_row[ml];
+    if (ORDER < 0 && order == LSK_EPI_V25) {  // the outlier side term needs (m, n): operands from memory
+      if (m < M && n < N) epilogue_store4(ep, m, n, N, v, vec);
+      continue;
+    }
     if (m < M && n < N)
       epilogue_store4_pre(ep.out, ep.ldo, order, odt, has_bias, ep.shift, m, n, N, v, rv, wsv, bv,
                           pow2 ? __float_as_int(rv) : 0, ecv, vec);
@@ -756,7 +760,7 @@ namespace lsk {
 
 // Shape checks shared by the dense and grouped entry points.
 int validate_epilogue(int order, int out_dtype, const float* asc, const float* ws, int64_t M, const char* who) {
-  LSK_REQUIRE(order >= LSK_EPI_V21 && order <= LSK_EPI_RAW, "%s: unknown epilogue order %d", who, order);
+  LSK_REQUIRE(order >= LSK_EPI_V21 && order <= LSK_EPI_V25, "%s: unknown epilogue order %d", who, order);
   if (order == LSK_EPI_RAW) {
     LSK_REQUIRE(out_dtype == LSK_I32, "%s: the RAW epilogue writes int32 (out_dtype %d)", who, out_dtype);
   } else if (order == LSK_EPI_POW2) {
@@ -764,7 +768,7 @@ int validate_epilogue(int order, int out_dtype, const float* asc, const float* w
   } else {
     LSK_REQUIRE(out_dtype == LSK_F32 || out_dtype == LSK_BF16 || out_dtype == LSK_F16 || out_dtype == LSK_BF16_AS_F32,
                 "%s: out_dtype %d not one of f32/bf16/f16/bf16-as-f32", who, out_dtype);
-    LSK_REQUIRE(M == 0 || (asc && ws), "%s: asc and ws are required by the V21/V2 epilogues", who);
+    LSK_REQUIRE(M == 0 || (asc && ws), "%s: asc and ws are required by the V21/V2/V25 epilogues", who);
   }
   return LSK_OK;
 }
@@ -961,6 +965,7 @@ extern "C" int lsk_gemm_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int6
   LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_gemm_w8a8: negative size M=%lld N=%lld K=%lld", (long long)M,
               (long long)N, (long long)K);
   LSK_REQUIRE(K <= 133144, "lsk_gemm_w8a8: K=%lld exceeds the int32-exact bound 133144", (long long)K);
+  LSK_REQUIRE(order != LSK_EPI_V25, "lsk_gemm_w8a8: the V25 epilogue takes its side inputs through lsk_gemm_w8a8_outlier");
   int rc = lsk::validate_epilogue(order, out_dtype, asc, ws, M, "lsk_gemm_w8a8");
   if (rc) return rc;
   if (M == 0 || N == 0) return LSK_OK;
@@ -1002,6 +1007,7 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
                                   void* stream) {
   LSK_REQUIRE(M >= 0 && N >= 0, "lsk_epilogue_apply: negative size");
   LSK_REQUIRE(order != LSK_EPI_RAW, "lsk_epilogue_apply: RAW is a copy, not an epilogue");
+  LSK_REQUIRE(order != LSK_EPI_V25, "lsk_epilogue_apply: V25 is applied by lsk_gemm_w8a8_outlier");
   int rc = lsk::validate_epilogue(order, out_dtype, asc, ws, M, "lsk_epilogue_apply");
   if (rc) return rc;
   if (M == 0 || N == 0) return LSK_OK;

@@ -117,12 +117,45 @@ struct EpiParams {
   int shift;                 // POW2 scalar
   void* out;
   int64_t ldo;               // elements
+  // V25 (the v2.5 outlier side path): ho binary32 [M, ko] (row stride ko), wo [N, ko] of
+  // wo_dtype (LSK_BF16 or LSK_F32, row stride ko)
+  const float* ho = nullptr;
+  const void* wo = nullptr;
+  int ko = 0;
+  int wo_dtype = LSK_BF16;
 };
+
+// The v2.5 side term of output (m, n) (lockstep_fullstack.py:549-557): sequential in j from +0,
+// each step one binary32 product and one binary32 add.
+LSK_DEV float outlier_side_value(const EpiParams& p, int64_t m, int64_t n) {
+  float s = 0.0f;
+  const float* h = p.ho + m * p.ko;
+  if (p.wo_dtype == LSK_BF16) {
+    const uint16_t* w = (const uint16_t*)p.wo + n * p.ko;
+    for (int j = 0; j < p.ko; ++j) s = f32_add(s, f32_mul(h[j], bf16_to_f32(w[j])));
+  } else {
+    const float* w = (const float*)p.wo + n * p.ko;
+    for (int j = 0; j < p.ko; ++j) s = f32_add(s, f32_mul(h[j], w[j]));
+  }
+  return s;
+}
+
+// The V25 value of one element (lockstep_fullstack.py:575-578): bf16-valued binary32.
+LSK_DEV float epi_v25(const EpiParams& p, int64_t m, int64_t n, int32_t acc) {
+  float y = bfr(f32_mul(f32_mul((float)acc, p.ws[n]), p.asc[m]));
+  y = bfr(f32_add(y, outlier_side_value(p, m, n)));
+  if (p.bias) y = bfr(f32_add(y, p.bias[n]));
+  return y;
+}
 
 LSK_DEV void epilogue_store(const EpiParams& p, int64_t m, int64_t n, int32_t acc) {
   const int64_t o = m * p.ldo + n;
   if (p.order == LSK_EPI_RAW) {
     ((int32_t*)p.out)[o] = acc;
+    return;
+  }
+  if (p.order == LSK_EPI_V25) {
+    store_out(p.out, p.out_dtype, o, epi_v25(p, m, n, acc));
     return;
   }
   const float v = (float)acc;  // int32 -> binary32, round to nearest even
@@ -148,6 +181,7 @@ LSK_DEV void epilogue_store(const EpiParams& p, int64_t m, int64_t n, int32_t ac
 
 // Epilogue value of one element, before the final rounding to the output type.
 LSK_DEV float epi_value(const EpiParams& p, int64_t m, int64_t n, int32_t acc) {
+  if (p.order == LSK_EPI_V25) return epi_v25(p, m, n, acc);
   const float v = (float)acc;  // int32 -> binary32, round to nearest even
   if (p.order == LSK_EPI_V21) {
     float y = f32_mul(f32_mul(v, p.ws[n]), p.asc[m]);
@@ -209,6 +243,10 @@ LSK_DEV EpiOps epi_ops_load(const EpiParams& p, int64_t m, int64_t n) {
 // epilogue_store with the operands from epi_ops_load.
 LSK_DEV void epilogue_store_ops(const EpiParams& p, int64_t m, int64_t n, int32_t acc, const EpiOps& o) {
   const int64_t off = m * p.ldo + n;
+  if (p.order == LSK_EPI_V25) {
+    store_out(p.out, p.out_dtype, off, epi_v25(p, m, n, acc));
+    return;
+  }
   if (p.order == LSK_EPI_RAW) {
     ((int32_t*)p.out)[off] = acc;
     return;

@@ -8,6 +8,8 @@ arithmetic runs in the HIP kernels of liblockstep_amd.so (GPU tensors only).
     w8a8_matmul(x, W8, ws, bias, out_dtype, rowchunk)   lockstep_fullstack.py:503-530
     quantize_weight_int8(W)                     lockstep_fullstack.py:581-587
     silu_contract(x), fwht_blocks(x2, blk, scale), pow2_f32(e)   :590-604, :533-546, :280-284
+    outlier_side(ho, wo)                        lockstep_fullstack.py:549-557
+    w8a8_outlier_linear(x, oidx, wo, W8, ws, bias, out_dtype, rot)   lockstep_fullstack.py:560-578
 """
 from __future__ import annotations
 
@@ -56,6 +58,36 @@ def w8a8_matmul(x, W8, ws, bias=None, out_dtype=None, rowchunk: int = 0):
     y = ops.w8a8_matmul(x2, w, ws, bias, L.EPI_V21, L.LSK_F32 if want64 else _OUT[odt])
     if want64:
         y = y.to(torch.float64)       # exact widening of the binary32 result
+    return y.reshape(*shp[:-1], N)
+
+
+def outlier_side(ho, wo):
+    """Contract v2.5 side path: side[m, n] = sum_k fl32(ho[m, k]) * fl32(wo[n, k]), the sum sequential
+    in k from +0 with binary32 adds.  ho [M, k], wo [N, k] -> f32 [M, N]."""
+    L.require_cuda(ho, wo, what="outlier_side")
+    return ops.outlier_side(ho, wo)
+
+
+def w8a8_outlier_linear(x, oidx, wo, W8, ws, bias=None, out_dtype=None, rot=True):
+    """The v2.5 norm-fed linear under R1 online: the declared channels oidx leave the row as ho,
+    the masked row takes the 256-block butterfly / 16 (rot; rot=False is the v2.5.1 o_proj form)
+    and the row quant, then y = bf16(fl32(bf16((fl32(acc) * ws[n]) * asc[m])) + side[m, n]), the
+    bias as a further bf16 rounding, and the result cast to out_dtype (default x.dtype)."""
+    L.require_cuda(x, oidx, wo, W8, ws, bias, what="w8a8_outlier_linear")
+    shp = x.shape
+    odt = out_dtype or x.dtype
+    N = W8.shape[0]
+    want64 = odt == torch.float64
+    if not want64 and odt not in _OUT:
+        raise TypeError("w8a8_outlier_linear: out_dtype %s not supported" % odt)
+    x2 = x.reshape(-1, shp[-1])
+    if rot and shp[-1] % 256:
+        raise RuntimeError("w8a8_outlier_linear: width %d is not a multiple of the 256-wide rotation block"
+                           % shp[-1])
+    w = W8 if W8.stride(-1) == 1 else W8.contiguous()
+    y = ops.w8a8_outlier_linear(x2, oidx, wo, w, ws, bias, rot, L.LSK_F32 if want64 else _OUT[odt])
+    if want64:
+        y = y.to(torch.float64)       # exact widening of the bf16-valued result
     return y.reshape(*shp[:-1], N)
 
 

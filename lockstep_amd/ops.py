@@ -119,6 +119,58 @@ def w8a8_matmul(x2: torch.Tensor, w_nk: torch.Tensor, ws: torch.Tensor, bias, or
     return out
 
 
+_OUT_T = {L.LSK_F32: torch.float32, L.LSK_BF16: torch.bfloat16, L.LSK_F16: torch.float16,
+          L.LSK_BF16_AS_F32: torch.float32}
+
+
+def _float_code(t: torch.Tensor):
+    """A float tensor as (contiguous tensor, dtype code): f32 / bf16 / f16 kept, others to f32."""
+    if t.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        t = t.to(torch.float32)
+    return (t if t.is_contiguous() else t.contiguous()), L.dtype_code(t.dtype)
+
+
+def outlier_side(ho: torch.Tensor, wo: torch.Tensor) -> torch.Tensor:
+    """side [M, N] binary32 = sum_j fl32(ho[m, j] * wo[n, j]), sequential in j from +0."""
+    L.require_cuda(ho, wo, what="outlier_side")
+    M, ko = ho.shape
+    N, ko2 = wo.shape
+    if ko != ko2:
+        raise ValueError("outlier_side: ho has %d channels, wo %d" % (ko, ko2))
+    h, hc = _float_code(ho)
+    w, wc = _float_code(wo)
+    side = torch.empty((M, N), dtype=torch.float32, device=ho.device)
+    L.call("lsk_outlier_side", L.ptr(h), hc, M, ko, L.ptr(w), wc, N, L.ptr(side), L.stream_of(ho))
+    return side
+
+
+def w8a8_outlier_linear(x2: torch.Tensor, oidx: torch.Tensor, wo: torch.Tensor, w_nk: torch.Tensor,
+                        ws: torch.Tensor, bias, rot: bool, out_dtype: int) -> torch.Tensor:
+    """The v2.5 outlier linear of rows x2 [M, K] -> [M, N] of out_dtype (one C-ABI call)."""
+    L.require_cuda(x2, oidx, wo, w_nk, ws, bias, what="w8a8_outlier_linear")
+    x2, xc = _float_code(_rows(x2))
+    M, K = x2.shape
+    N = w_nk.shape[0]
+    oi = oidx.reshape(-1).to(torch.int32).contiguous()
+    ko = oi.numel()
+    if wo.shape != (N, ko):
+        raise ValueError("w8a8_outlier_linear: wo shape %s, expected [%d, %d]" % (tuple(wo.shape), N, ko))
+    if wo.dtype == torch.bfloat16:
+        wod, woc = (wo if wo.is_contiguous() else wo.contiguous()), L.LSK_BF16
+    else:
+        wod, woc = wo.to(torch.float32).contiguous(), L.LSK_F32
+    out = torch.empty((M, N), dtype=_OUT_T[out_dtype], device=x2.device)
+    if M == 0 or N == 0:
+        return out
+    nbytes = L.load().lsk_w8a8_outlier_linear_workspace(M, K, ko)
+    work = torch.empty((nbytes,), dtype=torch.uint8, device=x2.device)
+    ws, bias = _f32(ws), _f32(bias)
+    L.call("lsk_w8a8_outlier_linear", L.ptr(x2), xc, x2.stride(0) if M > 1 else max(K, 1), M, K, L.ptr(oi), ko,
+           L.ptr(wod), woc, L.ptr(w_nk), w_nk.stride(0) if N > 1 else max(K, 1), N, L.ptr(ws), L.ptr(bias),
+           1 if rot else 0, L.ptr(out), out_dtype, N, L.ptr(work), nbytes, L.stream_of(x2))
+    return out
+
+
 def quant8_pow2(x: torch.Tensor, mode: int):
     """Power-of-two quant of x [M, K] binary32: mode 0 tensor, 1 rows, 2 columns.
     Returns (q int8 [M, K], e int32 [1] / [M] / [K])."""

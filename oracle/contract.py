@@ -337,6 +337,40 @@ def fwht_blocks(x2, blk=256, scale=1.0 / 16.0):
     return (v * F32(scale)).astype(F32).reshape(sh)
 
 
+# ----------------------------------------------------------------------------- v2.5 outlier side path
+def outlier_side(ho, wo):
+    """lockstep_fullstack.py:549-557: side[m, n] = sum_k fl32(ho[m, k]) * fl32(wo[n, k]), the sum
+    sequential in k from +0 with binary32 adds (each add rounds).  ho [M, k], wo [N, k] binary32
+    values (bf16-valued in the contract, so every product is exact)."""
+    h = np.asarray(ho, F32)
+    w = np.asarray(wo, F32)
+    side = np.zeros((h.shape[0], w.shape[0]), F32)
+    for k in range(h.shape[1]):
+        side = (side + (h[:, k:k + 1] * w[None, :, k]).astype(F32)).astype(F32)
+    return side
+
+
+def w8a8_outlier_linear(x, oidx, wo, W8, ws, bias=None, out="bf16", rot=True):
+    """lockstep_fullstack.py:560-578 (contract v2.5 / v2.5.1): the declared channels oidx leave the
+    row as ho (exact), the masked row takes the 256-block butterfly / 16 (rot) and the row quant,
+        y8 = bf16((fl32(acc) * ws[n]) * asc[m]);  y = bf16(fl32(y8) + side[m, n]);
+        with a bias y = bf16(fl32(y) + bias[n]);  then cast to `out` (from the bf16 value).
+    x [rows, K] binary32 values; oidx int [k]; wo [N, k]; W8 [N, K] int8; ws [N] fp32."""
+    x2 = np.asarray(x, F32).reshape(-1, np.shape(x)[-1])
+    idx = np.asarray(oidx).astype(np.int64)
+    ho = x2[:, idx]
+    xm = x2.copy()
+    xm[:, idx] = F32(0.0)
+    xr = fwht_blocks(xm) if rot else xm
+    q, asc = quantize_rows_int8(xr)
+    acc = int_mm(q, np.asarray(W8).T)
+    y = bfr(((acc.astype(F32) * np.asarray(ws, F32)[None, :]).astype(F32) * asc[:, None]).astype(F32))
+    y = bfr((y + outlier_side(ho, wo)).astype(F32))
+    if bias is not None:
+        y = bfr((y + np.asarray(bias, F32)[None, :]).astype(F32))
+    return cast_out(y, out)
+
+
 # ----------------------------------------------------------------------------- A12 router
 def table_scores(dgap, tab=None):
     """moe_ref.py:64-74: d = max(rint(fl32(dgap * C)), 0); s = tab[(d >> 13) & 8191] >> min(d >> 26, 63);

@@ -50,3 +50,20 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
     assert rc == 1
     # M == 0 is legal and a no-op
     assert lib.lsk_rowquant(None, 0, 0, 16, 16, None, 16, None, None) == 0
+
+
+def test_outlier_entry_points_refuse_bad_arguments_without_touching_the_gpu():
+    lib = L.load()
+    # V25 needs its side inputs: the plain GEMM refuses it
+    rc = lib.lsk_gemm_w8a8(None, 16, None, 16, 1, 1, 16, 4, None, None, None, None, None, 0, None, 1, 1, None)
+    assert rc == 1 and b"V25" in lib.lsk_last_error()
+    # the rotation needs whole 256-wide blocks
+    rc = lib.lsk_w8a8_outlier_linear(None, 1, 300, 1, 300, None, 0, None, 1, None, 300, 8, None, None, 1, None, 1, 8,
+                                     None, 0, None)
+    assert rc == 1 and b"256" in lib.lsk_last_error()
+    rc = lib.lsk_gemm_w8a8_outlier(None, 16, None, 16, 1, 1, 16, None, None, None, None, 0, None, 7, None, 1, 1, None)
+    assert rc == 1 and b"wo" in lib.lsk_last_error()
+    # zero rows: a no-op
+    assert lib.lsk_w8a8_outlier_linear(None, 1, 256, 0, 256, None, 3, None, 1, None, 256, 8, None, None, 1, None, 1, 8,
+                                       None, 0, None) == 0
+    assert lib.lsk_w8a8_outlier_linear_workspace(4, 256, 3) >= 4 * 256 * 5 + 4 * 3 * 4 + 16

@@ -85,6 +85,50 @@ def test_outlier_inputs_regenerate():
     _check("outlier.norot.w8", W8n, "int8")
 
 
+def outlier_weights(rot=True):
+    """The published outlier weights (tools/contract_vectors.py:88-99): wo from the bf16 weight's
+    oidx columns; W8 from the weight with those columns zeroed, block-rotated in binary32 when
+    `rot`, rounded to bf16 and quantised per output channel."""
+    x5, W5, oidx = outlier_inputs()
+    W64 = W5.astype(np.float64)
+    wo = C.bfr(W64[:, oidx].astype(np.float32))
+    W64[:, oidx] = 0.0
+    Wz = W64.astype(np.float32)
+    Wr = C.bfr(C.fwht_blocks(Wz) if rot else Wz)
+    W8, ws = C.quantize_weight_int8(Wr)
+    return x5, oidx, wo, W8, ws
+
+
+def test_outlier_side_and_linear_digests():
+    x5, oidx, wo, W8o, wso = outlier_weights(rot=True)
+    _check("outlier.w8", W8o, "int8")
+    _check("outlier.side", C.outlier_side(x5[:, oidx], wo), "float32")
+    _, _, _, bias = linear_inputs()
+    _check("linear.v2_5.outliers.no_bias", C.w8a8_outlier_linear(x5, oidx, wo, W8o, wso, None, "bf16"), "bfloat16")
+    _check("linear.v2_5.outliers.bias", C.w8a8_outlier_linear(x5, oidx, wo, W8o, wso, bias, "bf16"), "bfloat16")
+    x5, oidx, won, W8n, wsn = outlier_weights(rot=False)
+    _check("outlier.norot.w8", W8n, "int8")
+    _check("linear.v2_5_1.outliers_norot.no_bias",
+           C.w8a8_outlier_linear(x5, oidx, won, W8n, wsn, None, "bf16", rot=False), "bfloat16")
+
+
+def test_outlier_negative_controls():
+    """A plausible slip fails a digest: the side added before the y8 rounding, the side summed
+    in reverse order, or the rotation left out of the rotated case."""
+    x5, oidx, wo, W8o, wso = outlier_weights(rot=True)
+    ref = V["linear.v2_5.outliers.no_bias"]["sha256"]
+    xr = C.fwht_blocks(np.where(np.isin(np.arange(512), oidx)[None, :], np.float32(0), x5))
+    q, asc = C.rowquant(xr)
+    acc = C.int_mm(q, W8o.T)
+    y = ((acc.astype(np.float32) * wso[None, :]).astype(np.float32) * asc[:, None]).astype(np.float32)
+    fused = C.bf16_bits((y + C.outlier_side(x5[:, oidx], wo)).astype(np.float32))
+    assert C.digest(fused, "bfloat16") != ref
+    rev = C.outlier_side(x5[:, oidx][:, ::-1], wo[:, ::-1])
+    assert C.digest(rev, "float32") != V["outlier.side"]["sha256"]
+    norot = C.w8a8_outlier_linear(x5, oidx, wo, W8o, wso, None, "bf16", rot=False)
+    assert C.digest(norot, "bfloat16") != ref
+
+
 def test_frac_table_digest():
     t = C.frac_table()
     assert t.shape == (8192,)
