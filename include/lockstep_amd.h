@@ -140,6 +140,46 @@ int lsk_w8a8_outlier_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, 
                             const float* ws, const float* bias, int rot, void* out, int out_dtype, int64_t ldo,
                             void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------- two-plane wide-integer linears */
+
+/* Per-row quant to `bits` (8, 11 or 15) and its int8 planes (replaces t16h_lmvariants._quant_rows +
+ * _planes, reference/t16h_lmvariants.py:71-84, and quantize_weight :95-103 for weight rows):
+ *   v = x, or fl32(x / sdiv[k]) (sdiv_op 1, the runtime SmoothQuant divide, :154), or
+ *   fl32(x * sdiv[k]) (sdiv_op 2, the prepare-time fold, :145);
+ *   asc[m] = fl32(max(max_k |v|, fl32(1e-8)) / (2^(bits-1) - 1)) (true division);
+ *   a = clamp(rint_even(fl32(v / asc[m])), +-(2^(bits-1) - 1));
+ * then q32 [M, K] int32 = a when q32 is not NULL, else the planes into q (row stride ldq): bits 8
+ * one plane (q[m] = a); else hi = a >> (bits - 8) at row m and lo = a - (hi << (bits - 8)) at
+ * row M + m.  x: [M, K] of x_dtype (LSK_F32 / LSK_BF16 / LSK_F16), row stride ldx. */
+int lsk_quant_planes(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int bits, const float* sdiv,
+                     int sdiv_op, int8_t* q, int64_t ldq, int32_t* q32, float* asc, void* stream);
+
+/* The plane split of int32 values (replaces t16h_lmvariants._planes, reference/t16h_lmvariants.py:71-77):
+ * hi = a >> sh (floor), lo = a - (hi << sh); sh = 0 writes hi = a only.  a, hi, lo: n elements. */
+int lsk_split_planes(const int32_t* a, int64_t n, int sh, int8_t* hi, int8_t* lo, void* stream);
+
+/* The exact int64 plane combine and the logits epilogue (t16h_lmvariants.py:115-125):
+ * c [Pa * M, Pw * N] int32 (row stride ldc) holds the plane products, block (i, j) = activation
+ * plane i x weight plane j (plane 0 = hi when the width is above 8);
+ * s = sum acc_ij << (shift_i + shift_j) in int64; y = fl32(fl32(fl32(s) * asc[m]) * ws[n]),
+ * fl32(s) round-to-nearest-even from int64; with a bias y = fl32(y + bias[n]); out(y). */
+int lsk_planes_combine(const int32_t* c, int64_t ldc, int64_t M, int64_t N, int abits, int wbits, const float* asc,
+                       const float* ws, const float* bias, void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* Bytes of caller workspace lsk_planes_linear needs. */
+int64_t lsk_planes_linear_workspace(int64_t M, int64_t K, int64_t N, int abits, int wbits);
+
+/* The whole a<abits>w<wbits> linear / lm_head (replaces t16h_lmvariants._mm_planes and
+ * Variant.logits, reference/t16h_lmvariants.py:115-125,150-155, with the bias add and cast of
+ * lockstep_fullstack.get_logits_contract, reference/lockstep_fullstack.py:849-860):
+ * rows quantised to abits (divided by sdiv first when sdiv is not NULL), one exact GEMM of the
+ * stacked activation planes against the weight planes w [Pw * N, K] (row stride ldw; hi plane
+ * rows first, from lsk_quant_planes of the weight rows), then lsk_planes_combine.  Rows are
+ * processed in chunks whose plane products fit the workspace (lsk_planes_linear_workspace). */
+int lsk_planes_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int abits, const float* sdiv,
+                      const int8_t* w, int64_t ldw, int64_t N, int wbits, const float* ws, const float* bias, void* out,
+                      int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Tuning control with no counterpart in the reference: force the dense kernel
  * (0: 128x128 register-staged tile, 4 waves of 64x64; 1: ping-pong 256x256, 8 waves of 64x128;
  * 2: ping-pong 256x256, 8 waves of 128x64; 3: ping-pong 256x128, 8 waves of 64x64;

@@ -42,6 +42,12 @@ SIGNATURES = {
     "lsk_w8a8_outlier_linear_workspace": (_I64, [_I64, _I64, _I64]),
     "lsk_w8a8_outlier_linear": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I, _P, _I64, _I64, _P, _P, _I, _P, _I,
                                      _I64, _P, _I64, _P]),
+    "lsk_quant_planes": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _I, _P, _I64, _P, _P, _P]),
+    "lsk_split_planes": (_I, [_P, _I64, _I, _P, _P, _P]),
+    "lsk_planes_combine": (_I, [_P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P, _I, _I64, _P]),
+    "lsk_planes_linear_workspace": (_I64, [_I64, _I64, _I64, _I, _I]),
+    "lsk_planes_linear": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P, _P, _P, _I, _I64, _P, _I64,
+                               _P]),
     "lsk_gemm_select": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
     "lsk_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),

@@ -171,6 +171,76 @@ def w8a8_outlier_linear(x2: torch.Tensor, oidx: torch.Tensor, wo: torch.Tensor, 
     return out
 
 
+def _bits_ok(bits):
+    if bits not in (8, 11, 15):
+        raise ValueError("width %d not supported (8, 11, 15)" % bits)
+
+
+def quant_bits(x2: torch.Tensor, bits: int):
+    """Per-row <bits> quant of x2 [M, K]: (a int32 [M, K], asc f32 [M])."""
+    L.require_cuda(x2, what="quant_bits")
+    _bits_ok(bits)
+    x2, xc = _float_code(_rows(x2))
+    M, K = x2.shape
+    a = torch.empty((M, K), dtype=torch.int32, device=x2.device)
+    asc = torch.empty((M,), dtype=torch.float32, device=x2.device)
+    L.call("lsk_quant_planes", L.ptr(x2), xc, x2.stride(0) if M > 1 else max(K, 1), M, K, int(bits), None, 0, None,
+           max(K, 1), L.ptr(a), L.ptr(asc), L.stream_of(x2))
+    return a, asc
+
+
+def quant_planes(W: torch.Tensor, bits: int, sdiv=None, sdiv_op: int = 0):
+    """Per-row <bits> quant of W [N, K] (times / divided by sdiv per column) as stacked int8 planes
+    [P * N, K] (hi plane rows first) and the f32 scales [N]."""
+    L.require_cuda(W, sdiv, what="quant_planes")
+    _bits_ok(bits)
+    W2, wc = _float_code(_rows(W))
+    N, K = W2.shape
+    P = 1 if bits == 8 else 2
+    q = torch.empty((P * N, K), dtype=torch.int8, device=W.device)
+    ws = torch.empty((N,), dtype=torch.float32, device=W.device)
+    sd = _f32(sdiv) if sdiv_op else None
+    L.call("lsk_quant_planes", L.ptr(W2), wc, W2.stride(0) if N > 1 else max(K, 1), N, K, int(bits), L.ptr(sd),
+           int(sdiv_op), L.ptr(q), max(K, 1), None, L.ptr(ws), L.stream_of(W))
+    return q, ws
+
+
+def split_planes(a: torch.Tensor, sh: int):
+    """[(sh, hi int8), (0, lo int8)] of int32 values a (sh = 0: [(0, a as int8)])."""
+    L.require_cuda(a, what="split_planes")
+    a = a.to(torch.int32).contiguous()
+    hi = torch.empty(a.shape, dtype=torch.int8, device=a.device)
+    lo = torch.empty(a.shape, dtype=torch.int8, device=a.device) if sh else None
+    L.call("lsk_split_planes", L.ptr(a), a.numel(), int(sh), L.ptr(hi), L.ptr(lo), L.stream_of(a))
+    return [(0, hi)] if sh == 0 else [(int(sh), hi), (0, lo)]
+
+
+def planes_linear(x2: torch.Tensor, w2: torch.Tensor, wbits: int, ws: torch.Tensor, abits: int, sdiv=None,
+                  bias=None, out_dtype: int = L.LSK_F32) -> torch.Tensor:
+    """The a<abits>w<wbits> linear of rows x2 [M, K] against stacked weight planes w2 [P * N, K]."""
+    L.require_cuda(x2, w2, ws, sdiv, bias, what="planes_linear")
+    _bits_ok(abits)
+    _bits_ok(wbits)
+    x2, xc = _float_code(_rows(x2))
+    M, K = x2.shape
+    P = 1 if wbits == 8 else 2
+    if w2.shape[0] % P or w2.shape[1] != K:
+        raise ValueError("planes_linear: weight planes %s do not fit K=%d and %d planes" % (tuple(w2.shape), K, P))
+    if w2.stride(-1) != 1:
+        w2 = w2.contiguous()
+    N = w2.shape[0] // P
+    out = torch.empty((M, N), dtype=_OUT_T[out_dtype], device=x2.device)
+    if M == 0 or N == 0:
+        return out
+    nbytes = L.load().lsk_planes_linear_workspace(M, K, N, int(abits), int(wbits))
+    work = torch.empty((nbytes,), dtype=torch.uint8, device=x2.device)
+    ws, sdiv, bias = _f32(ws), _f32(sdiv), _f32(bias)
+    L.call("lsk_planes_linear", L.ptr(x2), xc, x2.stride(0) if M > 1 else max(K, 1), M, K, int(abits), L.ptr(sdiv),
+           L.ptr(w2), w2.stride(0) if w2.shape[0] > 1 else max(K, 1), N, int(wbits), L.ptr(ws), L.ptr(bias),
+           L.ptr(out), out_dtype, N, L.ptr(work), nbytes, L.stream_of(x2))
+    return out
+
+
 def quant8_pow2(x: torch.Tensor, mode: int):
     """Power-of-two quant of x [M, K] binary32: mode 0 tensor, 1 rows, 2 columns.
     Returns (q int8 [M, K], e int32 [1] / [M] / [K])."""

@@ -21,8 +21,13 @@ Pinning (how each function is checked, see tests/test_oracle_*.py):
   int_mm_mx: one-block closed form, equal-exponent integer identity, scalar brute force,
       and a negative control (reversed block order differs)
   router / combine / moe_forward*: scalar brute force in Python ints and numpy float32
-  w8a8_linear (E-v2 order), sigmoid_contract, act_swigluoai: parity unpinned by any
-      reference-held vector; checked by scalar brute force of the written rule only.
+  outlier_side / w8a8_outlier_linear: the digests outlier.*, linear.v2_5.*, linear.v2_5_1.*
+  quant_rows_bits / planes / quantize_weight_bits / mm_planes: rowquant at 8 bits (digest-pinned),
+      rational brute force of the quant at 11 / 15 bits, the plane identity (hi << sh) + lo = a,
+      the int64 combine equal to the direct exact product, an RNE brute force of fl32(s)
+  w8a8_linear (E-v2 order), sigmoid_contract, act_swigluoai, mm_planes' epilogue order:
+      parity unpinned by any reference-held vector; checked by scalar brute force of the
+      written rule only.  smooth_scales (binary32 pow): parity unpinned.
 """
 from __future__ import annotations
 
@@ -316,6 +321,70 @@ def act_swigluoai(gate, up):
     arg = bfr((gc * SWIGLU_ALPHA).astype(F32))
     glu = bfr((gc * sigmoid_contract(arg)).astype(F32))
     return bfr(((uc + F32(1.0)).astype(F32) * glu).astype(F32))
+
+
+# ----------------------------------------------------------------------------- two-plane wide-integer linears
+def quant_rows_bits(x2, abits, sdiv=None, sdiv_op=0):
+    """t16h_lmvariants.py:80-84 (_quant_rows) and :95-103 (quantize_weight's quant): amax_q =
+    2^(bits-1) - 1; asc = fl32(max(max_k |v|, fl32(1e-8)) / amax_q); a = clamp(rint(fl32(v / asc)),
+    +-amax_q) as int64.  v = x, or fl32(x / sdiv) (sdiv_op 1, Variant.logits :154), or
+    fl32(x * sdiv) (sdiv_op 2, the fold of Variant.prepare :145)."""
+    v = np.asarray(x2, F32)
+    if sdiv_op == 1:
+        v = (v / np.asarray(sdiv, F32)[None, :]).astype(F32)
+    elif sdiv_op == 2:
+        v = (v * np.asarray(sdiv, F32)[None, :]).astype(F32)
+    qmax = F32((1 << (abits - 1)) - 1)
+    am = np.abs(v).max(axis=1) if v.shape[1] else np.zeros(v.shape[0], F32)
+    asc = (np.maximum(am, RNE_MIN_AMAX) / qmax).astype(F32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        a = np.clip(np.rint((v / asc[:, None]).astype(F32)), -qmax, qmax).astype(np.int64)
+    return a, asc
+
+
+def planes(a, sh):
+    """t16h_lmvariants.py:71-77: a = (hi << sh) + lo, hi = a >> sh (floor), lo in [0, 2^sh - 1];
+    sh = 0 is one plane.  Returns [(shift, int8 plane)], the hi plane first."""
+    a = np.asarray(a, np.int64)
+    if sh == 0:
+        return [(0, a.astype(np.int8))]
+    hi = a >> sh
+    lo = a - (hi << sh)
+    return [(sh, hi.astype(np.int8)), (0, lo.astype(np.int8))]
+
+
+def quantize_weight_bits(W, wbits, sdiv=None):
+    """t16h_lmvariants.py:95-103 with the prepare-time fold :137-148: per-out-channel <wbits>
+    quant of W [N, K] (times sdiv per column when given) carried by int8 planes [N, K]."""
+    a, ws = quant_rows_bits(W, wbits, sdiv, 2 if sdiv is not None else 0)
+    return planes(a, wbits - 8), ws
+
+
+def mm_planes(x2, wplanes, ws, abits, sdiv=None):
+    """t16h_lmvariants.py:115-125 (_mm_planes, with Variant.logits' divide :150-155): the plane
+    products as exact integer GEMMs, combined in int64 (activation planes outer, weight planes
+    inner), then fl32(fl32(fl32(s) * asc[m]) * ws[n]) with fl32(s) rounded to nearest even."""
+    a, asc = quant_rows_bits(x2, abits, sdiv, 1 if sdiv is not None else 0)
+    ap = planes(a, abits - 8)
+    if len(ap) == 1 and len(wplanes) == 1:
+        acc = int_mm(ap[0][1], np.asarray(wplanes[0][1]).T).astype(F32)
+    else:
+        s = np.zeros((a.shape[0], np.asarray(wplanes[0][1]).shape[0]), np.int64)
+        for ash, p in ap:
+            for wsh, w in wplanes:
+                s = s + (int_mm(p, np.asarray(w).T).astype(np.int64) << (ash + wsh))
+        acc = s.astype(F32)                       # int64 -> binary32, round to nearest even
+    return ((acc * asc[:, None]).astype(F32) * np.asarray(ws, F32)[None, :]).astype(F32)
+
+
+def smooth_scales(act_amax, W, alpha):
+    """t16h_lmvariants.py:106-112: s = max(a_amax^alpha / w_amax^(1-alpha), 1e-5) per input channel,
+    w_amax / a_amax clamped below at 1e-5, in binary32 (pow is not correctly rounded: a prepare-time
+    artifact, parity unpinned beyond the tolerance its tests state)."""
+    w_amax = np.maximum(np.abs(np.asarray(W, F32)).max(axis=0), F32(1e-5))
+    a_amax = np.maximum(np.asarray(act_amax, F32), F32(1e-5))
+    s = (np.power(a_amax, F32(alpha)) / np.power(w_amax, F32(1.0 - alpha))).astype(F32)
+    return np.maximum(s, F32(1e-5)).astype(F32)
 
 
 # ----------------------------------------------------------------------------- rotation
