@@ -180,6 +180,28 @@ int lsk_planes_linear(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_
                       const int8_t* w, int64_t ldw, int64_t N, int wbits, const float* ws, const float* bias, void* out,
                       int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------- the contract 2.6 float norm */
+
+/* The float RMSNorm (replaces t16n_ref.rmsnorm_float / row_sum_float, reference/t16n_ref.py:53-92),
+ * optionally fused with the contract row quant of its bf16 output (what lockstep_fullstack.w8a8_matmul
+ * applies to the norm output, reference/lockstep_fullstack.py:476-481):
+ *   S = the pinned tree sum of fl32(x^2) (chains of 8, then the adjacent-pairs tree);
+ *   S = fl32(S + fl32(fl64(N) * eps)) when eps != 0; S = max(S, 2^-126);
+ *   rs = fl32(sN / fl32(sqrt S)) (sN <= 0 selects the width constant fl32(sqrt N));
+ *   out = bf16(fl32(fl32(x * rs) * g)) (no gain when g is NULL), stored as out_dtype (bf16, or the
+ *   bf16 value widened / narrowed to f32 / f16);
+ *   q, asc (when q is not NULL) = the row quant of the bf16 out values.
+ * x: [R, N] of x_dtype (row stride ldx), N % 8 == 0, N <= 65536; S (optional): the row sums before
+ * eps, binary32 [R]; out / q may each be NULL. */
+int lsk_rmsnorm_float(const void* x, int x_dtype, int64_t ldx, int64_t R, int64_t N, const void* g, int g_dtype,
+                      float sN, double eps, void* out, int out_dtype, int64_t ldo, int8_t* q, int64_t ldq,
+                      float* asc, float* S, void* stream);
+
+/* The pinned tree over given leaves (replaces t16n_ref.tree_sum, reference/t16n_ref.py:42-50):
+ * T(v) = fl32(T(v[:P]) + T(v[P:])), P the largest power of two below n.  v: [R, n] binary32
+ * (row stride ldv), 1 <= n <= 65536; out: [R]. */
+int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, void* stream);
+
 /* Tuning control with no counterpart in the reference: force the dense kernel
  * (0: 128x128 register-staged tile, 4 waves of 64x64; 1: ping-pong 256x256, 8 waves of 64x128;
  * 2: ping-pong 256x256, 8 waves of 128x64; 3: ping-pong 256x128, 8 waves of 64x64;

@@ -48,6 +48,9 @@ SIGNATURES = {
     "lsk_planes_linear_workspace": (_I64, [_I64, _I64, _I64, _I, _I]),
     "lsk_planes_linear": (_I, [_P, _I, _I64, _I64, _I64, _I, _P, _P, _I64, _I64, _I, _P, _P, _P, _I, _I64, _P, _I64,
                                _P]),
+    "lsk_rmsnorm_float": (_I, [_P, _I, _I64, _I64, _I64, _P, _I, ctypes.c_float, ctypes.c_double, _P, _I, _I64, _P,
+                               _I64, _P, _P, _P]),
+    "lsk_tree_sum": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lsk_gemm_select": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
     "lsk_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),

@@ -21,6 +21,8 @@ Pinning (how each function is checked, see tests/test_oracle_*.py):
   int_mm_mx: one-block closed form, equal-exponent integer identity, scalar brute force,
       and a negative control (reversed block order differs)
   router / combine / moe_forward*: scalar brute force in Python ints and numpy float32
+  row_sum_float / rmsnorm_float (contract 2.6 float norm): the digests norm_float.*, a
+      rational brute force of the tree, the zero-padded balanced tree identity
   outlier_side / w8a8_outlier_linear: the digests outlier.*, linear.v2_5.*, linear.v2_5_1.*
   quant_rows_bits / planes / quantize_weight_bits / mm_planes: rowquant at 8 bits (digest-pinned),
       rational brute force of the quant at 11 / 15 bits, the plane identity (hi << sh) + lo = a,
@@ -385,6 +387,66 @@ def smooth_scales(act_amax, W, alpha):
     a_amax = np.maximum(np.asarray(act_amax, F32), F32(1e-5))
     s = (np.power(a_amax, F32(alpha)) / np.power(w_amax, F32(1.0 - alpha))).astype(F32)
     return np.maximum(s, F32(1e-5)).astype(F32)
+
+
+# ----------------------------------------------------------------------------- contract 2.6 float norm
+FLT_MIN_NORMAL = F32(2.0 ** -126)
+
+
+def sqrt_n(N):
+    """t16n_ref.py:38-39: the published width constant fl32(sqrt(N)) (binary64 sqrt, one rounding)."""
+    return F32(np.sqrt(np.float64(N)))
+
+
+def tree_sum(v):
+    """t16n_ref.py:42-50: T(one value) = the value; T(v) = fl32(T(v[:P]) + T(v[P:])) with P the
+    largest power of two below n (a power-of-two count is halved).  v [R, n] -> [R]."""
+    v = np.asarray(v, F32)
+    n = v.shape[1]
+    if n == 1:
+        return v[:, 0].copy()
+    P = 1 << (n.bit_length() - 1)
+    if P == n:
+        P = n // 2
+    return (tree_sum(v[:, :P]) + tree_sum(v[:, P:])).astype(F32)
+
+
+def row_sum_float(x2):
+    """t16n_ref.py:53-62: sq = fl32(x * x); chains of 8 in index order; then tree_sum over groups."""
+    x = np.asarray(x2, F32)
+    R, N = x.shape
+    assert N % 8 == 0
+    sq = (x * x).astype(F32).reshape(R, N // 8, 8)
+    a = sq[:, :, 0].copy()
+    for i in range(1, 8):
+        a = (a + sq[:, :, i]).astype(F32)
+    return tree_sum(a)
+
+
+def eps_term(N, eps):
+    """t16n_ref.py:65-67: ne = fl32(fl64(N) * fl64(eps))."""
+    return F32(np.float64(N) * np.float64(eps or 0.0))
+
+
+def rmsnorm_float(x, weight, sN=None, eps=0.0):
+    """t16n_ref.py:70-92: S = row_sum_float, + ne when eps, max(S, 2^-126); rs = fl32(sN / fl32(sqrt S))
+    (IEEE sqrt and division); out = bf16(fl32(fl32(x * rs) * g)).  x [..., N] binary32 values; returns
+    bf16 bits of the input shape."""
+    x = np.asarray(x, F32)
+    shp = x.shape
+    N = shp[-1]
+    x2 = x.reshape(-1, N)
+    sN = sqrt_n(N) if sN is None else F32(sN)
+    S = row_sum_float(x2)
+    if eps:
+        S = (S + eps_term(N, eps)).astype(F32)
+    S = np.maximum(S, FLT_MIN_NORMAL).astype(F32)
+    rs = (sN / np.sqrt(S).astype(F32)).astype(F32)
+    y = (x2 * rs[:, None]).astype(F32)
+    g = np.asarray(weight, F32).reshape(-1)
+    if not np.all(g == 1.0):
+        y = (y * g[None, :]).astype(F32)
+    return bf16_bits(y).reshape(shp)
 
 
 # ----------------------------------------------------------------------------- rotation

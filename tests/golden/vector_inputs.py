@@ -74,3 +74,19 @@ def outlier_inputs():
     W5 = _bf16(g5.randn(96, 512) * F32(0.05))
     oidx = np.array([17, 300, 511], dtype=np.int32)
     return x5, W5, oidx
+
+
+def norm_float_inputs():
+    """tools/contract_vectors.py:155-164 (contract 2.6 float norm, its own stream): for N, eps in
+    (4096, 1e-6), (3072, 1e-5), (128, 1e-6): x bf16 [6, N] = randn * 2 with row 1 zero, x[2, 7] = 3
+    and row 3 = bf16(randn(N) * 1e-19); gain ones, or bf16(1 + 0.1 randn(N)) at N = 128."""
+    g3 = _Gen(2026_09_10)
+    out = []
+    for N, eps in ((4096, 1e-6), (3072, 1e-5), (128, 1e-6)):
+        xn = _bf16(g3.randn(6, N) * F32(2))
+        xn[1] = 0
+        xn[2, 7] = 3.0
+        xn[3] = _bf16(g3.randn(N) * F32(1e-19))
+        wn = np.ones(N, F32) if N != 128 else _bf16((F32(1.0) + F32(0.1) * g3.randn(N)).astype(F32))
+        out.append((N, eps, xn, wn))
+    return out

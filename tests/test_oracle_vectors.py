@@ -133,3 +133,36 @@ def test_frac_table_digest():
     t = C.frac_table()
     assert t.shape == (8192,)
     assert t.min() >= 1 << 14 and t.max() <= 1 << 15
+
+
+def test_norm_float_digests():
+    from vector_inputs import norm_float_inputs
+    for N, eps, xn, wn in norm_float_inputs():
+        _check("norm_float.N%d.out" % N, C.rmsnorm_float(xn, wn, eps=eps), "bfloat16")
+        _check("norm_float.N%d.S" % N, C.row_sum_float(xn), "float32")
+
+
+def test_tree_equals_negzero_padded_perfect_tree():
+    """The kernels evaluate the pinned tree as a perfect pairwise tree over leaves padded with -0
+    to a power of two; the two are the same function (x + (-0) == x in binary32), including
+    signed zeros, while +0 padding is not (a negative control)."""
+    r = np.random.default_rng(0)
+
+    def perfect(v, pad):
+        n = v.shape[1]
+        P = 1 << max(0, (n - 1).bit_length())
+        w = np.full((v.shape[0], P), pad, np.float32)
+        w[:, :n] = v
+        h = 1
+        while h < P:
+            w[:, 0::2 * h] = (w[:, 0::2 * h] + w[:, h::2 * h]).astype(np.float32)
+            h *= 2
+        return w[:, 0]
+
+    for n in (1, 2, 3, 5, 6, 7, 9, 100, 384, 448, 1000):
+        v = (r.standard_normal((6, n)) * np.exp2(r.integers(-30, 30, (6, n)))).astype(np.float32)
+        v[0] = -0.0
+        v[1, ::2] = -0.0
+        assert np.array_equal(C.tree_sum(v).view(np.uint32), perfect(v, -0.0).view(np.uint32)), n
+    v = np.full((1, 3), -0.0, np.float32)
+    assert C.tree_sum(v).view(np.uint32)[0] != perfect(v, 0.0).view(np.uint32)[0]
