@@ -363,6 +363,13 @@ int lsk_moe_forward(const lsk_moe_args* args, void* stream);
  * choice.  Process-wide. */
 int lsk_moe_select(int variant);
 
+/* Tuning control with no counterpart in the reference: the main loop of the grouped MXFP4
+ * expert GEMMs (0: direct-to-LDS operand staging with fp4 fragments converted per wave, a
+ * two-stage ring, three blocks per CU, the default; 1: register-staged operands converted to bf16
+ * before LDS; 2: as 0 with a three-stage ring and two blocks per CU).  Results are identical; only
+ * speed differs.  Process-wide, not thread-safe against concurrent launches. */
+int lsk_moe_mx_select(int variant);
+
 #ifdef __cplusplus
 }
 #endif

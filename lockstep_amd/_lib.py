@@ -64,6 +64,7 @@ SIGNATURES = {
     "lsk_moe_workspace": (_I64, [_I64, _I, _I64, _I64, _I64, _I, _I]),
     "lsk_moe_forward": (_I, [_P, _P]),
     "lsk_moe_select": (_I, [_I]),
+    "lsk_moe_mx_select": (_I, [_I]),
 }
 
 

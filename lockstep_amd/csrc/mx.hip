@@ -2,6 +2,7 @@
 // E2M1/E8M0 dequant, and the doubled-mantissa packer.  See mx_tile.h for the exactness argument.
 #include "contract_act.h"
 #include "moe_internal.h"
+#include "mx_pp.h"
 #include "mx_tile.h"
 
 namespace {
@@ -115,54 +116,28 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(const int8_t* __restrict__
 // ---------------------------------------------------------------- grouped MX GEMM (MoE)
 // MODE 0: gate/up + activation (tile columns interleave 16 gate / 16 up weight rows); MODE 1:
 // down + routing weight into the token-major slot rows.
-template <int MODE, bool SAFE>
-__global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
-  extern __shared__ char mx_smem[];
-  const int ntiles = MODE == 0 ? (a.N + 63) / 64 : (a.N + 127) / 128;
-  const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
-  const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
-  if (mt >= a.tiles[0]) return;
-  const int e = a.tiles[1 + 2 * mt];
-  const int p0 = a.tiles[2 + 2 * mt];
-  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
-  const uint8_t* wb = (const uint8_t*)a.w_ptrs[e];
-  const uint8_t* sb = (const uint8_t*)a.ws_ptrs[e];
-  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
-  const uint16_t* A = (const uint16_t*)a.A;
+
+// Weight row of tile row r (tile column block nt), or -1.
+template <int MODE>
+LSK_DEV int moe_mx_wrow(const lsk::MoeGemmArgs& a, int nt, int r) {
+  if (MODE == 0) {
+    const int blk = r >> 4;
+    const int hc = nt * 64 + (blk >> 1) * 16 + (r & 15);
+    return hc < a.N ? ((blk & 1) ? a.N + hc : hc) : -1;
+  }
+  const int n = nt * 128 + r;
+  return n < a.N ? n : -1;
+}
+
+// The tile's epilogue from the binary32 block accumulators (128 x 128, four waves of 64 x 64):
+// MODE 0 the gate / up values and the activation into h (with its row maxima); MODE 1 the
+// routing-weighted down values into the token-major slot rows.
+template <int MODE>
+LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int nt, int p0, int p1, const float* bias,
+                             char* smem) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / 2, wn = wave % 2;
-
-  auto wrow = [&](int r) -> int {  // weight row of tile row r, or -1
-    if (MODE == 0) {
-      const int blk = r >> 4;
-      const int hc = nt * 64 + (blk >> 1) * 16 + (r & 15);
-      return hc < a.N ? ((blk & 1) ? a.N + hc : hc) : -1;
-    }
-    const int n = nt * 128 + r;
-    return n < a.N ? n : -1;
-  };
-  auto rowA = [&](int r) -> const void* {
-    const int p = p0 + r;
-    if (p >= p1) return nullptr;
-    const int src = MODE == 0 ? a.row_tok[p] : p;
-    return (const void*)(A + (int64_t)src * a.lda);
-  };
-  auto rowB = [&](int r) -> const uint8_t* {
-    const int w = wrow(r);
-    return w >= 0 ? wb + (int64_t)w * a.ldw : nullptr;
-  };
-  auto rowS = [&](int r) -> const uint8_t* {
-    const int w = wrow(r);
-    return w >= 0 ? sb + (int64_t)w * a.lds : nullptr;
-  };
-  typename Cfg::Acc acc;
-#pragma unroll
-  for (int i = 0; i < Cfg::TM; ++i)
-#pragma unroll
-    for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  lsk::mx_mainloop<128, 128, 2, 2, NB, false, true, SAFE>(acc, rowA, rowB, rowS, a.K, mx_smem);
-
-  float* region = (float*)mx_smem + wave * Cfg::kStripFloats;
+  float* region = (float*)smem + wave * Cfg::kStripFloats;
 #pragma unroll
   for (int i = 0; i < Cfg::TM; ++i) {
     lsk::stage_strip_f<Cfg::TN, Cfg::kLdc>(acc[i], region);
@@ -242,6 +217,84 @@ __global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
   }
 }
 
+// Register-staged main loop (mx_tile.h), kept as a selectable variant.
+template <int MODE, bool SAFE>
+__global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
+  extern __shared__ char mx_smem[];
+  const int ntiles = MODE == 0 ? (a.N + 63) / 64 : (a.N + 127) / 128;
+  const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
+  const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
+  if (mt >= a.tiles[0]) return;
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  const uint8_t* wb = (const uint8_t*)a.w_ptrs[e];
+  const uint8_t* sb = (const uint8_t*)a.ws_ptrs[e];
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  const uint16_t* A = (const uint16_t*)a.A;
+  auto rowA = [&](int r) -> const void* {
+    const int p = p0 + r;
+    if (p >= p1) return nullptr;
+    const int src = MODE == 0 ? a.row_tok[p] : p;
+    return (const void*)(A + (int64_t)src * a.lda);
+  };
+  auto rowB = [&](int r) -> const uint8_t* {
+    const int w = moe_mx_wrow<MODE>(a, nt, r);
+    return w >= 0 ? wb + (int64_t)w * a.ldw : nullptr;
+  };
+  auto rowS = [&](int r) -> const uint8_t* {
+    const int w = moe_mx_wrow<MODE>(a, nt, r);
+    return w >= 0 ? sb + (int64_t)w * a.lds : nullptr;
+  };
+  typename Cfg::Acc acc;
+#pragma unroll
+  for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  lsk::mx_mainloop<128, 128, 2, 2, NB, false, true, SAFE>(acc, rowA, rowB, rowS, a.K, mx_smem);
+  moe_mx_epilogue<MODE>(a, acc, nt, p0, p1, bias, mx_smem);
+}
+
+// Direct-to-LDS main loop (mx_pp.h): the default.
+template <int MODE, bool SAFE, int RING>
+__global__ __launch_bounds__(256, RING == 2 ? 3 : 2) void moe_mx_pp_kernel(lsk::MoeGemmArgs a) {
+  extern __shared__ char mx_smem[];
+  const int ntiles = MODE == 0 ? (a.N + 63) / 64 : (a.N + 127) / 128;
+  const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
+  const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
+  if (mt >= a.tiles[0]) return;
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  const int nrows_w = MODE == 0 ? 2 * a.N : a.N;  // weight rows of one expert
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = lsk::make_rsrc((const void*)a.w_ptrs[e], a.w_bytes);
+  const __amdgpu_buffer_rsrc_t rs = lsk::make_rsrc((const void*)a.ws_ptrs[e], (int64_t)nrows_w * a.lds);
+  const lsk::MxPPRows rows = lsk::mx_pp_rows(
+      [&](int r) -> uint32_t {
+        const int p = p0 + r;
+        if (p >= p1) return lsk::kOob;
+        const int src = MODE == 0 ? a.row_tok[p] : p;
+        return (uint32_t)((int64_t)src * a.lda * 2);
+      },
+      [&](int r) -> uint32_t {
+        const int w = moe_mx_wrow<MODE>(a, nt, r);
+        return w >= 0 ? (uint32_t)((int64_t)w * a.ldw) : lsk::kOob;
+      },
+      [&](int r) -> uint32_t {
+        const int w = moe_mx_wrow<MODE>(a, nt, r);
+        return w >= 0 ? (uint32_t)((int64_t)w * a.lds) : lsk::kOob;
+      });
+  typename lsk::MxPPCfg<RING>::Acc acc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  lsk::mx_pp_mainloop<SAFE, RING>(acc, ra, rb, rs, rows, a.K, mx_smem);
+  moe_mx_epilogue<MODE>(a, acc, nt, p0, p1, bias, mx_smem);
+}
+
 // ---------------------------------------------------------------- dequant and packing
 __global__ __launch_bounds__(256) void dequant_mxfp4_kernel(const uint8_t* __restrict__ packed,
                                                             const uint8_t* __restrict__ scale, int64_t rows, int64_t K,
@@ -301,20 +354,44 @@ unsigned grid_for(int64_t n) {
   return (unsigned)(b > 8192 ? 8192 : (b < 1 ? 1 : b));
 }
 
+int g_mx_variant = 0;  // grouped MX main loop: 0 direct-to-LDS, two-stage ring, three blocks per CU (mx_pp.h);
+                       // 1 register-staged (mx_tile.h); 2 direct-to-LDS, three-stage ring, two blocks per CU
+
 template <int MODE, bool SAFE>
 int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s) {
-  static bool attr = false;
-  auto kern = moe_mx_gemm_kernel<MODE, SAFE>;
-  if (!attr) {
-    if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "moe_mx_gemm_kernel")) return rc;
-    attr = true;
-  }
   const int ntiles = MODE == 0 ? (ga.N + 63) / 64 : (ga.N + 127) / 128;
   const int64_t blocks = max_tiles * ntiles;
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "moe_mx_gemm_kernel: grid too large");
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), Cfg::kSmemBytes, s, ga);
-  return lsk::check_launch(MODE == 0 ? "moe_mx_gemm_kernel<gate_up>" : "moe_mx_gemm_kernel<down>");
+  if (g_mx_variant == 1) {
+    static bool attr = false;
+    auto kern = moe_mx_gemm_kernel<MODE, SAFE>;
+    if (!attr) {
+      if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "moe_mx_gemm_kernel")) return rc;
+      attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), Cfg::kSmemBytes, s, ga);
+    return lsk::check_launch(MODE == 0 ? "moe_mx_gemm_kernel<gate_up>" : "moe_mx_gemm_kernel<down>");
+  }
+  static_assert(lsk::MxPPCfg<2>::kRingBytes >= Cfg::kEpiBytes, "the epilogue strips fit in the ring");
+  if (g_mx_variant == 0) {
+    static bool attr_pp2 = false;
+    auto kern = moe_mx_pp_kernel<MODE, SAFE, 2>;
+    if (!attr_pp2) {
+      if (int rc = reserve_lds(kern, lsk::MxPPCfg<2>::kRingBytes, "moe_mx_pp_kernel")) return rc;
+      attr_pp2 = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lsk::MxPPCfg<2>::kRingBytes, s, ga);
+    return lsk::check_launch(MODE == 0 ? "moe_mx_pp_kernel<gate_up>" : "moe_mx_pp_kernel<down>");
+  }
+  static bool attr_pp = false;
+  auto kern = moe_mx_pp_kernel<MODE, SAFE, 3>;
+  if (!attr_pp) {
+    if (int rc = reserve_lds(kern, lsk::MxPPCfg<3>::kRingBytes, "moe_mx_pp_kernel")) return rc;
+    attr_pp = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lsk::MxPPCfg<3>::kRingBytes, s, ga);
+  return lsk::check_launch(MODE == 0 ? "moe_mx_pp_kernel<gate_up>" : "moe_mx_pp_kernel<down>");
 }
 
 template <bool B_FP4, bool SAFE>
@@ -653,4 +730,10 @@ extern "C" int lsk_mx_epilogue(const float* acc, int64_t M, int64_t N, const flo
   hipLaunchKernelGGL(mx_epilogue_kernel, dim3(grid_for(M * N)), dim3(256), 0, (hipStream_t)stream, acc, M, N, asc, bias,
                      out);
   return lsk::check_launch("mx_epilogue_kernel");
+}
+
+extern "C" int lsk_moe_mx_select(int variant) {
+  LSK_REQUIRE(variant >= 0 && variant <= 2, "lsk_moe_mx_select: variant %d not in [0, 2]", variant);
+  g_mx_variant = variant;
+  return LSK_OK;
 }

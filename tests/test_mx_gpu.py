@@ -218,3 +218,44 @@ def test_moe_mx_tiles_and_gemv(variant, big_exp):
     with np.errstate(over="ignore", invalid="ignore"):
         ref = C.moe_forward_mx(x, oexp, idx, w, C.act_swigluoai)
     assert np.array_equal(u16(y), ref)
+
+
+@pytest.mark.parametrize("mxv", [0, 1, 2])
+@pytest.mark.parametrize("big_exp", [False, True])
+def test_moe_mx_grouped_main_loops(mxv, big_exp):
+    """Every main loop of the grouped MX GEMM (0 / 2: direct-to-LDS with a two / three-stage ring,
+    1: register-staged) on the tiled
+    path against the oracle: several 128-row tiles per expert, a half 64-wide K stage in both
+    projections (H = 352, I = 224), partial column tiles, biases, and optionally exponent bytes
+    >= 240 (the multiply-then-add update)."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    T, E, k, H, I = 600, 4, 2, 352, 224
+    say("mx grouped main loop", mxv, big_exp)
+    x, experts, logits = WL.moe_mx_inputs(T, E, k, H, I, seed=71, bias=True)
+    if big_exp:
+        p13, s13, p2, s2, b13, b2 = experts[2]
+        s2 = s2.copy()
+        s2[::7, 3] = 244
+        experts[2] = (p13, s13, p2, s2, b13, b2)
+    idx, w = routing_from_logits(logits, k)
+    oexp, dexp = [], []
+    for (p13, s13, p2, s2, b13, b2) in experts:
+        m13, _ = C.mx_to_m2(p13, s13)
+        m2_, _ = C.mx_to_m2(p2, s2)
+        oexp.append(((m13, s13), (m2_, s2), b13, b2))
+        dexp.append(((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2)))
+    dexp = MR.ExpertTablesMX(dexp, packed=True)
+    ridx, rw = routing_device(idx, w)
+    L.call("lsk_moe_select", 0)
+    L.call("lsk_moe_mx_select", mxv)
+    try:
+        y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai,
+                                    routing=(ridx, rw))
+    finally:
+        L.call("lsk_moe_select", -1)
+        L.call("lsk_moe_mx_select", 0)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx(x, oexp, idx, w, C.act_swigluoai)
+    assert np.array_equal(u16(y), ref)
