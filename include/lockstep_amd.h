@@ -208,7 +208,8 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * 4: ping-pong 128x256, 8 waves of 64x64; 5: the decode GEMV when M <= 32, else tile 0;
  * 6, 7: for M <= 4 the 8-row register-buffered / LDS-ring GEMV instead of the whole-row GEMV;
  * 8..11: the whole-row GEMV with 1 / 2 / 4 / 8 rows per wave; 12, 13: tiles 3, 4 with a
- * three-stage LDS ring, two blocks per CU) or -1 to choose by shape (the default).  Results are identical for every choice; only speed
+ * three-stage LDS ring, two blocks per CU; 14 / 15: for 4 < M <= 32 the GEMV reading 64-byte row
+ * pieces straight into registers / whole rows through LDS) or -1 to choose by shape (the default).  Results are identical for every choice; only speed
  * differs.  Process-wide, not thread-safe against concurrent launches. */
 int lsk_gemm_select(int tile_id);
 

@@ -373,6 +373,133 @@ __global__ __launch_bounds__(1024) void gemv_i8_stream_kernel(const int8_t* __re
     }
 }
 
+// Decode GEMV (4 < M <= 32) with whole-row weight streaming through LDS.  A block owns 16
+// weight rows; its NW waves split K into slices of whole SB-byte stages.  Each wave streams its
+// slice of the 16 rows into its own LDS ring by direct loads, each instruction reading 1024 / SB
+// whole SB-byte row segments (long contiguous runs stream faster from HBM than the MFMA
+// operand's 64-byte pieces), then reads them back in the v_mfma_i32_16x16x64_i8 B layout (chunk c
+// of row r stored at c ^ r: the 16 rows one LDS cycle serves hit distinct bank groups).  The
+// activation fragments (MT tiles of 16 rows) are loaded into registers one stage ahead.  A wave
+// waits only for its own loads (exact counts, no barrier in the loop); the K-slices' exact int32
+// sums are added in LDS and wave 0 applies the epilogue.  Rows past N, activation rows past M and
+// bytes past K load zeros through the buffer ranges.
+template <int MT, int SB, int R>
+__global__ __launch_bounds__(1024) void gemv_i8_lds_kernel(const int8_t* __restrict__ A, int lda,
+                                                           const int8_t* __restrict__ W, int ldw, int M, int N,
+                                                           int K, int kslice, EpiParams ep) {
+  extern __shared__ __attribute__((aligned(16))) char smem_lds[];
+  constexpr int kRPI = 1024 / SB;        // rows per load instruction
+  constexpr int kCPR = SB / 16;          // 16-byte chunks per row per stage
+  constexpr int kWL = 16 / kRPI;         // weight loads per lane per stage
+  constexpr int kKS = SB / 64;           // MFMA K-steps per stage
+  constexpr int kAL = kKS * MT;          // activation loads per lane per stage
+  constexpr int kStage = 16 * SB;        // bytes of one ring stage
+  const int lane = threadIdx.x & 63, wave = wave_id(), NW = blockDim.x >> 6;
+  const int n0 = blockIdx.x * 16;
+  const int nrows = (N - n0) < 16 ? (N - n0) : 16;
+  const int kb = wave * kslice;
+  const int ke = (kb + kslice) < K ? (kb + kslice) : K;
+  const int nst = ke > kb ? (ke - kb + SB - 1) / SB : 0;
+  char* ring = smem_lds + wave * R * kStage;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)nrows * ldw);
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(A, (int64_t)M * lda);
+
+  // this lane's weight slots: instruction j reads its row's logical chunk.  (The load offsets are
+  // computed into locals before the direct-load builtin: with the conditional expression inside
+  // its argument list the host pass silently emitted no launch stub for this kernel.)
+  struct Slots {
+    uint32_t off[kWL];  // byte offset of the slot's row
+    int k[kWL];         // byte offset of the slot's logical chunk within a stage
+  } ws_;
+#pragma unroll
+  for (int j = 0; j < kWL; ++j) {
+    const int row = j * kRPI + lane / kCPR;
+    ws_.off[j] = (uint32_t)(row * ldw);
+    ws_.k[j] = 16 * ((lane % kCPR) ^ row);
+  }
+  uint32_t arow[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) arow[t] = (t * 16 + (lane & 15) < M) ? (uint32_t)((t * 16 + (lane & 15)) * lda) : lsk::kOob;
+  const int ag = 16 * (lane >> 4);
+
+  auto issue_w = [&](int st) {
+    char* slot = ring + (st % R) * kStage;
+    const int k0 = kb + st * SB;
+#pragma unroll
+    for (int j = 0; j < kWL; ++j) {
+      const int kk = k0 + ws_.k[j];
+      const uint32_t off = kk < ke ? ws_.off[j] + (uint32_t)kk : lsk::kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lsk::lds_void_t)(slot + j * 1024), 16, off, 0, 0,
+                                               2 /* non-temporal */);
+    }
+  };
+  auto issue_a = [&](int st, v4i (&a)[kKS][MT]) {
+    const int k0 = kb + st * SB;
+#pragma unroll
+    for (int s = 0; s < kKS; ++s)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int kk = k0 + s * 64 + ag;
+        a[s][t] = lsk::buf_load16(ra, kk < ke ? arow[t] + (uint32_t)kk : lsk::kOob);
+      }
+  };
+  v4i acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = zero4();
+  const int rr = lane & 15;
+  auto compute = [&](int st, const v4i (&a)[kKS][MT]) {
+    const char* slot = ring + (st % R) * kStage + rr * SB;
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) {
+      const v4i w = *(const v4i*)(slot + 16 * ((4 * s + (lane >> 4)) ^ rr));
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = lsk::mfma_i8(a[s][t], w, acc[t]);
+    }
+  };
+  // issue order: A(0) W(0) W(1) | step t: A(t+1) W(t+2), then wait for everything up to A(t)
+  v4i a0[kKS][MT], a1[kKS][MT];
+  auto step = [&](int st, v4i (&acur)[kKS][MT], v4i (&anext)[kKS][MT]) {
+    const bool n1 = st + 1 < nst, n2 = st + 2 < nst;
+    if (n1) issue_a(st + 1, anext);
+    if (n2) issue_w(st + 2);
+    lsk::compiler_fence();
+    // younger than A(st): W(st+1), A(st+1), W(st+2) when issued
+    if (n2) lsk::wait_vm<2 * kWL + kAL>();
+    else if (n1) lsk::wait_vm<kWL + kAL>();
+    else lsk::wait_vm<0>();
+    compute(st, acur);
+  };
+  if (nst > 0) {
+    issue_a(0, a0);
+    issue_w(0);
+    if (nst > 1) issue_w(1);
+    for (int st = 0; st < nst; st += 2) {
+      step(st, a0, a1);
+      if (st + 1 < nst) step(st + 1, a1, a0);
+    }
+  }
+  // the K-slices: waves 1.. park their sums, wave 0 adds them in any order (exact) and stores
+  __syncthreads();
+  v4i* red = (v4i*)smem_lds;
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[((wave - 1) * MT + t) * 64 + lane] = acc[t];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w2 = 1; w2 < NW; ++w2)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] += red[((w2 - 1) * MT + t) * 64 + lane];
+  const int n = n0 + rr;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + 4 * (lane >> 4) + r;
+      if (m < M && n < N) epilogue_store(ep, m, n, acc[t][r]);
+    }
+}
+
 // Batch-few decode GEMV (M <= MR <= 8) on the VALU (v_dot4c_i32_i8), bandwidth-bound on the
 // weight stream.  A block is four waves; each wave owns 8 weight rows and one of WK K-slices
 // (WK = 1, 2 or 4 waves per row group).  Lane l reads 16 bytes of row l / 8 at chunk l % 8 of
@@ -777,6 +904,7 @@ int validate_epilogue(int order, int out_dtype, const float* asc, const float* w
 static int g_force_tile = -1;
 static int g_row_rpw = 0;       // rows per wave of the whole-row GEMV (0: by shape)
 static int g_gemv_variant = 0;  // M <= 4: 0 whole-row GEMV, 1 register double-buffered 8-row GEMV, 2 LDS-ring 8-row GEMV
+static int g_gemv_mid = 0;      // 4 < M <= 32: 0 by shape, 1 direct 64-byte row pieces, 2 whole rows through LDS
 
 template <int BM, int BN, int WM, int WN>
 static int launch_tile(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K,
@@ -834,6 +962,40 @@ static int pick_tile(int64_t M, int64_t N) {
   const int64_t r256 = ((M + 255) / 256 * ((N + 255) / 256) + 255) / 256;
   const int64_t r128 = ((M + 255) / 256 * ((N + 127) / 128) + 255) / 256;
   return (double)r128 * 0.68 < (double)r256 ? 3 : 1;
+}
+
+// Columns to cover with whole rounds of 256x256 tiles before finishing with 256x128 tiles, or 0
+// when one tile shape is cheaper: a launch of 256x256 tiles that ends in a partial round of 256
+// blocks leaves CUs idle through that round; splitting the columns so the 256x256 part fills
+// whole rounds and the rest takes 256x128 tiles (0.68 of a 256x256 tile's time) costs
+// rounds1 + 0.68 * rounds2 instead.
+static int64_t split_columns(int64_t M, int64_t N) {
+  if (M <= 128) return 0;
+  const int64_t mt = (M + 255) / 256;
+  const int64_t t256 = mt * ((N + 255) / 256);
+  const int64_t full = t256 / 256;
+  if (full == 0 || t256 % 256 == 0) return 0;
+  const int64_t nt1 = full * 256 / mt;  // 256-column tiles the whole rounds cover
+  const int64_t n1 = nt1 * 256;
+  if (n1 <= 0 || n1 >= N) return 0;
+  const int64_t r1 = (nt1 * mt + 255) / 256;
+  const int64_t r2 = (mt * ((N - n1 + 127) / 128) + 255) / 256;
+  const int64_t r256 = (t256 + 255) / 256;
+  const int64_t r128 = (mt * ((N + 127) / 128) + 255) / 256;
+  const double best_one = (double)r128 * 0.68 < (double)r256 ? (double)r128 * 0.68 : (double)r256;
+  return ((double)r1 + 0.68 * (double)r2 < best_one) ? n1 : 0;
+}
+
+// The epilogue parameters of the output columns from n1 on.
+static EpiParams shift_columns(const EpiParams& ep, int64_t n1) {
+  EpiParams e = ep;
+  const int esz = (ep.out_dtype == LSK_BF16 || ep.out_dtype == LSK_F16) ? 2 : 4;
+  e.out = (char*)ep.out + n1 * esz;
+  if (e.ws) e.ws += n1;
+  if (e.bias) e.bias += n1;
+  if (e.ecol) e.ecol += n1;
+  if (e.wo) e.wo = (const char*)e.wo + n1 * e.ko * (e.wo_dtype == LSK_BF16 ? 2 : 4);
+  return e;
 }
 
 // Waves per block of the decode GEMV: enough blocks x waves (about 8192) to keep every CU's
@@ -915,6 +1077,32 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
 #undef LSK_RING
   }
   const int blocks = (N + 15) / 16;
+  // whole-row streaming through LDS wins over 64-byte row pieces for one activation tile over a
+  // long K (measured on MI355X at the Llama-3.1-8B decode shapes: down K=14336 M=8 15.1 vs 19.6 us;
+  // gate_up K=4096 M=8 30.7 vs 28.8 us; two activation tiles 2x slower)
+  const bool use_lds = g_gemv_mid == 2 || (g_gemv_mid == 0 && M <= 16 && K >= 8192);
+  if (use_lds) {
+    // waves per block so that at least 1024 waves stream, each K-slice a whole number of
+    // 512-byte stages
+    constexpr int SB = 512, R = 3;
+    const int nstg = (K + SB - 1) / SB;
+    int nw = 1;  // up to four waves per block (96 KB of rings): at least 1024 waves stream
+    while (nw < 4 && (int64_t)blocks * nw < 1024 && nstg >= 2 * nw) nw *= 2;
+    const int kslice = ((nstg + nw - 1) / nw) * SB;
+    const size_t smem = (size_t)nw * R * 16 * SB;
+    if (smem > 160 * 1024) return set_error("gemv: %zu bytes of LDS exceed the 160 KB limit", smem), LSK_ERR_ARG;
+#define LSK_LDS(MTV)                                                                                          \
+  {                                                                                                           \
+    auto kern = gemv_i8_lds_kernel<MTV, SB, R>;                                                               \
+    if (smem > 65536 &&                                                                                       \
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) \
+      return set_error("gemv: cannot reserve LDS"), LSK_ERR_HIP;                                              \
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * nw), smem, s, a, lda, w, ldw, M, N, K, kslice, ep); \
+    return check_launch("gemv_i8_lds_kernel");                                                                \
+  }
+    if (M <= 16) LSK_LDS(1) else LSK_LDS(2)
+#undef LSK_LDS
+  }
   int kw = 1;
   while (kw < 16 && (int64_t)blocks * kw < 2048 && (int64_t)(kw * 2) * 64 * 4 * 2 <= K) kw *= 2;
   const int kslice = ((K + kw * 64 - 1) / (kw * 64)) * 64;
@@ -945,6 +1133,15 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
   if (M <= 32 && (g_force_tile < 0 || g_force_tile == 5)) return launch_gemv(a, (int)lda, w, (int)ldw, iM, iN, iK, ep, s);
   const int vec_ok = out_vec_ok(ep.out, ep.out_dtype, ep.ldo) ? 1 : 0;
   const int ilda = (int)lda, ildw = (int)ldw;
+  int64_t n1 = 0;
+  if (g_force_tile < 0 && (n1 = split_columns(M, N)) > 0) {
+    // whole rounds of 256x256 tiles over the first n1 columns, the rest in 256x128 tiles
+    int rc = launch_pp<256, 256, 4, 2>(a, ilda, w, ildw, iM, (int)n1, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,4x2>");
+    if (rc) return rc;
+    const EpiParams ep2 = shift_columns(ep, n1);
+    return launch_pp<256, 128, 4, 2>(a, ilda, w + n1 * ldw, ildw, iM, (int)(N - n1), iK, ep2,
+                                     out_vec_ok(ep2.out, ep2.out_dtype, ep2.ldo) ? 1 : 0, s, "gemm_i8_pp<256x128,4x2>");
+  }
   switch (pick_tile(M, N)) {
     case 1: return launch_pp<256, 256, 4, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,4x2>");
     case 2: return launch_pp<256, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x256,2x4>");
@@ -1022,8 +1219,9 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 13, "lsk_gemm_select: tile id %d not in [-1, 13]", tile_id);
-  lsk::g_force_tile = (tile_id >= 6 && tile_id <= 11) ? 5 : tile_id;
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 15, "lsk_gemm_select: tile id %d not in [-1, 15]", tile_id);
+  lsk::g_force_tile = ((tile_id >= 6 && tile_id <= 11) || tile_id == 14 || tile_id == 15) ? 5 : tile_id;
+  lsk::g_gemv_mid = tile_id == 14 ? 1 : (tile_id == 15 ? 2 : 0);
   lsk::g_gemv_variant = (tile_id == 6 || tile_id == 7) ? tile_id - 5 : 0;
   lsk::g_row_rpw = (tile_id >= 8 && tile_id <= 11) ? (1 << (tile_id - 8)) : 0;
   return LSK_OK;

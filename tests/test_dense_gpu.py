@@ -245,9 +245,10 @@ def test_config2_prefill_rows_and_chunk_invariance(which):
     assert torch.equal(chunks.view(torch.int16), y.view(torch.int16))
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15])
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 257, 640), (512, 520, 2880), (64, 64, 16),
-                                   (1, 1000, 14336), (3, 77, 2880), (4, 300, 1040)])
+                                   (1, 1000, 14336), (3, 77, 2880), (4, 300, 1040), (8, 1000, 4096),
+                                   (17, 77, 2880), (32, 520, 14336), (5, 33, 48)])
 def test_every_tile_config_is_exact(tile, M, N, K):
     """The forced tile configurations produce the same bits (exact integer sums, any tiling)."""
     from lockstep_amd import _lib as L
@@ -322,3 +323,27 @@ def test_epilogue_special_scales(tile, out):
         assert np.array_equal(np.isnan(gf), nan)
         assert np.array_equal(got[~nan], f32_bits(ref)[~nan])
     assert acc[30, 20] != 0 and np.isinf(C.out_to_f32(ref, out)[30, 20])  # the case is present
+
+
+@pytest.mark.parametrize("N", [33024, 33064])
+def test_column_split_into_whole_rounds_is_exact(N):
+    """Shapes whose 256x256 tiles end in a partial round run as whole rounds of 256x256 tiles
+    over the first columns plus 256x128 tiles over the rest; every epilogue sees shifted column
+    operands (ws, bias, the outlier weights): the results equal the oracle's bit for bit."""
+    from lockstep_amd import lockstep_fullstack as FS
+    M, K = 300, 256
+    say("column split", M, N, K)
+    r = _rng(N)
+    x = C.bfr((r.standard_normal((M, K)) * 2).astype(F32))
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    bias = (r.standard_normal(N) * 0.1).astype(F32)
+    y = FS.w8a8_matmul(to_dev(x), to_dev(W8), to_dev(ws), to_dev(bias), out_dtype=torch.bfloat16)
+    assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, bias, "bf16"))
+    acc = FS._int_mm_exact(to_dev(C.rowquant(x)[0]), to_dev(W8).t())
+    assert np.array_equal(bits(acc), C.int_mm(C.rowquant(x)[0], W8.T))
+    oidx = np.array([3, 77, 200], dtype=np.int32)
+    wo = C.bfr((r.standard_normal((N, 3)) * 0.05).astype(F32))
+    yo = FS.w8a8_outlier_linear(bf16_dev(x), to_dev(oidx), bf16_dev(wo), to_dev(W8), to_dev(ws), to_dev(bias),
+                                out_dtype=torch.bfloat16)
+    assert np.array_equal(bits(yo), C.w8a8_outlier_linear(x, oidx, wo, W8, ws, bias, "bf16"))
