@@ -2,6 +2,7 @@
 """Benchmark of the contract matrix-multiply path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sections dense,decode,moe]
+                    [--moe-cases NAME,...] [--eager] [--mx-variant V]
 
 A step is one pass of the Llama-3.1-8B-shaped MLP contract GEMMs at M=2048 prefill rows:
 w8a8_matmul (row quant + exact int8 GEMM + v2.1 epilogue, bf16 out) of the gate+up projection
@@ -100,10 +101,17 @@ def dense_section(torch, args):
     }
 
 
+EAGER = False  # --eager: time the decode and MoE calls as plain launches (no HIP graph)
+
+
 def _graph_time(torch, calls, reps):
     """Average milliseconds per call of the callables in `calls`, captured once into a HIP graph
     (so host overhead between launches is not timed) and replayed `reps` times; HIP events on
-    the replay stream."""
+    the replay stream.  With --eager the calls are launched directly `reps` times instead."""
+    if EAGER:
+        for fn in calls:
+            fn()
+        return _events_time(torch, lambda: [fn() for fn in calls], reps) / len(calls)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -242,6 +250,8 @@ def moe_section(torch, args):
         act = MR.act_swigluoai if mx else MR.act_silu
         fwd = MR.moe_forward_mx if mx else MR.moe_forward
         for T in (1, 32, 4096):
+            if args.moe_cases and "%s_T%d" % (name, T) not in args.moe_cases.split(","):
+                continue
             x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
             logits = torch.randn((T, E), generator=g, device=dev)
             if not mx:
@@ -334,6 +344,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sections", default="dense,decode,moe")
+    ap.add_argument("--moe-cases", default="", help="comma list of MoE cases to run, e.g. gpt_oss_20b_mxfp4_T4096 "
+                                                     "(default: all)")
+    ap.add_argument("--eager", action="store_true", help="time decode / MoE calls as plain launches, no HIP graphs "
+                                                         "(for profilers that count per dispatch)")
+    ap.add_argument("--mx-variant", type=int, default=0, help="main loop of the grouped MXFP4 GEMMs "
+                                                              "(lsk_moe_mx_select; 0 is the default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (N=%d requested)" % args.gpus,
@@ -346,6 +362,9 @@ def main():
     from lockstep_amd import _lib
     _lib.load()
     sections = set(args.sections.split(","))
+    global EAGER
+    EAGER = args.eager
+    _lib.call("lsk_moe_mx_select", args.mx_variant)
 
     log("bench: dense prefill step (M=2048, gate_up 28672x4096 + down 4096x14336)")
     d = dense_section(torch, args)
