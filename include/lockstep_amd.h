@@ -237,6 +237,29 @@ int lsk_gemm_mx(const int8_t* a, int64_t lda, const void* b, int b_fmt, int64_t 
                 int64_t lds, int64_t M, int64_t N, int64_t K, int epilogue, const float* asc, const float* bias,
                 float* out, int64_t ldo, void* stream);
 
+/* Block quant of activations (block-scaled activations, contract addendum item 5b).  Replaces
+ * moe_ref.blockquant (reference/moe_ref.py:299-314): per 32-wide block of each row,
+ * ka = the least k with 127 * 2^k >= max |x| (the reference's ceil(log2(max / 127)) with its
+ * rounding guard), clamped to [-126, 127], -126 for an all-zero block; q = clamp(rint(x / 2^ka),
+ * +-127).  x: [M, K] bf16 or f32 (x_dtype, row stride ldx, rows 16-byte aligned); q: [M, K] int8
+ * (row stride ldq, a multiple of 8); ka: [M, K/32] int32 (row stride ldka).  K % 32 == 0.
+ * Infinite inputs give ka = 127, q = +-127; NaN inputs are not supported (the reference's int8
+ * conversion of NaN is undefined). */
+int lsk_blockquant(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int8_t* q, int64_t ldq, int32_t* ka,
+                   int64_t ldka, void* stream);
+
+/* The MX operand with block-scaled activations.  Replaces moe_ref.int_mm_mx2 and, with
+ * epilogue = 1, its bfr epilogue (reference/moe_ref.py:317-339):
+ *   for each 32-wide K block b, ascending: s = sum_{j in b} q[m, j] * m2[n, j] (exact);
+ *   p = fl32(2^(ka[m, b] + kexp[n, b] - 128)) (0 below 2^-149, inf from 2^128);
+ *   acc = fl32(acc + fl32(s * p)), from +0;
+ *   epilogue 0: out = acc; 1: out = bfr(acc), then bfr(out + bias[n]) when bias is given.
+ * q: [M, K] int8 (row stride ldq, 16-byte aligned rows); ka: [M, K/32] int32 (row stride ldka);
+ * weights and kexp as lsk_gemm_mx; out: [M, N] binary32 (row stride ldo).  K % 32 == 0. */
+int lsk_gemm_mx2(const int8_t* q, int64_t ldq, const int32_t* ka, int64_t ldka, const void* b, int b_fmt, int64_t ldb,
+                 const uint8_t* kexp, int64_t lds, int64_t M, int64_t N, int64_t K, int epilogue, const float* bias,
+                 float* out, int64_t ldo, void* stream);
+
 /* The MX epilogue alone (replaces moe_ref.lin_epilogue_mx, reference/moe_ref.py:258-261):
  * out = bfr(acc[m, n] * asc[m]), then bfr(out + bias[n]) when bias is given.  acc, out:
  * [M, N] binary32 contiguous (out may equal acc). */
@@ -302,8 +325,8 @@ int lsk_fwht_blocks(const float* x, int64_t rows, int64_t D, int64_t ldx, int bl
                     int64_t ldy, void* stream);
 
 /* The whole contract v3 MoE layer with int8 or MXFP4 experts and injected routing.
- * Replaces moe_ref.moe_forward / moe_forward_b / moe_forward_mx with routing=(idx, w)
- * (reference/moe_ref.py:117-140, 189-200, 213-230, 264-290):
+ * Replaces moe_ref.moe_forward / moe_forward_b / moe_forward_mx / moe_forward_mx2 with
+ * routing=(idx, w) (reference/moe_ref.py:117-140, 189-200, 213-230, 264-290, 329-352):
  *   for each expert e ascending and the tokens that chose it: rowquant(x) -> exact GEMM with
  *   w13[e] -> bfr(V21 epilogue) (+ bfr(+ b13)) -> act(gate, up) -> rowquant -> exact GEMM with
  *   w2[e] -> bfr(V21) (+ bfr(+ b2)); y[t] = bf16(sum over t's experts ascending of
@@ -326,7 +349,9 @@ typedef struct {
   int wfmt;                      /* 0: int8 experts; 1: MXFP4 experts (moe_forward_mx): w13/w2 tables
                                     point at packed E2M1 codes [N, K/2] (low nibble first, row stride
                                     ldw* bytes) and ws13/ws2 tables at their E8M0 bytes [N, K/32]
-                                    (row stride lds* bytes); K % 32 == 0 */
+                                    (row stride lds* bytes); K % 32 == 0; 2: MXFP4 experts with
+                                    block-scaled activations (moe_forward_mx2: blockquant instead of
+                                    rowquant, lsk_gemm_mx2's update, epilogues bfr(acc) (+ bias)) */
   int mx_safe;                   /* MXFP4: 1 when some E8M0 byte is >= 240 (exact multiply-then-add
                                     block update instead of the fused one) */
   int64_t lds13, lds2;           /* MXFP4: E8M0 row strides */
@@ -349,6 +374,9 @@ typedef struct {
   uint16_t* y;                   /* [T, H] bf16 */
   void* workspace;
   int64_t workspace_bytes;
+  int kw13_min, kw13_max;        /* wfmt 2: bounds of the E8M0 bytes of all w13 / w2 weights (any */
+  int kw2_min, kw2_max;          /* bounds that contain them keep results exact; tighter bounds let
+                                    more rows take the fused block update) */
 } lsk_moe_args;
 
 int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt);

@@ -974,6 +974,10 @@ struct MoeWs {
   uint16_t* slots;
   float* xrot;
   uint16_t* gu;  // decode path: bias-added gate and up values [R, 2I] bf16 (T <= kGemvMaxT)
+  int32_t* kax;    // block-scaled activations: block exponents of x [T, H/32] and of h [R, I/32],
+  int32_t* flagx;  // and the row flags of each
+  int32_t* kah;
+  int32_t* flagh;
   int64_t bytes;
   int64_t max_tiles;
 };
@@ -983,7 +987,7 @@ inline int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
 constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
 
 MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt) {
-  const int64_t qb = wfmt == 1 ? 2 : 1;  // bytes per quantised activation element
+  const int64_t qb = wfmt >= 1 ? 2 : 1;  // bytes per quantised activation element
   MoeWs w{};
   const int64_t R = T * k;
   w.max_tiles = R / kBM + (E < R ? E : R);
@@ -1011,6 +1015,12 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.slots = (uint16_t*)take(R * H * 2);
   w.xrot = rot_blk > 0 ? (float*)take(T * H * 4) : nullptr;
   w.gu = T <= kGemvMaxT ? (uint16_t*)take(R * 2 * I * 2) : nullptr;
+  if (wfmt == 2) {
+    w.kax = (int32_t*)take(T * (H / 32) * 4);
+    w.flagx = (int32_t*)take(T * 4);
+    w.kah = (int32_t*)take(R * (I / 32) * 4);
+    w.flagh = (int32_t*)take(R * 4);
+  }
   w.bytes = off;
   return w;
 }
@@ -1124,7 +1134,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   if (T == 0) return LSK_OK;
   LSK_REQUIRE(a->x && a->idx && a->w && a->w13_ptrs && a->ws13_ptrs && a->w2_ptrs && a->ws2_ptrs && a->frac && a->y,
               "lsk_moe_forward: null pointer");
-  if (a->wfmt == 1) {
+  if (a->wfmt >= 1) {
     LSK_REQUIRE(a->ldw13 >= H / 2 && a->ldw13 % 16 == 0 && a->ldw2 >= I / 2 && a->ldw2 % 16 == 0 &&
                     a->lds13 >= H / 32 && a->lds2 >= I / 32,
                 "lsk_moe_forward: MXFP4 row strides must cover K/2 (multiples of 16) and K/32");
@@ -1138,7 +1148,17 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(rb == 0 || (rb >= 2 && rb <= 1024 && (rb & (rb - 1)) == 0 && H % rb == 0 && I % rb == 0 && I <= 16384),
               "lsk_moe_forward: rot_blk=%d must be 0 or a power of two dividing H and I (I <= 16384)", rb);
   const int mx = a->wfmt;
-  LSK_REQUIRE(mx == 0 || mx == 1, "lsk_moe_forward: unknown weight format %d", mx);
+  LSK_REQUIRE(mx == 0 || mx == 1 || mx == 2, "lsk_moe_forward: unknown weight format %d", mx);
+  LSK_REQUIRE(mx != 2 || (0 <= a->kw13_min && a->kw13_min <= a->kw13_max && a->kw13_max <= 255 && 0 <= a->kw2_min &&
+                          a->kw2_min <= a->kw2_max && a->kw2_max <= 255),
+              "lsk_moe_forward: E8M0 bounds must satisfy 0 <= min <= max <= 255");
+  // block-scaled activations: the fused update on the dequantised values q * 2^ka is exact while
+  // 2^ka stays in range for the MFMA block sums (ka <= 111) and every exponent ka + kexp - 128 of
+  // a nonzero block lies in [-149, 111] (239 - kexp with the fused FMA, 255 - kexp with the
+  // multiply-then-add update): no product underflows, overflows or rounds
+  const int lo13 = -21 - a->kw13_min, lo2 = -21 - a->kw2_min;
+  const int top = a->mx_safe ? 255 : 239;
+  const int hi13 = std::min(111, top - a->kw13_max), hi2 = std::min(111, top - a->kw2_max);
   LSK_REQUIRE(!mx || (rb == 0 && H % 32 == 0 && I % 32 == 0), "lsk_moe_forward: MXFP4 experts need K %% 32 == 0 "
               "and no rotation");
   const MoeWs w = moe_layout((char*)a->workspace, T, k, E, H, I, rb, mx);
@@ -1152,7 +1172,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   // the grouped GEMV for decode token counts (whole weight rows streamed once per tile)
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
   const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096;
-  const bool use_mx_gemv = gemv_ok && mx && H <= 8192 && I <= 8192;
+  const bool use_mx_gemv = gemv_ok && mx == 1 && H <= 8192 && I <= 8192;
 
   int rc;
   if (rb > 0) {
@@ -1163,6 +1183,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::check_launch("widen_bf16_kernel"))) return rc;
     if ((rc = lsk_fwht_blocks(w.xrot, T, H, H, rb, a->rot_scale, w.xrot, H, stream))) return rc;
     rc = lsk_rowquant(w.xrot, LSK_F32, T, H, H, w.qx, H, w.ascx, stream);
+  } else if (mx == 2) {
+    rc = lsk::launch_blockquant_mx2(a->x, H, T, nullptr, (int)H, (uint16_t*)w.qx, w.kax, w.flagx, lo13, hi13, s);
   } else if (mx) {
     rc = lsk::launch_rowquant_bf16(a->x, T, H, (uint16_t*)w.qx, w.ascx, s);
   } else {
@@ -1220,8 +1242,19 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g1.h = w.h;
   g1.h_amax = w.h_amax;
   g1.lds = a->lds13;
+  if (mx == 2) {
+    g1.a_scale = nullptr;
+    g1.row_flag = w.flagx;
+    g1.a_ka = w.kax;
+    g1.ldka = H / 32;
+  }
   if (use_mx_gemv) {
     if ((rc = lsk::launch_moe_mx_gemv(0, g1, w.max_tiles, T, a->mx_safe, w.gu, s))) return rc;
+  } else if (mx == 2) {
+    g1.mx2 = 1;
+    if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
+    g1.mx2 = 2;
+    if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (use_gemv) {
@@ -1248,6 +1281,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     hipLaunchKernelGGL(moe_rot_requant_kernel, dim3((unsigned)R), dim3(256), (size_t)I * 4, s, w.h, w.offs + E, (int)I,
                        rb, a->rot_scale, w.qh, w.asch);
     if ((rc = lsk::check_launch("moe_rot_requant_kernel"))) return rc;
+  } else if (mx == 2) {
+    if ((rc = lsk::launch_blockquant_mx2(w.h, I, R, w.offs + E, (int)I, (uint16_t*)w.qh, w.kah, w.flagh, lo2, hi2, s)))
+      return rc;
   } else if (mx) {
     if ((rc = lsk::launch_requant_bf16(w.h, w.h_amax, w.offs + E, R, (int)I, (uint16_t*)w.qh, w.asch, s))) return rc;
   } else {
@@ -1275,8 +1311,19 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g2.row_dst = w.row_dst;
   g2.y = w.slots;
   g2.lds = a->lds2;
+  if (mx == 2) {
+    g2.a_scale = nullptr;
+    g2.row_flag = w.flagh;
+    g2.a_ka = w.kah;
+    g2.ldka = I / 32;
+  }
   if (use_mx_gemv) {
     if ((rc = lsk::launch_moe_mx_gemv(1, g2, w.max_tiles, T, a->mx_safe, nullptr, s))) return rc;
+  } else if (mx == 2) {
+    g2.mx2 = 1;
+    if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
+    g2.mx2 = 2;
+    if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (use_gemv) {

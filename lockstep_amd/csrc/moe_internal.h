@@ -30,6 +30,12 @@ struct MoeGemmArgs {
   const float* row_w;       // down: routing weight per row
   const int32_t* row_dst;   // down: destination slot row
   uint16_t* y;              // down out [T * k, N] bf16
+  // block-scaled activations (MXFP4 experts, moe_forward_mx2): 0 off; 1 the fused-update kernel
+  // over tiles without a flagged row; 2 the general kernel over tiles with one
+  int mx2;
+  const int32_t* row_flag;  // per A row (gate/up: per token)
+  const int32_t* a_ka;      // block exponents of the A rows [rows, K/32]
+  int64_t ldka;
 };
 
 // MXFP4 grouped GEMMs (mode 0: gate/up + activation; 1: down + routing weight).
@@ -42,6 +48,11 @@ int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64
 
 // Row quant emitting the int8 values as bf16 (the MX GEMM's operand form).
 int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, float* asc, hipStream_t s);
+
+// Block quant of bf16 rows for block-scaled activations: dequantised bf16 values (integer values
+// on flagged rows), exponents [R, K/32] and row flags (exponent outside [lo, hi]).
+int launch_blockquant_mx2(const uint16_t* x, int64_t ldx, int64_t R, const int32_t* nrows, int K, uint16_t* q,
+                          int32_t* ka, int32_t* flag, int lo, int hi, hipStream_t s);
 
 // Requant of h (bf16 values) with per-row maxima, emitting bf16 int8 values.
 int launch_requant_bf16(const uint16_t* h, const uint32_t* amax, const int32_t* nrows, int64_t R, int I, uint16_t* q,

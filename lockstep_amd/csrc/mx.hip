@@ -64,9 +64,123 @@ __global__ __launch_bounds__(256) void requant_bf16_kernel(const uint16_t* __res
   }
 }
 
-// ---------------------------------------------------------------- dense MX GEMM (int_mm_mx)
-template <bool B_FP4, bool SAFE>
-__global__ __launch_bounds__(256) void mx_gemm_kernel(const int8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B,
+// ---------------------------------------------------------------- block quant (block-scaled activations)
+// moe_ref.py:299-314.  ka = the least k with 127 * 2^k >= am (am = max |x| over the 32-wide
+// block), clamped to [-126, 127]; -126 for an all-zero block.  With am = 1.f * 2^(be - 127) (its
+// binary32 fields), 127 * 2^k >= am  <=>  k >= be - 133 when 1.f <= 127/64 (fraction field
+// <= 0x7E0000), else k >= be - 132.  The reference's ceil(log2(fl32(am / 127))), raised by one
+// where fl32(127 * 2^ka) < am, is the same least k.  q = clamp(rint(x * 2^-ka), +-127): x * 2^-ka
+// and the reference's x / 2^ka are the same correctly rounded quotient.  Infinite inputs give
+// ka = 127 and q = +-127; NaN has no defined quantisation in the reference.
+LSK_DEV int mx2_block_exp(float am) {
+  const uint32_t u = __float_as_uint(am);
+  const int be = (int)(u >> 23);
+  if (be == 0) return -126;   // zero or subnormal
+  if (be >= 255) return 127;  // infinity
+  const int k = be - ((u & 0x7fffffu) <= 0x7e0000u ? 133 : 132);
+  return k < -126 ? -126 : k;
+}
+
+LSK_DEV float mx2_q(float v, float inv) { return fminf(fmaxf(rintf(f32_mul(v, inv)), -127.0f), 127.0f); }
+
+// 8 consecutive elements (bf16 bits or binary32) as binary32
+template <bool X_F32>
+LSK_DEV void load8(const void* x, int64_t off, float (&v)[8]) {
+  if (X_F32) {
+    const float4 a = *(const float4*)((const float*)x + off), b = *(const float4*)((const float*)x + off + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const uint4 u = *(const uint4*)((const uint16_t*)x + off);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bf16_to_f32((uint16_t)(w[j] & 0xffff));
+      v[2 * j + 1] = bf16_to_f32((uint16_t)(w[j] >> 16));
+    }
+  }
+}
+
+// the block maximum of the 8 values of this thread and the 3 neighbours sharing its block
+LSK_DEV float block_amax(const float (&v)[8]) {
+  float am = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) am = fmaxf(am, fabsf(v[t]));
+  am = fmaxf(am, __shfl_xor(am, 1, 64));
+  return fmaxf(am, __shfl_xor(am, 2, 64));
+}
+
+// x [M, K] -> q int8 [M, K], ka int32 [M, K/32].  One block per row; a thread quantises 8
+// consecutive elements and the 4 threads of a 32-wide block share its maximum (K % 32 == 0, so
+// the groups of 4 never straddle the loop's end).
+template <bool X_F32>
+__global__ __launch_bounds__(256) void blockquant_i8_kernel(const void* __restrict__ x, int64_t ldx, int K,
+                                                            int8_t* __restrict__ q, int64_t ldq, int32_t* __restrict__ ka,
+                                                            int64_t ldka) {
+  const int64_t r = blockIdx.x;
+  for (int c = threadIdx.x; c < K / 8; c += 256) {
+    float v[8];
+    load8<X_F32>(x, r * ldx + 8 * c, v);
+    const int e = mx2_block_exp(block_amax(v));
+    const float inv = pow2f(-e);
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) w[t >> 2] |= ((uint32_t)(int)mx2_q(v[t], inv) & 0xffu) << (8 * (t & 3));
+    *(uint2*)(q + r * ldq + 8 * c) = make_uint2(w[0], w[1]);
+    if ((c & 3) == 0) ka[r * ldka + c / 4] = e;
+  }
+}
+
+// Block quant of bf16 rows for the grouped MX GEMMs.  Each row gets the dequantised values
+// q * 2^ka as bf16 (exact: |q| <= 127 has 7 significant bits and 2^ka is in range whenever the
+// row is not flagged), its exponents ka [rows, K/32] and a flag set when some nonzero block has
+// ka outside [lo, hi], the range in which the fused block update on the dequantised values is
+// exact for the experts' weight exponents.  A flagged row is rewritten with the integer values q
+// (as bf16), which the general kernel pairs with ka.  One block per row; rows from *nrows on
+// (when given) are skipped; q and ka rows are packed (strides K and K/32).
+__global__ __launch_bounds__(256) void blockquant_mx2_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                             const int32_t* __restrict__ nrows, int K,
+                                                             uint16_t* __restrict__ q, int32_t* __restrict__ ka,
+                                                             int32_t* __restrict__ flag, int lo, int hi) {
+  const int64_t r = blockIdx.x;
+  if (nrows && r >= *nrows) return;
+  int bad = 0;
+  for (int c = threadIdx.x; c < K / 8; c += 256) {
+    float v[8];
+    load8<false>(x, r * ldx + 8 * c, v);
+    const float am = block_amax(v);
+    const int e = mx2_block_exp(am);
+    const float inv = pow2f(-e), sc = pow2f(e);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)f32_to_bf16(f32_mul(mx2_q(v[2 * j], inv), sc)) |
+             ((uint32_t)f32_to_bf16(f32_mul(mx2_q(v[2 * j + 1], inv), sc)) << 16);
+    *(uint4*)(q + r * K + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+    if ((c & 3) == 0) ka[r * (K / 32) + c / 4] = e;
+    if (am > 0.0f && (e < lo || e > hi)) bad = 1;
+  }
+  bad = __syncthreads_or(bad);
+  if (bad) {
+    for (int c = threadIdx.x; c < K / 8; c += 256) {
+      float v[8];
+      load8<false>(x, r * ldx + 8 * c, v);
+      const float inv = pow2f(-mx2_block_exp(block_amax(v)));
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)f32_to_bf16(mx2_q(v[2 * j], inv)) | ((uint32_t)f32_to_bf16(mx2_q(v[2 * j + 1], inv)) << 16);
+      *(uint4*)(q + r * K + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  if (threadIdx.x == 0) flag[r] = bad;
+}
+
+// ---------------------------------------------------------------- dense MX GEMM (int_mm_mx, int_mm_mx2)
+// ROWSCALE: the activation rows carry block exponents ka [M, K/32] (int_mm_mx2); asc == null: the
+// epilogue has no row scale (y = bfr(acc)).
+template <bool B_FP4, bool SAFE, bool ROWSCALE>
+__global__ __launch_bounds__(256) void mx_gemm_kernel(const int8_t* __restrict__ A, int64_t lda, const int32_t* __restrict__ KA,
+                                                      int64_t ldka, const uint8_t* __restrict__ B,
                                                       int64_t ldb, const uint8_t* __restrict__ S, int64_t lds, int M, int N,
                                                       int K, int epi, const float* __restrict__ asc,
                                                       const float* __restrict__ bias, float* __restrict__ out,
@@ -85,7 +199,8 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(const int8_t* __restrict__
   auto rowA = [&](int r) -> const void* { return m0 + r < M ? (const void*)(A + (int64_t)(m0 + r) * lda) : nullptr; };
   auto rowB = [&](int r) -> const uint8_t* { return n0 + r < N ? B + (int64_t)(n0 + r) * ldb : nullptr; };
   auto rowS = [&](int r) -> const uint8_t* { return n0 + r < N ? S + (int64_t)(n0 + r) * lds : nullptr; };
-  lsk::mx_mainloop<128, 128, 2, 2, NB, true, B_FP4, SAFE>(acc, rowA, rowB, rowS, K, mx_smem);
+  auto rowK = [&](int r) -> const int32_t* { return m0 + r < M ? KA + (int64_t)(m0 + r) * ldka : nullptr; };
+  lsk::mx_mainloop<128, 128, 2, 2, NB, true, B_FP4, SAFE, ROWSCALE>(acc, rowA, rowB, rowS, rowK, K, mx_smem);
 
   float* region = (float*)mx_smem + wave * Cfg::kStripFloats;
 #pragma unroll
@@ -102,7 +217,7 @@ __global__ __launch_bounds__(256) void mx_gemm_kernel(const int8_t* __restrict__
           if (n + t >= N) break;
           float v = region[row * Cfg::kLdc + c4 + t];
           if (epi) {
-            v = bfr(f32_mul(v, asc[m]));
+            v = bfr(asc ? f32_mul(v, asc[m]) : v);
             if (bias) v = bfr(f32_add(v, bias[n + t]));
           }
           out[(int64_t)m * ldo + n + t] = v;
@@ -151,7 +266,7 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
         const int hc0 = nt * 64 + wn * 32 + pair * 16 + c4;
         float am = 0.0f;
         if (p < p1) {
-          const float asc = a.a_scale[a.row_tok[p]];
+          const float asc = a.a_scale ? a.a_scale[a.row_tok[p]] : 1.0f;  // none for block-scaled rows
           uint16_t hb[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
@@ -190,7 +305,7 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
         const int p = p0 + wm * 64 + i * 16 + row;
         const int n0 = nt * 128 + wn * 64 + c4;
         if (p < p1 && n0 < a.N) {
-          const float asc = a.a_scale[p];
+          const float asc = a.a_scale ? a.a_scale[p] : 1.0f;
           const float wt = a.row_w[p];
           uint16_t ob[4];
 #pragma unroll
@@ -217,8 +332,21 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
   }
 }
 
-// Register-staged main loop (mx_tile.h), kept as a selectable variant.
-template <int MODE, bool SAFE>
+// Block-scaled activations: a tile goes to the fused-update kernel (mx2 == 1) when none of its
+// rows is flagged, to the general one (mx2 == 2) otherwise.  Every thread of the block calls it.
+template <int MODE>
+LSK_DEV bool mx2_takes_tile(const lsk::MoeGemmArgs& a, int p0, int p1) {
+  int f = 0;
+  const int t = threadIdx.x;
+  if (t < lsk::kMoeBM && p0 + t < p1) f = a.row_flag[MODE == 0 ? a.row_tok[p0 + t] : p0 + t];
+  const int any = __syncthreads_or(f);
+  return a.mx2 == 1 ? any == 0 : any != 0;
+}
+
+// Register-staged main loop (mx_tile.h), kept as a selectable variant; with ROWSCALE the general
+// kernel of block-scaled activations (flagged rows: integer values and their exponents ka;
+// other rows: the dequantised values with exponent 0).
+template <int MODE, bool SAFE, bool ROWSCALE>
 __global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
   extern __shared__ char mx_smem[];
   const int ntiles = MODE == 0 ? (a.N + 63) / 64 : (a.N + 127) / 128;
@@ -228,6 +356,7 @@ __global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
   const int e = a.tiles[1 + 2 * mt];
   const int p0 = a.tiles[2 + 2 * mt];
   const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  if (a.mx2 && !mx2_takes_tile<MODE>(a, p0, p1)) return;
   const uint8_t* wb = (const uint8_t*)a.w_ptrs[e];
   const uint8_t* sb = (const uint8_t*)a.ws_ptrs[e];
   const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
@@ -246,12 +375,18 @@ __global__ __launch_bounds__(256) void moe_mx_gemm_kernel(lsk::MoeGemmArgs a) {
     const int w = moe_mx_wrow<MODE>(a, nt, r);
     return w >= 0 ? sb + (int64_t)w * a.lds : nullptr;
   };
+  auto rowK = [&](int r) -> const int32_t* {
+    const int p = p0 + r;
+    if (p >= p1) return nullptr;
+    const int src = MODE == 0 ? a.row_tok[p] : p;
+    return a.row_flag[src] ? a.a_ka + (int64_t)src * a.ldka : nullptr;
+  };
   typename Cfg::Acc acc;
 #pragma unroll
   for (int i = 0; i < Cfg::TM; ++i)
 #pragma unroll
     for (int j = 0; j < Cfg::TN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-  lsk::mx_mainloop<128, 128, 2, 2, NB, false, true, SAFE>(acc, rowA, rowB, rowS, a.K, mx_smem);
+  lsk::mx_mainloop<128, 128, 2, 2, NB, false, true, SAFE, ROWSCALE>(acc, rowA, rowB, rowS, rowK, a.K, mx_smem);
   moe_mx_epilogue<MODE>(a, acc, nt, p0, p1, bias, mx_smem);
 }
 
@@ -266,6 +401,7 @@ __global__ __launch_bounds__(256, RING == 2 ? 3 : 2) void moe_mx_pp_kernel(lsk::
   const int e = a.tiles[1 + 2 * mt];
   const int p0 = a.tiles[2 + 2 * mt];
   const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  if (a.mx2 && !mx2_takes_tile<MODE>(a, p0, p1)) return;
   const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
   const int nrows_w = MODE == 0 ? 2 * a.N : a.N;  // weight rows of one expert
   const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
@@ -363,9 +499,20 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
   const int64_t blocks = max_tiles * ntiles;
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "moe_mx_gemm_kernel: grid too large");
+  if (ga.mx2 == 2) {
+    static bool attr_rs = false;
+    auto kern = moe_mx_gemm_kernel<MODE, true, true>;
+    if (!attr_rs) {
+      if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "moe_mx_gemm_kernel")) return rc;
+      attr_rs = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), Cfg::kSmemBytes, s, ga);
+    return lsk::check_launch(MODE == 0 ? "moe_mx_gemm_kernel<gate_up, block exponents>"
+                                       : "moe_mx_gemm_kernel<down, block exponents>");
+  }
   if (g_mx_variant == 1) {
     static bool attr = false;
-    auto kern = moe_mx_gemm_kernel<MODE, SAFE>;
+    auto kern = moe_mx_gemm_kernel<MODE, SAFE, false>;
     if (!attr) {
       if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "moe_mx_gemm_kernel")) return rc;
       attr = true;
@@ -394,19 +541,20 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
   return lsk::check_launch(MODE == 0 ? "moe_mx_pp_kernel<gate_up>" : "moe_mx_pp_kernel<down>");
 }
 
-template <bool B_FP4, bool SAFE>
-int launch_dense(const int8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, const uint8_t* kexp, int64_t lds, int M,
-                 int N, int K, int epi, const float* asc, const float* bias, float* out, int64_t ldo, hipStream_t s) {
+template <bool B_FP4, bool SAFE, bool ROWSCALE>
+int launch_dense(const int8_t* a, int64_t lda, const int32_t* ka, int64_t ldka, const uint8_t* b, int64_t ldb,
+                 const uint8_t* kexp, int64_t lds, int M, int N, int K, int epi, const float* asc, const float* bias,
+                 float* out, int64_t ldo, hipStream_t s) {
   static bool attr = false;
-  auto kern = mx_gemm_kernel<B_FP4, SAFE>;
+  auto kern = mx_gemm_kernel<B_FP4, SAFE, ROWSCALE>;
   if (!attr) {
     if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "mx_gemm_kernel")) return rc;
     attr = true;
   }
   const int64_t blocks = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
   LSK_REQUIRE(blocks <= 0x7fffffff, "mx_gemm_kernel: grid too large");
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), Cfg::kSmemBytes, s, a, lda, b, ldb, kexp, lds, M, N, K, epi,
-                     asc, bias, out, ldo);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), Cfg::kSmemBytes, s, a, lda, ka, ldka, b, ldb, kexp, lds, M, N,
+                     K, epi, asc, bias, out, ldo);
   return lsk::check_launch("mx_gemm_kernel");
 }
 
@@ -654,6 +802,14 @@ int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, f
   return check_launch("rowquant_bf16_kernel");
 }
 
+int launch_blockquant_mx2(const uint16_t* x, int64_t ldx, int64_t R, const int32_t* nrows, int K, uint16_t* q,
+                          int32_t* ka, int32_t* flag, int lo, int hi, hipStream_t s) {
+  if (R == 0) return LSK_OK;
+  LSK_REQUIRE(R <= 0x7fffffff, "blockquant_mx2: too many rows");
+  hipLaunchKernelGGL(blockquant_mx2_kernel, dim3((unsigned)R), dim3(256), 0, s, x, ldx, nrows, K, q, ka, flag, lo, hi);
+  return check_launch("blockquant_mx2_kernel");
+}
+
 int launch_requant_bf16(const uint16_t* h, const uint32_t* amax, const int32_t* nrows, int64_t R, int I, uint16_t* q,
                         float* asc, hipStream_t s) {
   hipLaunchKernelGGL(requant_bf16_kernel, dim3(grid_for(R * (I / 8))), dim3(256), 0, s, h, amax, nrows, I, q, asc);
@@ -680,10 +836,56 @@ extern "C" int lsk_gemm_mx(const int8_t* a, int64_t lda, const void* b, int b_fm
   // the host cannot see device data, so the general entry point always takes the SAFE update
   hipStream_t s = (hipStream_t)stream;
   if (b_fmt == 1)
-    return launch_dense<true, true>(a, lda, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K, epilogue, asc,
-                                    bias, out, ldo, s);
-  return launch_dense<false, true>(a, lda, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K, epilogue, asc, bias,
-                                   out, ldo, s);
+    return launch_dense<true, true, false>(a, lda, nullptr, 0, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K,
+                                           epilogue, asc, bias, out, ldo, s);
+  return launch_dense<false, true, false>(a, lda, nullptr, 0, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K,
+                                          epilogue, asc, bias, out, ldo, s);
+}
+
+extern "C" int lsk_blockquant(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, int8_t* q, int64_t ldq,
+                              int32_t* ka, int64_t ldka, void* stream) {
+  LSK_REQUIRE(M >= 0 && K >= 0, "lsk_blockquant: negative size");
+  LSK_REQUIRE(K % 32 == 0, "lsk_blockquant: K=%lld not a multiple of the 32-element block", (long long)K);
+  LSK_REQUIRE(x_dtype == LSK_BF16 || x_dtype == LSK_F32, "lsk_blockquant: x must be bf16 or f32");
+  if (M == 0 || K == 0) return LSK_OK;
+  LSK_REQUIRE(x && q && ka, "lsk_blockquant: null pointer");
+  LSK_REQUIRE(M <= 0x7fffffff && K <= 0x7fffffff, "lsk_blockquant: size too large");
+  const int esz = x_dtype == LSK_F32 ? 4 : 2;
+  LSK_REQUIRE(ldx >= K && (ldx * esz) % 16 == 0 && ((uintptr_t)x & 15) == 0,
+              "lsk_blockquant: x rows must be 16-byte aligned");
+  LSK_REQUIRE(ldq >= K && ldq % 8 == 0 && ((uintptr_t)q & 7) == 0, "lsk_blockquant: q rows must be 8-byte aligned");
+  LSK_REQUIRE(ldka >= K / 32, "lsk_blockquant: ldka too small");
+  hipStream_t s = (hipStream_t)stream;
+  if (x_dtype == LSK_F32)
+    hipLaunchKernelGGL(blockquant_i8_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, (int)K, q, ldq, ka, ldka);
+  else
+    hipLaunchKernelGGL(blockquant_i8_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, x, ldx, (int)K, q, ldq, ka, ldka);
+  return lsk::check_launch("blockquant_i8_kernel");
+}
+
+extern "C" int lsk_gemm_mx2(const int8_t* q, int64_t ldq, const int32_t* ka, int64_t ldka, const void* b, int b_fmt,
+                            int64_t ldb, const uint8_t* kexp, int64_t lds, int64_t M, int64_t N, int64_t K, int epilogue,
+                            const float* bias, float* out, int64_t ldo, void* stream) {
+  LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_gemm_mx2: negative size");
+  LSK_REQUIRE(K % 32 == 0, "lsk_gemm_mx2: K=%lld not a multiple of the 32-element block", (long long)K);
+  LSK_REQUIRE(b_fmt == 0 || b_fmt == 1, "lsk_gemm_mx2: b_fmt %d not 0 (m2 int8) or 1 (packed E2M1)", b_fmt);
+  LSK_REQUIRE(epilogue == 0 || epilogue == 1, "lsk_gemm_mx2: epilogue must be 0 or 1");
+  if (M == 0 || N == 0) return LSK_OK;
+  LSK_REQUIRE(q && ka && b && kexp && out, "lsk_gemm_mx2: null pointer");
+  LSK_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, "lsk_gemm_mx2: size too large");
+  const int64_t rowbytes = b_fmt == 1 ? K / 2 : K;
+  LSK_REQUIRE(ldq >= K && ldq % 16 == 0 && ((uintptr_t)q & 15) == 0, "lsk_gemm_mx2: q rows must be 16-byte aligned");
+  LSK_REQUIRE(ldb >= rowbytes && ldb % 16 == 0 && ((uintptr_t)b & 15) == 0,
+              "lsk_gemm_mx2: weight rows must be 16-byte aligned");
+  LSK_REQUIRE(ldka >= K / 32 && lds >= K / 32 && ldo >= N, "lsk_gemm_mx2: leading dimension too small");
+  // the exponent of each product depends on the row and the column; the general entry point
+  // always takes the multiply-then-add update with the correctly rounded 2^(ka + kexp - 128)
+  hipStream_t s = (hipStream_t)stream;
+  if (b_fmt == 1)
+    return launch_dense<true, true, true>(q, ldq, ka, ldka, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K,
+                                          epilogue, nullptr, bias, out, ldo, s);
+  return launch_dense<false, true, true>(q, ldq, ka, ldka, (const uint8_t*)b, ldb, kexp, lds, (int)M, (int)N, (int)K,
+                                         epilogue, nullptr, bias, out, ldo, s);
 }
 
 extern "C" int lsk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t K, int block,

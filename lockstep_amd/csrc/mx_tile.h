@@ -12,6 +12,11 @@
 // fma(s_b, 2^(k-128), acc) rounds exactly once, like the reference's multiply-then-add.  Weight
 // sets holding an exponent byte >= 240 take the SAFE variant (a multiply, then an add).
 // Blocks are never summed together before rounding and K is never split.
+//
+// ROWSCALE adds a per-row block exponent ka[m, b] (block-scaled activations, moe_ref.py:317-326):
+// the update becomes acc = fl32(acc + fl32(s_b * p)) with p = fl32(2^ka * 2^(kexp - 128)), the
+// correctly rounded 2^(ka + kexp - 128) (0 below 2^-149, inf from 2^128), always as a multiply
+// and then an add.
 #pragma once
 #include "mfma_tile.h"
 
@@ -75,7 +80,8 @@ struct MxCfg {
   static constexpr int kRowChunks = BK * 2 / 16;                 // 16-byte bf16 chunks per LDS row
   static constexpr int kSmemA = BM * kRowChunks, kSmemB = BN * kRowChunks;  // v4i per stage
   static constexpr int kScale = BN * NB;                          // floats per stage
-  static constexpr int kStageBytes = (kSmemA + kSmemB) * 16 + kScale * 4;
+  static constexpr int kScaleA = BM * NB;                         // row scales per stage (ROWSCALE)
+  static constexpr int kStageBytes = (kSmemA + kSmemB) * 16 + (kScale + kScaleA) * 4;
   static constexpr int kLdc = WTN + 4;
   static constexpr int kStripFloats = 16 * kLdc;
   static constexpr int kEpiBytes = WM * WN * kStripFloats * 4;
@@ -94,9 +100,12 @@ LSK_DEV int swz(int r, int c) {
 // acc[TM][TN] (binary32) accumulates the MX blocks of this tile in ascending order.
 // rowA(r): tile row r's activation row (bf16 [K] or int8 [K]; null = zero row);
 // rowB(r): tile row r's weight row (packed fp4 [K/2] or m2 int8 [K]; null = zero row);
-// rowS(r): its e8m0 exponents [K/32].  Each is evaluated once per load slot, before the K loop.
-template <int BM, int BN, int WM, int WN, int NB, bool A_I8, bool B_FP4, bool SAFE, class FA, class FB, class FS>
-LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, FB rowB, FS rowS, int K, char* smem) {
+// rowS(r): its e8m0 exponents [K/32]; rowK(r) (ROWSCALE only): tile row r's block exponents
+// ka [K/32] (int32; null = all 0).  Each is evaluated once per load slot, before the K loop.
+template <int BM, int BN, int WM, int WN, int NB, bool A_I8, bool B_FP4, bool SAFE, bool ROWSCALE, class FA, class FB,
+          class FS, class FK>
+LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, FB rowB, FS rowS, FK rowK, int K,
+                         char* smem) {
   using C = MxCfg<BM, BN, WM, WN, NB>;
   constexpr int T = C::kThreads;
   constexpr int RC = C::kRowChunks;
@@ -113,9 +122,11 @@ LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, 
   const int wm = wave / WN, wn = wave % WN;
 
   constexpr int kSPer = (BN * NB + T - 1) / T;  // scale bytes per thread per stage
+  constexpr int kKPer = ROWSCALE ? (BM * NB + T - 1) / T : 0;  // row exponents per thread per stage
   const char* pa[kAPer];
   const uint8_t* pb[kBPer];
   const uint8_t* ps[kSPer];
+  const int32_t* pk[kKPer > 0 ? kKPer : 1];
 #pragma unroll
   for (int j = 0; j < kAPer; ++j) {
     const int i = tid + j * T;
@@ -131,8 +142,14 @@ LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, 
     const int i = tid + j * T;
     ps[j] = i < BN * NB ? rowS(i / NB) : nullptr;
   }
+#pragma unroll
+  for (int j = 0; j < kKPer; ++j) {
+    const int i = tid + j * T;
+    pk[j] = i < BM * NB ? rowK(i / NB) : nullptr;
+  }
   v4i ra[kAPer], rb[kBPer];
   uint32_t rs[kSPer];
+  int rk[kKPer > 0 ? kKPer : 1];
   auto gload = [&](int k0) {
 #pragma unroll
     for (int j = 0; j < kAPer; ++j) {
@@ -153,6 +170,12 @@ LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, 
       const int i = tid + j * T;
       const int b = i % NB;
       rs[j] = (ps[j] && k0 + 32 * b < K) ? ps[j][k0 / 32 + b] : 128u;
+    }
+#pragma unroll
+    for (int j = 0; j < kKPer; ++j) {
+      const int i = tid + j * T;
+      const int b = i % NB;
+      rk[j] = (pk[j] && k0 + 32 * b < K) ? pk[j][k0 / 32 + b] : 0;
     }
   };
   auto sstore = [&](int buf) {
@@ -197,6 +220,11 @@ LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, 
       const int i = tid + j * T;
       if (i < BN * NB) sS[i] = pow2f((int)rs[j] - 128);
     }
+#pragma unroll
+    for (int j = 0; j < kKPer; ++j) {
+      const int i = tid + j * T;
+      if (i < BM * NB) sS[C::kScale + (i % NB) * BM + i / NB] = pow2f(rk[j]);  // ka in [-126, 127]
+    }
   };
 
   const int nk = (K + C::BK - 1) / C::BK;
@@ -216,6 +244,12 @@ LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, 
       const int c = b * 4 + (lane >> 4);
       v4i af[C::TM], bf[C::TN];
       float sc[C::TN];
+      v4f sa[C::TM];
+      if (ROWSCALE) {
+        // the C rows of lane l in a 16x16 tile are 4 (l / 16) + r
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) sa[i] = *(const v4f*)(sS + C::kScale + b * BM + wm * C::WTM + i * 16 + 4 * (lane >> 4));
+      }
 #pragma unroll
       for (int i = 0; i < C::TM; ++i) af[i] = sA[swz<RC>(wm * C::WTM + i * 16 + (lane & 15), c)];
 #pragma unroll
@@ -231,7 +265,8 @@ LSK_DEV void mx_mainloop(typename MxCfg<BM, BN, WM, WN, NB>::Acc& acc, FA rowA, 
           const v4f d = mfma_bf16(af[i], bf[j]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (SAFE) acc[i][j][r] = f32_add(acc[i][j][r], f32_mul(d[r], sc[j]));
+            if (ROWSCALE) acc[i][j][r] = f32_add(acc[i][j][r], f32_mul(d[r], f32_mul(sa[i][r], sc[j])));
+            else if (SAFE) acc[i][j][r] = f32_add(acc[i][j][r], f32_mul(d[r], sc[j]));
             else acc[i][j][r] = __builtin_fmaf(d[r], sc[j], acc[i][j][r]);
           }
         }

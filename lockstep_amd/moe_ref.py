@@ -11,6 +11,8 @@ Same names and signatures; GPU tensors only; results bit-identical to the refere
     sigmoid_contract, act_swigluoai, act_silu              moe_ref.py:150-186
     expert_swiglu, expert_block                            moe_ref.py:100-114, 189-200
     moe_forward, moe_forward_b                             moe_ref.py:117-140, 213-230
+    int_mm_mx, lin_epilogue_mx, expert_block_mx, moe_forward_mx   moe_ref.py:243-290
+    blockquant, int_mm_mx2, expert_block_mx2, moe_forward_mx2     moe_ref.py:299-352
 """
 from __future__ import annotations
 
@@ -321,6 +323,7 @@ class ExpertTablesMX:
         keep = []
         p13, s13, p2, s2, b13, b2 = [], [], [], [], [], []
         safe = False
+        kw = []
         for ex in experts:
             (m13, k13), (m2_, k2_) = ex[0], ex[1]
             c13 = m13.to(torch.uint8).contiguous() if packed else ops.pack_m2(m13)
@@ -337,12 +340,16 @@ class ExpertTablesMX:
             b13.append(bb13.data_ptr() if bb13 is not None else 0)
             b2.append(bb2.data_ptr() if bb2 is not None else 0)
             safe = safe or bool((e13.max() >= 240).item()) or bool((e2.max() >= 240).item())
+            kw.append(torch.stack([e13.min(), e13.max(), e2.min(), e2.max()]).to(torch.int32))
         two_i, hh = keep[0].shape
         self.I = int(two_i) // 2
         self.H = int(hh) * 2
         self.ldw13, self.ldw2 = int(keep[0].stride(0)), int(keep[1].stride(0))
         self.lds13, self.lds2 = int(keep[2].stride(0)), int(keep[3].stride(0))
         self.mx_safe = 1 if safe else 0
+        # E8M0 bounds over all experts (w13 min / max, w2 min / max): block-scaled activations use them
+        kr = torch.stack(kw).cpu()
+        self.kw_bounds = (int(kr[:, 0].min()), int(kr[:, 1].max()), int(kr[:, 2].min()), int(kr[:, 3].max()))
         dev = self.device
 
         def table(vals):
@@ -367,10 +374,11 @@ def expert_tables_mx(experts) -> ExpertTablesMX:
     return hit
 
 
-def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int):
-    L.require_cuda(x, idx, w, what="moe_forward_mx")
+def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1):
+    what = "moe_forward_mx2" if wfmt == 2 else "moe_forward_mx"
+    L.require_cuda(x, idx, w, what=what)
     if x.dtype != BF:
-        raise TypeError("moe_forward_mx: x must be bf16 [T, H] (got %s)" % x.dtype)
+        raise TypeError("%s: x must be bf16 [T, H] (got %s)" % (what, x.dtype))
     x = x.contiguous()
     T, H = x.shape
     k = int(idx.shape[1])
@@ -381,9 +389,11 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int):
     y = torch.empty((T, H), dtype=BF, device=x.device)
     if T == 0:
         return y
-    nbytes = L.load().lsk_moe_workspace(T, k, t.E, H, t.I, 0, 1)
+    nbytes = L.load().lsk_moe_workspace(T, k, t.E, H, t.I, 0, wfmt)
     work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
-    a = L.MoeArgs(T=T, H=H, I=t.I, E=t.E, k=k, act=act, wfmt=1, mx_safe=t.mx_safe, lds13=t.lds13, lds2=t.lds2,
+    kb = t.kw_bounds
+    a = L.MoeArgs(T=T, H=H, I=t.I, E=t.E, k=k, act=act, wfmt=wfmt, mx_safe=t.mx_safe, lds13=t.lds13, lds2=t.lds2,
+                  kw13_min=kb[0], kw13_max=kb[1], kw2_min=kb[2], kw2_max=kb[3],
                   x=x.data_ptr(), idx=idx.data_ptr(), w=w.data_ptr(), w13_ptrs=t.w13.data_ptr(), ldw13=t.ldw13,
                   ws13_ptrs=t.ws13.data_ptr(), b13_ptrs=t.b13.data_ptr() if t.b13 is not None else None,
                   w2_ptrs=t.w2.data_ptr(), ldw2=t.ldw2, ws2_ptrs=t.ws2.data_ptr(),
@@ -402,4 +412,38 @@ def moe_forward_mx(x, gate, experts, k, renormalize, tab, win, act, routing=None
     else:
         idx, w = routing[0].to(torch.int64), routing[1].to(BF)
     y = _moe_layer_mx(x, idx, w, expert_tables_mx(experts), _act_code(act))
+    return y, idx, w
+
+
+# ============================================================================ block-scaled activations (MX2)
+def blockquant(x: torch.Tensor):
+    """x [T, K] -> (q int8 [T, K], ka int32 [T, K/32]): per 32-wide block, ka = the least k with
+    127 * 2^k >= max |x| (clamped to [-126, 127], -126 for a zero block), q = rint(x / 2^ka)."""
+    return ops.blockquant(x)
+
+
+def int_mm_mx2(q: torch.Tensor, ka: torch.Tensor, m2: torch.Tensor, kexp: torch.Tensor) -> torch.Tensor:
+    """q int8 [T, K], ka int32 [T, nb]; m2 int8 [N, K], kexp uint8 [N, nb] -> binary32 [T, N]: per
+    block s (exact), acc = fl32(acc + fl32(s * fl32(2^(ka + kexp - 128)))) in ascending order."""
+    return ops.gemm_mx2(q, ka, m2, kexp, 0)
+
+
+def expert_block_mx2(x_rows, w13, w2, act, b13=None, b2=None):
+    """blockquant -> int_mm_mx2 -> bfr (+ b13) -> act -> blockquant(bf16 h) -> int_mm_mx2 -> bfr (+ b2)."""
+    q, ka = blockquant(x_rows)
+    y = ops.gemm_mx2(q, ka, w13[0], w13[1], 0, bias=b13, epilogue=1)
+    I = y.shape[-1] // 2
+    h = act(y[:, :I], y[:, I:])
+    q2, ka2 = blockquant(h.to(BF))
+    return ops.gemm_mx2(q2, ka2, w2[0], w2[1], 0, bias=b2, epilogue=1)
+
+
+def moe_forward_mx2(x, gate, experts, k, renormalize, tab, win, act, routing=None):
+    """As moe_forward_mx with block-scaled activations (no per-row scale; epilogues bfr(acc) + b).
+    experts[e] = ((m2_13, kexp_13), (m2_2, kexp_2), b13 | None, b2 | None) or an ExpertTablesMX."""
+    if routing is None:
+        idx, w, _ = router_b(x, gate[0], gate[1], k, renormalize, tab, win, gate[2] if len(gate) > 2 else None)
+    else:
+        idx, w = routing[0].to(torch.int64), routing[1].to(BF)
+    y = _moe_layer_mx(x, idx, w, expert_tables_mx(experts), _act_code(act), wfmt=2)
     return y, idx, w

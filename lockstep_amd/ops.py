@@ -345,6 +345,50 @@ def gemm_mx(a8: torch.Tensor, b: torch.Tensor, kexp: torch.Tensor, b_fmt: int, a
     return out
 
 
+def blockquant(x: torch.Tensor):
+    """Per-32-block int8 quant with power-of-two block exponents: x [T, K] (bf16 / f32; other float
+    dtypes go through f32), K % 32 == 0 -> (q int8 [T, K], ka int32 [T, K/32])."""
+    L.require_cuda(x, what="blockquant")
+    if x.dim() != 2:
+        raise ValueError("blockquant: x must be [T, K]")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.to(torch.float32)
+    T, K = x.shape
+    if K % 32:
+        raise ValueError("blockquant: K=%d not a multiple of 32" % K)
+    x = x.contiguous()
+    q = torch.empty((T, K), dtype=torch.int8, device=x.device)
+    ka = torch.empty((T, K // 32), dtype=torch.int32, device=x.device)
+    if T and K:
+        L.call("lsk_blockquant", L.ptr(x), L.dtype_code(x.dtype), K, T, K, L.ptr(q), K, L.ptr(ka), K // 32,
+               L.stream_of(x))
+    return q, ka
+
+
+def gemm_mx2(q: torch.Tensor, ka: torch.Tensor, b: torch.Tensor, kexp: torch.Tensor, b_fmt: int, bias=None,
+             epilogue: int = 0) -> torch.Tensor:
+    """MX operand with block-scaled activations: q int8 [M, K] and ka int32 [M, K/32] with m2 int8
+    [N, K] (b_fmt 0) or packed E2M1 [N, K/2] (b_fmt 1) and E8M0 kexp [N, K/32] -> binary32 [M, N]
+    (epilogue 1: bfr(acc), then bfr(+ bias))."""
+    L.require_cuda(q, ka, b, kexp, bias, what="gemm_mx2")
+    if q.dtype != torch.int8:
+        raise TypeError("gemm_mx2: q must be int8")
+    M, K = q.shape
+    if tuple(ka.shape) != (M, K // 32):
+        raise ValueError("gemm_mx2: ka %s does not match q %s" % (tuple(ka.shape), tuple(q.shape)))
+    q = q if (q.stride(-1) == 1 and q.stride(0) % 16 == 0) else q.contiguous()
+    ka = ka.to(torch.int32).contiguous()
+    b = b.contiguous()
+    kexp = kexp.to(torch.uint8).contiguous()
+    N = b.shape[0]
+    out = torch.empty((M, N), dtype=torch.float32, device=q.device)
+    if M and N:
+        ld_q = q.stride(0) if M > 1 else K
+        L.call("lsk_gemm_mx2", L.ptr(q), ld_q, L.ptr(ka), K // 32, L.ptr(b), int(b_fmt), b.stride(0), L.ptr(kexp),
+               kexp.stride(0), M, N, K, int(epilogue), L.ptr(_f32(bias)), L.ptr(out), N, L.stream_of(q))
+    return out
+
+
 def mx_epilogue(acc: torch.Tensor, asc: torch.Tensor, bias=None) -> torch.Tensor:
     L.require_cuda(acc, asc, bias, what="lin_epilogue_mx")
     acc = acc.to(torch.float32).contiguous()

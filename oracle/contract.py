@@ -21,6 +21,12 @@ Pinning (how each function is checked, see tests/test_oracle_*.py):
   int_mm_mx: one-block closed form, equal-exponent integer identity, scalar brute force,
       and a negative control (reversed block order differs)
   router / combine / moe_forward*: scalar brute force in Python ints and numpy float32
+  blockquant (MX2): the exact exponent min{k : 127 * 2^k >= am} clamped to [-126, 127] from the
+      binary32 bits, round-half-even halves, the reconstruction bound, negative controls
+  int_mm_mx2: equals int_mm_mx with kexp + c when every ka is c (row by row), the one-block
+      closed form fl32(s * fl32(2^e)) from binary64 including underflow to 0 / overflow to inf,
+      a negative control (the fused block update differs below 2^-149)
+  expert_block_mx2 / moe_forward_mx2: compositions of the pinned pieces in moe_ref.py's order
   row_sum_float / rmsnorm_float (contract 2.6 float norm): the digests norm_float.*, a
       rational brute force of the tree, the zero-padded balanced tree identity
   outlier_side / w8a8_outlier_linear: the digests outlier.*, linear.v2_5.*, linear.v2_5_1.*
@@ -605,6 +611,68 @@ def lin_epilogue_mx(acc, asc, bias=None):
     return y
 
 
+# ----------------------------------------------------------------------------- A13 MX2 block-scaled activations
+KA_MIN, KA_MAX = -126, 127
+
+
+def blockquant(x):
+    """moe_ref.py:299-314: per 32-wide block of each row, am = max |x|; ka = ceil(log2(fl32(am / 127)))
+    (-126 for an all-zero block), clamped to [-126, 127], raised by one where fl32(127 * 2^ka) < am;
+    q = clamp(rint(x / 2^ka), +-127).  x [T, K] binary32 values -> (q int8 [T, K], ka int32 [T, K/32])."""
+    xf = np.asarray(x, F32)
+    T, K = xf.shape
+    nb = K // MX_BLOCK
+    xb = xf.reshape(T, nb, MX_BLOCK)
+    am = np.abs(xb).max(axis=-1).astype(F32)
+    with np.errstate(divide="ignore"):
+        l2 = np.log2((am / F32(127.0)).astype(F32)).astype(F32)
+    ka = np.where(am > 0, np.ceil(l2), F32(KA_MIN)).astype(F32)
+    ka = np.clip(ka, KA_MIN, KA_MAX).astype(F32)
+    with np.errstate(over="ignore"):
+        bad = (F32(127.0) * np.ldexp(np.ones_like(ka), ka.astype(np.int32))).astype(F32) < am
+    ka = np.where(bad, ka + F32(1.0), ka).astype(np.int32)
+    sc = np.ldexp(np.ones(ka.shape, F32), ka).astype(F32)
+    with np.errstate(invalid="ignore"):
+        q = np.clip(np.rint((xb / sc[..., None]).astype(F32)), -INT8_LIM, INT8_LIM).astype(np.int8)
+    return q.reshape(T, K), ka
+
+
+def int_mm_mx2(q, ka, m2, kexp):
+    """moe_ref.py:317-326: for blocks b ascending, p = fl32(2^(ka[m,b] + kexp[n,b] - 128)) (0 below
+    2^-149, inf from 2^128) and acc = fl32(acc + fl32(s_b * p)), s_b the exact int block sum."""
+    a = np.asarray(q).astype(np.int64)
+    m = np.asarray(m2).astype(np.int64)
+    kaa = np.asarray(ka).astype(np.int64)
+    kw = np.asarray(kexp).astype(np.int64)
+    T, K = a.shape
+    N = m.shape[0]
+    acc = np.zeros((T, N), F32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        for b in range(K // MX_BLOCK):
+            sl = slice(b * MX_BLOCK, (b + 1) * MX_BLOCK)
+            s = (a[:, sl] @ m[:, sl].T).astype(F32)
+            e = kaa[:, b][:, None] + (kw[:, b] - 128)[None, :]
+            p = np.ldexp(np.ones(e.shape, F32), np.clip(e, -400, 400).astype(np.int32)).astype(F32)
+            acc = (acc + (s * p).astype(F32)).astype(F32)
+    return acc
+
+
+def expert_block_mx2(x_rows, w13, w2, act, b13=None, b2=None):
+    """moe_ref.py:329-339: blockquant -> int_mm_mx2 -> bfr (+ bfr(+ b13)) -> act -> blockquant of
+    the bf16-rounded h -> int_mm_mx2 -> bfr (+ bfr(+ b2)); no per-row scale."""
+    q, ka = blockquant(x_rows)
+    y = bfr(int_mm_mx2(q, ka, w13[0], w13[1]))
+    if b13 is not None:
+        y = bfr((y + np.asarray(b13, F32)[None, :]).astype(F32))
+    I = y.shape[-1] // 2
+    h = act(y[:, :I], y[:, I:])
+    q2, ka2 = blockquant(bfr(h))
+    o = bfr(int_mm_mx2(q2, ka2, w2[0], w2[1]))
+    if b2 is not None:
+        o = bfr((o + np.asarray(b2, F32)[None, :]).astype(F32))
+    return o
+
+
 # ----------------------------------------------------------------------------- A10 expert blocks
 def expert_swiglu(x_rows, w13col, ws13, w2col, ws2, act=act_silu, rot=False):
     """moe_ref.py:100-114 (w13col [H, 2I], w2col [I, H])."""
@@ -694,6 +762,18 @@ def moe_forward_mx(x, experts, idx, w, act):
         ex = experts[e]
         return expert_block_mx(x[tok], ex[0], ex[1], act,
                                ex[2] if len(ex) > 2 else None, ex[3] if len(ex) > 3 else None)
+    return bf16_bits(_combine(T, H, idx, w, run, len(experts)))
+
+
+def moe_forward_mx2(x, experts, idx, w, act):
+    """moe_ref.py:342-352 with routing injected; experts[e] as moe_forward_mx."""
+    x = np.asarray(x, F32)
+    T, H = x.shape
+
+    def run(e, tok):
+        ex = experts[e]
+        return expert_block_mx2(x[tok], ex[0], ex[1], act,
+                                ex[2] if len(ex) > 2 else None, ex[3] if len(ex) > 3 else None)
     return bf16_bits(_combine(T, H, idx, w, run, len(experts)))
 
 
