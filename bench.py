@@ -241,17 +241,23 @@ def moe_section(torch, args):
     g.manual_seed(3)
     tab = CC.table_on(dev)
     res = {}
-    cases = [("qwen3_30b_a3b_int8", WL.QWEN3_30B_A3B, False, 75497472, 4718592 + 4 * (2 * 768 + 2048)),
-             ("gpt_oss_20b_mxfp4", WL.GPT_OSS_20B, True, 199065600, 13219200)]
-    for name, c, mx, ops_tok, bytes_expert in cases:
+    cases = [("qwen3_30b_a3b_int8", WL.QWEN3_30B_A3B, 0, 75497472, 4718592 + 4 * (2 * 768 + 2048)),
+             ("gpt_oss_20b_mxfp4", WL.GPT_OSS_20B, 1, 199065600, 13219200),
+             ("gpt_oss_20b_mxfp4_mx2", WL.GPT_OSS_20B, 2, 199065600, 13219200)]
+    copies = None
+    for name, c, kind, ops_tok, bytes_expert in cases:
         E, k, H, I = c["E"], c["k"], c["H"], c["I"]
-        mk = _mx_expert_tables if mx else _int8_expert_tables
-        copies = [mk(torch, MR, g, dev, E, H, I) for _ in range(2)]
+        mx = kind > 0
+        wanted = [T for T in (1, 32, 4096)
+                  if not args.moe_cases or "%s_T%d" % (name, T) in args.moe_cases.split(",")]
+        if not wanted:
+            continue
+        if kind != 2 or copies is None:  # the block-scaled case reuses the MXFP4 experts
+            mk = _mx_expert_tables if mx else _int8_expert_tables
+            copies = [mk(torch, MR, g, dev, E, H, I) for _ in range(2)]
         act = MR.act_swigluoai if mx else MR.act_silu
-        fwd = MR.moe_forward_mx if mx else MR.moe_forward
-        for T in (1, 32, 4096):
-            if args.moe_cases and "%s_T%d" % (name, T) not in args.moe_cases.split(","):
-                continue
+        fwd = (MR.moe_forward, MR.moe_forward_mx, MR.moe_forward_mx2)[kind]
+        for T in wanted:
             x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
             logits = torch.randn((T, E), generator=g, device=dev)
             if not mx:
@@ -273,12 +279,16 @@ def moe_section(torch, args):
                 "weight_GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "TOPS": round(tops, 2),
                 "frac_mfma": round(tops / peak_t, 4)}
             log("bench: %s T=%d: %.1f us, %.0f tokens/s" % (name, T, ms * 1e3, T / (ms * 1e-3)))
-        del copies
-        torch.cuda.empty_cache()
+        if kind == 0:
+            copies = None
+            torch.cuda.empty_cache()
+    copies = None
+    torch.cuda.empty_cache()
     res["note"] = ("tokens/s of one MoE layer (router from logits + fused layer); weight_GB/s counts the active "
                    "experts' weight bytes (int8 + f32 scales, or 4-bit codes + E8M0 bytes); TOPS counts "
                    "2 * k * (2I*H + I*H) ops per token; MXFP4 fractions are of the bf16 MFMA peak (2.5 PF) the "
-                   "exact block contraction runs on")
+                   "exact block contraction runs on; _mx2: the same layer with block-scaled activations "
+                   "(moe_forward_mx2)")
     return res
 
 

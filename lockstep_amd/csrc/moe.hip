@@ -1009,7 +1009,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.ccnt = (int32_t*)take(nchunks * E * 4);
   w.cbase = (int32_t*)take(nchunks * E * 4);
   w.h = (uint16_t*)take(R * I * 2);
-  w.h_amax = (uint32_t*)take(R * 4);
+  w.h_amax = (uint32_t*)take((R + 2) * 4);  // + the two "some row flagged" words of block-scaled activations
   w.qh = (int8_t*)take(R * I * qb);
   w.asch = (float*)take(R * 4);
   w.slots = (uint16_t*)take(R * H * 2);
@@ -1184,7 +1184,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk_fwht_blocks(w.xrot, T, H, H, rb, a->rot_scale, w.xrot, H, stream))) return rc;
     rc = lsk_rowquant(w.xrot, LSK_F32, T, H, H, w.qx, H, w.ascx, stream);
   } else if (mx == 2) {
-    rc = lsk::launch_blockquant_mx2(a->x, H, T, nullptr, (int)H, (uint16_t*)w.qx, w.kax, w.flagx, lo13, hi13, s);
+    rc = LSK_OK;  // after the dispatch, which clears the flag words it raises
   } else if (mx) {
     rc = lsk::launch_rowquant_bf16(a->x, T, H, (uint16_t*)w.qx, w.ascx, s);
   } else {
@@ -1203,16 +1203,20 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
       }
     dispatch_lds = true;
   }
+  // the dispatch also clears the per-row |h| maxima and, for block-scaled activations, the words
+  // anyf[0] / anyf[1] that the block quants of x / h raise when they flag a row
+  const int64_t nzero = mx == 2 ? R + 2 : R;
+  int32_t* anyf = (int32_t*)(w.h_amax + R);
   const int64_t nchunks = (T + 255) / 256;
   if (nchunks == 1) {
     const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
     hipLaunchKernelGGL(moe_dispatch_small_kernel, dim3(1), dim3(256), dsm, s, a->idx, a->w, (int)T, k, (int)E, w.offs,
-                       w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, R);
+                       w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero);
     if ((rc = lsk::check_launch("moe_dispatch_small_kernel"))) return rc;
   } else {
     hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 4 + (size_t)256 * k * 4, s,
                        a->idx, (int)T, k,
-                       (int)E, w.ccnt, w.tok_cnt, w.h_amax, R);
+                       (int)E, w.ccnt, w.tok_cnt, w.h_amax, nzero);
     if ((rc = lsk::check_launch("moe_count_kernel"))) return rc;
     hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), (size_t)E * 4, s, w.ccnt, (int)nchunks, (int)E, w.cbase,
                        w.offs, w.tiles);
@@ -1222,6 +1226,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
                        (int)T, k, (int)E, w.cbase, w.row_tok, w.row_dst, w.row_w);
     if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
   }
+  if (mx == 2 &&
+      (rc = lsk::launch_blockquant_mx2(a->x, H, T, nullptr, (int)H, (uint16_t*)w.qx, w.kax, w.flagx, anyf, lo13, hi13, s)))
+    return rc;
   MoeGemmArgs g1{};
   g1.A = w.qx;
   g1.lda = H;
@@ -1245,6 +1252,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   if (mx == 2) {
     g1.a_scale = nullptr;
     g1.row_flag = w.flagx;
+    g1.any_flag = anyf;
     g1.a_ka = w.kax;
     g1.ldka = H / 32;
   }
@@ -1282,7 +1290,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
                        rb, a->rot_scale, w.qh, w.asch);
     if ((rc = lsk::check_launch("moe_rot_requant_kernel"))) return rc;
   } else if (mx == 2) {
-    if ((rc = lsk::launch_blockquant_mx2(w.h, I, R, w.offs + E, (int)I, (uint16_t*)w.qh, w.kah, w.flagh, lo2, hi2, s)))
+    if ((rc = lsk::launch_blockquant_mx2(w.h, I, R, w.offs + E, (int)I, (uint16_t*)w.qh, w.kah, w.flagh, anyf + 1, lo2,
+                                         hi2, s)))
       return rc;
   } else if (mx) {
     if ((rc = lsk::launch_requant_bf16(w.h, w.h_amax, w.offs + E, R, (int)I, (uint16_t*)w.qh, w.asch, s))) return rc;
@@ -1314,6 +1323,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   if (mx == 2) {
     g2.a_scale = nullptr;
     g2.row_flag = w.flagh;
+    g2.any_flag = anyf + 1;
     g2.a_ka = w.kah;
     g2.ldka = I / 32;
   }

@@ -34,6 +34,7 @@ struct MoeGemmArgs {
   // over tiles without a flagged row; 2 the general kernel over tiles with one
   int mx2;
   const int32_t* row_flag;  // per A row (gate/up: per token)
+  const int32_t* any_flag;  // nonzero when some row is flagged
   const int32_t* a_ka;      // block exponents of the A rows [rows, K/32]
   int64_t ldka;
 };
@@ -50,9 +51,10 @@ int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64
 int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, float* asc, hipStream_t s);
 
 // Block quant of bf16 rows for block-scaled activations: dequantised bf16 values (integer values
-// on flagged rows), exponents [R, K/32] and row flags (exponent outside [lo, hi]).
+// on flagged rows), exponents [R, K/32] and row flags (exponent outside [lo, hi]); *any is raised
+// (integer atomic OR) when some row is flagged.
 int launch_blockquant_mx2(const uint16_t* x, int64_t ldx, int64_t R, const int32_t* nrows, int K, uint16_t* q,
-                          int32_t* ka, int32_t* flag, int lo, int hi, hipStream_t s);
+                          int32_t* ka, int32_t* flag, int32_t* any, int lo, int hi, hipStream_t s);
 
 // Requant of h (bf16 values) with per-row maxima, emitting bf16 int8 values.
 int launch_requant_bf16(const uint16_t* h, const uint32_t* amax, const int32_t* nrows, int64_t R, int I, uint16_t* q,

@@ -135,12 +135,13 @@ __global__ __launch_bounds__(256) void blockquant_i8_kernel(const void* __restri
 // row is not flagged), its exponents ka [rows, K/32] and a flag set when some nonzero block has
 // ka outside [lo, hi], the range in which the fused block update on the dequantised values is
 // exact for the experts' weight exponents.  A flagged row is rewritten with the integer values q
-// (as bf16), which the general kernel pairs with ka.  One block per row; rows from *nrows on
-// (when given) are skipped; q and ka rows are packed (strides K and K/32).
+// (as bf16), which the general kernel pairs with ka, and *any is raised.  One block per row; rows
+// from *nrows on (when given) are skipped; q and ka rows are packed (strides K and K/32).
 __global__ __launch_bounds__(256) void blockquant_mx2_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                              const int32_t* __restrict__ nrows, int K,
                                                              uint16_t* __restrict__ q, int32_t* __restrict__ ka,
-                                                             int32_t* __restrict__ flag, int lo, int hi) {
+                                                             int32_t* __restrict__ flag, int32_t* __restrict__ any,
+                                                             int lo, int hi) {
   const int64_t r = blockIdx.x;
   if (nrows && r >= *nrows) return;
   int bad = 0;
@@ -172,7 +173,10 @@ __global__ __launch_bounds__(256) void blockquant_mx2_kernel(const uint16_t* __r
       *(uint4*)(q + r * K + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
-  if (threadIdx.x == 0) flag[r] = bad;
+  if (threadIdx.x == 0) {
+    flag[r] = bad;
+    if (bad) atomicOr(any, 1);
+  }
 }
 
 // ---------------------------------------------------------------- dense MX GEMM (int_mm_mx, int_mm_mx2)
@@ -333,9 +337,11 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
 }
 
 // Block-scaled activations: a tile goes to the fused-update kernel (mx2 == 1) when none of its
-// rows is flagged, to the general one (mx2 == 2) otherwise.  Every thread of the block calls it.
+// rows is flagged, to the general one (mx2 == 2) otherwise.  Every thread of the block calls it;
+// when no row at all is flagged (the usual case) it decides without a barrier.
 template <int MODE>
 LSK_DEV bool mx2_takes_tile(const lsk::MoeGemmArgs& a, int p0, int p1) {
+  if (*a.any_flag == 0) return a.mx2 == 1;
   int f = 0;
   const int t = threadIdx.x;
   if (t < lsk::kMoeBM && p0 + t < p1) f = a.row_flag[MODE == 0 ? a.row_tok[p0 + t] : p0 + t];
@@ -803,10 +809,11 @@ int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, f
 }
 
 int launch_blockquant_mx2(const uint16_t* x, int64_t ldx, int64_t R, const int32_t* nrows, int K, uint16_t* q,
-                          int32_t* ka, int32_t* flag, int lo, int hi, hipStream_t s) {
+                          int32_t* ka, int32_t* flag, int32_t* any, int lo, int hi, hipStream_t s) {
   if (R == 0) return LSK_OK;
   LSK_REQUIRE(R <= 0x7fffffff, "blockquant_mx2: too many rows");
-  hipLaunchKernelGGL(blockquant_mx2_kernel, dim3((unsigned)R), dim3(256), 0, s, x, ldx, nrows, K, q, ka, flag, lo, hi);
+  hipLaunchKernelGGL(blockquant_mx2_kernel, dim3((unsigned)R), dim3(256), 0, s, x, ldx, nrows, K, q, ka, flag, any, lo,
+                     hi);
   return check_launch("blockquant_mx2_kernel");
 }
 
