@@ -2,7 +2,7 @@
 """Benchmark of the contract matrix-multiply path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sections dense,decode,moe]
-                    [--moe-cases NAME,...] [--eager] [--mx-variant V]
+                    [--moe-cases NAME,...] [--eager] [--mx-variant V] [--moe-variant V]
 
 A step is one pass of the Llama-3.1-8B-shaped MLP contract GEMMs at M=2048 prefill rows:
 w8a8_matmul (row quant + exact int8 GEMM + v2.1 epilogue, bf16 out) of the gate+up projection
@@ -360,6 +360,8 @@ def main():
                                                          "(for profilers that count per dispatch)")
     ap.add_argument("--mx-variant", type=int, default=0, help="main loop of the grouped MXFP4 GEMMs "
                                                               "(lsk_moe_mx_select; 0 is the default)")
+    ap.add_argument("--moe-variant", type=int, default=-1, help="int8 grouped GEMM kernel "
+                                                                "(lsk_moe_select; -1, by size, is the default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (N=%d requested)" % args.gpus,
@@ -375,6 +377,7 @@ def main():
     global EAGER
     EAGER = args.eager
     _lib.call("lsk_moe_mx_select", args.mx_variant)
+    _lib.call("lsk_moe_select", args.moe_variant)
 
     log("bench: dense prefill step (M=2048, gate_up 28672x4096 + down 4096x14336)")
     d = dense_section(torch, args)

@@ -209,8 +209,9 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * 6, 7: for M <= 4 the 8-row register-buffered / LDS-ring GEMV instead of the whole-row GEMV;
  * 8..11: the whole-row GEMV with 1 / 2 / 4 / 8 rows per wave; 12, 13: tiles 3, 4 with a
  * three-stage LDS ring, two blocks per CU; 14 / 15: for 4 < M <= 32 the GEMV reading 64-byte row
- * pieces straight into registers / whole rows through LDS) or -1 to choose by shape (the default).  Results are identical for every choice; only speed
- * differs.  Process-wide, not thread-safe against concurrent launches. */
+ * pieces straight into registers / whole rows through LDS; 16 / 17: four-wave 256x256 / 256x128,
+ * one wave per SIMD with 128x128 / 128x64 wave tiles) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
+ * Process-wide, not thread-safe against concurrent launches. */
 int lsk_gemm_select(int tile_id);
 
 /* Power-of-two int8 quantisation of ref_block_v1 (reference/ref_block_v1.py:56-72,122-130).
@@ -377,9 +378,20 @@ typedef struct {
   int kw13_min, kw13_max;        /* wfmt 2: bounds of the E8M0 bytes of all w13 / w2 weights (any */
   int kw2_min, kw2_max;          /* bounds that contain them keep results exact; tighter bounds let
                                     more rows take the fused block update) */
+  const float* act_tab;          /* NULL, or lsk_act_table's table for `act` built from `frac`: the
+                                    same results, the activation read per gate value */
 } lsk_moe_args;
 
 int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt);
+
+/* The activation's gate part over all 65536 bf16 bit patterns g, for lsk_moe_args.act_tab (no
+ * reference counterpart as a table; the values are moe_ref's): act = LSK_ACT_SILU:
+ * table[g] = silu_contract(g) (binary32, lockstep_fullstack.py:590-604); LSK_ACT_SWIGLUOAI:
+ * table[g] = bfr(gc * sigmoid_contract(bfr(gc * 1.702))), gc = min(g, 7) (moe_ref.py:172-180).
+ * In the MoE epilogues the gate value is always bf16-valued, so act(g, u) = bfr(table[g] * u)
+ * (SiLU) or bfr((clamp(u, -7, 7) + 1) * table[g]) (SwiGLU-OAI), the same bits as step by step.
+ * frac: the [8192] FRAC table; table: [65536] binary32 on the device. */
+int lsk_act_table(const int32_t* frac, int act, float* table, void* stream);
 
 int lsk_moe_forward(const lsk_moe_args* args, void* stream);
 
@@ -387,7 +399,8 @@ int lsk_moe_forward(const lsk_moe_args* args, void* stream);
  * lsk_moe_forward on the 128x128 register-staged tile (0), on the eight-wave ping-pong
  * 128x256 tile (1), on the grouped GEMV (2: whole weight rows streamed once against up to 8
  * rows per expert at a time; taken only for int8 experts without rotation, T <= 64 and
- * H, I <= 4096, the tiles otherwise), or chosen by size (-1, the default: the GEMV where it
+ * H, I <= 4096, the tiles otherwise), on the 128x256 tile with the four-wave main loop (3: one wave
+ * per SIMD per block, 64x128 wave tiles), or chosen by size (-1, the default: the GEMV where it
  * applies, ping-pong once the routed rows reach E x 128).  Results are identical for every
  * choice.  Process-wide. */
 int lsk_moe_select(int variant);

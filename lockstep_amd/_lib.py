@@ -61,6 +61,7 @@ SIGNATURES = {
     "lsk_mx_epilogue": (_I, [_P, _I64, _I64, _P, _P, _P, _P]),
     "lsk_dequant_mxfp4": (_I, [_P, _P, _I64, _I64, _I, _P, _I, _P]),
     "lsk_blockquant": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
+    "lsk_act_table": (_I, [_P, _I, _P, _P]),
     "lsk_gemm_mx2": (_I, [_P, _I64, _P, _I64, _P, _I, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _P]),
     "lsk_mx_pack_m2": (_I, [_P, _I64, _P, _P, _P]),
     "lsk_moe_workspace": (_I64, [_I64, _I, _I64, _I64, _I64, _I, _I]),
@@ -77,7 +78,7 @@ class MoeArgs(ctypes.Structure):
                 ("x", _P), ("idx", _P), ("w", _P), ("w13_ptrs", _P), ("ldw13", _I64), ("ws13_ptrs", _P),
                 ("b13_ptrs", _P), ("w2_ptrs", _P), ("ldw2", _I64), ("ws2_ptrs", _P), ("b2_ptrs", _P),
                 ("frac", _P), ("rot_blk", _I), ("rot_scale", ctypes.c_float), ("shared", _P), ("y", _P), ("workspace", _P), ("workspace_bytes", _I64),
-                ("kw13_min", _I), ("kw13_max", _I), ("kw2_min", _I), ("kw2_max", _I)]
+                ("kw13_min", _I), ("kw13_max", _I), ("kw2_min", _I), ("kw2_max", _I), ("act_tab", _P)]
 
 _lock = threading.Lock()
 _lib = None

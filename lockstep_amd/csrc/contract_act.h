@@ -37,12 +37,34 @@ LSK_DEV float act_silu(float g, float u, const int32_t* frac) { return bfr(f32_m
 
 // moe_ref.py:172-180: gc = min(g, 7); uc = clamp(u, -7, 7); arg = bfr(gc * 1.702);
 // glu = bfr(gc * sig(arg)); h = bfr((uc + 1) * glu)
-LSK_DEV float act_swigluoai(float g, float u, const int32_t* frac) {
+LSK_DEV float glu_oai(float g, const int32_t* frac) {
   const float gc = fminf(g, 7.0f);
-  const float uc = fminf(fmaxf(u, -7.0f), 7.0f);
   const float arg = bfr(f32_mul(gc, kAlpha));
-  const float glu = bfr(f32_mul(gc, sigmoid_contract(arg, frac)));
+  return bfr(f32_mul(gc, sigmoid_contract(arg, frac)));
+}
+LSK_DEV float swigluoai_up(float u, float glu) {
+  const float uc = fminf(fmaxf(u, -7.0f), 7.0f);
   return bfr(f32_mul(f32_add(uc, 1.0f), glu));
+}
+LSK_DEV float act_swigluoai(float g, float u, const int32_t* frac) { return swigluoai_up(u, glu_oai(g, frac)); }
+
+// The gate's part of an activation depends on g alone, and in the MoE epilogues g is always
+// bf16-valued (a bfr result), so it can be read from a table of the 65536 bf16 bit patterns built
+// once by the functions above (lsk_act_table): SiLU tab[g] = silu_contract(g) (binary32, the
+// unrounded factor of bfr(silu(g) * u)); SwiGLU-OAI tab[g] = glu_oai(g).  The lookup then replaces
+// the FRAC gather, the divide and the rest of the per-element steps with the same values.
+LSK_DEV float act_table_entry(int act, uint32_t bits, const int32_t* frac) {
+  const float g = __uint_as_float(bits << 16);
+  return act == LSK_ACT_SILU ? silu_contract(g, frac) : glu_oai(g, frac);
+}
+
+// act(g, u) for bf16-valued g: from the table when one is given, else step by step.
+LSK_DEV float act_eval(int act, float g, float u, const int32_t* frac, const float* tab) {
+  if (tab) {
+    const float t = tab[__float_as_uint(g) >> 16];
+    return act == LSK_ACT_SILU ? bfr(f32_mul(t, u)) : swigluoai_up(u, t);
+  }
+  return act == LSK_ACT_SILU ? act_silu(g, u, frac) : act_swigluoai(g, u, frac);
 }
 
 }  // namespace lsk

@@ -19,6 +19,13 @@ __global__ __launch_bounds__(256) void act_kernel(const float* __restrict__ g, c
   }
 }
 
+// The activation's gate table over the 65536 bf16 bit patterns (contract_act.h).
+__global__ __launch_bounds__(256) void act_table_kernel(const int32_t* __restrict__ frac, int act,
+                                                        float* __restrict__ tab) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  tab[i] = lsk::act_table_entry(act, i, frac);
+}
+
 // moe_ref.py:64-74
 __global__ __launch_bounds__(256) void table_scores_kernel(const float* __restrict__ dgap, int64_t n,
                                                            const int32_t* __restrict__ tab, int64_t* __restrict__ out) {
@@ -97,4 +104,11 @@ extern "C" int lsk_fwht_blocks(const float* x, int64_t rows, int64_t D, int64_t 
   hipLaunchKernelGGL(fwht_kernel, dim3((unsigned)(rows * nb)), dim3(threads), 0, (hipStream_t)stream, x, ldx, (int)nb, blk,
                      scale, y, ldy);
   return lsk::check_launch("fwht_kernel");
+}
+
+extern "C" int lsk_act_table(const int32_t* frac, int act, float* table, void* stream) {
+  LSK_REQUIRE(act == LSK_ACT_SILU || act == LSK_ACT_SWIGLUOAI, "lsk_act_table: unknown act %d", act);
+  LSK_REQUIRE(frac && table, "lsk_act_table: null pointer");
+  hipLaunchKernelGGL(act_table_kernel, dim3(65536 / 256), dim3(256), 0, (hipStream_t)stream, frac, act, table);
+  return lsk::check_launch("act_table_kernel");
 }

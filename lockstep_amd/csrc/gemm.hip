@@ -12,6 +12,7 @@
 // tiling and K-splits never change a bit; the epilogue is applied once per output element.
 #include "mfma_tile.h"
 #include "pp_tile.h"
+#include "w4_tile.h"
 
 namespace {
 
@@ -184,16 +185,16 @@ __device__ __forceinline__ void pp_epilogue(const typename C::Acc& acc, const Ep
   }
 }
 
-// Dense ping-pong tile kernel (512 threads, eight waves in two alternating groups); same
-// operand contract and tile order as gemm_i8_mfma_kernel.  The epilogue operands of the tile
-// (asc / row exponents, ws, bias, column exponents) are loaded into registers before the main
-// loop and parked in LDS after it, so the epilogue itself touches global memory only to store.
-template <int BM, int BN, int WM, int WN, int RING, int BKB>
-__global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(const int8_t* __restrict__ A, int lda,
-                                                         const int8_t* __restrict__ W, int ldw, int M, int N, int K,
-                                                         EpiParams ep, int vec_ok) {
-  using C = lsk::PPCfg<BM, BN, WM, WN, RING, BKB>;
-  extern __shared__ __attribute__((aligned(16))) char smem_pp[];
+// One dense tile (eight-wave ping-pong or four-wave main loop, MAIN); same operand contract and
+// tile order as gemm_i8_mfma_kernel.  The epilogue operands of the tile (asc / row exponents,
+// ws, bias, column exponents) are loaded into registers before the main loop and parked in LDS
+// after it, so the epilogue itself touches global memory only to store.
+template <class C, class MAIN>
+__device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int lda, const int8_t* __restrict__ W,
+                                              int ldw, int M, int N, int K, const EpiParams& ep, int vec_ok,
+                                              char* smem_pp, MAIN main) {
+  constexpr int BM = C::kBM, BN = C::kBN;
+  constexpr int kWaves = C::kThreads / 64;
   const int mtiles = (M + BM - 1) / BM, ntiles = (N + BN - 1) / BN;
   const int L = lsk::xcd_logical_id(blockIdx.x, mtiles * ntiles);
   constexpr int GM = 16;
@@ -204,7 +205,6 @@ __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(co
   const int m0 = (first_m + r % gsize) * BM, n0 = (r / gsize) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int wm = wave / WN, wn = wave % WN;
 
   // epilogue operands: thread t holds row m0 + t and column n0 + t
   float s_row = 0.0f, s_ws = 0.0f, s_b = 0.0f;
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(co
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra_res, pa, rb_res, pb, K, smem_pp);
+  main(acc, ra_res, pa, rb_res, pb, K, smem_pp);
 
   // every wave is past its last read of the LDS ring
   float* sc_row = (float*)(smem_pp + C::kScaleOff);
@@ -257,12 +257,14 @@ __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(co
     sc_b[tid] = s_b;
     sc_ec[tid] = s_ec;
   }
-  // per wave: whether one of its operands rules out the fast epilogue (a NaN output possible)
+  // per wave: whether one of its operands rules out the fast epilogue (a NaN output possible);
+  // eight flag words, the unused ones clear
   int* sc_flag = (int*)(smem_pp + C::kFlagOff);
   const bool odd = (tid < BM && !(__builtin_fabsf(s_row) < __builtin_inff())) ||
                    (tid < BN && !(__builtin_fabsf(s_ws) < 0x1p96f));
   const bool wave_odd = __builtin_amdgcn_ballot_w64(odd) != 0;
   if (lane == 0) sc_flag[wave] = wave_odd ? 1 : 0;
+  if (kWaves < 8 && tid < 8 - kWaves) sc_flag[kWaves + tid] = 0;
   __syncthreads();
   // each wave stages its own 32-row strips, then stores them through the epilogue
   const bool bias = ep.bias != nullptr;
@@ -291,6 +293,34 @@ __global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(co
   LSK_PP_EPI(LSK_EPI_RAW, LSK_I32, false)
 #undef LSK_PP_EPI
   pp_epilogue<C, -1, -1, false, 0>(acc, ep, m0, n0, M, N, vec_ok, smem_pp);  // any other combination
+}
+
+// Dense ping-pong tile kernel (512 threads, eight waves in two alternating groups).
+template <int BM, int BN, int WM, int WN, int RING, int BKB>
+__global__ __launch_bounds__(512, (RING == 3 ? 2 : 1)) void gemm_i8_pp_kernel(const int8_t* __restrict__ A, int lda,
+                                                         const int8_t* __restrict__ W, int ldw, int M, int N, int K,
+                                                         EpiParams ep, int vec_ok) {
+  using C = lsk::PPCfg<BM, BN, WM, WN, RING, BKB>;
+  extern __shared__ __attribute__((aligned(16))) char smem_pp[];
+  contract_tile<C>(A, lda, W, ldw, M, N, K, ep, vec_ok, smem_pp,
+                   [](typename C::Acc& acc, __amdgpu_buffer_rsrc_t ra, const typename C::RowsA& pa,
+                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm) {
+                     lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra, pa, rb, pb, K_, sm);
+                   });
+}
+
+// Dense four-wave tile kernel (256 threads, one wave per SIMD, 128-row wave tiles; w4_tile.h).
+template <int BM, int BN, int RING>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_i8_w4_kernel(
+    const int8_t* __restrict__ A, int lda, const int8_t* __restrict__ W, int ldw, int M, int N, int K, EpiParams ep,
+    int vec_ok) {
+  using C = lsk::W4Cfg<BM, BN, RING>;
+  extern __shared__ __attribute__((aligned(16))) char smem_pp[];
+  contract_tile<C>(A, lda, W, ldw, M, N, K, ep, vec_ok, smem_pp,
+                   [](typename C::Acc& acc, __amdgpu_buffer_rsrc_t ra, const typename C::RowsA& pa,
+                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm) {
+                     lsk::w4_mainloop<C>(acc, ra, pa, rb, pb, K_, sm);
+                   });
 }
 
 // Decode GEMV (M <= 32), bandwidth-bound on the weight stream: one block per 16 output
@@ -952,6 +982,29 @@ static int launch_pp(const int8_t* a, int lda, const int8_t* w, int ldw, int M, 
   return check_launch(name);
 }
 
+template <int BM, int BN, int RING = 4>
+static int launch_w4(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K, const EpiParams& ep,
+                     int vec_ok, hipStream_t s, const char* name) {
+  using C = W4Cfg<BM, BN, RING>;
+  static bool attr_set = false;
+  auto kern = gemm_i8_w4_kernel<BM, BN, RING>;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmemBytes) !=
+        hipSuccess) {
+      set_error("%s: cannot reserve %d bytes of LDS", name, C::kSmemBytes);
+      return LSK_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  LSK_REQUIRE(tiles <= 0x7fffffff, "gemm: too many tiles");
+  const int64_t esz = (ep.out_dtype == LSK_BF16 || ep.out_dtype == LSK_F16) ? 2 : 4;
+  const int vflag = (vec_ok && (int64_t)(BM - 1) * ep.ldo * esz + BN * esz < 0x7fffffff) ? 2 : vec_ok;
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C::kThreads), C::kSmemBytes, s, a, lda, w, ldw, M, N, K, ep,
+                     vflag);
+  return check_launch(name);
+}
+
 static int pick_tile(int64_t M, int64_t N) {
   if (g_force_tile >= 0) return g_force_tile;
   if (g_force_tile == 5) return 0;  // the GEMV takes M <= 32 only
@@ -1149,6 +1202,8 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     case 4: return launch_pp<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4>");
     case 12: return launch_pp<256, 128, 4, 2, 3>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x128,4x2,r3>");
     case 13: return launch_pp<128, 256, 2, 4, 3>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4,r3>");
+    case 16: return launch_w4<256, 256>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_w4<256x256>");
+    case 17: return launch_w4<256, 128>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_w4<256x128>");
     default: return launch_tile<128, 128, 2, 2>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8<128x128,2x2>");
   }
 }
@@ -1219,7 +1274,7 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 15, "lsk_gemm_select: tile id %d not in [-1, 15]", tile_id);
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 17, "lsk_gemm_select: tile id %d not in [-1, 17]", tile_id);
   lsk::g_force_tile = ((tile_id >= 6 && tile_id <= 11) || tile_id == 14 || tile_id == 15) ? 5 : tile_id;
   lsk::g_gemv_mid = tile_id == 14 ? 1 : (tile_id == 15 ? 2 : 0);
   lsk::g_gemv_variant = (tile_id == 6 || tile_id == 7) ? tile_id - 5 : 0;

@@ -17,13 +17,16 @@
 #include "mfma_tile.h"
 #include "moe_internal.h"
 #include "pp_tile.h"
+#include "w4_tile.h"
 
 namespace {
 
 constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
 constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
 constexpr int kBM = lsk::kMoeBM;
-int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV
+int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV,
+                       // 3 the 128x256 tile on the four-wave main loop
+int g_moe_w4 = 0;      // the 128x256 tile's main loop: 0 eight-wave ping-pong, 1 four waves
 
 // ---------------------------------------------------------------- router
 LSK_DEV long long wave_max_ll(long long v) {
@@ -403,7 +406,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
                   yu = bfr(f32_add(yu, bias[a.N + hc]));
                 }
                 const float hv =
-                    a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
+                    lsk::act_eval(a.act, yg, yu, a.frac, a.act_tab);
                 hb[t] = f32_to_bf16(hv);
                 am = fmaxf(am, fabsf(hv));
               }
@@ -459,19 +462,23 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
     }
 }
 
-// Grouped GEMM on the eight-wave ping-pong main loop: a 128-row expert tile (the dispatch's tile
-// granularity) by 256 weight rows; a three-stage LDS ring keeps a block under 80 KB so two
-// blocks share a CU and one's epilogue overlaps the other's main loop.  MODE 0 (gate/up): the 256 weight rows are 128 h-columns'
-// gate and up rows interleaved per 32, so each wave's 64-column strip holds a [gate 32 | up 32]
-// pair and the activation is thread-local; MODE 1 (down): 256 output columns.  The epilogue
-// operands of the tile (row scales, routing weights and slots, column scales and biases) are
-// loaded before the main loop and parked in LDS after it.
-using PPM = lsk::PPCfg<128, 256, 2, 4, 3>;  // three-stage ring: two blocks per CU
+// Grouped GEMM tile: a 128-row expert tile (the dispatch's tile granularity) by 256 weight rows,
+// on the eight-wave ping-pong main loop (PPM: waves of 64 x 64) or the four-wave one (W4M: waves of
+// 64 x 128, one barrier per 16 MFMAs instead of two per 8); both rings take three stages, so two
+// blocks share a CU and one's epilogue overlaps the other's main loop.  MODE 0 (gate/up): the 256
+// weight rows are 128 h-columns' gate and up rows interleaved per 32, so a wave's strip holds
+// [gate 32 | up 32] pairs and the activation is thread-local; MODE 1 (down): 256 output columns.
+// The epilogue operands of the tile (row scales, routing weights and slots, column scales and
+// biases) are loaded before the main loop and parked in LDS after it.
+using PPM = lsk::PPCfg<128, 256, 2, 4, 3>;
+using W4M = lsk::W4Cfg<128, 256, 3>;
 static_assert(PPM::kSmemBytes - PPM::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
+static_assert(W4M::kSmemBytes - W4M::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
+static_assert(2 * W4M::kSmemBytes <= 160 * 1024 && 2 * PPM::kSmemBytes <= 160 * 1024, "two blocks per CU");
 
-template <int MODE>
-__global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char smem_moe[];
+template <class C, int MODE, class MAIN>
+__device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, MAIN main) {
+  static_assert(C::kBM == 128 && C::kBN == 256 && C::TM == 2, "128 x 256 tiles, two 32-row strips per wave");
   const int ntiles = MODE == 0 ? (a.N + 127) / 128 : (a.N + 255) / 256;
   const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
   const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
@@ -483,7 +490,7 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
   const float* ws = (const float*)a.ws_ptrs[e];
   const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int wm = wave / PPM::kWN, wn = wave % PPM::kWN;
+  const int wm = wave / C::kWN, wn = wave % C::kWN;
 
   // weight row of local column c (gate/up interleave) and whether it exists
   auto wrow_of = [&](int c, int& hc) {
@@ -520,33 +527,33 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
 
   const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(a.A, a.a_bytes);
   const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(wb, a.w_bytes);
-  typename PPM::RowsA pa;
-  typename PPM::RowsB pb;
+  typename C::RowsA pa;
+  typename C::RowsB pb;
 #pragma unroll
-  for (int j = 0; j < PPM::kLA; ++j) {
+  for (int j = 0; j < C::kLA; ++j) {
     int row, kb;
-    lsk::pp_slot<PPM::kThreads, PPM::kChunks>(tid, j, row, kb);
+    lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
     const int p = p0 + row;
     const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
     pa[j] = src >= 0 ? (uint32_t)(src * a.lda) : lsk::kOob;
   }
 #pragma unroll
-  for (int j = 0; j < PPM::kLB; ++j) {
+  for (int j = 0; j < C::kLB; ++j) {
     int row, kb, hc;
-    lsk::pp_slot<PPM::kThreads, PPM::kChunks>(tid, j, row, kb);
+    lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
     const int wr = wrow_of(row, hc);
     pb[j] = hc < a.N ? (uint32_t)(wr * a.ldw) : lsk::kOob;
   }
-  typename PPM::Acc acc;
+  typename C::Acc acc;
 #pragma unroll
-  for (int i = 0; i < PPM::TM; ++i)
+  for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < PPM::TN; ++j) acc[i][j] = lsk::zero16();
+    for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  lsk::pp_mainloop<128, 256, 2, 4, 3>(acc, ra_res, pa, rb_res, pb, a.K, smem_moe);
+  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe);
 
   // park the operands in LDS (past every wave's last ring read)
-  float* sc_asc = (float*)(smem_moe + PPM::kScaleOff);
+  float* sc_asc = (float*)(smem_moe + C::kScaleOff);
   float* sc_w = sc_asc + 128;
   int* sc_dst = (int*)(sc_w + 128);
   float* sc_ws = (float*)(sc_dst + 128);
@@ -562,19 +569,22 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
   }
   __syncthreads();
 
-  int32_t* region = (int32_t*)(smem_moe + wave * PPM::kStripBytes);
+  int32_t* region = (int32_t*)(smem_moe + wave * C::kStripBytes);
   auto strip = [&](int i) {
     if (MODE == 0) {
-      // 32 rows x 8 column quads of [gate | up]; a lane keeps one quad (lane & 7)
+      // a wave strip is 32 rows x P [gate 32 | up 32] pairs; 8 lanes cover a pair's 32 columns
+      // by quads, LPR lanes a row
+      constexpr int P = C::WTN / 64, LPR = 8 * P, RPP = 64 / LPR;
+      const int pr = (lane >> 3) % P;
       const int c4 = (lane & 7) * 4;
-      const int hc0 = nt * 128 + wn * 32 + c4;
+      const int hc0 = nt * 128 + wn * (32 * P) + pr * 32 + c4;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int row = (lane >> 3) + 8 * t;
-        const int ml = wm * PPM::WTM + i * 32 + row;
+      for (int t = 0; t < 32 / RPP; ++t) {
+        const int row = lane / LPR + RPP * t;
+        const int ml = wm * C::WTM + i * 32 + row;
         const int p = p0 + ml;
-        const v4i vg = *(const v4i*)(region + row * PPM::kLdc + c4);
-        const v4i vu = *(const v4i*)(region + row * PPM::kLdc + 32 + c4);
+        const v4i vg = *(const v4i*)(region + row * C::kLdc + pr * 64 + c4);
+        const v4i vu = *(const v4i*)(region + row * C::kLdc + pr * 64 + 32 + c4);
         float am = 0.0f;
         if (p < p1) {
           const float asc = sc_asc[ml];
@@ -584,7 +594,7 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
             const int hc = hc0 + q;
             hb[q] = 0;
             if (hc < a.N) {
-              const int cg = wn * 64 + c4 + q, cu = cg + 32;
+              const int cg = wn * C::WTN + pr * 64 + c4 + q, cu = cg + 32;
               float yg = bfr(f32_mul(f32_mul((float)vg[q], sc_ws[cg]), asc));
               float yu = bfr(f32_mul(f32_mul((float)vu[q], sc_ws[cu]), asc));
               if (bias) {
@@ -592,7 +602,7 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
                 yu = bfr(f32_add(yu, sc_b[cu]));
               }
               const float hv =
-                  a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
+                  lsk::act_eval(a.act, yg, yu, a.frac, a.act_tab);
               hb[q] = f32_to_bf16(hv);
               am = fmaxf(am, fabsf(hv));
             }
@@ -606,28 +616,28 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
               if (hc0 + q < a.N) dst[q] = hb[q];
           }
         }
-        am = fmaxf(am, __shfl_xor(am, 1, 64));
-        am = fmaxf(am, __shfl_xor(am, 2, 64));
-        am = fmaxf(am, __shfl_xor(am, 4, 64));
-        if ((lane & 7) == 0 && p < p1) atomicMax(&a.h_amax[p], __float_as_uint(am));
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+        if (lane % LPR == 0 && p < p1) atomicMax(&a.h_amax[p], __float_as_uint(am));
       }
     } else {
-      // 32 rows x 16 column quads; a lane keeps one quad (lane & 15)
-      const int c4 = (lane & 15) * 4;
-      const int n0 = nt * 256 + wn * 64 + c4;
+      // 32 rows x QPR column quads; a lane keeps one quad
+      constexpr int QPR = C::WTN / 4, RPP = 64 / QPR;
+      const int c4 = (lane % QPR) * 4;
+      const int n0 = nt * 256 + wn * C::WTN + c4;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int row = (lane >> 4) + 4 * t;
-        const int ml = wm * PPM::WTM + i * 32 + row;
+      for (int t = 0; t < 32 / RPP; ++t) {
+        const int row = lane / QPR + RPP * t;
+        const int ml = wm * C::WTM + i * 32 + row;
         const int p = p0 + ml;
-        const v4i v = *(const v4i*)(region + row * PPM::kLdc + c4);
+        const v4i v = *(const v4i*)(region + row * C::kLdc + c4);
         if (p < p1 && n0 < a.N) {
           const float asc = sc_asc[ml];
           const float wt = sc_w[ml];
           uint16_t ob[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int cl = wn * 64 + c4 + q;
+            const int cl = wn * C::WTN + c4 + q;
             ob[q] = 0;
             if (n0 + q < a.N) {
               float yv = bfr(f32_mul(f32_mul((float)v[q], sc_ws[cl]), asc));
@@ -647,10 +657,28 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
       }
     }
   };
-  lsk::pp_stage_strip<PPM::TN, PPM::kLdc>(acc[0], region);
+  lsk::pp_stage_strip<C::TN, C::kLdc>(acc[0], region);
   strip(0);
-  lsk::pp_stage_strip<PPM::TN, PPM::kLdc>(acc[1], region);
+  lsk::pp_stage_strip<C::TN, C::kLdc>(acc[1], region);
   strip(1);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_moe[];
+  moe_tile<PPM, MODE>(a, smem_moe,
+                      [](PPM::Acc& acc, __amdgpu_buffer_rsrc_t ra, const PPM::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
+                         const PPM::RowsB& pb, int K, char* sm) {
+                        lsk::pp_mainloop<128, 256, 2, 4, 3>(acc, ra, pa, rb, pb, K, sm);
+                      });
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void moe_w4_kernel(MoeGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_moe[];
+  moe_tile<W4M, MODE>(a, smem_moe,
+                      [](W4M::Acc& acc, __amdgpu_buffer_rsrc_t ra, const W4M::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
+                         const W4M::RowsB& pb, int K, char* sm) { lsk::w4_mainloop<W4M>(acc, ra, pa, rb, pb, K, sm); });
 }
 
 // ---------------------------------------------------------------- decode-sized grouped GEMV
@@ -805,6 +833,7 @@ template <int PER, bool OUT_BF16>
 __global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* __restrict__ gu,
                                                               const int32_t* __restrict__ nrows, int I, int act,
                                                               const int32_t* __restrict__ frac,
+                                                              const float* __restrict__ tab,
                                                               void* __restrict__ q, float* __restrict__ asc) {
   __shared__ float red[16];
   const int p = blockIdx.x;
@@ -820,7 +849,7 @@ __global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* _
     hv[t] = 0.0f;
     if (c < I) {
       const float yg = bf16_to_f32(g[c]), yu = bf16_to_f32(u[c]);
-      hv[t] = act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, frac) : lsk::act_swigluoai(yg, yu, frac);
+      hv[t] = lsk::act_eval(act, yg, yu, frac, tab);
       am = fmaxf(am, fabsf(hv[t]));
     }
   }
@@ -1027,7 +1056,23 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
 
 template <int MODE>
 int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const char* name) {
-  static_assert(PPM::TM == 2, "the epilogue stages two 32-row strips");
+  const int ntiles = MODE == 0 ? (ga.N + 127) / 128 : (ga.N + 255) / 256;
+  const int64_t blocks = max_tiles * ntiles;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  if (g_moe_w4) {
+    static bool attr_w4 = false;
+    if (!attr_w4) {
+      if (hipFuncSetAttribute((const void*)moe_w4_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              W4M::kSmemBytes) != hipSuccess) {
+        lsk::set_error("%s: cannot reserve %d bytes of LDS", name, W4M::kSmemBytes);
+        return LSK_ERR_HIP;
+      }
+      attr_w4 = true;
+    }
+    hipLaunchKernelGGL(moe_w4_kernel<MODE>, dim3((unsigned)blocks), dim3(256), W4M::kSmemBytes, s, ga);
+    return lsk::check_launch(name);
+  }
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)moe_pp_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1037,10 +1082,6 @@ int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const
     }
     attr_set = true;
   }
-  const int ntiles = MODE == 0 ? (ga.N + 127) / 128 : (ga.N + 255) / 256;
-  const int64_t blocks = max_tiles * ntiles;
-  if (blocks == 0) return LSK_OK;
-  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
   hipLaunchKernelGGL(moe_pp_kernel<MODE>, dim3((unsigned)blocks), dim3(512), PPM::kSmemBytes, s, ga);
   return lsk::check_launch(name);
 }
@@ -1110,8 +1151,9 @@ extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t 
 }
 
 extern "C" int lsk_moe_select(int variant) {
-  LSK_REQUIRE(variant >= -1 && variant <= 2, "lsk_moe_select: variant %d not in [-1, 2]", variant);
+  LSK_REQUIRE(variant >= -1 && variant <= 3, "lsk_moe_select: variant %d not in [-1, 3]", variant);
   g_moe_force = variant;
+  g_moe_w4 = variant == 3 ? 1 : 0;
   return LSK_OK;
 }
 
@@ -1168,7 +1210,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   const int64_t R = T * k;
   // the ping-pong grouped GEMM once experts average a full 128-row tile or more; the 128x128
   // register-staged tile below that (decode-sized token counts)
-  const bool use_pp = g_moe_force >= 0 ? g_moe_force == 1 : R >= (int64_t)E * kBM;
+  const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= (int64_t)E * kBM;
   // the grouped GEMV for decode token counts (whole weight rows streamed once per tile)
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
   const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096;
@@ -1246,6 +1288,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   g1.N = (int)I;
   g1.act = a->act;
   g1.frac = a->frac;
+  g1.act_tab = a->act_tab;
   g1.h = w.h;
   g1.h_amax = w.h_amax;
   g1.lds = a->lds13;
@@ -1278,9 +1321,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
 #define LSK_ACTQ(P)                                                                                             \
   {                                                                                                             \
     if (mx) hipLaunchKernelGGL((moe_act_requant_kernel<P, true>), grid, blk, 0, s, w.gu, w.offs + E, (int)I,    \
-                               a->act, a->frac, (void*)w.qh, w.asch);                                           \
+                               a->act, a->frac, a->act_tab, (void*)w.qh, w.asch);                               \
     else hipLaunchKernelGGL((moe_act_requant_kernel<P, false>), grid, blk, 0, s, w.gu, w.offs + E, (int)I,      \
-                            a->act, a->frac, (void*)w.qh, w.asch);                                              \
+                            a->act, a->frac, a->act_tab, (void*)w.qh, w.asch);                                  \
   }
     if (per <= 1) LSK_ACTQ(1) else if (per <= 2) LSK_ACTQ(2) else if (per <= 4) LSK_ACTQ(4) else LSK_ACTQ(8)
 #undef LSK_ACTQ

@@ -25,6 +25,7 @@ struct MoeGemmArgs {
   int N;                    // gate/up: I (h columns); down: H
   int act;
   const int32_t* frac;
+  const float* act_tab;     // the activation's gate table (65536 entries) or null
   uint16_t* h;              // gate/up out [R, I] bf16
   uint32_t* h_amax;         // [R]
   const float* row_w;       // down: routing weight per row

@@ -283,7 +283,7 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
                 yg = bfr(f32_add(yg, bias[hc]));
                 yu = bfr(f32_add(yu, bias[a.N + hc]));
               }
-              const float hv = a.act == LSK_ACT_SILU ? lsk::act_silu(yg, yu, a.frac) : lsk::act_swigluoai(yg, yu, a.frac);
+              const float hv = lsk::act_eval(a.act, yg, yu, a.frac, a.act_tab);
               hb[t] = f32_to_bf16(hv);
               am = fmaxf(am, fabsf(hv));
             }

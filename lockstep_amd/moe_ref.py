@@ -26,6 +26,13 @@ from . import ops
 BF = torch.bfloat16
 F32 = torch.float32
 INT8_MIN_ROWS = 17   # API compatibility only: the kernels take any row count
+# The fused layers read the activation's gate part from a per-device table of all bf16 gate values
+# (ops.act_table); False evaluates it step by step in the epilogues (the same bits, slower).
+USE_ACT_TABLE = True
+
+
+def _act_tab(dev, act: int):
+    return ops.act_table(dev, act).data_ptr() if USE_ACT_TABLE else None
 
 
 def bfr(x: torch.Tensor) -> torch.Tensor:
@@ -249,7 +256,7 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
                   b13_ptrs=tables.b13.data_ptr() if tables.b13 is not None else None,
                   w2_ptrs=tables.w2.data_ptr(), ldw2=tables.ldw2, ws2_ptrs=tables.ws2.data_ptr(),
                   b2_ptrs=tables.b2.data_ptr() if tables.b2 is not None else None,
-                  frac=ops.frac_i32(x.device).data_ptr(), rot_blk=int(rot_blk),
+                  frac=ops.frac_i32(x.device).data_ptr(), act_tab=_act_tab(x.device, act), rot_blk=int(rot_blk),
                   rot_scale=(1.0 / (rot_blk ** 0.5)) if rot_blk else 0.0,
                   shared=sh.data_ptr() if sh is not None else None, y=y.data_ptr(),
                   workspace=work.data_ptr(), workspace_bytes=nbytes)
@@ -398,7 +405,7 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1):
                   ws13_ptrs=t.ws13.data_ptr(), b13_ptrs=t.b13.data_ptr() if t.b13 is not None else None,
                   w2_ptrs=t.w2.data_ptr(), ldw2=t.ldw2, ws2_ptrs=t.ws2.data_ptr(),
                   b2_ptrs=t.b2.data_ptr() if t.b2 is not None else None, frac=ops.frac_i32(x.device).data_ptr(),
-                  rot_blk=0, rot_scale=0.0, shared=None, y=y.data_ptr(), workspace=work.data_ptr(),
+                  act_tab=_act_tab(x.device, act), rot_blk=0, rot_scale=0.0, shared=None, y=y.data_ptr(), workspace=work.data_ptr(),
                   workspace_bytes=nbytes)
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
     return y

@@ -266,6 +266,22 @@ def frac_i32(dev) -> torch.Tensor:
     return CC.table_i32_on(dev)
 
 
+_ACT_TABLES = {}
+
+
+def act_table(dev, act: int) -> torch.Tensor:
+    """The activation's gate table over the 65536 bf16 bit patterns (lsk_act_table), built once per
+    device and activation."""
+    dev = torch.device(dev)
+    key = (str(dev), int(act))
+    t = _ACT_TABLES.get(key)
+    if t is None:
+        t = torch.empty(65536, dtype=torch.float32, device=dev)
+        L.call("lsk_act_table", L.ptr(frac_i32(dev)), int(act), L.ptr(t), L.stream_of(t))
+        _ACT_TABLES[key] = t
+    return t
+
+
 def tab_i32(tab: torch.Tensor) -> torch.Tensor:
     """A caller's router table (int64 in the reference) as the int32 table the kernels read."""
     L.require_cuda(tab, what="table")

@@ -132,6 +132,39 @@ def test_moe_small():
     _run_case(24, 8, 2, 256, 128, seed=3)
 
 
+def test_act_tables_over_every_bf16_gate():
+    """lsk_act_table against the oracle for every non-NaN bf16 gate pattern (65282 values, both
+    infinities included): SiLU's table is silu_contract(g) in binary32; SwiGLU-OAI's is the glu
+    factor, which the oracle's act gives at u = 0 (bfr(1 * glu) = glu).  A NaN gate has no value in
+    the reference (its table index is the int64 cast of NaN)."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import ops
+    g = C.bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    ok = ~np.isnan(g)
+    with np.errstate(all="ignore"):
+        want = {L.LSK_ACT_SILU: C.silu_contract(g[ok]),
+                L.LSK_ACT_SWIGLUOAI: C.act_swigluoai(g[ok], np.zeros_like(g[ok]))}
+    for act, ref in want.items():
+        got = ops.act_table(dev(), act).cpu().numpy()[ok]
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), act
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_moe_step_by_step_activation(variant):
+    """The layer without the activation table (the epilogues evaluate every step) gives the same
+    bits: the int8 kernels and the MXFP4 layer."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    MR.USE_ACT_TABLE = False
+    L.call("lsk_moe_select", variant)
+    try:
+        _run_case(150, 6, 2, 320, 96, seed=14, bias=True, act="swigluoai")
+        _run_case(40, 8, 3, 256, 192, seed=16)
+    finally:
+        MR.USE_ACT_TABLE = True
+        L.call("lsk_moe_select", -1)
+
+
 def test_moe_single_token_and_zero_load_experts():
     _run_case(1, 16, 4, 256, 128, seed=4)
 
@@ -160,10 +193,10 @@ def test_moe_multi_chunk_dispatch(T, E, k):
     _run_case(T, E, k, 128, 64, seed=11 + T)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_moe_grouped_gemm_variants(variant):
     """Every grouped-GEMM kernel (register-staged 128x128 tile, ping-pong 128x256 tile, the
-    decode GEMV) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
+    decode GEMV, the 128x256 tile on four waves) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
     their rows eight at a time), empty experts, a bias and SwiGLU-OAI."""
     from lockstep_amd import _lib as L
     L.call("lsk_moe_select", variant)

@@ -141,6 +141,18 @@ def test_moe_mx_small():
     assert np.array_equal(got, C.moe_forward_mx(x, oexp, idx, w, oact))
 
 
+@pytest.mark.parametrize("T", [5, 300])
+def test_moe_mx_step_by_step_activation(T):
+    """Without the activation table (decode GEMV at T = 5, tiles at T = 300) the same bits."""
+    from lockstep_amd import moe_ref as MR
+    MR.USE_ACT_TABLE = False
+    try:
+        x, oexp, idx, w, oact, got = _mx_case(T, 6, 2, 320, 192, seed=17, bias=True, act="swigluoai")
+    finally:
+        MR.USE_ACT_TABLE = True
+    assert np.array_equal(got, C.moe_forward_mx(x, oexp, idx, w, oact))
+
+
 def test_moe_mx_bias_swigluoai_packed_tables():
     x, oexp, idx, w, oact, got = _mx_case(40, 6, 3, 320, 192, seed=2, bias=True, act="swigluoai", from_m2=False)
     assert np.array_equal(got, C.moe_forward_mx(x, oexp, idx, w, oact))
