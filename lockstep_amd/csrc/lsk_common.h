@@ -58,6 +58,24 @@ LSK_DEV float f32_mul(float a, float b) { return a * b; }
 LSK_DEV float f32_add(float a, float b) { return a + b; }
 LSK_DEV float f32_div(float a, float b) { return a / b; }   // correctly rounded (build flag)
 
+// rint(fl32(v / s)) for the 8-bit row quantisers, given r = fl32(1 / s); there |v / s| is about 127
+// at most (|v| is at most the row maximum and s = fl32(max / 127)), and the argument holds for any
+// |v / s| < 256: y = fl32(v * r) differs from v / s by at most 256 * 2^-23 = 2^-15 (two roundings of
+// relative error <= 2^-24 each) and fl32(v / s) from v / s by at most half an ulp, 2^-17, so
+// |y - fl32(v / s)| < 2^-14.  Unless y lies within 2^-13 of a half-integer, both therefore round to
+// the same integer; only there is the division evaluated, behind a branch on the wave's ballot (a
+// select would have the compiler evaluate the division for every element).  (y - floor(y) is exact for |y| < 2^23; infinities and NaNs give what the division
+// gives: v * 0 for s = inf, NaN for NaN or infinite v over an infinite s.)
+LSK_DEV float rint_div8(float v, float s, float r) {
+  const float y = f32_mul(v, r);
+  const bool near = fabsf(y - floorf(y) - 0.5f) < 0x1p-13f;
+  float t = rintf(y);
+  if (__builtin_amdgcn_ballot_w64(near) != 0) {
+    if (near) t = rintf(f32_div(v, s));
+  }
+  return t;
+}
+
 // Load one activation element of the given dtype as binary32 (bf16 and f16 widen exactly).
 LSK_DEV float load_as_f32(const void* p, int dtype, int64_t i) {
   switch (dtype) {

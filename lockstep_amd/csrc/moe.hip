@@ -149,15 +149,16 @@ LSK_DEV void expert_offsets_and_tiles(const int32_t* cnt, int E, int32_t* offs, 
   for (int e = e0; e < e0 + per && e < E; ++e) {
     offs[e] = rbase;
     const int c = cnt[e];
-    for (int r0 = 0; r0 < c; r0 += kBM, ++tbase) {
-      tiles[1 + 2 * tbase] = e;
-      tiles[2 + 2 * tbase] = rbase + r0;
-    }
+    if (tiles)
+      for (int r0 = 0; r0 < c; r0 += kBM, ++tbase) {
+        tiles[1 + 2 * tbase] = e;
+        tiles[2 + 2 * tbase] = rbase + r0;
+      }
     rbase += c;
   }
   if (threadIdx.x == 0) {
     offs[E] = rows_all;
-    tiles[0] = tiles_all;
+    if (tiles) tiles[0] = tiles_all;
   }
 }
 
@@ -275,40 +276,44 @@ __global__ __launch_bounds__(256) void moe_count_kernel(const int64_t* __restric
   for (int e = tid; e < E; e += 256) ccnt[(int64_t)blockIdx.x * E + e] = cnt[e];
 }
 
-// Large T, step 2 (one block): expert offsets, tile table, and each chunk's first row per
-// expert cbase[chunk][E] (chunks ascending inside each expert: token order).
-__global__ __launch_bounds__(1024) void moe_scan_kernel(const int32_t* __restrict__ ccnt, int nchunks, int E,
-                                                        int32_t* __restrict__ cbase, int32_t* __restrict__ offs,
-                                                        int32_t* __restrict__ tiles) {
-  extern __shared__ int32_t tot[];  // [E]
-  __shared__ int tmp[16];
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    int s2 = 0;
-    for (int c = 0; c < nchunks; ++c) s2 += ccnt[(int64_t)c * E + e];
-    tot[e] = s2;
-  }
-  __syncthreads();
-  expert_offsets_and_tiles<1024>(tot, E, offs, tiles, tmp);
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    int run = offs[e];
-    for (int c = 0; c < nchunks; ++c) {
-      cbase[(int64_t)c * E + e] = run;
-      run += ccnt[(int64_t)c * E + e];
-    }
-  }
-}
-
-// Large T, step 3: place each chunk's rows.
+// Large T, step 2: each block sums the per-chunk counts itself (totals per expert and the
+// counts of the chunks before its own), derives the expert offsets, and places its chunk's rows
+// (chunks ascending inside each expert: token order); block 0 also writes the offsets and the
+// M-tile table.  LDS: tot / pre / offs [E, E, E + 1], the placement mask [E][8], the chunk's ids
+// [256 k] and weights [256 k] u16.
 __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restrict__ idx, const uint16_t* __restrict__ w,
-                                                        int T, int k, int E, const int32_t* __restrict__ cbase,
-                                                        int32_t* __restrict__ row_tok, int32_t* __restrict__ row_dst,
-                                                        float* __restrict__ row_w) {
-  extern __shared__ uint32_t mask[];  // [E][8], then the chunk's ids [256 k] and weights [256 k] u16
+                                                        int T, int k, int E, const int32_t* __restrict__ ccnt,
+                                                        int nchunks, int32_t* __restrict__ offs,
+                                                        int32_t* __restrict__ tiles, int32_t* __restrict__ row_tok,
+                                                        int32_t* __restrict__ row_dst, float* __restrict__ row_w) {
+  extern __shared__ int32_t sm_place[];
+  int32_t* tot = sm_place;
+  int32_t* pre = tot + E;
+  int32_t* offl = pre + E;
+  uint32_t* mask = (uint32_t*)(offl + E + 1);
   int32_t* ids = (int32_t*)(mask + 8 * E);
   uint16_t* wts = (uint16_t*)(ids + 256 * k);
-  load_chunk_routes(idx, w, T, k, E, blockIdx.x * 256, ids, wts);
-  place_chunk(ids, wts, T, k, E, blockIdx.x * 256, cbase + (int64_t)blockIdx.x * E, mask, row_tok, row_dst, row_w);
+  __shared__ int tmp[4];
+  const int c0 = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += 256) {
+    int all = 0, before = 0;
+    for (int c = 0; c < nchunks; ++c) {
+      const int v = ccnt[(int64_t)c * E + e];
+      all += v;
+      before += c < c0 ? v : 0;
+    }
+    tot[e] = all;
+    pre[e] = before;
+  }
+  __syncthreads();
+  expert_offsets_and_tiles<256>(tot, E, offl, c0 == 0 ? tiles : nullptr, tmp);
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += 256) {
+    if (c0 == 0) offs[e] = offl[e];
+    if (e < E) offl[e] += pre[e];  // this chunk's first row per expert
+  }
+  load_chunk_routes(idx, w, T, k, E, c0 * 256, ids, wts);  // ends with a barrier
+  place_chunk(ids, wts, T, k, E, c0 * 256, offl, mask, row_tok, row_dst, row_w);
 }
 
 __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x, int64_t n, float* __restrict__ y) {
@@ -860,14 +865,14 @@ __global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* _
   am = red[0];
 #pragma unroll
   for (int w2 = 1; w2 < 16; ++w2) am = fmaxf(am, red[w2]);
-  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f);
+  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, s);
   if (tid == 0) asc[p] = s;
 #pragma unroll
   for (int t = 0; t < PER; ++t) {
     const int c = tid + 1024 * t;
     if (c < I) {
       const float hb = bf16_to_f32(f32_to_bf16(hv[t]));  // h as the tiled kernels store it
-      const float qv = fminf(fmaxf(rintf(f32_div(hb, s)), -127.0f), 127.0f);
+      const float qv = fminf(fmaxf(rint_div8(hb, s, rs), -127.0f), 127.0f);
       if (OUT_BF16) ((uint16_t*)q)[(int64_t)p * I + c] = (uint16_t)(__float_as_uint(qv) >> 16);  // exact
       else ((int8_t*)q)[(int64_t)p * I + c] = (int8_t)(int)qv;
     }
@@ -885,7 +890,7 @@ __global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __rest
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int64_t p = i / chunks;
     const int c = (int)(i - p * chunks);
-    const float s = f32_div(fmaxf(__uint_as_float(amax[p]), kAmaxFloor), 127.0f);
+    const float s = f32_div(fmaxf(__uint_as_float(amax[p]), kAmaxFloor), 127.0f), rs = f32_div(1.0f, s);
     if (c == 0) asc[p] = s;
     const uint4 u = *(const uint4*)(h + p * I + c * 8);
     const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
@@ -894,8 +899,8 @@ __global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __rest
     for (int j = 0; j < 4; ++j) {
       const float v0 = bf16_to_f32((uint16_t)(wd[j] & 0xffff));
       const float v1 = bf16_to_f32((uint16_t)(wd[j] >> 16));
-      float q0 = fminf(fmaxf(rintf(f32_div(v0, s)), -127.0f), 127.0f);
-      float q1 = fminf(fmaxf(rintf(f32_div(v1, s)), -127.0f), 127.0f);
+      float q0 = fminf(fmaxf(rint_div8(v0, s, rs), -127.0f), 127.0f);
+      float q1 = fminf(fmaxf(rint_div8(v1, s, rs), -127.0f), 127.0f);
       const uint32_t b = ((uint32_t)(uint8_t)(int8_t)(int)q0) | (((uint32_t)(uint8_t)(int8_t)(int)q1) << 8);
       if (j < 2) lo |= b << (16 * j);
       else hi |= b << (16 * (j - 2));
@@ -940,10 +945,10 @@ __global__ __launch_bounds__(256) void moe_rot_requant_kernel(const uint16_t* __
   if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
   am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f);
+  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, s);
   if (tid == 0) asc[p] = s;
   for (int i = tid; i < I; i += 256) {
-    const float t = fminf(fmaxf(rintf(f32_div(rv[i], s)), -127.0f), 127.0f);
+    const float t = fminf(fmaxf(rint_div8(rv[i], s, rs), -127.0f), 127.0f);
     q[p * I + i] = (int8_t)(int)t;
   }
 }
@@ -995,7 +1000,6 @@ struct MoeWs {
   float* row_w;
   int32_t* tok_cnt;
   int32_t* ccnt;   // [chunks][E] per-chunk expert counts (T > 256)
-  int32_t* cbase;  // [chunks][E] first row of each chunk's rows per expert
   uint16_t* h;
   uint32_t* h_amax;
   int8_t* qh;
@@ -1036,7 +1040,6 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.tok_cnt = (int32_t*)take(T * 4);
   const int64_t nchunks = (T + 255) / 256;
   w.ccnt = (int32_t*)take(nchunks * E * 4);
-  w.cbase = (int32_t*)take(nchunks * E * 4);
   w.h = (uint16_t*)take(R * I * 2);
   w.h_amax = (uint32_t*)take((R + 2) * 4);  // + the two "some row flagged" words of block-scaled activations
   w.qh = (int8_t*)take(R * I * qb);
@@ -1234,7 +1237,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   }
   if (rc) return rc;
   // dispatch (and the zeroing of the per-row |h| maxima, which the gate/up GEMM raises); the
-  // routes of a 256-token chunk are staged in LDS (up to 88 KB at E = 1024, k = 32)
+  // routes of a 256-token chunk are staged in LDS (up to 92 KB at E = 1024, k = 32)
   static bool dispatch_lds = false;
   if (!dispatch_lds) {
     for (const void* f : {(const void*)moe_dispatch_small_kernel, (const void*)moe_count_kernel,
@@ -1260,12 +1263,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
                        a->idx, (int)T, k,
                        (int)E, w.ccnt, w.tok_cnt, w.h_amax, nzero);
     if ((rc = lsk::check_launch("moe_count_kernel"))) return rc;
-    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), (size_t)E * 4, s, w.ccnt, (int)nchunks, (int)E, w.cbase,
-                       w.offs, w.tiles);
-    if ((rc = lsk::check_launch("moe_scan_kernel"))) return rc;
-    hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 8 * 4 + (size_t)256 * k * 6,
-                       s, a->idx, a->w,
-                       (int)T, k, (int)E, w.cbase, w.row_tok, w.row_dst, w.row_w);
+    hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nchunks), dim3(256),
+                       (size_t)(11 * E + 1) * 4 + (size_t)256 * k * 6, s, a->idx, a->w, (int)T, k, (int)E, w.ccnt,
+                       (int)nchunks, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w);
     if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
   }
   if (mx == 2 &&

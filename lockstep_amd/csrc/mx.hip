@@ -21,8 +21,8 @@ int reserve_lds(K kern, int bytes, const char* name) {
 }
 
 // ---------------------------------------------------------------- quantisers emitting bf16 values
-LSK_DEV uint16_t q_bf16(float v, float s) {
-  const float t = fminf(fmaxf(rintf(f32_div(v, s)), -127.0f), 127.0f);
+LSK_DEV uint16_t q_bf16(float v, float s, float r) {
+  const float t = fminf(fmaxf(rint_div8(v, s, r), -127.0f), 127.0f);
   return (uint16_t)(__float_as_uint(t) >> 16);  // an integer of magnitude <= 127: exact in bf16
 }
 
@@ -37,9 +37,9 @@ __global__ __launch_bounds__(256) void rowquant_bf16_kernel(const uint16_t* __re
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
   __syncthreads();
   am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f);
+  const float s = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, s);
   if (threadIdx.x == 0) asc[t] = s;
-  for (int64_t i = threadIdx.x; i < H; i += 256) q[t * H + i] = q_bf16(bf16_to_f32(row[i]), s);
+  for (int64_t i = threadIdx.x; i < H; i += 256) q[t * H + i] = q_bf16(bf16_to_f32(row[i]), s, rs);
 }
 
 __global__ __launch_bounds__(256) void requant_bf16_kernel(const uint16_t* __restrict__ h, const uint32_t* __restrict__ amax,
@@ -51,15 +51,15 @@ __global__ __launch_bounds__(256) void requant_bf16_kernel(const uint16_t* __res
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int64_t p = i / chunks;
     const int c = (int)(i - p * chunks);
-    const float s = f32_div(fmaxf(__uint_as_float(amax[p]), kAmaxFloor), 127.0f);
+    const float s = f32_div(fmaxf(__uint_as_float(amax[p]), kAmaxFloor), 127.0f), rs = f32_div(1.0f, s);
     if (c == 0) asc[p] = s;
     const uint4 u = *(const uint4*)(h + p * I + c * 8);
     const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      o[j] = (uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] & 0xffff)), s) |
-             ((uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] >> 16)), s) << 16);
+      o[j] = (uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] & 0xffff)), s, rs) |
+             ((uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] >> 16)), s, rs) << 16);
     *(uint4*)(q + p * I + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }

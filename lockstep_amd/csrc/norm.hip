@@ -157,7 +157,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_float_kernel(NormArgs p, int vec
     amax = redq[0];
     for (int i = 1; i < W; ++i) amax = fmaxf(amax, redq[i]);
   }
-  const float s = f32_div(fmaxf(amax, kAmaxFloor), 127.0f);
+  const float s = f32_div(fmaxf(amax, kAmaxFloor), 127.0f), rcp = f32_div(1.0f, s);
   if (threadIdx.x == 0) p.asc[m] = s;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_float_kernel(NormArgs p, int vec
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      float t = rintf(f32_div(xv[c][j], s));
+      float t = rint_div8(xv[c][j], s, rcp);
       t = fminf(fmaxf(t, -127.0f), 127.0f);
       const uint32_t b = (uint32_t)(uint8_t)(int8_t)(int)t;
       if (j < 4) lo |= b << (8 * j);

@@ -19,8 +19,8 @@ LSK_DEV float block_max(float v, float* red) {
   return r;
 }
 
-LSK_DEV int8_t quant_one(float v, float s) {
-  float t = rintf(f32_div(v, s));  // fl32(x / asc), then round half to even
+LSK_DEV int8_t quant_one(float v, float s, float r) {
+  float t = rint_div8(v, s, r);  // fl32(x / asc), then round half to even (r = fl32(1 / asc))
   t = fminf(fmaxf(t, -127.0f), 127.0f);
   return (int8_t)(int)t;
 }
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(THREADS) void rowquant_kernel(const void* __restric
   }
   am = block_max<THREADS>(am, red);
   am = fmaxf(am, kAmaxFloor);
-  const float s = f32_div(am, 127.0f);
+  const float s = f32_div(am, 127.0f), rs = f32_div(1.0f, s);
   if (tid == 0) asc[m] = s;
   int8_t* qrow = q + m * ldq;
   if (vec) {
@@ -95,13 +95,13 @@ __global__ __launch_bounds__(THREADS) void rowquant_kernel(const void* __restric
       }
       uint32_t lo = 0, hi = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= ((uint32_t)(uint8_t)quant_one(v[j], s)) << (8 * j);
+      for (int j = 0; j < 4; ++j) lo |= ((uint32_t)(uint8_t)quant_one(v[j], s, rs)) << (8 * j);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= ((uint32_t)(uint8_t)quant_one(v[4 + j], s)) << (8 * j);
+      for (int j = 0; j < 4; ++j) hi |= ((uint32_t)(uint8_t)quant_one(v[4 + j], s, rs)) << (8 * j);
       ((uint2*)qrow)[c] = make_uint2(lo, hi);
     }
   } else {
-    for (int64_t k = tid; k < K; k += THREADS) qrow[k] = quant_one(load_as_f32(x, dtype, base + k), s);
+    for (int64_t k = tid; k < K; k += THREADS) qrow[k] = quant_one(load_as_f32(x, dtype, base + k), s, rs);
   }
 }
 
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __res
   }
   am = block_max<THREADS>(am, red);
   am = fmaxf(am, kAmaxFloor);
-  const float s = f32_div(am, 127.0f);
+  const float s = f32_div(am, 127.0f), rs = f32_div(1.0f, s);
   if (tid == 0) asc[m] = s;
   int8_t* qrow = q + m * ldq;
 #pragma unroll
@@ -163,9 +163,9 @@ __global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __res
     if (c < K8) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) lo |= ((uint32_t)(uint8_t)quant_one(v[j][e], s)) << (8 * e);
+      for (int e = 0; e < 4; ++e) lo |= ((uint32_t)(uint8_t)quant_one(v[j][e], s, rs)) << (8 * e);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) hi |= ((uint32_t)(uint8_t)quant_one(v[j][4 + e], s)) << (8 * e);
+      for (int e = 0; e < 4; ++e) hi |= ((uint32_t)(uint8_t)quant_one(v[j][4 + e], s, rs)) << (8 * e);
       ((uint2*)qrow)[c] = make_uint2(lo, hi);
     }
   }

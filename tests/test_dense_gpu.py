@@ -347,3 +347,37 @@ def test_column_split_into_whole_rounds_is_exact(N):
     yo = FS.w8a8_outlier_linear(bf16_dev(x), to_dev(oidx), bf16_dev(wo), to_dev(W8), to_dev(ws), to_dev(bias),
                                 out_dtype=torch.bfloat16)
     assert np.array_equal(bits(yo), C.w8a8_outlier_linear(x, oidx, wo, W8, ws, bias, "bf16"))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("K", [1024, 4104, 14336])
+def test_rowquant_near_half_integer_quotients(dtype, K):
+    """Values whose quotient x / asc lies on or next to a half-integer (x = fl32((n + 1/2) asc) and
+    its neighbours, for every n in [-127, 126]) under several row maxima (asc exact, inexact,
+    tiny, below the 1e-8 floor, huge): the quantisers round fl32(x / asc), which the fast
+    reciprocal path must reproduce exactly, ties to even included."""
+    from lockstep_amd import ops
+    say("rowquant near ties", dtype, K)
+    rows = []
+    for amax in (127.0, 100.0, 3.3, 1e-3, 5e-9, 7e30, 0.7):
+        a = np.float32(amax)
+        s = np.float32(max(a, np.float32(1e-8)) / np.float32(127.0))
+        vals = [a]
+        for n in range(-127, 127):
+            c = np.float32((n + 0.5) * np.float64(s))
+            vals += [c, np.nextafter(c, np.float32(np.inf)), np.nextafter(c, np.float32(-np.inf))]
+        v = np.array(vals, np.float32)
+        v = v[np.abs(v) <= a]
+        row = np.resize(v, K).astype(np.float32)
+        row[0] = a
+        rows.append(row)
+    x = np.stack(rows)
+    if dtype == "bf16":
+        x = C.bf16_to_f32(C.bf16_bits(x))
+        xd = bf16_dev(x)
+    else:
+        xd = to_dev(x)
+    q, asc = ops.rowquant(xd)
+    rq, rasc = C.rowquant(x)
+    assert np.array_equal(bits(asc), f32_bits(rasc))
+    assert np.array_equal(bits(q), rq)
