@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the contract matrix-multiply path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sections dense,decode,moe]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sections dense,decode,moe[,vendor]]
                     [--moe-cases NAME,...] [--eager] [--mx-variant V] [--moe-variant V]
 
 A step is one pass of the Llama-3.1-8B-shaped MLP contract GEMMs at M=2048 prefill rows:
@@ -99,6 +99,45 @@ def dense_section(torch, args):
                      "kernel": "gemm_i8_pp_kernel", "per_shape": per_shape,
                      "note": "int8 ops (2 per MAC) per launch / average launch time, HIP events"},
     }
+
+
+def vendor_section(torch, args):
+    """Reference points for the dominant kernel on the step shapes (random int8 operands, warm
+    part, best of 6 interleaved rounds): hipBLASLt's int8 GEMM through torch._int_mm (int32
+    output, W as a column-major operand) and this library's exact GEMM with the bf16 v2.1
+    epilogue on forced tiles (1: 256x256, 3: 256x128, 16: four-wave 256x256, 18: 256x128 with
+    128-byte K stages)."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import ops
+    from lockstep_amd import workloads as WL
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    M = 2048
+    res = {}
+    for name, (N, K) in (("gate_up", WL.LLAMA8B["gate_up"]), ("down", WL.LLAMA8B["down"])):
+        a = torch.randint(-127, 128, (M, K), generator=g, device=dev, dtype=torch.int8)
+        w = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        asc = torch.empty(M, device=dev).uniform_(1e-3, 1e-2, generator=g)
+        ws = torch.empty(N, device=dev).uniform_(1e-3, 1e-2, generator=g)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        wt = w.t()
+        cases = {"hipblaslt_int_mm_i32": (-1, lambda: torch._int_mm(a, wt))}
+        for tile in (-1, 1, 3, 16, 18):
+            cases["lockstep_bf16_tile%d" % tile] = (
+                tile, lambda: ops.gemm(a, w, L.EPI_V21, L.LSK_BF16, asc=asc, ws=ws, out=out))
+        for _ in range(100):
+            cases["lockstep_bf16_tile-1"][1]()
+        best = {}
+        for _ in range(6):
+            for key, (tile, fn) in cases.items():
+                L.call("lsk_gemm_select", tile)
+                best[key] = min(best.get(key, 1e9), _events_time(torch, fn, 10))
+        L.call("lsk_gemm_select", -1)
+        res[name] = {k: {"ms": round(v, 4), "TOPS": round(2 * M * N * K / (v * 1e-3) / 1e12, 1)} for k, v in best.items()}
+        log("bench: vendor %s: %s" % (name, ", ".join("%s %.4f ms" % (k, v) for k, v in best.items())))
+    return res
 
 
 EAGER = False  # --eager: time the decode and MoE calls as plain launches (no HIP graph)
@@ -351,7 +390,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the part's clocks take about 30 ms of sustained load to settle (the step falls from 0.45 to
+    # 0.42 ms over its first 60 calls), so the default warm-up runs 100 untimed steps
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sections", default="dense,decode,moe")
     ap.add_argument("--moe-cases", default="", help="comma list of MoE cases to run, e.g. gpt_oss_20b_mxfp4_T4096 "
@@ -398,6 +439,8 @@ def main():
                                            "WRITE_SIZE, profiles/dense_prefill_llama8b_pmc.md")
     if "copy" in sections:
         out["copy"] = copy_section(torch, args)
+    if "vendor" in sections:
+        out["vendor"] = vendor_section(torch, args)
     if "decode" in sections:
         log("bench: decode rows M in {1, 8, 32}")
         out["decode"] = decode_section(torch, args)

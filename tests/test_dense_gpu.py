@@ -245,7 +245,7 @@ def test_config2_prefill_rows_and_chunk_invariance(which):
     assert torch.equal(chunks.view(torch.int16), y.view(torch.int16))
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 16, 17])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 16, 17, 18])
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 257, 640), (512, 520, 2880), (64, 64, 16),
                                    (1, 1000, 14336), (3, 77, 2880), (4, 300, 1040), (8, 1000, 4096),
                                    (17, 77, 2880), (32, 520, 14336), (5, 33, 48)])
@@ -269,7 +269,7 @@ def test_every_tile_config_is_exact(tile, M, N, K):
     assert np.array_equal(bits(acc), C.int_mm(C.rowquant(x)[0], W8.T))
 
 
-@pytest.mark.parametrize("tile", [1, 3, 4, 12, 13, 16, 17])
+@pytest.mark.parametrize("tile", [1, 3, 4, 12, 13, 16, 17, 18])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_epilogue_special_scales(tile, out):
     """Scales that can make outputs infinite or NaN, placed so that some tiles hold none of them
