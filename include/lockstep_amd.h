@@ -210,7 +210,8 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * 8..11: the whole-row GEMV with 1 / 2 / 4 / 8 rows per wave; 12, 13: tiles 3, 4 with a
  * three-stage LDS ring, two blocks per CU; 14 / 15: for 4 < M <= 32 the GEMV reading 64-byte row
  * pieces straight into registers / whole rows through LDS; 16 / 17: four-wave 256x256 / 256x128,
- * one wave per SIMD with 128x128 / 128x64 wave tiles) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
+ * one wave per SIMD with 128x128 / 128x64 wave tiles; 18: ping-pong 256x128 with 128-byte K stages
+ * in a three-stage ring, the shape's default) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
  * Process-wide, not thread-safe against concurrent launches. */
 int lsk_gemm_select(int tile_id);
 
