@@ -58,12 +58,14 @@ LSK_DEV float act_table_entry(int act, uint32_t bits, const int32_t* frac) {
   return act == LSK_ACT_SILU ? silu_contract(g, frac) : glu_oai(g, frac);
 }
 
+// act(g, u) from the table entry t = tab[g] of the gate value.
+LSK_DEV float act_from_entry(int act, float t, float u) {
+  return act == LSK_ACT_SILU ? bfr(f32_mul(t, u)) : swigluoai_up(u, t);
+}
+
 // act(g, u) for bf16-valued g: from the table when one is given, else step by step.
 LSK_DEV float act_eval(int act, float g, float u, const int32_t* frac, const float* tab) {
-  if (tab) {
-    const float t = tab[__float_as_uint(g) >> 16];
-    return act == LSK_ACT_SILU ? bfr(f32_mul(t, u)) : swigluoai_up(u, t);
-  }
+  if (tab) return act_from_entry(act, tab[__float_as_uint(g) >> 16], u);
   return act == LSK_ACT_SILU ? act_silu(g, u, frac) : act_swigluoai(g, u, frac);
 }
 

@@ -578,36 +578,54 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
   auto strip = [&](int i) {
     if (MODE == 0) {
       // a wave strip is 32 rows x P [gate 32 | up 32] pairs; 8 lanes cover a pair's 32 columns
-      // by quads, LPR lanes a row
-      constexpr int P = C::WTN / 64, LPR = 8 * P, RPP = 64 / LPR;
+      // by quads, LPR lanes a row.  First every pass's gate / up values (and, with the table, all
+      // their table entries, gathered together so that one latency covers the strip), then the
+      // activations, the stores and the row maxima.
+      constexpr int P = C::WTN / 64, LPR = 8 * P, RPP = 64 / LPR, NP = 32 / RPP;
       const int pr = (lane >> 3) % P;
       const int c4 = (lane & 7) * 4;
       const int hc0 = nt * 128 + wn * (32 * P) + pr * 32 + c4;
+      float gv[NP][4], uv[NP][4];
 #pragma unroll
-      for (int t = 0; t < 32 / RPP; ++t) {
+      for (int t = 0; t < NP; ++t) {
+        const int row = lane / LPR + RPP * t;
+        const int ml = wm * C::WTM + i * 32 + row;
+        const v4i vg = *(const v4i*)(region + row * C::kLdc + pr * 64 + c4);
+        const v4i vu = *(const v4i*)(region + row * C::kLdc + pr * 64 + 32 + c4);
+        const float asc = sc_asc[ml];  // 0 past the tile's rows
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cg = wn * C::WTN + pr * 64 + c4 + q, cu = cg + 32;
+          float yg = bfr(f32_mul(f32_mul((float)vg[q], sc_ws[cg]), asc));
+          float yu = bfr(f32_mul(f32_mul((float)vu[q], sc_ws[cu]), asc));
+          if (bias) {
+            yg = bfr(f32_add(yg, sc_b[cg]));
+            yu = bfr(f32_add(yu, sc_b[cu]));
+          }
+          gv[t][q] = yg;
+          uv[t][q] = yu;
+        }
+      }
+      if (a.act_tab) {
+#pragma unroll
+        for (int t = 0; t < NP; ++t)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) gv[t][q] = a.act_tab[__float_as_uint(gv[t][q]) >> 16];
+      }
+#pragma unroll
+      for (int t = 0; t < NP; ++t) {
         const int row = lane / LPR + RPP * t;
         const int ml = wm * C::WTM + i * 32 + row;
         const int p = p0 + ml;
-        const v4i vg = *(const v4i*)(region + row * C::kLdc + pr * 64 + c4);
-        const v4i vu = *(const v4i*)(region + row * C::kLdc + pr * 64 + 32 + c4);
         float am = 0.0f;
         if (p < p1) {
-          const float asc = sc_asc[ml];
           uint16_t hb[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int hc = hc0 + q;
             hb[q] = 0;
-            if (hc < a.N) {
-              const int cg = wn * C::WTN + pr * 64 + c4 + q, cu = cg + 32;
-              float yg = bfr(f32_mul(f32_mul((float)vg[q], sc_ws[cg]), asc));
-              float yu = bfr(f32_mul(f32_mul((float)vu[q], sc_ws[cu]), asc));
-              if (bias) {
-                yg = bfr(f32_add(yg, sc_b[cg]));
-                yu = bfr(f32_add(yu, sc_b[cu]));
-              }
-              const float hv =
-                  lsk::act_eval(a.act, yg, yu, a.frac, a.act_tab);
+            if (hc0 + q < a.N) {
+              const float hv = a.act_tab ? lsk::act_from_entry(a.act, gv[t][q], uv[t][q])
+                                         : lsk::act_eval(a.act, gv[t][q], uv[t][q], a.frac, nullptr);
               hb[q] = f32_to_bf16(hv);
               am = fmaxf(am, fabsf(hv));
             }
