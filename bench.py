@@ -92,12 +92,33 @@ def dense_section(torch, args):
     achieved = sum(gemm_ops) / (sum(gemm_ms) * 1e-3) / 1e12
     per_shape = {name: {"ms": round(t, 4), "TOPS": round(o / (t * 1e-3) / 1e12, 1)}
                  for (name, *_), t, o in zip(data, gemm_ms, gemm_ops)}
+
+    # the Qwen2.5-7B block GEMMs at 8192 rows, the shapes whose H100 times the reference publishes
+    # (int8 GEMM with the fused v2.1 epilogue on pre-quantised rows)
+    ref_shapes = {}
+    Mq = 8192
+    aq = torch.randint(-127, 128, (Mq, 18944), generator=g, device=dev, dtype=torch.int8)
+    ascq = torch.empty(Mq, device=dev).uniform_(1e-3, 1e-2, generator=g)
+    for name, N, K in (("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)):
+        a = aq[:, :K]
+        W8 = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        ws = torch.empty(N, device=dev).uniform_(1e-3, 1e-2, generator=g)
+        out = torch.empty((Mq, N), dtype=torch.bfloat16, device=dev)
+        fn = lambda: ops.gemm(a, W8, L.EPI_V21, L.LSK_BF16, asc=ascq, ws=ws, out=out)  # noqa: E731
+        for _ in range(3):
+            fn()
+        t = _events_time(torch, fn, 10)
+        ref_shapes["qwen2.5_7b_%s_M8192" % name] = {"us": round(t * 1e3, 1), "TOPS": round(2 * Mq * N * K / (t * 1e-3) / 1e12, 1)}
+        del W8, out
+    torch.cuda.empty_cache()
     return {
         "ms_per_step": ms, "value": tops, "wall_s": wall, "ops_step": ops_step,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
                      "kernel": "gemm_i8_pp_kernel", "per_shape": per_shape,
                      "note": "int8 ops (2 per MAC) per launch / average launch time, HIP events"},
+        "qwen2_5_7b_m8192": dict(ref_shapes, note="int8 GEMM + fused v2.1 epilogue (bf16 out) on pre-quantised "
+                                                   "rows, HIP events; the shapes the reference times on H100"),
     }
 
 
@@ -430,6 +451,7 @@ def main():
                    "M": 2048, "gate_up": [28672, 4096], "down": [4096, 14336], "x": "f32 N(0,1), 0.1% +-20",
                    "out": "bf16", "parallelism": "single GPU"},
         "roofline": d["roofline"],
+        "qwen2_5_7b_m8192": d["qwen2_5_7b_m8192"],
     }
     tr = measured_traffic()
     if tr and "gate_up" in tr and "down" in tr:
