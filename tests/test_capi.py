@@ -67,3 +67,31 @@ def test_outlier_entry_points_refuse_bad_arguments_without_touching_the_gpu():
     assert lib.lsk_w8a8_outlier_linear(None, 1, 256, 0, 256, None, 3, None, 1, None, 256, 8, None, None, 1, None, 1, 8,
                                        None, 0, None) == 0
     assert lib.lsk_w8a8_outlier_linear_workspace(4, 256, 3) >= 4 * 256 * 5 + 4 * 3 * 4 + 16
+
+
+def test_block_scaled_and_router_entry_points_without_touching_the_gpu():
+    """lsk_blockquant / lsk_gemm_mx2 / lsk_router_topk / lsk_act_table: zero rows are a no-op that
+    needs no pointer; bad sizes, formats and activation codes are refused before any HIP call."""
+    lib = L.load()
+    # lsk_blockquant(x, x_dtype, ldx, M, K, q, ldq, ka, ldka, stream)
+    assert lib.lsk_blockquant(None, L.LSK_BF16, 64, 0, 64, None, 64, None, 2, None) == 0
+    assert lib.lsk_blockquant(None, L.LSK_F32, 48, 3, 48, None, 48, None, 1, None) == 1
+    assert b"multiple of the 32-element block" in lib.lsk_last_error()
+    assert lib.lsk_blockquant(None, L.LSK_F32, 64, -1, 64, None, 64, None, 2, None) == 1
+    assert b"negative" in lib.lsk_last_error()
+    # lsk_gemm_mx2(q, ldq, ka, ldka, b, b_fmt, ldb, kexp, lds, M, N, K, epilogue, bias, out, ldo, stream)
+    assert lib.lsk_gemm_mx2(None, 64, None, 2, None, 1, 32, None, 2, 0, 16, 64, 0, None, None, 16, None) == 0
+    assert lib.lsk_gemm_mx2(None, 64, None, 2, None, 1, 32, None, 2, 5, 0, 64, 0, None, None, 16, None) == 0
+    assert lib.lsk_gemm_mx2(None, 64, None, 2, None, 2, 32, None, 2, 1, 16, 64, 0, None, None, 16, None) == 1
+    assert b"b_fmt" in lib.lsk_last_error()
+    assert lib.lsk_gemm_mx2(None, 64, None, 2, None, 1, 32, None, 2, 1, 16, 64, 3, None, None, 16, None) == 1
+    assert b"epilogue" in lib.lsk_last_error()
+    # lsk_router_topk(g, g_dtype, ldg, T, E, k, renormalize, tab, idx, w, stream)
+    assert lib.lsk_router_topk(None, L.LSK_F32, 8, 0, 8, 2, 1, None, None, None, None) == 0
+    assert lib.lsk_router_topk(None, L.LSK_F32, 8, 4, 8, 9, 1, None, None, None, None) == 1
+    assert b"k=9" in lib.lsk_last_error()
+    # lsk_act_table(frac, act, table, stream): an unknown activation code, then null tables
+    assert lib.lsk_act_table(None, 7, None, None) == 1
+    assert b"unknown act 7" in lib.lsk_last_error()
+    assert lib.lsk_act_table(None, L.LSK_ACT_SILU, None, None) == 1
+    assert b"null pointer" in lib.lsk_last_error()

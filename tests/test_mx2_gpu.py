@@ -235,3 +235,37 @@ def test_moe_mx2_gpt_oss_t4096_token_subset():
     rows = np.sort(np.random.default_rng(3).choice(4096, 24, replace=False))
     ref = C.moe_forward_mx2(x[rows], oexp, idx[rows], w[rows], oact)
     assert np.array_equal(got[rows], ref)
+
+
+def test_zero_tokens_through_the_layers():
+    """T = 0: the router, block quant, the block-scaled GEMM and the int8 / MXFP4 / MX2 layers return
+    empty results of the right shape and dtype (the reference's functions do the same on an
+    empty batch)."""
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    from moe_util import device_experts
+    say("zero tokens")
+    E, k, H, I = 8, 2, 256, 128
+    g0 = torch.empty((0, E), dtype=torch.bfloat16, device=dev())
+    idx0, w0, _ = MR.router_from_logits(g0, k, True, _tab())
+    assert idx0.shape == (0, k) and idx0.dtype == torch.int64 and w0.shape == (0, k) and w0.dtype == torch.bfloat16
+    x0 = torch.empty((0, H), dtype=torch.bfloat16, device=dev())
+    q0, ka0 = MR.blockquant(x0)
+    assert q0.shape == (0, H) and ka0.shape == (0, H // 32)
+    m2 = to_dev(np.ones((16, H), np.int8))
+    kexp = to_dev(np.full((16, H // 32), 127, np.uint8))
+    assert MR.int_mm_mx2(q0, ka0, m2, kexp).shape == (0, 16)
+
+    x, experts, logits = WL.moe_inputs(4, E, k, H, I, seed=1)
+    idx, w = routing_from_logits(logits, k)
+    ridx, rw = routing_device(idx[:0], w[:0])
+    y, _, _ = MR.moe_forward_b(x0, None, device_experts(experts), k, True, _tab(), 0, MR.act_silu, rot_blk=0,
+                               routing=(ridx, rw))
+    assert y.shape == (0, H) and y.dtype == torch.bfloat16
+
+    x, experts, logits = WL.moe_mx_inputs(4, E, k, H, I, seed=1, bias=True)
+    dexp = MR.ExpertTablesMX([((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2))
+                              for (p13, s13, p2, s2, b13, b2) in experts], packed=True)
+    for fwd in (MR.moe_forward_mx, MR.moe_forward_mx2):
+        y, _, _ = fwd(x0, None, dexp, k, True, _tab(), 0, MR.act_swigluoai, routing=(ridx, rw))
+        assert y.shape == (0, H) and y.dtype == torch.bfloat16
