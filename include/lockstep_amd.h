@@ -402,7 +402,9 @@ int lsk_moe_forward(const lsk_moe_args* args, void* stream);
  * rows per expert at a time; taken only for int8 experts without rotation, T <= 64 and
  * H, I <= 4096, the tiles otherwise), on the 128x256 tile with the four-wave main loop (3: one wave
  * per SIMD per block, 64x128 wave tiles), or chosen by size (-1, the default: the GEMV where it
- * applies, ping-pong once the routed rows reach E x 128).  Results are identical for every
+ * applies, ping-pong once the routed rows reach E x 128).  MXFP4 experts (H, I <= 8192, no
+ * rotation) take the MX GEMV under 2 for T <= 64 and by default for T <= 24 (T <= 16 with
+ * block-scaled activations), the MX grouped tiles otherwise.  Results are identical for every
  * choice.  Process-wide. */
 int lsk_moe_select(int variant);
 

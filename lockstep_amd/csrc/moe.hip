@@ -1036,6 +1036,8 @@ struct MoeWs {
 inline int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
 
 constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
+constexpr int64_t kMxGemvMaxT = 24;   // ... with MXFP4 experts
+constexpr int64_t kMx2GemvMaxT = 16;  // ... with MXFP4 experts and block-scaled activations
 
 MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt) {
   const int64_t qb = wfmt >= 1 ? 2 : 1;  // bytes per quantised activation element
@@ -1235,7 +1237,13 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   // the grouped GEMV for decode token counts (whole weight rows streamed once per tile)
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
   const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096;
-  const bool use_mx_gemv = gemv_ok && mx == 1 && H <= 8192 && I <= 8192;
+  // (MX experts: the GEMV re-streams each expert's weights per 4-row pass, so past about 24 tokens
+  // the tiled kernels win: GPT-OSS-20B on MI355X, T = 24 242 vs 276 us, T = 48 368 vs 278 us)
+  const bool use_mx_gemv = gemv_ok && mx == 1 && (g_moe_force == 2 || T <= kMxGemvMaxT) && H <= 8192 && I <= 8192;
+  // block-scaled activations at decode sizes: the same GEMV over integer-valued rows (every row
+  // quantised in the general form) with the block exponents (T = 1 50 vs 116 us, T = 16 221 vs
+  // 278 us, T = 24 281 vs 277 us)
+  const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
 
   int rc;
   if (rb > 0) {
@@ -1287,7 +1295,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
   }
   if (mx == 2 &&
-      (rc = lsk::launch_blockquant_mx2(a->x, H, T, nullptr, (int)H, (uint16_t*)w.qx, w.kax, w.flagx, anyf, lo13, hi13, s)))
+      (rc = lsk::launch_blockquant_mx2(a->x, H, T, nullptr, (int)H, (uint16_t*)w.qx, w.kax, w.flagx, anyf,
+                                       use_mx2_gemv ? 1 : lo13, use_mx2_gemv ? 0 : hi13, s)))
     return rc;
   MoeGemmArgs g1{};
   g1.A = w.qx;
@@ -1317,8 +1326,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     g1.a_ka = w.kax;
     g1.ldka = H / 32;
   }
-  if (use_mx_gemv) {
-    if ((rc = lsk::launch_moe_mx_gemv(0, g1, w.max_tiles, T, a->mx_safe, w.gu, s))) return rc;
+  if (use_mx_gemv || use_mx2_gemv) {
+    if ((rc = lsk::launch_moe_mx_gemv(0, g1, w.max_tiles, T, a->mx_safe, use_mx2_gemv ? nullptr : w.gu, s))) return rc;
   } else if (mx == 2) {
     g1.mx2 = 1;
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
@@ -1351,8 +1360,8 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
                        rb, a->rot_scale, w.qh, w.asch);
     if ((rc = lsk::check_launch("moe_rot_requant_kernel"))) return rc;
   } else if (mx == 2) {
-    if ((rc = lsk::launch_blockquant_mx2(w.h, I, R, w.offs + E, (int)I, (uint16_t*)w.qh, w.kah, w.flagh, anyf + 1, lo2,
-                                         hi2, s)))
+    if ((rc = lsk::launch_blockquant_mx2(w.h, I, R, w.offs + E, (int)I, (uint16_t*)w.qh, w.kah, w.flagh, anyf + 1,
+                                         use_mx2_gemv ? 1 : lo2, use_mx2_gemv ? 0 : hi2, s)))
       return rc;
   } else if (mx) {
     if ((rc = lsk::launch_requant_bf16(w.h, w.h_amax, w.offs + E, R, (int)I, (uint16_t*)w.qh, w.asch, s))) return rc;
@@ -1388,7 +1397,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     g2.a_ka = w.kah;
     g2.ldka = I / 32;
   }
-  if (use_mx_gemv) {
+  if (use_mx_gemv || use_mx2_gemv) {
     if ((rc = lsk::launch_moe_mx_gemv(1, g2, w.max_tiles, T, a->mx_safe, nullptr, s))) return rc;
   } else if (mx == 2) {
     g2.mx2 = 1;

@@ -575,16 +575,19 @@ int launch_dense(const int8_t* a, int64_t lda, const int32_t* ka, int64_t ldka, 
 // blocks in ascending order from +0 (one FMA, exact product; SAFE: multiply, then add).  MODE
 // 0: gate row c and up row N + c, bias-added bfr values into gu for the activation-and-requant
 // kernel; MODE 1: bfr(w * y) into the token's slot row.
+// MX2 (block-scaled activations, integer-valued rows with block exponents ka): the update is
+// acc = fl32(acc + fl32(s_b * fl32(2^ka_b * 2^(k_b - 128)))) with no row scale, and MODE 0 writes
+// the activation h = act(gate, up) straight into h (the owner lane holds both values).
 typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
 
-template <int MODE, int MR, int NCH, int RPW, bool SAFE>
+template <int MODE, int MR, int NCH, int RPW, bool SAFE, bool MX2>
 __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu) {
   constexpr int kRows = MODE == 0 ? 2 : 1;
   constexpr int V = MR * RPW * kRows;  // chains per row chunk, q = (m * RPW + i) * kRows + r
   static_assert(V <= 64, "one lane per chain");
   constexpr int kB = 64 * NCH;          // blocks a wave covers
   constexpr int kSbStride = kB + 4;     // floats per chain row in LDS (16-byte aligned, skewed banks)
-  constexpr int kWaveBytes = V * kSbStride * 4 + RPW * kRows * kB * 4;
+  constexpr int kWaveBytes = V * kSbStride * 4 + RPW * kRows * kB * 4 + (MX2 ? MR * kB * 4 : 0);
   extern __shared__ __attribute__((aligned(16))) char gemv_smem[];
   const int cols_blk = 4 * RPW;
   const int nchunk = (a.N + cols_blk - 1) / cols_blk;
@@ -599,6 +602,7 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
   const int nw = MODE == 0 ? 2 * a.N : a.N;  // weight rows of the expert
   float* sb = (float*)(gemv_smem + wave * kWaveBytes);
   float* scl = sb + V * kSbStride;  // 2^(k - 128) per (weight row, block)
+  float* sa = scl + RPW * kRows * kB;  // MX2: 2^ka per (activation row of the chunk, block)
   const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)a.w_ptrs[e], (int64_t)nw * a.ldw);
   const __amdgpu_buffer_rsrc_t rsc = lsk::make_rsrc((const void*)a.ws_ptrs[e], (int64_t)nw * a.lds);
   const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
@@ -647,6 +651,8 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
         const uint32_t off = in ? (uint32_t)((src * a.lda + b * 32) * 2) : lsk::kOob;
 #pragma unroll
         for (int h = 0; h < 4; ++h) act[m][j][h] = lsk::buf_load16(ra, in ? off + 16 * h : lsk::kOob);
+        // (this wave alone writes and reads its LDS area, in program order)
+        if constexpr (MX2) sa[m * kB + b] = in ? pow2f(a.a_ka[(int64_t)src * a.ldka + b]) : 0.0f;
       }
     }
     (void)A;
@@ -655,7 +661,7 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
     float asc = 0.0f, wt = 0.0f;
     int dst = 0;
     if (rowok) {
-      asc = a.a_scale[MODE == 0 ? a.row_tok[p] : p];
+      asc = a.a_scale ? a.a_scale[MODE == 0 ? a.row_tok[p] : p] : 1.0f;
       if (MODE == 1) {
         wt = a.row_w[p];
         dst = a.row_dst[p];
@@ -713,16 +719,32 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
         acc = SAFE ? f32_add(acc, f32_mul(sv, sc)) : __builtin_fmaf(sv, sc, acc);
       };
       int b = 0;
+      if constexpr (MX2) {
+        const float* arow = sa + q_m * kB;
+        auto upd2 = [&](float sv, float av, float sc) { acc = f32_add(acc, f32_mul(sv, f32_mul(av, sc))); };
 #pragma unroll 2
-      for (; b + 4 <= nb; b += 4) {
-        const v4f s4 = *(const v4f*)(srow + b);
-        const v4f c4 = *(const v4f*)(crow + b);
-        upd(s4[0], c4[0]);
-        upd(s4[1], c4[1]);
-        upd(s4[2], c4[2]);
-        upd(s4[3], c4[3]);
+        for (; b + 4 <= nb; b += 4) {
+          const v4f s4 = *(const v4f*)(srow + b);
+          const v4f a4 = *(const v4f*)(arow + b);
+          const v4f c4 = *(const v4f*)(crow + b);
+          upd2(s4[0], a4[0], c4[0]);
+          upd2(s4[1], a4[1], c4[1]);
+          upd2(s4[2], a4[2], c4[2]);
+          upd2(s4[3], a4[3], c4[3]);
+        }
+        for (; b < nb; ++b) upd2(srow[b], arow[b], crow[b]);
+      } else {
+#pragma unroll 2
+        for (; b + 4 <= nb; b += 4) {
+          const v4f s4 = *(const v4f*)(srow + b);
+          const v4f c4 = *(const v4f*)(crow + b);
+          upd(s4[0], c4[0]);
+          upd(s4[1], c4[1]);
+          upd(s4[2], c4[2]);
+          upd(s4[3], c4[3]);
+        }
+        for (; b < nb; ++b) upd(srow[b], crow[b]);
       }
-      for (; b < nb; ++b) upd(srow[b], crow[b]);
     }
     const float accu = MODE == 0 ? __shfl_down(acc, 1, 64) : 0.0f;  // the up chain sits in lane q + 1
     if (rowok) {
@@ -733,9 +755,13 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
           yg = bfr(f32_add(yg, b0));
           yu = bfr(f32_add(yu, b1));
         }
-        uint16_t* row = gu + (int64_t)p * 2 * a.N;
-        row[c] = f32_to_bf16(yg);
-        row[a.N + c] = f32_to_bf16(yu);
+        if constexpr (MX2) {
+          a.h[(int64_t)p * a.N + c] = f32_to_bf16(lsk::act_eval(a.act, yg, yu, a.frac, a.act_tab));
+        } else {
+          uint16_t* row = gu + (int64_t)p * 2 * a.N;
+          row[c] = f32_to_bf16(yg);
+          row[a.N + c] = f32_to_bf16(yu);
+        }
       } else {
         float yv = bfr(f32_mul(acc, asc));
         if (bias) yv = bfr(f32_add(yv, b0));
@@ -745,14 +771,14 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
   }
 }
 
-template <int MODE, int MR, int NCH, bool SAFE>
+template <int MODE, int MR, int NCH, bool SAFE, bool MX2>
 int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
   constexpr int RPW = MODE == 0 ? 2 : 4;
   constexpr int kRows = MODE == 0 ? 2 : 1;
   constexpr int V = MR * RPW * kRows;
-  constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH * 4);
+  constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH * 4 + (MX2 ? MR * 64 * NCH * 4 : 0));
   static bool attr = false;
-  auto kern = moe_mx_gemv_kernel<MODE, MR, NCH, RPW, SAFE>;
+  auto kern = moe_mx_gemv_kernel<MODE, MR, NCH, RPW, SAFE, MX2>;
   if (!attr) {
     if (int rc = reserve_lds(kern, smem, name)) return rc;
     attr = true;
@@ -767,20 +793,20 @@ int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu
 
 // MR: activation rows per pass (their bf16 blocks live in registers: 16 words per row and block
 // sweep), fewer when K needs more sweeps.
-template <int MODE, int MR, bool SAFE>
+template <int MODE, int MR, bool SAFE, bool MX2>
 int launch_mx_gemv_mr(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
   const int nch = (ga.K / 32 + 63) / 64;
-  if (nch <= 1) return launch_mx_gemv_k<MODE, MR, 1, SAFE>(ga, max_tiles, gu, s, name);
-  if (nch <= 2) return launch_mx_gemv_k<MODE, (MR > 2 ? 2 : MR), 2, SAFE>(ga, max_tiles, gu, s, name);
-  return launch_mx_gemv_k<MODE, 1, 4, SAFE>(ga, max_tiles, gu, s, name);
+  if (nch <= 1) return launch_mx_gemv_k<MODE, MR, 1, SAFE, MX2>(ga, max_tiles, gu, s, name);
+  if (nch <= 2) return launch_mx_gemv_k<MODE, (MR > 2 ? 2 : MR), 2, SAFE, MX2>(ga, max_tiles, gu, s, name);
+  return launch_mx_gemv_k<MODE, 1, 4, SAFE, MX2>(ga, max_tiles, gu, s, name);
 }
 
-template <int MODE, bool SAFE>
+template <int MODE, bool SAFE, bool MX2 = false>
 int launch_mx_gemv(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint16_t* gu, hipStream_t s,
                    const char* name) {
-  if (T <= 1) return launch_mx_gemv_mr<MODE, 1, SAFE>(ga, max_tiles, gu, s, name);
-  if (T <= 2) return launch_mx_gemv_mr<MODE, 2, SAFE>(ga, max_tiles, gu, s, name);
-  return launch_mx_gemv_mr<MODE, 4, SAFE>(ga, max_tiles, gu, s, name);
+  if (T <= 1) return launch_mx_gemv_mr<MODE, 1, SAFE, MX2>(ga, max_tiles, gu, s, name);
+  if (T <= 2) return launch_mx_gemv_mr<MODE, 2, SAFE, MX2>(ga, max_tiles, gu, s, name);
+  return launch_mx_gemv_mr<MODE, 4, SAFE, MX2>(ga, max_tiles, gu, s, name);
 }
 
 }  // namespace
@@ -794,6 +820,11 @@ int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int s
 
 int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,
                        hipStream_t s) {
+  if (ga.a_ka) {  // block-scaled activations: one update form, whatever safe says
+    LSK_REQUIRE(!ga.a_scale && ga.ldka >= ga.K / 32 && (mode == 1 || ga.h), "moe_mx_gemv: MX2 arguments");
+    return mode == 0 ? launch_mx_gemv<0, false, true>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<gate_up, mx2>")
+                     : launch_mx_gemv<1, false, true>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<down, mx2>");
+  }
   if (mode == 0)
     return safe ? launch_mx_gemv<0, true>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<gate_up>")
                 : launch_mx_gemv<0, false>(ga, max_tiles, T, gu, s, "moe_mx_gemv_kernel<gate_up>");

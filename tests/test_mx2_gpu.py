@@ -138,11 +138,12 @@ def test_expert_block_mx2_composed():
 
 
 def _mx2_layer(T, E, k, H, I, seed, tiny_rows=0.0, low_exp=False, big_exp=False, bias=True, act="swigluoai",
-               mxv=0):
+               mxv=0, moe_force=-1):
     """The layer on device vs the oracle.  tiny_rows: fraction of tokens scaled by 2^-40 (block
     exponents far below the fused window when low_exp puts E8M0 bytes <= 10 into one expert's
     w13 and w2); big_exp: bytes >= 240 in one expert's w2 (the multiply-then-add update and a
-    narrower window at the top)."""
+    narrower window at the top).  moe_force: lsk_moe_select's variant (0 keeps decode-sized
+    layers on the tiled kernels instead of the GEMV)."""
     from lockstep_amd import _lib as L
     from lockstep_amd import moe_ref as MR
     from lockstep_amd import workloads as WL
@@ -176,10 +177,12 @@ def _mx2_layer(T, E, k, H, I, seed, tiny_rows=0.0, low_exp=False, big_exp=False,
     oact = C.act_silu if act == "silu" else C.act_swigluoai
     dact = MR.act_silu if act == "silu" else MR.act_swigluoai
     L.call("lsk_moe_mx_select", mxv)
+    L.call("lsk_moe_select", moe_force)
     try:
         y, _, _ = MR.moe_forward_mx2(bf16_dev(x), None, dexp, k, True, _tab(), 0, dact, routing=(ridx, rw))
     finally:
         L.call("lsk_moe_mx_select", 0)
+        L.call("lsk_moe_select", -1)
     return x, oexp, idx, w, oact, u16(y), dexp
 
 
@@ -193,7 +196,7 @@ def _flagged_tokens(x, dexp):
 
 
 def test_moe_mx2_small_fused_only():
-    x, oexp, idx, w, oact, got, dexp = _mx2_layer(24, 8, 2, 256, 128, seed=1, act="silu", bias=False)
+    x, oexp, idx, w, oact, got, dexp = _mx2_layer(24, 8, 2, 256, 128, seed=1, act="silu", bias=False, moe_force=0)
     assert not _flagged_tokens(x, dexp).any()
     assert np.array_equal(got, C.moe_forward_mx2(x, oexp, idx, w, oact))
 
@@ -221,11 +224,27 @@ def test_moe_mx2_every_row_general():
 
 
 @pytest.mark.parametrize("T", [1, 32])
-def test_moe_mx2_gpt_oss_shapes(T):
+@pytest.mark.parametrize("path", ["gemv", "tiled"])
+def test_moe_mx2_gpt_oss_shapes(T, path):
+    """Decode sizes through the grouped GEMV (the default) and through the tiled kernels."""
     from lockstep_amd import workloads as WL
     c = WL.GPT_OSS_20B
-    x, oexp, idx, w, oact, got, dexp = _mx2_layer(T, c["E"], c["k"], c["H"], c["I"], seed=80 + T, bias=True)
+    x, oexp, idx, w, oact, got, dexp = _mx2_layer(T, c["E"], c["k"], c["H"], c["I"], seed=80 + T, bias=True,
+                                                  moe_force=-1 if path == "gemv" else 0)
     assert np.array_equal(got, C.moe_forward_mx2(x, oexp, idx, w, oact))
+
+
+@pytest.mark.parametrize("act", ["silu", "swigluoai"])
+def test_moe_mx2_gemv_extreme_exponents(act):
+    """The decode GEMV (T <= 64) on tiny rows (block exponents near -126), E8M0 bytes <= 10 and
+    >= 240 (products 2^(ka + k - 128) underflowing to subnormals and zero, and large ones), a
+    partial column chunk and K of 11 / 7 blocks."""
+    x, oexp, idx, w, oact, got, dexp = _mx2_layer(48, 4, 2, 352, 224, seed=91, tiny_rows=0.15, low_exp=True,
+                                                  big_exp=True, act=act)
+    assert _flagged_tokens(x, dexp).any()
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx2(x, oexp, idx, w, oact)
+    assert np.array_equal(got, ref)
 
 
 def test_moe_mx2_gpt_oss_t4096_token_subset():
