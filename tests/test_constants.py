@@ -112,3 +112,29 @@ def test_loaded_constants_feed_the_device_linears(tmp_path):
     logits = ops.planes_linear(xd.float(), w2, 15, hwsd, 15)
     ref = C.mm_planes(x, wp, hws, 15)
     assert np.array_equal(logits.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+def test_every_problem_is_reported(tmp_path):
+    """A file with several faults is refused once, with one record per fault (digest faults are
+    reported only after the structural checks pass)."""
+    t = _consts()
+    m = _manifest(t)
+    bad = dict(t)
+    bad["lm_head.ws"] = bad["lm_head.ws"][:31]          # shape
+    del bad["model.norm.G"]                              # absent
+    bad["stray"] = torch.ones(3)                         # unlisted
+    K.save_constants(str(tmp_path / "constants.safetensors"), bad)
+    with pytest.raises(K.ConstantsRejected) as ei:
+        K.load_constants(str(tmp_path), m, "cpu")
+    kinds = sorted((p.kind, p.tensor) for p in ei.value.problems)
+    assert kinds == [("absent", "model.norm.G"), ("shape", "lm_head.ws"), ("unlisted", "stray")]
+    bad = dict(t)
+    for n in ("lm_head.plane0", "model.layers.0.mlp.down_proj.ws"):
+        w = bad[n].clone()
+        w.view(torch.uint8).view(-1)[5] ^= 1
+        bad[n] = w
+    K.save_constants(str(tmp_path / "constants.safetensors"), bad)
+    with pytest.raises(K.ConstantsRejected) as ei:
+        K.load_constants(str(tmp_path), m, "cpu")
+    assert sorted(p.tensor for p in ei.value.problems if p.kind == "digest") == \
+        ["lm_head.plane0", "model.layers.0.mlp.down_proj.ws"]
