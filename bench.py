@@ -1,17 +1,20 @@
 #!/usr/bin/env python3
 """Benchmark of the contract matrix-multiply path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--sections dense,decode,moe[,vendor]]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                    [--sections block,dense,decode,moe[,vendor,copy]] [--block-rows T]
                     [--moe-cases NAME,...] [--eager] [--mx-variant V] [--moe-variant V]
 
-A step is one pass of the Llama-3.1-8B-shaped MLP contract GEMMs at M=2048 prefill rows:
-w8a8_matmul (row quant + exact int8 GEMM + v2.1 epilogue, bf16 out) of the gate+up projection
-(N=28672, K=4096) and of the down projection (N=4096, K=14336), synthetic inputs resident in HBM.
-`value` is int8 TOPS (2 ops per multiply-accumulate) of the whole step.  One JSON line is printed.
+A step (the headline `value`) is one Qwen2.5-7B-shaped decoder block's four GEMMs through
+ref_block_v1 at T=8192 prefill rows: per GEMM site quant8_dyn of the binary32 activation, the exact
+int8 GEMM and the pow2 dequant (binary32 out); qkv 4608x3584, o 3584x3584, gate+up 37888x3584,
+down 3584x18944; synthetic inputs resident in HBM.  `value` is int8 TOPS (2 ops per
+multiply-accumulate) of the whole step.  Extra keys: the Llama-3.1-8B MLP step (w8a8_matmul v2.1 at
+M=2048), decode rows, the MoE layers and their grouped-GEMM stages.  One JSON line is printed.
 
 The `roofline` object prices the dominant kernel (the int8 MFMA GEMM) from HIP events recorded on
-the stream it is launched on; `cpu_baseline` times the reference's own CPU op sequence
-(oracle/cpu_baseline.py) on a bounded row sample on this host's cores.
+the stream it is launched on; `cpu_baseline` times the reference's own CPU op sequence on a
+bounded row sample on this host's cores.
 """
 from __future__ import annotations
 
@@ -120,6 +123,109 @@ def dense_section(torch, args):
         "qwen2_5_7b_m8192": dict(ref_shapes, note="int8 GEMM + fused v2.1 epilogue (bf16 out) on pre-quantised "
                                                    "rows, HIP events; the shapes the reference times on H100"),
     }
+
+
+QWEN25_7B_BLOCK = (("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944))
+BLOCK_EW = 7   # quant8_dyn of the float weight W8 / 128 gives back (W8, 7)
+
+
+def block_section(torch, args):
+    """The headline step: one Qwen2.5-7B-shaped decoder block's GEMMs through ref_block_v1 at T=8192
+    prefill rows (hidden 3584; qkv 4608 = 28 query + 2 x 4 KV heads of 128; o 3584; gate+up 37888 =
+    2 x 18944; down K = 18944).  Each GEMM site (ref_block_v1.py:166-167, 191-193, 196-198, 216-218)
+    is ref_block_v1.linear_dyn: quant8_dyn of the binary32 activation (two launches) and the exact
+    int8 GEMM with the pow2 dequant fused into its epilogue, binary32 out.  Activations N(0,1) and
+    int8 weights uniform on [-127, 127] (exponent 7), resident in HBM.  HIP events recorded on the
+    launch stream around every launch of the timed steps give the GEMM kernel's and the quantiser's
+    own times."""
+    from lockstep_amd import ref_block_v1 as RB
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    T = args.block_rows
+    sites = []
+    for name, N, K in QWEN25_7B_BLOCK:
+        x = torch.randn((T, K), generator=g, device=dev, dtype=torch.float32)
+        W8 = torch.randint(-127, 128, (N, K), generator=g, device=dev, dtype=torch.int8)
+        sites.append((name, N, K, x, W8))
+    ops_site = [2 * T * N * K for _, N, K, _, _ in sites]
+    ops_step = sum(ops_site)
+    s = torch.cuda.current_stream()
+
+    def step(marks=None):
+        for i, (_, N, K, x, W8) in enumerate(sites):
+            RB.linear_dyn(x, W8.t(), BLOCK_EW)
+            if marks is not None:
+                marks[i + 1].record(s)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    # events on the launch stream at every site boundary of every timed step (recording an event
+    # costs the GPU nothing), so the site split comes from the timed steps themselves
+    marks = [[ev() for _ in range(len(sites) + 1)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        marks[k][0].record(s)
+        step(marks[k])
+    marks[-1][-1].synchronize()
+    wall = time.perf_counter() - t0
+    ms = marks[0][0].elapsed_time(marks[-1][-1]) / args.steps
+    site_ms = [sum(mk[i].elapsed_time(mk[i + 1]) for mk in marks) / args.steps for i in range(len(sites))]
+    # each site's GEMM alone on its quantised operands: the dominant kernel's launch time
+    gemm_ms = []
+    for _, N, K, x, W8 in sites:
+        from lockstep_amd import _lib as L
+        from lockstep_amd import ops
+        q8, _, erow = ops.quant8_dyn(x, erow=True)
+        out = torch.empty((T, N), dtype=torch.float32, device=dev)
+        fn = lambda: ops.gemm(q8, W8, L.EPI_POW2, L.LSK_F32, erow=erow, shift=BLOCK_EW, out=out)  # noqa: E731
+        for _ in range(2):
+            fn()
+        gemm_ms.append(_events_time(torch, fn, max(args.steps, 5)))
+        del q8, erow, out
+    achieved = ops_step / (sum(gemm_ms) * 1e-3) / 1e12
+    per_site = {name: {"site_us": round(t * 1e3, 1), "gemm_us": round(gk * 1e3, 1),
+                       "quant8_dyn_us": round((t - gk) * 1e3, 1), "TOPS": round(o / (t * 1e-3) / 1e12, 1),
+                       "gemm_TOPS": round(o / (gk * 1e-3) / 1e12, 1)}
+                for (name, *_), t, gk, o in zip(sites, site_ms, gemm_ms, ops_site)}
+    del sites
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "value": ops_step / (ms * 1e-3) / 1e12, "wall_s": wall, "ops_step": ops_step,
+            "T": T, "per_site": per_site,
+            "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                         "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                         "kernel": "gemm_i8_pp_kernel (POW2 epilogue, binary32 out)",
+                         "note": "2*T*N*K int8 ops of the four GEMMs / the sum of their average launch times "
+                                 "(HIP events on the launch stream, each GEMM alone on its quantised operands)"}}
+
+
+def cpu_baseline_block(args):
+    """The reference's own CPU op sequence of one block GEMM site, ref_block_v1.py:122-133 and
+    :167 (numpy quant8_dyn, int64 `a @ b`, the pow2 dequant), restated in the oracle, on a row
+    sample of each of the four Qwen2.5-7B GEMMs.  numpy's int64 matmul runs on one core."""
+    import numpy as np
+
+    from oracle import contract as C
+
+    rows = 6
+    g = np.random.Generator(np.random.PCG64(13))
+    total_ops, total_t = 0, 0.0
+    for name, N, K in QWEN25_7B_BLOCK:
+        x = g.standard_normal((rows, K), dtype=np.float32)
+        W = g.integers(-127, 128, (K, N), dtype=np.int64)    # the reference's quantised weights are int64
+        t0 = time.perf_counter()
+        q, e = C.quant8_dyn(x)
+        C.dequant_pow2(C.gemm_int(q, W), e + BLOCK_EW)
+        total_t += time.perf_counter() - t0
+        total_ops += 2 * rows * N * K
+    return {"value": round(total_ops / total_t / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": "%d rows of each of the four Qwen2.5-7B block GEMMs (qkv 4608x3584, o 3584x3584, gate_up "
+                      "37888x3584, down 3584x18944): numpy quant8_dyn, int64 matmul and pow2 dequant as in "
+                      "ref_block_v1.py:122-133,167 (rows are independent, so TOPS extrapolates linearly to T=%d); "
+                      "host os.cpu_count()=%s" % (rows, args.block_rows, os.cpu_count())}
 
 
 def vendor_section(torch, args):
@@ -248,10 +354,13 @@ def copy_section(torch, args):
     return {"bytes_per_launch": n}
 
 
-def measured_traffic():
-    """HBM bytes per launch of the dominant kernel at the two step shapes, from the committed
+TRAFFIC_FILES = {"qwen25_7b_block": "block_qwen25_7b_t8192_pmc.md", "llama8b": "dense_prefill_llama8b_pmc.md"}
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch of the dominant kernel for each GEMM of a workload, from the committed
     rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, scaled by the 1 GiB copy's reading), or None."""
-    path = os.path.join(ROOT, "profiles", "dense_prefill_llama8b_pmc.md")
+    path = os.path.join(ROOT, "profiles", TRAFFIC_FILES[workload])
     try:
         with open(path) as f:
             for line in f:
@@ -411,11 +520,12 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # the part's clocks take about 30 ms of sustained load to settle (the step falls from 0.45 to
-    # 0.42 ms over its first 60 calls), so the default warm-up runs 100 untimed steps
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sections", default="dense,decode,moe")
+    ap.add_argument("--sections", default="block,dense,decode,moe",
+                    help="comma list of block (the headline), dense, decode, moe, vendor, copy; the JSON line's "
+                         "value is the block step when block runs, else the dense step")
+    ap.add_argument("--block-rows", type=int, default=8192, help="prefill rows T of the block step (8192 or 2048)")
     ap.add_argument("--moe-cases", default="", help="comma list of MoE cases to run, e.g. gpt_oss_20b_mxfp4_T4096 "
                                                      "(default: all)")
     ap.add_argument("--eager", action="store_true", help="time decode / MoE calls as plain launches, no HIP graphs "
@@ -441,24 +551,41 @@ def main():
     _lib.call("lsk_moe_mx_select", args.mx_variant)
     _lib.call("lsk_moe_select", args.moe_variant)
 
-    log("bench: dense prefill step (M=2048, gate_up 28672x4096 + down 4096x14336)")
-    d = dense_section(torch, args)
-    out = {
-        "metric": METRIC, "value": round(d["value"], 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(d["ms_per_step"], 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
-        "config": {"workload": "Llama-3.1-8B MLP contract GEMMs, w8a8_matmul v2.1, M=2048 prefill rows",
-                   "M": 2048, "gate_up": [28672, 4096], "down": [4096, 14336], "x": "f32 N(0,1), 0.1% +-20",
-                   "out": "bf16", "parallelism": "single GPU"},
-        "roofline": d["roofline"],
-        "qwen2_5_7b_m8192": d["qwen2_5_7b_m8192"],
-    }
-    tr = measured_traffic()
-    if tr and "gate_up" in tr and "down" in tr:
-        out["roofline"]["traffic"] = (tr["gate_up"] + tr["down"]) // 2
-        out["roofline"]["traffic_per_shape"] = {"gate_up": tr["gate_up"], "down": tr["down"]}
-        out["roofline"]["traffic_note"] = ("HBM bytes per launch (mean of the two shapes) from rocprofv3 FETCH_SIZE + "
-                                           "WRITE_SIZE, profiles/dense_prefill_llama8b_pmc.md")
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic"}
+    if "block" in sections:
+        log("bench: Qwen2.5-7B block GEMMs through ref_block_v1, T=%d" % args.block_rows)
+        b = block_section(torch, args)
+        out.update({
+            "value": round(b["value"], 2), "unit": "TOPS", "ms_per_step": round(b["ms_per_step"], 4),
+            "config": {"workload": "Qwen2.5-7B decoder block GEMMs through ref_block_v1 (quant8_dyn + exact int8 "
+                                   "GEMM + pow2 dequant, binary32 out), T=%d prefill rows" % b["T"],
+                       "T": b["T"], "qkv": [4608, 3584], "o": [3584, 3584], "gate_up": [37888, 3584],
+                       "down": [3584, 18944], "x": "f32 N(0,1)", "weights": "int8 U[-127,127], exponent 7",
+                       "parallelism": "single GPU"},
+            "roofline": b["roofline"], "per_site": b["per_site"]})
+        tr = measured_traffic("qwen25_7b_block")
+        if tr:
+            out["roofline"]["traffic"] = sum(tr.values()) // len(tr)
+            out["roofline"]["traffic_per_site"] = tr
+            out["roofline"]["traffic_note"] = ("HBM bytes per launch (mean of the four GEMMs) from rocprofv3 "
+                                               "FETCH_SIZE + WRITE_SIZE, profiles/block_qwen25_7b_t8192_pmc.md")
+    if "dense" in sections:
+        log("bench: Llama-3.1-8B MLP step (M=2048, gate_up 28672x4096 + down 4096x14336)")
+        d = dense_section(torch, args)
+        dense = {"workload": "Llama-3.1-8B MLP contract GEMMs, w8a8_matmul v2.1, M=2048 prefill rows, x f32 N(0,1) "
+                             "with 0.1% +-20 outliers, bf16 out",
+                 "TOPS": round(d["value"], 2), "ms_per_step": round(d["ms_per_step"], 4), "roofline": d["roofline"]}
+        tr = measured_traffic("llama8b")
+        if tr:
+            dense["roofline"]["traffic"] = sum(tr.values()) // len(tr)
+            dense["roofline"]["traffic_per_shape"] = tr
+        out["llama3_1_8b_mlp_m2048"] = dense
+        out["qwen2_5_7b_m8192_v21"] = d["qwen2_5_7b_m8192"]
+        if "value" not in out:
+            out.update({"value": dense["TOPS"], "unit": "TOPS", "ms_per_step": dense["ms_per_step"],
+                        "config": {"workload": dense["workload"], "parallelism": "single GPU"},
+                        "roofline": d["roofline"]})
     if "copy" in sections:
         out["copy"] = copy_section(torch, args)
     if "vendor" in sections:
@@ -470,8 +597,13 @@ def main():
         log("bench: MoE layers")
         out["moe"] = moe_section(torch, args)
     if not args.no_cpu_baseline:
-        log("bench: CPU baseline (reference op sequence, row sample)")
-        out["cpu_baseline"] = cpu_baseline_dense(args)
+        log("bench: CPU baselines (reference op sequences, row samples)")
+        if "block" in sections:
+            out["cpu_baseline"] = cpu_baseline_block(args)
+        if "dense" in sections:
+            cb = cpu_baseline_dense(args)
+            out["llama3_1_8b_mlp_m2048"]["cpu_baseline"] = cb
+            out.setdefault("cpu_baseline", cb)
         if "moe" in sections:
             out["moe"]["cpu_baseline"] = cpu_baseline_moe(args)
     print(json.dumps(out), flush=True)

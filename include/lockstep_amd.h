@@ -224,6 +224,16 @@ int lsk_gemm_select(int tile_id);
 int lsk_quant8_pow2(const float* x, int64_t M, int64_t K, int64_t ldx, int mode,
                     int8_t* q, int64_t ldq, int32_t* e_out, void* workspace, void* stream);
 
+/* quant8_dyn of the golden block (reference/ref_block_v1.py:122-130), the quantiser in front of each
+ * of its GEMM sites (:166-167 qkv, :191-193 o, :196-198 up, :216-218 down): one exponent for the
+ * whole x [M, K] binary32 (row stride ldx), the same rule and q as lsk_quant8_pow2 mode 0.  Writes
+ * e_out[0] and, when erow_out is not null, erow_out[0..M) = e, the per-row exponent vector that
+ * lsk_gemm_w8a8's POW2 epilogue takes, so the exponent never leaves the device.  Two launches and
+ * nothing to clear beforehand (graph-capturable).  workspace: lsk_quant8_dyn_workspace() bytes. */
+int64_t lsk_quant8_dyn_workspace(void);
+int lsk_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
+                   int32_t* e_out, int32_t* erow_out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- the MXFP4 operand */
 
 /* The MXFP4-consuming GEMM (contract addendum item 5).  Replaces moe_ref.int_mm_mx and,

@@ -53,6 +53,8 @@ SIGNATURES = {
     "lsk_tree_sum": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lsk_gemm_select": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
+    "lsk_quant8_dyn_workspace": (_I64, []),
+    "lsk_quant8_dyn": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
     "lsk_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "lsk_act_elementwise": (_I, [_P, _P, _I64, _I, _P, _P, _P]),
     "lsk_table_scores": (_I, [_P, _I64, _P, _P, _P]),

@@ -161,6 +161,37 @@ __device__ __forceinline__ void pp_strip_store_fast(int i, const int32_t* region
   }
 }
 
+// Fast epilogue of a whole tile under the POW2 order (ref_block_v1.py:167,193,198,218) with
+// binary32 output and no column exponents: y = fl32(acc) * fl32(2^-(shift + erow[m])), one
+// factor per row (the row exponent sits in the tile's row-operand slot), two 8-byte buffer
+// stores per four columns.
+template <class C>
+__device__ __forceinline__ void pp_strip_store_fast_pow2(int i, const int32_t* region, __amdgpu_buffer_rsrc_t ro,
+                                                         int ldo_bytes, int shift, const char* smem) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int wm = wave / C::kWN, wn = wave % C::kWN;
+  const float* sc_row = (const float*)(smem + C::kScaleOff);
+  constexpr int kQuads = C::WTN / 4;
+  constexpr int kRowStep = 64 / kQuads;
+  const int c4 = lane % kQuads, r0 = lane / kQuads;
+  const int nl = wn * C::WTN + c4 * 4;
+  const int ml0 = wm * C::WTM + i * 32 + r0;
+  const uint32_t off = (uint32_t)(ml0 * ldo_bytes + nl * 4);
+#pragma unroll
+  for (int t = 0; t < 32 / kRowStep; ++t) {
+    const v4i v = *(const v4i*)(region + (r0 + kRowStep * t) * C::kLdc + c4 * 4);
+    const float sc = pow2_descale(shift + __float_as_int(sc_row[ml0 + kRowStep * t]));
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y[k] = f32_mul((float)v[k], sc);
+    const v2u32 u0 = {__float_as_uint(y[0]), __float_as_uint(y[1])};
+    const v2u32 u1 = {__float_as_uint(y[2]), __float_as_uint(y[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(u0, ro, off, kRowStep * t * ldo_bytes, 0);
+    __asm__ volatile("" ::: "memory");  // keeps the two 8-byte stores from being merged into one
+    __builtin_amdgcn_raw_buffer_store_b64(u1, ro, off + 8, kRowStep * t * ldo_bytes, 0);
+  }
+}
+
 template <class C, int I>
 __device__ __forceinline__ void pp_epilogue_fast(const typename C::Acc& acc, __amdgpu_buffer_rsrc_t ro, int ldo_bytes,
                                                  char* smem) {
@@ -169,6 +200,17 @@ __device__ __forceinline__ void pp_epilogue_fast(const typename C::Acc& acc, __a
     lsk::pp_stage_strip<C::TN, C::kLdc>(acc[I], region);
     pp_strip_store_fast<C>(I, region, ro, ldo_bytes, smem);
     pp_epilogue_fast<C, I + 1>(acc, ro, ldo_bytes, smem);
+  }
+}
+
+template <class C, int I>
+__device__ __forceinline__ void pp_epilogue_fast_pow2(const typename C::Acc& acc, __amdgpu_buffer_rsrc_t ro,
+                                                      int ldo_bytes, int shift, char* smem) {
+  if constexpr (I < C::TM) {
+    int32_t* region = (int32_t*)(smem + wave_id() * C::kStripBytes);
+    lsk::pp_stage_strip<C::TN, C::kLdc>(acc[I], region);
+    pp_strip_store_fast_pow2<C>(I, region, ro, ldo_bytes, shift, smem);
+    pp_epilogue_fast_pow2<C, I + 1>(acc, ro, ldo_bytes, shift, smem);
   }
 }
 
@@ -278,6 +320,14 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
       pp_epilogue_fast<C, 0>(acc, ro, ldo_bytes, smem_pp);
       return;
     }
+  }
+  if (ep.order == LSK_EPI_POW2 && ep.ecol == nullptr && vec_ok == 2 && m0 + BM <= M && n0 + BN <= N &&
+      ep.out_dtype == LSK_F32) {
+    const int ldo_bytes = (int)(ep.ldo * 4);
+    char* base = (char*)ep.out + ((int64_t)m0 * ep.ldo + n0) * 4;
+    const __amdgpu_buffer_rsrc_t ro = lsk::make_rsrc(base, (int64_t)(BM - 1) * ldo_bytes + BN * 4);
+    pp_epilogue_fast_pow2<C, 0>(acc, ro, ldo_bytes, ep.shift, smem_pp);
+    return;
   }
 #define LSK_PP_EPI(O, D, B)                                                        \
   if (ep.order == O && ep.out_dtype == D && bias == B) {                           \

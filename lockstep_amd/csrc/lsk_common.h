@@ -45,6 +45,18 @@ LSK_DEV uint32_t pack_bf16x2_nonan(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f_t){a, b}, v2bf16_t));
 }
 
+// 16 bytes to global memory as two 8-byte stores.  On MI355X a 16-byte global / buffer store
+// followed three to four instructions later by VALU writes to its data registers was measured to
+// store the newer values, and the compiler separates the two by one wait state only; 8-byte
+// stores have no such hazard.  The empty asm with a memory clobber between the halves keeps the
+// load/store vectoriser from fusing them back into one 16-byte store.  p is 8-byte aligned.
+LSK_DEV void store16_split(void* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  ((v2u32*)p)[0] = v2u32{a, b};
+  __asm__ volatile("" ::: "memory");
+  ((v2u32*)p)[1] = v2u32{c, d};
+}
+LSK_DEV void store16_split(void* p, v4u32 v) { store16_split(p, v[0], v[1], v[2], v[3]); }
+
 // fl32 -> bf16 -> fl32 (one bf16 rounding, kept in binary32)
 LSK_DEV float bfr(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
@@ -52,6 +64,12 @@ LSK_DEV float bfr(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 LSK_DEV float pow2f(int e) {
   if (e >= -126) return __uint_as_float((uint32_t)(e + 127) << 23);
   return __uint_as_float(1u << (e + 149));
+}
+
+// The POW2 dequant factor fl32(2^-s) (ref_block_v1.py:167: F(2.0**(-e)), binary64 rounded once to
+// binary32): exact for s in [-127, 149], +0 above (2^-150 and below round to zero), +inf below.
+LSK_DEV float pow2_descale(int s) {
+  return s > 149 ? 0.0f : (s < -127 ? __uint_as_float(0x7f800000u) : pow2f(-s));
 }
 
 LSK_DEV float f32_mul(float a, float b) { return a * b; }
@@ -192,8 +210,7 @@ LSK_DEV void epilogue_store(const EpiParams& p, int64_t m, int64_t n, int32_t ac
     int s = p.shift;
     if (p.erow) s += p.erow[m];
     if (p.ecol) s += p.ecol[n];
-    float sc = (s > 149) ? 0.0f : (s < -127 ? __uint_as_float(0x7f800000u) : pow2f(-s));
-    store_out(p.out, p.out_dtype, o, f32_mul(v, sc));
+    store_out(p.out, p.out_dtype, o, f32_mul(v, pow2_descale(s)));
   }
 }
 
@@ -214,8 +231,7 @@ LSK_DEV float epi_value(const EpiParams& p, int64_t m, int64_t n, int32_t acc) {
   int s = p.shift;
   if (p.erow) s += p.erow[m];
   if (p.ecol) s += p.ecol[n];
-  float sc = (s > 149) ? 0.0f : (s < -127 ? __uint_as_float(0x7f800000u) : pow2f(-s));
-  return f32_mul(v, sc);
+  return f32_mul(v, pow2_descale(s));
 }
 
 // Epilogue value of one element from operands already in registers: the row operand (asc[m],
@@ -234,8 +250,7 @@ LSK_DEV float epi_value_pre(int order, int out_dtype, bool has_bias, int32_t acc
     if (has_bias) y = f32_add(y, bn);
     return y;
   }
-  float sc = (pshift > 149) ? 0.0f : (pshift < -127 ? __uint_as_float(0x7f800000u) : pow2f(-pshift));
-  return f32_mul(v, sc);
+  return f32_mul(v, pow2_descale(pshift));
 }
 
 // The per-element epilogue operands of output (m, n), loaded ahead of the accumulator so a
@@ -276,7 +291,7 @@ LSK_DEV void epilogue_store_ops(const EpiParams& p, int64_t m, int64_t n, int32_
 // vector store (the row segment is aligned and in range).  RAW stores the accumulators.
 LSK_DEV void store4_out(void* out, int order, int out_dtype, int64_t o, const float* y, v4i acc) {
   if (order == LSK_EPI_RAW) {
-    *(v4i*)((int32_t*)out + o) = acc;
+    store16_split((int32_t*)out + o, (uint32_t)acc[0], (uint32_t)acc[1], (uint32_t)acc[2], (uint32_t)acc[3]);
     return;
   }
   switch (out_dtype) {
@@ -297,10 +312,12 @@ LSK_DEV void store4_out(void* out, int order, int out_dtype, int64_t o, const fl
       break;
     }
     case LSK_BF16_AS_F32:
-      *(float4*)((float*)out + o) = make_float4(bfr(y[0]), bfr(y[1]), bfr(y[2]), bfr(y[3]));
+      store16_split((float*)out + o, __float_as_uint(bfr(y[0])), __float_as_uint(bfr(y[1])),
+                    __float_as_uint(bfr(y[2])), __float_as_uint(bfr(y[3])));
       break;
     default:
-      *(float4*)((float*)out + o) = make_float4(y[0], y[1], y[2], y[3]);
+      store16_split((float*)out + o, __float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]),
+                    __float_as_uint(y[3]));
   }
 }
 

@@ -1003,7 +1003,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
     o.y = (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
     o.z = (uint32_t)f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
     o.w = (uint32_t)f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
-    *(uint4*)(out + t * H + c) = o;
+    store16_split(out + t * H + c, o.x, o.y, o.z, o.w);
   }
 }
 

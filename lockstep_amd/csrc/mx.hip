@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void requant_bf16_kernel(const uint16_t* __res
     for (int j = 0; j < 4; ++j)
       o[j] = (uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] & 0xffff)), s, rs) |
              ((uint32_t)q_bf16(bf16_to_f32((uint16_t)(wd[j] >> 16)), s, rs) << 16);
-    *(uint4*)(q + p * I + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+    store16_split(q + p * I + c * 8, o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void blockquant_mx2_kernel(const uint16_t* __r
     for (int j = 0; j < 4; ++j)
       w[j] = (uint32_t)f32_to_bf16(f32_mul(mx2_q(v[2 * j], inv), sc)) |
              ((uint32_t)f32_to_bf16(f32_mul(mx2_q(v[2 * j + 1], inv), sc)) << 16);
-    *(uint4*)(q + r * K + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+    store16_split(q + r * K + 8 * c, w[0], w[1], w[2], w[3]);
     if ((c & 3) == 0) ka[r * (K / 32) + c / 4] = e;
     if (am > 0.0f && (e < lo || e > hi)) bad = 1;
   }
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void blockquant_mx2_kernel(const uint16_t* __r
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         w[j] = (uint32_t)f32_to_bf16(mx2_q(v[2 * j], inv)) | ((uint32_t)f32_to_bf16(mx2_q(v[2 * j + 1], inv)) << 16);
-      *(uint4*)(q + r * K + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+      store16_split(q + r * K + 8 * c, w[0], w[1], w[2], w[3]);
     }
   }
   if (threadIdx.x == 0) {

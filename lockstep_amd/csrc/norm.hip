@@ -141,7 +141,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_float_kernel(NormArgs p, int vec
         u.y = (uint32_t)f32_to_bf16(xv[c][2]) | ((uint32_t)f32_to_bf16(xv[c][3]) << 16);
         u.z = (uint32_t)f32_to_bf16(xv[c][4]) | ((uint32_t)f32_to_bf16(xv[c][5]) << 16);
         u.w = (uint32_t)f32_to_bf16(xv[c][6]) | ((uint32_t)f32_to_bf16(xv[c][7]) << 16);
-        *(uint4*)((uint16_t*)p.out + o) = u;
+        store16_split((uint16_t*)p.out + o, u.x, u.y, u.z, u.w);
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) store_out(p.out, p.out_dtype, o + j, xv[c][j]);

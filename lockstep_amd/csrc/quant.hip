@@ -203,20 +203,6 @@ LSK_DEV int8_t quant_pow2_one(float v, float scale) {
   return (int8_t)(int)t;
 }
 
-// |x| max over the whole tensor as order-free integer atomics on the float bits.
-__global__ __launch_bounds__(256) void amax_all_kernel(const float* __restrict__ x, int64_t M, int64_t K,
-                                                       int64_t ldx, uint32_t* __restrict__ out) {
-  __shared__ float red[4];
-  float am = 0.0f;
-  const int64_t total = M * K;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t r = i / K, c = i - r * K;
-    am = fmaxf(am, fabsf(x[r * ldx + c]));
-  }
-  am = block_max<256>(am, red);
-  if (threadIdx.x == 0) atomicMax(out, __float_as_uint(am));
-}
-
 __global__ __launch_bounds__(256) void amax_cols_kernel(const float* __restrict__ x, int64_t M, int64_t K,
                                                         int64_t ldx, uint32_t* __restrict__ out) {
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -227,25 +213,17 @@ __global__ __launch_bounds__(256) void amax_cols_kernel(const float* __restrict_
   atomicMax(out + c, __float_as_uint(am));
 }
 
-// mode 0: tensor exponent from amax_bits[0]; mode 2: column exponents from amax_bits[K]
-__global__ __launch_bounds__(256) void quant_pow2_kernel(const float* __restrict__ x, int64_t M, int64_t K,
-                                                         int64_t ldx, int mode,
-                                                         const uint32_t* __restrict__ amax_bits,
-                                                         int8_t* __restrict__ q, int64_t ldq,
-                                                         int32_t* __restrict__ e_out) {
+// per-column exponents from the column maxima amax_bits[K] (float bits)
+__global__ __launch_bounds__(256) void quant_pow2_cols_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                              int64_t ldx, const uint32_t* __restrict__ amax_bits,
+                                                              int8_t* __restrict__ q, int64_t ldq,
+                                                              int32_t* __restrict__ e_out) {
   const int64_t total = M * K;
-  if (mode == 0 && blockIdx.x == 0 && threadIdx.x == 0) e_out[0] = pow2_exponent(__uint_as_float(amax_bits[0]));
-  if (mode == 2) {
-    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < K; c += (int64_t)gridDim.x * 256)
-      e_out[c] = pow2_exponent(__uint_as_float(amax_bits[c]));
-  }
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < K; c += (int64_t)gridDim.x * 256)
+    e_out[c] = pow2_exponent(__uint_as_float(amax_bits[c]));
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int64_t r = i / K, c = i - r * K;
-    const float m = __uint_as_float(amax_bits[mode == 0 ? 0 : c]);
-    const float v = x[r * ldx + c];
-    int8_t qq = 0;
-    if (!(mode == 0 && m == 0.0f)) qq = quant_pow2_one(v, pow2f(pow2_exponent(m)));
-    q[r * ldq + c] = qq;
+    q[r * ldq + c] = quant_pow2_one(x[r * ldx + c], pow2f(pow2_exponent(__uint_as_float(amax_bits[c]))));
   }
 }
 
@@ -263,7 +241,115 @@ __global__ __launch_bounds__(256) void quant_pow2_rows_kernel(const float* __res
   for (int64_t k = threadIdx.x; k < K; k += 256) q[m * ldq + k] = quant_pow2_one(x[m * ldx + k], sc);
 }
 
+// ---------------------------------------------------------------- quant8_dyn (one exponent per tensor)
+// Two launches, nothing to clear beforehand (so the pair can be captured in a graph): pass 1
+// writes one |x| maximum per block to partial[blockIdx.x]; pass 2 has every block reduce those
+// partials (at most kDynBlocks floats, read from L2), derive the tensor exponent and quantise its
+// share of the tensor.  The maximum is exact in any order, so the grid shape does not matter.
+constexpr int kDynBlocks = 2048;
+
+// Contiguous tensors ([M, K] with ldx == K) are walked as one flat array of float4s, eight
+// elements per thread-step in pass 2; other strides go row by row.
+__global__ __launch_bounds__(256) void dyn_amax_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                       int64_t ldx, int flat, float* __restrict__ partial) {
+  __shared__ float red[4];
+  float am = 0.0f;
+  if (flat) {
+    const int64_t n4 = (M * K) >> 2;
+    const float4* x4 = (const float4*)x;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+      const float4 a = x4[i], b = x4[i + stride], c = x4[i + 2 * stride], d = x4[i + 3 * stride];
+      am = fmaxf(am, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                           fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+      am = fmaxf(am, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
+                           fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
+    }
+    for (; i < n4; i += stride) {
+      const float4 a = x4[i];
+      am = fmaxf(am, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    }
+    for (int64_t j = (n4 << 2) + (int64_t)blockIdx.x * 256 + threadIdx.x; j < M * K; j += stride)
+      am = fmaxf(am, fabsf(x[j]));
+  } else {
+    for (int64_t r = blockIdx.x; r < M; r += gridDim.x)
+      for (int64_t c = threadIdx.x; c < K; c += 256) am = fmaxf(am, fabsf(x[r * ldx + c]));
+  }
+  am = block_max<256>(am, red);
+  if (threadIdx.x == 0) partial[blockIdx.x] = am;
+}
+
+LSK_DEV uint32_t quant_pow2_x4(float4 v, float sc) {
+  return (uint32_t)(uint8_t)quant_pow2_one(v.x, sc) | ((uint32_t)(uint8_t)quant_pow2_one(v.y, sc) << 8) |
+         ((uint32_t)(uint8_t)quant_pow2_one(v.z, sc) << 16) | ((uint32_t)(uint8_t)quant_pow2_one(v.w, sc) << 24);
+}
+
+__global__ __launch_bounds__(256) void dyn_quant_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                        int64_t ldx, int flat, const float* __restrict__ partial,
+                                                        int nparts, int8_t* __restrict__ q, int64_t ldq,
+                                                        int32_t* __restrict__ e_out, int32_t* __restrict__ erow) {
+  __shared__ float red[4];
+  float am = 0.0f;
+  for (int j = threadIdx.x; j < nparts; j += 256) am = fmaxf(am, partial[j]);
+  am = block_max<256>(am, red);
+  const int e = pow2_exponent(am);   // 0 for an all-zero tensor, whose q is then 0 as well
+  const float sc = pow2f(e);         // e in [-32, 40]: a normal power of two
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  if (blockIdx.x == 0 && threadIdx.x == 0) e_out[0] = e;
+  if (erow)
+    for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < M; r += stride) erow[r] = e;
+  if (flat) {
+    const int64_t n8 = (M * K) >> 3;
+    const float4* x4 = (const float4*)x;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
+      const float4 a = x4[2 * i], b = x4[2 * i + 1];
+      *(v2u32*)(q + 8 * i) = v2u32{quant_pow2_x4(a, sc), quant_pow2_x4(b, sc)};
+    }
+    for (int64_t j = (n8 << 3) + (int64_t)blockIdx.x * 256 + threadIdx.x; j < M * K; j += stride)
+      q[j] = quant_pow2_one(x[j], sc);
+  } else {
+    for (int64_t r = blockIdx.x; r < M; r += gridDim.x)
+      for (int64_t c = threadIdx.x; c < K; c += 256) q[r * ldq + c] = quant_pow2_one(x[r * ldx + c], sc);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+// Launches of quant8_dyn on a workspace of kDynBlocks floats.
+int launch_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, int32_t* e_out,
+                      int32_t* erow, float* partial, hipStream_t s) {
+  const int64_t total = M * K;
+  const int flat = (ldx == K && ldq == K && ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 8) == 0) ? 1 : 0;
+  int64_t blocks = flat ? (total + 256 * 16 - 1) / (256 * 16) : M;
+  blocks = blocks < 1 ? 1 : (blocks > kDynBlocks ? kDynBlocks : blocks);
+  hipLaunchKernelGGL(dyn_amax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat, partial);
+  int rc = lsk::check_launch("dyn_amax_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(dyn_quant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat,
+                     (const float*)partial, (int)blocks, q, ldq, e_out, erow);
+  return lsk::check_launch("dyn_quant_kernel");
+}
+
 }  // namespace
+
+extern "C" int64_t lsk_quant8_dyn_workspace(void) { return (int64_t)kDynBlocks * sizeof(float); }
+
+extern "C" int lsk_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
+                              int32_t* e_out, int32_t* erow_out, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
+  LSK_REQUIRE(M >= 0 && K >= 0, "lsk_quant8_dyn: negative size M=%lld K=%lld", (long long)M, (long long)K);
+  LSK_REQUIRE(ldx >= K && ldq >= K, "lsk_quant8_dyn: ldx=%lld / ldq=%lld below K=%lld", (long long)ldx,
+              (long long)ldq, (long long)K);
+  LSK_REQUIRE(e_out, "lsk_quant8_dyn: e_out is required");
+  LSK_REQUIRE(workspace && workspace_bytes >= lsk_quant8_dyn_workspace(),
+              "lsk_quant8_dyn: workspace of %lld bytes required (%lld given)", (long long)lsk_quant8_dyn_workspace(),
+              (long long)workspace_bytes);
+  LSK_REQUIRE(M * K == 0 || (x && q), "lsk_quant8_dyn: null pointer");
+  return launch_quant8_dyn(x, M, K, ldx, q, ldq, e_out, erow_out, (float*)workspace, (hipStream_t)stream);
+}
 
 extern "C" int lsk_rowquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q,
                             int64_t ldq, float* asc, void* stream) {
@@ -305,31 +391,30 @@ extern "C" int lsk_quant8_pow2(const float* x, int64_t M, int64_t K, int64_t ldx
     return lsk::check_launch("quant_pow2_rows_kernel");
   }
   LSK_REQUIRE(workspace, "lsk_quant8_pow2: workspace required");
+  if (mode == 0) {
+    // the workspace (4 * (M + K + 64) bytes) holds the partial maxima of every grid quant8_dyn
+    // launches for this size
+    return launch_quant8_dyn(x, M, K, ldx, q, ldq, e_out, nullptr, (float*)workspace, s);
+  }
   uint32_t* amax = (uint32_t*)workspace;
-  const int64_t nam = mode == 0 ? 1 : K;
-  if (nam > 0) {
-    if (hipMemsetAsync(amax, 0, nam * sizeof(uint32_t), s) != hipSuccess) {
-      lsk::set_error("lsk_quant8_pow2: hipMemsetAsync failed");
-      return LSK_ERR_HIP;
-    }
+  if (K > 0) {
+    // column maxima are integer atomics on the float bits: clear them with a kernel (no memset
+    // node if the caller captures this into a graph)
+    int64_t fb = (K + 255) / 256;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)(fb > 1024 ? 1024 : fb)), dim3(256), 0, s, amax, K, 0u);
+    int rc = lsk::check_launch("fill_u32_kernel");
+    if (rc) return rc;
   }
   if (M > 0 && K > 0) {
-    if (mode == 0) {
-      const int64_t total = M * K;
-      int64_t blocks = (total + 255) / 256;
-      if (blocks > 4096) blocks = 4096;
-      hipLaunchKernelGGL(amax_all_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, amax);
-    } else {
-      dim3 g((unsigned)((K + 255) / 256), (unsigned)((M + 63) / 64));
-      hipLaunchKernelGGL(amax_cols_kernel, g, dim3(256), 0, s, x, M, K, ldx, amax);
-    }
+    dim3 g((unsigned)((K + 255) / 256), (unsigned)((M + 63) / 64));
+    hipLaunchKernelGGL(amax_cols_kernel, g, dim3(256), 0, s, x, M, K, ldx, amax);
     int rc = lsk::check_launch("amax kernel");
     if (rc) return rc;
   }
   int64_t blocks = (M * K + 255) / 256;
   if (blocks < 1) blocks = 1;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(quant_pow2_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, mode, amax, q, ldq,
+  hipLaunchKernelGGL(quant_pow2_cols_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, amax, q, ldq,
                      e_out);
-  return lsk::check_launch("quant_pow2_kernel");
+  return lsk::check_launch("quant_pow2_cols_kernel");
 }

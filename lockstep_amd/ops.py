@@ -257,6 +257,26 @@ def quant8_pow2(x: torch.Tensor, mode: int):
     return q, e[:ne]
 
 
+def quant8_dyn(x: torch.Tensor, erow: bool = False):
+    """Per-tensor power-of-two quant of x [..., K] binary32 on the device (lsk_quant8_dyn).
+    Returns (q int8 [..., K], e int32 [1]) and, with erow, also the exponent repeated per row
+    ([rows] int32, the POW2 epilogue's row operand); the exponent stays on the device."""
+    L.require_cuda(x, what="quant8_dyn")
+    x = x.to(torch.float32)
+    lead, K = x.shape[:-1], x.shape[-1]
+    x2 = _rows(x)
+    M = x2.shape[0]
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    e = torch.empty((1,), dtype=torch.int32, device=x.device)
+    er = torch.empty((M,), dtype=torch.int32, device=x.device) if erow else None
+    nbytes = L.load().lsk_quant8_dyn_workspace()
+    work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
+    L.call("lsk_quant8_dyn", L.ptr(x2), M, K, x2.stride(0) if M > 1 else max(K, 1), L.ptr(q), max(K, 1), L.ptr(e),
+           L.ptr(er), L.ptr(work), nbytes, L.stream_of(x))
+    q = q.reshape(*lead, K)
+    return (q, e, er) if erow else (q, e)
+
+
 OP_SILU, OP_SIGMOID, OP_ACT_SILU, OP_ACT_SWIGLUOAI = 0, 1, 2, 3
 
 

@@ -6,6 +6,8 @@
     quant8_dyn(x)       ref_block_v1.py:122-130
     gemm_int(a, b)      ref_block_v1.py:132-133
     gemm_pow2(q8, e_a, w8, e_w)   the pow2 dequant sites :167, 193, 198, 218 fused into the GEMM
+    linear_dyn(x, W8, ew)         a whole GEMM site (quant8_dyn, gemm_int, pow2 dequant), the
+                                  activation exponent kept on the device
 
 The reference works on numpy arrays; these functions take numpy arrays or GPU tensors and
 return the same kind.  numpy inputs are uploaded to the current GPU and the results copied
@@ -59,16 +61,34 @@ def quant8_cols(w):
 
 
 def quant8_dyn(x):
-    """Per-tensor pow2 quant: (q, e) with e a Python int (0 and q = 0 for an all-zero tensor)."""
+    """Per-tensor pow2 quant: (q, e) with e a Python int (0 and q = 0 for an all-zero tensor).
+    The exponent is computed on the device; returning it as an int (as the reference does)
+    synchronises with the device once.  linear_dyn keeps it on the device."""
     t, was_np = _to_dev(x, torch.float32)
     shp = t.shape
     t2 = t.reshape(-1, shp[-1]) if t.dim() >= 2 else t.reshape(1, -1)
-    q, e = ops.quant8_pow2(t2, 0)
+    q, e = ops.quant8_dyn(t2)
     q = q.reshape(shp)
     e = int(e[0].item())
     if was_np:
         return q.cpu().numpy().astype(np.int64), e
     return q, e
+
+
+def linear_dyn(x, W8, ew):
+    """One GEMM site of the block, fused: (gemm_int(q8, W8).astype(F) * F(2.0**(-ex-ew))).astype(F)
+    with (q8, ex) = quant8_dyn(x) -- ref_block_v1.py:166-167 (qkv), :191-193 (o), :196-198 (up),
+    :216-218 (down, per-tensor form).  x [T, K] binary32 tensor; W8 the reference's right
+    operand [K, N] of int8 values (a transposed view of a row-major [N, K] int8 weight is used in
+    place); ew the weight's exponent from quant8_dyn at arm time.  The activation exponent stays on
+    the device (no host synchronisation).  Returns (y binary32 [T, N], ex int32 [1] on the device)."""
+    L.require_cuda(x, W8, what="linear_dyn")
+    if x.dim() != 2:
+        raise ValueError("linear_dyn: x must be [T, K], got %s" % (tuple(x.shape),))
+    q8, ex, erow = ops.quant8_dyn(x, erow=True)
+    w_nk = ops.weight_nk(_as_int8(W8))
+    y = ops.gemm(q8, w_nk, L.EPI_POW2, L.LSK_F32, erow=erow, shift=int(ew))
+    return y, ex
 
 
 def _as_int8(t):
@@ -100,6 +120,8 @@ def gemm_pow2(q8, e_a, w8, e_w):
     erow = ecol = None
     if np.ndim(e_a) == 0 and not (isinstance(e_a, torch.Tensor) and e_a.dim() > 0):
         shift += int(e_a)
+    elif isinstance(e_a, torch.Tensor) and e_a.numel() == 1 and ta.shape[0] != 1:
+        erow = e_a.reshape(1).to(torch.int32).expand(ta.shape[0])   # a per-tensor exponent on the device
     else:
         erow = _to_dev(e_a, torch.int32)[0] if not isinstance(e_a, torch.Tensor) else e_a
     if np.ndim(e_w) == 0 and not (isinstance(e_w, torch.Tensor) and e_w.dim() > 0):

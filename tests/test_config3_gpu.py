@@ -1,0 +1,183 @@
+"""One Qwen2.5-7B-shaped decoder block's GEMMs through ref_block_v1, at 2048 and 8192 prefill rows.
+
+Shapes (hidden 3584; 28 query heads and 4 KV heads of 128 -> qkv N = 4608; o_proj 3584; SwiGLU
+intermediate 18944 -> gate+up N = 37888, down K = 18944), each GEMM fed a synthetic N(0,1)
+binary32 activation [T, K] and an int8 weight uniform on [-127, 127]:
+
+  pow2 form, the block's GEMM sites (reference/ref_block_v1.py:166-167, 191-193, 196-198,
+      216-218): q8, ex = quant8_dyn(x); y = fl32(gemm_int(q8, W8)) * fl32(2^-(ex + ew)), binary32.
+      The weight's exponent is ew = 7: quant8_dyn of the float weight W8 / 128 returns (W8, 7)
+      whenever the weight holds a +-127, which these weights do.
+  v2.1 form, the same shapes through lockstep_fullstack.w8a8_matmul with per-channel scales
+      U(1e-3, 1e-2) and bf16 output (reference/lockstep_fullstack.py:503-530).
+
+Checks per case: the exponent, and q, y on a seeded sample of rows (first, last and random) against
+the oracle; for every row, the int32 accumulator's column sums and row sums against exact integer
+identities (sum_m acc[m, n] = sum_k (sum_m q[m, k]) W[n, k], and the transpose), q against the
+rounding rule evaluated in torch, and the fused POW2 / v2.1 outputs against the RAW accumulator
+passed through a separate epilogue.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits, dev, f32_bits, say
+from oracle import contract as C
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+SHAPES = {"qkv": (4608, 3584), "o": (3584, 3584), "gate_up": (37888, 3584), "down": (3584, 18944)}
+EW = 7
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import lockstep_amd._lib as L
+    L.load()
+
+
+def _inputs(T, name):
+    N, K = SHAPES[name]
+    g = np.random.Generator(np.random.PCG64(3000 + T + list(SHAPES).index(name)))
+    x = g.standard_normal((T, K), dtype=np.float32)
+    W8 = g.integers(-127, 128, (N, K), dtype=np.int8)
+    W8[0, 0] = 127                                   # quant8_dyn(W8 / 128) = (W8, 7)
+    ws = g.uniform(1e-3, 1e-2, N).astype(F32)
+    rows = np.unique(np.concatenate([[0, 1, T - 1], g.choice(T, 21, replace=False)]))
+    return x, W8, ws, rows
+
+
+def _exact_rows(q_rows, W8):
+    """Exact int32 products of a few quantised rows (float64 BLAS: every partial sum < 2^53)."""
+    return C.int_mm(q_rows.astype(np.int8), W8.T, method="f64")
+
+
+@pytest.mark.parametrize("T", [2048, 8192])
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_qwen25_7b_block_gemm(T, name):
+    from lockstep_amd import _lib as L
+    from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import ops
+    from lockstep_amd import ref_block_v1 as RB
+
+    N, K = SHAPES[name]
+    say("config 3: %s T=%d (N=%d, K=%d)" % (name, T, N, K))
+    x, W8, ws, rows = _inputs(T, name)
+    xd = torch.from_numpy(x).to(dev())
+    Wd = torch.from_numpy(W8).to(dev())
+    wsd = torch.from_numpy(ws).to(dev())
+
+    # ---- pow2 form through the fused site and through the drop-in's separate calls
+    y, ex_dev = RB.linear_dyn(xd, Wd.t(), EW)
+    q8, ex = RB.quant8_dyn(xd)
+    assert int(ex_dev[0].item()) == ex
+    m = F32(np.max(np.abs(x)))
+    _, ex_ref = C.quant8_dyn(np.array([[m]], dtype=F32))   # the exponent depends on the maximum alone
+    assert ex == ex_ref
+    mrow = np.zeros((1, K), F32)
+    mrow[0, 0] = m                                           # keeps the tensor maximum in the sample
+    q_ref_rows, _ = C.quant8_dyn(np.concatenate([x[rows], mrow]))
+    assert np.array_equal(bits(q8[rows]).astype(np.int64), q_ref_rows[:-1])
+    # q for every row: the same rule in torch (one binary32 product by an exact power of two,
+    # round half to even, clamp)
+    q_t = torch.clamp(torch.round(xd * float(2.0 ** ex)), -127, 127).to(torch.int8)
+    assert torch.equal(q8, q_t)
+    del q_t
+    y_ref_rows = C.dequant_pow2(_exact_rows(q_ref_rows[:-1], W8), ex + EW)
+    assert np.array_equal(bits(y[rows]), f32_bits(y_ref_rows))
+    y2 = RB.gemm_pow2(q8, ex, Wd.t(), EW)
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    del y2
+    # every row: exact integer identities of the accumulator, and the fused epilogue against a
+    # separate one over the RAW accumulator
+    acc = ops.gemm(q8, Wd, L.EPI_RAW, L.LSK_I32)
+    colsum = acc.sum(0, dtype=torch.int64).cpu().numpy()
+    qsum = q8.sum(0, dtype=torch.int64).cpu().numpy()
+    assert np.array_equal(colsum, W8.astype(np.int64) @ qsum)
+    rowsum = acc.sum(1, dtype=torch.int64).cpu().numpy()
+    wsum = W8.sum(0, dtype=np.int64)
+    assert np.array_equal(rowsum, bits(q8).astype(np.int64) @ wsum)
+    assert torch.equal(y.view(torch.int32), (acc.float() * float(2.0 ** -(ex + EW))).view(torch.int32))
+    del y, q8
+
+    # ---- v2.1 form, bf16 out
+    yb = FS.w8a8_matmul(xd, Wd, wsd, out_dtype=torch.bfloat16)
+    ref_b = C.w8a8_matmul(x[rows], W8, ws, None, "bf16")
+    assert np.array_equal(bits(yb[rows]), ref_b)
+    qr, asc = ops.rowquant(xd)
+    acc = ops.gemm(qr, Wd, L.EPI_RAW, L.LSK_I32)
+    yb2 = ops.epilogue(acc, L.EPI_V21, L.LSK_BF16, asc=asc, ws=wsd)
+    assert torch.equal(yb.view(torch.int16), yb2.view(torch.int16))
+    del acc, yb, yb2, qr
+    torch.cuda.empty_cache()
+
+
+def test_quant8_dyn_edge_cases():
+    """Device quant8_dyn against the oracle: all-zero tensor (e = 0, q = 0), a maximum exactly at
+    127 * 2^j (no decrement) and just above (decrement), the clip at e = -32 / 40, strided rows,
+    and tails that are not a multiple of eight elements."""
+    from lockstep_amd import ops
+    from lockstep_amd import ref_block_v1 as RB
+
+    g = np.random.default_rng(77)
+    cases = [np.zeros((5, 7), F32),
+             (g.standard_normal((3, 33)) * 0.01).astype(F32),
+             np.full((2, 9), F32(127.0 * 2.0 ** -3)),
+             np.full((2, 9), np.nextafter(F32(127.0 * 2.0 ** -3), F32(1))),
+             (g.standard_normal((4, 16)) * 1e12).astype(F32),
+             (g.standard_normal((4, 16)) * 1e-14).astype(F32),
+             g.standard_normal((1, 1)).astype(F32),
+             g.standard_normal((257, 1001)).astype(F32)]
+    for x in cases:
+        q_ref, e_ref = C.quant8_dyn(x)
+        q, e = RB.quant8_dyn(torch.from_numpy(x).to(dev()))
+        assert e == e_ref, (x.shape, e, e_ref)
+        assert np.array_equal(bits(q).astype(np.int64), q_ref)
+    # a strided view (row stride > K) takes the row-by-row kernels
+    big = g.standard_normal((64, 300)).astype(F32)
+    xs = torch.from_numpy(big).to(dev())[:, :250]
+    q, e, er = ops.quant8_dyn(xs, erow=True)
+    q_ref, e_ref = C.quant8_dyn(big[:, :250])
+    assert int(e[0].item()) == e_ref and torch.all(er == e_ref)
+    assert np.array_equal(bits(q).astype(np.int64), q_ref)
+    # numpy in, numpy out (the reference's own types)
+    q_np, e_np = RB.quant8_dyn(big)
+    q_ref, e_ref = C.quant8_dyn(big)
+    assert e_np == e_ref and np.array_equal(q_np, q_ref)
+
+
+def test_linear_dyn_partial_tiles_and_graph_capture():
+    """linear_dyn on shapes whose tiles are partial (general epilogue) and whole (fast POW2
+    epilogue), and replayed from a captured HIP graph: every replay equals the eager result."""
+    from lockstep_amd import ref_block_v1 as RB
+
+    g = np.random.default_rng(5)
+    for T, N, K in [(300, 200, 96), (512, 512, 256), (257, 640, 160)]:
+        x = g.standard_normal((T, K)).astype(F32)
+        W8 = g.integers(-127, 128, (N, K), dtype=np.int8)
+        y, ex = RB.linear_dyn(torch.from_numpy(x).to(dev()), torch.from_numpy(W8).to(dev()).t(), 3)
+        q_ref, e_ref = C.quant8_dyn(x)
+        assert int(ex[0].item()) == e_ref
+        ref = C.dequant_pow2(C.gemm_int(q_ref, W8.T.astype(np.int64)), e_ref + 3)
+        assert np.array_equal(bits(y), f32_bits(ref)), (T, N, K)
+    T, N, K = 512, 768, 512
+    x = torch.from_numpy(g.standard_normal((T, K)).astype(F32)).to(dev())
+    W = torch.from_numpy(g.integers(-127, 128, (N, K), dtype=np.int8)).to(dev())
+    eager, _ = RB.linear_dyn(x, W.t(), 7)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        RB.linear_dyn(x, W.t(), 7)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out, _ = RB.linear_dyn(x, W.t(), 7)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32))
+        x.mul_(1.0)            # eager work between replays
