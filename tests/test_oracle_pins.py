@@ -355,3 +355,96 @@ def test_expert_rows_are_independent():
     full = C.expert_swiglu(x, *ex)
     for r in range(7):
         assert np.array_equal(C.expert_swiglu(x[r:r + 1], *ex)[0], full[r])
+
+
+# ------------------------------------------------------------------ table_scores, exactly
+def _router_c() -> float:
+    """moe_ref.py:61,68: 2^26 / ln 2 divided in binary64, then rounded once to binary32."""
+    return f32_round(Fraction(float(2 ** 26) / 0.6931471805599453))
+
+
+def _table_scores_rule(dgap: float, tab) -> int:
+    """moe_ref.py:64-74 in Python integers and rationals: d = rint_even(fl32(dgap * C)) clamped at
+    0; 0 when d >= 16 << 26; else tab[(d >> 13) & 8191] >> min(d >> 26, 63)."""
+    p = f32_round(Fraction(float(dgap)) * Fraction(_router_c()))
+    d = max(round(Fraction(p)), 0)            # round() of a Fraction: nearest, ties to even
+    if d >= 16 << 26:
+        return 0
+    return int(tab[(d >> 13) & 8191]) >> min(d >> 26, 63)
+
+
+def _straddling_gaps():
+    """Gaps whose binary32 product fl32(dgap * C) lies in [8192 j - 0.5, 8192 j): rounding to the
+    nearest integer gives d = 8192 j (table index j), truncation d = 8192 j - 1 (index j - 1)."""
+    c = _router_c()
+    out = []
+    for j in list(range(1, 40)) + list(range(40, 1024, 37)):
+        target = Fraction(8192 * j) - Fraction(1, 4)
+        x = F32(float(target) / c)
+        for _ in range(64):
+            p = Fraction(f32_round(Fraction(float(x)) * Fraction(c)))
+            if 8192 * j - Fraction(1, 2) <= p < 8192 * j:
+                out.append(float(x))
+                break
+            x = np.nextafter(x, F32(np.inf)) if p < target else np.nextafter(x, F32(0))
+    return out
+
+
+def test_table_scores_exact_rule_and_rounding_negative_control():
+    tab = C.frac_table()
+    c = _router_c()
+    assert float(C.ROUTER_C) == c
+    gaps = _straddling_gaps()
+    assert len(gaps) >= 60
+    # the window edge: the largest gap whose product stays below 16 << 26 = 2^30 and the next one
+    # up (products near 2^30 step by more than their 64-unit spacing), and far beyond it
+    x = F32(2 ** 30 / c)
+    while f32_round(Fraction(float(x)) * Fraction(c)) >= 2 ** 30:
+        x = np.nextafter(x, F32(0))
+    while f32_round(Fraction(float(np.nextafter(x, F32(np.inf)))) * Fraction(c)) < 2 ** 30:
+        x = np.nextafter(x, F32(np.inf))
+    edge = [float(x), float(np.nextafter(x, F32(np.inf))), float(F32(2 ** 33 / c))]
+    allg = np.array(gaps + edge + [0.0, 1e-30, 3.5, 11.0], F32)
+    got = C.table_scores(allg)
+    ref = [_table_scores_rule(float(v), tab) for v in allg]
+    assert [int(v) for v in got] == ref
+    d_in = round(Fraction(f32_round(Fraction(edge[0]) * Fraction(c))))
+    assert d_in < 2 ** 30 and ref[len(gaps)] == int(tab[(d_in >> 13) & 8191]) >> 15   # tab < 2^16
+    assert ref[len(gaps) + 1] == 0 and ref[len(gaps) + 2] == 0
+    # planted slip: truncating instead of rounding moves every straddling gap one table entry
+    def floor_variant(dg):
+        d = np.floor((np.asarray(dg, F32) * C.ROUTER_C).astype(F32)).astype(np.int64)
+        d = np.maximum(d, 0)
+        s = tab[(d >> 13) & 8191] >> np.minimum(d >> 26, 63)
+        return np.where(d < (16 << 26), s, 0)
+    slipped = floor_variant(np.array(gaps, F32))
+    assert np.all(slipped != np.array(ref[:len(gaps)]))
+
+
+# ------------------------------------------------------------------ E-v2 with a bias
+def test_epilogue_v2_bias_brute_force_and_negative_control():
+    """contract_common.py:172-174: y = fl32(fl32(fl32(acc) * asc) * ws); the bias is added in
+    binary32 before the single cast to the output type (y + bias.float(), then .to(x.dtype))."""
+    rng = np.random.default_rng(41)
+    M, N = 5, 40
+    acc = rng.integers(-(2 ** 27), 2 ** 27, (M, N)).astype(np.int32)
+    asc = rng.uniform(1e-3, 1e-1, M).astype(F32)
+    ws = rng.uniform(1e-3, 1e-2, N).astype(F32)
+    bias = (rng.standard_normal(N) * 3).astype(F32)
+    for out in ("bf16", "f32"):
+        y = C.out_to_f32(C.epilogue_v2(acc, ws, asc, bias, out), out)
+        slip = 0
+        for m in range(M):
+            for n in range(N):
+                a = f32_round(Fraction(int(acc[m, n])))
+                t = f32_round(Fraction(a) * Fraction(float(asc[m])))
+                t = f32_round(Fraction(t) * Fraction(float(ws[n])))
+                ref = f32_round(Fraction(t) + Fraction(float(bias[n])))
+                if out == "bf16":
+                    ref = bf16_round(ref)
+                    # the planted slip: cast first, add the bias after, cast again
+                    wrong = bf16_round(f32_round(Fraction(bf16_round(t)) + Fraction(float(bias[n]))))
+                    slip += wrong != ref
+                assert float(y[m, n]) == ref, (out, m, n)
+        if out == "bf16":
+            assert slip > 0
