@@ -100,6 +100,18 @@ int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
                     int order, void* out, int out_dtype, int64_t ldo,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* lsk_w8a8_matmul without a workspace argument and without allocating: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The quantised rows and their scales go to a
+ * fixed 16 MiB array of this library on each GPU (held until the process ends), so M rows of width
+ * K are accepted only while lsk_w8a8_matmul_workspace(M, K) <= 16 MiB (e.g. M = 2048 at K = 4096);
+ * larger sizes return LSK_ERR_ARG with a message.  Every call on one GPU uses that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race.  Same results and the same
+ * other arguments as lsk_w8a8_matmul. */
+int lsk_w8a8_matmul_noalloc(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                            const int8_t* w, int64_t ldw, int64_t N, const float* ws, const float* bias,
+                            int order, void* out, int out_dtype, int64_t ldo, void* stream);
+
 /* ---------------------------------------------------------------- the v2.5 outlier side path */
 
 /* The side term alone (replaces lockstep_fullstack.outlier_side, reference/lockstep_fullstack.py:549-557):

@@ -95,3 +95,12 @@ def test_block_scaled_and_router_entry_points_without_touching_the_gpu():
     assert b"unknown act 7" in lib.lsk_last_error()
     assert lib.lsk_act_table(None, L.LSK_ACT_SILU, None, None) == 1
     assert b"null pointer" in lib.lsk_last_error()
+
+
+def test_noalloc_entry_point_refuses_sizes_beyond_its_scratch_without_touching_the_gpu():
+    lib = L.load()
+    M, K = 4096, 8192                      # 32 MiB of quantised rows: above the 16 MiB scratch
+    rc = lib.lsk_w8a8_matmul_noalloc(None, 0, K, M, K, None, K, 64, None, None, 0, None, 1, 64, None)
+    assert rc == 1 and b"maximum" in lib.lsk_last_error()
+    # M == 0 is a no-op, as for lsk_w8a8_matmul
+    assert lib.lsk_w8a8_matmul_noalloc(None, 0, K, 0, K, None, K, 64, None, None, 0, None, 1, 64, None) == 0
