@@ -1,6 +1,7 @@
 """Builds liblockstep_amd.so from csrc/*.hip with hipcc for gfx950 only.
 
     python -m lockstep_amd.build          # or lockstep_amd.build.build()
+    python -m lockstep_amd.build --incremental   # recompile only sources older than their inputs
 
 Floating-point flags are part of the contract: no contraction into FMA, correctly rounded
 binary32 division, denormals kept, no packed-fp32 instructions.
@@ -41,8 +42,18 @@ FILE_FLAGS = {
 }
 
 
-def _compile(src: str) -> str:
+def _stale(src: str, obj: str) -> bool:
+    """Whether obj is missing or older than src, any header of csrc/ or include/, or this file."""
+    if not os.path.exists(obj):
+        return True
+    deps = [src, __file__] + glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h"))
+    return os.path.getmtime(obj) < max(os.path.getmtime(d) for d in deps)
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
+    if incremental and not _stale(src, obj):
+        return obj
     cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -50,11 +61,12 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compile every csrc/*.hip (all of them unless incremental) and link the library."""
     os.makedirs(OBJDIR, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda f: _compile(f, incremental), srcs))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -67,5 +79,5 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv[1:])
     sys.exit(0)
