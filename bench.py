@@ -417,8 +417,10 @@ def moe_section(torch, args):
     for name, c, kind, ops_tok, bytes_expert in cases:
         E, k, H, I = c["E"], c["k"], c["H"], c["I"]
         mx = kind > 0
-        wanted = [T for T in (1, 32, 4096)
-                  if not args.moe_cases or "%s_T%d" % (name, T) in args.moe_cases.split(",")]
+        # Qwen3-30B-A3B also at the token counts the reference publishes its fused-layer H100 times for
+        # (8, 256, 2048)
+        counts = (1, 8, 32, 256, 2048, 4096) if kind == 0 else (1, 32, 4096)
+        wanted = [T for T in counts if not args.moe_cases or "%s_T%d" % (name, T) in args.moe_cases.split(",")]
         if not wanted:
             continue
         if kind != 2 or copies is None:  # the block-scaled case reuses the MXFP4 experts

@@ -11,6 +11,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import subprocess
 import sys
 
@@ -42,11 +43,25 @@ FILE_FLAGS = {
 }
 
 
+def _includes(path: str, seen: set) -> set:
+    """path and the local headers it includes, transitively (#include "..." in csrc/ or include/)."""
+    if path in seen or not os.path.exists(path):
+        return seen
+    seen.add(path)
+    with open(path) as f:
+        for line in f:
+            m = re.match(r'\s*#\s*include\s+"([^"]+)"', line)
+            if m:
+                for d in (CSRC, INCLUDE):
+                    _includes(os.path.join(d, m.group(1)), seen)
+    return seen
+
+
 def _stale(src: str, obj: str) -> bool:
-    """Whether obj is missing or older than src, any header of csrc/ or include/, or this file."""
+    """Whether obj is missing or older than src, a header it includes, or this file."""
     if not os.path.exists(obj):
         return True
-    deps = [src, __file__] + glob.glob(os.path.join(CSRC, "*.h")) + glob.glob(os.path.join(INCLUDE, "*.h"))
+    deps = _includes(src, set()) | {__file__}
     return os.path.getmtime(obj) < max(os.path.getmtime(d) for d in deps)
 
 

@@ -232,16 +232,13 @@ LSK_DEV void count_chunk(const int32_t* ids, int T, int k, int c0, int32_t* cnt,
   }
 }
 
-// T <= 256: the whole dispatch in one block.
-__global__ __launch_bounds__(256) void moe_dispatch_small_kernel(const int64_t* __restrict__ idx,
-                                                                 const uint16_t* __restrict__ w, int T, int k, int E,
-                                                                 int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
-                                                                 int32_t* __restrict__ row_tok,
-                                                                 int32_t* __restrict__ row_dst,
-                                                                 float* __restrict__ row_w,
-                                                                 int32_t* __restrict__ tok_cnt,
-                                                                 uint32_t* __restrict__ zero_buf, int64_t zero_n) {
-  extern __shared__ int32_t dsm[];  // cnt [E], base [E + 1], mask [8 E], ids [256 k], wts [256 k] u16
+// T <= 256: the whole dispatch in one block (dynamic LDS: cnt [E], base [E + 1], mask [8 E],
+// ids [256 k], wts [256 k] u16).
+LSK_DEV void dispatch_small_block(const int64_t* __restrict__ idx, const uint16_t* __restrict__ w, int T, int k, int E,
+                                  int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
+                                  int32_t* __restrict__ row_tok, int32_t* __restrict__ row_dst,
+                                  float* __restrict__ row_w, int32_t* __restrict__ tok_cnt,
+                                  uint32_t* __restrict__ zero_buf, int64_t zero_n, int32_t* dsm) {
   __shared__ int tmp[4];
   int32_t* cnt = dsm;
   int32_t* base = dsm + E;
@@ -259,6 +256,105 @@ __global__ __launch_bounds__(256) void moe_dispatch_small_kernel(const int64_t* 
   for (int e = tid; e <= E; e += 256) offs[e] = base[e];  // base[E] = all rows
   __syncthreads();
   place_chunk(ids, wts, T, k, E, 0, base, mask, row_tok, row_dst, row_w);
+}
+
+__global__ __launch_bounds__(256) void moe_dispatch_small_kernel(const int64_t* __restrict__ idx,
+                                                                 const uint16_t* __restrict__ w, int T, int k, int E,
+                                                                 int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
+                                                                 int32_t* __restrict__ row_tok,
+                                                                 int32_t* __restrict__ row_dst,
+                                                                 float* __restrict__ row_w,
+                                                                 int32_t* __restrict__ tok_cnt,
+                                                                 uint32_t* __restrict__ zero_buf, int64_t zero_n) {
+  extern __shared__ int32_t dsm[];
+  dispatch_small_block(idx, w, T, k, E, offs, tiles, row_tok, row_dst, row_w, tok_cnt, zero_buf, zero_n, dsm);
+}
+
+// Decode-sized layers (the grouped GEMV path) start with one launch: block 0 runs the dispatch
+// (clearing the per-row |h| maxima, zero_buf), block 1 + t the row quant of token t -- int8 rows, or their values as bf16 for MXFP4 experts -- with the
+// scale and rounding of lsk_rowquant.
+__global__ __launch_bounds__(256) void moe_decode_prep_kernel(const int64_t* __restrict__ idx,
+                                                              const uint16_t* __restrict__ w, int T, int k, int E,
+                                                              int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
+                                                              int32_t* __restrict__ row_tok,
+                                                              int32_t* __restrict__ row_dst, float* __restrict__ row_w,
+                                                              int32_t* __restrict__ tok_cnt,
+                                                              uint32_t* __restrict__ zero_buf, int64_t zero_n,
+                                                              const uint16_t* __restrict__ x, int H,
+                                                              void* __restrict__ qx, float* __restrict__ ascx,
+                                                              int q_bf16) {
+  extern __shared__ int32_t dsm[];
+  if (blockIdx.x == 0) {
+    dispatch_small_block(idx, w, T, k, E, offs, tiles, row_tok, row_dst, row_w, tok_cnt, zero_buf, zero_n, dsm);
+    return;
+  }
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x - 1;
+  const uint16_t* row = x + t * H;
+  const int tid = threadIdx.x;
+  if ((H & 7) == 0 && H <= 8192 && ((uintptr_t)x & 15) == 0) {
+    // the row in registers: thread tid holds elements 8 tid + 2048 j .. + 7 (16-byte loads, all
+    // issued before the maximum)
+    constexpr int NJ = 4;
+    uint4 v[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = 8 * tid + 2048 * j;
+      v[j] = c < H ? *(const uint4*)(row + c) : make_uint4(0, 0, 0, 0);
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        am = fmaxf(am, fmaxf(fabsf(bf16_to_f32((uint16_t)(wd[e] & 0xffff))), fabsf(bf16_to_f32((uint16_t)(wd[e] >> 16)))));
+    }
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = am;
+    __syncthreads();
+    am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float sc = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, sc);
+    if (tid == 0) ascx[t] = sc;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = 8 * tid + 2048 * j;
+      if (c >= H) break;
+      const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+      float qv[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qv[2 * e] = fminf(fmaxf(rint_div8(bf16_to_f32((uint16_t)(wd[e] & 0xffff)), sc, rs), -127.0f), 127.0f);
+        qv[2 * e + 1] = fminf(fmaxf(rint_div8(bf16_to_f32((uint16_t)(wd[e] >> 16)), sc, rs), -127.0f), 127.0f);
+      }
+      if (q_bf16) {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = (__float_as_uint(qv[2 * e]) >> 16) | (__float_as_uint(qv[2 * e + 1]) & 0xffff0000u);
+        store16_split((uint16_t*)qx + t * H + c, o[0], o[1], o[2], o[3]);
+      } else {
+        uint32_t o[2] = {0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e >> 2] |= (uint32_t)(uint8_t)(int8_t)(int)qv[e] << (8 * (e & 3));
+        *(v2u32*)((int8_t*)qx + t * H + c) = v2u32{o[0], o[1]};
+      }
+    }
+    return;
+  }
+  float am = 0.0f;
+  for (int i = tid; i < H; i += 256) am = fmaxf(am, fabsf(bf16_to_f32(row[i])));
+  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, sc);
+  if (tid == 0) ascx[t] = sc;
+  for (int i = tid; i < H; i += 256) {
+    const float qv = fminf(fmaxf(rint_div8(bf16_to_f32(row[i]), sc, rs), -127.0f), 127.0f);
+    if (q_bf16) ((uint16_t*)qx)[t * H + i] = (uint16_t)(__float_as_uint(qv) >> 16);  // exact in bf16
+    else ((int8_t*)qx)[t * H + i] = (int8_t)(int)qv;
+  }
 }
 
 // Large T, step 1: per-chunk expert counts ccnt[chunk][E].
@@ -985,13 +1081,21 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
     const int n = tok_cnt[t];
-    for (int r = 0; r < n; ++r) {
-      const uint4 u = *(const uint4*)(slots + (t * k + r) * H + c);
-      const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+    // the token's slots four at a time, their loads issued together before the ordered adds
+    for (int r0 = 0; r0 < n; r0 += 4) {
+      uint4 u[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        u[j] = r0 + j < n ? *(const uint4*)(slots + (t * k + r0 + j) * H + c) : make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        acc[2 * j] = f32_add(acc[2 * j], bf16_to_f32((uint16_t)(wd[j] & 0xffff)));
-        acc[2 * j + 1] = f32_add(acc[2 * j + 1], bf16_to_f32((uint16_t)(wd[j] >> 16)));
+        if (r0 + j >= n) break;
+        const uint32_t wd[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[2 * q] = f32_add(acc[2 * q], bf16_to_f32((uint16_t)(wd[q] & 0xffff)));
+          acc[2 * q + 1] = f32_add(acc[2 * q + 1], bf16_to_f32((uint16_t)(wd[q] >> 16)));
+        }
       }
     }
     if (shared) {
@@ -1245,8 +1349,12 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   // 278 us, T = 24 281 vs 277 us)
   const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
 
+  // up to 256 tokens: the dispatch and the row quant of x in one launch
+  const bool prep_decode = T <= 256 && rb == 0 && mx != 2;
   int rc;
-  if (rb > 0) {
+  if (prep_decode) {
+    rc = LSK_OK;  // the prep kernel below quantises x
+  } else if (rb > 0) {
     // xrot = fwht_blocks(fl32(x)): widen, then butterfly in place
     int64_t blocks = (T * H + 255) / 256;
     blocks = blocks > 8192 ? 8192 : blocks;
@@ -1267,7 +1375,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   static bool dispatch_lds = false;
   if (!dispatch_lds) {
     for (const void* f : {(const void*)moe_dispatch_small_kernel, (const void*)moe_count_kernel,
-                          (const void*)moe_place_kernel})
+                          (const void*)moe_place_kernel, (const void*)moe_decode_prep_kernel})
       if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess) {
         lsk::set_error("lsk_moe_forward: cannot reserve LDS for the dispatch");
         return LSK_ERR_HIP;
@@ -1279,7 +1387,13 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   const int64_t nzero = mx == 2 ? R + 2 : R;
   int32_t* anyf = (int32_t*)(w.h_amax + R);
   const int64_t nchunks = (T + 255) / 256;
-  if (nchunks == 1) {
+  if (prep_decode) {
+    const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
+    hipLaunchKernelGGL(moe_decode_prep_kernel, dim3((unsigned)(T + 1)), dim3(256), dsm, s, a->idx, a->w, (int)T, k,
+                       (int)E, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero,
+                       a->x, (int)H, (void*)w.qx, w.ascx, mx ? 1 : 0);
+    if ((rc = lsk::check_launch("moe_decode_prep_kernel"))) return rc;
+  } else if (nchunks == 1) {
     const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
     hipLaunchKernelGGL(moe_dispatch_small_kernel, dim3(1), dim3(256), dsm, s, a->idx, a->w, (int)T, k, (int)E, w.offs,
                        w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero);

@@ -282,3 +282,41 @@ def test_config4_t4096_token_subset():
     rows = np.sort(np.random.default_rng(1).choice(T, 48, replace=False))
     ref = C.moe_forward(x[rows], oracle_experts(experts), idx[rows], w[rows])
     assert np.array_equal(u16(y)[rows], ref)
+
+
+def test_moe_decode_layers_replayed_from_a_graph():
+    """The decode-sized layer (dispatch and row quant in one launch; activation / requant and
+    combine as the GEMVs' last-block tails, whose arrival counters reset themselves): layers of
+    1, 12 and 1 tokens in a row, then one layer captured in a HIP graph and replayed, with eager
+    layers of another size between the replays; every output against the oracle."""
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+
+    def case(T, seed):
+        x, experts, logits = WL.moe_inputs(T, 16, 4, 256, 128, seed=seed)
+        idx, w = routing_from_logits(logits, 4)
+        ref = C.moe_forward(x, oracle_experts(experts), idx, w, act=C.act_silu)
+        ridx, rw = routing_device(idx, w)
+        return bf16_dev(x), device_experts(experts), (ridx, rw), ref
+
+    cases = [case(T, 60 + T) for T in (1, 12, 1)]
+    for dx, dexp, rt, ref in cases:
+        y, _, _ = MR.moe_forward(dx, None, dexp, 4, True, _tab(), 0, MR.act_silu, routing=rt)
+        assert np.array_equal(u16(y), ref)
+    dx, dexp, rt, ref = case(3, 70)
+    other = case(7, 71)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        MR.moe_forward(dx, None, dexp, 4, True, _tab(), 0, MR.act_silu, routing=rt)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        yg, _, _ = MR.moe_forward(dx, None, dexp, 4, True, _tab(), 0, MR.act_silu, routing=rt)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(u16(yg), ref)
+        yo, _, _ = MR.moe_forward(other[0], None, other[1], 4, True, _tab(), 0, MR.act_silu, routing=other[2])
+        assert np.array_equal(u16(yo), other[3])
