@@ -285,9 +285,8 @@ def test_config4_t4096_token_subset():
 
 
 def test_moe_decode_layers_replayed_from_a_graph():
-    """The decode-sized layer (dispatch and row quant in one launch; activation / requant and
-    combine as the GEMVs' last-block tails, whose arrival counters reset themselves): layers of
-    1, 12 and 1 tokens in a row, then one layer captured in a HIP graph and replayed, with eager
+    """The decode-sized layer (dispatch and row quant of x in one launch, then the GEMVs): layers
+    of 1, 12 and 1 tokens in a row, then one layer captured in a HIP graph and replayed, with eager
     layers of another size between the replays; every output against the oracle."""
     from lockstep_amd import moe_ref as MR
     from lockstep_amd import workloads as WL
