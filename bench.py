@@ -463,6 +463,91 @@ def moe_section(torch, args):
     return res
 
 
+# The reference's published grouped-GEMM times on H100 (ms) for the same shapes, with their source.
+REF_GROUPED_H100 = {
+    "qwen3_gate_up_R16384": (0.2378, "results/s3/logs/s21_m1g90b_h100.log:3"),
+    "qwen3_down_R16384": (0.1508, "results/s3/logs/s21_m1g90b_h100.log:8"),
+    "gptoss_int8_gate_up_R8192": (0.4620, "results/s3/logs/s21_m2x8_h100.log:11"),
+    "gptoss_int8_gate_up_R256": (0.2012, "results/s3/logs/s21_m2x13_h100.log:11"),
+    "gptoss_int8_down_R256": (0.1042, "results/s3/logs/s21_m2x13_h100.log:24"),
+    "gptoss_mx_gate_up_R8192": (2.2807, "results/s3/logs/s21_m2x11_h100.log:4"),
+    "gptoss_mx_down_R8192": (1.1408, "results/s3/logs/s21_m2x11_h100.log:22"),
+    "gptoss_mx_gate_up_R256": (0.2693, "results/s3/logs/s21_m2x16_h100.log:5"),
+    "gptoss_mx_down_R256": (0.1656, "results/s3/logs/s21_m2x16_h100.log:21"),
+}
+
+
+def grouped_section(torch, args):
+    """The grouped expert GEMM stage alone (lsk_grouped_gemm_w8a8 / lsk_grouped_gemm_mx: expert-sorted
+    rows through each expert's projection with the contract epilogue, bf16 out) at the shapes the
+    reference publishes H100 times for: Qwen3-30B-A3B gate_up (N=1536, K=2048) and down (N=2048,
+    K=768) over the 16384 rows of 2048 tokens x top-8; GPT-OSS-20B gate_up (N=5760) and down
+    (N=2880) at K=2880 over 8192 rows (2048 tokens x top-4) and 256 rows (64 tokens), int8 and
+    MXFP4.  Rows per expert come from the router on synthetic logits (Zipf-biased for Qwen3).
+    HIP events over repeated launches on the launch stream."""
+    from lockstep_amd import contract_common as CC
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    tab = CC.table_on(dev)
+    res = {}
+
+    def rows_of(T, E, k, zipf):
+        logits = torch.randn((T, E), generator=g, device=dev)
+        if zipf:
+            rank = torch.randperm(E, generator=g, device=dev).to(torch.float32)
+            logits = logits - 1.1 * torch.log1p(rank)[None, :]
+        idx, _, _ = MR.router_from_logits(logits.to(torch.bfloat16), k, True, tab)
+        cnt = torch.bincount(idx.reshape(-1), minlength=E)
+        offs = torch.zeros(E + 1, dtype=torch.int32, device=dev)
+        offs[1:] = torch.cumsum(cnt, 0).to(torch.int32)
+        return offs, int(cnt.sum().item())
+
+    def run(name, fn, R, N, K):
+        for _ in range(3):
+            fn()
+        ms = _events_time(torch, fn, 20)
+        ref_ms, src = REF_GROUPED_H100[name]
+        res[name] = {"us": round(ms * 1e3, 1), "TOPS": round(2 * R * N * K / (ms * 1e-3) / 1e12, 1), "rows": R,
+                     "N": N, "K": K, "reference_h100_us": round(ref_ms * 1e3, 1), "reference_source": src}
+        log("bench: grouped %s: %.1f us (reference H100 %.1f us)" % (name, ms * 1e3, ref_ms * 1e3))
+
+    # Qwen3-30B-A3B, int8
+    c = WL.QWEN3_30B_A3B
+    tables = _int8_expert_tables(torch, MR, g, dev, c["E"], c["H"], c["I"])
+    offs, R = rows_of(2048, c["E"], c["k"], True)
+    a8 = torch.randint(-127, 128, (R, c["H"]), generator=g, device=dev, dtype=torch.int8)
+    asc = torch.empty(R, device=dev).uniform_(1e-3, 1e-2, generator=g)
+    run("qwen3_gate_up_R16384", lambda: MR.grouped_linear(tables, "w13", a8, asc, offs), R, 2 * c["I"], c["H"])
+    a8 = torch.randint(-127, 128, (R, c["I"]), generator=g, device=dev, dtype=torch.int8)
+    run("qwen3_down_R16384", lambda: MR.grouped_linear(tables, "w2", a8, asc, offs), R, c["H"], c["I"])
+    del tables, a8
+    # GPT-OSS-20B shapes, int8 then MXFP4
+    c = WL.GPT_OSS_20B
+    for kind in ("int8", "mx"):
+        mk = _int8_expert_tables if kind == "int8" else _mx_expert_tables
+        tables = mk(torch, MR, g, dev, c["E"], c["H"], c["I"])
+        fwd = MR.grouped_linear if kind == "int8" else MR.grouped_linear_mx
+        for T in (2048, 64):
+            offs, R = rows_of(T, c["E"], c["k"], False)
+            asc = torch.empty(R, device=dev).uniform_(1e-3, 1e-2, generator=g)
+            a8 = torch.randint(-127, 128, (R, c["H"]), generator=g, device=dev, dtype=torch.int8)
+            if "gptoss_%s_gate_up_R%d" % (kind, R) in REF_GROUPED_H100:
+                run("gptoss_%s_gate_up_R%d" % (kind, R), lambda: fwd(tables, "w13", a8, asc, offs), R, 2 * c["I"],
+                    c["H"])
+            if "gptoss_%s_down_R%d" % (kind, R) in REF_GROUPED_H100:
+                a8 = torch.randint(-127, 128, (R, c["I"]), generator=g, device=dev, dtype=torch.int8)
+                run("gptoss_%s_down_R%d" % (kind, R), lambda: fwd(tables, "w2", a8, asc, offs), R, c["H"], c["I"])
+        del tables
+        torch.cuda.empty_cache()
+    res["note"] = ("grouped expert GEMM stage alone (rows already sorted by expert, contract epilogue, bf16 out), "
+                   "HIP events; reference_h100_us: the reference's published time for the same shape on H100")
+    return res
+
+
 def cpu_baseline_moe(args):
     """The reference's moe_forward op sequence on the host (per-expert loop, int64 matmuls), on a
     token sample of the config-4 layer."""
@@ -524,8 +609,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sections", default="block,dense,decode,moe",
-                    help="comma list of block (the headline), dense, decode, moe, vendor, copy; the JSON line's "
+    ap.add_argument("--sections", default="block,dense,decode,moe,grouped",
+                    help="comma list of block (the headline), dense, decode, moe, grouped, vendor, copy; the JSON line's "
                          "value is the block step when block runs, else the dense step")
     ap.add_argument("--block-rows", type=int, default=8192, help="prefill rows T of the block step (8192 or 2048)")
     ap.add_argument("--moe-cases", default="", help="comma list of MoE cases to run, e.g. gpt_oss_20b_mxfp4_T4096 "
@@ -598,6 +683,9 @@ def main():
     if "moe" in sections:
         log("bench: MoE layers")
         out["moe"] = moe_section(torch, args)
+    if "grouped" in sections:
+        log("bench: grouped expert GEMM stage")
+        out["grouped"] = grouped_section(torch, args)
     if not args.no_cpu_baseline:
         log("bench: CPU baselines (reference op sequences, row samples)")
         if "block" in sections:

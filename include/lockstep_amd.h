@@ -418,6 +418,33 @@ int lsk_act_table(const int32_t* frac, int act, float* table, void* stream);
 
 int lsk_moe_forward(const lsk_moe_args* args, void* stream);
 
+/* One grouped expert linear over rows already sorted by expert: expert e owns rows
+ * offs[e] .. offs[e + 1] - 1 (offs [E + 1] int32 on the device, nondecreasing) of a, and
+ *   out[p, n] = bfr(fl32(fl32(acc[p, n]) * ws_e[n]) * asc[p]), then bfr(out + b_e[n]) with a bias,
+ *   acc[p, n] = sum_k a[p, k] * w_e[n, k] exact,
+ * bf16 out [R, N] (row stride N).  The grouped form of the per-expert int_mm + lin_epilogue /
+ * lin_epilogue_b that moe_ref.expert_block runs for each expert (reference/moe_ref.py:40-55,
+ * 164-169, 189-200) -- the grouped-GEMM stage of lsk_moe_forward without the routing weight.
+ * a: [R, K] int8 (row stride lda); asc: [R]; w_ptrs[e]: int8 [N, K] (row stride ldw, the
+ * reference's W.t() of w_col [K, N]); ws_ptrs[e]: f32 [N]; b_ptrs: null or [E] of f32 [N].
+ * workspace: lsk_grouped_gemm_workspace(R, E) bytes, 256-byte aligned (the tile table). */
+int64_t lsk_grouped_gemm_workspace(int64_t R, int64_t E);
+int lsk_grouped_gemm_w8a8(const int8_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E, int64_t R,
+                          const int64_t* w_ptrs, int64_t ldw, const int64_t* ws_ptrs, const int64_t* b_ptrs,
+                          int64_t N, int64_t K, uint16_t* out, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/* The MXFP4 form: per expert e, int_mm_mx then lin_epilogue_mx (reference/moe_ref.py:243-261, run
+ * per expert by expert_block_mx :264-271): acc = the ordered block accumulation of int_mm_mx,
+ * out = bfr(fl32(acc * asc[p])), then bfr(out + b_e[n]).  a: the int8 row values held as bf16
+ * [R, K] (row stride lda elements, the MX kernels' operand form); w_ptrs[e]: packed E2M1 codes
+ * [N, K / 2] (row stride ldw bytes); kx_ptrs[e]: E8M0 bytes [N, K / 32] (row stride lds); safe as
+ * lsk_moe_args.mx_safe.  Same offsets, output and workspace as lsk_grouped_gemm_w8a8. */
+int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E, int64_t R,
+                        const int64_t* w_ptrs, int64_t ldw, const int64_t* kx_ptrs, int64_t lds, const int64_t* b_ptrs,
+                        int64_t N, int64_t K, int safe, uint16_t* out, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
 /* Tuning control with no counterpart in the reference: the int8 grouped expert GEMMs of
  * lsk_moe_forward on the 128x128 register-staged tile (0), on the eight-wave ping-pong
  * 128x256 tile (1), on the grouped GEMV (2: whole weight rows streamed once against up to 8

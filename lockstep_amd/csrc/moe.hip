@@ -536,7 +536,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
           const int n0 = nt * 128 + wn * 64 + c4;
           if (p < p1 && n0 < a.N) {
             const float asc = a.a_scale[p];
-            const float wt = a.row_w[p];
+            const float wt = a.row_w ? a.row_w[p] : 1.0f;  // none: a plain grouped linear
             uint16_t ob[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -548,7 +548,7 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
                 ob[t] = f32_to_bf16(f32_mul(wt, yv));
               }
             }
-            uint16_t* dst = a.y + (int64_t)a.row_dst[p] * a.N + n0;
+            uint16_t* dst = a.y + (int64_t)(a.row_dst ? a.row_dst[p] : p) * a.N + n0;
             if (n0 + 4 <= a.N) {
               *(uint2*)dst =
                   make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
@@ -613,8 +613,8 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
       r_asc = a.a_scale[a.row_tok[p]];
     } else {
       r_asc = a.a_scale[p];
-      r_w = a.row_w[p];
-      r_dst = a.row_dst[p];
+      r_w = a.row_w ? a.row_w[p] : 1.0f;  // none: a plain grouped linear (weight 1, row p out)
+      r_dst = a.row_dst ? a.row_dst[p] : p;
     }
   }
   if (tid < 256) {
@@ -898,8 +898,8 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemmArgs a, uint16_t* 
     if (rowok) {
       asc = a.a_scale[MODE == 0 ? a.row_tok[p] : p];
       if (MODE == 1) {
-        wt = a.row_w[p];
-        dst = a.row_dst[p];
+        wt = a.row_w ? a.row_w[p] : 1.0f;
+        dst = a.row_dst ? a.row_dst[p] : p;
       }
     }
     int v[V];
@@ -1275,6 +1275,110 @@ extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t 
   else hipLaunchKernelGGL(router_topk_kernel<16>, grid, blk, 0, s, g, g_dtype, ldg, (int)T, (int)E, k, renormalize,
                           tab, idx, w_bf16);
   return lsk::check_launch("router_topk_kernel");
+}
+
+// ---------------------------------------------------------------- the grouped expert linear alone
+// Tile table of expert-sorted rows from their offsets (one block): tiles[0] = number of kBM-row
+// tiles, then (expert, first row) per tile, experts ascending; first rows come from offs itself.
+__global__ __launch_bounds__(256) void grouped_tiles_kernel(const int32_t* __restrict__ offs, int E,
+                                                            int32_t* __restrict__ tiles) {
+  __shared__ int tmp[4];
+  const int per = (E + 255) / 256;
+  const int e0 = threadIdx.x * per;
+  int ntl = 0;
+  for (int e = e0; e < e0 + per && e < E; ++e) ntl += (max(offs[e + 1] - offs[e], 0) + kBM - 1) / kBM;
+  int total;
+  int tbase = block_excl_scan<256>(ntl, tmp, total);
+  for (int e = e0; e < e0 + per && e < E; ++e)
+    for (int r0 = offs[e]; r0 < offs[e + 1]; r0 += kBM, ++tbase) {
+      tiles[1 + 2 * tbase] = e;
+      tiles[2 + 2 * tbase] = r0;
+    }
+  if (threadIdx.x == 0) tiles[0] = total;
+}
+
+static int64_t grouped_max_tiles(int64_t R, int64_t E) { return R / kBM + (E < R ? E : R); }
+
+extern "C" int64_t lsk_grouped_gemm_workspace(int64_t R, int64_t E) {
+  return up256((1 + 2 * grouped_max_tiles(R, E)) * 4);
+}
+
+// Shared checks and the tile table of the two grouped entry points.
+static int grouped_setup(const char* who, const void* a, const float* asc, const int32_t* offs, int64_t E, int64_t R,
+                         const int64_t* w_ptrs, const int64_t* ws_ptrs, int64_t N, int64_t K, const void* out,
+                         void* workspace, int64_t workspace_bytes, hipStream_t s) {
+  LSK_REQUIRE(R >= 0 && N > 0 && K > 0 && E >= 1 && E <= 1024, "%s: bad sizes R=%lld N=%lld K=%lld E=%lld", who,
+              (long long)R, (long long)N, (long long)K, (long long)E);
+  LSK_REQUIRE(K <= 133144, "%s: K above the int32-exact bound", who);
+  LSK_REQUIRE(R <= 0x7fffffff && N <= 0x7fffffff, "%s: sizes beyond 31 bits", who);
+  if (R == 0) return LSK_OK;
+  LSK_REQUIRE(a && asc && offs && w_ptrs && ws_ptrs && out, "%s: null pointer", who);
+  LSK_REQUIRE(workspace && workspace_bytes >= lsk_grouped_gemm_workspace(R, E) && ((uintptr_t)workspace & 255) == 0,
+              "%s: workspace of %lld bytes (256-byte aligned) needed", who, (long long)lsk_grouped_gemm_workspace(R, E));
+  hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(256), 0, s, offs, (int)E, (int32_t*)workspace);
+  return lsk::check_launch("grouped_tiles_kernel");
+}
+
+extern "C" int lsk_grouped_gemm_w8a8(const int8_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E,
+                                     int64_t R, const int64_t* w_ptrs, int64_t ldw, const int64_t* ws_ptrs,
+                                     const int64_t* b_ptrs, int64_t N, int64_t K, uint16_t* out, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  int rc = grouped_setup("lsk_grouped_gemm_w8a8", a, asc, offs, E, R, w_ptrs, ws_ptrs, N, K, out, workspace,
+                         workspace_bytes, s);
+  if (rc || R == 0) return rc;
+  LSK_REQUIRE(lda >= K && lda % 16 == 0 && ldw >= K && ldw % 16 == 0 && N * ldw < 0x7fffffff &&
+                  R * lda < 0x7fffffff,
+              "lsk_grouped_gemm_w8a8: row strides must cover K and be multiples of 16 (31-bit buffer offsets)");
+  MoeGemmArgs g{};
+  g.A = a;
+  g.lda = lda;
+  g.a_bytes = R * lda;
+  g.w_bytes = N * ldw;
+  g.a_scale = asc;
+  g.offs = offs;
+  g.tiles = (const int32_t*)workspace;
+  g.w_ptrs = w_ptrs;
+  g.ldw = ldw;
+  g.ws_ptrs = ws_ptrs;
+  g.b_ptrs = b_ptrs;
+  g.K = (int)K;
+  g.N = (int)N;
+  g.y = out;  // row_w / row_dst null: weight 1, row p of the output
+  const int64_t mt = grouped_max_tiles(R, E);
+  if (R >= E * kBM) return launch_moe_pp<1>(g, mt, s, "moe_pp_kernel<grouped>");
+  return launch_moe_gemm<1>(g, mt, (int)((N + 127) / 128), s, "moe_gemm_kernel<grouped>");
+}
+
+extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E,
+                                   int64_t R, const int64_t* w_ptrs, int64_t ldw, const int64_t* kx_ptrs, int64_t lds,
+                                   const int64_t* b_ptrs, int64_t N, int64_t K, int safe, uint16_t* out,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  int rc = grouped_setup("lsk_grouped_gemm_mx", a, asc, offs, E, R, w_ptrs, kx_ptrs, N, K, out, workspace,
+                         workspace_bytes, s);
+  if (rc || R == 0) return rc;
+  LSK_REQUIRE(K % 32 == 0 && lda >= K && lda % 8 == 0 && ldw >= K / 2 && ldw % 16 == 0 && lds >= K / 32 &&
+                  N * ldw < 0x7fffffff && R * lda * 2 < 0x7fffffff,
+              "lsk_grouped_gemm_mx: K %% 32 == 0; row strides must cover K (bf16 rows, multiples of 8), K/2 (code "
+              "bytes, multiples of 16) and K/32 (31-bit buffer offsets)");
+  MoeGemmArgs g{};
+  g.A = a;
+  g.lda = lda;
+  g.a_bytes = R * lda * 2;
+  g.w_bytes = N * ldw;
+  g.a_scale = asc;
+  g.offs = offs;
+  g.tiles = (const int32_t*)workspace;
+  g.w_ptrs = w_ptrs;
+  g.ldw = ldw;
+  g.ws_ptrs = kx_ptrs;
+  g.lds = lds;
+  g.b_ptrs = b_ptrs;
+  g.K = (int)K;
+  g.N = (int)N;
+  g.y = out;
+  return lsk::launch_moe_mx_gemm(1, g, grouped_max_tiles(R, E), safe, s);
 }
 
 extern "C" int lsk_moe_select(int variant) {

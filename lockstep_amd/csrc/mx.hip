@@ -310,7 +310,7 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
         const int n0 = nt * 128 + wn * 64 + c4;
         if (p < p1 && n0 < a.N) {
           const float asc = a.a_scale ? a.a_scale[p] : 1.0f;
-          const float wt = a.row_w[p];
+          const float wt = a.row_w ? a.row_w[p] : 1.0f;  // none: a plain grouped linear
           uint16_t ob[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
@@ -322,7 +322,7 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
               ob[t] = f32_to_bf16(f32_mul(wt, yv));
             }
           }
-          uint16_t* dst = a.y + (int64_t)a.row_dst[p] * a.N + n0;
+          uint16_t* dst = a.y + (int64_t)(a.row_dst ? a.row_dst[p] : p) * a.N + n0;
           if (n0 + 4 <= a.N) {
             *(uint2*)dst = make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
           } else {
@@ -663,8 +663,8 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
     if (rowok) {
       asc = a.a_scale ? a.a_scale[MODE == 0 ? a.row_tok[p] : p] : 1.0f;
       if (MODE == 1) {
-        wt = a.row_w[p];
-        dst = a.row_dst[p];
+        wt = a.row_w ? a.row_w[p] : 1.0f;
+        dst = a.row_dst ? a.row_dst[p] : p;
       }
     }
     if (rb == p0) {

@@ -381,6 +381,56 @@ def expert_tables_mx(experts) -> ExpertTablesMX:
     return hit
 
 
+# ============================================================================ one grouped expert linear
+def _grouped_common(tables, which, a, asc, offs, what):
+    if which not in ("w13", "w2"):
+        raise ValueError("%s: which must be 'w13' or 'w2'" % what)
+    L.require_cuda(a, asc, offs, what=what)
+    if offs.dtype != torch.int32 or offs.dim() != 1 or offs.numel() != tables.E + 1:
+        raise ValueError("%s: offs must be int32 [E + 1] = [%d]" % (what, tables.E + 1))
+    R = a.shape[0]
+    N = 2 * tables.I if which == "w13" else tables.H
+    out = torch.empty((R, N), dtype=BF, device=a.device)
+    nbytes = L.load().lsk_grouped_gemm_workspace(R, tables.E)
+    work = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=a.device)
+    return R, N, out, work, nbytes
+
+
+def grouped_linear(tables, which: str, a8, asc, offs):
+    """One projection of every expert over rows already sorted by expert (expert e owns rows
+    offs[e] .. offs[e + 1] - 1): per expert lin_epilogue(_b)(int_mm(a8[rows], w_col_e), ws_e, asc[rows]
+    [, b_e]) -- the per-expert linears of expert_block (moe_ref.py:189-200, :40-55, :164-169) as one
+    grouped launch, bf16 out [R, N].  tables: ExpertTables; which: 'w13' (N = 2I, K = H) or 'w2'
+    (N = H, K = I); a8 int8 [R, K]; asc f32 [R]; offs int32 [E + 1] on the device."""
+    tables = expert_tables(tables)
+    R, N, out, work, nbytes = _grouped_common(tables, which, a8, asc, offs, "grouped_linear")
+    w, ws, b = (tables.w13, tables.ws13, tables.b13) if which == "w13" else (tables.w2, tables.ws2, tables.b2)
+    ldw = tables.ldw13 if which == "w13" else tables.ldw2
+    a8 = a8 if a8.stride(-1) == 1 else a8.contiguous()
+    asc = asc.to(F32).contiguous()
+    L.call("lsk_grouped_gemm_w8a8", L.ptr(a8), a8.stride(0) if R > 1 else a8.shape[1], L.ptr(asc), L.ptr(offs),
+           tables.E, R, L.ptr(w), ldw, L.ptr(ws), L.ptr(b), N, a8.shape[1], L.ptr(out), L.ptr(work), nbytes,
+           L.stream_of(a8))
+    return out
+
+
+def grouped_linear_mx(tables, which: str, a8, asc, offs):
+    """The MXFP4 form (moe_ref.py:243-261 per expert, as expert_block_mx :264-271 runs them):
+    lin_epilogue_mx(int_mm_mx(a8[rows], m2_e, kexp_e), asc[rows][, b_e]) over expert-sorted rows.
+    a8: the int8 row values [R, K] (int8, or held as bf16 as the MX kernels read them)."""
+    tables = expert_tables_mx(tables)
+    R, N, out, work, nbytes = _grouped_common(tables, which, a8, asc, offs, "grouped_linear_mx")
+    ab = a8 if a8.dtype == BF else a8.to(BF)        # int8 values are exact in bf16
+    ab = ab if ab.stride(-1) == 1 else ab.contiguous()
+    w, kx, b = (tables.w13, tables.ws13, tables.b13) if which == "w13" else (tables.w2, tables.ws2, tables.b2)
+    ldw, lds = (tables.ldw13, tables.lds13) if which == "w13" else (tables.ldw2, tables.lds2)
+    asc = asc.to(F32).contiguous()
+    L.call("lsk_grouped_gemm_mx", L.ptr(ab), ab.stride(0) if R > 1 else ab.shape[1], L.ptr(asc), L.ptr(offs),
+           tables.E, R, L.ptr(w), ldw, L.ptr(kx), lds, L.ptr(b), N, ab.shape[1], tables.mx_safe, L.ptr(out),
+           L.ptr(work), nbytes, L.stream_of(ab))
+    return out
+
+
 def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1):
     what = "moe_forward_mx2" if wfmt == 2 else "moe_forward_mx"
     L.require_cuda(x, idx, w, what=what)
