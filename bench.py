@@ -336,8 +336,55 @@ def decode_section(torch, args):
                                          "gemv_us": round(ms_k * 1e3, 2), "gemv_GB/s": round(gbs_k, 1),
                                          "gemv_frac_hbm": round(gbs_k / PEAK_HBM_GBS, 4)}
         del Ws
+    # the single contract GEMM of the CPU-runnable case: M=16 rows of the Qwen2.5-7B o_proj shape
+    # (N = K = 3584), x N(0,1) from seed 0, int8 weights, per-channel scales, bf16 out
+    x, W8, ws = WL.dense_inputs(16, 3584, 3584, seed=0)
+    xd, wsd = torch.from_numpy(x).to(dev), torch.from_numpy(ws).to(dev)
+    W0 = torch.from_numpy(W8).to(dev)
+    N, K, M = 3584, 3584, 16
+    Ws = [W0.clone() for _ in range(int((768 << 20) // (N * K)) + 1)]
+    q, asc = ops.rowquant(xd)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    full = [(lambda W=W: FS.w8a8_matmul(xd, W, wsd, out_dtype=torch.bfloat16)) for W in Ws]
+    gemv = [(lambda W=W: ops.gemm(q, W, L.EPI_V21, L.LSK_BF16, asc=asc, ws=wsd, out=out)) for W in Ws]
+    ms, ms_k = _graph_time(torch, full, 8), _graph_time(torch, gemv, 8)
+    nbytes = N * K + 4 * N + 4 * M * K + 2 * M * N
+    res["qwen25_7b_o_M16_seed0"] = {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                    "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                    "gemv_us": round(ms_k * 1e3, 2),
+                                    "gemv_frac_hbm": round(nbytes / (ms_k * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    del Ws
     res["note"] = ("us / GB/s: one w8a8_matmul call (row quant + GEMV kernels); gemv_*: the GEMV kernel alone on "
                    "pre-quantised rows; both from HIP-graph replays over > 768 MB of weight copies")
+    return res
+
+
+def ceiling_section(torch, args):
+    """The part's int8 MFMA ceiling (lsk_mfma_probe: register-only v_mfma_i32_32x32x32_i8, 8 waves per
+    SIMD) on all-zero, constant and uniformly random int8 operands: what the power budget leaves the
+    GEMM kernels on the contract's random operands."""
+    from lockstep_amd import _lib as L
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(23)
+    blocks, iters = 2048, 2000
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    nops = 1 << 16
+    cases = {"zero": torch.zeros(nops * 16, dtype=torch.int8, device=dev),
+             "constant_0x55": torch.full((nops * 16,), 0x55, dtype=torch.int8, device=dev),
+             "uniform_random": torch.randint(-127, 128, (nops * 16,), generator=g, device=dev, dtype=torch.int8)}
+    ops_launch = blocks * 4 * iters * 16 * 65536
+    res = {}
+    for name, buf in cases.items():
+        fn = lambda: L.call("lsk_mfma_probe", L.ptr(buf), nops, blocks, iters, L.ptr(sink), L.stream_of(buf))  # noqa
+        for _ in range(3):
+            fn()
+        ms = _events_time(torch, fn, 5)
+        res[name] = {"TOPS": round(ops_launch / (ms * 1e-3) / 1e12, 1), "ms": round(ms, 3)}
+        log("bench: MFMA ceiling, %s operands: %.0f TOPS" % (name, res[name]["TOPS"]))
+    res["note"] = ("register-only int8 MFMA loop, 2048 x 256 threads, 65536 ops per v_mfma_i32_32x32x32_i8; "
+                   "HIP events")
     return res
 
 
@@ -609,8 +656,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--sections", default="block,dense,decode,moe,grouped",
-                    help="comma list of block (the headline), dense, decode, moe, grouped, vendor, copy; the JSON line's "
+    ap.add_argument("--sections", default="block,dense,decode,moe,grouped,ceiling",
+                    help="comma list of block (the headline), dense, decode, moe, grouped, ceiling, vendor, copy; the "
+                         "JSON line's "
                          "value is the block step when block runs, else the dense step")
     ap.add_argument("--block-rows", type=int, default=8192, help="prefill rows T of the block step (8192 or 2048)")
     ap.add_argument("--moe-cases", default="", help="comma list of MoE cases to run, e.g. gpt_oss_20b_mxfp4_T4096 "
@@ -675,6 +723,8 @@ def main():
                         "roofline": d["roofline"]})
     if "copy" in sections:
         out["copy"] = copy_section(torch, args)
+    if "ceiling" in sections:
+        out["mfma_ceiling"] = ceiling_section(torch, args)
     if "vendor" in sections:
         out["vendor"] = vendor_section(torch, args)
     if "decode" in sections:

@@ -464,6 +464,22 @@ int lsk_moe_select(int variant);
  * speed differs.  Process-wide, not thread-safe against concurrent launches. */
 int lsk_moe_mx_select(int variant);
 
+/* ---------------------------------------------------------------- diagnostics */
+
+/* The part's int8 MFMA ceiling, no counterpart in the reference: `blocks` x 256 threads each run
+ * iters x 16 v_mfma_i32_32x32x32_i8 on operands read once from ops (nops 16-byte values, reused
+ * modulo nops), registers only, and write one checksum each to sink [blocks * 256].  Timed by the
+ * caller; 65536 int8 ops per MFMA.  Constant versus uniformly random operands shows the power cost
+ * of toggling operands. */
+int lsk_mfma_probe(const void* ops, int64_t nops, int64_t blocks, int iters, int32_t* sink, void* stream);
+
+/* The fast epilogues' bf16 conversion check, no counterpart in the reference: over the binary32
+ * patterns start .. start + count - 1 (start + count <= 2^32) that are not NaN, gfx950's packed
+ * v_cvt_pk_bf16_f32 against the round-to-nearest-even bit method torch's .to(bfloat16) uses; adds
+ * the number of disagreements to *mismatches and lowers *first to the smallest disagreeing pattern
+ * (initialise them to 0 and 0xFFFFFFFF). */
+int lsk_bf16_cvt_check(uint64_t start, uint64_t count, uint32_t* mismatches, uint32_t* first, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,8 @@ SIGNATURES = {
     "lsk_grouped_gemm_mx": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I, _P, _P, _I64,
                                  _P]),
     "lsk_moe_select": (_I, [_I]),
+    "lsk_mfma_probe": (_I, [_P, _I64, _I64, _I, _P, _P]),
+    "lsk_bf16_cvt_check": (_I, [ctypes.c_uint64, ctypes.c_uint64, _P, _P, _P]),
     "lsk_moe_mx_select": (_I, [_I]),
 }
 

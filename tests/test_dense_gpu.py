@@ -381,3 +381,17 @@ def test_rowquant_near_half_integer_quotients(dtype, K):
     rq, rasc = C.rowquant(x)
     assert np.array_equal(bits(asc), f32_bits(rasc))
     assert np.array_equal(bits(q), rq)
+
+
+def test_bf16_conversion_instruction_equals_rne_on_every_binary32():
+    """The fast bf16 epilogues use gfx950's packed conversion instruction: it must give the round-
+    to-nearest-even bits (torch's .to(bfloat16)) for every one of the 2^32 binary32 patterns that
+    is not a NaN, both halves of the pair, denormals included."""
+    from lockstep_amd import _lib as L
+    mism = torch.zeros(1, dtype=torch.int32, device=dev())
+    first = torch.full((1,), -1, dtype=torch.int32, device=dev())    # 0xFFFFFFFF
+    s = L.stream_of(mism)
+    for c in range(4):
+        L.call("lsk_bf16_cvt_check", c << 30, 1 << 30, L.ptr(mism), L.ptr(first), s)
+    torch.cuda.synchronize()
+    assert int(mism.item()) == 0, "%d patterns differ, first 0x%08x" % (int(mism.item()), int(first.item()) & 0xffffffff)
