@@ -224,7 +224,7 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * pieces straight into registers / whole rows through LDS; 16 / 17: four-wave 256x256 / 256x128,
  * one wave per SIMD with 128x128 / 128x64 wave tiles; 18: ping-pong 256x128 with 128-byte K stages
  * in a three-stage ring, the shape's default) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
- * Process-wide, not thread-safe against concurrent launches. */
+ * The choice applies to the calling host thread's later launches only (thread-local). */
 int lsk_gemm_select(int tile_id);
 
 /* Power-of-two int8 quantisation of ref_block_v1 (reference/ref_block_v1.py:56-72,122-130).
@@ -451,17 +451,18 @@ int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const 
  * rows per expert at a time; taken only for int8 experts without rotation, T <= 64 and
  * H, I <= 4096, the tiles otherwise), on the 128x256 tile with the four-wave main loop (3: one wave
  * per SIMD per block, 64x128 wave tiles), or chosen by size (-1, the default: the GEMV where it
- * applies, ping-pong once the routed rows reach E x 128).  MXFP4 experts (H, I <= 8192, no
+ * applies, the ping-pong tile once the routed rows reach 16 E).  MXFP4 experts (H, I <= 8192, no
  * rotation) take the MX GEMV under 2 for T <= 64 and by default for T <= 24 (T <= 16 with
  * block-scaled activations), the MX grouped tiles otherwise.  Results are identical for every
- * choice.  Process-wide. */
+ * choice.  4: the ping-pong tile with 128-byte K stages (one block per CU).  The choice applies to the calling
+ * host thread's later launches only (thread-local). */
 int lsk_moe_select(int variant);
 
 /* Tuning control with no counterpart in the reference: the main loop of the grouped MXFP4
  * expert GEMMs (0: direct-to-LDS operand staging with fp4 fragments converted per wave, a
  * two-stage ring, three blocks per CU, the default; 1: register-staged operands converted to bf16
  * before LDS; 2: as 0 with a three-stage ring and two blocks per CU).  Results are identical; only
- * speed differs.  Process-wide, not thread-safe against concurrent launches. */
+ * speed differs.  The choice applies to the calling host thread's later launches only (thread-local). */
 int lsk_moe_mx_select(int variant);
 
 /* ---------------------------------------------------------------- diagnostics */

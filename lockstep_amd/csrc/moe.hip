@@ -13,6 +13,8 @@
 //   5. grouped down GEMM, v2.1 epilogue (+ bias), times the routing weight, bf16 into a
 //      token-major slot r = rank of the expert among the token's experts;
 //   6. combine: per token, binary32 adds of its slots in ascending expert order from +0.
+#include <atomic>
+
 #include "contract_act.h"
 #include "mfma_tile.h"
 #include "moe_internal.h"
@@ -24,9 +26,9 @@ namespace {
 constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
 constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
 constexpr int kBM = lsk::kMoeBM;
-int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV,
+thread_local int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV,
                        // 3 the 128x256 tile on the four-wave main loop
-int g_moe_w4 = 0;      // the 128x256 tile's main loop: 0 eight-wave ping-pong, 1 four waves
+thread_local int g_moe_w4 = 0;      // the 128x256 tile's main loop: 0 eight-wave ping-pong, 1 four waves
 
 // ---------------------------------------------------------------- router
 LSK_DEV long long wave_max_ll(long long v) {
@@ -393,10 +395,16 @@ __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restric
   const int c0 = blockIdx.x;
   for (int e = threadIdx.x; e < E; e += 256) {
     int all = 0, before = 0;
-    for (int c = 0; c < nchunks; ++c) {
-      const int v = ccnt[(int64_t)c * E + e];
-      all += v;
-      before += c < c0 ? v : 0;
+    // the chunks' counts eight at a time, their loads issued together (one latency per eight)
+    for (int cb = 0; cb < nchunks; cb += 8) {
+      int v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = cb + j < nchunks ? ccnt[(int64_t)(cb + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        all += v[j];
+        before += cb + j < c0 ? v[j] : 0;
+      }
     }
     tot[e] = all;
     pre[e] = before;
@@ -572,8 +580,11 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
 // The epilogue operands of the tile (row scales, routing weights and slots, column scales and
 // biases) are loaded before the main loop and parked in LDS after it.
 using PPM = lsk::PPCfg<128, 256, 2, 4, 3>;
+using PPM128 = lsk::PPCfg<128, 256, 2, 4, 3, 128>;  // 128-byte K stages, one block per CU
 using W4M = lsk::W4Cfg<128, 256, 3>;
 static_assert(PPM::kSmemBytes - PPM::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
+static_assert(PPM128::kSmemBytes - PPM128::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
+static_assert(PPM128::kSmemBytes <= 160 * 1024, "one block per CU");
 static_assert(W4M::kSmemBytes - W4M::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
 static_assert(2 * W4M::kSmemBytes <= 160 * 1024 && 2 * PPM::kSmemBytes <= 160 * 1024, "two blocks per CU");
 
@@ -790,6 +801,16 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
                          const PPM::RowsB& pb, int K, char* sm) {
                         lsk::pp_mainloop<128, 256, 2, 4, 3>(acc, ra, pa, rb, pb, K, sm);
                       });
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void moe_pp128_kernel(MoeGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_moe[];
+  moe_tile<PPM128, MODE>(a, smem_moe,
+                         [](PPM128::Acc& acc, __amdgpu_buffer_rsrc_t ra, const PPM128::RowsA& pa,
+                            __amdgpu_buffer_rsrc_t rb, const PPM128::RowsB& pb, int K, char* sm) {
+                           lsk::pp_mainloop<128, 256, 2, 4, 3, 128>(acc, ra, pa, rb, pb, K, sm);
+                         });
 }
 
 template <int MODE>
@@ -1187,8 +1208,21 @@ int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const
   const int64_t blocks = max_tiles * ntiles;
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  if (g_moe_w4 == 2) {
+    static std::atomic<bool> attr_128{false};
+    if (!attr_128) {
+      if (hipFuncSetAttribute((const void*)moe_pp128_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              PPM128::kSmemBytes) != hipSuccess) {
+        lsk::set_error("%s: cannot reserve %d bytes of LDS", name, PPM128::kSmemBytes);
+        return LSK_ERR_HIP;
+      }
+      attr_128 = true;
+    }
+    hipLaunchKernelGGL(moe_pp128_kernel<MODE>, dim3((unsigned)blocks), dim3(512), PPM128::kSmemBytes, s, ga);
+    return lsk::check_launch(name);
+  }
   if (g_moe_w4) {
-    static bool attr_w4 = false;
+    static std::atomic<bool> attr_w4{false};
     if (!attr_w4) {
       if (hipFuncSetAttribute((const void*)moe_w4_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
                               W4M::kSmemBytes) != hipSuccess) {
@@ -1200,7 +1234,7 @@ int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const
     hipLaunchKernelGGL(moe_w4_kernel<MODE>, dim3((unsigned)blocks), dim3(256), W4M::kSmemBytes, s, ga);
     return lsk::check_launch(name);
   }
-  static bool attr_set = false;
+  static std::atomic<bool> attr_set{false};
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)moe_pp_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
                             PPM::kSmemBytes) != hipSuccess) {
@@ -1346,7 +1380,7 @@ extern "C" int lsk_grouped_gemm_w8a8(const int8_t* a, int64_t lda, const float* 
   g.N = (int)N;
   g.y = out;  // row_w / row_dst null: weight 1, row p of the output
   const int64_t mt = grouped_max_tiles(R, E);
-  if (R >= E * kBM) return launch_moe_pp<1>(g, mt, s, "moe_pp_kernel<grouped>");
+  if (R >= 16 * E) return launch_moe_pp<1>(g, mt, s, "moe_pp_kernel<grouped>");
   return launch_moe_gemm<1>(g, mt, (int)((N + 127) / 128), s, "moe_gemm_kernel<grouped>");
 }
 
@@ -1382,9 +1416,9 @@ extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* 
 }
 
 extern "C" int lsk_moe_select(int variant) {
-  LSK_REQUIRE(variant >= -1 && variant <= 3, "lsk_moe_select: variant %d not in [-1, 3]", variant);
-  g_moe_force = variant;
-  g_moe_w4 = variant == 3 ? 1 : 0;
+  LSK_REQUIRE(variant >= -1 && variant <= 4, "lsk_moe_select: variant %d not in [-1, 4]", variant);
+  g_moe_force = variant == 4 ? 1 : variant;
+  g_moe_w4 = variant == 3 ? 1 : (variant == 4 ? 2 : 0);
   return LSK_OK;
 }
 
@@ -1439,9 +1473,10 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
               "lsk_moe_forward: workspace of %lld bytes (256-byte aligned) needed", (long long)w.bytes);
   hipStream_t s = (hipStream_t)stream;
   const int64_t R = T * k;
-  // the ping-pong grouped GEMM once experts average a full 128-row tile or more; the 128x128
-  // register-staged tile below that (decode-sized token counts)
-  const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= (int64_t)E * kBM;
+  // the ping-pong grouped GEMM once experts average 16 routed rows (Qwen3-30B-A3B on MI355X: 256
+  // tokens, 16 rows per expert, 187 us against 225 us on the 128x128 register-staged tile, level at
+  // 2048 tokens); the register-staged tile below that
+  const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= 16 * E;
   // the grouped GEMV for decode token counts (whole weight rows streamed once per tile)
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
   const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096;
@@ -1476,7 +1511,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   if (rc) return rc;
   // dispatch (and the zeroing of the per-row |h| maxima, which the gate/up GEMM raises); the
   // routes of a 256-token chunk are staged in LDS (up to 92 KB at E = 1024, k = 32)
-  static bool dispatch_lds = false;
+  static std::atomic<bool> dispatch_lds{false};
   if (!dispatch_lds) {
     for (const void* f : {(const void*)moe_dispatch_small_kernel, (const void*)moe_count_kernel,
                           (const void*)moe_place_kernel, (const void*)moe_decode_prep_kernel})

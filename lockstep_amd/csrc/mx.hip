@@ -1,5 +1,7 @@
 // MXFP4 kernels on gfx950: the MX-operand GEMM (dense and grouped for the MoE layer), the exact
 // E2M1/E8M0 dequant, and the doubled-mantissa packer.  See mx_tile.h for the exactness argument.
+#include <atomic>
+
 #include "contract_act.h"
 #include "moe_internal.h"
 #include "mx_pp.h"
@@ -496,7 +498,7 @@ unsigned grid_for(int64_t n) {
   return (unsigned)(b > 8192 ? 8192 : (b < 1 ? 1 : b));
 }
 
-int g_mx_variant = 0;  // grouped MX main loop: 0 direct-to-LDS, two-stage ring, three blocks per CU (mx_pp.h);
+thread_local int g_mx_variant = 0;  // grouped MX main loop: 0 direct-to-LDS, two-stage ring, three blocks per CU (mx_pp.h);
                        // 1 register-staged (mx_tile.h); 2 direct-to-LDS, three-stage ring, two blocks per CU
 
 template <int MODE, bool SAFE>
@@ -506,7 +508,7 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "moe_mx_gemm_kernel: grid too large");
   if (ga.mx2 == 2) {
-    static bool attr_rs = false;
+    static std::atomic<bool> attr_rs{false};
     auto kern = moe_mx_gemm_kernel<MODE, true, true>;
     if (!attr_rs) {
       if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "moe_mx_gemm_kernel")) return rc;
@@ -517,7 +519,7 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
                                        : "moe_mx_gemm_kernel<down, block exponents>");
   }
   if (g_mx_variant == 1) {
-    static bool attr = false;
+    static std::atomic<bool> attr{false};
     auto kern = moe_mx_gemm_kernel<MODE, SAFE, false>;
     if (!attr) {
       if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "moe_mx_gemm_kernel")) return rc;
@@ -528,7 +530,7 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
   }
   static_assert(lsk::MxPPCfg<2>::kRingBytes >= Cfg::kEpiBytes, "the epilogue strips fit in the ring");
   if (g_mx_variant == 0) {
-    static bool attr_pp2 = false;
+    static std::atomic<bool> attr_pp2{false};
     auto kern = moe_mx_pp_kernel<MODE, SAFE, 2>;
     if (!attr_pp2) {
       if (int rc = reserve_lds(kern, lsk::MxPPCfg<2>::kRingBytes, "moe_mx_pp_kernel")) return rc;
@@ -537,7 +539,7 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lsk::MxPPCfg<2>::kRingBytes, s, ga);
     return lsk::check_launch(MODE == 0 ? "moe_mx_pp_kernel<gate_up>" : "moe_mx_pp_kernel<down>");
   }
-  static bool attr_pp = false;
+  static std::atomic<bool> attr_pp{false};
   auto kern = moe_mx_pp_kernel<MODE, SAFE, 3>;
   if (!attr_pp) {
     if (int rc = reserve_lds(kern, lsk::MxPPCfg<3>::kRingBytes, "moe_mx_pp_kernel")) return rc;
@@ -551,7 +553,7 @@ template <bool B_FP4, bool SAFE, bool ROWSCALE>
 int launch_dense(const int8_t* a, int64_t lda, const int32_t* ka, int64_t ldka, const uint8_t* b, int64_t ldb,
                  const uint8_t* kexp, int64_t lds, int M, int N, int K, int epi, const float* asc, const float* bias,
                  float* out, int64_t ldo, hipStream_t s) {
-  static bool attr = false;
+  static std::atomic<bool> attr{false};
   auto kern = mx_gemm_kernel<B_FP4, SAFE, ROWSCALE>;
   if (!attr) {
     if (int rc = reserve_lds(kern, Cfg::kSmemBytes, "mx_gemm_kernel")) return rc;
@@ -777,7 +779,7 @@ int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu
   constexpr int kRows = MODE == 0 ? 2 : 1;
   constexpr int V = MR * RPW * kRows;
   constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH * 4 + (MX2 ? MR * 64 * NCH * 4 : 0));
-  static bool attr = false;
+  static std::atomic<bool> attr{false};
   auto kern = moe_mx_gemv_kernel<MODE, MR, NCH, RPW, SAFE, MX2>;
   if (!attr) {
     if (int rc = reserve_lds(kern, smem, name)) return rc;

@@ -248,8 +248,23 @@ __global__ __launch_bounds__(256) void quant_pow2_rows_kernel(const float* __res
 // share of the tensor.  The maximum is exact in any order, so the grid shape does not matter.
 constexpr int kDynBlocks = 2048;
 
-// Contiguous tensors ([M, K] with ldx == K) are walked as one flat array of float4s, eight
-// elements per thread-step in pass 2; other strides go row by row.
+// Contiguous tensors ([M, K] with ldx == K) are walked as one flat array of float4s, each block
+// a contiguous run of them (eight 4 KB block-wide loads in flight per step, non-temporal: the
+// tensor is read twice, once per pass, and nothing else should be evicted for it); other strides
+// go row by row.
+constexpr int kDynUnroll = 8;
+
+LSK_DEV float4 ld_nt(const float4* p) {
+  const v4f v = __builtin_nontemporal_load((const v4f*)p);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+LSK_DEV void block_run(int64_t n, int64_t& b0, int64_t& b1) {
+  const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+  b0 = (int64_t)blockIdx.x * per;
+  b1 = b0 + per < n ? b0 + per : n;
+}
+
 __global__ __launch_bounds__(256) void dyn_amax_kernel(const float* __restrict__ x, int64_t M, int64_t K,
                                                        int64_t ldx, int flat, float* __restrict__ partial) {
   __shared__ float red[4];
@@ -257,21 +272,23 @@ __global__ __launch_bounds__(256) void dyn_amax_kernel(const float* __restrict__
   if (flat) {
     const int64_t n4 = (M * K) >> 2;
     const float4* x4 = (const float4*)x;
-    const int64_t stride = (int64_t)gridDim.x * 256;
-    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    for (; i + 3 * stride < n4; i += 4 * stride) {
-      const float4 a = x4[i], b = x4[i + stride], c = x4[i + 2 * stride], d = x4[i + 3 * stride];
-      am = fmaxf(am, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                           fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
-      am = fmaxf(am, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
-                           fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
+    int64_t b0, b1;
+    block_run(n4, b0, b1);
+    int64_t i = b0 + threadIdx.x;
+    for (; i + 256 * (kDynUnroll - 1) < b1; i += 256 * kDynUnroll) {
+      float4 v[kDynUnroll];
+#pragma unroll
+      for (int u = 0; u < kDynUnroll; ++u) v[u] = ld_nt(x4 + i + 256 * u);
+#pragma unroll
+      for (int u = 0; u < kDynUnroll; ++u)
+        am = fmaxf(am, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
     }
-    for (; i < n4; i += stride) {
-      const float4 a = x4[i];
-      am = fmaxf(am, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+    for (; i < b1; i += 256) {
+      const float4 v = ld_nt(x4 + i);
+      am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
-    for (int64_t j = (n4 << 2) + (int64_t)blockIdx.x * 256 + threadIdx.x; j < M * K; j += stride)
-      am = fmaxf(am, fabsf(x[j]));
+    if (blockIdx.x == gridDim.x - 1)
+      for (int64_t j = (n4 << 2) + threadIdx.x; j < M * K; j += 256) am = fmaxf(am, fabsf(x[j]));
   } else {
     for (int64_t r = blockIdx.x; r < M; r += gridDim.x)
       for (int64_t c = threadIdx.x; c < K; c += 256) am = fmaxf(am, fabsf(x[r * ldx + c]));
@@ -300,14 +317,30 @@ __global__ __launch_bounds__(256) void dyn_quant_kernel(const float* __restrict_
   if (erow)
     for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < M; r += stride) erow[r] = e;
   if (flat) {
+    // pairs of float4 (eight elements, one 8-byte store of q), each block a contiguous run
     const int64_t n8 = (M * K) >> 3;
     const float4* x4 = (const float4*)x;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
-      const float4 a = x4[2 * i], b = x4[2 * i + 1];
+    int64_t b0, b1;
+    block_run(n8, b0, b1);
+    int64_t i = b0 + threadIdx.x;
+    constexpr int U = kDynUnroll / 2;
+    for (; i + 256 * (U - 1) < b1; i += 256 * U) {
+      float4 v[U][2];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        v[u][0] = ld_nt(x4 + 2 * (i + 256 * u));
+        v[u][1] = ld_nt(x4 + 2 * (i + 256 * u) + 1);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        *(v2u32*)(q + 8 * (i + 256 * u)) = v2u32{quant_pow2_x4(v[u][0], sc), quant_pow2_x4(v[u][1], sc)};
+    }
+    for (; i < b1; i += 256) {
+      const float4 a = ld_nt(x4 + 2 * i), b = ld_nt(x4 + 2 * i + 1);
       *(v2u32*)(q + 8 * i) = v2u32{quant_pow2_x4(a, sc), quant_pow2_x4(b, sc)};
     }
-    for (int64_t j = (n8 << 3) + (int64_t)blockIdx.x * 256 + threadIdx.x; j < M * K; j += stride)
-      q[j] = quant_pow2_one(x[j], sc);
+    if (blockIdx.x == gridDim.x - 1)
+      for (int64_t j = (n8 << 3) + threadIdx.x; j < M * K; j += 256) q[j] = quant_pow2_one(x[j], sc);
   } else {
     for (int64_t r = blockIdx.x; r < M; r += gridDim.x)
       for (int64_t c = threadIdx.x; c < K; c += 256) q[r * ldq + c] = quant_pow2_one(x[r * ldx + c], sc);

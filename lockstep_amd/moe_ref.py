@@ -174,7 +174,7 @@ class ExpertTables:
         self.E = len(experts)
         self.H = int(ex0[0].shape[0])
         self.I = int(ex0[0].shape[1]) // 2
-        keep = []
+        keep, pairs = [], []
         w13, ws13, w2, ws2, b13, b2 = [], [], [], [], [], []
         for ex in experts:
             W13 = ops.weight_nk(ex[0])
@@ -188,6 +188,8 @@ class ExpertTables:
             c13 = ex[4].to(F32).contiguous() if len(ex) > 4 and ex[4] is not None else None
             c2 = ex[5].to(F32).contiguous() if len(ex) > 5 and ex[5] is not None else None
             keep += [W13, W2, s13, s2, c13, c2]
+            pairs += [(ex[1], s13), (ex[3], s2)] + ([(ex[4], c13)] if c13 is not None else []) + \
+                     ([(ex[5], c2)] if c2 is not None else [])
             w13.append(W13)
             w2.append(W2)
             ws13.append(s13.data_ptr())
@@ -215,22 +217,38 @@ class ExpertTables:
         self.b13 = table(b13) if any(b13) else None
         self.b2 = table(b2) if any(b2) else None
         self._keep = keep
+        pairs += [(ex[0], t) for ex, t in zip(experts, w13)] + [(ex[2], t) for ex, t in zip(experts, w2)]
+        self._derived = _derived(pairs)
+
+
+def _derived(pairs):
+    """(source, version) of every source tensor a table reads through a copy: an in-place update of
+    such a source makes the table stale; sources used in place need no check."""
+    return [(src, src._version) for src, used in pairs if used.data_ptr() != src.data_ptr()]
 
 
 _TABLES = {}
 
 
+def _cached(kind, experts, build):
+    """The cached tables of an experts list: keyed by the list and its per-expert tuples (cheap: one
+    id per expert), valid while every source read through a copy keeps its version."""
+    key = (kind, id(experts), tuple(map(id, experts)))
+    hit = _TABLES.get(key)
+    if hit is not None and hit._src is experts and all(t._version == v for t, v in hit._derived):
+        return hit
+    if len(_TABLES) >= 8 and key not in _TABLES:
+        _TABLES.pop(next(iter(_TABLES)))
+    hit = _TABLES[key] = build(experts)
+    hit._src = experts
+    return hit
+
+
 def expert_tables(experts) -> ExpertTables:
-    """Cached ExpertTables for an experts list (keyed by every tensor's address and version)."""
+    """Cached ExpertTables for an experts list."""
     if isinstance(experts, ExpertTables):
         return experts
-    key = (id(experts),) + tuple((t.data_ptr(), t._version) for ex in experts for t in ex if t is not None)
-    hit = _TABLES.get(key)
-    if hit is None:
-        if len(_TABLES) >= 8:
-            _TABLES.pop(next(iter(_TABLES)))
-        hit = _TABLES[key] = ExpertTables(experts)
-    return hit
+    return _cached("int8", experts, ExpertTables)
 
 
 def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_out=None):
@@ -327,9 +345,8 @@ class ExpertTablesMX:
         L.require_cuda(first, what="experts")
         self.device = first.device
         self.E = len(experts)
-        keep = []
+        keep, pairs = [], []
         p13, s13, p2, s2, b13, b2 = [], [], [], [], [], []
-        safe = False
         kw = []
         for ex in experts:
             (m13, k13), (m2_, k2_) = ex[0], ex[1]
@@ -346,17 +363,19 @@ class ExpertTablesMX:
             s2.append(e2.data_ptr())
             b13.append(bb13.data_ptr() if bb13 is not None else 0)
             b2.append(bb2.data_ptr() if bb2 is not None else 0)
-            safe = safe or bool((e13.max() >= 240).item()) or bool((e2.max() >= 240).item())
+            pairs += [(m13, c13), (m2_, c2), (k13, e13), (k2_, e2)] + \
+                     ([(ex[2], bb13)] if bb13 is not None else []) + ([(ex[3], bb2)] if bb2 is not None else [])
             kw.append(torch.stack([e13.min(), e13.max(), e2.min(), e2.max()]).to(torch.int32))
         two_i, hh = keep[0].shape
         self.I = int(two_i) // 2
         self.H = int(hh) * 2
         self.ldw13, self.ldw2 = int(keep[0].stride(0)), int(keep[1].stride(0))
         self.lds13, self.lds2 = int(keep[2].stride(0)), int(keep[3].stride(0))
-        self.mx_safe = 1 if safe else 0
-        # E8M0 bounds over all experts (w13 min / max, w2 min / max): block-scaled activations use them
+        # E8M0 bounds over all experts (w13 min / max, w2 min / max), one host synchronisation: the
+        # multiply-then-add update once an exponent reaches 240; block-scaled activations use them all
         kr = torch.stack(kw).cpu()
         self.kw_bounds = (int(kr[:, 0].min()), int(kr[:, 1].max()), int(kr[:, 2].min()), int(kr[:, 3].max()))
+        self.mx_safe = 1 if max(self.kw_bounds[1], self.kw_bounds[3]) >= 240 else 0
         dev = self.device
 
         def table(vals):
@@ -365,20 +384,13 @@ class ExpertTablesMX:
         self.b13 = table(b13) if any(b13) else None
         self.b2 = table(b2) if any(b2) else None
         self._keep = keep
+        self._derived = _derived(pairs)
 
 
 def expert_tables_mx(experts) -> ExpertTablesMX:
     if isinstance(experts, ExpertTablesMX):
         return experts
-    key = ("mx", id(experts)) + tuple((t.data_ptr(), t._version) for ex in experts
-                                      for part in ex if part is not None
-                                      for t in (part if isinstance(part, tuple) else (part,)))
-    hit = _TABLES.get(key)
-    if hit is None:
-        if len(_TABLES) >= 8:
-            _TABLES.pop(next(iter(_TABLES)))
-        hit = _TABLES[key] = ExpertTablesMX(experts)
-    return hit
+    return _cached("mx", experts, ExpertTablesMX)
 
 
 # ============================================================================ one grouped expert linear

@@ -193,10 +193,11 @@ def test_moe_multi_chunk_dispatch(T, E, k):
     _run_case(T, E, k, 128, 64, seed=11 + T)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
 def test_moe_grouped_gemm_variants(variant):
     """Every grouped-GEMM kernel (register-staged 128x128 tile, ping-pong 128x256 tile, the
-    decode GEMV, the 128x256 tile on four waves) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
+    decode GEMV, the 128x256 tile on four waves, the ping-pong tile with 128-byte K stages) gives
+    the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
     their rows eight at a time), empty experts, a bias and SwiGLU-OAI."""
     from lockstep_amd import _lib as L
     L.call("lsk_moe_select", variant)
