@@ -214,33 +214,48 @@ def test_config1_o_proj_m16_bit_exact():
     assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, None, "bf16"))
 
 
+@pytest.mark.parametrize("seed", [1, 3, 4])
 @pytest.mark.parametrize("M", [1, 8, 32])
 @pytest.mark.parametrize("which", ["gate_up", "down"])
-def test_config2_decode_bit_exact(M, which):
+def test_config2_decode_bit_exact(M, which, seed):
     from lockstep_amd import lockstep_fullstack as FS
     from lockstep_amd import workloads as WL
     N, K = WL.LLAMA8B[which]
-    say("config2 decode", which, M, N, K)
-    x, W8, ws = WL.dense_inputs(M, N, K, seed=1, outliers=True)
+    say("config2 decode", which, M, N, K, "seed", seed)
+    x, W8, ws = WL.dense_inputs(M, N, K, seed=seed, outliers=True)
     y = FS.w8a8_matmul(to_dev(x), to_dev(W8), to_dev(ws), out_dtype=torch.bfloat16)
     assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, None, "bf16"))
 
 
+@pytest.mark.parametrize("seed", [2, 4])
 @pytest.mark.parametrize("which", ["gate_up", "down"])
-def test_config2_prefill_rows_and_chunk_invariance(which):
-    """M=2048: a seeded subset of rows against the oracle, and the whole result equal to the
-    same rows computed in 64-row chunks (row independence: per-token scales, exact sums)."""
+def test_config2_prefill_rows_and_chunk_invariance(which, seed):
+    """M=2048: a seeded subset of rows against the oracle; for every row the quantised rows
+    against the oracle's quantiser, the int32 accumulator's column and row sums against exact
+    integer identities, the fused v2.1 epilogue against the separate epilogue over that
+    accumulator, and the whole result equal to the same rows computed in 64-row chunks (row
+    independence: per-token scales, exact sums)."""
+    from lockstep_amd import _lib as L
     from lockstep_amd import lockstep_fullstack as FS
+    from lockstep_amd import ops
     from lockstep_amd import workloads as WL
     N, K = WL.LLAMA8B[which]
     M = 2048
-    say("config2 prefill", which, M, N, K)
-    x, W8, ws = WL.dense_inputs(M, N, K, seed=2, outliers=True)
+    say("config2 prefill", which, M, N, K, "seed", seed)
+    x, W8, ws = WL.dense_inputs(M, N, K, seed=seed, outliers=True)
     xd, Wd, wsd = to_dev(x), to_dev(W8), to_dev(ws)
     y = FS.w8a8_matmul(xd, Wd, wsd, out_dtype=torch.bfloat16)
-    rows = np.sort(_rng(3).choice(M, 24, replace=False))
+    rows = np.sort(_rng(3 + seed).choice(M, 24, replace=False))
     ref = C.w8a8_matmul(x[rows], W8, ws, None, "bf16")
     assert np.array_equal(bits(y)[rows], ref)
+    q, asc = ops.rowquant(xd)
+    q_ref, asc_ref = C.rowquant(x)
+    assert np.array_equal(bits(q), q_ref) and np.array_equal(bits(asc), f32_bits(asc_ref))
+    acc = ops.gemm(q, Wd, L.EPI_RAW, L.LSK_I32)
+    assert np.array_equal(acc.sum(0, dtype=torch.int64).cpu().numpy(), W8.astype(np.int64) @ q_ref.sum(0, dtype=np.int64))
+    assert np.array_equal(acc.sum(1, dtype=torch.int64).cpu().numpy(), q_ref.astype(np.int64) @ W8.sum(0, dtype=np.int64))
+    y2 = ops.epilogue(acc, L.EPI_V21, L.LSK_BF16, asc=asc, ws=wsd)
+    assert torch.equal(y2.view(torch.int16), y.view(torch.int16))
     chunks = torch.cat([FS.w8a8_matmul(xd[i:i + 64], Wd, wsd, out_dtype=torch.bfloat16) for i in range(0, M, 64)])
     assert torch.equal(chunks.view(torch.int16), y.view(torch.int16))
 
