@@ -173,33 +173,36 @@ __device__ __forceinline__ void pp_strip_store_fast(int i, const int32_t* region
 
 // Fast epilogue of a whole tile under the POW2 order (ref_block_v1.py:167,193,198,218) with
 // binary32 output and no column exponents: y = fl32(acc) * fl32(2^-(shift + erow[m])), one
-// factor per row (the row exponent sits in the tile's row-operand slot), two 8-byte buffer
-// stores per four columns.
+// factor per row (the row exponent sits in the tile's row-operand slot).  Stored straight from
+// the accumulators, no LDS staging: register r of lane l of a 32 x 32 block holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32, so each 4-byte store instruction writes 32
+// consecutive binary32 values (128 bytes) of two rows.  (On MI355X at the Qwen2.5-7B gate/up
+// shape, 8192 x 37888 x 3584, this is 3-4% faster than staging 32-row strips through LDS for
+// 8-byte stores.)
 template <class C>
-__device__ __forceinline__ void pp_strip_store_fast_pow2(int i, const int32_t* region, __amdgpu_buffer_rsrc_t ro,
-                                                         int ldo_bytes, int shift, const char* smem) {
+__device__ __forceinline__ void pp_epilogue_direct_pow2(const typename C::Acc& acc, __amdgpu_buffer_rsrc_t ro,
+                                                        int ldo_bytes, int shift, const char* smem) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int wm = wave / C::kWN, wn = wave % C::kWN;
   const float* sc_row = (const float*)(smem + C::kScaleOff);
-  constexpr int kQuads = C::WTN / 4;
-  constexpr int kRowStep = 64 / kQuads;
-  const int c4 = lane % kQuads, r0 = lane / kQuads;
-  const int nl = wn * C::WTN + c4 * 4;
-  const int ml0 = wm * C::WTM + i * 32 + r0;
-  const uint32_t off = (uint32_t)(ml0 * ldo_bytes + nl * 4);
+  const int colb = (wn * C::WTN + (lane & 31)) * 4;
 #pragma unroll
-  for (int t = 0; t < 32 / kRowStep; ++t) {
-    const v4i v = *(const v4i*)(region + (r0 + kRowStep * t) * C::kLdc + c4 * 4);
-    const float sc = pow2_descale(shift + __float_as_int(sc_row[ml0 + kRowStep * t]));
-    float y[4];
+  for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) y[k] = f32_mul((float)v[k], sc);
-    const v2u32 u0 = {__float_as_uint(y[0]), __float_as_uint(y[1])};
-    const v2u32 u1 = {__float_as_uint(y[2]), __float_as_uint(y[3])};
-    __builtin_amdgcn_raw_buffer_store_b64(u0, ro, off, kRowStep * t * ldo_bytes, 0);
-    __asm__ volatile("" ::: "memory");  // keeps the two 8-byte stores from being merged into one
-    __builtin_amdgcn_raw_buffer_store_b64(u1, ro, off + 8, kRowStep * t * ldo_bytes, 0);
-  }
+    for (int g = 0; g < 4; ++g) {
+      // rows row0 .. row0 + 3 of this lane (registers 4 g .. 4 g + 3 of each block)
+      const int row0 = wm * C::WTM + i * 32 + 8 * g + 4 * (lane >> 5);
+      const v4f e4 = *(const v4f*)(sc_row + row0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float sc = pow2_descale(shift + __float_as_int(e4[q]));
+        const uint32_t off = (uint32_t)((row0 + q) * ldo_bytes + colb);
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(f32_mul((float)acc[i][j][4 * g + q], sc)), ro,
+                                                off + j * 128, 0, 0);
+      }
+    }
 }
 
 template <class C, int I>
@@ -210,17 +213,6 @@ __device__ __forceinline__ void pp_epilogue_fast(const typename C::Acc& acc, __a
     lsk::pp_stage_strip<C::TN, C::kLdc>(acc[I], region);
     pp_strip_store_fast<C>(I, region, ro, ldo_bytes, smem);
     pp_epilogue_fast<C, I + 1>(acc, ro, ldo_bytes, smem);
-  }
-}
-
-template <class C, int I>
-__device__ __forceinline__ void pp_epilogue_fast_pow2(const typename C::Acc& acc, __amdgpu_buffer_rsrc_t ro,
-                                                      int ldo_bytes, int shift, char* smem) {
-  if constexpr (I < C::TM) {
-    int32_t* region = (int32_t*)(smem + wave_id() * C::kStripBytes);
-    lsk::pp_stage_strip<C::TN, C::kLdc>(acc[I], region);
-    pp_strip_store_fast_pow2<C>(I, region, ro, ldo_bytes, shift, smem);
-    pp_epilogue_fast_pow2<C, I + 1>(acc, ro, ldo_bytes, shift, smem);
   }
 }
 
@@ -336,7 +328,7 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
     const int ldo_bytes = (int)(ep.ldo * 4);
     char* base = (char*)ep.out + ((int64_t)m0 * ep.ldo + n0) * 4;
     const __amdgpu_buffer_rsrc_t ro = lsk::make_rsrc(base, (int64_t)(BM - 1) * ldo_bytes + BN * 4);
-    pp_epilogue_fast_pow2<C, 0>(acc, ro, ldo_bytes, ep.shift, smem_pp);
+    pp_epilogue_direct_pow2<C>(acc, ro, ldo_bytes, ep.shift, smem_pp);
     return;
   }
 #define LSK_PP_EPI(O, D, B)                                                        \

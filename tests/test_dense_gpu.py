@@ -203,6 +203,38 @@ def test_pow2_quant_and_gemm_parity():
     assert np.array_equal(RB._e_from_max(em), C._e_from_max(em))
 
 
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 12, 13, 16, 17, 18])
+def test_pow2_whole_tile_epilogue_exponent_range(tile):
+    """The POW2 epilogue of whole ping-pong / four-wave tiles (binary32 out, per-row exponents,
+    stored straight from the accumulators) over the whole exponent range: shift + erow from -140
+    (factor 2^140 overflows: inf, NaN for a zero sum) through 0 to 126 .. 149 (subnormal factors,
+    exact) and 150, 200 (factor 0)."""
+    import lockstep_amd._lib as L
+    from lockstep_amd import ops
+    M, N, K, shift = 512, 512, 192, 7
+    say("pow2 range", tile, M, N, K)
+    r = _rng(900 + tile)
+    a = r.integers(-127, 128, (M, K), dtype=np.int8)
+    w = r.integers(-127, 128, (N, K), dtype=np.int8)
+    a[5] = 0  # a zero row under every factor
+    picks = np.array([-147, -135, -134, -100, -7, 0, 3, 30, 119, 120, 126, 130, 142, 143, 150, 193], np.int32)
+    erow = r.choice(picks, M).astype(np.int32)
+    erow[:len(picks)] = picks
+    erow[5] = -147
+    L.call("lsk_gemm_select", tile)
+    try:
+        y = ops.gemm(to_dev(a), to_dev(w), L.EPI_POW2, L.LSK_F32, erow=to_dev(erow), shift=shift)
+        got = bits(y)
+    finally:
+        L.call("lsk_gemm_select", -1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.dequant_pow2(C.int_mm(a, w.T), erow[:, None].astype(np.int64) + shift)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got.view(F32)), nan)
+    assert np.array_equal(got[~nan], f32_bits(ref)[~nan])
+    assert nan[5].all() and np.isinf(ref[0]).any() and (ref[np.where(erow + shift > 149)[0]] == 0).all()
+
+
 # ------------------------------------------------------------------ the dense configurations
 def test_config1_o_proj_m16_bit_exact():
     """M=16 tokens, K=N=3584: x N(0,1) seed 0 quantised by the contract quantiser, W8 uniform

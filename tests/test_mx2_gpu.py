@@ -226,22 +226,40 @@ def test_moe_mx2_every_row_general():
 @pytest.mark.parametrize("T", [1, 32])
 @pytest.mark.parametrize("path", ["gemv", "tiled"])
 def test_moe_mx2_gpt_oss_shapes(T, path):
-    """Decode sizes through the grouped GEMV (the default) and through the tiled kernels."""
+    """Decode sizes through the grouped GEMV (forced at T = 32, past the default's 16-token switch)
+    and through the tiled kernels.  K = 2880 (90 blocks): the GEMV's two-chunk form."""
     from lockstep_amd import workloads as WL
     c = WL.GPT_OSS_20B
     x, oexp, idx, w, oact, got, dexp = _mx2_layer(T, c["E"], c["k"], c["H"], c["I"], seed=80 + T, bias=True,
-                                                  moe_force=-1 if path == "gemv" else 0)
+                                                  moe_force=2 if path == "gemv" else 0)
     assert np.array_equal(got, C.moe_forward_mx2(x, oexp, idx, w, oact))
 
 
 @pytest.mark.parametrize("act", ["silu", "swigluoai"])
 def test_moe_mx2_gemv_extreme_exponents(act):
-    """The decode GEMV (T <= 64) on tiny rows (block exponents near -126), E8M0 bytes <= 10 and
-    >= 240 (products 2^(ka + k - 128) underflowing to subnormals and zero, and large ones), a
-    partial column chunk and K of 11 / 7 blocks."""
+    """The decode GEMV (forced at T = 48) on tiny rows (block exponents near -126), E8M0 bytes <= 10
+    and >= 240 (products 2^(ka + k - 128) underflowing to subnormals and zero, and large ones), with
+    K of 11 / 7 blocks (one-chunk form, four rows per pass)."""
     x, oexp, idx, w, oact, got, dexp = _mx2_layer(48, 4, 2, 352, 224, seed=91, tiny_rows=0.15, low_exp=True,
-                                                  big_exp=True, act=act)
+                                                  big_exp=True, act=act, moe_force=2)
     assert _flagged_tokens(x, dexp).any()
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx2(x, oexp, idx, w, oact)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("T", [2, 8, 16])
+@pytest.mark.parametrize("H,I", [(352, 224), (4160, 128)])
+def test_moe_mx2_gemv_token_counts(T, H, I):
+    """The decode GEMV at the token counts the default routes to it (T <= 16): T = 2 takes two rows
+    per pass, T = 8 and 16 four (the per-row block exponents sa[m * kB + b] of every row of a pass).
+    H = 352 (11 blocks) keeps the gate/up in the one-chunk form; H = 4160 (130 blocks, above 128)
+    takes the four-chunk form with one row per pass, and I = 128 (4 blocks) the down projection's
+    one-chunk form.  Tiny rows and extreme E8M0 bytes put the block products 2^(ka + k - 128) near
+    both ends of the binary32 range.  (Every MX row count is a multiple of 32, so a GEMV column
+    chunk of 8 or 16 columns is always whole.)"""
+    x, oexp, idx, w, oact, got, dexp = _mx2_layer(T, 4, 2, H, I, seed=100 + T + H, tiny_rows=0.3, low_exp=True,
+                                                  big_exp=True, moe_force=-1)
     with np.errstate(over="ignore", invalid="ignore"):
         ref = C.moe_forward_mx2(x, oexp, idx, w, oact)
     assert np.array_equal(got, ref)
