@@ -442,16 +442,25 @@ __global__ __launch_bounds__(1024) void gemv_i8_stream_kernel(const int8_t* __re
   }
   __syncthreads();
   if (wave != 0) return;
-  for (int w2 = 1; w2 < KW; ++w2)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] += red_gemv[((w2 - 1) * MT + t) * 64 + lane];
   const int n = n0 + col;
+  const EpiCol ec = n < N ? epi_col_load(ep, n) : EpiCol{};
+  EpiRow er[MT][4];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = t * 16 + kg * 4 + r;
-      if (m < M && n < N) epilogue_store(ep, m, n, acc[t][r]);
+      er[t][r] = m < M ? epi_row_load(ep, m) : EpiRow{};
+    }
+  for (int w2 = 1; w2 < KW; ++w2)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] += red_gemv[((w2 - 1) * MT + t) * 64 + lane];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + kg * 4 + r;
+      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], er[t][r], ec);
     }
 }
 
@@ -569,16 +578,25 @@ __global__ __launch_bounds__(1024) void gemv_i8_lds_kernel(const int8_t* __restr
   }
   __syncthreads();
   if (wave != 0) return;
-  for (int w2 = 1; w2 < NW; ++w2)
-#pragma unroll
-    for (int t = 0; t < MT; ++t) acc[t] += red[((w2 - 1) * MT + t) * 64 + lane];
   const int n = n0 + rr;
+  const EpiCol ec = n < N ? epi_col_load(ep, n) : EpiCol{};
+  EpiRow er[MT][4];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = t * 16 + 4 * (lane >> 4) + r;
-      if (m < M && n < N) epilogue_store(ep, m, n, acc[t][r]);
+      er[t][r] = m < M ? epi_row_load(ep, m) : EpiRow{};
+    }
+  for (int w2 = 1; w2 < NW; ++w2)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] += red[((w2 - 1) * MT + t) * 64 + lane];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + 4 * (lane >> 4) + r;
+      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], er[t][r], ec);
     }
 }
 

@@ -94,6 +94,40 @@ LSK_DEV float rint_div8(float v, float s, float r) {
   return t;
 }
 
+// The contract's per-row int8 quant of one element: clamp(rint(fl32(x / asc)), -127, 127) with
+// r = fl32(1 / asc); asc = fl32(max(amax, kAmaxFloor) / 127) over the row.
+constexpr float kAmaxFloor = 0x1.5798eep-27f;  // binary32 nearest 1e-8 (torch clamp(min=1e-8))
+
+LSK_DEV int8_t quant_one(float v, float s, float r) {
+  float t = rint_div8(v, s, r);
+  t = fminf(fmaxf(t, -127.0f), 127.0f);
+  return (int8_t)(int)t;
+}
+
+// Load 8 consecutive elements of dtype DT (16-byte aligned) as binary32.
+template <int DT>
+LSK_DEV void load8_as_f32(const void* x, int64_t i8, float* v) {
+  if (DT == LSK_F32) {
+    const float4* p = (const float4*)x + 2 * i8;
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 u = ((const uint4*)x)[i8];
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (DT == LSK_BF16) {
+        v[2 * j] = bf16_to_f32((uint16_t)(w[j] & 0xffff));
+        v[2 * j + 1] = bf16_to_f32((uint16_t)(w[j] >> 16));
+      } else {
+        v[2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffff));
+        v[2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
+      }
+    }
+  }
+}
+
 // Load one activation element of the given dtype as binary32 (bf16 and f16 widen exactly).
 LSK_DEV float load_as_f32(const void* p, int dtype, int64_t i) {
   switch (dtype) {
@@ -285,6 +319,42 @@ LSK_DEV void epilogue_store_ops(const EpiParams& p, int64_t m, int64_t n, int32_
     return;
   }
   store_out(p.out, p.out_dtype, off, epi_value_pre(p.order, p.out_dtype, p.bias != nullptr, acc, o.row, o.ws, o.b, o.sh));
+}
+
+// The operands of output row m and of output column n, loaded apart so a kernel that owns a
+// block of rows and columns loads each once, all ahead of its first store (loads after a store
+// to memory the compiler cannot prove distinct would each wait a round trip): the row operand
+// (asc[m]; POW2: shift + erow[m]) and the column operands (ws[n], bias[n] or 0; POW2: ecol[n]).
+struct EpiRow {
+  float row;
+  int sh;
+};
+struct EpiCol {
+  float ws, b;
+  int sh;
+};
+
+LSK_DEV EpiRow epi_row_load(const EpiParams& p, int64_t m) {
+  EpiRow r{0.0f, 0};
+  if (p.order == LSK_EPI_V21 || p.order == LSK_EPI_V2) r.row = p.asc[m];
+  else if (p.order == LSK_EPI_POW2) r.sh = p.shift + (p.erow ? p.erow[m] : 0);
+  return r;
+}
+
+LSK_DEV EpiCol epi_col_load(const EpiParams& p, int64_t n) {
+  EpiCol c{0.0f, 0.0f, 0};
+  if (p.order == LSK_EPI_V21 || p.order == LSK_EPI_V2) {
+    c.ws = p.ws[n];
+    if (p.bias) c.b = p.bias[n];
+  } else if (p.order == LSK_EPI_POW2) {
+    c.sh = p.ecol ? p.ecol[n] : 0;
+  }
+  return c;
+}
+
+LSK_DEV void epilogue_store_rc(const EpiParams& p, int64_t m, int64_t n, int32_t acc, const EpiRow& r,
+                               const EpiCol& c) {
+  epilogue_store_ops(p, m, n, acc, EpiOps{r.row, c.ws, c.b, r.sh + c.sh});
 }
 
 // Round four epilogue values to the output type and store them at element offset o with one

@@ -4,8 +4,6 @@
 
 namespace {
 
-constexpr float kAmaxFloor = 0x1.5798eep-27f;  // binary32 nearest 1e-8 (torch clamp(min=1e-8))
-
 // Block-wide max of non-negative floats; every thread gets the result.
 template <int THREADS>
 LSK_DEV float block_max(float v, float* red) {
@@ -17,12 +15,6 @@ LSK_DEV float block_max(float v, float* red) {
   for (int w = 1; w < THREADS / 64; ++w) r = fmaxf(r, red[w]);
   __syncthreads();
   return r;
-}
-
-LSK_DEV int8_t quant_one(float v, float s, float r) {
-  float t = rint_div8(v, s, r);  // fl32(x / asc), then round half to even (r = fl32(1 / asc))
-  t = fminf(fmaxf(t, -127.0f), 127.0f);
-  return (int8_t)(int)t;
 }
 
 // One block per row.  Pass 1: amax over the row (exact, order-free).  Pass 2: quantise.
@@ -105,30 +97,6 @@ __global__ __launch_bounds__(THREADS) void rowquant_kernel(const void* __restric
   }
 }
 
-// Load 8 consecutive elements of dtype DT (16-byte aligned) as binary32.
-template <int DT>
-LSK_DEV void load8(const void* x, int64_t i8, float* v) {
-  if (DT == LSK_F32) {
-    const float4* p = (const float4*)x + 2 * i8;
-    const float4 a = p[0], b = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  } else {
-    const uint4 u = ((const uint4*)x)[i8];
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (DT == LSK_BF16) {
-        v[2 * j] = bf16_to_f32((uint16_t)(w[j] & 0xffff));
-        v[2 * j + 1] = bf16_to_f32((uint16_t)(w[j] >> 16));
-      } else {
-        v[2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffff));
-        v[2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16));
-      }
-    }
-  }
-}
-
 // Single-pass row quant: one block per row, the row held in registers (NV chunks of 8
 // elements per thread, K <= 8 * NV * THREADS), so x is read from memory once.  Same
 // arithmetic as rowquant_kernel: exact amax, asc = fl32(max(amax, 1e-8) / 127), q = clamp(rint(x / asc)).
@@ -147,7 +115,7 @@ __global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __res
   for (int j = 0; j < NV; ++j) {
     const int64_t c = tid + (int64_t)j * THREADS;
     if (c < K8) {
-      load8<DT>(row, c, v[j]);
+      load8_as_f32<DT>(row, c, v[j]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(v[j][e]));
     }

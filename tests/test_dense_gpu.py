@@ -203,6 +203,46 @@ def test_pow2_quant_and_gemm_parity():
     assert np.array_equal(RB._e_from_max(em), C._e_from_max(em))
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("N,K", [(1000, 4096), (77, 2880), (300, 1040), (520, 14336), (64, 16), (33, 32768)])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_decode_w8a8_rows(M, N, K, xdt):
+    """w8a8_matmul at M <= 4 (row quant, then the whole-row GEMV) against the oracle's rowquant +
+    int_mm + epilogue: V21 with and without bias and V2, bf16 and binary32 out, K up to 32768.  x
+    carries 20-sigma outliers, an exact amax of 127 in row 0 (asc = 1, so 2.5, -3.5, 0.5 and 126.5
+    are rounding ties) and, for M >= 2, an all-zero last row (the 1e-8 floor)."""
+    import lockstep_amd._lib as L
+    from lockstep_amd import ops
+    say("decode rows", M, N, K, xdt)
+    r = _rng(1000 * M + N + K)
+    x = (r.standard_normal((M, K)) * 2).astype(F32)
+    out_idx = r.random((M, K)) < 1e-3
+    x[out_idx] = np.sign(x[out_idx]) * 40.0
+    if K >= 8:
+        x[0, 1] = 127.0
+        x[0, 2:6] = [2.5, -3.5, 0.5, 126.5]
+    if M >= 2:
+        x[M - 1] = 0.0
+    if xdt == "bf16":
+        x = C.bf16_to_f32(C.bf16_bits(x))
+        xd = bf16_dev(x)
+    else:
+        xd = to_dev(x)
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    bias = (r.standard_normal(N) * 0.1).astype(F32)
+    q, asc = C.rowquant(x)
+    acc = C.int_mm(q, W8.T)
+    Wd, wsd, bd = to_dev(W8), to_dev(ws), to_dev(bias)
+    for order, b in ((L.EPI_V21, None), (L.EPI_V21, bias), (L.EPI_V2, bias)):
+        for odt, name in ((L.LSK_BF16, "bf16"), (L.LSK_F32, "f32")):
+            y = ops.w8a8_matmul(xd, Wd, wsd, None if b is None else bd, order, odt)
+            f = C.epilogue_v21 if order == L.EPI_V21 else C.epilogue_v2
+            ref = f(acc, ws, asc, b, name)
+            want = ref if name == "bf16" else f32_bits(ref)
+            assert np.array_equal(bits(y), want), (order, b is not None, name)
+
+
 @pytest.mark.parametrize("tile", [1, 2, 3, 4, 12, 13, 16, 17, 18])
 def test_pow2_whole_tile_epilogue_exponent_range(tile):
     """The POW2 epilogue of whole ping-pong / four-wave tiles (binary32 out, per-row exponents,
@@ -295,7 +335,7 @@ def test_config2_prefill_rows_and_chunk_invariance(which, seed):
 @pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 16, 17, 18])
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 257, 640), (512, 520, 2880), (64, 64, 16),
                                    (1, 1000, 14336), (3, 77, 2880), (4, 300, 1040), (8, 1000, 4096),
-                                   (17, 77, 2880), (32, 520, 14336), (5, 33, 48)])
+                                   (17, 77, 2880), (32, 520, 14336), (5, 33, 48), (24, 32800, 320)])
 def test_every_tile_config_is_exact(tile, M, N, K):
     """The forced tile configurations produce the same bits (exact integer sums, any tiling)."""
     from lockstep_amd import _lib as L
