@@ -227,6 +227,13 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * The choice applies to the calling host thread's later launches only (thread-local). */
 int lsk_gemm_select(int tile_id);
 
+/* Tuning control with no counterpart in the reference: the persistent form of the 256x256
+ * ping-pong kernel, taken for whole tiles under the POW2 epilogue with binary32 output (the
+ * ref_block_v1 GEMMs): 1 one block per compute unit (the default), 0 off (one tile per block),
+ * blocks > 1 that many blocks.  Results are identical for every choice; only speed differs.
+ * Thread-local, like lsk_gemm_select. */
+int lsk_gemm_persist(int blocks);
+
 /* Power-of-two int8 quantisation of ref_block_v1 (reference/ref_block_v1.py:56-72,122-130).
  * mode 0 = per tensor (quant8_dyn: one exponent e_out[0]); 1 = per row (quant8_rows: e_out[M]);
  * 2 = per column (quant8_cols: e_out[K]).  e = 6 - (biased_exp(m) - 127), minus 1 when

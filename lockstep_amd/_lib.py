@@ -53,6 +53,7 @@ SIGNATURES = {
                                _I64, _P, _P, _P]),
     "lsk_tree_sum": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lsk_gemm_select": (_I, [_I]),
+    "lsk_gemm_persist": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
     "lsk_quant8_dyn_workspace": (_I64, []),
     "lsk_quant8_dyn": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P]),

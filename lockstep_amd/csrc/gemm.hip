@@ -181,10 +181,9 @@ __device__ __forceinline__ void pp_strip_store_fast(int i, const int32_t* region
 // 8-byte stores.)
 template <class C>
 __device__ __forceinline__ void pp_epilogue_direct_pow2(const typename C::Acc& acc, __amdgpu_buffer_rsrc_t ro,
-                                                        int ldo_bytes, int shift, const char* smem) {
+                                                        int ldo_bytes, int shift, const float* sc_row) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int wm = wave / C::kWN, wn = wave % C::kWN;
-  const float* sc_row = (const float*)(smem + C::kScaleOff);
   const int colb = (wn * C::WTN + (lane & 31)) * 4;
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
@@ -328,7 +327,7 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
     const int ldo_bytes = (int)(ep.ldo * 4);
     char* base = (char*)ep.out + ((int64_t)m0 * ep.ldo + n0) * 4;
     const __amdgpu_buffer_rsrc_t ro = lsk::make_rsrc(base, (int64_t)(BM - 1) * ldo_bytes + BN * 4);
-    pp_epilogue_direct_pow2<C>(acc, ro, ldo_bytes, ep.shift, smem_pp);
+    pp_epilogue_direct_pow2<C>(acc, ro, ldo_bytes, ep.shift, (const float*)(smem_pp + C::kScaleOff));
     return;
   }
 #define LSK_PP_EPI(O, D, B)                                                        \
@@ -359,6 +358,84 @@ __global__ __launch_bounds__(512, (RING == 3 && BKB == 64 ? 2 : 1)) void gemm_i8
                       __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm) {
                      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra, pa, rb, pb, K_, sm);
                    });
+}
+
+// Persistent form of the ping-pong kernel for whole tiles under the POW2 order with binary32
+// output and no column exponents (the ref_block_v1 GEMMs, ref_block_v1.py:167,193,198,218): one
+// block per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ... in the one-tile-per-block
+// launch's order (hardware ids congruent mod 8 stay on one XCD).  After a tile's main loop the
+// block fills the whole ring with the next tile's first stages (no wave reads it any more) and
+// only then stores the finished tile from its accumulators: the next tile's first loads and the
+// block start leave the critical path, and the stores drain while the next tile's first three
+// stages are multiplied.  M % BM == 0, N % BN == 0, K % BKB == 0 with at least kRing + 2 stages.
+// (Measured on MI355X: the Qwen2.5-7B block GEMMs at 8192 rows 1.5% faster than one tile per
+// block.)
+template <int BM, int BN, int WM, int WN, int RING, int BKB>
+__global__ __launch_bounds__(512, 1) void gemm_i8_pp_pow2_persist_kernel(const int8_t* __restrict__ A, int lda,
+                                                                         const int8_t* __restrict__ W, int ldw, int M,
+                                                                         int N, int K, EpiParams ep) {
+  using C = lsk::PPCfg<BM, BN, WM, WN, RING, BKB>;
+  extern __shared__ __attribute__((aligned(16))) char smem_pp[];
+  const int mtiles = M / BM, ntiles = N / BN, tiles = mtiles * ntiles;
+  const int tid = threadIdx.x;
+  float* sc_row = (float*)(smem_pp + C::kScaleOff);
+  constexpr int GM = LSK_GROUP_M;
+  struct Tile {
+    int m0, n0;
+    __amdgpu_buffer_rsrc_t ra, rb;
+    typename C::RowsA pa;
+    typename C::RowsB pb;
+    float erow;
+  };
+  auto setup = [&](int v, Tile& t) {
+    const int L = lsk::xcd_logical_id(v, tiles);
+    const int group = L / (GM * ntiles);
+    const int first_m = group * GM;
+    const int gsize = (mtiles - first_m) < GM ? (mtiles - first_m) : GM;
+    const int r = L - group * GM * ntiles;
+    t.m0 = (first_m + r % gsize) * BM;
+    t.n0 = (r / gsize) * BN;
+    t.ra = lsk::make_rsrc(A + (int64_t)t.m0 * lda, (int64_t)BM * lda);
+    t.rb = lsk::make_rsrc(W + (int64_t)t.n0 * ldw, (int64_t)BN * ldw);
+#pragma unroll
+    for (int j = 0; j < C::kLA; ++j) {
+      int row, kb;
+      lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
+      t.pa[j] = (uint32_t)(row * lda);
+    }
+#pragma unroll
+    for (int j = 0; j < C::kLB; ++j) {
+      int row, kb;
+      lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
+      t.pb[j] = (uint32_t)(row * ldw);
+    }
+    t.erow = (tid < BM && ep.erow) ? __int_as_float(ep.erow[t.m0 + tid]) : 0.0f;
+  };
+  const int ldo_bytes = (int)(ep.ldo * 4);
+  Tile cur;
+  setup(blockIdx.x, cur);
+  for (int v = blockIdx.x, it = 0; v < tiles; v += gridDim.x, ++it) {
+    typename C::Acc acc;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
+    if (it == 0)
+      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, false>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp);
+    else
+      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, true>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp);
+    // every wave is past its last read of the ring; the previous tile's epilogue (the last
+    // reader of sc_row) ended before this tile's first barrier
+    if (tid < BM) sc_row[tid] = cur.erow;
+    const __amdgpu_buffer_rsrc_t ro =
+        lsk::make_rsrc((char*)ep.out + ((int64_t)cur.m0 * ep.ldo + cur.n0) * 4, (int64_t)(BM - 1) * ldo_bytes + BN * 4);
+    if (v + (int)gridDim.x < tiles) {
+      setup(v + gridDim.x, cur);
+      lsk::pp_issue_prologue<BM, BN, WM, WN, RING, BKB>(cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp);
+    }
+    __syncthreads();
+    pp_epilogue_direct_pow2<C>(acc, ro, ldo_bytes, ep.shift, sc_row);
+  }
 }
 
 // Dense four-wave tile kernel (256 threads, one wave per SIMD, 128-row wave tiles; w4_tile.h).
@@ -1006,6 +1083,22 @@ thread_local int g_row_rpw = 0;       // rows per wave of the whole-row GEMV (0:
 thread_local int g_gemv_variant = 0;  // M <= 4: 0 whole-row GEMV, 1 register double-buffered 8-row GEMV, 2 LDS-ring 8-row GEMV
 thread_local int g_gemv_mid = 0;      // 4 < M <= 32: 0 by shape, 1 direct 64-byte row pieces, 2 whole rows through LDS
 
+// the persistent POW2 kernel: 1 on (one block per CU), 0 off, > 1 that many blocks (tests)
+thread_local int g_pp_persist = 1;
+
+// Compute units of the current device (the persistent kernels' grid), cached per device.
+static int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 template <int BM, int BN, int WM, int WN>
 static int launch_tile(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K,
                        const EpiParams& ep, int vec_ok, hipStream_t s, const char* name) {
@@ -1047,6 +1140,26 @@ static int launch_pp(const int8_t* a, int lda, const int8_t* w, int ldw, int M, 
   // (the kernel's fast epilogue)
   const int64_t esz = (ep.out_dtype == LSK_BF16 || ep.out_dtype == LSK_F16) ? 2 : 4;
   const int vflag = (vec_ok && (int64_t)(BM - 1) * ep.ldo * esz + BN * esz < 0x7fffffff) ? 2 : vec_ok;
+  if constexpr (BM == 256 && BN == 256 && WM == 4 && WN == 2 && RING == 4 && BKB == 64) {
+    // whole tiles under POW2 with binary32 out: the persistent kernel, one block per CU
+    if (g_pp_persist != 0 && ep.order == LSK_EPI_POW2 && ep.ecol == nullptr && ep.out_dtype == LSK_F32 &&
+        vflag == 2 && M % BM == 0 && N % BN == 0 && K % BKB == 0 && K / BKB >= C::kRing + 2) {
+      auto pk = gemm_i8_pp_pow2_persist_kernel<BM, BN, WM, WN, RING, BKB>;
+      static std::atomic<bool> pattr{false};
+      if (!pattr) {
+        if (hipFuncSetAttribute((const void*)pk, hipFuncAttributeMaxDynamicSharedMemorySize, C::kSmemBytes) !=
+            hipSuccess) {
+          set_error("%s: cannot reserve %d bytes of LDS", name, C::kSmemBytes);
+          return LSK_ERR_HIP;
+        }
+        pattr = true;
+      }
+      int64_t grid = g_pp_persist > 1 ? g_pp_persist : cu_count();
+      grid = grid < tiles ? grid : tiles;
+      hipLaunchKernelGGL(pk, dim3((unsigned)grid), dim3(C::kThreads), C::kSmemBytes, s, a, lda, w, ldw, M, N, K, ep);
+      return check_launch(name);
+    }
+  }
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(C::kThreads), C::kSmemBytes, s, a, lda, w, ldw, M, N, K, ep,
                      vflag);
   return check_launch(name);
@@ -1345,6 +1458,12 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
   hipLaunchKernelGGL(epilogue_apply_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, acc, ldc, M,
                      N, ep);
   return lsk::check_launch("epilogue_apply_kernel");
+}
+
+extern "C" int lsk_gemm_persist(int blocks) {
+  LSK_REQUIRE(blocks >= 0 && blocks <= 65536, "lsk_gemm_persist: %d blocks", blocks);
+  lsk::g_pp_persist = blocks;
+  return LSK_OK;
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {

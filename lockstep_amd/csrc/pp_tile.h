@@ -97,7 +97,47 @@ LSK_DEV void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Issue this thread's direct-to-LDS loads of the first kRing stages of a tile into ring slots
+// 0 .. kRing-1, the whole ring (a persistent kernel's next tile, ahead of the current tile's
+// stores); chunks past K read zeros.
 template <int BM, int BN, int WM, int WN, int RING, int BKB = 64>
+LSK_DEV void pp_issue_prologue(__amdgpu_buffer_rsrc_t ra, const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsA& pa,
+                               __amdgpu_buffer_rsrc_t rb, const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb,
+                               int K, char* smem) {
+  using C = PPCfg<BM, BN, WM, WN, RING, BKB>;
+  const int tid = threadIdx.x, wave = wave_id();
+  const int nk = (K + C::kBK - 1) / C::kBK;
+#pragma unroll
+  for (int s = 0; s < C::kRing; ++s) {
+    if (s >= nk) break;
+    char* st = smem + s * C::kStage;
+    const int k0 = s * C::kBK;
+#pragma unroll
+    for (int j = 0; j < C::kLA; ++j) {
+      int r, kbyte;
+      pp_slot<C::kThreads, C::kChunks>(tid, j, r, kbyte);
+      const int kk = k0 + kbyte;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t)(st + (j * C::kThreads + wave * 64) * 16), 16,
+                                               kk < K ? pa[j] + (uint32_t)kk : kOob, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < C::kLB; ++j) {
+      int r, kbyte;
+      pp_slot<C::kThreads, C::kChunks>(tid, j, r, kbyte);
+      const int kk = k0 + kbyte;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t)(st + C::kStageA + (j * C::kThreads + wave * 64) * 16),
+                                               16, kk < K ? pb[j] + (uint32_t)kk : kOob, 0, 0, 0);
+    }
+  }
+}
+
+// PRE: the first kRing stages were issued by pp_issue_prologue before at least 63 more vector
+// memory instructions of this thread (the previous tile's stores).  Vector memory instructions
+// complete in issue order and at most 63 are outstanding, so those stages are complete: no wait
+// for them; the first step issues nothing (its stage kAhead is in the ring already) and the
+// first three steps (which wait for stages 1 .. 3) wait for nothing, leaving the stores to
+// drain while stages 0 .. 2 are multiplied.  Needs K / kBK >= kRing + 2 whole stages.
+template <int BM, int BN, int WM, int WN, int RING, int BKB = 64, bool PRE = false>
 LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __amdgpu_buffer_rsrc_t ra,
                          const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
                          const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb, int K, char* smem) {
@@ -184,10 +224,12 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __
   // like waiting for stage 0 alone).  A counted wait here could also count a caller's plain
   // loads that the compiler placed among these; inside the loop only ring loads are issued,
   // so the counted waits there are exact.
+  if constexpr (!PRE) {
 #pragma unroll
-  for (int s = 0; s < C::kAhead; ++s)
-    if (s < nk) issue(s, Chk{});
-  wait_vm<0>();
+    for (int s = 0; s < C::kAhead; ++s)
+      if (s < nk) issue(s, Chk{});
+    wait_vm<0>();
+  }
   phase_barrier();
   if (group == 1) phase_barrier();
 
@@ -197,6 +239,13 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __
     using WSteady = std::integral_constant<int, (C::kAhead - 1) * kPer>;
     const int nfull = K / C::kBK;
     int kt = 0;
+    if constexpr (PRE) {
+      using WNone = std::integral_constant<int, 63>;
+      step(0, WNone{}, false, NoChk{});
+      step(1, WNone{}, true, NoChk{});
+      step(2, WNone{}, true, NoChk{});
+      kt = 3;
+    }
     for (; kt + C::kAhead < nfull; ++kt) step(kt, WSteady{}, true, NoChk{});
     for (; kt + C::kAhead < nk; ++kt) step(kt, WSteady{}, true, Chk{});
     // drain: the last kAhead stages, nothing more to issue

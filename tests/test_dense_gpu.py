@@ -275,6 +275,38 @@ def test_pow2_whole_tile_epilogue_exponent_range(tile):
     assert nan[5].all() and np.isinf(ref[0]).any() and (ref[np.where(erow + shift > 149)[0]] == 0).all()
 
 
+@pytest.mark.parametrize("M,N,K", [(512, 512, 384), (2048, 1536, 640), (1024, 2304, 3584)])
+@pytest.mark.parametrize("blocks", [1, 3, 7])
+def test_pow2_persistent_kernel(M, N, K, blocks):
+    """The persistent POW2 kernel (whole 256 x 256 tiles, each block walking several tiles and
+    issuing the next tile's first stages before storing the current one): bits equal to the
+    one-tile-per-block launch and, on a row subset, to the oracle, with one block per CU (1) and
+    with 3 or 7 blocks (many tiles per block, uneven counts)."""
+    import lockstep_amd._lib as L
+    from lockstep_amd import ops
+    say("pow2 persistent", M, N, K, blocks)
+    r = _rng(M + N + K + blocks)
+    a = r.integers(-127, 128, (M, K), dtype=np.int8)
+    w = r.integers(-127, 128, (N, K), dtype=np.int8)
+    erow = r.integers(-20, 20, M).astype(np.int32)
+    erow[:4] = [-150, 150, 130, -130]
+    ad, wd, ed = to_dev(a), to_dev(w), to_dev(erow)
+    L.call("lsk_gemm_persist", blocks)
+    try:
+        y = bits(ops.gemm(ad, wd, L.EPI_POW2, L.LSK_F32, erow=ed, shift=5))
+        L.call("lsk_gemm_persist", 0)
+        y0 = bits(ops.gemm(ad, wd, L.EPI_POW2, L.LSK_F32, erow=ed, shift=5))
+    finally:
+        L.call("lsk_gemm_persist", 1)
+    assert np.array_equal(y, y0)
+    rows = np.sort(np.concatenate([[0, 1, 2, 3, M - 1], r.choice(M, 12, replace=False)]))
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.dequant_pow2(C.int_mm(a[rows], w.T), erow[rows, None].astype(np.int64) + 5)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(y[rows].view(F32)), nan)
+    assert np.array_equal(y[rows][~nan], f32_bits(ref)[~nan])
+
+
 # ------------------------------------------------------------------ the dense configurations
 def test_config1_o_proj_m16_bit_exact():
     """M=16 tokens, K=N=3584: x N(0,1) seed 0 quantised by the contract quantiser, W8 uniform
