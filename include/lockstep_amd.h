@@ -481,11 +481,12 @@ int lsk_moe_mx_select(int variant);
  * of toggling operands. */
 int lsk_mfma_probe(const void* ops, int64_t nops, int64_t blocks, int iters, int32_t* sink, void* stream);
 
-/* The fast epilogues' bf16 conversion check, no counterpart in the reference: over the binary32
- * patterns start .. start + count - 1 (start + count <= 2^32) that are not NaN, gfx950's packed
- * v_cvt_pk_bf16_f32 against the round-to-nearest-even bit method torch's .to(bfloat16) uses; adds
- * the number of disagreements to *mismatches and lowers *first to the smallest disagreeing pattern
- * (initialise them to 0 and 0xFFFFFFFF). */
+/* The library's bf16 conversion check, no counterpart in the reference: over the binary32
+ * patterns start .. start + count - 1 (start + count <= 2^32), gfx950's packed v_cvt_pk_bf16_f32
+ * (patterns that are not NaN) and the library's binary32 -> bf16 conversion (every pattern; the
+ * instruction with NaN mapped to 0x7FC0) against the round-to-nearest-even bit method torch's
+ * .to(bfloat16) uses; adds the number of disagreements to *mismatches and lowers *first to the
+ * smallest disagreeing pattern (initialise them to 0 and 0xFFFFFFFF). */
 int lsk_bf16_cvt_check(uint64_t start, uint64_t count, uint32_t* mismatches, uint32_t* first, void* stream);
 
 #ifdef __cplusplus

@@ -26,7 +26,9 @@ LSK_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x 
 
 // binary32 -> bf16, round to nearest even; every NaN becomes 0x7FC0 (the conversion torch's
 // c10::BFloat16 performs, which is what the reference's `.to(torch.bfloat16)` runs).
-LSK_DEV uint16_t f32_to_bf16(float f) {
+// binary32 -> bf16 by the round-to-nearest-even bit method torch uses, every NaN to 0x7FC0: the
+// definition the conversions below are checked against.
+LSK_DEV uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
   u += 0x7fffu + ((u >> 16) & 1u);
@@ -36,13 +38,21 @@ LSK_DEV uint16_t f32_to_bf16(float f) {
 LSK_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
 // Two binary32 values to packed bf16 (a in the low half) with gfx950's conversion instruction:
-// round to nearest even, denormals kept; equal to f32_to_bf16 for every binary32 that is not a
-// NaN (checked exhaustively over all 2^32 patterns on MI355X).  NaN inputs are the caller's to
-// exclude.
+// round to nearest even, denormals kept; equal to f32_to_bf16_bits for every binary32 that is
+// not a NaN (checked exhaustively over all 2^32 patterns on MI355X).  NaN inputs are the
+// caller's to exclude.
 typedef float v2f_t __attribute__((ext_vector_type(2)));
 typedef __bf16 v2bf16_t __attribute__((ext_vector_type(2)));
 LSK_DEV uint32_t pack_bf16x2_nonan(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f_t){a, b}, v2bf16_t));
+}
+
+// binary32 -> bf16, equal to f32_to_bf16_bits for every input (checked over all 2^32 patterns on
+// MI355X): the conversion instruction, with a NaN replaced by 0x7FC0 (three VALU instructions
+// against the bit method's six or seven).
+LSK_DEV uint16_t f32_to_bf16(float f) {
+  const uint16_t h = (uint16_t)pack_bf16x2_nonan(f, f);
+  return f != f ? (uint16_t)0x7fc0 : h;
 }
 
 // 16 bytes to global memory as two 8-byte stores.  On MI355X a 16-byte global / buffer store

@@ -35,20 +35,22 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(const v4i* __restrict__
   sink[t] = s;
 }
 
-// Every binary32 pattern start .. start + count - 1 that is not a NaN: gfx950's packed bf16
-// conversion (pack_bf16x2_nonan, both halves) against the round-to-nearest-even bit method
-// (f32_to_bf16).  Disagreements are counted (integer atomics) and the smallest such pattern kept.
+// Every binary32 pattern start .. start + count - 1: gfx950's packed bf16 conversion
+// (pack_bf16x2_nonan, both halves, patterns that are not NaN) and the library's f32_to_bf16 (every
+// pattern, NaN included) against the round-to-nearest-even bit method (f32_to_bf16_bits).
+// Disagreements are counted (integer atomics) and the smallest such pattern kept.
 __global__ __launch_bounds__(256) void bf16_cvt_check_kernel(uint64_t start, uint64_t count,
                                                              uint32_t* __restrict__ mismatches,
                                                              uint32_t* __restrict__ first) {
   uint32_t bad = 0, lo = 0xffffffffu;
   for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (uint64_t)gridDim.x * 256) {
     const uint32_t u = (uint32_t)(start + i);
-    if ((u & 0x7fffffffu) > 0x7f800000u) continue;  // NaN: excluded by the conversion's contract
     const float f = __uint_as_float(u), g = __uint_as_float(u ^ 0x80000000u);
-    const uint32_t hw = pack_bf16x2_nonan(f, g);
-    const uint32_t sw = (uint32_t)f32_to_bf16(f) | ((uint32_t)f32_to_bf16(g) << 16);
-    if (hw != sw) {
+    const bool nan = (u & 0x7fffffffu) > 0x7f800000u;  // excluded by pack_bf16x2_nonan's contract
+    const uint32_t sw = (uint32_t)f32_to_bf16_bits(f) | ((uint32_t)f32_to_bf16_bits(g) << 16);
+    const uint32_t hw = nan ? sw : pack_bf16x2_nonan(f, g);
+    const uint32_t lib = (uint32_t)f32_to_bf16(f) | ((uint32_t)f32_to_bf16(g) << 16);
+    if (hw != sw || lib != sw) {
       ++bad;
       lo = u < lo ? u : lo;
     }

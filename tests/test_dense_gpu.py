@@ -503,9 +503,10 @@ def test_rowquant_near_half_integer_quotients(dtype, K):
 
 
 def test_bf16_conversion_instruction_equals_rne_on_every_binary32():
-    """The fast bf16 epilogues use gfx950's packed conversion instruction: it must give the round-
-    to-nearest-even bits (torch's .to(bfloat16)) for every one of the 2^32 binary32 patterns that
-    is not a NaN, both halves of the pair, denormals included."""
+    """Every bf16 rounding of the library is gfx950's packed conversion instruction: it must give
+    the round-to-nearest-even bits (torch's .to(bfloat16)) for every one of the 2^32 binary32
+    patterns that is not a NaN, both halves of the pair, denormals included; and the library's
+    conversion (that instruction, NaN -> 0x7FC0) must equal the bit method on all 2^32 patterns."""
     from lockstep_amd import _lib as L
     mism = torch.zeros(1, dtype=torch.int32, device=dev())
     first = torch.full((1,), -1, dtype=torch.int32, device=dev())    # 0xFFFFFFFF
