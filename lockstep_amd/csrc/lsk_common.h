@@ -55,6 +55,14 @@ LSK_DEV uint16_t f32_to_bf16(float f) {
   return f != f ? (uint16_t)0x7fc0 : h;
 }
 
+// Two binary32 values to packed bf16 (a in the low half), each equal to f32_to_bf16.
+LSK_DEV uint32_t pack_bf16x2(float a, float b) {
+  uint32_t h = pack_bf16x2_nonan(a, b);
+  if (a != a) h = (h & 0xffff0000u) | 0x7fc0u;
+  if (b != b) h = (h & 0xffffu) | 0x7fc00000u;
+  return h;
+}
+
 // 16 bytes to global memory as two 8-byte stores.  On MI355X a 16-byte global / buffer store
 // followed three to four instructions later by VALU writes to its data registers was measured to
 // store the newer values, and the compiler separates the two by one wait state only; 8-byte

@@ -692,6 +692,10 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
       const int pr = (lane >> 3) % P;
       const int c4 = (lane & 7) * 4;
       const int hc0 = nt * 128 + wn * (32 * P) + pr * 32 + c4;
+      // this lane's four gate and four up columns: the same in every pass
+      const int cg0 = wn * C::WTN + pr * 64 + c4;
+      const v4f wsg = *(const v4f*)(sc_ws + cg0), wsu = *(const v4f*)(sc_ws + cg0 + 32);
+      const v4f bg = *(const v4f*)(sc_b + cg0), bu = *(const v4f*)(sc_b + cg0 + 32);
       float gv[NP][4], uv[NP][4];
 #pragma unroll
       for (int t = 0; t < NP; ++t) {
@@ -702,12 +706,11 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
         const float asc = sc_asc[ml];  // 0 past the tile's rows
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int cg = wn * C::WTN + pr * 64 + c4 + q, cu = cg + 32;
-          float yg = bfr(f32_mul(f32_mul((float)vg[q], sc_ws[cg]), asc));
-          float yu = bfr(f32_mul(f32_mul((float)vu[q], sc_ws[cu]), asc));
+          float yg = bfr(f32_mul(f32_mul((float)vg[q], wsg[q]), asc));
+          float yu = bfr(f32_mul(f32_mul((float)vu[q], wsu[q]), asc));
           if (bias) {
-            yg = bfr(f32_add(yg, sc_b[cg]));
-            yu = bfr(f32_add(yu, sc_b[cu]));
+            yg = bfr(f32_add(yg, bg[q]));
+            yu = bfr(f32_add(yu, bu[q]));
           }
           gv[t][q] = yg;
           uv[t][q] = yu;
@@ -725,7 +728,17 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
         const int ml = wm * C::WTM + i * 32 + row;
         const int p = p0 + ml;
         float am = 0.0f;
-        if (p < p1) {
+        if (p < p1 && hc0 + 4 <= a.N) {
+          // a whole quad: no column tests
+          float hv[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            hv[q] = a.act_tab ? lsk::act_from_entry(a.act, gv[t][q], uv[t][q])
+                              : lsk::act_eval(a.act, gv[t][q], uv[t][q], a.frac, nullptr);
+            am = fmaxf(am, fabsf(hv[q]));
+          }
+          *(uint2*)(a.h + (int64_t)p * a.N + hc0) = make_uint2(pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3]));
+        } else if (p < p1) {
           uint16_t hb[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -755,13 +768,28 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
       constexpr int QPR = C::WTN / 4, RPP = 64 / QPR;
       const int c4 = (lane % QPR) * 4;
       const int n0 = nt * 256 + wn * C::WTN + c4;
+      // this lane's four columns: the same in every pass
+      const int cl0 = wn * C::WTN + c4;
+      const v4f wsq = *(const v4f*)(sc_ws + cl0), bq = *(const v4f*)(sc_b + cl0);
 #pragma unroll
       for (int t = 0; t < 32 / RPP; ++t) {
         const int row = lane / QPR + RPP * t;
         const int ml = wm * C::WTM + i * 32 + row;
         const int p = p0 + ml;
         const v4i v = *(const v4i*)(region + row * C::kLdc + c4);
-        if (p < p1 && n0 < a.N) {
+        if (p < p1 && n0 + 4 <= a.N) {
+          // a whole quad: no column tests
+          const float asc = sc_asc[ml];
+          const float wt = sc_w[ml];
+          float o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float yv = bfr(f32_mul(f32_mul((float)v[q], wsq[q]), asc));
+            if (bias) yv = bfr(f32_add(yv, bq[q]));
+            o[q] = f32_mul(wt, yv);
+          }
+          *(uint2*)(a.y + (int64_t)sc_dst[ml] * a.N + n0) = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+        } else if (p < p1 && n0 < a.N) {
           const float asc = sc_asc[ml];
           const float wt = sc_w[ml];
           uint16_t ob[4];

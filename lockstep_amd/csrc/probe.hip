@@ -36,8 +36,9 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(const v4i* __restrict__
 }
 
 // Every binary32 pattern start .. start + count - 1: gfx950's packed bf16 conversion
-// (pack_bf16x2_nonan, both halves, patterns that are not NaN) and the library's f32_to_bf16 (every
-// pattern, NaN included) against the round-to-nearest-even bit method (f32_to_bf16_bits).
+// (pack_bf16x2_nonan, both halves, patterns that are not NaN) and the library's f32_to_bf16 and
+// pack_bf16x2 (every pattern, NaN included) against the round-to-nearest-even bit method
+// (f32_to_bf16_bits).
 // Disagreements are counted (integer atomics) and the smallest such pattern kept.
 __global__ __launch_bounds__(256) void bf16_cvt_check_kernel(uint64_t start, uint64_t count,
                                                              uint32_t* __restrict__ mismatches,
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(256) void bf16_cvt_check_kernel(uint64_t start, uin
     const uint32_t sw = (uint32_t)f32_to_bf16_bits(f) | ((uint32_t)f32_to_bf16_bits(g) << 16);
     const uint32_t hw = nan ? sw : pack_bf16x2_nonan(f, g);
     const uint32_t lib = (uint32_t)f32_to_bf16(f) | ((uint32_t)f32_to_bf16(g) << 16);
-    if (hw != sw || lib != sw) {
+    if (hw != sw || lib != sw || pack_bf16x2(f, g) != sw) {
       ++bad;
       lo = u < lo ? u : lo;
     }
