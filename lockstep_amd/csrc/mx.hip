@@ -252,50 +252,85 @@ LSK_DEV int moe_mx_wrow(const lsk::MoeGemmArgs& a, int nt, int r) {
 
 // The tile's epilogue from the binary32 block accumulators (128 x 128, four waves of 64 x 64):
 // MODE 0 the gate / up values and the activation into h (with its row maxima); MODE 1 the
-// routing-weighted down values into the token-major slot rows.
+// routing-weighted down values into the token-major slot rows.  The operands of every row and
+// column a lane stores (row scales, routing weights and slots, biases) are loaded together before
+// the first store: loads after a store to memory the compiler cannot prove distinct would each
+// wait a round trip.
 template <int MODE>
 LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int nt, int p0, int p1, const float* bias,
                              char* smem) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / 2, wn = wave % 2;
   float* region = (float*)smem + wave * Cfg::kStripFloats;
+  constexpr int NPASS = MODE == 0 ? 2 : 4;  // passes of 64 lanes over a 16-row strip
+  constexpr int QPR = MODE == 0 ? 8 : 16;   // lanes per row
+  const int c4 = MODE == 0 ? ((lane & 7) & 3) * 4 : (lane & 15) * 4;
+  const int pair = MODE == 0 ? (lane & 7) >> 2 : 0;
+  const int col0 = MODE == 0 ? nt * 64 + wn * 32 + pair * 16 + c4 : nt * 128 + wn * 64 + c4;
+  const bool whole = col0 + 4 <= a.N;
+  float b0[4], b1[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    b0[t] = 0.0f;
+    b1[t] = 0.0f;
+    if (bias && col0 + t < a.N) {
+      b0[t] = bias[col0 + t];
+      if (MODE == 0) b1[t] = bias[a.N + col0 + t];
+    }
+  }
+  float r_asc[Cfg::TM][NPASS], r_w[Cfg::TM][NPASS];
+  int r_dst[Cfg::TM][NPASS];
+#pragma unroll
+  for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+    for (int pass = 0; pass < NPASS; ++pass) {
+      const int p = p0 + wm * 64 + i * 16 + (pass * 64 + lane) / QPR;
+      r_asc[i][pass] = 0.0f;
+      r_w[i][pass] = 1.0f;
+      r_dst[i][pass] = p;
+      if (p < p1) {
+        if (MODE == 0) {
+          r_asc[i][pass] = a.a_scale ? a.a_scale[a.row_tok[p]] : 1.0f;  // none for block-scaled rows
+        } else {
+          r_asc[i][pass] = a.a_scale ? a.a_scale[p] : 1.0f;
+          if (a.row_w) r_w[i][pass] = a.row_w[p];  // none: a plain grouped linear
+          if (a.row_dst) r_dst[i][pass] = a.row_dst[p];
+        }
+      }
+    }
 #pragma unroll
   for (int i = 0; i < Cfg::TM; ++i) {
     lsk::stage_strip_f<Cfg::TN, Cfg::kLdc>(acc[i], region);
     __syncthreads();
     if (MODE == 0) {
 #pragma unroll
-      for (int pass = 0; pass < 2; ++pass) {
-        const int q = pass * 64 + lane;
-        const int row = q >> 3, hq = q & 7, pair = hq >> 2, c4 = (hq & 3) * 4;
+      for (int pass = 0; pass < NPASS; ++pass) {
+        const int row = (pass * 64 + lane) / QPR;
         const int p = p0 + wm * 64 + i * 16 + row;
-        const int hc0 = nt * 64 + wn * 32 + pair * 16 + c4;
+        const float asc = r_asc[i][pass];
         float am = 0.0f;
         if (p < p1) {
-          const float asc = a.a_scale ? a.a_scale[a.row_tok[p]] : 1.0f;  // none for block-scaled rows
-          uint16_t hb[4];
+          float hv[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const int hc = hc0 + t;
-            hb[t] = 0;
-            if (hc < a.N) {
+            hv[t] = 0.0f;
+            if (whole || col0 + t < a.N) {
               float yg = bfr(f32_mul(region[row * Cfg::kLdc + pair * 32 + c4 + t], asc));
               float yu = bfr(f32_mul(region[row * Cfg::kLdc + pair * 32 + 16 + c4 + t], asc));
               if (bias) {
-                yg = bfr(f32_add(yg, bias[hc]));
-                yu = bfr(f32_add(yu, bias[a.N + hc]));
+                yg = bfr(f32_add(yg, b0[t]));
+                yu = bfr(f32_add(yu, b1[t]));
               }
-              const float hv = lsk::act_eval(a.act, yg, yu, a.frac, a.act_tab);
-              hb[t] = f32_to_bf16(hv);
-              am = fmaxf(am, fabsf(hv));
+              hv[t] = lsk::act_eval(a.act, yg, yu, a.frac, a.act_tab);
+              am = fmaxf(am, fabsf(hv[t]));
             }
           }
-          uint16_t* dst = a.h + (int64_t)p * a.N + hc0;
-          if (hc0 + 4 <= a.N) {
-            *(uint2*)dst = make_uint2((uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16));
+          uint16_t* dst = a.h + (int64_t)p * a.N + col0;
+          if (whole) {
+            *(uint2*)dst = make_uint2(pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3]));
           } else {
             for (int t = 0; t < 4; ++t)
-              if (hc0 + t < a.N) dst[t] = hb[t];
+              if (col0 + t < a.N) dst[t] = f32_to_bf16(hv[t]);
           }
         }
         am = fmaxf(am, __shfl_xor(am, 1, 64));
@@ -305,31 +340,27 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
       }
     } else {
 #pragma unroll
-      for (int pass = 0; pass < 4; ++pass) {
-        const int q = pass * 64 + lane;
-        const int row = q >> 4, c4 = (q & 15) * 4;
+      for (int pass = 0; pass < NPASS; ++pass) {
+        const int row = (pass * 64 + lane) / QPR;
         const int p = p0 + wm * 64 + i * 16 + row;
-        const int n0 = nt * 128 + wn * 64 + c4;
-        if (p < p1 && n0 < a.N) {
-          const float asc = a.a_scale ? a.a_scale[p] : 1.0f;
-          const float wt = a.row_w ? a.row_w[p] : 1.0f;  // none: a plain grouped linear
-          uint16_t ob[4];
+        if (p < p1 && col0 < a.N) {
+          const float asc = r_asc[i][pass], wt = r_w[i][pass];
+          float o[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const int n = n0 + t;
-            ob[t] = 0;
-            if (n < a.N) {
+            o[t] = 0.0f;
+            if (whole || col0 + t < a.N) {
               float yv = bfr(f32_mul(region[row * Cfg::kLdc + c4 + t], asc));
-              if (bias) yv = bfr(f32_add(yv, bias[n]));
-              ob[t] = f32_to_bf16(f32_mul(wt, yv));
+              if (bias) yv = bfr(f32_add(yv, b0[t]));
+              o[t] = f32_mul(wt, yv);
             }
           }
-          uint16_t* dst = a.y + (int64_t)(a.row_dst ? a.row_dst[p] : p) * a.N + n0;
-          if (n0 + 4 <= a.N) {
-            *(uint2*)dst = make_uint2((uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16));
+          uint16_t* dst = a.y + (int64_t)r_dst[i][pass] * a.N + col0;
+          if (whole) {
+            *(uint2*)dst = make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
           } else {
             for (int t = 0; t < 4; ++t)
-              if (n0 + t < a.N) dst[t] = ob[t];
+              if (col0 + t < a.N) dst[t] = f32_to_bf16(o[t]);
           }
         }
       }
