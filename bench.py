@@ -483,8 +483,9 @@ def moe_section(torch, args):
                 logits = logits - 1.1 * torch.log1p(rank)[None, :]
             logits = logits.to(torch.bfloat16)
             def step(cp):
-                idx, w, _ = MR.router_from_logits(logits, k, True, tab)
-                fwd(x, None, cp, k, True, tab, 0, act, routing=(idx, w))
+                # the router from the logits inside the layer (moe_ref's logits= form: the same
+                # routing as router_from_logits, in fewer launches)
+                fwd(x, None, cp, k, True, tab, 0, act, logits=logits)
             reps = 20 if T < 4096 else 5
             ms = _graph_time(torch, [(lambda cp=cp: step(cp)) for cp in copies], reps)
             idx, _, _ = MR.router_from_logits(logits, k, True, tab)

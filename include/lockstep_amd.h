@@ -410,6 +410,18 @@ typedef struct {
                                     more rows take the fused block update) */
   const float* act_tab;          /* NULL, or lsk_act_table's table for `act` built from `frac`: the
                                     same results, the activation read per gate value */
+  /* Routing from logits inside the layer (no reference counterpart as one call: the same as
+   * moe_ref.router_from_logits, i.e. lsk_router_topk, followed by the layer with routing=(idx, w)).
+   * When logits is not NULL, idx and w are not read: the layer writes the routing to idx_out
+   * [T, k] int64 and w_out [T, k] bf16 and uses it (for up to 4 tokens inside the layer's first
+   * launch).  k <= E. */
+  const void* logits;            /* [T, E] f32 or bf16 (row stride ld_logits), or NULL */
+  int logits_dtype;              /* LSK_F32 or LSK_BF16 */
+  int renormalize;               /* as lsk_router_topk */
+  int64_t ld_logits;
+  const int32_t* router_tab;     /* the [8192] FRAC table, as lsk_router_topk */
+  int64_t* idx_out;              /* [T, k] */
+  uint16_t* w_out;               /* [T, k] bf16 */
 } lsk_moe_args;
 
 int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt);

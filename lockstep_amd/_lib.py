@@ -88,7 +88,9 @@ class MoeArgs(ctypes.Structure):
                 ("x", _P), ("idx", _P), ("w", _P), ("w13_ptrs", _P), ("ldw13", _I64), ("ws13_ptrs", _P),
                 ("b13_ptrs", _P), ("w2_ptrs", _P), ("ldw2", _I64), ("ws2_ptrs", _P), ("b2_ptrs", _P),
                 ("frac", _P), ("rot_blk", _I), ("rot_scale", ctypes.c_float), ("shared", _P), ("y", _P), ("workspace", _P), ("workspace_bytes", _I64),
-                ("kw13_min", _I), ("kw13_max", _I), ("kw2_min", _I), ("kw2_max", _I), ("act_tab", _P)]
+                ("kw13_min", _I), ("kw13_max", _I), ("kw2_min", _I), ("kw2_max", _I), ("act_tab", _P),
+                ("logits", _P), ("logits_dtype", _I), ("renormalize", _I), ("ld_logits", _I64), ("router_tab", _P),
+                ("idx_out", _P), ("w_out", _P)]
 
 _lock = threading.Lock()
 _lib = None

@@ -43,12 +43,9 @@ LSK_DEV long long wave_max_ll(long long v) {
 // reference's ranking key s * E + (E - 1 - e) orders like the pair (s, E - 1 - e), so the key is
 // kept as s << 32 | (E - 1 - e) and decoded with shifts.
 template <int EPL>
-__global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ g, int gdt, int64_t ldg, int T,
-                                                          int E, int k, int renorm, const int32_t* __restrict__ tab,
-                                                          int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
+LSK_DEV void route_token(const void* __restrict__ g, int gdt, int64_t ldg, int t, int E, int k, int renorm,
+                         const int32_t* __restrict__ tab, int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
   float gv[EPL];
   float m = -__builtin_inff();
 #pragma unroll
@@ -101,6 +98,15 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
     S = S < 1 ? 1 : S;
     w_out[(int64_t)t * k + lane] = f32_to_bf16(f32_div((float)s_sel_mine, (float)S));
   }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict__ g, int gdt, int64_t ldg, int T,
+                                                          int E, int k, int renorm, const int32_t* __restrict__ tab,
+                                                          int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  route_token<EPL>(g, gdt, ldg, t, E, k, renorm, tab, idx_out, w_out);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -284,9 +290,21 @@ __global__ __launch_bounds__(256) void moe_decode_prep_kernel(const int64_t* __r
                                                               uint32_t* __restrict__ zero_buf, int64_t zero_n,
                                                               const uint16_t* __restrict__ x, int H,
                                                               void* __restrict__ qx, float* __restrict__ ascx,
-                                                              int q_bf16) {
+                                                              int q_bf16, const void* __restrict__ logits, int gdt,
+                                                              int64_t ldg, const int32_t* __restrict__ rtab,
+                                                              int renorm, int64_t* __restrict__ idx_out,
+                                                              uint16_t* __restrict__ w_out) {
   extern __shared__ int32_t dsm[];
   if (blockIdx.x == 0) {
+    if (logits) {
+      // the routing first (T <= 4, E <= 256: a wave per token), then the dispatch reads it back
+      for (int t = threadIdx.x >> 6; t < T; t += 4)
+        route_token<4>(logits, gdt, ldg, t, E, k, renorm, rtab, idx_out, w_out);
+      __threadfence_block();
+      __syncthreads();
+      idx = idx_out;
+      w = w_out;
+    }
     dispatch_small_block(idx, w, T, k, E, offs, tiles, row_tok, row_dst, row_w, tok_cnt, zero_buf, zero_n, dsm);
     return;
   }
@@ -1467,8 +1485,21 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(T * k <= 0x7fffffff && T * H * 2 < 0x7fffffff && T * k * I * 2 < 0x7fffffff,
               "lsk_moe_forward: activations beyond 2 GB (31-bit buffer offsets)");
   if (T == 0) return LSK_OK;
-  LSK_REQUIRE(a->x && a->idx && a->w && a->w13_ptrs && a->ws13_ptrs && a->w2_ptrs && a->ws2_ptrs && a->frac && a->y,
+  LSK_REQUIRE(a->x && a->w13_ptrs && a->ws13_ptrs && a->w2_ptrs && a->ws2_ptrs && a->frac && a->y,
               "lsk_moe_forward: null pointer");
+  // the routing: given (idx, w), or computed here from the logits into (idx_out, w_out)
+  const int64_t* ridx = a->idx;
+  const uint16_t* rwt = a->w;
+  if (a->logits) {
+    LSK_REQUIRE(a->idx_out && a->w_out && a->router_tab, "lsk_moe_forward: logits need idx_out, w_out and router_tab");
+    LSK_REQUIRE(a->logits_dtype == LSK_F32 || a->logits_dtype == LSK_BF16, "lsk_moe_forward: logits must be f32 or bf16");
+    LSK_REQUIRE(a->ld_logits >= E, "lsk_moe_forward: ld_logits below E");
+    LSK_REQUIRE(k <= E, "lsk_moe_forward: k=%d above E=%lld", k, (long long)E);
+    ridx = a->idx_out;
+    rwt = a->w_out;
+  } else {
+    LSK_REQUIRE(a->idx && a->w, "lsk_moe_forward: null routing");
+  }
   if (a->wfmt >= 1) {
     LSK_REQUIRE(a->ldw13 >= H / 2 && a->ldw13 % 16 == 0 && a->ldw2 >= I / 2 && a->ldw2 % 16 == 0 &&
                     a->lds13 >= H / 32 && a->lds2 >= I / 32,
@@ -1518,6 +1549,16 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
 
   // up to 256 tokens: the dispatch and the row quant of x in one launch
   const bool prep_decode = T <= 256 && rb == 0 && mx != 2;
+  // routing from logits: inside that launch for up to 4 tokens (a wave per token in its
+  // dispatch block; with more, the waves' serial tokens cost more than the router launch they
+  // save: Qwen3-30B-A3B on MI355X, T = 1 32.0 -> 31.4 us, T = 8 59.0 -> 63.4 us), else the
+  // router kernel first
+  const bool route_in_prep = a->logits && prep_decode && T <= 4 && E <= 256;
+  if (a->logits && !route_in_prep) {
+    const int rrc = lsk_router_topk(a->logits, a->logits_dtype, a->ld_logits, T, E, k, a->renormalize, a->router_tab,
+                                    a->idx_out, a->w_out, stream);
+    if (rrc) return rrc;
+  }
   int rc;
   if (prep_decode) {
     rc = LSK_OK;  // the prep kernel below quantises x
@@ -1556,22 +1597,23 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   const int64_t nchunks = (T + 255) / 256;
   if (prep_decode) {
     const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
-    hipLaunchKernelGGL(moe_decode_prep_kernel, dim3((unsigned)(T + 1)), dim3(256), dsm, s, a->idx, a->w, (int)T, k,
+    hipLaunchKernelGGL(moe_decode_prep_kernel, dim3((unsigned)(T + 1)), dim3(256), dsm, s, ridx, rwt, (int)T, k,
                        (int)E, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero,
-                       a->x, (int)H, (void*)w.qx, w.ascx, mx ? 1 : 0);
+                       a->x, (int)H, (void*)w.qx, w.ascx, mx ? 1 : 0, route_in_prep ? a->logits : nullptr,
+                       a->logits_dtype, a->ld_logits, a->router_tab, a->renormalize, a->idx_out, a->w_out);
     if ((rc = lsk::check_launch("moe_decode_prep_kernel"))) return rc;
   } else if (nchunks == 1) {
     const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
-    hipLaunchKernelGGL(moe_dispatch_small_kernel, dim3(1), dim3(256), dsm, s, a->idx, a->w, (int)T, k, (int)E, w.offs,
+    hipLaunchKernelGGL(moe_dispatch_small_kernel, dim3(1), dim3(256), dsm, s, ridx, rwt, (int)T, k, (int)E, w.offs,
                        w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero);
     if ((rc = lsk::check_launch("moe_dispatch_small_kernel"))) return rc;
   } else {
     hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 4 + (size_t)256 * k * 4, s,
-                       a->idx, (int)T, k,
+                       ridx, (int)T, k,
                        (int)E, w.ccnt, w.tok_cnt, w.h_amax, nzero);
     if ((rc = lsk::check_launch("moe_count_kernel"))) return rc;
     hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nchunks), dim3(256),
-                       (size_t)(11 * E + 1) * 4 + (size_t)256 * k * 6, s, a->idx, a->w, (int)T, k, (int)E, w.ccnt,
+                       (size_t)(11 * E + 1) * 4 + (size_t)256 * k * 6, s, ridx, rwt, (int)T, k, (int)E, w.ccnt,
                        (int)nchunks, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w);
     if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
   }

@@ -251,7 +251,33 @@ def expert_tables(experts) -> ExpertTables:
     return _cached("int8", experts, ExpertTables)
 
 
-def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_out=None):
+def _route_fields(x, route):
+    """Routing inside the layer: route = (logits [T, E], k, renormalize, tab).  Returns (idx, w, the
+    lsk_moe_args fields, the tensors the fields point at), idx / w the outputs the layer fills --
+    the same values as router_from_logits(logits, k, renormalize, tab)."""
+    g, k, renormalize, tab = route
+    L.require_cuda(g, tab, what="moe_forward")
+    T = x.shape[0]
+    if g.dim() != 2 or g.shape[0] != T:
+        raise ValueError("moe_forward: logits must be [T, E] with T = %d rows" % T)
+    if g.dtype == torch.bfloat16:
+        gd, code = g.contiguous(), L.LSK_BF16
+    else:
+        gd, code = g.to(torch.float32).contiguous(), L.LSK_F32
+    tb = ops.tab_i32(tab)
+    idx = torch.empty((T, int(k)), dtype=torch.int64, device=x.device)
+    w = torch.empty((T, int(k)), dtype=BF, device=x.device)
+    fields = dict(logits=gd.data_ptr(), logits_dtype=code, renormalize=1 if renormalize else 0, ld_logits=gd.shape[1],
+                  router_tab=tb.data_ptr(), idx_out=idx.data_ptr(), w_out=w.data_ptr())
+    return idx, w, fields, (gd, tb)
+
+
+def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_out=None, route=None):
+    """The layer on given routing (idx, w), or with route = (logits, k, renormalize, tab) on the
+    routing it computes itself; returns y, or (y, idx, w) with route."""
+    fields, keep = {}, None
+    if route is not None:
+        idx, w, fields, keep = _route_fields(x, route)
     L.require_cuda(x, idx, w, what="moe_forward")
     if x.dtype != BF:
         raise TypeError("moe_forward: x must be bf16 [T, H] (got %s)" % x.dtype)
@@ -264,7 +290,7 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
     w = w.to(BF).contiguous()
     y = torch.empty((T, H), dtype=BF, device=x.device)
     if T == 0:
-        return y
+        return y if route is None else (y, idx, w)
     nbytes = L.load().lsk_moe_workspace(T, k, tables.E, H, tables.I, rot_blk, 0)
     work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     sh = None if shared_out is None else shared_out.to(F32).contiguous()
@@ -277,15 +303,23 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
                   frac=ops.frac_i32(x.device).data_ptr(), act_tab=_act_tab(x.device, act), rot_blk=int(rot_blk),
                   rot_scale=(1.0 / (rot_blk ** 0.5)) if rot_blk else 0.0,
                   shared=sh.data_ptr() if sh is not None else None, y=y.data_ptr(),
-                  workspace=work.data_ptr(), workspace_bytes=nbytes)
+                  workspace=work.data_ptr(), workspace_bytes=nbytes, **fields)
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
-    return y
+    del keep
+    return y if route is None else (y, idx, w)
 
 
 def moe_forward(x: torch.Tensor, gate, experts, k: int, renormalize: bool, tab: torch.Tensor, win: int, silu_fn,
-                shared=None, routing=None, rot: bool = False):
+                shared=None, routing=None, rot: bool = False, logits=None):
     """x bf16 [T, H] -> (y bf16 [T, H], idx, w).  routing=(idx, w) injects a routing; the
-    declared router runs otherwise.  experts: the reference's list, or an ExpertTables."""
+    declared router runs otherwise.  experts: the reference's list, or an ExpertTables.
+    logits (no reference counterpart as one call): router logits [T, E] whose routing the layer
+    computes itself -- the same results as routing=router_from_logits(logits, k, renormalize,
+    tab)[:2], in fewer launches."""
+    if logits is not None:
+        sh = shared(x) if shared is not None else None
+        return _moe_layer(x, None, None, expert_tables(experts), _act_code(silu_fn), 256 if rot else 0, sh,
+                          route=(logits, k, renormalize, tab))
     if routing is None:
         idx, w, _ = router(x, gate[0], gate[1], k, renormalize, tab, win)
     else:
@@ -443,8 +477,11 @@ def grouped_linear_mx(tables, which: str, a8, asc, offs):
     return out
 
 
-def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1):
+def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1, route=None):
     what = "moe_forward_mx2" if wfmt == 2 else "moe_forward_mx"
+    fields, keep = {}, None
+    if route is not None:
+        idx, w, fields, keep = _route_fields(x, route)
     L.require_cuda(x, idx, w, what=what)
     if x.dtype != BF:
         raise TypeError("%s: x must be bf16 [T, H] (got %s)" % (what, x.dtype))
@@ -457,7 +494,7 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1):
     w = w.to(BF).contiguous()
     y = torch.empty((T, H), dtype=BF, device=x.device)
     if T == 0:
-        return y
+        return y if route is None else (y, idx, w)
     nbytes = L.load().lsk_moe_workspace(T, k, t.E, H, t.I, 0, wfmt)
     work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     kb = t.kw_bounds
@@ -468,14 +505,18 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1):
                   w2_ptrs=t.w2.data_ptr(), ldw2=t.ldw2, ws2_ptrs=t.ws2.data_ptr(),
                   b2_ptrs=t.b2.data_ptr() if t.b2 is not None else None, frac=ops.frac_i32(x.device).data_ptr(),
                   act_tab=_act_tab(x.device, act), rot_blk=0, rot_scale=0.0, shared=None, y=y.data_ptr(), workspace=work.data_ptr(),
-                  workspace_bytes=nbytes)
+                  workspace_bytes=nbytes, **fields)
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
-    return y
+    del keep
+    return y if route is None else (y, idx, w)
 
 
-def moe_forward_mx(x, gate, experts, k, renormalize, tab, win, act, routing=None):
+def moe_forward_mx(x, gate, experts, k, renormalize, tab, win, act, routing=None, logits=None):
     """experts[e] = ((m2_13, kexp_13), (m2_2, kexp_2), b13 | None, b2 | None), or an
-    ExpertTablesMX; gate as moe_forward_b.  Returns (y bf16 [T, H], idx, w)."""
+    ExpertTablesMX; gate as moe_forward_b.  Returns (y bf16 [T, H], idx, w).  logits: as
+    moe_forward's."""
+    if logits is not None:
+        return _moe_layer_mx(x, None, None, expert_tables_mx(experts), _act_code(act), route=(logits, k, renormalize, tab))
     if routing is None:
         idx, w, _ = router_b(x, gate[0], gate[1], k, renormalize, tab, win, gate[2] if len(gate) > 2 else None)
     else:
@@ -507,9 +548,13 @@ def expert_block_mx2(x_rows, w13, w2, act, b13=None, b2=None):
     return ops.gemm_mx2(q2, ka2, w2[0], w2[1], 0, bias=b2, epilogue=1)
 
 
-def moe_forward_mx2(x, gate, experts, k, renormalize, tab, win, act, routing=None):
+def moe_forward_mx2(x, gate, experts, k, renormalize, tab, win, act, routing=None, logits=None):
     """As moe_forward_mx with block-scaled activations (no per-row scale; epilogues bfr(acc) + b).
-    experts[e] = ((m2_13, kexp_13), (m2_2, kexp_2), b13 | None, b2 | None) or an ExpertTablesMX."""
+    experts[e] = ((m2_13, kexp_13), (m2_2, kexp_2), b13 | None, b2 | None) or an ExpertTablesMX.
+    logits: as moe_forward's."""
+    if logits is not None:
+        return _moe_layer_mx(x, None, None, expert_tables_mx(experts), _act_code(act), wfmt=2,
+                             route=(logits, k, renormalize, tab))
     if routing is None:
         idx, w, _ = router_b(x, gate[0], gate[1], k, renormalize, tab, win, gate[2] if len(gate) > 2 else None)
     else:

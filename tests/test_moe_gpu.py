@@ -320,3 +320,43 @@ def test_moe_decode_layers_replayed_from_a_graph():
         assert np.array_equal(u16(yg), ref)
         yo, _, _ = MR.moe_forward(other[0], None, other[1], 4, True, _tab(), 0, MR.act_silu, routing=other[2])
         assert np.array_equal(u16(yo), other[3])
+
+
+@pytest.mark.parametrize("T", [1, 3, 4, 5, 40, 300])
+def test_moe_forward_from_logits(T):
+    """moe_forward(logits=...): the routing computed inside the layer (up to 4 tokens in the layer's
+    first launch, a wave per token; beyond that by the router kernel first; past 256 tokens with
+    the multi-chunk dispatch) against the oracle's router_from_logits and moe_forward: y, idx and
+    w bit for bit, logits given as binary32 and as bf16."""
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("moe from logits", T)
+    x, experts, logits = WL.moe_inputs(T, 16, 4, 256, 128, seed=90 + T)
+    idx, w = routing_from_logits(logits, 4)
+    ref = C.moe_forward(x, oracle_experts(experts), idx, w, act=C.act_silu)
+    dx, dexp = bf16_dev(x), device_experts(experts)
+    for g in (to_dev(logits), bf16_dev(logits)):
+        y, di, dw = MR.moe_forward(dx, None, dexp, 4, True, _tab(), 0, MR.act_silu, logits=g)
+        assert np.array_equal(u16(y), ref)
+        assert np.array_equal(di.cpu().numpy(), idx)
+        assert np.array_equal(u16(dw), w)
+
+
+@pytest.mark.parametrize("T", [1, 6, 40])
+@pytest.mark.parametrize("wfmt", [1, 2])
+def test_moe_mx_forward_from_logits(T, wfmt):
+    """MXFP4 experts (per-row and block-scaled activations) with the routing computed inside the
+    layer: the same bits as router_from_logits followed by the layer with routing=(idx, w)."""
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("moe mx from logits", T, wfmt)
+    x, experts, logits = WL.moe_mx_inputs(T, 8, 2, 256, 128, seed=120 + T, bias=True)
+    dexp = MR.ExpertTablesMX([((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2))
+                              for (p13, s13, p2, s2, b13, b2) in experts], packed=True)
+    dx, g = bf16_dev(x), bf16_dev(logits)
+    fwd = MR.moe_forward_mx if wfmt == 1 else MR.moe_forward_mx2
+    ri, rw, _ = MR.router_from_logits(g, 2, True, _tab())
+    y0, _, _ = fwd(dx, None, dexp, 2, True, _tab(), 0, MR.act_swigluoai, routing=(ri, rw))
+    y1, di, dw = fwd(dx, None, dexp, 2, True, _tab(), 0, MR.act_swigluoai, logits=g)
+    assert torch.equal(y1.view(torch.int16), y0.view(torch.int16))
+    assert torch.equal(di, ri) and torch.equal(dw.view(torch.int16), rw.view(torch.int16))
