@@ -367,7 +367,8 @@ def test_config2_prefill_rows_and_chunk_invariance(which, seed):
 @pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 16, 17, 18])
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 257, 640), (512, 520, 2880), (64, 64, 16),
                                    (1, 1000, 14336), (3, 77, 2880), (4, 300, 1040), (8, 1000, 4096),
-                                   (17, 77, 2880), (32, 520, 14336), (5, 33, 48), (24, 32800, 320)])
+                                   (17, 77, 2880), (32, 520, 14336), (5, 33, 48), (24, 32800, 320),
+                                   (16, 700, 8192), (13, 129, 1040), (7, 1001, 14336)])
 def test_every_tile_config_is_exact(tile, M, N, K):
     """The forced tile configurations produce the same bits (exact integer sums, any tiling)."""
     from lockstep_amd import _lib as L
