@@ -1011,6 +1011,101 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemmArgs a, uint16_t* 
   }
 }
 
+// The down projection and the combine of a one-token layer in one launch (the decode GEMV path at
+// T = 1).  The token's routed rows are its experts in ascending order, one row each (row s = slot
+// s, expert tiles[1 + 2 s]), so a wave owning RPW output columns computes every slot's value for
+// them -- moe_gemv_kernel's MODE 1 value bfr(w * bfr(fl32(fl32(acc) * ws[c]) * asc)) (with a bias
+// bfr(... + b[c]) first) -- and adds the slots in order from +0 as moe_combine_kernel does (then
+// bfr(shared[c])), writing y directly: no slot rows and no combine launch.  All weight and
+// activation loads of a wave are issued together; the KMAX x RPW exact int32 sums are reduced by
+// the transposing butterfly, and the column's owner lane gathers the slot values by shuffles.
+template <int NC, int RPW, int KMAX>
+__global__ __launch_bounds__(256) void moe_down_combine1_kernel(MoeGemmArgs a, const float* __restrict__ shared,
+                                                               uint16_t* __restrict__ out) {
+  constexpr int V = KMAX * RPW;
+  static_assert(V >= 2 && V <= 64 && (V & (V - 1)) == 0, "a power of two of at most 64 values");
+  constexpr int kRep = 64 / V;
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int c0 = (blockIdx.x * 4 + wave) * RPW;
+  if (c0 >= a.N) return;  // whole waves; no barrier follows
+  const int n = a.tiles[0];  // routed rows (the host checks k <= KMAX)
+  uint32_t koff[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int kk = j * 1024 + lane * 16;
+    koff[j] = kk < a.K ? (uint32_t)kk : lsk::kOob;
+  }
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+  int es[KMAX];
+  v4i wv[KMAX][RPW][NC], xv[KMAX][NC];
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    es[s] = s < n ? a.tiles[1 + 2 * s] : 0;
+    const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)a.w_ptrs[es[s]], s < n ? a.w_bytes : 0);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const uint32_t ro = c0 + i < a.N ? (uint32_t)((c0 + i) * a.ldw) : lsk::kOob;
+#pragma unroll
+      for (int j = 0; j < NC; ++j)
+        wv[s][i][j] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, (ro == lsk::kOob || koff[j] == lsk::kOob) ? lsk::kOob
+                                                                                                    : ro + koff[j],
+                                                       0, 2 /* non-temporal */));
+    }
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+      xv[s][j] = lsk::buf_load16(ra, (s < n && koff[j] != lsk::kOob) ? (uint32_t)(s * a.lda) + koff[j] : lsk::kOob);
+  }
+  // this lane's value after the exchange: slot vs, column c0 + vc; its epilogue operands
+  const int vi = lane / kRep, vs = vi / RPW, vc = vi % RPW;
+  const int c = c0 + vc;
+  const bool live = vs < n && c < a.N;
+  float ws = 0.0f, b = 0.0f, asc = 0.0f, wt = 0.0f;
+  if (live) {
+    ws = ((const float*)a.ws_ptrs[es[vs]])[c];
+    if (a.b_ptrs) b = ((const float*)a.b_ptrs[es[vs]])[c];
+    asc = a.a_scale[vs];
+    wt = a.row_w[vs];
+  }
+  const float sh = (shared && vs == 0 && c < a.N) ? bfr(shared[c]) : 0.0f;
+  int v[V];
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s)
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      int t = 0;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        t = __builtin_amdgcn_sdot4(xv[s][j][0], wv[s][i][j][0], t, false);
+        t = __builtin_amdgcn_sdot4(xv[s][j][1], wv[s][i][j][1], t, false);
+        t = __builtin_amdgcn_sdot4(xv[s][j][2], wv[s][i][j][2], t, false);
+        t = __builtin_amdgcn_sdot4(xv[s][j][3], wv[s][i][j][3], t, false);
+      }
+      v[s * RPW + i] = t;
+    }
+  wave_xchg_sum<V, 32>(v, lane);
+  int tot = v[0];
+#pragma unroll
+  for (int o = kRep / 2; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+  float f = 0.0f;
+  if (live) {
+    float yv = bfr(f32_mul(f32_mul((float)tot, ws), asc));
+    if (a.b_ptrs) yv = bfr(f32_add(yv, b));
+    f = bfr(f32_mul(wt, yv));
+  }
+  // the column's slots in order from +0 (the combine), gathered from the lanes holding them
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < KMAX; ++s) {
+    const float g = __shfl(f, (s * RPW + vc) * kRep, 64);
+    if (s < n) acc = f32_add(acc, g);
+  }
+  if (vs == 0 && (lane % kRep) == 0 && c < a.N) {
+    if (shared) acc = f32_add(acc, sh);
+    out[c] = f32_to_bf16(acc);
+  }
+}
+
 // Decode path after the gate/up GEMV: per row, h = act(gate, up) (the values the tiled kernels
 // store), its |h| maximum (fmaxf from +0, so a NaN is passed over as there), and the row quant
 // of h exactly as moe_requant_kernel does it (int8, or its values as bf16 for the MX GEMV).
@@ -1729,6 +1824,16 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (use_gemv && T == 1 && k <= 8 && I <= 2048) {
+    // one token: the down GEMV and the combine in one launch (writes y itself)
+    const int64_t blocks = (H + 4 * 2 - 1) / (4 * 2);
+#define LSK_DC(NCV)                                                                                    \
+  hipLaunchKernelGGL((moe_down_combine1_kernel<NCV, 2, 8>), dim3((unsigned)blocks), dim3(256), 0, s, g2, \
+                     a->shared, a->y)
+    if (I <= 1024) LSK_DC(1);
+    else LSK_DC(2);
+#undef LSK_DC
+    return lsk::check_launch("moe_down_combine1_kernel");
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<1>(g2, w.max_tiles, T, nullptr, s, "moe_gemv_kernel<down>"))) return rc;
   } else if (use_pp) {

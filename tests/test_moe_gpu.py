@@ -360,3 +360,24 @@ def test_moe_mx_forward_from_logits(T, wfmt):
     y1, di, dw = fwd(dx, None, dexp, 2, True, _tab(), 0, MR.act_swigluoai, logits=g)
     assert torch.equal(y1.view(torch.int16), y0.view(torch.int16))
     assert torch.equal(di, ri) and torch.equal(dw.view(torch.int16), rw.view(torch.int16))
+
+
+@pytest.mark.parametrize("k,I,extra", [(8, 768, None), (4, 1024, "shared"), (6, 2048, "bias"), (3, 512, "skip"),
+                                       (8, 1536, "skip_all"), (1, 256, None)])
+def test_moe_one_token_down_and_combine(k, I, extra):
+    """One token (the down projection and the combine in one launch): k experts of 1 to 8, I up to
+    2048 (one and two 1 KB chunks), with a shared expert, with biases (SwiGLU-OAI), with some or
+    all routing entries outside [0, E) (skipped: the token's output is then the shared part or
+    zero), against the oracle."""
+    E, H = 32, 512
+    if extra == "skip":
+        idx = np.array([[40, 3, 17]], np.int64)
+        w = C.bf16_bits(np.array([[0.5, 0.25, 0.125]], F32))
+        _run_case(1, E, k, H, I, seed=130, routing_override=(idx, w))
+    elif extra == "skip_all":
+        idx = np.arange(E, E + k, dtype=np.int64)[None, :]
+        w = C.bf16_bits(np.full((1, k), 0.125, F32))
+        _run_case(1, E, k, H, I, seed=131, routing_override=(idx, w))
+    else:
+        _run_case(1, E, k, H, I, seed=132 + k, bias=extra == "bias", act="swigluoai" if extra == "bias" else "silu",
+                  shared=extra == "shared")
