@@ -680,7 +680,9 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe);
+  // the wave's 32-row strips that hold rows of the tile (the others are neither multiplied nor stored)
+  const int na = max(0, min(C::TM, (p1 - p0 - wm * C::WTM + 31) / 32));
+  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe, na);
 
   // park the operands in LDS (past every wave's last ring read)
   float* sc_asc = (float*)(smem_moe + C::kScaleOff);
@@ -833,10 +835,14 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
       }
     }
   };
-  lsk::pp_stage_strip<C::TN, C::kLdc>(acc[0], region);
-  strip(0);
-  lsk::pp_stage_strip<C::TN, C::kLdc>(acc[1], region);
-  strip(1);
+  if (na > 0) {
+    lsk::pp_stage_strip<C::TN, C::kLdc>(acc[0], region);
+    strip(0);
+  }
+  if (na > 1) {
+    lsk::pp_stage_strip<C::TN, C::kLdc>(acc[1], region);
+    strip(1);
+  }
 }
 
 template <int MODE>
@@ -844,8 +850,8 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
   moe_tile<PPM, MODE>(a, smem_moe,
                       [](PPM::Acc& acc, __amdgpu_buffer_rsrc_t ra, const PPM::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
-                         const PPM::RowsB& pb, int K, char* sm) {
-                        lsk::pp_mainloop<128, 256, 2, 4, 3>(acc, ra, pa, rb, pb, K, sm);
+                         const PPM::RowsB& pb, int K, char* sm, int na) {
+                        lsk::pp_mainloop<128, 256, 2, 4, 3, 64, false, true>(acc, ra, pa, rb, pb, K, sm, na);
                       });
 }
 
@@ -854,8 +860,8 @@ __global__ __launch_bounds__(512, 1) void moe_pp128_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
   moe_tile<PPM128, MODE>(a, smem_moe,
                          [](PPM128::Acc& acc, __amdgpu_buffer_rsrc_t ra, const PPM128::RowsA& pa,
-                            __amdgpu_buffer_rsrc_t rb, const PPM128::RowsB& pb, int K, char* sm) {
-                           lsk::pp_mainloop<128, 256, 2, 4, 3, 128>(acc, ra, pa, rb, pb, K, sm);
+                            __amdgpu_buffer_rsrc_t rb, const PPM128::RowsB& pb, int K, char* sm, int na) {
+                           lsk::pp_mainloop<128, 256, 2, 4, 3, 128, false, true>(acc, ra, pa, rb, pb, K, sm, na);
                          });
 }
 
@@ -864,7 +870,9 @@ __global__ __launch_bounds__(256, 2) void moe_w4_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
   moe_tile<W4M, MODE>(a, smem_moe,
                       [](W4M::Acc& acc, __amdgpu_buffer_rsrc_t ra, const W4M::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
-                         const W4M::RowsB& pb, int K, char* sm) { lsk::w4_mainloop<W4M>(acc, ra, pa, rb, pb, K, sm); });
+                         const W4M::RowsB& pb, int K, char* sm, int) {
+                        lsk::w4_mainloop<W4M>(acc, ra, pa, rb, pb, K, sm);
+                      });
 }
 
 // ---------------------------------------------------------------- decode-sized grouped GEMV

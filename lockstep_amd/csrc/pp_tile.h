@@ -137,10 +137,13 @@ LSK_DEV void pp_issue_prologue(__amdgpu_buffer_rsrc_t ra, const typename PPCfg<B
 // for them; the first step issues nothing (its stage kAhead is in the ring already) and the
 // first three steps (which wait for stages 1 .. 3) wait for nothing, leaving the stores to
 // drain while stages 0 .. 2 are multiplied.  Needs K / kBK >= kRing + 2 whole stages.
-template <int BM, int BN, int WM, int WN, int RING, int BKB = 64, bool PRE = false>
+// SKIP (two 32-row strips per wave): only the wave's first na strips hold rows of the tile
+// (na in 0 .. 2, wave-uniform), so the fragment reads and MFMAs of the others are left out; their
+// accumulators stay zero.  The loads and barriers are the same for every wave.
+template <int BM, int BN, int WM, int WN, int RING, int BKB = 64, bool PRE = false, bool SKIP = false>
 LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __amdgpu_buffer_rsrc_t ra,
                          const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
-                         const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb, int K, char* smem) {
+                         const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb, int K, char* smem, int na = 0) {
   using C = PPCfg<BM, BN, WM, WN, RING, BKB>;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int group = wave >> 2;
@@ -200,24 +203,35 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __
     if (do_issue) issue(kt + C::kAhead, check);
     const char* st = smem + (kt % C::kRing) * C::kStage;
     v4i fa[C::kKS][C::TM], fb[C::kKS][C::TN];
+    // strip i's fragments and MFMAs only where it holds rows (SKIP; na is wave-uniform)
+    auto live = [&](int i) { return !SKIP || i < na; };
+    const bool any = !SKIP || na > 0;
+    if (any) {
 #pragma unroll
-    for (int ks = 0; ks < C::kKS; ++ks) {
+      for (int ks = 0; ks < C::kKS; ++ks) {
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i) fa[ks][i] = *(const v4i*)(st + offA + i * 32 * C::kBK + slot[ks]);
+        for (int i = 0; i < C::TM; ++i)
+          if (live(i)) fa[ks][i] = *(const v4i*)(st + offA + i * 32 * C::kBK + slot[ks]);
 #pragma unroll
-      for (int j = 0; j < C::TN; ++j) fb[ks][j] = *(const v4i*)(st + offB + j * 32 * C::kBK + slot[ks]);
+        for (int j = 0; j < C::TN; ++j) fb[ks][j] = *(const v4i*)(st + offB + j * 32 * C::kBK + slot[ks]);
+      }
     }
     wait_vm<kWait>();
     wait_lgkm0();
     phase_barrier();
+    if (any) {
 #pragma unroll
-    for (int ks = 0; ks < C::kKS; ++ks)
+      for (int ks = 0; ks < C::kKS; ++ks)
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i)
+        for (int i = 0; i < C::TM; ++i)
+          if (live(i)) {
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma_i8_32(fa[ks][i], fb[ks][j], acc[i][j]);
+            for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma_i8_32(fa[ks][i], fb[ks][j], acc[i][j]);
+          }
+    }
     phase_barrier();
   };
+  static_assert(!SKIP || C::TM == 2, "strip skipping takes two 32-row strips per wave");
   using W0 = std::integral_constant<int, 0>;
 
   // prologue: stages 0 .. kAhead-1 issued together and all waited for (about one latency,
