@@ -174,18 +174,21 @@ def block_section(torch, args):
     wall = time.perf_counter() - t0
     ms = marks[0][0].elapsed_time(marks[-1][-1]) / args.steps
     site_ms = [sum(mk[i].elapsed_time(mk[i + 1]) for mk in marks) / args.steps for i in range(len(sites))]
-    # each site's GEMM alone on its quantised operands: the dominant kernel's launch time
+    # each site's GEMM alone on its quantised operands (the site's own quant left in its work
+    # buffer, in the layout the site's GEMM reads): the dominant kernel's launch time
     gemm_ms = []
     for _, N, K, x, W8 in sites:
         from lockstep_amd import _lib as L
         from lockstep_amd import ops
-        q8, _, erow = ops.quant8_dyn(x, erow=True)
+        work = torch.empty((L.load().lsk_linear_dyn_workspace(T, K),), dtype=torch.uint8, device=dev)
         out = torch.empty((T, N), dtype=torch.float32, device=dev)
-        fn = lambda: ops.gemm(q8, W8, L.EPI_POW2, L.LSK_F32, erow=erow, shift=BLOCK_EW, out=out)  # noqa: E731
+        ex = torch.empty((1,), dtype=torch.int32, device=dev)
+        ops.linear_dyn(x, W8, BLOCK_EW, stages=1, work=work, y=out, ex=ex)
+        fn = lambda: ops.linear_dyn(x, W8, BLOCK_EW, stages=2, work=work, y=out, ex=ex)  # noqa: E731
         for _ in range(2):
             fn()
         gemm_ms.append(_events_time(torch, fn, max(args.steps, 5)))
-        del q8, erow, out
+        del work, out, ex
     achieved = ops_step / (sum(gemm_ms) * 1e-3) / 1e12
     per_site = {name: {"site_us": round(t * 1e3, 1), "gemm_us": round(gk * 1e3, 1),
                        "quant8_dyn_us": round((t - gk) * 1e3, 1), "TOPS": round(o / (t * 1e-3) / 1e12, 1),
@@ -197,9 +200,11 @@ def block_section(torch, args):
             "T": T, "per_site": per_site,
             "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                          "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                         "kernel": "gemm_i8_pp_kernel (POW2 epilogue, binary32 out)",
+                         "kernel": "gemm_i8_pp_pow2_persist_kernel (row-pair A operand, POW2 epilogue, binary32 "
+                                   "out) with its 256x128 column tails",
                          "note": "2*T*N*K int8 ops of the four GEMMs / the sum of their average launch times "
-                                 "(HIP events on the launch stream, each GEMM alone on its quantised operands)"}}
+                                 "(HIP events on the launch stream, each site's GEMM alone on its quantised "
+                                 "operands: lsk_linear_dyn stage 2)"}}
 
 
 def cpu_baseline_block(args):

@@ -253,6 +253,22 @@ int64_t lsk_quant8_dyn_workspace(void);
 int lsk_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
                    int32_t* e_out, int32_t* erow_out, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* One GEMM site of the golden block whole (reference/ref_block_v1.py:166-167 qkv, :191-193 o,
+ * :196-198 up, :216-218 down, each `q8, ex = quant8_dyn(x); y = gemm_int(q8, W8) * 2^-(ex + ew)`):
+ * (q, ex) = quant8_dyn(x) as lsk_quant8_dyn, then y[m, n] = fl32(fl32(acc[m, n]) * 2^-(ex + ew))
+ * with acc = q @ w^T exact -- the same y as lsk_quant8_dyn followed by lsk_gemm_w8a8 (POW2,
+ * erow, shift = ew, binary32 out), bit for bit.  x [M, K] binary32 (row stride ldx); w [N, K] int8
+ * (row stride ldw); y [M, N] binary32 (row stride ldy); ex_out[0] = ex.  q stays in the workspace
+ * (lsk_linear_dyn_workspace(M, K) bytes, 256-byte aligned), written in the layout the GEMM tiles
+ * read fastest (rows paired by 64-byte K chunks when every tile is a ping-pong tile).  Three
+ * launches, nothing to clear beforehand (graph-capturable).  stages: 3 the whole site; 1 only the
+ * quant (q and the exponents into the workspace, ex_out), 2 only the GEMM from a workspace that a
+ * stage-1 call with the same arguments filled (to time the GEMM alone). */
+int64_t lsk_linear_dyn_workspace(int64_t M, int64_t K);
+int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t ldw, int64_t N,
+                   int ew, float* y, int64_t ldy, int32_t* ex_out, int stages, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- the MXFP4 operand */
 
 /* The MXFP4-consuming GEMM (contract addendum item 5).  Replaces moe_ref.int_mm_mx and,

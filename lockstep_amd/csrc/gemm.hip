@@ -265,7 +265,10 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
     }
   }
 
-  const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(A + (int64_t)m0 * lda, (int64_t)(M - m0) * lda);
+  // (the row-pair layout: m0 is even, so the tile's rows start at byte m0 * lda as well; an odd M
+  // ends in a pair whose second row is never read)
+  const int64_t a_rows = ep.a_pair ? (int64_t)((M - m0 + 1) & ~1) : (int64_t)(M - m0);
+  const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(A + (int64_t)m0 * lda, a_rows * lda);
   const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)(N - n0) * ldw);
   typename C::RowsA pa;
   typename C::RowsB pb;
@@ -273,7 +276,8 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
   for (int j = 0; j < C::kLA; ++j) {
     int row, kb;
     lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
-    pa[j] = (m0 + row < M) ? (uint32_t)(row * lda) : lsk::kOob;
+    const uint32_t ro = ep.a_pair ? (uint32_t)((row >> 1) * 2 * lda + (row & 1) * 64) : (uint32_t)(row * lda);
+    pa[j] = (m0 + row < M) ? ro : lsk::kOob;
   }
 #pragma unroll
   for (int j = 0; j < C::kLB; ++j) {
@@ -287,7 +291,7 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  main(acc, ra_res, pa, rb_res, pb, K, smem_pp);
+  main(acc, ra_res, pa, rb_res, pb, K, smem_pp, ep.a_pair);
 
   // every wave is past its last read of the LDS ring
   float* sc_row = (float*)(smem_pp + C::kScaleOff);
@@ -355,8 +359,8 @@ __global__ __launch_bounds__(512, (RING == 3 && BKB == 64 ? 2 : 1)) void gemm_i8
   extern __shared__ __attribute__((aligned(16))) char smem_pp[];
   contract_tile<C>(A, lda, W, ldw, M, N, K, ep, vec_ok, smem_pp,
                    [](typename C::Acc& acc, __amdgpu_buffer_rsrc_t ra, const typename C::RowsA& pa,
-                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm) {
-                     lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra, pa, rb, pb, K_, sm);
+                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm, int apair) {
+                     lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra, pa, rb, pb, K_, sm, 0, apair);
                    });
 }
 
@@ -401,7 +405,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_pow2_persist_kernel(const i
     for (int j = 0; j < C::kLA; ++j) {
       int row, kb;
       lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
-      t.pa[j] = (uint32_t)(row * lda);
+      t.pa[j] = ep.a_pair ? (uint32_t)((row >> 1) * 2 * lda + (row & 1) * 64) : (uint32_t)(row * lda);
     }
 #pragma unroll
     for (int j = 0; j < C::kLB; ++j) {
@@ -421,9 +425,9 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_pow2_persist_kernel(const i
 #pragma unroll
       for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
     if (it == 0)
-      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, false>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp);
+      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, false>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, 0, ep.a_pair);
     else
-      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, true>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp);
+      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, true>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, 0, ep.a_pair);
     // every wave is past its last read of the ring; the previous tile's epilogue (the last
     // reader of sc_row) ended before this tile's first barrier
     if (tid < BM) sc_row[tid] = cur.erow;
@@ -431,7 +435,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_pow2_persist_kernel(const i
         lsk::make_rsrc((char*)ep.out + ((int64_t)cur.m0 * ep.ldo + cur.n0) * 4, (int64_t)(BM - 1) * ldo_bytes + BN * 4);
     if (v + (int)gridDim.x < tiles) {
       setup(v + gridDim.x, cur);
-      lsk::pp_issue_prologue<BM, BN, WM, WN, RING, BKB>(cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp);
+      lsk::pp_issue_prologue<BM, BN, WM, WN, RING, BKB>(cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, ep.a_pair);
     }
     __syncthreads();
     pp_epilogue_direct_pow2<C>(acc, ro, ldo_bytes, ep.shift, sc_row);
@@ -447,8 +451,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   extern __shared__ __attribute__((aligned(16))) char smem_pp[];
   contract_tile<C>(A, lda, W, ldw, M, N, K, ep, vec_ok, smem_pp,
                    [](typename C::Acc& acc, __amdgpu_buffer_rsrc_t ra, const typename C::RowsA& pa,
-                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm) {
-                     lsk::w4_mainloop<C>(acc, ra, pa, rb, pb, K_, sm);
+                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm, int) {
+                     lsk::w4_mainloop<C>(acc, ra, pa, rb, pb, K_, sm);  // row-major A only
                    });
 }
 
@@ -1360,12 +1364,29 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
   return check_launch("gemv_i8_stream_kernel");
 }
 
+static bool tiles_fast(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K) {
+  // the tile kernels address rows by 32-bit offsets inside a 256-row tile
+  return (K % 16 == 0) && (lda % 16 == 0) && (ldw % 16 == 0) && aligned16(a) && aligned16(w) && M <= 0x7fffffff &&
+         N <= 0x7fffffff && K > 0 && lda * 256 < 0x7fffffff && ldw * 256 < 0x7fffffff;
+}
+
+// Whether launch_gemm runs (M, N, K) on the ping-pong tile kernels only (the kernels that read an
+// A operand in the row-pair layout), for an A of row stride lda at a 16-byte aligned address.
+bool gemm_takes_pp(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int64_t lda) {
+  if (M <= 0 || N <= 0 || !tiles_fast(w, lda, w, ldw, M, N, K)) return false;  // (A aligned: the caller)
+  if (M <= 32 && (g_force_tile < 0 || g_force_tile == 5)) return false;
+  if (g_force_tile < 0 && split_columns(M, N) > 0) return true;
+  const int t = pick_tile(M, N);
+  return t == 1 || t == 2 || t == 3 || t == 4 || t == 12 || t == 13 || t == 18;
+}
+
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiParams& ep, hipStream_t s) {
   if (M == 0 || N == 0) return LSK_OK;
-  // the tile kernels address rows by 32-bit offsets inside a 256-row tile
-  const bool fast = (K % 16 == 0) && (lda % 16 == 0) && (ldw % 16 == 0) && aligned16(a) && aligned16(w) &&
-                    M <= 0x7fffffff && N <= 0x7fffffff && K > 0 && lda * 256 < 0x7fffffff && ldw * 256 < 0x7fffffff;
+  LSK_REQUIRE(!ep.a_pair || (lda % 64 == 0 && aligned16(a) && gemm_takes_pp(w, ldw, M, N, K, lda)),
+              "gemm: an A operand in the row-pair layout needs the ping-pong tiles (M=%lld N=%lld K=%lld lda=%lld)",
+              (long long)M, (long long)N, (long long)K, (long long)lda);
+  const bool fast = tiles_fast(a, lda, w, ldw, M, N, K);
   if (!fast) {
     const int64_t total = M * N;
     const int64_t blocks = (total + 255) / 256;

@@ -2,6 +2,12 @@
 // power-of-two quantisers of the golden training block.
 #include "lsk_common.h"
 
+namespace lsk {
+int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                const EpiParams& ep, hipStream_t s);
+bool gemm_takes_pp(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int64_t lda);
+}  // namespace lsk
+
 namespace {
 
 // Block-wide max of non-negative floats; every thread gets the result.
@@ -315,6 +321,57 @@ __global__ __launch_bounds__(256) void dyn_quant_kernel(const float* __restrict_
   }
 }
 
+// Pass 2 of quant8_dyn writing q in the row-pair layout the ping-pong GEMM tiles read (rows 2i
+// and 2i+1 interleaved by 64-byte K chunks: element (m, k) at byte (m >> 1) * 2 ldq + (k >> 6) *
+// 128 + (m & 1) * 64 + (k & 63); ldq % 64 == 0, K % 8 == 0, x rows 16-byte aligned).  A block
+// takes whole row pairs; thread t writes 8-byte items t, t + 256, ... of the pair's 2 ldq bytes
+// (contiguous stores), each from 8 consecutive elements of one x row.  Bytes past K (and the
+// second row of a last pair when M is odd) are written as 0 and never read.
+__global__ __launch_bounds__(256) void dyn_quant_pair_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                             int64_t ldx, const float* __restrict__ partial,
+                                                             int nparts, int8_t* __restrict__ q, int64_t ldq,
+                                                             int32_t* __restrict__ e_out,
+                                                             int32_t* __restrict__ erow) {
+  __shared__ float red[4];
+  float am = 0.0f;
+  for (int j = threadIdx.x; j < nparts; j += 256) am = fmaxf(am, partial[j]);
+  am = block_max<256>(am, red);
+  const int e = pow2_exponent(am);
+  const float sc = pow2f(e);
+  if (blockIdx.x == 0 && threadIdx.x == 0) e_out[0] = e;
+  if (erow)
+    for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < M; r += (int64_t)gridDim.x * 256) erow[r] = e;
+  const int64_t npair = (M + 1) >> 1;
+  const int per = (int)(ldq >> 2);  // 8-byte items per row pair
+  constexpr int U = 4;
+  for (int64_t p = blockIdx.x; p < npair; p += gridDim.x) {
+    int8_t* qp = q + p * 2 * ldq;
+    for (int r0 = threadIdx.x; r0 < per; r0 += 256 * U) {
+      float4 v[U][2];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int o = (r0 + 256 * u) * 8;
+        const int64_t m = 2 * p + ((o >> 6) & 1);
+        const int64_t k = (int64_t)(o >> 7) * 64 + (o & 63);
+        ok[u] = r0 + 256 * u < per && m < M && k < K;
+        if (ok[u]) {
+          const float4* src = (const float4*)(x + m * ldx + k);
+          v[u][0] = ld_nt(src);
+          v[u][1] = ld_nt(src + 1);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (r0 + 256 * u >= per) continue;
+        v2u32 out = v2u32{0u, 0u};
+        if (ok[u]) out = v2u32{quant_pow2_x4(v[u][0], sc), quant_pow2_x4(v[u][1], sc)};
+        *(v2u32*)(qp + (int64_t)(r0 + 256 * u) * 8) = out;
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
 }
@@ -334,9 +391,82 @@ int launch_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t*
   return lsk::check_launch("dyn_quant_kernel");
 }
 
+// quant8_dyn into the row-pair layout (ldq % 64 == 0, K % 8 == 0, x rows 16-byte aligned).
+int launch_quant8_dyn_pair(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, int32_t* e_out,
+                           int32_t* erow, float* partial, hipStream_t s) {
+  const int64_t total = M * K;
+  const int flat = (ldx == K && ((uintptr_t)x % 16) == 0) ? 1 : 0;
+  int64_t blocks = flat ? (total + 256 * 16 - 1) / (256 * 16) : M;
+  blocks = blocks < 1 ? 1 : (blocks > kDynBlocks ? kDynBlocks : blocks);
+  hipLaunchKernelGGL(dyn_amax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat, partial);
+  int rc = lsk::check_launch("dyn_amax_kernel");
+  if (rc) return rc;
+  int64_t qblocks = (M + 1) / 2;
+  qblocks = qblocks < 1 ? 1 : (qblocks > kDynBlocks ? kDynBlocks : qblocks);
+  hipLaunchKernelGGL(dyn_quant_pair_kernel, dim3((unsigned)qblocks), dim3(256), 0, s, x, M, K, ldx,
+                     (const float*)partial, (int)blocks, q, ldq, e_out, erow);
+  return lsk::check_launch("dyn_quant_pair_kernel");
+}
+
+// Workspace of lsk_linear_dyn: the quant8_dyn partial maxima, the per-row exponents and q
+// (rows rounded up to a pair, K up to a multiple of 64), each 256-byte aligned.
+struct LinDynWs {
+  int64_t partial, erow, q, bytes;
+};
+LinDynWs lindyn_layout(int64_t M, int64_t K) {
+  auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
+  LinDynWs l;
+  l.partial = 0;
+  l.erow = up((int64_t)kDynBlocks * 4);
+  l.q = l.erow + up(M * 4);
+  l.bytes = l.q + up(((M + 1) & ~(int64_t)1) * ((K + 63) / 64 * 64));
+  return l;
+}
+
 }  // namespace
 
 extern "C" int64_t lsk_quant8_dyn_workspace(void) { return (int64_t)kDynBlocks * sizeof(float); }
+
+extern "C" int64_t lsk_linear_dyn_workspace(int64_t M, int64_t K) {
+  if (M < 0 || K < 0) return -1;
+  return lindyn_layout(M, K).bytes;
+}
+
+extern "C" int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t ldw,
+                              int64_t N, int ew, float* y, int64_t ldy, int32_t* ex_out, int stages, void* workspace,
+                              int64_t workspace_bytes, void* stream) {
+  LSK_REQUIRE(stages >= 1 && stages <= 3, "lsk_linear_dyn: stages=%d not 1, 2 or 3", stages);
+  LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_linear_dyn: negative size M=%lld N=%lld K=%lld", (long long)M,
+              (long long)N, (long long)K);
+  LSK_REQUIRE(K <= 133144, "lsk_linear_dyn: K=%lld exceeds the int32-exact bound 133144", (long long)K);
+  LSK_REQUIRE(ldx >= K && ldw >= K && ldy >= N, "lsk_linear_dyn: leading dimension too small");
+  LSK_REQUIRE(ex_out || !(stages & 1), "lsk_linear_dyn: ex_out is required");
+  const LinDynWs l = lindyn_layout(M, K);
+  LSK_REQUIRE(workspace && workspace_bytes >= l.bytes && ((uintptr_t)workspace & 255) == 0,
+              "lsk_linear_dyn: workspace of %lld bytes (256-byte aligned) required (%lld given)", (long long)l.bytes,
+              (long long)workspace_bytes);
+  LSK_REQUIRE(M * K == 0 || (x && w), "lsk_linear_dyn: null pointer");
+  LSK_REQUIRE(M * N == 0 || y, "lsk_linear_dyn: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  float* partial = (float*)(ws + l.partial);
+  int32_t* erow = (int32_t*)(ws + l.erow);
+  int8_t* q = (int8_t*)(ws + l.q);
+  // the row-pair layout when every tile of the GEMM is a ping-pong tile; row-major otherwise
+  const int64_t kp = (K + 63) / 64 * 64;
+  const bool pair = M > 0 && N > 0 && K > 0 && K % 8 == 0 && ldx % 4 == 0 && ((uintptr_t)x % 16) == 0 &&
+                    lsk::gemm_takes_pp(w, ldw, M, N, K, kp);
+  const int64_t ldq = pair ? kp : (K + 15) / 16 * 16;
+  if (stages & 1) {
+    const int rc = pair ? launch_quant8_dyn_pair(x, M, K, ldx, q, ldq, ex_out, erow, partial, s)
+                        : launch_quant8_dyn(x, M, K, ldx, q, ldq, ex_out, erow, partial, s);
+    if (rc) return rc;
+  }
+  if (!(stages & 2) || M == 0 || N == 0) return LSK_OK;
+  EpiParams ep{LSK_EPI_POW2, LSK_F32, nullptr, nullptr, nullptr, erow, nullptr, ew, y, ldy};
+  ep.a_pair = pair ? 1 : 0;
+  return lsk::launch_gemm(q, ldq, w, ldw, M, N, K, ep, s);
+}
 
 extern "C" int lsk_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
                               int32_t* e_out, int32_t* erow_out, void* workspace, int64_t workspace_bytes,

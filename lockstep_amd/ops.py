@@ -277,6 +277,37 @@ def quant8_dyn(x: torch.Tensor, erow: bool = False):
     return (q, e, er) if erow else (q, e)
 
 
+def linear_dyn(x: torch.Tensor, w_nk: torch.Tensor, ew: int, stages: int = 3, work=None, y=None, ex=None):
+    """quant8_dyn of x [T, K] binary32 and the exact GEMM with w_nk [N, K] int8 under the POW2
+    dequant 2^-(ex + ew), in one call (lsk_linear_dyn).  Returns (y binary32 [T, N], ex int32 [1]
+    on the device).  stages 1 / 2 run only the quant / only the GEMM (the same work buffer
+    carries q between them), for timing the GEMM alone."""
+    L.require_cuda(x, w_nk, what="linear_dyn")
+    x = x.to(torch.float32)
+    if x.dim() != 2 or w_nk.dim() != 2 or w_nk.dtype != torch.int8 or w_nk.shape[1] != x.shape[1]:
+        raise ValueError("linear_dyn: x [T, K] binary32 and w [N, K] int8 expected, got %s and %s %s"
+                         % (tuple(x.shape), tuple(w_nk.shape), w_nk.dtype))
+    if x.shape[1] > 0 and x.stride(1) != 1:
+        x = x.contiguous()
+    if w_nk.shape[1] > 0 and w_nk.stride(1) != 1:
+        w_nk = w_nk.contiguous()
+    M, K = x.shape
+    N = w_nk.shape[0]
+    if y is None:
+        y = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    if ex is None:
+        ex = torch.empty((1,), dtype=torch.int32, device=x.device)
+    nbytes = L.load().lsk_linear_dyn_workspace(M, K)
+    if work is None:
+        work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
+    elif work.numel() < nbytes:
+        raise ValueError("linear_dyn: work buffer of %d bytes, %d needed" % (work.numel(), nbytes))
+    L.call("lsk_linear_dyn", L.ptr(x), M, K, x.stride(0) if M > 1 else max(K, 1), L.ptr(w_nk),
+           w_nk.stride(0) if N > 1 else max(K, 1), N, int(ew), L.ptr(y), y.stride(0) if M > 1 else max(N, 1),
+           L.ptr(ex), int(stages), L.ptr(work), work.numel(), L.stream_of(x))
+    return y, ex
+
+
 OP_SILU, OP_SIGMOID, OP_ACT_SILU, OP_ACT_SWIGLUOAI = 0, 1, 2, 3
 
 

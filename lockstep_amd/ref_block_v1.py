@@ -85,10 +85,7 @@ def linear_dyn(x, W8, ew):
     L.require_cuda(x, W8, what="linear_dyn")
     if x.dim() != 2:
         raise ValueError("linear_dyn: x must be [T, K], got %s" % (tuple(x.shape),))
-    q8, ex, erow = ops.quant8_dyn(x, erow=True)
-    w_nk = ops.weight_nk(_as_int8(W8))
-    y = ops.gemm(q8, w_nk, L.EPI_POW2, L.LSK_F32, erow=erow, shift=int(ew))
-    return y, ex
+    return ops.linear_dyn(x, ops.weight_nk(_as_int8(W8)), int(ew))
 
 
 def _as_int8(t):

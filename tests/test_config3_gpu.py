@@ -149,6 +149,36 @@ def test_quant8_dyn_edge_cases():
     assert e_np == e_ref and np.array_equal(q_np, q_ref)
 
 
+@pytest.mark.parametrize("T,N,K", [(301, 520, 3600), (256, 512, 64), (1000, 264, 208), (64, 320, 192),
+                                   (24, 256, 128), (200, 130, 100), (513, 1000, 8)])
+def test_linear_dyn_operand_layouts(T, N, K):
+    """linear_dyn where the quantised operand takes the row-pair layout (ping-pong tiles: odd T, K
+    not a multiple of 64, a single 64-byte chunk, partial tiles) and where it stays row-major (the
+    128x128 tile, the decode GEMV, K % 16 != 0 on the generic kernel, K = 8), against the oracle;
+    the quant-only and GEMM-only stages give the same y."""
+    from lockstep_amd import ops
+    from lockstep_amd import ref_block_v1 as RB
+
+    say("linear_dyn layouts: T=%d N=%d K=%d" % (T, N, K))
+    g = np.random.default_rng(T * 7 + K)
+    x = g.standard_normal((T, K)).astype(F32)
+    W8 = g.integers(-127, 128, (N, K), dtype=np.int8)
+    xd, Wd = torch.from_numpy(x).to(dev()), torch.from_numpy(W8).to(dev())
+    y, ex = RB.linear_dyn(xd, Wd.t(), 5)
+    q_ref, e_ref = C.quant8_dyn(x)
+    assert int(ex[0].item()) == e_ref
+    ref = C.dequant_pow2(C.gemm_int(q_ref, W8.T.astype(np.int64)), e_ref + 5)
+    assert np.array_equal(bits(y), f32_bits(ref))
+    from lockstep_amd import _lib as L
+    work = torch.empty((L.load().lsk_linear_dyn_workspace(T, K),), dtype=torch.uint8, device=dev())
+    y2 = torch.full((T, N), float("nan"), device=dev())
+    ex2 = torch.zeros((1,), dtype=torch.int32, device=dev())
+    ops.linear_dyn(xd, Wd, 5, stages=1, work=work, y=y2, ex=ex2)
+    assert int(ex2[0].item()) == e_ref and bool(torch.isnan(y2).all())
+    ops.linear_dyn(xd, Wd, 5, stages=2, work=work, y=y2, ex=ex2)
+    assert torch.equal(y2.view(torch.int32), y.view(torch.int32))
+
+
 def test_linear_dyn_partial_tiles_and_graph_capture():
     """linear_dyn on shapes whose tiles are partial (general epilogue) and whole (fast POW2
     epilogue), and replayed from a captured HIP graph: every replay equals the eager result."""
