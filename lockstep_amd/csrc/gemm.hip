@@ -1442,9 +1442,21 @@ extern "C" int lsk_gemm_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int6
   return lsk::launch_gemm(a, lda, w, ldw, M, N, K, ep, (hipStream_t)stream);
 }
 
+namespace lsk {
+bool rowquant_pair_ok(const void* x, int x_dtype, int64_t ldx, int64_t K);
+int rowquant_pair(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* asc,
+                  hipStream_t s);
+}  // namespace lsk
+
+// The quantised rows' share of lsk_w8a8_matmul's workspace: room for either layout (row-major
+// rows of K rounded up to 16, or row pairs of K rounded up to 64).
+static int64_t w8a8_q_bytes(int64_t M, int64_t K) {
+  const int64_t major = M * ((K + 15) / 16 * 16), pair = ((M + 1) & ~(int64_t)1) * ((K + 63) / 64 * 64);
+  return ((major > pair ? major : pair) + 255) / 256 * 256;
+}
+
 extern "C" int64_t lsk_w8a8_matmul_workspace(int64_t M, int64_t K) {
-  const int64_t ldq = (K + 15) / 16 * 16;
-  return ((M * ldq + 255) / 256) * 256 + ((M * 4 + 255) / 256) * 256;
+  return w8a8_q_bytes(M, K) + ((M * 4 + 255) / 256) * 256;
 }
 
 extern "C" int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
@@ -1459,13 +1471,22 @@ extern "C" int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t 
   LSK_REQUIRE(workspace && workspace_bytes >= need, "lsk_w8a8_matmul: workspace of %lld bytes needed",
               (long long)need);
   LSK_REQUIRE(((uintptr_t)workspace & 255) == 0, "lsk_w8a8_matmul: workspace must be 256-byte aligned");
-  const int64_t ldq = (K + 15) / 16 * 16;
+  // the row-pair layout when every tile of the GEMM is a ping-pong tile; row-major otherwise
+  const int64_t kp = (K + 63) / 64 * 64;
+  const bool pair = lsk::rowquant_pair_ok(x, x_dtype, ldx, K) && lsk::gemm_takes_pp(w, ldw, M, N, K, kp);
+  const int64_t ldq = pair ? kp : (K + 15) / 16 * 16;
   int8_t* q = (int8_t*)workspace;
-  float* asc = (float*)((char*)workspace + ((M * ldq + 255) / 256) * 256);
-  rc = lsk_rowquant(x, x_dtype, M, K, ldx, q, ldq, asc, stream);
-  if (rc) return rc;
-  return lsk_gemm_w8a8(q, ldq, w, ldw, M, N, K, order, asc, ws, bias, nullptr, nullptr, 0, out, out_dtype, ldo,
-                       stream);
+  float* asc = (float*)((char*)workspace + w8a8_q_bytes(M, K));
+  if (!pair)
+    return (rc = lsk_rowquant(x, x_dtype, M, K, ldx, q, ldq, asc, stream))
+               ? rc
+               : lsk_gemm_w8a8(q, ldq, w, ldw, M, N, K, order, asc, ws, bias, nullptr, nullptr, 0, out, out_dtype,
+                               ldo, stream);
+  LSK_REQUIRE(x && w && out && ldw >= K && ldo >= N, "lsk_w8a8_matmul: bad operand");
+  if ((rc = lsk::rowquant_pair(x, x_dtype, M, K, ldx, q, ldq, asc, (hipStream_t)stream))) return rc;
+  EpiParams ep{order, out_dtype, ws, asc, bias, nullptr, nullptr, 0, out, ldo};
+  ep.a_pair = 1;
+  return lsk::launch_gemm(q, ldq, w, ldw, M, N, K, ep, (hipStream_t)stream);
 }
 
 extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, int64_t N, int order,

@@ -106,7 +106,10 @@ __global__ __launch_bounds__(THREADS) void rowquant_kernel(const void* __restric
 // Single-pass row quant: one block per row, the row held in registers (NV chunks of 8
 // elements per thread, K <= 8 * NV * THREADS), so x is read from memory once.  Same
 // arithmetic as rowquant_kernel: exact amax, asc = fl32(max(amax, 1e-8) / 127), q = clamp(rint(x / asc)).
-template <int THREADS, int NV, int DT>
+// PAIR: q in the row-pair layout of the ping-pong GEMM tiles (rows 2i and 2i+1 interleaved by
+// 64-byte K chunks: element (m, k) at byte (m >> 1) * 2 ldq + (k >> 6) * 128 + (m & 1) * 64 +
+// (k & 63); ldq % 64 == 0).
+template <int THREADS, int NV, int DT, bool PAIR = false>
 __global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __restrict__ x, int64_t K, int64_t ldx,
                                                                int8_t* __restrict__ q, int64_t ldq,
                                                                float* __restrict__ asc) {
@@ -130,7 +133,7 @@ __global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __res
   am = fmaxf(am, kAmaxFloor);
   const float s = f32_div(am, 127.0f), rs = f32_div(1.0f, s);
   if (tid == 0) asc[m] = s;
-  int8_t* qrow = q + m * ldq;
+  int8_t* qrow = PAIR ? q + (m >> 1) * 2 * ldq + (m & 1) * 64 : q + m * ldq;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int64_t c = tid + (int64_t)j * THREADS;
@@ -140,23 +143,24 @@ __global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __res
       for (int e = 0; e < 4; ++e) lo |= ((uint32_t)(uint8_t)quant_one(v[j][e], s, rs)) << (8 * e);
 #pragma unroll
       for (int e = 0; e < 4; ++e) hi |= ((uint32_t)(uint8_t)quant_one(v[j][4 + e], s, rs)) << (8 * e);
-      ((uint2*)qrow)[c] = make_uint2(lo, hi);
+      // 8 elements from K byte 8c: ((8c) >> 6) * 128 + (8c & 63) in the row-pair layout
+      *(uint2*)(qrow + (PAIR ? (c >> 3) * 128 + (c & 7) * 8 : c * 8)) = make_uint2(lo, hi);
     }
   }
 }
 
-template <int THREADS, int NV>
+template <int THREADS, int NV, bool PAIR = false>
 int launch_rowquant_reg(const void* x, int dt, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* asc,
                         hipStream_t s) {
   if (dt == LSK_F32)
-    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_F32>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K, ldx,
-                       q, ldq, asc);
-  else if (dt == LSK_BF16)
-    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_BF16>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K,
+    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_F32, PAIR>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K,
                        ldx, q, ldq, asc);
+  else if (dt == LSK_BF16)
+    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_BF16, PAIR>), dim3((unsigned)M), dim3(THREADS), 0, s, x,
+                       K, ldx, q, ldq, asc);
   else
-    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_F16>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K, ldx,
-                       q, ldq, asc);
+    hipLaunchKernelGGL((rowquant_reg_kernel<THREADS, NV, LSK_F16, PAIR>), dim3((unsigned)M), dim3(THREADS), 0, s, x, K,
+                       ldx, q, ldq, asc);
   return lsk::check_launch("rowquant_reg_kernel");
 }
 
@@ -424,6 +428,32 @@ LinDynWs lindyn_layout(int64_t M, int64_t K) {
 }
 
 }  // namespace
+
+namespace lsk {
+// Whether rowquant_pair can quantise x (the single-pass register kernels: K % 8 == 0, K <= 32768,
+// 16-byte aligned rows).
+bool rowquant_pair_ok(const void* x, int x_dtype, int64_t ldx, int64_t K) {
+  const int esz = x_dtype == LSK_F32 ? 4 : 2;
+  return K > 0 && K % 8 == 0 && K <= 32768 && ldx % 8 == 0 && ((uintptr_t)x % 16) == 0 && ((ldx * esz) % 16) == 0 &&
+         (x_dtype == LSK_F32 || x_dtype == LSK_BF16 || x_dtype == LSK_F16);
+}
+
+// The contract's per-row int8 quant (as lsk_rowquant) with q in the row-pair layout (ldq % 64 == 0).
+int rowquant_pair(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, float* asc,
+                  hipStream_t s) {
+  LSK_REQUIRE(rowquant_pair_ok(x, x_dtype, ldx, K) && ldq % 64 == 0 && ldq >= K && ((uintptr_t)q % 64) == 0 &&
+                  M <= 0x7fffffff,
+              "rowquant_pair: unsupported operand (K=%lld ldx=%lld ldq=%lld)", (long long)K, (long long)ldx,
+              (long long)ldq);
+  if (M == 0) return LSK_OK;
+  const int64_t K8 = K >> 3;
+  if (K8 <= 256) return launch_rowquant_reg<256, 1, true>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+  if (K8 <= 512) return launch_rowquant_reg<256, 2, true>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+  if (K8 <= 1024) return launch_rowquant_reg<256, 4, true>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+  if (K8 <= 2048) return launch_rowquant_reg<512, 4, true>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+  return launch_rowquant_reg<512, 8, true>(x, x_dtype, M, K, ldx, q, ldq, asc, s);
+}
+}  // namespace lsk
 
 extern "C" int64_t lsk_quant8_dyn_workspace(void) { return (int64_t)kDynBlocks * sizeof(float); }
 
