@@ -183,12 +183,13 @@ def block_section(torch, args):
         work = torch.empty((L.load().lsk_linear_dyn_workspace(T, K),), dtype=torch.uint8, device=dev)
         out = torch.empty((T, N), dtype=torch.float32, device=dev)
         ex = torch.empty((1,), dtype=torch.int32, device=dev)
-        ops.linear_dyn(x, W8, BLOCK_EW, stages=1, work=work, y=out, ex=ex)
-        fn = lambda: ops.linear_dyn(x, W8, BLOCK_EW, stages=2, work=work, y=out, ex=ex)  # noqa: E731
+        wp = RB.row_pairs_of(W8)
+        ops.linear_dyn(x, W8, BLOCK_EW, stages=1, work=work, y=out, ex=ex, w_pairs=wp)
+        fn = lambda: ops.linear_dyn(x, W8, BLOCK_EW, stages=2, work=work, y=out, ex=ex, w_pairs=wp)  # noqa: E731
         for _ in range(2):
             fn()
         gemm_ms.append(_events_time(torch, fn, max(args.steps, 5)))
-        del work, out, ex
+        del work, out, ex, wp
     achieved = ops_step / (sum(gemm_ms) * 1e-3) / 1e12
     per_site = {name: {"site_us": round(t * 1e3, 1), "gemm_us": round(gk * 1e3, 1),
                        "quant8_dyn_us": round((t - gk) * 1e3, 1), "TOPS": round(o / (t * 1e-3) / 1e12, 1),
@@ -200,7 +201,7 @@ def block_section(torch, args):
             "T": T, "per_site": per_site,
             "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                          "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                         "kernel": "gemm_i8_pp_pow2_persist_kernel (row-pair A operand, POW2 epilogue, binary32 "
+                         "kernel": "gemm_i8_pp_pow2_persist_kernel (row-pair operands, POW2 epilogue, binary32 "
                                    "out) with its 256x128 column tails",
                          "note": "2*T*N*K int8 ops of the four GEMMs / the sum of their average launch times "
                                  "(HIP events on the launch stream, each site's GEMM alone on its quantised "

@@ -261,13 +261,24 @@ int lsk_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q,
  * (row stride ldw); y [M, N] binary32 (row stride ldy); ex_out[0] = ex.  q stays in the workspace
  * (lsk_linear_dyn_workspace(M, K) bytes, 256-byte aligned), written in the layout the GEMM tiles
  * read fastest (rows paired by 64-byte K chunks when every tile is a ping-pong tile).  Three
- * launches, nothing to clear beforehand (graph-capturable).  stages: 3 the whole site; 1 only the
- * quant (q and the exponents into the workspace, ex_out), 2 only the GEMM from a workspace that a
- * stage-1 call with the same arguments filled (to time the GEMM alone). */
+ * launches, nothing to clear beforehand (graph-capturable).  w_pairs: null, or the same weight in
+ * the row-pair layout (lsk_pack_row_pairs), which the GEMM then reads when q takes that layout.
+ * stages: 3 the whole site; 1 only the quant (q and the exponents into the workspace, ex_out), 2
+ * only the GEMM from a workspace that a stage-1 call with the same arguments filled (to time the
+ * GEMM alone). */
 int64_t lsk_linear_dyn_workspace(int64_t M, int64_t K);
-int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t ldw, int64_t N,
-                   int ew, float* y, int64_t ldy, int32_t* ex_out, int stages, void* workspace,
-                   int64_t workspace_bytes, void* stream);
+int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t ldw,
+                   const int8_t* w_pairs, int64_t N, int ew, float* y, int64_t ldy, int32_t* ex_out, int stages,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* No counterpart in the reference: a weight w [N, K] int8 (row stride ldw; K and ldw multiples of
+ * 16, 16-byte aligned) copied into the row-pair layout the GEMM tiles read whole 128-byte lines
+ * of -- rows 2i and 2i+1 interleaved by 64-byte K chunks, element (n, k) at byte (n >> 1) * 2 kp
+ * + (k >> 6) * 128 + (n & 1) * 64 + (k & 63) with kp = (K + 63) / 64 * 64 -- into out
+ * (lsk_row_pairs_bytes(N, K) bytes; padding bytes 0), for lsk_linear_dyn's w_pairs.  Made once per
+ * weight (a prepared weight, like the reference's arm-time weight quant). */
+int64_t lsk_row_pairs_bytes(int64_t N, int64_t K);
+int lsk_pack_row_pairs(const int8_t* w, int64_t N, int64_t K, int64_t ldw, int8_t* out, void* stream);
 
 /* ---------------------------------------------------------------- the MXFP4 operand */
 

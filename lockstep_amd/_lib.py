@@ -58,7 +58,9 @@ SIGNATURES = {
     "lsk_quant8_dyn_workspace": (_I64, []),
     "lsk_quant8_dyn": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P]),
     "lsk_linear_dyn_workspace": (_I64, [_I64, _I64]),
-    "lsk_linear_dyn": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I, _P, _I64, _P, _I, _P, _I64, _P]),
+    "lsk_linear_dyn": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I, _P, _I64, _P]),
+    "lsk_row_pairs_bytes": (_I64, [_I64, _I64]),
+    "lsk_pack_row_pairs": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lsk_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "lsk_act_elementwise": (_I, [_P, _P, _I64, _I, _P, _P, _P]),
     "lsk_table_scores": (_I, [_P, _I64, _P, _P, _P]),

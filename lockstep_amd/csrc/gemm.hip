@@ -265,25 +265,28 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
     }
   }
 
-  // (the row-pair layout: m0 is even, so the tile's rows start at byte m0 * lda as well; an odd M
-  // ends in a pair whose second row is never read)
-  const int64_t a_rows = ep.a_pair ? (int64_t)((M - m0 + 1) & ~1) : (int64_t)(M - m0);
+  // (the row-pair layouts: m0 and n0 are even, so a tile's rows start at byte m0 * lda / n0 * ldw
+  // as well; an odd M or N ends in a pair whose second row is never read)
+  const int ap = ep.pairs & 1, bp = ep.pairs & 2;
+  const int64_t a_rows = ap ? (int64_t)((M - m0 + 1) & ~1) : (int64_t)(M - m0);
+  const int64_t b_rows = bp ? (int64_t)((N - n0 + 1) & ~1) : (int64_t)(N - n0);
   const __amdgpu_buffer_rsrc_t ra_res = lsk::make_rsrc(A + (int64_t)m0 * lda, a_rows * lda);
-  const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)(N - n0) * ldw);
+  const __amdgpu_buffer_rsrc_t rb_res = lsk::make_rsrc(W + (int64_t)n0 * ldw, b_rows * ldw);
   typename C::RowsA pa;
   typename C::RowsB pb;
 #pragma unroll
   for (int j = 0; j < C::kLA; ++j) {
     int row, kb;
     lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
-    const uint32_t ro = ep.a_pair ? (uint32_t)((row >> 1) * 2 * lda + (row & 1) * 64) : (uint32_t)(row * lda);
+    const uint32_t ro = ap ? (uint32_t)((row >> 1) * 2 * lda + (row & 1) * 64) : (uint32_t)(row * lda);
     pa[j] = (m0 + row < M) ? ro : lsk::kOob;
   }
 #pragma unroll
   for (int j = 0; j < C::kLB; ++j) {
     int row, kb;
     lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
-    pb[j] = (n0 + row < N) ? (uint32_t)(row * ldw) : lsk::kOob;
+    const uint32_t ro = bp ? (uint32_t)((row >> 1) * 2 * ldw + (row & 1) * 64) : (uint32_t)(row * ldw);
+    pb[j] = (n0 + row < N) ? ro : lsk::kOob;
   }
   typename C::Acc acc;
 #pragma unroll
@@ -291,7 +294,7 @@ __device__ __forceinline__ void contract_tile(const int8_t* __restrict__ A, int 
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
 
-  main(acc, ra_res, pa, rb_res, pb, K, smem_pp, ep.a_pair);
+  main(acc, ra_res, pa, rb_res, pb, K, smem_pp, ep.pairs);
 
   // every wave is past its last read of the LDS ring
   float* sc_row = (float*)(smem_pp + C::kScaleOff);
@@ -359,8 +362,8 @@ __global__ __launch_bounds__(512, (RING == 3 && BKB == 64 ? 2 : 1)) void gemm_i8
   extern __shared__ __attribute__((aligned(16))) char smem_pp[];
   contract_tile<C>(A, lda, W, ldw, M, N, K, ep, vec_ok, smem_pp,
                    [](typename C::Acc& acc, __amdgpu_buffer_rsrc_t ra, const typename C::RowsA& pa,
-                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm, int apair) {
-                     lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra, pa, rb, pb, K_, sm, 0, apair);
+                      __amdgpu_buffer_rsrc_t rb, const typename C::RowsB& pb, int K_, char* sm, int pairs) {
+                     lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB>(acc, ra, pa, rb, pb, K_, sm, 0, pairs);
                    });
 }
 
@@ -405,13 +408,13 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_pow2_persist_kernel(const i
     for (int j = 0; j < C::kLA; ++j) {
       int row, kb;
       lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
-      t.pa[j] = ep.a_pair ? (uint32_t)((row >> 1) * 2 * lda + (row & 1) * 64) : (uint32_t)(row * lda);
+      t.pa[j] = (ep.pairs & 1) ? (uint32_t)((row >> 1) * 2 * lda + (row & 1) * 64) : (uint32_t)(row * lda);
     }
 #pragma unroll
     for (int j = 0; j < C::kLB; ++j) {
       int row, kb;
       lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
-      t.pb[j] = (uint32_t)(row * ldw);
+      t.pb[j] = (ep.pairs & 2) ? (uint32_t)((row >> 1) * 2 * ldw + (row & 1) * 64) : (uint32_t)(row * ldw);
     }
     t.erow = (tid < BM && ep.erow) ? __int_as_float(ep.erow[t.m0 + tid]) : 0.0f;
   };
@@ -425,9 +428,9 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_pow2_persist_kernel(const i
 #pragma unroll
       for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
     if (it == 0)
-      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, false>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, 0, ep.a_pair);
+      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, false>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, 0, ep.pairs);
     else
-      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, true>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, 0, ep.a_pair);
+      lsk::pp_mainloop<BM, BN, WM, WN, RING, BKB, true>(acc, cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, 0, ep.pairs);
     // every wave is past its last read of the ring; the previous tile's epilogue (the last
     // reader of sc_row) ended before this tile's first barrier
     if (tid < BM) sc_row[tid] = cur.erow;
@@ -435,7 +438,7 @@ __global__ __launch_bounds__(512, 1) void gemm_i8_pp_pow2_persist_kernel(const i
         lsk::make_rsrc((char*)ep.out + ((int64_t)cur.m0 * ep.ldo + cur.n0) * 4, (int64_t)(BM - 1) * ldo_bytes + BN * 4);
     if (v + (int)gridDim.x < tiles) {
       setup(v + gridDim.x, cur);
-      lsk::pp_issue_prologue<BM, BN, WM, WN, RING, BKB>(cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, ep.a_pair);
+      lsk::pp_issue_prologue<BM, BN, WM, WN, RING, BKB>(cur.ra, cur.pa, cur.rb, cur.pb, K, smem_pp, ep.pairs);
     }
     __syncthreads();
     pp_epilogue_direct_pow2<C>(acc, ro, ldo_bytes, ep.shift, sc_row);
@@ -1383,9 +1386,10 @@ bool gemm_takes_pp(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiParams& ep, hipStream_t s) {
   if (M == 0 || N == 0) return LSK_OK;
-  LSK_REQUIRE(!ep.a_pair || (lda % 64 == 0 && aligned16(a) && gemm_takes_pp(w, ldw, M, N, K, lda)),
-              "gemm: an A operand in the row-pair layout needs the ping-pong tiles (M=%lld N=%lld K=%lld lda=%lld)",
-              (long long)M, (long long)N, (long long)K, (long long)lda);
+  LSK_REQUIRE(!ep.pairs || (aligned16(a) && gemm_takes_pp(w, ldw, M, N, K, lda) && (!(ep.pairs & 1) || lda % 64 == 0) &&
+                            (!(ep.pairs & 2) || ldw % 64 == 0)),
+              "gemm: operands in the row-pair layout need the ping-pong tiles (M=%lld N=%lld K=%lld lda=%lld ldw=%lld)",
+              (long long)M, (long long)N, (long long)K, (long long)lda, (long long)ldw);
   const bool fast = tiles_fast(a, lda, w, ldw, M, N, K);
   if (!fast) {
     const int64_t total = M * N;
@@ -1485,7 +1489,7 @@ extern "C" int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t 
   LSK_REQUIRE(x && w && out && ldw >= K && ldo >= N, "lsk_w8a8_matmul: bad operand");
   if ((rc = lsk::rowquant_pair(x, x_dtype, M, K, ldx, q, ldq, asc, (hipStream_t)stream))) return rc;
   EpiParams ep{order, out_dtype, ws, asc, bias, nullptr, nullptr, 0, out, ldo};
-  ep.a_pair = 1;
+  ep.pairs = 1;
   return lsk::launch_gemm(q, ldq, w, ldw, M, N, K, ep, (hipStream_t)stream);
 }
 

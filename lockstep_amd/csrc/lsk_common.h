@@ -211,10 +211,10 @@ struct EpiParams {
   const void* wo = nullptr;
   int ko = 0;
   int wo_dtype = LSK_BF16;
-  // layout of the A operand (read by the ping-pong tile kernels only): 0 rows of lda bytes; 1
-  // row pairs interleaved by 64-byte K chunks (element (m, k) at byte (m >> 1) * 2 lda +
-  // (k >> 6) * 128 + (m & 1) * 64 + (k & 63), lda % 64 == 0)
-  int a_pair = 0;
+  // operand layouts (read by the ping-pong tile kernels only): bit 0 A, bit 1 B in the row-pair
+  // layout -- row pairs interleaved by 64-byte K chunks, element (m, k) at byte (m >> 1) * 2 ld +
+  // (k >> 6) * 128 + (m & 1) * 64 + (k & 63), ld % 64 == 0 -- instead of rows of ld bytes
+  int pairs = 0;
 };
 
 // The v2.5 side term of output (m, n) (lockstep_fullstack.py:549-557): sequential in j from +0,

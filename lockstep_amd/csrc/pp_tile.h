@@ -97,10 +97,11 @@ LSK_DEV void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Byte offset of K byte kk of an A row relative to the row's offset in the row-pair layout (apair
-// = 1: rows 2i and 2i+1 interleaved by 64-byte K chunks, so each 128-byte line holds one chunk of
-// both rows): kk + (kk & ~63); kk itself in the row-major layout.
-LSK_DEV uint32_t a_koff(int kk, int apair) { return (uint32_t)(apair ? kk + (kk & ~63) : kk); }
+// Byte offset of K byte kk of an operand row relative to the row's offset: kk in the row-major
+// layout; kk + (kk & ~63) in the row-pair layout (rows 2i and 2i+1 interleaved by 64-byte K
+// chunks, so each 128-byte line holds one chunk of both rows).  `pairs`: bit 0 the A operand,
+// bit 1 the B operand in the row-pair layout.
+LSK_DEV uint32_t pair_koff(int kk, int paired) { return (uint32_t)(paired ? kk + (kk & ~63) : kk); }
 
 // Issue this thread's direct-to-LDS loads of the first kRing stages of a tile into ring slots
 // 0 .. kRing-1, the whole ring (a persistent kernel's next tile, ahead of the current tile's
@@ -108,7 +109,7 @@ LSK_DEV uint32_t a_koff(int kk, int apair) { return (uint32_t)(apair ? kk + (kk 
 template <int BM, int BN, int WM, int WN, int RING, int BKB = 64>
 LSK_DEV void pp_issue_prologue(__amdgpu_buffer_rsrc_t ra, const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsA& pa,
                                __amdgpu_buffer_rsrc_t rb, const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb,
-                               int K, char* smem, int apair = 0) {
+                               int K, char* smem, int pairs = 0) {
   using C = PPCfg<BM, BN, WM, WN, RING, BKB>;
   const int tid = threadIdx.x, wave = wave_id();
   const int nk = (K + C::kBK - 1) / C::kBK;
@@ -123,7 +124,7 @@ LSK_DEV void pp_issue_prologue(__amdgpu_buffer_rsrc_t ra, const typename PPCfg<B
       pp_slot<C::kThreads, C::kChunks>(tid, j, r, kbyte);
       const int kk = k0 + kbyte;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t)(st + (j * C::kThreads + wave * 64) * 16), 16,
-                                               kk < K ? pa[j] + a_koff(kk, apair) : kOob, 0, 0, 0);
+                                               kk < K ? pa[j] + pair_koff(kk, pairs & 1) : kOob, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < C::kLB; ++j) {
@@ -131,7 +132,7 @@ LSK_DEV void pp_issue_prologue(__amdgpu_buffer_rsrc_t ra, const typename PPCfg<B
       pp_slot<C::kThreads, C::kChunks>(tid, j, r, kbyte);
       const int kk = k0 + kbyte;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t)(st + C::kStageA + (j * C::kThreads + wave * 64) * 16),
-                                               16, kk < K ? pb[j] + (uint32_t)kk : kOob, 0, 0, 0);
+                                               16, kk < K ? pb[j] + pair_koff(kk, pairs & 2) : kOob, 0, 0, 0);
     }
   }
 }
@@ -149,27 +150,29 @@ template <int BM, int BN, int WM, int WN, int RING, int BKB = 64, bool PRE = fal
 LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __amdgpu_buffer_rsrc_t ra,
                          const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
                          const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb, int K, char* smem, int na = 0,
-                         int apair = 0) {
+                         int pairs = 0) {
   using C = PPCfg<BM, BN, WM, WN, RING, BKB>;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int group = wave >> 2;
   const int wm = wave / WN, wn = wave % WN;
   const int nk = (K + C::kBK - 1) / C::kBK;
 
-  // per-slot chunk byte offsets (the LDS side of each load is fixed by the lane); A's K offset
-  // in its layout is k0a + kax[j] for stage start k0 (a multiple of 64): k0 + ka in the
-  // row-major layout, 2 k0 + ka + (ka & 64) in the row-pair layout
-  int ka[C::kLA], kb[C::kLB], kax[C::kLA];
+  // per-slot chunk byte offsets (the LDS side of each load is fixed by the lane); an operand's K
+  // offset in its layout is k0x + kx[j] for stage start k0 (a multiple of 64): k0 + k in the
+  // row-major layout, 2 k0 + k + (k & 64) in the row-pair layout
+  const int ap = pairs & 1, bp = (pairs >> 1) & 1;
+  int ka[C::kLA], kb[C::kLB], kax[C::kLA], kbx[C::kLB];
 #pragma unroll
   for (int j = 0; j < C::kLA; ++j) {
     int r;
     pp_slot<C::kThreads, C::kChunks>(tid, j, r, ka[j]);
-    kax[j] = ka[j] + (apair ? (ka[j] & 64) : 0);
+    kax[j] = ka[j] + (ap ? (ka[j] & 64) : 0);
   }
 #pragma unroll
   for (int j = 0; j < C::kLB; ++j) {
     int r;
     pp_slot<C::kThreads, C::kChunks>(tid, j, r, kb[j]);
+    kbx[j] = kb[j] + (bp ? (kb[j] & 64) : 0);
   }
 
   // issue this thread's direct-to-LDS loads of stage s; CHECK: the stage may reach past K
@@ -178,7 +181,7 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __
     constexpr bool kCheck = decltype(check)::value;
     char* st = smem + (s % C::kRing) * C::kStage;
     const int k0 = s * C::kBK;
-    const int k0a = apair ? 2 * k0 : k0;
+    const int k0a = ap ? 2 * k0 : k0, k0b = bp ? 2 * k0 : k0;
 #pragma unroll
     for (int j = 0; j < C::kLA; ++j) {
       const int kk = k0 + ka[j];
@@ -189,7 +192,7 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __
 #pragma unroll
     for (int j = 0; j < C::kLB; ++j) {
       const int kk = k0 + kb[j];
-      const uint32_t off = (!kCheck || kk < K) ? pb[j] + (uint32_t)kk : kOob;
+      const uint32_t off = (!kCheck || kk < K) ? pb[j] + (uint32_t)(k0b + kbx[j]) : kOob;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rb, (lds_void_t)(st + C::kStageA + (j * C::kThreads + wave * 64) * 16), 16, off, 0, 0, 0);
     }

@@ -376,6 +376,23 @@ __global__ __launch_bounds__(256) void dyn_quant_pair_kernel(const float* __rest
   }
 }
 
+// w [N, K] int8 (row stride ldw) into the row-pair layout (row stride (K + 63) / 64 * 64 per row of
+// a pair): one 16-byte chunk of the output per thread and step (two 8-byte stores); bytes past K,
+// and the second row of a last pair when N is odd, are 0.  K % 16 == 0.
+__global__ __launch_bounds__(256) void pack_row_pairs_kernel(const int8_t* __restrict__ w, int64_t N, int64_t K,
+                                                             int64_t ldw, int8_t* __restrict__ out) {
+  const int64_t kp = (K + 63) / 64 * 64;
+  const int64_t chunks = ((N + 1) >> 1) * 2 * kp / 16;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * 256) {
+    const int64_t o = c * 16;
+    const int64_t p = o / (2 * kp), r = o - p * 2 * kp;
+    const int64_t n = 2 * p + ((r >> 6) & 1), k = (r >> 7) * 64 + (r & 63);
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (n < N && k < K) v = *(const uint4*)(w + n * ldw + k);
+    store16_split(out + o, v.x, v.y, v.z, v.w);
+  }
+}
+
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
 }
@@ -462,9 +479,29 @@ extern "C" int64_t lsk_linear_dyn_workspace(int64_t M, int64_t K) {
   return lindyn_layout(M, K).bytes;
 }
 
+extern "C" int64_t lsk_row_pairs_bytes(int64_t N, int64_t K) {
+  if (N < 0 || K < 0) return -1;
+  return ((N + 1) & ~(int64_t)1) * ((K + 63) / 64 * 64);
+}
+
+extern "C" int lsk_pack_row_pairs(const int8_t* w, int64_t N, int64_t K, int64_t ldw, int8_t* out, void* stream) {
+  LSK_REQUIRE(N >= 0 && K >= 0 && ldw >= K, "lsk_pack_row_pairs: bad sizes N=%lld K=%lld ldw=%lld", (long long)N,
+              (long long)K, (long long)ldw);
+  LSK_REQUIRE(K % 16 == 0 && ldw % 16 == 0, "lsk_pack_row_pairs: K and ldw must be multiples of 16");
+  if (N == 0 || K == 0) return LSK_OK;
+  LSK_REQUIRE(w && out && ((uintptr_t)w % 16) == 0 && ((uintptr_t)out % 16) == 0,
+              "lsk_pack_row_pairs: null or unaligned pointer");
+  const int64_t chunks = lsk_row_pairs_bytes(N, K) / 16;
+  int64_t blocks = (chunks + 255) / 256;
+  blocks = blocks > 8192 ? 8192 : blocks;
+  hipLaunchKernelGGL(pack_row_pairs_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, w, N, K, ldw,
+                     out);
+  return lsk::check_launch("pack_row_pairs_kernel");
+}
+
 extern "C" int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t ldw,
-                              int64_t N, int ew, float* y, int64_t ldy, int32_t* ex_out, int stages, void* workspace,
-                              int64_t workspace_bytes, void* stream) {
+                              const int8_t* w_pairs, int64_t N, int ew, float* y, int64_t ldy, int32_t* ex_out,
+                              int stages, void* workspace, int64_t workspace_bytes, void* stream) {
   LSK_REQUIRE(stages >= 1 && stages <= 3, "lsk_linear_dyn: stages=%d not 1, 2 or 3", stages);
   LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_linear_dyn: negative size M=%lld N=%lld K=%lld", (long long)M,
               (long long)N, (long long)K);
@@ -494,7 +531,12 @@ extern "C" int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx,
   }
   if (!(stages & 2) || M == 0 || N == 0) return LSK_OK;
   EpiParams ep{LSK_EPI_POW2, LSK_F32, nullptr, nullptr, nullptr, erow, nullptr, ew, y, ldy};
-  ep.a_pair = pair ? 1 : 0;
+  ep.pairs = pair ? 1 : 0;
+  // the weight's row-pair copy with the quantised rows' row-pair layout
+  if (pair && w_pairs && lsk::gemm_takes_pp(w_pairs, kp, M, N, K, kp)) {
+    ep.pairs = 3;
+    return lsk::launch_gemm(q, ldq, w_pairs, kp, M, N, K, ep, s);
+  }
   return lsk::launch_gemm(q, ldq, w, ldw, M, N, K, ep, s);
 }
 

@@ -277,11 +277,27 @@ def quant8_dyn(x: torch.Tensor, erow: bool = False):
     return (q, e, er) if erow else (q, e)
 
 
-def linear_dyn(x: torch.Tensor, w_nk: torch.Tensor, ew: int, stages: int = 3, work=None, y=None, ex=None):
+def pack_row_pairs(w_nk: torch.Tensor) -> torch.Tensor:
+    """w_nk [N, K] int8 (K % 16 == 0) copied into the row-pair layout of the GEMM tiles
+    (lsk_pack_row_pairs): a flat int8 tensor of lsk_row_pairs_bytes(N, K) bytes."""
+    L.require_cuda(w_nk, what="pack_row_pairs")
+    if w_nk.dim() != 2 or w_nk.dtype != torch.int8:
+        raise ValueError("pack_row_pairs: w [N, K] int8 expected, got %s %s" % (tuple(w_nk.shape), w_nk.dtype))
+    if w_nk.shape[1] > 0 and (w_nk.stride(1) != 1 or w_nk.stride(0) % 16 != 0):
+        w_nk = w_nk.contiguous()
+    N, K = w_nk.shape
+    out = torch.empty((L.load().lsk_row_pairs_bytes(N, K),), dtype=torch.int8, device=w_nk.device)
+    L.call("lsk_pack_row_pairs", L.ptr(w_nk), N, K, w_nk.stride(0) if N > 1 else max(K, 16), L.ptr(out),
+           L.stream_of(w_nk))
+    return out
+
+
+def linear_dyn(x: torch.Tensor, w_nk: torch.Tensor, ew: int, stages: int = 3, work=None, y=None, ex=None,
+               w_pairs=None):
     """quant8_dyn of x [T, K] binary32 and the exact GEMM with w_nk [N, K] int8 under the POW2
     dequant 2^-(ex + ew), in one call (lsk_linear_dyn).  Returns (y binary32 [T, N], ex int32 [1]
     on the device).  stages 1 / 2 run only the quant / only the GEMM (the same work buffer
-    carries q between them), for timing the GEMM alone."""
+    carries q between them), for timing the GEMM alone.  w_pairs: pack_row_pairs(w_nk) or None."""
     L.require_cuda(x, w_nk, what="linear_dyn")
     x = x.to(torch.float32)
     if x.dim() != 2 or w_nk.dim() != 2 or w_nk.dtype != torch.int8 or w_nk.shape[1] != x.shape[1]:
@@ -302,8 +318,12 @@ def linear_dyn(x: torch.Tensor, w_nk: torch.Tensor, ew: int, stages: int = 3, wo
         work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     elif work.numel() < nbytes:
         raise ValueError("linear_dyn: work buffer of %d bytes, %d needed" % (work.numel(), nbytes))
+    if w_pairs is not None and (w_pairs.dtype != torch.int8 or w_pairs.device != x.device
+                                or w_pairs.numel() < L.load().lsk_row_pairs_bytes(N, K)):
+        raise ValueError("linear_dyn: w_pairs is not pack_row_pairs of a [%d, %d] weight" % (N, K))
     L.call("lsk_linear_dyn", L.ptr(x), M, K, x.stride(0) if M > 1 else max(K, 1), L.ptr(w_nk),
-           w_nk.stride(0) if N > 1 else max(K, 1), N, int(ew), L.ptr(y), y.stride(0) if M > 1 else max(N, 1),
+           w_nk.stride(0) if N > 1 else max(K, 1), L.ptr(w_pairs), N, int(ew), L.ptr(y),
+           y.stride(0) if M > 1 else max(N, 1),
            L.ptr(ex), int(stages), L.ptr(work), work.numel(), L.stream_of(x))
     return y, ex
 

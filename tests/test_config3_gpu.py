@@ -179,6 +179,62 @@ def test_linear_dyn_operand_layouts(T, N, K):
     assert torch.equal(y2.view(torch.int32), y.view(torch.int32))
 
 
+def test_pack_row_pairs_layout():
+    """lsk_pack_row_pairs against the layout written out in numpy: element (n, k) at byte
+    (n >> 1) * 2 kp + (k >> 6) * 128 + (n & 1) * 64 + (k & 63), kp = K rounded up to 64, padding 0;
+    odd N, K not a multiple of 64, a strided weight."""
+    from lockstep_amd import ops
+
+    g = np.random.default_rng(9)
+    for N, K, ld in [(257, 208, 208), (64, 64, 64), (3, 16, 48), (130, 1040, 1056)]:
+        full = g.integers(-127, 128, (N, ld), dtype=np.int8)
+        w = torch.from_numpy(full).to(dev())[:, :K]
+        got = ops.pack_row_pairs(w).cpu().numpy()
+        kp = (K + 63) // 64 * 64
+        want = np.zeros(((N + 1) // 2) * 2 * kp, np.int8)
+        n, k = np.meshgrid(np.arange(N), np.arange(K), indexing="ij")
+        want[(n >> 1) * 2 * kp + (k >> 6) * 128 + (n & 1) * 64 + (k & 63)] = full[:, :K]
+        assert np.array_equal(got, want), (N, K, ld)
+
+
+def test_linear_dyn_weight_copy_follows_the_weight():
+    """The row-pair weight copy linear_dyn keeps is remade when the weight changes in place (its
+    version counter) and when another tensor takes the same storage address."""
+    from lockstep_amd import ref_block_v1 as RB
+
+    g = np.random.default_rng(10)
+    T, N, K = 512, 258, 320
+    x = g.standard_normal((T, K)).astype(F32)
+    xd = torch.from_numpy(x).to(dev())
+    W8 = g.integers(-127, 128, (N, K), dtype=np.int8)
+    Wd = torch.from_numpy(W8).to(dev())
+    q_ref, e_ref = C.quant8_dyn(x)
+
+    def check(wnp, y):
+        ref = C.dequant_pow2(C.gemm_int(q_ref, wnp.T.astype(np.int64)), e_ref + 7)
+        assert np.array_equal(bits(y), f32_bits(ref))
+
+    y, _ = RB.linear_dyn(xd, Wd.t(), 7)
+    check(W8, y)
+    Wd.neg_()                                   # in place: the cached copy is stale
+    y, _ = RB.linear_dyn(xd, Wd.t(), 7)
+    check(-W8, y)
+    Wd[:, 5:9] = 3                              # in place through a view
+    W2 = -W8
+    W2[:, 5:9] = 3
+    y, _ = RB.linear_dyn(xd, Wd.t(), 7)
+    check(W2, y)
+    ptr = Wd.data_ptr()
+    del Wd
+    torch.cuda.synchronize()
+    W3 = g.integers(-127, 128, (N, K), dtype=np.int8)
+    Wn = torch.empty((N, K), dtype=torch.int8, device=dev())
+    Wn.copy_(torch.from_numpy(W3))              # often the freed block again
+    say("same storage address reused: %s" % (Wn.data_ptr() == ptr))
+    y, _ = RB.linear_dyn(xd, Wn.t(), 7)
+    check(W3, y)
+
+
 def test_linear_dyn_partial_tiles_and_graph_capture():
     """linear_dyn on shapes whose tiles are partial (general epilogue) and whole (fast POW2
     epilogue), and replayed from a captured HIP graph: every replay equals the eager result."""
