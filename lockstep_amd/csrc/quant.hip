@@ -353,17 +353,17 @@ __global__ __launch_bounds__(256) void dyn_quant_pair_kernel(const float* __rest
     for (int r0 = threadIdx.x; r0 < per; r0 += 256 * U) {
       float4 v[U][2];
       bool ok[U];
+      // every load issued before the first use, none under a branch (a lane without an element
+      // reads its pair's first row start and discards it)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int o = (r0 + 256 * u) * 8;
         const int64_t m = 2 * p + ((o >> 6) & 1);
         const int64_t k = (int64_t)(o >> 7) * 64 + (o & 63);
         ok[u] = r0 + 256 * u < per && m < M && k < K;
-        if (ok[u]) {
-          const float4* src = (const float4*)(x + m * ldx + k);
-          v[u][0] = ld_nt(src);
-          v[u][1] = ld_nt(src + 1);
-        }
+        const float4* src = (const float4*)(x + (ok[u] ? m * ldx + k : 2 * p * ldx));
+        v[u][0] = ld_nt(src);
+        v[u][1] = ld_nt(src + 1);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
