@@ -665,7 +665,9 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
     lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
     const int p = p0 + row;
     const int src = p < p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
-    pa[j] = src >= 0 ? (uint32_t)(src * a.lda) : lsk::kOob;
+    const uint32_t ro = (MODE == 1 && (a.pairs & 1)) ? (uint32_t)((src >> 1) * 2 * a.lda + (src & 1) * 64)
+                                                      : (uint32_t)(src * a.lda);
+    pa[j] = src >= 0 ? ro : lsk::kOob;
   }
 #pragma unroll
   for (int j = 0; j < C::kLB; ++j) {
@@ -682,7 +684,7 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
 
   // the wave's 32-row strips that hold rows of the tile (the others are neither multiplied nor stored)
   const int na = max(0, min(C::TM, (p1 - p0 - wm * C::WTM + 31) / 32));
-  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe, na);
+  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe, na, MODE == 1 ? (a.pairs & 1) : 0);
 
   // park the operands in LDS (past every wave's last ring read)
   float* sc_asc = (float*)(smem_moe + C::kScaleOff);
@@ -850,8 +852,8 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
   moe_tile<PPM, MODE>(a, smem_moe,
                       [](PPM::Acc& acc, __amdgpu_buffer_rsrc_t ra, const PPM::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
-                         const PPM::RowsB& pb, int K, char* sm, int na) {
-                        lsk::pp_mainloop<128, 256, 2, 4, 3, 64, false, true>(acc, ra, pa, rb, pb, K, sm, na);
+                         const PPM::RowsB& pb, int K, char* sm, int na, int pairs) {
+                        lsk::pp_mainloop<128, 256, 2, 4, 3, 64, false, true>(acc, ra, pa, rb, pb, K, sm, na, pairs);
                       });
 }
 
@@ -860,8 +862,8 @@ __global__ __launch_bounds__(512, 1) void moe_pp128_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
   moe_tile<PPM128, MODE>(a, smem_moe,
                          [](PPM128::Acc& acc, __amdgpu_buffer_rsrc_t ra, const PPM128::RowsA& pa,
-                            __amdgpu_buffer_rsrc_t rb, const PPM128::RowsB& pb, int K, char* sm, int na) {
-                           lsk::pp_mainloop<128, 256, 2, 4, 3, 128, false, true>(acc, ra, pa, rb, pb, K, sm, na);
+                            __amdgpu_buffer_rsrc_t rb, const PPM128::RowsB& pb, int K, char* sm, int na, int pairs) {
+                           lsk::pp_mainloop<128, 256, 2, 4, 3, 128, false, true>(acc, ra, pa, rb, pb, K, sm, na, pairs);
                          });
 }
 
@@ -870,8 +872,8 @@ __global__ __launch_bounds__(256, 2) void moe_w4_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
   moe_tile<W4M, MODE>(a, smem_moe,
                       [](W4M::Acc& acc, __amdgpu_buffer_rsrc_t ra, const W4M::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
-                         const W4M::RowsB& pb, int K, char* sm, int) {
-                        lsk::w4_mainloop<W4M>(acc, ra, pa, rb, pb, K, sm);
+                         const W4M::RowsB& pb, int K, char* sm, int, int) {
+                        lsk::w4_mainloop<W4M>(acc, ra, pa, rb, pb, K, sm);  // row-major A only
                       });
 }
 
@@ -1164,10 +1166,11 @@ __global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* _
 }
 
 // ---------------------------------------------------------------- requant and combine
-// rowquant of the activation output h (bf16 values), with the row maxima from the GEMM.
+// rowquant of the activation output h (bf16 values), with the row maxima from the GEMM; q row-major
+// [R, I], or with pair in the row-pair layout the down tiles read (I % 64 == 0).
 __global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __restrict__ h, const uint32_t* __restrict__ amax,
                                                           const int32_t* __restrict__ nrows, int I,
-                                                          int8_t* __restrict__ q, float* __restrict__ asc) {
+                                                          int8_t* __restrict__ q, float* __restrict__ asc, int pair) {
   const int R = *nrows;
   const int chunks = I / 8;
   const int64_t total = (int64_t)R * chunks;
@@ -1189,7 +1192,9 @@ __global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __rest
       if (j < 2) lo |= b << (16 * j);
       else hi |= b << (16 * (j - 2));
     }
-    *(uint2*)(q + p * I + c * 8) = make_uint2(lo, hi);
+    const int64_t k = (int64_t)c * 8;
+    const int64_t at = pair ? (p >> 1) * 2 * I + (k >> 6) * 128 + (p & 1) * 64 + (k & 63) : p * I + k;
+    *(uint2*)(q + at) = make_uint2(lo, hi);
   }
 }
 
@@ -1336,7 +1341,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.ccnt = (int32_t*)take(nchunks * E * 4);
   w.h = (uint16_t*)take(R * I * 2);
   w.h_amax = (uint32_t*)take((R + 2) * 4);  // + the two "some row flagged" words of block-scaled activations
-  w.qh = (int8_t*)take(R * I * qb);
+  w.qh = (int8_t*)take(((R + 1) & ~(int64_t)1) * I * qb);  // (room for a last row pair)
   w.asch = (float*)take(R * 4);
   w.slots = (uint16_t*)take(R * H * 2);
   w.xrot = rot_blk > 0 ? (float*)take(T * H * 4) : nullptr;
@@ -1649,6 +1654,9 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   // quantised in the general form) with the block exponents (T = 1 50 vs 116 us, T = 16 221 vs
   // 278 us, T = 24 281 vs 277 us)
   const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
+  // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
+  // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
+  const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && I % 64 == 0 && g_moe_w4 == 0;
 
   // up to 256 tokens: the dispatch and the row quant of x in one launch
   const bool prep_decode = T <= 256 && rb == 0 && mx != 2;
@@ -1795,13 +1803,14 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
     int64_t blocks = (R * (I / 8) + 255) / 256;
     blocks = blocks > 8192 ? 8192 : (blocks < 1 ? 1 : blocks);
     hipLaunchKernelGGL(moe_requant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w.h, w.h_amax, w.offs + E, (int)I,
-                       w.qh, w.asch);
+                       w.qh, w.asch, pair_down ? 1 : 0);
     if ((rc = lsk::check_launch("moe_requant_kernel"))) return rc;
   }
   MoeGemmArgs g2{};
   g2.A = w.qh;
   g2.lda = I;
-  g2.a_bytes = R * I * (mx ? 2 : 1);
+  g2.a_bytes = pair_down ? ((R + 1) & ~(int64_t)1) * I : R * I * (mx ? 2 : 1);
+  g2.pairs = pair_down ? 1 : 0;
   g2.w_bytes = H * a->ldw2;
   g2.a_scale = w.asch;
   g2.offs = w.offs;

@@ -198,11 +198,13 @@ def test_moe_grouped_gemm_variants(variant):
     """Every grouped-GEMM kernel (register-staged 128x128 tile, ping-pong 128x256 tile, the
     decode GEMV, the 128x256 tile on four waves, the ping-pong tile with 128-byte K stages) gives
     the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
-    their rows eight at a time), empty experts, a bias and SwiGLU-OAI."""
+    their rows eight at a time), empty experts, a bias and SwiGLU-OAI; an odd number of routed rows
+    (the down tiles' row-pair operand ends in a half pair)."""
     from lockstep_amd import _lib as L
     L.call("lsk_moe_select", variant)
     try:
         _run_case(300, 12, 4, 256, 192, seed=13)
+        _run_case(301, 8, 3, 256, 128, seed=17)
         _run_case(150, 6, 2, 320, 96, seed=14, bias=True, act="swigluoai")
         _run_case(5, 16, 4, 256, 128, seed=15)
     finally:
