@@ -189,7 +189,7 @@ LSK_DEV void load_chunk_routes(const int64_t* __restrict__ idx, const uint16_t* 
 // routed to e); base (LDS or global) is advanced by the caller.  mask: E x 8 words.
 LSK_DEV void place_chunk(const int32_t* ids, const uint16_t* wts, int T, int k, int E, int c0, const int32_t* base,
                          uint32_t* mask, int32_t* __restrict__ row_tok, int32_t* __restrict__ row_dst,
-                         float* __restrict__ row_w) {
+                         float* __restrict__ row_w, int wlo = 0, int whi = 256) {
   const int tid = threadIdx.x;
   for (int i = tid; i < E * 8; i += 256) mask[i] = 0;
   __syncthreads();
@@ -202,7 +202,7 @@ LSK_DEV void place_chunk(const int32_t* ids, const uint16_t* wts, int T, int k, 
     }
   }
   __syncthreads();
-  if (t < T) {
+  if (t < T && tid >= wlo && tid < whi) {  // (the rows of tokens wlo .. whi-1 of the chunk)
     for (int j = 0; j < k; ++j) {
       const int e = my[j];
       if (e < 0) continue;
@@ -393,9 +393,10 @@ __global__ __launch_bounds__(256) void moe_count_kernel(const int64_t* __restric
 }
 
 // Large T, step 2: each block sums the per-chunk counts itself (totals per expert and the
-// counts of the chunks before its own), derives the expert offsets, and places its chunk's rows
-// (chunks ascending inside each expert: token order); block 0 also writes the offsets and the
-// M-tile table.  LDS: tot / pre / offs [E, E, E + 1], the placement mask [E][8], the chunk's ids
+// counts of the chunks before its own), derives the expert offsets, and places a quarter of its
+// chunk's rows (block b: chunk b / 4, tokens 64 (b % 4) .. +63; chunks ascending inside each
+// expert: token order; four blocks per chunk spread the scattered row writes over more CUs);
+// block 0 also writes the offsets and the M-tile table.  LDS: tot / pre / offs [E, E, E + 1], the placement mask [E][8], the chunk's ids
 // [256 k] and weights [256 k] u16.
 __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restrict__ idx, const uint16_t* __restrict__ w,
                                                         int T, int k, int E, const int32_t* __restrict__ ccnt,
@@ -410,7 +411,7 @@ __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restric
   int32_t* ids = (int32_t*)(mask + 8 * E);
   uint16_t* wts = (uint16_t*)(ids + 256 * k);
   __shared__ int tmp[4];
-  const int c0 = blockIdx.x;
+  const int c0 = blockIdx.x >> 2, qr = blockIdx.x & 3;
   for (int e = threadIdx.x; e < E; e += 256) {
     int all = 0, before = 0;
     // the chunks' counts eight at a time, their loads issued together (one latency per eight)
@@ -428,14 +429,14 @@ __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restric
     pre[e] = before;
   }
   __syncthreads();
-  expert_offsets_and_tiles<256>(tot, E, offl, c0 == 0 ? tiles : nullptr, tmp);
+  expert_offsets_and_tiles<256>(tot, E, offl, blockIdx.x == 0 ? tiles : nullptr, tmp);
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += 256) {
-    if (c0 == 0) offs[e] = offl[e];
+    if (blockIdx.x == 0) offs[e] = offl[e];
     if (e < E) offl[e] += pre[e];  // this chunk's first row per expert
   }
   load_chunk_routes(idx, w, T, k, E, c0 * 256, ids, wts);  // ends with a barrier
-  place_chunk(ids, wts, T, k, E, c0 * 256, offl, mask, row_tok, row_dst, row_w);
+  place_chunk(ids, wts, T, k, E, c0 * 256, offl, mask, row_tok, row_dst, row_w, qr * 64, qr * 64 + 64);
 }
 
 __global__ __launch_bounds__(256) void widen_bf16_kernel(const uint16_t* __restrict__ x, int64_t n, float* __restrict__ y) {
@@ -1167,34 +1168,48 @@ __global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* _
 
 // ---------------------------------------------------------------- requant and combine
 // rowquant of the activation output h (bf16 values), with the row maxima from the GEMM; q row-major
-// [R, I], or with pair in the row-pair layout the down tiles read (I % 64 == 0).
+// [R, I], or with pair in the row-pair layout the down tiles read (I % 64 == 0).  One wave per
+// row (the row's scale and its reciprocal computed once), 8 elements per lane and step, two steps'
+// loads in flight; rows w, w + (waves in the grid), ...
 __global__ __launch_bounds__(256) void moe_requant_kernel(const uint16_t* __restrict__ h, const uint32_t* __restrict__ amax,
                                                           const int32_t* __restrict__ nrows, int I,
                                                           int8_t* __restrict__ q, float* __restrict__ asc, int pair) {
   const int R = *nrows;
   const int chunks = I / 8;
-  const int64_t total = (int64_t)R * chunks;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t p = i / chunks;
-    const int c = (int)(i - p * chunks);
+  const int lane = threadIdx.x & 63;
+  const int nwaves = gridDim.x * 4;
+  for (int p = blockIdx.x * 4 + wave_id(); p < R; p += nwaves) {
     const float s = f32_div(fmaxf(__uint_as_float(amax[p]), kAmaxFloor), 127.0f), rs = f32_div(1.0f, s);
-    if (c == 0) asc[p] = s;
-    const uint4 u = *(const uint4*)(h + p * I + c * 8);
-    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
-    uint32_t lo = 0, hi = 0;
+    if (lane == 0) asc[p] = s;
+    const uint16_t* hr = h + (int64_t)p * I;
+    int8_t* qr = pair ? q + (int64_t)(p >> 1) * 2 * I + (p & 1) * 64 : q + (int64_t)p * I;
+    for (int c0 = lane; c0 < chunks; c0 += 128) {
+      uint4 u[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float v0 = bf16_to_f32((uint16_t)(wd[j] & 0xffff));
-      const float v1 = bf16_to_f32((uint16_t)(wd[j] >> 16));
-      float q0 = fminf(fmaxf(rint_div8(v0, s, rs), -127.0f), 127.0f);
-      float q1 = fminf(fmaxf(rint_div8(v1, s, rs), -127.0f), 127.0f);
-      const uint32_t b = ((uint32_t)(uint8_t)(int8_t)(int)q0) | (((uint32_t)(uint8_t)(int8_t)(int)q1) << 8);
-      if (j < 2) lo |= b << (16 * j);
-      else hi |= b << (16 * (j - 2));
+      for (int t = 0; t < 2; ++t) {
+        const int c = c0 + 64 * t;
+        u[t] = *(const uint4*)(hr + (c < chunks ? c : c0) * 8);
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int c = c0 + 64 * t;
+        if (c >= chunks) continue;
+        const uint32_t wd[4] = {u[t].x, u[t].y, u[t].z, u[t].w};
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v0 = bf16_to_f32((uint16_t)(wd[j] & 0xffff));
+          const float v1 = bf16_to_f32((uint16_t)(wd[j] >> 16));
+          float q0 = fminf(fmaxf(rint_div8(v0, s, rs), -127.0f), 127.0f);
+          float q1 = fminf(fmaxf(rint_div8(v1, s, rs), -127.0f), 127.0f);
+          const uint32_t b = ((uint32_t)(uint8_t)(int8_t)(int)q0) | (((uint32_t)(uint8_t)(int8_t)(int)q1) << 8);
+          if (j < 2) lo |= b << (16 * j);
+          else hi |= b << (16 * (j - 2));
+        }
+        const int k = c * 8;
+        *(uint2*)(qr + (pair ? (k >> 6) * 128 + (k & 63) : k)) = make_uint2(lo, hi);
+      }
     }
-    const int64_t k = (int64_t)c * 8;
-    const int64_t at = pair ? (p >> 1) * 2 * I + (k >> 6) * 128 + (p & 1) * 64 + (k & 63) : p * I + k;
-    *(uint2*)(q + at) = make_uint2(lo, hi);
   }
 }
 
@@ -1723,7 +1738,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
                        ridx, (int)T, k,
                        (int)E, w.ccnt, w.tok_cnt, w.h_amax, nzero);
     if ((rc = lsk::check_launch("moe_count_kernel"))) return rc;
-    hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nchunks), dim3(256),
+    hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)(4 * nchunks)), dim3(256),
                        (size_t)(11 * E + 1) * 4 + (size_t)256 * k * 6, s, ridx, rwt, (int)T, k, (int)E, w.ccnt,
                        (int)nchunks, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w);
     if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
@@ -1800,7 +1815,7 @@ extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   } else if (mx) {
     if ((rc = lsk::launch_requant_bf16(w.h, w.h_amax, w.offs + E, R, (int)I, (uint16_t*)w.qh, w.asch, s))) return rc;
   } else {
-    int64_t blocks = (R * (I / 8) + 255) / 256;
+    int64_t blocks = (R + 3) / 4;  // a wave per row
     blocks = blocks > 8192 ? 8192 : (blocks < 1 ? 1 : blocks);
     hipLaunchKernelGGL(moe_requant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w.h, w.h_amax, w.offs + E, (int)I,
                        w.qh, w.asch, pair_down ? 1 : 0);

@@ -56,7 +56,8 @@ def test_conformance_vectors_on_gpu():
 
 # ------------------------------------------------------------------ row quant
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("shape", [(1, 16), (3, 37), (7, 512), (33, 4096), (2, 18944), (0, 64)])
+@pytest.mark.parametrize("shape", [(1, 16), (3, 37), (7, 512), (33, 4096), (2, 18944), (0, 64), (64, 16), (65, 520),
+                                   (200, 2048), (129, 4096), (70, 37)])
 def test_rowquant_parity(dtype, shape):
     from lockstep_amd import moe_ref as MR
     say("rowquant", dtype, shape)
