@@ -1328,10 +1328,15 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
 #undef LSK_RING
   }
   const int blocks = (N + 15) / 16;
-  // whole-row streaming through LDS wins over 64-byte row pieces for one activation tile over a
-  // long K (measured on MI355X at the Llama-3.1-8B decode shapes: down K=14336 M=8 15.1 vs 19.6 us;
-  // gate_up K=4096 M=8 30.7 vs 28.8 us; two activation tiles 2x slower)
-  const bool use_lds = g_gemv_mid == 2 || (g_gemv_mid == 0 && M <= 16 && K >= 8192);
+  // whole-row streaming through LDS wins over 64-byte row pieces for one activation tile (M <= 16)
+  // except where N leaves just over one round of 256 blocks or is very wide (measured on MI355X,
+  // graph replays over weight copies, us LDS / pieces: K = 3584 and N = 2048 .. 4096 at M = 8 / 16
+  // 5.9-7.0 / 7.1-7.9; N = 4608 10.8 / 10.4 and 11.9 / 11.4; N = 3584, K = 2048 / 5120 5.1-5.4 /
+  // 5.6-6.0 and 7.4-8.2 / 9.8-10.4; N = 14336, K = 4096 17.6 / 20.3 and 19.9 / 22.7; N = 28672,
+  // K = 4096 level at M = 8 (the whole w8a8_matmul call 33.3 / 32.2), 34.2 / 32.9 at M = 16;
+  // K = 14336 14.5 / 17.0 and 16.4 / 19.5; two activation tiles (M > 16) about 2x slower)
+  const bool use_lds = g_gemv_mid == 2 ||
+                       (g_gemv_mid == 0 && M <= 16 && (K >= 8192 || N <= 4096 || (N >= 8192 && N <= 16384)));
   if (use_lds) {
     // waves per block so that at least 1024 waves stream, each K-slice a whole number of
     // 512-byte stages
