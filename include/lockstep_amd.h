@@ -449,6 +449,12 @@ typedef struct {
   const int32_t* router_tab;     /* the [8192] FRAC table, as lsk_router_topk */
   int64_t* idx_out;              /* [T, k] */
   uint16_t* w_out;               /* [T, k] bf16 */
+  /* Kernel choice for this call only (no reference counterpart; results are the same bits either
+   * way): 0 keeps the calling thread's lsk_moe_select / lsk_moe_mx_select settings; select = v + 2
+   * applies lsk_moe_select(v) (v in [-1, 4]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
+   * (v in [0, 2]) to this call, leaving the thread's settings as they were. */
+  int select;
+  int mx_select;
 } lsk_moe_args;
 
 int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt);

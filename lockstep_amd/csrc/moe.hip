@@ -1595,8 +1595,25 @@ extern "C" int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int
   return moe_layout(nullptr, T, k, E, H, I, rot_blk, wfmt).bytes;
 }
 
+static int moe_forward_call(const lsk_moe_args* a, void* stream);
+
 extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(a, "lsk_moe_forward: null args");
+  LSK_REQUIRE(a->select >= 0 && a->select <= 6 && a->mx_select >= 0 && a->mx_select <= 3,
+              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 6] / [0, 3]", a->select, a->mx_select);
+  if (a->select == 0 && a->mx_select == 0) return moe_forward_call(a, stream);
+  // this call's kernel choice, the thread's own restored afterwards
+  const int force = g_moe_force, w4 = g_moe_w4, mxv = lsk::mx_variant();
+  if (a->select) lsk_moe_select(a->select - 2);
+  if (a->mx_select) lsk_moe_mx_select(a->mx_select - 1);
+  const int rc = moe_forward_call(a, stream);
+  g_moe_force = force;
+  g_moe_w4 = w4;
+  lsk_moe_mx_select(mxv);
+  return rc;
+}
+
+static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   const int64_t T = a->T, H = a->H, I = a->I, E = a->E;
   const int k = a->k;
   LSK_REQUIRE(T >= 0 && H > 0 && I > 0 && E >= 1 && E <= 1024, "lsk_moe_forward: bad sizes T=%lld H=%lld I=%lld E=%lld",

@@ -44,6 +44,9 @@ struct MoeGemmArgs {
   int pairs;
 };
 
+// The calling thread's grouped MX main-loop choice (lsk_moe_mx_select).
+int mx_variant();
+
 // MXFP4 grouped GEMMs (mode 0: gate/up + activation; 1: down + routing weight).
 int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, hipStream_t s);
 

@@ -1005,6 +1005,10 @@ extern "C" int lsk_mx_epilogue(const float* acc, int64_t M, int64_t N, const flo
   return lsk::check_launch("mx_epilogue_kernel");
 }
 
+namespace lsk {
+int mx_variant() { return g_mx_variant; }
+}  // namespace lsk
+
 extern "C" int lsk_moe_mx_select(int variant) {
   LSK_REQUIRE(variant >= 0 && variant <= 2, "lsk_moe_mx_select: variant %d not in [0, 2]", variant);
   g_mx_variant = variant;

@@ -16,7 +16,9 @@ Same names and signatures; GPU tensors only; results bit-identical to the refere
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import threading
 
 import torch
 
@@ -272,6 +274,33 @@ def _route_fields(x, route):
     return idx, w, fields, (gd, tb)
 
 
+_CHOICE = threading.local()
+
+
+@contextlib.contextmanager
+def kernel_choice(moe=None, mx=None):
+    """The MoE layers called inside run with this kernel choice, passed per call
+    (lsk_moe_args.select / mx_select; no reference counterpart, the same bits either way): moe as
+    lsk_moe_select's variant (-1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV, 3 the
+    four-wave tile, 4 128-byte K stages), mx as lsk_moe_mx_select's (0, 1, 2); None keeps the
+    calling thread's setting.  Scoped to this Python thread and the with-block."""
+    if moe is not None and not -1 <= moe <= 4:
+        raise ValueError("kernel_choice: moe=%r not in [-1, 4]" % (moe,))
+    if mx is not None and not 0 <= mx <= 2:
+        raise ValueError("kernel_choice: mx=%r not in [0, 2]" % (mx,))
+    prev = getattr(_CHOICE, "v", (0, 0))
+    _CHOICE.v = (0 if moe is None else moe + 2, 0 if mx is None else mx + 1)
+    try:
+        yield
+    finally:
+        _CHOICE.v = prev
+
+
+def _choice_fields():
+    sel, mxsel = getattr(_CHOICE, "v", (0, 0))
+    return {"select": sel, "mx_select": mxsel}
+
+
 def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_out=None, route=None):
     """The layer on given routing (idx, w), or with route = (logits, k, renormalize, tab) on the
     routing it computes itself; returns y, or (y, idx, w) with route."""
@@ -303,7 +332,7 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
                   frac=ops.frac_i32(x.device).data_ptr(), act_tab=_act_tab(x.device, act), rot_blk=int(rot_blk),
                   rot_scale=(1.0 / (rot_blk ** 0.5)) if rot_blk else 0.0,
                   shared=sh.data_ptr() if sh is not None else None, y=y.data_ptr(),
-                  workspace=work.data_ptr(), workspace_bytes=nbytes, **fields)
+                  workspace=work.data_ptr(), workspace_bytes=nbytes, **fields, **_choice_fields())
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
     del keep
     return y if route is None else (y, idx, w)
@@ -505,7 +534,7 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1, route=N
                   w2_ptrs=t.w2.data_ptr(), ldw2=t.ldw2, ws2_ptrs=t.ws2.data_ptr(),
                   b2_ptrs=t.b2.data_ptr() if t.b2 is not None else None, frac=ops.frac_i32(x.device).data_ptr(),
                   act_tab=_act_tab(x.device, act), rot_blk=0, rot_scale=0.0, shared=None, y=y.data_ptr(), workspace=work.data_ptr(),
-                  workspace_bytes=nbytes, **fields)
+                  workspace_bytes=nbytes, **fields, **_choice_fields())
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
     del keep
     return y if route is None else (y, idx, w)

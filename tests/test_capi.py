@@ -104,3 +104,14 @@ def test_noalloc_entry_point_refuses_sizes_beyond_its_scratch_without_touching_t
     assert rc == 1 and b"maximum" in lib.lsk_last_error()
     # M == 0 is a no-op, as for lsk_w8a8_matmul
     assert lib.lsk_w8a8_matmul_noalloc(None, 0, K, 0, K, None, K, 64, None, None, 0, None, 1, 64, None) == 0
+
+
+def test_moe_forward_rejects_bad_kernel_choice():
+    """lsk_moe_args.select / mx_select outside their ranges are rejected before any device work."""
+    import ctypes
+    from lockstep_amd import _lib as L
+    lib = L.load()
+    for sel, mxsel in ((7, 0), (0, 4), (-1, 0)):
+        a = L.MoeArgs(T=1, H=16, I=16, E=1, k=1, select=sel, mx_select=mxsel)
+        assert lib.lsk_moe_forward(ctypes.addressof(a), None) != 0
+        assert b"select" in lib.lsk_last_error()

@@ -211,6 +211,21 @@ def test_moe_grouped_gemm_variants(variant):
         L.call("lsk_moe_select", -1)
 
 
+def test_moe_per_call_kernel_choice():
+    """lsk_moe_args.select / mx_select choose the kernels of one call (moe_ref.kernel_choice) over
+    the thread's lsk_moe_select setting, with the oracle's bits, and leave that setting in place."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    L.call("lsk_moe_select", 2)            # the thread: the decode GEMV
+    try:
+        for v in (0, 1, 3, 4, -1):
+            with MR.kernel_choice(moe=v):
+                _run_case(300, 12, 4, 256, 192, seed=13)
+        _run_case(40, 8, 3, 256, 192, seed=16)   # the thread's setting again
+    finally:
+        L.call("lsk_moe_select", -1)
+
+
 @pytest.mark.parametrize("T", [1, 3, 12])
 def test_moe_gemv_wide_k(T):
     """The decode GEMV with K beyond one 1 KB lane sweep and not a multiple of it (H = 2064:
