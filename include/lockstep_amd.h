@@ -100,6 +100,14 @@ int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t 
                     int order, void* out, int out_dtype, int64_t ldo,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* lsk_w8a8_matmul with w_pairs: NULL, or the same weight in the row-pair layout
+ * (lsk_pack_row_pairs), which the GEMM reads when its tiles take the quantised rows in that layout
+ * (no reference counterpart as an argument: a prepared copy of W8; the same results). */
+int lsk_w8a8_matmul_pairs(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                          int64_t ldw, const int8_t* w_pairs, int64_t N, const float* ws, const float* bias,
+                          int order, void* out, int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
 /* lsk_w8a8_matmul without a workspace argument and without allocating: no counterpart in the
  * reference.  For callers that cannot allocate device memory (code under graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The quantised rows and their scales go to a

@@ -35,6 +35,7 @@ SIGNATURES = {
     "lsk_epilogue_apply": (_I, [_P, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _I, _P, _I, _I64, _P]),
     "lsk_w8a8_matmul_workspace": (_I64, [_I64, _I64]),
     "lsk_w8a8_matmul": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P, _I64, _P]),
+    "lsk_w8a8_matmul_pairs": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _I, _P, _I, _I64, _P, _I64, _P]),
     "lsk_w8a8_matmul_noalloc": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _P, _I, _I64, _P]),
     "lsk_outlier_side": (_I, [_P, _I, _I64, _I64, _P, _I, _I64, _P, _P]),
     "lsk_outlier_split": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P]),

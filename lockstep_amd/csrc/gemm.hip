@@ -1468,9 +1468,22 @@ extern "C" int64_t lsk_w8a8_matmul_workspace(int64_t M, int64_t K) {
   return w8a8_q_bytes(M, K) + ((M * 4 + 255) / 256) * 256;
 }
 
+extern "C" int lsk_w8a8_matmul_pairs(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                                     const int8_t* w, int64_t ldw, const int8_t* w_pairs, int64_t N, const float* ws,
+                                     const float* bias, int order, void* out, int out_dtype, int64_t ldo,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
+
 extern "C" int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
                                int64_t ldw, int64_t N, const float* ws, const float* bias, int order, void* out,
                                int out_dtype, int64_t ldo, void* workspace, int64_t workspace_bytes, void* stream) {
+  return lsk_w8a8_matmul_pairs(x, x_dtype, ldx, M, K, w, ldw, nullptr, N, ws, bias, order, out, out_dtype, ldo,
+                               workspace, workspace_bytes, stream);
+}
+
+extern "C" int lsk_w8a8_matmul_pairs(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K,
+                                     const int8_t* w, int64_t ldw, const int8_t* w_pairs, int64_t N, const float* ws,
+                                     const float* bias, int order, void* out, int out_dtype, int64_t ldo,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
   LSK_REQUIRE(order == LSK_EPI_V21 || order == LSK_EPI_V2, "lsk_w8a8_matmul: order must be V21 or V2");
   LSK_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lsk_w8a8_matmul: negative size");
   int rc = lsk::validate_epilogue(order, out_dtype, (const float*)1, ws, M, "lsk_w8a8_matmul");
@@ -1495,6 +1508,11 @@ extern "C" int lsk_w8a8_matmul(const void* x, int x_dtype, int64_t ldx, int64_t 
   if ((rc = lsk::rowquant_pair(x, x_dtype, M, K, ldx, q, ldq, asc, (hipStream_t)stream))) return rc;
   EpiParams ep{order, out_dtype, ws, asc, bias, nullptr, nullptr, 0, out, ldo};
   ep.pairs = 1;
+  // the weight's row-pair copy with the quantised rows' row-pair layout
+  if (w_pairs && lsk::gemm_takes_pp(w_pairs, kp, M, N, K, kp)) {
+    ep.pairs = 3;
+    return lsk::launch_gemm(q, ldq, w_pairs, kp, M, N, K, ep, (hipStream_t)stream);
+  }
   return lsk::launch_gemm(q, ldq, w, ldw, M, N, K, ep, (hipStream_t)stream);
 }
 

@@ -5,6 +5,9 @@ These are the building blocks of the drop-in modules (`lockstep_fullstack`, `moe
 """
 from __future__ import annotations
 
+import collections
+import weakref
+
 import torch
 
 from . import _lib as L
@@ -97,8 +100,9 @@ def epilogue(acc: torch.Tensor, order: int, out_dtype: int, asc=None, ws=None, b
 
 
 def w8a8_matmul(x2: torch.Tensor, w_nk: torch.Tensor, ws: torch.Tensor, bias, order: int,
-                out_dtype: int) -> torch.Tensor:
-    """Row quant + exact GEMM + epilogue in two launches, x2 [M, K] -> [M, N]."""
+                out_dtype: int, w_pairs=None) -> torch.Tensor:
+    """Row quant + exact GEMM + epilogue in two launches, x2 [M, K] -> [M, N]; w_pairs: None or
+    pack_row_pairs(w_nk), read when the GEMM takes the quantised rows in the row-pair layout."""
     L.require_cuda(x2, w_nk, ws, bias, what="w8a8_matmul")
     if x2.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         x2 = x2.to(torch.float32)
@@ -113,9 +117,9 @@ def w8a8_matmul(x2: torch.Tensor, w_nk: torch.Tensor, ws: torch.Tensor, bias, or
     nbytes = L.load().lsk_w8a8_matmul_workspace(M, K)
     ws_buf = torch.empty((nbytes,), dtype=torch.uint8, device=x2.device)
     ws, bias = _f32(ws), _f32(bias)
-    L.call("lsk_w8a8_matmul", L.ptr(x2), L.dtype_code(x2.dtype), x2.stride(0) if M > 1 else max(K, 1), M, K,
-           L.ptr(w_nk), w_nk.stride(0) if N > 1 else max(K, 1), N, L.ptr(ws), L.ptr(bias), order, L.ptr(out),
-           out_dtype, N, L.ptr(ws_buf), nbytes, L.stream_of(x2))
+    L.call("lsk_w8a8_matmul_pairs", L.ptr(x2), L.dtype_code(x2.dtype), x2.stride(0) if M > 1 else max(K, 1), M, K,
+           L.ptr(w_nk), w_nk.stride(0) if N > 1 else max(K, 1), L.ptr(w_pairs), N, L.ptr(ws), L.ptr(bias), order,
+           L.ptr(out), out_dtype, N, L.ptr(ws_buf), nbytes, L.stream_of(x2))
     return out
 
 
@@ -290,6 +294,39 @@ def pack_row_pairs(w_nk: torch.Tensor) -> torch.Tensor:
     L.call("lsk_pack_row_pairs", L.ptr(w_nk), N, K, w_nk.stride(0) if N > 1 else max(K, 16), L.ptr(out),
            L.stream_of(w_nk))
     return out
+
+
+# Row-pair copies of the weights the GEMM sites have seen (the GEMM tiles read them in whole 128-byte
+# lines), keyed by the weight's storage and kept while the weight tensor lives and is unchanged:
+# an entry holds a weak reference to the tensor that owns the storage and that tensor's version
+# counter, which every in-place write through it or a view of it advances.
+_ROW_PAIRS = collections.OrderedDict()
+_ROW_PAIRS_MAX = 64
+
+
+def row_pairs_of(w_nk):
+    """pack_row_pairs(w_nk), made once per weight and reused while the weight is unchanged;
+    None where the layout does not apply (K % 16 != 0, a weight being captured into a graph for the
+    first time)."""
+    N, K = w_nk.shape
+    if K == 0 or N == 0 or K % 16 != 0 or w_nk.stride(1) != 1 or w_nk.stride(0) % 16 != 0:
+        return None
+    owner = w_nk._base if w_nk._base is not None else w_nk
+    key = (w_nk.device.index, w_nk.data_ptr(), N, K, w_nk.stride(0))
+    hit = _ROW_PAIRS.get(key)
+    if hit is not None:
+        ref, version, packed = hit
+        if ref() is owner and owner._version == version:
+            _ROW_PAIRS.move_to_end(key)
+            return packed
+        del _ROW_PAIRS[key]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    packed = pack_row_pairs(w_nk)
+    _ROW_PAIRS[key] = (weakref.ref(owner), owner._version, packed)
+    while len(_ROW_PAIRS) > _ROW_PAIRS_MAX:
+        _ROW_PAIRS.popitem(last=False)
+    return packed
 
 
 def linear_dyn(x: torch.Tensor, w_nk: torch.Tensor, ew: int, stages: int = 3, work=None, y=None, ex=None,

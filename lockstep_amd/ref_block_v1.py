@@ -16,9 +16,6 @@ back (the arithmetic is always the HIP kernels').  gemm_int's operands must be i
 """
 from __future__ import annotations
 
-import collections
-import weakref
-
 import numpy as np
 import torch
 
@@ -92,37 +89,8 @@ def linear_dyn(x, W8, ew):
     return ops.linear_dyn(x, w_nk, int(ew), w_pairs=row_pairs_of(w_nk))
 
 
-# Row-pair copies of the weights linear_dyn has seen (the GEMM tiles read them in whole 128-byte
-# lines), keyed by the weight's storage and kept while the weight tensor lives and is unchanged:
-# an entry holds a weak reference to the tensor that owns the storage and that tensor's version
-# counter, which every in-place write through it or a view of it advances.
-_ROW_PAIRS = collections.OrderedDict()
-_ROW_PAIRS_MAX = 64
-
-
-def row_pairs_of(w_nk):
-    """ops.pack_row_pairs(w_nk), made once per weight and reused while the weight is unchanged;
-    None where the layout does not apply (K % 16 != 0, a weight being captured into a graph for the
-    first time)."""
-    N, K = w_nk.shape
-    if K == 0 or N == 0 or K % 16 != 0 or w_nk.stride(1) != 1 or w_nk.stride(0) % 16 != 0:
-        return None
-    owner = w_nk._base if w_nk._base is not None else w_nk
-    key = (w_nk.device.index, w_nk.data_ptr(), N, K, w_nk.stride(0))
-    hit = _ROW_PAIRS.get(key)
-    if hit is not None:
-        ref, version, packed = hit
-        if ref() is owner and owner._version == version:
-            _ROW_PAIRS.move_to_end(key)
-            return packed
-        del _ROW_PAIRS[key]
-    if torch.cuda.is_current_stream_capturing():
-        return None
-    packed = ops.pack_row_pairs(w_nk)
-    _ROW_PAIRS[key] = (weakref.ref(owner), owner._version, packed)
-    while len(_ROW_PAIRS) > _ROW_PAIRS_MAX:
-        _ROW_PAIRS.popitem(last=False)
-    return packed
+# the weights' row-pair copies (ops.row_pairs_of: one per weight, kept while it is unchanged)
+row_pairs_of = ops.row_pairs_of
 
 
 def _as_int8(t):
