@@ -463,6 +463,11 @@ typedef struct {
    * (v in [0, 2]) to this call, leaving the thread's settings as they were. */
   int select;
   int mx_select;
+  /* NULL, or per expert the same int8 weights in the row-pair layout (lsk_pack_row_pairs of the
+   * [2I, H] and [H, I] matrices; row stride (K + 63) / 64 * 64), which the ping-pong expert tiles
+   * read instead (int8 experts; the same results). */
+  const int64_t* w13_pair_ptrs;
+  const int64_t* w2_pair_ptrs;
 } lsk_moe_args;
 
 int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int wfmt);

@@ -95,7 +95,8 @@ class MoeArgs(ctypes.Structure):
                 ("frac", _P), ("rot_blk", _I), ("rot_scale", ctypes.c_float), ("shared", _P), ("y", _P), ("workspace", _P), ("workspace_bytes", _I64),
                 ("kw13_min", _I), ("kw13_max", _I), ("kw2_min", _I), ("kw2_max", _I), ("act_tab", _P),
                 ("logits", _P), ("logits_dtype", _I), ("renormalize", _I), ("ld_logits", _I64), ("router_tab", _P),
-                ("idx_out", _P), ("w_out", _P), ("select", _I), ("mx_select", _I)]
+                ("idx_out", _P), ("w_out", _P), ("select", _I), ("mx_select", _I),
+                ("w13_pair_ptrs", _P), ("w2_pair_ptrs", _P)]
 
 _lock = threading.Lock()
 _lib = None

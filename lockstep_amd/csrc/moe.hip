@@ -675,7 +675,8 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
     int row, kb, hc;
     lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
     const int wr = wrow_of(row, hc);
-    pb[j] = hc < a.N ? (uint32_t)(wr * a.ldw) : lsk::kOob;
+    const uint32_t ro = (a.pairs & 2) ? (uint32_t)((wr >> 1) * 2 * a.ldw + (wr & 1) * 64) : (uint32_t)(wr * a.ldw);
+    pb[j] = hc < a.N ? ro : lsk::kOob;
   }
   typename C::Acc acc;
 #pragma unroll
@@ -685,7 +686,7 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
 
   // the wave's 32-row strips that hold rows of the tile (the others are neither multiplied nor stored)
   const int na = max(0, min(C::TM, (p1 - p0 - wm * C::WTM + 31) / 32));
-  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe, na, MODE == 1 ? (a.pairs & 1) : 0);
+  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe, na, (MODE == 1 ? (a.pairs & 1) : 0) | (a.pairs & 2));
 
   // park the operands in LDS (past every wave's last ring read)
   float* sc_asc = (float*)(smem_moe + C::kScaleOff);
@@ -1689,6 +1690,8 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
   // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
   const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && I % 64 == 0 && g_moe_w4 == 0;
+  // the experts' row-pair weight copies on the same tiles, when the caller has them
+  const bool pair_w = use_pp && !mx && !use_gemv && g_moe_w4 == 0 && a->w13_pair_ptrs && a->w2_pair_ptrs;
 
   // up to 256 tokens: the dispatch and the row quant of x in one launch
   const bool prep_decode = T <= 256 && rb == 0 && mx != 2;
@@ -1804,6 +1807,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<0>(g1, w.max_tiles, T, w.gu, s, "moe_gemv_kernel<gate_up>"))) return rc;
   } else if (use_pp) {
+    if (pair_w) {
+      g1.w_ptrs = a->w13_pair_ptrs;
+      g1.ldw = (H + 63) / 64 * 64;
+      g1.w_bytes = 2 * I * g1.ldw;
+      g1.pairs |= 2;
+    }
     if ((rc = launch_moe_pp<0>(g1, w.max_tiles, s, "moe_pp_kernel<gate_up>"))) return rc;
   } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
     return rc;
@@ -1886,6 +1895,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<1>(g2, w.max_tiles, T, nullptr, s, "moe_gemv_kernel<down>"))) return rc;
   } else if (use_pp) {
+    if (pair_w) {
+      g2.w_ptrs = a->w2_pair_ptrs;
+      g2.ldw = (I + 63) / 64 * 64;
+      g2.w_bytes = H * g2.ldw;
+      g2.pairs |= 2;
+    }
     if ((rc = launch_moe_pp<1>(g2, w.max_tiles, s, "moe_pp_kernel<down>"))) return rc;
   } else if ((rc = launch_moe_gemm<1>(g2, w.max_tiles, (int)((H + 127) / 128), s, "moe_gemm_kernel<down>"))) {
     return rc;

@@ -38,9 +38,10 @@ struct MoeGemmArgs {
   const int32_t* any_flag;  // nonzero when some row is flagged
   const int32_t* a_ka;      // block exponents of the A rows [rows, K/32]
   int64_t ldka;
-  // 1: the A rows (down projection, rows p) in the row-pair layout -- rows 2i and 2i+1
+  // bit 0: the A rows (down projection, rows p) in the row-pair layout -- rows 2i and 2i+1
   // interleaved by 64-byte K chunks, byte (p >> 1) * 2 lda + (k >> 6) * 128 + (p & 1) * 64 +
-  // (k & 63), lda % 64 == 0 (ping-pong tiles only)
+  // (k & 63), lda % 64 == 0; bit 1: the weights (w_ptrs) in that layout, ldw % 64 == 0
+  // (ping-pong tiles only)
   int pairs;
 };
 

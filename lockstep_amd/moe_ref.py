@@ -162,6 +162,11 @@ def expert_block(x_rows, w13_8, ws13, w2_8, ws2, act, b13=None, b2=None, rot_blk
 
 
 # ============================================================================ the fused layer (moe_ref.py:117-140, 213-230)
+# ExpertTables keep a row-pair copy of every int8 expert weight (one more copy of the weights in
+# HBM; the ping-pong expert tiles read it faster).  False: the tables read the weights alone.
+ROW_PAIRS = True
+
+
 class ExpertTables:
     """Device address tables of the experts' int8 weights, scales and biases, as the fused
     layer reads them.  experts[e] = (w13col [H, 2I], ws13 [2I], w2col [I, H], ws2 [H][, b13, b2]),
@@ -218,6 +223,16 @@ class ExpertTables:
         self.ws2 = table(ws2)
         self.b13 = table(b13) if any(b13) else None
         self.b2 = table(b2) if any(b2) else None
+        # the weights' row-pair copies (ops.pack_row_pairs), which the ping-pong expert tiles read
+        # in whole 128-byte lines (the decode GEMVs and the other tiles read the weights above)
+        self.w13_pairs = self.w2_pairs = None
+        if ROW_PAIRS and self.H % 16 == 0 and self.I % 16 == 0:
+            p13 = [ops.pack_row_pairs(t) for t in w13]
+            p2 = [ops.pack_row_pairs(t) for t in w2]
+            keep += p13 + p2
+            self.w13_pairs = table([t.data_ptr() for t in p13])
+            self.w2_pairs = table([t.data_ptr() for t in p2])
+            pairs += [(ex[0], t) for ex, t in zip(experts, p13)] + [(ex[2], t) for ex, t in zip(experts, p2)]
         self._keep = keep
         pairs += [(ex[0], t) for ex, t in zip(experts, w13)] + [(ex[2], t) for ex, t in zip(experts, w2)]
         self._derived = _derived(pairs)
@@ -332,7 +347,10 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
                   frac=ops.frac_i32(x.device).data_ptr(), act_tab=_act_tab(x.device, act), rot_blk=int(rot_blk),
                   rot_scale=(1.0 / (rot_blk ** 0.5)) if rot_blk else 0.0,
                   shared=sh.data_ptr() if sh is not None else None, y=y.data_ptr(),
-                  workspace=work.data_ptr(), workspace_bytes=nbytes, **fields, **_choice_fields())
+                  workspace=work.data_ptr(), workspace_bytes=nbytes,
+                  w13_pair_ptrs=tables.w13_pairs.data_ptr() if tables.w13_pairs is not None else None,
+                  w2_pair_ptrs=tables.w2_pairs.data_ptr() if tables.w2_pairs is not None else None,
+                  **fields, **_choice_fields())
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
     del keep
     return y if route is None else (y, idx, w)
