@@ -498,6 +498,14 @@ int lsk_grouped_gemm_w8a8(const int8_t* a, int64_t lda, const float* asc, const 
                           const int64_t* w_ptrs, int64_t ldw, const int64_t* ws_ptrs, const int64_t* b_ptrs,
                           int64_t N, int64_t K, uint16_t* out, void* workspace, int64_t workspace_bytes,
                           void* stream);
+/* The same with w_pair_ptrs: NULL, or per expert the weight in the row-pair layout
+ * (lsk_pack_row_pairs; row stride (K + 63) / 64 * 64), read by the ping-pong tiles (R >= 16 E)
+ * instead of w_ptrs (no reference counterpart as an argument: prepared weight copies; the same
+ * results). */
+int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E,
+                                int64_t R, const int64_t* w_ptrs, int64_t ldw, const int64_t* w_pair_ptrs,
+                                const int64_t* ws_ptrs, const int64_t* b_ptrs, int64_t N, int64_t K, uint16_t* out,
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /* The MXFP4 form: per expert e, int_mm_mx then lin_epilogue_mx (reference/moe_ref.py:243-261, run
  * per expert by expert_block_mx :264-271): acc = the ordered block accumulation of int_mm_mx,

@@ -77,6 +77,8 @@ SIGNATURES = {
     "lsk_moe_forward": (_I, [_P, _P]),
     "lsk_grouped_gemm_workspace": (_I64, [_I64, _I64]),
     "lsk_grouped_gemm_w8a8": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
+    "lsk_grouped_gemm_w8a8_pairs": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _P, _P, _I64,
+                                         _P]),
     "lsk_grouped_gemm_mx": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I, _P, _P, _I64,
                                  _P]),
     "lsk_moe_select": (_I, [_I]),

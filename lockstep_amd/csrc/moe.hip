@@ -1523,10 +1523,25 @@ static int grouped_setup(const char* who, const void* a, const float* asc, const
   return lsk::check_launch("grouped_tiles_kernel");
 }
 
+extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const float* asc, const int32_t* offs,
+                                           int64_t E, int64_t R, const int64_t* w_ptrs, int64_t ldw,
+                                           const int64_t* w_pair_ptrs, const int64_t* ws_ptrs, const int64_t* b_ptrs,
+                                           int64_t N, int64_t K, uint16_t* out, void* workspace,
+                                           int64_t workspace_bytes, void* stream);
+
 extern "C" int lsk_grouped_gemm_w8a8(const int8_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E,
                                      int64_t R, const int64_t* w_ptrs, int64_t ldw, const int64_t* ws_ptrs,
                                      const int64_t* b_ptrs, int64_t N, int64_t K, uint16_t* out, void* workspace,
                                      int64_t workspace_bytes, void* stream) {
+  return lsk_grouped_gemm_w8a8_pairs(a, lda, asc, offs, E, R, w_ptrs, ldw, nullptr, ws_ptrs, b_ptrs, N, K, out,
+                                     workspace, workspace_bytes, stream);
+}
+
+extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const float* asc, const int32_t* offs,
+                                           int64_t E, int64_t R, const int64_t* w_ptrs, int64_t ldw,
+                                           const int64_t* w_pair_ptrs, const int64_t* ws_ptrs, const int64_t* b_ptrs,
+                                           int64_t N, int64_t K, uint16_t* out, void* workspace,
+                                           int64_t workspace_bytes, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   int rc = grouped_setup("lsk_grouped_gemm_w8a8", a, asc, offs, E, R, w_ptrs, ws_ptrs, N, K, out, workspace,
                          workspace_bytes, s);
@@ -1550,7 +1565,15 @@ extern "C" int lsk_grouped_gemm_w8a8(const int8_t* a, int64_t lda, const float* 
   g.N = (int)N;
   g.y = out;  // row_w / row_dst null: weight 1, row p of the output
   const int64_t mt = grouped_max_tiles(R, E);
-  if (R >= 16 * E) return launch_moe_pp<1>(g, mt, s, "moe_pp_kernel<grouped>");
+  if (R >= 16 * E) {
+    if (w_pair_ptrs && g_moe_w4 == 0) {  // the weights' row-pair copies on the ping-pong tiles
+      g.w_ptrs = w_pair_ptrs;
+      g.ldw = (K + 63) / 64 * 64;
+      g.w_bytes = ((N + 1) & ~(int64_t)1) * g.ldw;
+      g.pairs = 2;
+    }
+    return launch_moe_pp<1>(g, mt, s, "moe_pp_kernel<grouped>");
+  }
   return launch_moe_gemm<1>(g, mt, (int)((N + 127) / 128), s, "moe_gemm_kernel<grouped>");
 }
 

@@ -501,9 +501,10 @@ def grouped_linear(tables, which: str, a8, asc, offs):
     ldw = tables.ldw13 if which == "w13" else tables.ldw2
     a8 = a8 if a8.stride(-1) == 1 else a8.contiguous()
     asc = asc.to(F32).contiguous()
-    L.call("lsk_grouped_gemm_w8a8", L.ptr(a8), a8.stride(0) if R > 1 else a8.shape[1], L.ptr(asc), L.ptr(offs),
-           tables.E, R, L.ptr(w), ldw, L.ptr(ws), L.ptr(b), N, a8.shape[1], L.ptr(out), L.ptr(work), nbytes,
-           L.stream_of(a8))
+    wp = tables.w13_pairs if which == "w13" else tables.w2_pairs
+    L.call("lsk_grouped_gemm_w8a8_pairs", L.ptr(a8), a8.stride(0) if R > 1 else a8.shape[1], L.ptr(asc),
+           L.ptr(offs), tables.E, R, L.ptr(w), ldw, L.ptr(wp), L.ptr(ws), L.ptr(b), N, a8.shape[1], L.ptr(out),
+           L.ptr(work), nbytes, L.stream_of(a8))
     return out
 
 
