@@ -24,6 +24,15 @@ typedef unsigned int v4u32 __attribute__((ext_vector_type(4)));
 // prove threadIdx.x / 64 uniform by itself, and treats code that depends on it as divergent.
 LSK_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// A 64-bit value the caller knows to be equal in every lane (an entry of a per-block table, say)
+// moved to scalar registers.  Without it a buffer resource built from such a pointer can end up
+// in vector registers, and every load through it is wrapped in a loop over distinct resources.
+LSK_DEV int64_t wave_uniform64(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // binary32 -> bf16, round to nearest even; every NaN becomes 0x7FC0 (the conversion torch's
 // c10::BFloat16 performs, which is what the reference's `.to(torch.bfloat16)` runs).
 // binary32 -> bf16 by the round-to-nearest-even bit method torch uses, every NaN to 0x7FC0: the

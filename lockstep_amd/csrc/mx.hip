@@ -444,8 +444,10 @@ __global__ __launch_bounds__(256, RING == 2 ? 3 : 2) void moe_mx_pp_kernel(lsk::
   const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
   const int nrows_w = MODE == 0 ? 2 * a.N : a.N;  // weight rows of one expert
   const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
-  const __amdgpu_buffer_rsrc_t rb = lsk::make_rsrc((const void*)a.w_ptrs[e], a.w_bytes);
-  const __amdgpu_buffer_rsrc_t rs = lsk::make_rsrc((const void*)a.ws_ptrs[e], (int64_t)nrows_w * a.lds);
+  // the expert's code and exponent resources in scalar registers (a tile's expert is one value)
+  const __amdgpu_buffer_rsrc_t rb = lsk::make_rsrc((const void*)wave_uniform64(a.w_ptrs[e]), a.w_bytes);
+  const __amdgpu_buffer_rsrc_t rs =
+      lsk::make_rsrc((const void*)wave_uniform64(a.ws_ptrs[e]), (int64_t)nrows_w * a.lds);
   const lsk::MxPPRows rows = lsk::mx_pp_rows(
       [&](int r) -> uint32_t {
         const int p = p0 + r;
