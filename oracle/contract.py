@@ -16,10 +16,14 @@ Pinning (how each function is checked, see tests/test_oracle_*.py):
   fwht_blocks: the r4.block256 digest and the Hadamard closed form
   frac table: FRAC_DIGEST (sha256 of the 8192 uint16 entries)
   int_mm: two independent exact methods (int64 and float64-BLAS) against each other
-  quant8_* (pow2): brute force over exponents and closed-form edge cases
+  quant8_* (pow2): brute force over exponents and closed-form edge cases; the quantised values
+      of quant8_rows / quant8_cols by round-half-even of the exact rational x * 2^e in Python
+      integers, with a truncation slip that must differ
   fp4 / dequant_mxfp4: the closed form fp4 * 2^(e-127) over all codes and exponents
   int_mm_mx: one-block closed form, equal-exponent integer identity, scalar brute force,
       and a negative control (reversed block order differs)
+  lin_epilogue_mx: rational brute force of bfr(fl32(acc * asc)) then bfr(fl32(y + b)), with two
+      slips that must differ (bias before the first bf16 rounding; one merged rounding)
   router / combine / moe_forward*: scalar brute force in Python ints and numpy float32
   blockquant (MX2): the exact exponent min{k : 127 * 2^k >= am} clamped to [-126, 127] from the
       binary32 bits, round-half-even halves, the reconstruction bound, negative controls

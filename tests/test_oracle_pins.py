@@ -448,3 +448,74 @@ def test_epilogue_v2_bias_brute_force_and_negative_control():
                 assert float(y[m, n]) == ref, (out, m, n)
         if out == "bf16":
             assert slip > 0
+
+
+# ------------------------------------------------------------------ A9 MX epilogue
+def test_lin_epilogue_mx_brute_force_and_negative_controls():
+    """moe_ref.py:258-261: y = bfr(fl32(acc * asc[m])); with a bias y = bfr(fl32(y + b[n])).
+    Each step is evaluated on exact rationals and rounded by f32_round / bf16_round; two
+    planted slips must differ somewhere: the bias added before the first bf16 rounding, and
+    the two bf16 roundings merged into one after the bias."""
+    rng = np.random.default_rng(58)
+    T, N = 6, 48
+    # accumulators of the size the MX block chain produces: sums of s * 2^(k-128), k in [119, 130]
+    acc = (rng.standard_normal((T, N)) * 2.0 ** rng.integers(-20, 12, (T, N))).astype(F32)
+    acc[0, :4] = [0.0, -0.0, 1.0, -3.0]
+    asc = rng.uniform(1e-3, 1e-1, T).astype(F32)
+    bias = (rng.standard_normal(N) * 0.5).astype(F32)
+    y0 = C.lin_epilogue_mx(acc, asc)
+    y1 = C.lin_epilogue_mx(acc, asc, bias)
+    assert y0.dtype == F32 and y1.dtype == F32
+    early = merged = 0
+    for m in range(T):
+        for n in range(N):
+            p = f32_round(Fraction(float(acc[m, n])) * Fraction(float(asc[m])))
+            t = bf16_round(p)
+            assert float(y0[m, n]) == t, (m, n)
+            ref = bf16_round(f32_round(Fraction(t) + Fraction(float(bias[n]))))
+            assert float(y1[m, n]) == ref, (m, n)
+            early += bf16_round(bf16_round(f32_round(Fraction(p) + Fraction(float(bias[n]))))) != ref
+            merged += bf16_round(f32_round(Fraction(p) + Fraction(float(bias[n])))) != ref
+    assert early > 0 and merged > 0
+
+
+# ------------------------------------------------------------------ A6 pow2 quantised values
+def _rne_int(fr: Fraction) -> int:
+    """Round an exact rational to the nearest integer, ties to even, in Python integers."""
+    n = fr.numerator // fr.denominator
+    r = fr - n
+    if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return n
+
+
+def test_quant8_rows_cols_values_brute_force_and_truncation_control():
+    """ref_block_v1.py:64-72: q = clip(rint(fl32(x * 2^e)), -127, 127) with e from the row (or
+    column) maximum.  The scaling by a power of two is exact, so q equals round-half-even of the
+    exact rational x * 2^e clamped to +-127, computed here in Python integers with the exponent
+    from the independent brute-force search.  A truncating rint must differ somewhere."""
+    rng = np.random.default_rng(64)
+    x = (rng.standard_normal((7, 40)) * 2.0 ** rng.integers(-6, 6, (7, 1))).astype(F32)
+    x[1, :] = 0.0                                  # an all-zero row: e = 0, q = 0
+    x[2, 5] = F32(127.0 / 64.0)                    # the maximum lands exactly on 127 after scaling
+    # exact half-integers after scaling put the ties-to-even rule to work
+    e3 = _e_brute(float(np.abs(x[3]).max()))
+    x[3, :8] = (np.array([0.5, 1.5, 2.5, -0.5, -2.5, 3.5, 126.5, -125.5]) * 2.0 ** -e3).astype(F32)
+    for fn, xx in ((C.quant8_rows, x), (C.quant8_cols, x.T.copy())):
+        q, e = fn(xx)
+        q = np.asarray(q)
+        rows = xx if fn is C.quant8_rows else xx.T
+        qq = q if fn is C.quant8_rows else q.T
+        ee = np.asarray(e)
+        trunc_slips = 0
+        for i in range(rows.shape[0]):
+            m = float(np.abs(rows[i]).max())
+            ei = _e_brute(m)
+            assert int(ee[i]) == ei
+            for j in range(rows.shape[1]):
+                v = Fraction(float(rows[i, j])) * Fraction(2) ** ei
+                ref = max(-127, min(127, _rne_int(v)))
+                assert int(qq[i, j]) == ref, (fn.__name__, i, j)
+                tr = max(-127, min(127, int(v)))      # the planted slip: truncation toward zero
+                trunc_slips += tr != ref
+        assert trunc_slips > 0
