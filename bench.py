@@ -183,7 +183,7 @@ def block_section(torch, args):
         work = torch.empty((L.load().lsk_linear_dyn_workspace(T, K),), dtype=torch.uint8, device=dev)
         out = torch.empty((T, N), dtype=torch.float32, device=dev)
         ex = torch.empty((1,), dtype=torch.int32, device=dev)
-        wp = RB.row_pairs_of(W8)
+        wp = RB.row_pairs_of(W8, T)
         ops.linear_dyn(x, W8, BLOCK_EW, stages=1, work=work, y=out, ex=ex, w_pairs=wp)
         fn = lambda: ops.linear_dyn(x, W8, BLOCK_EW, stages=2, work=work, y=out, ex=ex, w_pairs=wp)  # noqa: E731
         for _ in range(2):
@@ -257,7 +257,7 @@ def vendor_section(torch, args):
         out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         wt = w.t()
         cases = {"hipblaslt_int_mm_i32": (-1, lambda: torch._int_mm(a, wt))}
-        for tile in (-1, 1, 3, 16, 18):
+        for tile in (-1, 1, 3, 17, 18):
             cases["lockstep_bf16_tile%d" % tile] = (
                 tile, lambda: ops.gemm(a, w, L.EPI_V21, L.LSK_BF16, asc=asc, ws=ws, out=out))
         for _ in range(100):

@@ -229,8 +229,9 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * 6, 7: for M <= 4 the 8-row register-buffered / LDS-ring GEMV instead of the whole-row GEMV;
  * 8..11: the whole-row GEMV with 1 / 2 / 4 / 8 rows per wave; 12, 13: tiles 3, 4 with a
  * three-stage LDS ring, two blocks per CU; 14 / 15: for 4 < M <= 32 the GEMV reading 64-byte row
- * pieces straight into registers / whole rows through LDS; 16 / 17: four-wave 256x256 / 256x128,
- * one wave per SIMD with 128x128 / 128x64 wave tiles; 18: ping-pong 256x128 with 128-byte K stages
+ * pieces straight into registers / for M <= 16 whole rows through LDS; 17: four-wave 256x128,
+ * one wave per SIMD with 128x64 wave tiles (16, its 256x256 form, spilled registers and is
+ * refused); 18: ping-pong 256x128 with 128-byte K stages
  * in a three-stage ring, the shape's default) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
  * The choice applies to the calling host thread's later launches only (thread-local). */
 int lsk_gemm_select(int tile_id);
@@ -287,6 +288,12 @@ int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8
  * weight (a prepared weight, like the reference's arm-time weight quant). */
 int64_t lsk_row_pairs_bytes(int64_t N, int64_t K);
 int lsk_pack_row_pairs(const int8_t* w, int64_t N, int64_t K, int64_t ldw, int8_t* out, void* stream);
+
+/* No counterpart in the reference: 1 when lsk_w8a8_matmul / lsk_linear_dyn with M rows, N output
+ * channels and depth K (K % 16 == 0) run every tile of the GEMM on the tiles that read a w_pairs
+ * copy, under the calling thread's lsk_gemm_select; 0 otherwise (no device work, callable without
+ * a GPU).  A caller makes the copy only when this says it will be read. */
+int lsk_gemm_reads_row_pairs(int64_t M, int64_t N, int64_t K);
 
 /* ---------------------------------------------------------------- the MXFP4 operand */
 
@@ -459,7 +466,7 @@ typedef struct {
   uint16_t* w_out;               /* [T, k] bf16 */
   /* Kernel choice for this call only (no reference counterpart; results are the same bits either
    * way): 0 keeps the calling thread's lsk_moe_select / lsk_moe_mx_select settings; select = v + 2
-   * applies lsk_moe_select(v) (v in [-1, 4]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
+   * applies lsk_moe_select(v) (v in [-1, 5]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
    * (v in [0, 2]) to this call, leaving the thread's settings as they were. */
   int select;
   int mx_select;
@@ -483,6 +490,13 @@ int lsk_act_table(const int32_t* frac, int act, float* table, void* stream);
 
 int lsk_moe_forward(const lsk_moe_args* args, void* stream);
 
+/* No counterpart in the reference: 1 when lsk_moe_forward on int8 experts with T tokens, top-k over
+ * E experts, hidden H, intermediate I and rotation block rot_blk, under the per-call kernel choice
+ * select (lsk_moe_args.select) and the calling thread's settings, reads the experts' row-pair weight
+ * copies (w13_pair_ptrs / w2_pair_ptrs); 0 otherwise.  No device work, callable without a GPU: a
+ * caller makes the copies only when a call will read them. */
+int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int select);
+
 /* One grouped expert linear over rows already sorted by expert: expert e owns rows
  * offs[e] .. offs[e + 1] - 1 (offs [E + 1] int32 on the device, nondecreasing) of a, and
  *   out[p, n] = bfr(fl32(fl32(acc[p, n]) * ws_e[n]) * asc[p]), then bfr(out + b_e[n]) with a bias,
@@ -492,7 +506,10 @@ int lsk_moe_forward(const lsk_moe_args* args, void* stream);
  * 164-169, 189-200) -- the grouped-GEMM stage of lsk_moe_forward without the routing weight.
  * a: [R, K] int8 (row stride lda); asc: [R]; w_ptrs[e]: int8 [N, K] (row stride ldw, the
  * reference's W.t() of w_col [K, N]); ws_ptrs[e]: f32 [N]; b_ptrs: null or [E] of f32 [N].
- * workspace: lsk_grouped_gemm_workspace(R, E) bytes, 256-byte aligned (the tile table). */
+ * workspace: lsk_grouped_gemm_workspace(R, E) bytes, 256-byte aligned (the tile table and a clamped
+ * copy of offs).  Offsets that decrease or leave [0, R] are made monotone and clamped on the device
+ * (offs'[j] = min(R, max(0, offs[0..j]))) before any tile reads them: such experts come out empty or
+ * shortened, and no row outside [0, R) is read or written. */
 int64_t lsk_grouped_gemm_workspace(int64_t R, int64_t E);
 int lsk_grouped_gemm_w8a8(const int8_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E, int64_t R,
                           const int64_t* w_ptrs, int64_t ldw, const int64_t* ws_ptrs, const int64_t* b_ptrs,
@@ -527,7 +544,10 @@ int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const 
  * applies, the ping-pong tile once the routed rows reach 16 E).  MXFP4 experts (H, I <= 8192, no
  * rotation) take the MX GEMV under 2 for T <= 64 and by default for T <= 24 (T <= 16 with
  * block-scaled activations), the MX grouped tiles otherwise.  Results are identical for every
- * choice.  4: the ping-pong tile with 128-byte K stages (one block per CU).  The choice applies to the calling
+ * choice.  4: the ping-pong tile with 128-byte K stages (one block per CU).  5: the 256x256 ping-pong
+ * tile (the dense kernel's tile: eight waves of 64x128, a four-stage ring, one block per CU, its own
+ * 256-row tile table; slower than the two-blocks-per-CU 128x256 tile, so never chosen by size).  The
+ * choice applies to the calling
  * host thread's later launches only (thread-local). */
 int lsk_moe_select(int variant);
 

@@ -62,6 +62,8 @@ SIGNATURES = {
     "lsk_linear_dyn": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I, _P, _I64, _P, _I, _P, _I64, _P]),
     "lsk_row_pairs_bytes": (_I64, [_I64, _I64]),
     "lsk_pack_row_pairs": (_I, [_P, _I64, _I64, _I64, _P, _P]),
+    "lsk_gemm_reads_row_pairs": (_I, [_I64, _I64, _I64]),
+    "lsk_moe_reads_row_pairs": (_I, [_I64, _I, _I64, _I64, _I64, _I, _I]),
     "lsk_router_topk": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "lsk_act_elementwise": (_I, [_P, _P, _I64, _I, _P, _P, _P]),
     "lsk_table_scores": (_I, [_P, _I64, _P, _P, _P]),

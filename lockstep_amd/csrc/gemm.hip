@@ -1335,8 +1335,9 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
   // 5.6-6.0 and 7.4-8.2 / 9.8-10.4; N = 14336, K = 4096 17.6 / 20.3 and 19.9 / 22.7; N = 28672,
   // K = 4096 level at M = 8 (the whole w8a8_matmul call 33.3 / 32.2), 34.2 / 32.9 at M = 16;
   // K = 14336 14.5 / 17.0 and 16.4 / 19.5; two activation tiles (M > 16) about 2x slower)
-  const bool use_lds = g_gemv_mid == 2 ||
-                       (g_gemv_mid == 0 && M <= 16 && (K >= 8192 || N <= 4096 || (N >= 8192 && N <= 16384)));
+  // (one activation tile only: the two-tile form spilled registers and measured about 2x slower)
+  const bool use_lds = M <= 16 && (g_gemv_mid == 2 ||
+                                   (g_gemv_mid == 0 && (K >= 8192 || N <= 4096 || (N >= 8192 && N <= 16384))));
   if (use_lds) {
     // waves per block so that at least 1024 waves stream, each K-slice a whole number of
     // 512-byte stages
@@ -1356,7 +1357,7 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * nw), smem, s, a, lda, w, ldw, M, N, K, kslice, ep); \
     return check_launch("gemv_i8_lds_kernel");                                                                \
   }
-    if (M <= 16) LSK_LDS(1) else LSK_LDS(2)
+    LSK_LDS(1)
 #undef LSK_LDS
   }
   int kw = 1;
@@ -1424,7 +1425,6 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     case 4: return launch_pp<128, 256, 2, 4>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4>");
     case 12: return launch_pp<256, 128, 4, 2, 3>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<256x128,4x2,r3>");
     case 13: return launch_pp<128, 256, 2, 4, 3>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_pp<128x256,2x4,r3>");
-    case 16: return launch_w4<256, 256>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_w4<256x256>");
     case 17: return launch_w4<256, 128>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s, "gemm_i8_w4<256x128>");
     case 18: return launch_pp<256, 128, 4, 2, 3, 128>(a, ilda, w, ildw, iM, iN, iK, ep, vec_ok, s,
                                                       "gemm_i8_pp<256x128,4x2,r3,k128>");
@@ -1543,7 +1543,8 @@ extern "C" int lsk_gemm_persist(int blocks) {
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 18, "lsk_gemm_select: tile id %d not in [-1, 18]", tile_id);
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 18 && tile_id != 16,
+              "lsk_gemm_select: tile id %d not in [-1, 18] (16, the four-wave 256x256 tile, was removed)", tile_id);
   lsk::g_force_tile = ((tile_id >= 6 && tile_id <= 11) || tile_id == 14 || tile_id == 15) ? 5 : tile_id;
   lsk::g_gemv_mid = tile_id == 14 ? 1 : (tile_id == 15 ? 2 : 0);
   lsk::g_gemv_variant = (tile_id == 6 || tile_id == 7) ? tile_id - 5 : 0;

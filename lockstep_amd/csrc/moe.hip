@@ -26,9 +26,11 @@ namespace {
 constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
 constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
 constexpr int kBM = lsk::kMoeBM;
+constexpr int kBM2 = 256;  // rows per tile of the 256 x 256 expert tiles (their own tile table)
 thread_local int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV,
                        // 3 the 128x256 tile on the four-wave main loop
-thread_local int g_moe_w4 = 0;      // the 128x256 tile's main loop: 0 eight-wave ping-pong, 1 four waves
+thread_local int g_moe_w4 = 0;      // the ping-pong tile: 0 128x256 eight-wave ping-pong, 1 128x256 four waves,
+                                    // 2 128x256 with 128-byte K stages, 3 256x256 (eight waves, four-stage ring)
 
 // ---------------------------------------------------------------- router
 LSK_DEV long long wave_max_ll(long long v) {
@@ -138,22 +140,25 @@ LSK_DEV int block_excl_scan(int v, int* tmp, int& total) {
   return base + x - v;
 }
 
-// Expert offsets and the M-tile table from per-expert row counts cnt[E] (any memory the block
+// Expert offsets and the M-tile tables from per-expert row counts cnt[E] (any memory the block
 // reads): offs[e] = rows of experts < e, offs[E] = all rows; tiles[0] = number of kBM-row tiles,
-// then (expert, first row) per tile, experts ascending.  Each thread owns a contiguous run of
-// experts.
+// then (expert, first row) per tile, experts ascending; tiles2 (if not null) the same in
+// kBM2-row tiles (the 256 x 256 expert tiles).  Each thread owns a contiguous run of experts.
 template <int THREADS>
-LSK_DEV void expert_offsets_and_tiles(const int32_t* cnt, int E, int32_t* offs, int32_t* tiles, int* tmp) {
+LSK_DEV void expert_offsets_and_tiles(const int32_t* cnt, int E, int32_t* offs, int32_t* tiles, int* tmp,
+                                      int32_t* tiles2 = nullptr) {
   const int per = (E + THREADS - 1) / THREADS;
   const int e0 = threadIdx.x * per;
-  int rows = 0, ntl = 0;
+  int rows = 0, ntl = 0, ntl2 = 0;
   for (int e = e0; e < e0 + per && e < E; ++e) {
     rows += cnt[e];
     ntl += (cnt[e] + kBM - 1) / kBM;
+    ntl2 += (cnt[e] + kBM2 - 1) / kBM2;
   }
-  int rows_all, tiles_all;
+  int rows_all, tiles_all, tiles2_all;
   int rbase = block_excl_scan<THREADS>(rows, tmp, rows_all);
   int tbase = block_excl_scan<THREADS>(ntl, tmp, tiles_all);
+  int tbase2 = block_excl_scan<THREADS>(ntl2, tmp, tiles2_all);
   for (int e = e0; e < e0 + per && e < E; ++e) {
     offs[e] = rbase;
     const int c = cnt[e];
@@ -162,11 +167,17 @@ LSK_DEV void expert_offsets_and_tiles(const int32_t* cnt, int E, int32_t* offs, 
         tiles[1 + 2 * tbase] = e;
         tiles[2 + 2 * tbase] = rbase + r0;
       }
+    if (tiles2)
+      for (int r0 = 0; r0 < c; r0 += kBM2, ++tbase2) {
+        tiles2[1 + 2 * tbase2] = e;
+        tiles2[2 + 2 * tbase2] = rbase + r0;
+      }
     rbase += c;
   }
   if (threadIdx.x == 0) {
     offs[E] = rows_all;
     if (tiles) tiles[0] = tiles_all;
+    if (tiles2) tiles2[0] = tiles2_all;
   }
 }
 
@@ -246,7 +257,8 @@ LSK_DEV void dispatch_small_block(const int64_t* __restrict__ idx, const uint16_
                                   int32_t* __restrict__ offs, int32_t* __restrict__ tiles,
                                   int32_t* __restrict__ row_tok, int32_t* __restrict__ row_dst,
                                   float* __restrict__ row_w, int32_t* __restrict__ tok_cnt,
-                                  uint32_t* __restrict__ zero_buf, int64_t zero_n, int32_t* dsm) {
+                                  uint32_t* __restrict__ zero_buf, int64_t zero_n, int32_t* dsm,
+                                  int32_t* __restrict__ tiles2) {
   __shared__ int tmp[4];
   int32_t* cnt = dsm;
   int32_t* base = dsm + E;
@@ -259,7 +271,7 @@ LSK_DEV void dispatch_small_block(const int64_t* __restrict__ idx, const uint16_
   load_chunk_routes(idx, w, T, k, E, 0, ids, wts);  // ends with a barrier
   count_chunk(ids, T, k, 0, cnt, tok_cnt);
   __syncthreads();
-  expert_offsets_and_tiles<256>(cnt, E, base, tiles, tmp);
+  expert_offsets_and_tiles<256>(cnt, E, base, tiles, tmp, tiles2);
   __syncthreads();
   for (int e = tid; e <= E; e += 256) offs[e] = base[e];  // base[E] = all rows
   __syncthreads();
@@ -273,9 +285,10 @@ __global__ __launch_bounds__(256) void moe_dispatch_small_kernel(const int64_t* 
                                                                  int32_t* __restrict__ row_dst,
                                                                  float* __restrict__ row_w,
                                                                  int32_t* __restrict__ tok_cnt,
-                                                                 uint32_t* __restrict__ zero_buf, int64_t zero_n) {
+                                                                 uint32_t* __restrict__ zero_buf, int64_t zero_n,
+                                                                 int32_t* __restrict__ tiles2) {
   extern __shared__ int32_t dsm[];
-  dispatch_small_block(idx, w, T, k, E, offs, tiles, row_tok, row_dst, row_w, tok_cnt, zero_buf, zero_n, dsm);
+  dispatch_small_block(idx, w, T, k, E, offs, tiles, row_tok, row_dst, row_w, tok_cnt, zero_buf, zero_n, dsm, tiles2);
 }
 
 // Decode-sized layers (the grouped GEMV path) start with one launch: block 0 runs the dispatch
@@ -293,7 +306,7 @@ __global__ __launch_bounds__(256) void moe_decode_prep_kernel(const int64_t* __r
                                                               int q_bf16, const void* __restrict__ logits, int gdt,
                                                               int64_t ldg, const int32_t* __restrict__ rtab,
                                                               int renorm, int64_t* __restrict__ idx_out,
-                                                              uint16_t* __restrict__ w_out) {
+                                                              uint16_t* __restrict__ w_out, int32_t* __restrict__ tiles2) {
   extern __shared__ int32_t dsm[];
   if (blockIdx.x == 0) {
     if (logits) {
@@ -305,7 +318,8 @@ __global__ __launch_bounds__(256) void moe_decode_prep_kernel(const int64_t* __r
       idx = idx_out;
       w = w_out;
     }
-    dispatch_small_block(idx, w, T, k, E, offs, tiles, row_tok, row_dst, row_w, tok_cnt, zero_buf, zero_n, dsm);
+    dispatch_small_block(idx, w, T, k, E, offs, tiles, row_tok, row_dst, row_w, tok_cnt, zero_buf, zero_n, dsm,
+                         tiles2);
     return;
   }
   __shared__ float red[4];
@@ -402,7 +416,8 @@ __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restric
                                                         int T, int k, int E, const int32_t* __restrict__ ccnt,
                                                         int nchunks, int32_t* __restrict__ offs,
                                                         int32_t* __restrict__ tiles, int32_t* __restrict__ row_tok,
-                                                        int32_t* __restrict__ row_dst, float* __restrict__ row_w) {
+                                                        int32_t* __restrict__ row_dst, float* __restrict__ row_w,
+                                                        int32_t* __restrict__ tiles2) {
   extern __shared__ int32_t sm_place[];
   int32_t* tot = sm_place;
   int32_t* pre = tot + E;
@@ -429,7 +444,8 @@ __global__ __launch_bounds__(256) void moe_place_kernel(const int64_t* __restric
     pre[e] = before;
   }
   __syncthreads();
-  expert_offsets_and_tiles<256>(tot, E, offl, blockIdx.x == 0 ? tiles : nullptr, tmp);
+  expert_offsets_and_tiles<256>(tot, E, offl, blockIdx.x == 0 ? tiles : nullptr, tmp,
+                                blockIdx.x == 0 ? tiles2 : nullptr);
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += 256) {
     if (blockIdx.x == 0) offs[e] = offl[e];
@@ -601,22 +617,31 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeGemmArgs a) {
 using PPM = lsk::PPCfg<128, 256, 2, 4, 3>;
 using PPM128 = lsk::PPCfg<128, 256, 2, 4, 3, 128>;  // 128-byte K stages, one block per CU
 using W4M = lsk::W4Cfg<128, 256, 3>;
-static_assert(PPM::kSmemBytes - PPM::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
-static_assert(PPM128::kSmemBytes - PPM128::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
-static_assert(PPM128::kSmemBytes <= 160 * 1024, "one block per CU");
-static_assert(W4M::kSmemBytes - W4M::kScaleOff >= (3 * 128 + 2 * 256) * 4, "tile operands fit the scale area");
-static_assert(2 * W4M::kSmemBytes <= 160 * 1024 && 2 * PPM::kSmemBytes <= 160 * 1024, "two blocks per CU");
+// 256 x 256 expert tiles (the dense kernel's tile and wave shape, four-stage ring, one block per
+// CU) over the 256-row tile table: half the operand bytes per MFMA of the 128-row tiles
+using PPM256 = lsk::PPCfg<256, 256, 4, 2, 4>;
+// LDS of a MoE tile: the ring / strip staging, then the tile's row operands (scale, weight, slot)
+// and column operands (scale, bias)
+template <class C>
+constexpr int moe_smem_bytes() {
+  return C::kSmemBytes > C::kScaleOff + (3 * C::kBM + 2 * C::kBN) * 4 ? C::kSmemBytes
+                                                                    : C::kScaleOff + (3 * C::kBM + 2 * C::kBN) * 4;
+}
+static_assert(moe_smem_bytes<PPM128>() <= 160 * 1024 && moe_smem_bytes<PPM256>() <= 160 * 1024, "one block per CU");
+static_assert(2 * moe_smem_bytes<W4M>() <= 160 * 1024 && 2 * moe_smem_bytes<PPM>() <= 160 * 1024, "two blocks per CU");
 
 template <class C, int MODE, class MAIN>
 __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, MAIN main) {
-  static_assert(C::kBM == 128 && C::kBN == 256 && C::TM == 2, "128 x 256 tiles, two 32-row strips per wave");
+  static_assert((C::kBM == 128 || C::kBM == 256) && C::kBN == 256 && C::TM == 2,
+                "128 or 256 x 256 tiles, two 32-row strips per wave");
+  // a.tiles: the tile table in C::kBM-row tiles
   const int ntiles = MODE == 0 ? (a.N + 127) / 128 : (a.N + 255) / 256;
   const int L = lsk::xcd_logical_id(blockIdx.x, gridDim.x);
   const int mt = L / ntiles, nt = L - (L / ntiles) * ntiles;
   if (mt >= a.tiles[0]) return;  // the whole block leaves: no barrier is left waiting
   const int e = a.tiles[1 + 2 * mt];
   const int p0 = a.tiles[2 + 2 * mt];
-  const int p1 = min(a.offs[e + 1], p0 + kBM);
+  const int p1 = min(a.offs[e + 1], p0 + C::kBM);
   const int8_t* wb = (const int8_t*)a.w_ptrs[e];
   const float* ws = (const float*)a.ws_ptrs[e];
   const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
@@ -637,7 +662,7 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
   // epilogue operands, held in registers across the main loop
   float r_asc = 0.0f, r_w = 0.0f, c_ws = 0.0f, c_b = 0.0f;
   int r_dst = 0;
-  if (tid < 128 && p0 + tid < p1) {
+  if (tid < C::kBM && p0 + tid < p1) {
     const int p = p0 + tid;
     if (MODE == 0) {
       r_asc = a.a_scale[a.row_tok[p]];
@@ -690,11 +715,11 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
 
   // park the operands in LDS (past every wave's last ring read)
   float* sc_asc = (float*)(smem_moe + C::kScaleOff);
-  float* sc_w = sc_asc + 128;
-  int* sc_dst = (int*)(sc_w + 128);
-  float* sc_ws = (float*)(sc_dst + 128);
+  float* sc_w = sc_asc + C::kBM;
+  int* sc_dst = (int*)(sc_w + C::kBM);
+  float* sc_ws = (float*)(sc_dst + C::kBM);
   float* sc_b = sc_ws + 256;
-  if (tid < 128) {
+  if (tid < C::kBM) {
     sc_asc[tid] = r_asc;
     sc_w[tid] = r_w;
     sc_dst[tid] = r_dst;
@@ -857,6 +882,16 @@ __global__ __launch_bounds__(512, 2) void moe_pp_kernel(MoeGemmArgs a) {
                          const PPM::RowsB& pb, int K, char* sm, int na, int pairs) {
                         lsk::pp_mainloop<128, 256, 2, 4, 3, 64, false, true>(acc, ra, pa, rb, pb, K, sm, na, pairs);
                       });
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void moe_pp256_kernel(MoeGemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem_moe[];
+  moe_tile<PPM256, MODE>(a, smem_moe,
+                         [](PPM256::Acc& acc, __amdgpu_buffer_rsrc_t ra, const PPM256::RowsA& pa,
+                            __amdgpu_buffer_rsrc_t rb, const PPM256::RowsB& pb, int K, char* sm, int na, int pairs) {
+                           lsk::pp_mainloop<256, 256, 4, 2, 4, 64, false, true>(acc, ra, pa, rb, pb, K, sm, na, pairs);
+                         });
 }
 
 template <int MODE>
@@ -1326,11 +1361,22 @@ struct MoeWs {
   int32_t* flagh;
   int64_t bytes;
   int64_t max_tiles;
+  int32_t* tiles2;     // the tile table in kBM2-row tiles
+  int64_t max_tiles2;
 };
 
 inline int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
 
 constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
+
+// Whether the ping-pong grouped GEMM runs on the 256 x 256 tiles: only when chosen
+// (lsk_moe_select(5)).  One block per CU there leaves the load latency and the epilogue of a tile
+// unhidden, which the two resident 128 x 256 blocks overlap: measured on MI355X, Qwen3-30B-A3B
+// layer at 256 / 2048 / 4096 tokens 222 / 358 / 520 us against 169 / 299 / 425 us, the grouped
+// gate/up and down stages at 16384 rows 179 / 137 us against 143 / 101 us, despite a third fewer
+// operand bytes per MFMA.
+static bool moe_uses_pp256(int64_t, int64_t) { return g_moe_w4 == 3; }
+
 constexpr int64_t kMxGemvMaxT = 24;   // ... with MXFP4 experts
 constexpr int64_t kMx2GemvMaxT = 16;  // ... with MXFP4 experts and block-scaled activations
 
@@ -1339,6 +1385,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   MoeWs w{};
   const int64_t R = T * k;
   w.max_tiles = R / kBM + (E < R ? E : R);
+  w.max_tiles2 = R / kBM2 + (E < R ? E : R);
   int64_t off = 0;
   auto take = [&](int64_t nbytes) {
     char* p = base ? base + off : nullptr;
@@ -1349,6 +1396,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.ascx = (float*)take(T * 4);
   w.offs = (int32_t*)take((E + 1) * 4);
   w.tiles = (int32_t*)take((1 + 2 * w.max_tiles) * 4);
+  w.tiles2 = (int32_t*)take((1 + 2 * w.max_tiles2) * 4);
   w.row_tok = (int32_t*)take(R * 4);
   w.row_dst = (int32_t*)take(R * 4);
   w.row_w = (float*)take(R * 4);
@@ -1382,38 +1430,59 @@ int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const
     static std::atomic<bool> attr_128{false};
     if (!attr_128) {
       if (hipFuncSetAttribute((const void*)moe_pp128_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              PPM128::kSmemBytes) != hipSuccess) {
-        lsk::set_error("%s: cannot reserve %d bytes of LDS", name, PPM128::kSmemBytes);
+                              moe_smem_bytes<PPM128>()) != hipSuccess) {
+        lsk::set_error("%s: cannot reserve %d bytes of LDS", name, moe_smem_bytes<PPM128>());
         return LSK_ERR_HIP;
       }
       attr_128 = true;
     }
-    hipLaunchKernelGGL(moe_pp128_kernel<MODE>, dim3((unsigned)blocks), dim3(512), PPM128::kSmemBytes, s, ga);
+    hipLaunchKernelGGL(moe_pp128_kernel<MODE>, dim3((unsigned)blocks), dim3(512), moe_smem_bytes<PPM128>(), s, ga);
     return lsk::check_launch(name);
   }
   if (g_moe_w4) {
     static std::atomic<bool> attr_w4{false};
     if (!attr_w4) {
       if (hipFuncSetAttribute((const void*)moe_w4_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              W4M::kSmemBytes) != hipSuccess) {
-        lsk::set_error("%s: cannot reserve %d bytes of LDS", name, W4M::kSmemBytes);
+                              moe_smem_bytes<W4M>()) != hipSuccess) {
+        lsk::set_error("%s: cannot reserve %d bytes of LDS", name, moe_smem_bytes<W4M>());
         return LSK_ERR_HIP;
       }
       attr_w4 = true;
     }
-    hipLaunchKernelGGL(moe_w4_kernel<MODE>, dim3((unsigned)blocks), dim3(256), W4M::kSmemBytes, s, ga);
+    hipLaunchKernelGGL(moe_w4_kernel<MODE>, dim3((unsigned)blocks), dim3(256), moe_smem_bytes<W4M>(), s, ga);
     return lsk::check_launch(name);
   }
   static std::atomic<bool> attr_set{false};
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)moe_pp_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            PPM::kSmemBytes) != hipSuccess) {
-      lsk::set_error("%s: cannot reserve %d bytes of LDS", name, PPM::kSmemBytes);
+                            moe_smem_bytes<PPM>()) != hipSuccess) {
+      lsk::set_error("%s: cannot reserve %d bytes of LDS", name, moe_smem_bytes<PPM>());
       return LSK_ERR_HIP;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL(moe_pp_kernel<MODE>, dim3((unsigned)blocks), dim3(512), PPM::kSmemBytes, s, ga);
+  hipLaunchKernelGGL(moe_pp_kernel<MODE>, dim3((unsigned)blocks), dim3(512), moe_smem_bytes<PPM>(), s, ga);
+  return lsk::check_launch(name);
+}
+
+// The 256 x 256 expert tiles: ga.tiles is the kBM2-row tile table, max_tiles its bound.
+template <int MODE>
+int launch_moe_pp256(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const char* name) {
+  const int ntiles = MODE == 0 ? (ga.N + 127) / 128 : (ga.N + 255) / 256;
+  const int64_t blocks = max_tiles * ntiles;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  constexpr int kSmem = moe_smem_bytes<PPM256>();
+  static std::atomic<bool> attr_set{false};
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)moe_pp256_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, kSmem) !=
+        hipSuccess) {
+      lsk::set_error("%s: cannot reserve %d bytes of LDS", name, kSmem);
+      return LSK_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(moe_pp256_kernel<MODE>, dim3((unsigned)blocks), dim3(512), kSmem, s, ga);
   return lsk::check_launch(name);
 }
 
@@ -1482,19 +1551,38 @@ extern "C" int lsk_router_topk(const void* g, int g_dtype, int64_t ldg, int64_t 
 }
 
 // ---------------------------------------------------------------- the grouped expert linear alone
-// Tile table of expert-sorted rows from their offsets (one block): tiles[0] = number of kBM-row
-// tiles, then (expert, first row) per tile, experts ascending; first rows come from offs itself.
-__global__ __launch_bounds__(256) void grouped_tiles_kernel(const int32_t* __restrict__ offs, int E,
-                                                            int32_t* __restrict__ tiles) {
+// Tile table of expert-sorted rows from the caller's offsets (one block).  The offsets are first
+// made monotone and clamped to [0, R] (coffs[j] = min(R, max(0, offs[0..j]))), so offsets that
+// decrease or run past R give empty or shortened experts, never rows outside [0, R) nor more tiles
+// than grouped_max_tiles(R, E); the tiles read coffs.  tiles[0] = number of bm-row tiles (bm = kBM
+// or kBM2), then (expert, first row) per tile, experts ascending.
+__global__ __launch_bounds__(256) void grouped_tiles_kernel(const int32_t* __restrict__ offs, int E, int R, int bm,
+                                                            int32_t* __restrict__ tiles, int32_t* __restrict__ coffs) {
   __shared__ int tmp[4];
-  const int per = (E + 255) / 256;
-  const int e0 = threadIdx.x * per;
+  __shared__ int run_max[256];
+  __shared__ int co[1025];
+  const int per = (E + 1 + 255) / 256;  // offsets 0..E, a contiguous run per thread
+  const int j0 = threadIdx.x * per;
+  int m = 0;
+  for (int j = j0; j < j0 + per && j <= E; ++j) m = max(m, min(max(offs[j], 0), R));
+  run_max[threadIdx.x] = m;
+  __syncthreads();
+  int run = 0;
+  for (int t = 0; t < (int)threadIdx.x; ++t) run = max(run, run_max[t]);
+  for (int j = j0; j < j0 + per && j <= E; ++j) {
+    run = max(run, min(max(offs[j], 0), R));
+    co[j] = run;
+    coffs[j] = run;
+  }
+  __syncthreads();
+  const int pe = (E + 255) / 256;
+  const int e0 = threadIdx.x * pe;
   int ntl = 0;
-  for (int e = e0; e < e0 + per && e < E; ++e) ntl += (max(offs[e + 1] - offs[e], 0) + kBM - 1) / kBM;
+  for (int e = e0; e < e0 + pe && e < E; ++e) ntl += (co[e + 1] - co[e] + bm - 1) / bm;
   int total;
   int tbase = block_excl_scan<256>(ntl, tmp, total);
-  for (int e = e0; e < e0 + per && e < E; ++e)
-    for (int r0 = offs[e]; r0 < offs[e + 1]; r0 += kBM, ++tbase) {
+  for (int e = e0; e < e0 + pe && e < E; ++e)
+    for (int r0 = co[e]; r0 < co[e + 1]; r0 += bm, ++tbase) {
       tiles[1 + 2 * tbase] = e;
       tiles[2 + 2 * tbase] = r0;
     }
@@ -1503,14 +1591,21 @@ __global__ __launch_bounds__(256) void grouped_tiles_kernel(const int32_t* __res
 
 static int64_t grouped_max_tiles(int64_t R, int64_t E) { return R / kBM + (E < R ? E : R); }
 
+static int64_t grouped_tiles_bytes(int64_t R, int64_t E) { return up256((1 + 2 * grouped_max_tiles(R, E)) * 4); }
+
 extern "C" int64_t lsk_grouped_gemm_workspace(int64_t R, int64_t E) {
-  return up256((1 + 2 * grouped_max_tiles(R, E)) * 4);
+  return grouped_tiles_bytes(R, E) + up256((E + 1) * 4);
+}
+
+// The clamped offsets grouped_tiles_kernel leaves in the workspace, which the tiles read.
+static const int32_t* grouped_offs(void* workspace, int64_t R, int64_t E) {
+  return (const int32_t*)((char*)workspace + grouped_tiles_bytes(R, E));
 }
 
 // Shared checks and the tile table of the two grouped entry points.
 static int grouped_setup(const char* who, const void* a, const float* asc, const int32_t* offs, int64_t E, int64_t R,
                          const int64_t* w_ptrs, const int64_t* ws_ptrs, int64_t N, int64_t K, const void* out,
-                         void* workspace, int64_t workspace_bytes, hipStream_t s) {
+                         void* workspace, int64_t workspace_bytes, hipStream_t s, int bm = kBM) {
   LSK_REQUIRE(R >= 0 && N > 0 && K > 0 && E >= 1 && E <= 1024, "%s: bad sizes R=%lld N=%lld K=%lld E=%lld", who,
               (long long)R, (long long)N, (long long)K, (long long)E);
   LSK_REQUIRE(K <= 133144, "%s: K above the int32-exact bound", who);
@@ -1519,7 +1614,8 @@ static int grouped_setup(const char* who, const void* a, const float* asc, const
   LSK_REQUIRE(a && asc && offs && w_ptrs && ws_ptrs && out, "%s: null pointer", who);
   LSK_REQUIRE(workspace && workspace_bytes >= lsk_grouped_gemm_workspace(R, E) && ((uintptr_t)workspace & 255) == 0,
               "%s: workspace of %lld bytes (256-byte aligned) needed", who, (long long)lsk_grouped_gemm_workspace(R, E));
-  hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(256), 0, s, offs, (int)E, (int32_t*)workspace);
+  hipLaunchKernelGGL(grouped_tiles_kernel, dim3(1), dim3(256), 0, s, offs, (int)E, (int)R, bm, (int32_t*)workspace,
+                     (int32_t*)grouped_offs(workspace, R, E));
   return lsk::check_launch("grouped_tiles_kernel");
 }
 
@@ -1543,8 +1639,10 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
                                            int64_t N, int64_t K, uint16_t* out, void* workspace,
                                            int64_t workspace_bytes, void* stream) {
   hipStream_t s = (hipStream_t)stream;
+  // the ping-pong tiles once experts average 16 rows (the 256 x 256 ones when chosen)
+  const bool pp = R >= 16 * E, pp256 = pp && moe_uses_pp256(R, E);
   int rc = grouped_setup("lsk_grouped_gemm_w8a8", a, asc, offs, E, R, w_ptrs, ws_ptrs, N, K, out, workspace,
-                         workspace_bytes, s);
+                         workspace_bytes, s, pp256 ? kBM2 : kBM);
   if (rc || R == 0) return rc;
   LSK_REQUIRE(lda >= K && lda % 16 == 0 && ldw >= K && ldw % 16 == 0 && N * ldw < 0x7fffffff &&
                   R * lda < 0x7fffffff,
@@ -1555,7 +1653,7 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
   g.a_bytes = R * lda;
   g.w_bytes = N * ldw;
   g.a_scale = asc;
-  g.offs = offs;
+  g.offs = grouped_offs(workspace, R, E);
   g.tiles = (const int32_t*)workspace;
   g.w_ptrs = w_ptrs;
   g.ldw = ldw;
@@ -1565,13 +1663,14 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
   g.N = (int)N;
   g.y = out;  // row_w / row_dst null: weight 1, row p of the output
   const int64_t mt = grouped_max_tiles(R, E);
-  if (R >= 16 * E) {
-    if (w_pair_ptrs && g_moe_w4 == 0) {  // the weights' row-pair copies on the ping-pong tiles
+  if (pp) {
+    if (w_pair_ptrs && (g_moe_w4 == 0 || g_moe_w4 == 3)) {  // the weights' row-pair copies on the ping-pong tiles
       g.w_ptrs = w_pair_ptrs;
       g.ldw = (K + 63) / 64 * 64;
       g.w_bytes = ((N + 1) & ~(int64_t)1) * g.ldw;
       g.pairs = 2;
     }
+    if (pp256) return launch_moe_pp256<1>(g, R / kBM2 + (E < R ? E : R), s, "moe_pp256_kernel<grouped>");
     return launch_moe_pp<1>(g, mt, s, "moe_pp_kernel<grouped>");
   }
   return launch_moe_gemm<1>(g, mt, (int)((N + 127) / 128), s, "moe_gemm_kernel<grouped>");
@@ -1595,7 +1694,7 @@ extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* 
   g.a_bytes = R * lda * 2;
   g.w_bytes = N * ldw;
   g.a_scale = asc;
-  g.offs = offs;
+  g.offs = grouped_offs(workspace, R, E);
   g.tiles = (const int32_t*)workspace;
   g.w_ptrs = w_ptrs;
   g.ldw = ldw;
@@ -1609,9 +1708,9 @@ extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* 
 }
 
 extern "C" int lsk_moe_select(int variant) {
-  LSK_REQUIRE(variant >= -1 && variant <= 4, "lsk_moe_select: variant %d not in [-1, 4]", variant);
-  g_moe_force = variant == 4 ? 1 : variant;
-  g_moe_w4 = variant == 3 ? 1 : (variant == 4 ? 2 : 0);
+  LSK_REQUIRE(variant >= -1 && variant <= 5, "lsk_moe_select: variant %d not in [-1, 5]", variant);
+  g_moe_force = variant >= 4 ? 1 : variant;
+  g_moe_w4 = variant == 3 ? 1 : (variant == 4 ? 2 : (variant == 5 ? 3 : 0));
   return LSK_OK;
 }
 
@@ -1621,10 +1720,31 @@ extern "C" int64_t lsk_moe_workspace(int64_t T, int k, int64_t E, int64_t H, int
 
 static int moe_forward_call(const lsk_moe_args* a, void* stream);
 
+// Whether an int8 layer of T tokens, top-k over E experts, runs its grouped GEMMs on the ping-pong
+// tiles that read the experts' row-pair weight copies (w13_pair_ptrs / w2_pair_ptrs), under the
+// calling thread's kernel selection: the rule moe_forward_call applies.
+static bool moe_reads_pair_weights(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rb) {
+  const int64_t R = T * k;
+  const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= 16 * E;
+  const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
+  const bool use_gemv = gemv_ok && H <= 4096 && I <= 4096;
+  return use_pp && !use_gemv && (g_moe_w4 == 0 || g_moe_w4 == 3);
+}
+
+extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int select) {
+  if (T <= 0 || k < 1 || E < 1 || H <= 0 || I <= 0 || select < 0 || select > 7) return 0;
+  const int force = g_moe_force, w4 = g_moe_w4;
+  if (select) lsk_moe_select(select - 2);
+  const bool r = moe_reads_pair_weights(T, k, E, H, I, rot_blk);
+  g_moe_force = force;
+  g_moe_w4 = w4;
+  return r ? 1 : 0;
+}
+
 extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(a, "lsk_moe_forward: null args");
-  LSK_REQUIRE(a->select >= 0 && a->select <= 6 && a->mx_select >= 0 && a->mx_select <= 3,
-              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 6] / [0, 3]", a->select, a->mx_select);
+  LSK_REQUIRE(a->select >= 0 && a->select <= 7 && a->mx_select >= 0 && a->mx_select <= 3,
+              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 7] / [0, 3]", a->select, a->mx_select);
   if (a->select == 0 && a->mx_select == 0) return moe_forward_call(a, stream);
   // this call's kernel choice, the thread's own restored afterwards
   const int force = g_moe_force, w4 = g_moe_w4, mxv = lsk::mx_variant();
@@ -1712,9 +1832,11 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
   // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
   // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
-  const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && I % 64 == 0 && g_moe_w4 == 0;
+  const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && I % 64 == 0 && (g_moe_w4 == 0 || g_moe_w4 == 3);
+  // the 256 x 256 expert tiles (their own tile table) for the ping-pong GEMMs
+  const bool pp256 = use_pp && !mx && !use_gemv && moe_uses_pp256(R, E);
   // the experts' row-pair weight copies on the same tiles, when the caller has them
-  const bool pair_w = use_pp && !mx && !use_gemv && g_moe_w4 == 0 && a->w13_pair_ptrs && a->w2_pair_ptrs;
+  const bool pair_w = !mx && moe_reads_pair_weights(T, k, E, H, I, rb) && a->w13_pair_ptrs && a->w2_pair_ptrs;
 
   // up to 256 tokens: the dispatch and the row quant of x in one launch
   const bool prep_decode = T <= 256 && rb == 0 && mx != 2;
@@ -1769,12 +1891,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     hipLaunchKernelGGL(moe_decode_prep_kernel, dim3((unsigned)(T + 1)), dim3(256), dsm, s, ridx, rwt, (int)T, k,
                        (int)E, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero,
                        a->x, (int)H, (void*)w.qx, w.ascx, mx ? 1 : 0, route_in_prep ? a->logits : nullptr,
-                       a->logits_dtype, a->ld_logits, a->router_tab, a->renormalize, a->idx_out, a->w_out);
+                       a->logits_dtype, a->ld_logits, a->router_tab, a->renormalize, a->idx_out, a->w_out, w.tiles2);
     if ((rc = lsk::check_launch("moe_decode_prep_kernel"))) return rc;
   } else if (nchunks == 1) {
     const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
     hipLaunchKernelGGL(moe_dispatch_small_kernel, dim3(1), dim3(256), dsm, s, ridx, rwt, (int)T, k, (int)E, w.offs,
-                       w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero);
+                       w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero, w.tiles2);
     if ((rc = lsk::check_launch("moe_dispatch_small_kernel"))) return rc;
   } else {
     hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)nchunks), dim3(256), (size_t)E * 4 + (size_t)256 * k * 4, s,
@@ -1783,7 +1905,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::check_launch("moe_count_kernel"))) return rc;
     hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)(4 * nchunks)), dim3(256),
                        (size_t)(11 * E + 1) * 4 + (size_t)256 * k * 6, s, ridx, rwt, (int)T, k, (int)E, w.ccnt,
-                       (int)nchunks, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w);
+                       (int)nchunks, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w, w.tiles2);
     if ((rc = lsk::check_launch("moe_place_kernel"))) return rc;
   }
   if (mx == 2 &&
@@ -1836,7 +1958,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
       g1.w_bytes = 2 * I * g1.ldw;
       g1.pairs |= 2;
     }
-    if ((rc = launch_moe_pp<0>(g1, w.max_tiles, s, "moe_pp_kernel<gate_up>"))) return rc;
+    if (pp256) {
+      g1.tiles = w.tiles2;
+      if ((rc = launch_moe_pp256<0>(g1, w.max_tiles2, s, "moe_pp256_kernel<gate_up>"))) return rc;
+    } else if ((rc = launch_moe_pp<0>(g1, w.max_tiles, s, "moe_pp_kernel<gate_up>"))) {
+      return rc;
+    }
   } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
     return rc;
   }
@@ -1924,7 +2051,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
       g2.w_bytes = H * g2.ldw;
       g2.pairs |= 2;
     }
-    if ((rc = launch_moe_pp<1>(g2, w.max_tiles, s, "moe_pp_kernel<down>"))) return rc;
+    if (pp256) {
+      g2.tiles = w.tiles2;
+      if ((rc = launch_moe_pp256<1>(g2, w.max_tiles2, s, "moe_pp256_kernel<down>"))) return rc;
+    } else if ((rc = launch_moe_pp<1>(g2, w.max_tiles, s, "moe_pp_kernel<down>"))) {
+      return rc;
+    }
   } else if ((rc = launch_moe_gemm<1>(g2, w.max_tiles, (int)((H + 127) / 128), s, "moe_gemm_kernel<down>"))) {
     return rc;
   }

@@ -499,6 +499,14 @@ extern "C" int lsk_pack_row_pairs(const int8_t* w, int64_t N, int64_t K, int64_t
   return lsk::check_launch("pack_row_pairs_kernel");
 }
 
+extern "C" int lsk_gemm_reads_row_pairs(int64_t M, int64_t N, int64_t K) {
+  // the question lsk_w8a8_matmul and lsk_linear_dyn ask of a 16-byte aligned weight copy whose
+  // rows are kp bytes apart, with the calling thread's tile selection
+  if (M <= 0 || N <= 0 || K <= 0 || K % 16 != 0) return 0;
+  const int64_t kp = (K + 63) / 64 * 64;
+  return lsk::gemm_takes_pp((const int8_t*)(uintptr_t)256, kp, M, N, K, kp) ? 1 : 0;
+}
+
 extern "C" int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t ldw,
                               const int8_t* w_pairs, int64_t N, int ew, float* y, int64_t ldy, int32_t* ex_out,
                               int stages, void* workspace, int64_t workspace_bytes, void* stream) {

@@ -223,19 +223,39 @@ class ExpertTables:
         self.ws2 = table(ws2)
         self.b13 = table(b13) if any(b13) else None
         self.b2 = table(b2) if any(b2) else None
-        # the weights' row-pair copies (ops.pack_row_pairs), which the ping-pong expert tiles read
-        # in whole 128-byte lines (the decode GEMVs and the other tiles read the weights above)
+        # the weights' row-pair copies, which the ping-pong expert tiles read in whole 128-byte
+        # lines (the decode GEMVs and the other tiles read the weights above): made by pair_ptrs()
+        # on the first call that reads them, held by each weight tensor (ops.row_pair_copy)
         self.w13_pairs = self.w2_pairs = None
-        if ROW_PAIRS and self.H % 16 == 0 and self.I % 16 == 0:
-            p13 = [ops.pack_row_pairs(t) for t in w13]
-            p2 = [ops.pack_row_pairs(t) for t in w2]
-            keep += p13 + p2
-            self.w13_pairs = table([t.data_ptr() for t in p13])
-            self.w2_pairs = table([t.data_ptr() for t in p2])
-            pairs += [(ex[0], t) for ex, t in zip(experts, p13)] + [(ex[2], t) for ex, t in zip(experts, p2)]
+        self._w13, self._w2 = w13, w2
         self._keep = keep
         pairs += [(ex[0], t) for ex, t in zip(experts, w13)] + [(ex[2], t) for ex, t in zip(experts, w2)]
+        # an in-place update of an int8 weight makes its row-pair copy stale as well
+        self._weights = [(ex[0], ex[0]._version) for ex in experts] + [(ex[2], ex[2]._version) for ex in experts]
         self._derived = _derived(pairs)
+
+    def pair_ptrs(self, T, k, rot_blk, select):
+        """(w13_pair_ptrs, w2_pair_ptrs) for a layer call of T tokens, top-k: the tables of the experts'
+        row-pair copies when that call reads them (lsk_moe_reads_row_pairs), else (None, None)."""
+        if not L.load().lsk_moe_reads_row_pairs(int(T), int(k), self.E, self.H, self.I, int(rot_blk), int(select)):
+            return None, None
+        return self.make_pairs()
+
+    def make_pairs(self):
+        """(w13_pair_ptrs, w2_pair_ptrs): the row-pair copy tables, made on first use; (None, None)
+        with ROW_PAIRS off, widths not multiples of 16, or while a graph is being captured."""
+        if not ROW_PAIRS or self.H % 16 or self.I % 16:
+            return None, None
+        if self.w13_pairs is None:
+            p13 = [ops.row_pair_copy(t) for t in self._w13]
+            p2 = [ops.row_pair_copy(t) for t in self._w2]
+            if any(t is None for t in p13 + p2):
+                return None, None              # (being captured into a graph: the weights themselves)
+            dev = self.device
+            self._pairs_keep = p13 + p2
+            self.w13_pairs = torch.tensor([t.data_ptr() for t in p13], dtype=torch.int64).to(dev)
+            self.w2_pairs = torch.tensor([t.data_ptr() for t in p2], dtype=torch.int64).to(dev)
+        return self.w13_pairs, self.w2_pairs
 
 
 def _derived(pairs):
@@ -244,7 +264,14 @@ def _derived(pairs):
     return [(src, src._version) for src, used in pairs if used.data_ptr() != src.data_ptr()]
 
 
+# Tables of the experts lists the layers have seen, keyed by the list and its per-expert tuples.  A
+# table holds device address tables (a few KB) and references to the list's tensors; the large
+# derived data, the int8 weights' row-pair copies, is held by the weight tensors themselves
+# (ops.row_pair_copy), so a table rebuilt after eviction re-packs nothing.  TABLES_MAX bounds how
+# many lists keep their tensors referenced here (more than the MoE layers of the largest model
+# served: Qwen3-30B-A3B has 48).
 _TABLES = {}
+TABLES_MAX = 256
 
 
 def _cached(kind, experts, build):
@@ -252,9 +279,12 @@ def _cached(kind, experts, build):
     id per expert), valid while every source read through a copy keeps its version."""
     key = (kind, id(experts), tuple(map(id, experts)))
     hit = _TABLES.get(key)
-    if hit is not None and hit._src is experts and all(t._version == v for t, v in hit._derived):
+    if hit is not None and hit._src is experts and all(t._version == v for t, v in hit._derived) \
+            and all(t._version == v for t, v in getattr(hit, "_weights", ())):
+        _TABLES[key] = _TABLES.pop(key)       # most recently used last
         return hit
-    if len(_TABLES) >= 8 and key not in _TABLES:
+    _TABLES.pop(key, None)
+    while len(_TABLES) >= TABLES_MAX:
         _TABLES.pop(next(iter(_TABLES)))
     hit = _TABLES[key] = build(experts)
     hit._src = experts
@@ -297,10 +327,10 @@ def kernel_choice(moe=None, mx=None):
     """The MoE layers called inside run with this kernel choice, passed per call
     (lsk_moe_args.select / mx_select; no reference counterpart, the same bits either way): moe as
     lsk_moe_select's variant (-1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV, 3 the
-    four-wave tile, 4 128-byte K stages), mx as lsk_moe_mx_select's (0, 1, 2); None keeps the
+    four-wave tile, 4 128-byte K stages, 5 the 256x256 tile), mx as lsk_moe_mx_select's (0, 1, 2); None keeps the
     calling thread's setting.  Scoped to this Python thread and the with-block."""
-    if moe is not None and not -1 <= moe <= 4:
-        raise ValueError("kernel_choice: moe=%r not in [-1, 4]" % (moe,))
+    if moe is not None and not -1 <= moe <= 5:
+        raise ValueError("kernel_choice: moe=%r not in [-1, 5]" % (moe,))
     if mx is not None and not 0 <= mx <= 2:
         raise ValueError("kernel_choice: mx=%r not in [0, 2]" % (mx,))
     prev = getattr(_CHOICE, "v", (0, 0))
@@ -338,6 +368,8 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
     nbytes = L.load().lsk_moe_workspace(T, k, tables.E, H, tables.I, rot_blk, 0)
     work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     sh = None if shared_out is None else shared_out.to(F32).contiguous()
+    choice = _choice_fields()
+    p13, p2 = tables.pair_ptrs(T, k, rot_blk, choice["select"])
     a = L.MoeArgs(T=T, H=H, I=tables.I, E=tables.E, k=k, act=act, x=x.data_ptr(), idx=idx.data_ptr(),
                   w=w.data_ptr(), w13_ptrs=tables.w13.data_ptr(), ldw13=tables.ldw13,
                   ws13_ptrs=tables.ws13.data_ptr(),
@@ -348,9 +380,9 @@ def _moe_layer(x, idx, w, tables: ExpertTables, act: int, rot_blk: int, shared_o
                   rot_scale=(1.0 / (rot_blk ** 0.5)) if rot_blk else 0.0,
                   shared=sh.data_ptr() if sh is not None else None, y=y.data_ptr(),
                   workspace=work.data_ptr(), workspace_bytes=nbytes,
-                  w13_pair_ptrs=tables.w13_pairs.data_ptr() if tables.w13_pairs is not None else None,
-                  w2_pair_ptrs=tables.w2_pairs.data_ptr() if tables.w2_pairs is not None else None,
-                  **fields, **_choice_fields())
+                  w13_pair_ptrs=p13.data_ptr() if p13 is not None else None,
+                  w2_pair_ptrs=p2.data_ptr() if p2 is not None else None,
+                  **fields, **choice)
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
     del keep
     return y if route is None else (y, idx, w)
@@ -501,7 +533,8 @@ def grouped_linear(tables, which: str, a8, asc, offs):
     ldw = tables.ldw13 if which == "w13" else tables.ldw2
     a8 = a8 if a8.stride(-1) == 1 else a8.contiguous()
     asc = asc.to(F32).contiguous()
-    wp = tables.w13_pairs if which == "w13" else tables.w2_pairs
+    # the ping-pong tiles, which read the row-pair copies, run once experts average 16 rows
+    wp = tables.make_pairs()[0 if which == "w13" else 1] if R >= 16 * tables.E else None
     L.call("lsk_grouped_gemm_w8a8_pairs", L.ptr(a8), a8.stride(0) if R > 1 else a8.shape[1], L.ptr(asc),
            L.ptr(offs), tables.E, R, L.ptr(w), ldw, L.ptr(wp), L.ptr(ws), L.ptr(b), N, a8.shape[1], L.ptr(out),
            L.ptr(work), nbytes, L.stream_of(a8))

@@ -5,8 +5,6 @@ These are the building blocks of the drop-in modules (`lockstep_fullstack`, `moe
 """
 from __future__ import annotations
 
-import collections
-import weakref
 
 import torch
 
@@ -296,37 +294,68 @@ def pack_row_pairs(w_nk: torch.Tensor) -> torch.Tensor:
     return out
 
 
-# Row-pair copies of the weights the GEMM sites have seen (the GEMM tiles read them in whole 128-byte
-# lines), keyed by the weight's storage and kept while the weight tensor lives and is unchanged:
-# an entry holds a weak reference to the tensor that owns the storage and that tensor's version
-# counter, which every in-place write through it or a view of it advances.
-_ROW_PAIRS = collections.OrderedDict()
-_ROW_PAIRS_MAX = 64
+# Row-pair copies of weights (the GEMM tiles read them in whole 128-byte lines): a prepared weight,
+# like the reference's arm-time W8 / ws on the module (lockstep_fullstack.py:1010-1011).  The copy is
+# held by the tensor that owns the weight's storage (an attribute of that tensor object), so it lives
+# exactly as long as the weight, with no cap and no eviction: one more copy of each such weight in HBM
+# (lsk_row_pairs_bytes(N, K), about N * K bytes).  Each entry records the owner's version counter,
+# which every in-place write through the weight or a view of it advances; a stale copy is remade.
+# ROW_PAIR_COPIES = False turns the copies off (the GEMMs then read the weights themselves);
+# release_row_pairs(w) frees a weight's copies.  row_pair_packs counts the copies made.
+ROW_PAIR_COPIES = True
+row_pair_packs = 0
+_ATTR = "_lsk_row_pairs"
 
 
-def row_pairs_of(w_nk):
-    """pack_row_pairs(w_nk), made once per weight and reused while the weight is unchanged;
-    None where the layout does not apply (K % 16 != 0, a weight being captured into a graph for the
-    first time)."""
-    N, K = w_nk.shape
-    if K == 0 or N == 0 or K % 16 != 0 or w_nk.stride(1) != 1 or w_nk.stride(0) % 16 != 0:
-        return None
+def _pair_key(w_nk):
     owner = w_nk._base if w_nk._base is not None else w_nk
-    key = (w_nk.device.index, w_nk.data_ptr(), N, K, w_nk.stride(0))
-    hit = _ROW_PAIRS.get(key)
-    if hit is not None:
-        ref, version, packed = hit
-        if ref() is owner and owner._version == version:
-            _ROW_PAIRS.move_to_end(key)
-            return packed
-        del _ROW_PAIRS[key]
-    if torch.cuda.is_current_stream_capturing():
+    return owner, (w_nk.data_ptr(), int(w_nk.shape[0]), int(w_nk.shape[1]), int(w_nk.stride(0)))
+
+
+def row_pair_copy(w_nk):
+    """pack_row_pairs(w_nk), made once per weight and kept on the tensor owning its storage while
+    that tensor is unchanged; None where the layout does not apply (K % 16 != 0, a strided or
+    unaligned weight), while a graph is being captured (the graph then reads the weight itself, so
+    replays follow later in-place updates of it), or with ROW_PAIR_COPIES off."""
+    global row_pair_packs
+    if not ROW_PAIR_COPIES or w_nk.dim() != 2 or w_nk.dtype != torch.int8:
         return None
+    N, K = w_nk.shape
+    if K == 0 or N == 0 or K % 16 != 0 or w_nk.stride(1) != 1 or w_nk.stride(0) % 16 != 0 \
+            or w_nk.data_ptr() % 16 != 0:
+        return None
+    if w_nk.is_cuda and torch.cuda.is_current_stream_capturing():
+        return None
+    owner, key = _pair_key(w_nk)
+    held = owner.__dict__.get(_ATTR)
+    if held is None:
+        held = {}
+        setattr(owner, _ATTR, held)
+    hit = held.get(key)
+    if hit is not None and hit[0] == owner._version:
+        return hit[1]
+    held.pop(key, None)                      # stale: free it before the new copy is made
     packed = pack_row_pairs(w_nk)
-    _ROW_PAIRS[key] = (weakref.ref(owner), owner._version, packed)
-    while len(_ROW_PAIRS) > _ROW_PAIRS_MAX:
-        _ROW_PAIRS.popitem(last=False)
+    row_pair_packs += 1
+    held[key] = (owner._version, packed)
     return packed
+
+
+def row_pairs_of(w_nk, rows):
+    """The weight's row-pair copy when a GEMM of `rows` activation rows against w_nk [N, K] reads one
+    (lsk_gemm_reads_row_pairs under the calling thread's tile selection), else None."""
+    if w_nk.dim() != 2 or not int(rows) > 0:
+        return None
+    N, K = w_nk.shape
+    if K % 16 != 0 or not L.load().lsk_gemm_reads_row_pairs(int(rows), int(N), int(K)):
+        return None
+    return row_pair_copy(w_nk)
+
+
+def release_row_pairs(w_nk):
+    """Free every row-pair copy held for the weight's storage."""
+    owner, _ = _pair_key(w_nk)
+    owner.__dict__.pop(_ATTR, None)
 
 
 def linear_dyn(x: torch.Tensor, w_nk: torch.Tensor, ew: int, stages: int = 3, work=None, y=None, ex=None,

@@ -86,10 +86,11 @@ def linear_dyn(x, W8, ew):
     if x.dim() != 2:
         raise ValueError("linear_dyn: x must be [T, K], got %s" % (tuple(x.shape),))
     w_nk = ops.weight_nk(_as_int8(W8))
-    return ops.linear_dyn(x, w_nk, int(ew), w_pairs=row_pairs_of(w_nk))
+    return ops.linear_dyn(x, w_nk, int(ew), w_pairs=row_pairs_of(w_nk, x.shape[0]))
 
 
-# the weights' row-pair copies (ops.row_pairs_of: one per weight, kept while it is unchanged)
+# the weights' row-pair copies (ops.row_pairs_of: one per weight, held by the weight while it is
+# unchanged, made only when the GEMM at that row count reads it)
 row_pairs_of = ops.row_pairs_of
 
 

@@ -244,7 +244,7 @@ def test_decode_w8a8_rows(M, N, K, xdt):
             assert np.array_equal(bits(y), want), (order, b is not None, name)
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 12, 13, 16, 17, 18])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 12, 13, 17, 18])
 def test_pow2_whole_tile_epilogue_exponent_range(tile):
     """The POW2 epilogue of whole ping-pong / four-wave tiles (binary32 out, per-row exponents,
     stored straight from the accumulators) over the whole exponent range: shift + erow from -140
@@ -365,7 +365,7 @@ def test_config2_prefill_rows_and_chunk_invariance(which, seed):
     assert torch.equal(chunks.view(torch.int16), y.view(torch.int16))
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 16, 17, 18])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 17, 18])
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 257, 640), (512, 520, 2880), (64, 64, 16),
                                    (1, 1000, 14336), (3, 77, 2880), (4, 300, 1040), (8, 1000, 4096),
                                    (17, 77, 2880), (32, 520, 14336), (5, 33, 48), (24, 32800, 320),
@@ -390,7 +390,7 @@ def test_every_tile_config_is_exact(tile, M, N, K):
     assert np.array_equal(bits(acc), C.int_mm(C.rowquant(x)[0], W8.T))
 
 
-@pytest.mark.parametrize("tile", [1, 3, 4, 12, 13, 16, 17, 18])
+@pytest.mark.parametrize("tile", [1, 3, 4, 12, 13, 17, 18])
 @pytest.mark.parametrize("out", ["bf16", "f32"])
 def test_epilogue_special_scales(tile, out):
     """Scales that can make outputs infinite or NaN, placed so that some tiles hold none of them

@@ -89,3 +89,62 @@ def test_grouped_linear_mx(R, E, N, K, bias):
         m2, kexp = C.mx_to_m2(codes, kx)
         ref = C.lin_epilogue_mx(C.int_mm_mx(a8[r0:r1], m2, kexp), asc[r0:r1], b)
         assert np.array_equal(got[r0:r1], C.bf16_bits(ref)), "expert %d" % e
+
+
+@pytest.mark.parametrize("variant", [1, 5])
+def test_grouped_linear_int8_tile_choice(variant):
+    """The grouped linear on the 128x256 (1) and the 256x256 (5) ping-pong tiles, each chosen, with
+    experts of several 256-row tiles and a bias: the oracle's bits."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    R, E, N, K = 1500, 5, 384, 320
+    g = np.random.default_rng(91 + variant)
+    cnt = _counts(g, E, R)
+    offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)
+    a8 = g.integers(-127, 128, (R, K), dtype=np.int8)
+    asc = g.uniform(1e-3, 1e-1, R).astype(F32)
+    experts = [(g.integers(-127, 128, (N, K), dtype=np.int8), g.uniform(1e-3, 1e-2, N).astype(F32),
+                g.standard_normal(N).astype(F32)) for _ in range(E)]
+    dev_ex = [(to_dev(W).t(), to_dev(ws), to_dev(np.zeros((K, N // 2), np.int8)).t(), to_dev(np.ones(K, F32)),
+               to_dev(b), None) for (W, ws, b) in experts]
+    L.call("lsk_moe_select", variant)
+    try:
+        out = MR.grouped_linear(dev_ex, "w13", to_dev(a8), to_dev(asc), to_dev(offs))
+    finally:
+        L.call("lsk_moe_select", -1)
+    got = bits(out)
+    for e, (W, ws, b) in enumerate(experts):
+        r0, r1 = offs[e], offs[e + 1]
+        if r1 > r0:
+            ref = C.lin_epilogue_b(C.int_mm(a8[r0:r1], W.T), ws, asc[r0:r1], b)
+            assert np.array_equal(got[r0:r1], C.bf16_bits(ref)), "expert %d" % e
+
+
+def test_grouped_linear_clamps_bad_offsets():
+    """Offsets that decrease or run past R are made monotone and clamped to R on the device (a
+    running maximum): experts come out empty or shortened, the rows they keep match the oracle, and
+    nothing outside [0, R) is touched (the output has guard rows after R that stay as written)."""
+    from lockstep_amd import moe_ref as MR
+    R, E, N, K = 500, 6, 128, 256
+    g = np.random.default_rng(77)
+    offs = np.array([0, 100, 80, 300, 700, 650, 900], np.int32)       # -> 0 100 100 300 500 500 500
+    co = np.minimum(np.maximum.accumulate(np.maximum(offs, 0)), R)
+    a8 = g.integers(-127, 128, (R, K), dtype=np.int8)
+    asc = g.uniform(1e-3, 1e-1, R).astype(F32)
+    experts = [(g.integers(-127, 128, (N, K), dtype=np.int8), g.uniform(1e-3, 1e-2, N).astype(F32))
+               for _ in range(E)]
+    dev_ex = [(to_dev(W).t(), to_dev(ws), to_dev(np.zeros((K, N // 2), np.int8)).t(), to_dev(np.ones(K, F32)),
+               None, None) for (W, ws) in experts]
+    for variant in (-1, 0, 1, 5):
+        from lockstep_amd import _lib as L
+        L.call("lsk_moe_select", variant)
+        try:
+            out = MR.grouped_linear(dev_ex, "w13", to_dev(a8), to_dev(asc), to_dev(offs))
+        finally:
+            L.call("lsk_moe_select", -1)
+        got = bits(out)
+        for e, (W, ws) in enumerate(experts):
+            r0, r1 = co[e], co[e + 1]
+            if r1 > r0:
+                ref = C.lin_epilogue(C.int_mm(a8[r0:r1], W.T), ws, asc[r0:r1])
+                assert np.array_equal(got[r0:r1], C.bf16_bits(ref)), (variant, e)

@@ -193,11 +193,11 @@ def test_moe_multi_chunk_dispatch(T, E, k):
     _run_case(T, E, k, 128, 64, seed=11 + T)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
 def test_moe_grouped_gemm_variants(variant):
     """Every grouped-GEMM kernel (register-staged 128x128 tile, ping-pong 128x256 tile, the
-    decode GEMV, the 128x256 tile on four waves, the ping-pong tile with 128-byte K stages) gives
-    the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
+    decode GEMV, the 128x256 tile on four waves, the ping-pong tile with 128-byte K stages, the
+    256x256 tile) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
     their rows eight at a time), empty experts, a bias and SwiGLU-OAI; an odd number of routed rows
     (the down tiles' row-pair operand ends in a half pair)."""
     from lockstep_amd import _lib as L
@@ -207,6 +207,22 @@ def test_moe_grouped_gemm_variants(variant):
         _run_case(301, 8, 3, 256, 128, seed=17)
         _run_case(150, 6, 2, 320, 96, seed=14, bias=True, act="swigluoai")
         _run_case(5, 16, 4, 256, 128, seed=15)
+        if variant in (1, 5):
+            # experts of several 256-row tiles and a partial last one, I not a multiple of 128
+            _run_case(1100, 6, 3, 384, 320, seed=18)
+    finally:
+        L.call("lsk_moe_select", -1)
+
+
+def test_moe_256_tiles():
+    """The 256x256 expert tiles (chosen): Zipf-skewed experts of one to several 256-row tiles, with a
+    bias and SwiGLU-OAI, and with the shared expert on."""
+    from lockstep_amd import _lib as L
+    L.call("lsk_moe_select", 5)
+    try:
+        _run_case(700, 8, 4, 256, 256, seed=31)
+        _run_case(513, 4, 2, 512, 192, seed=32, bias=True, act="swigluoai")
+        _run_case(900, 8, 2, 256, 128, seed=33, shared=True)
     finally:
         L.call("lsk_moe_select", -1)
 
@@ -218,7 +234,7 @@ def test_moe_per_call_kernel_choice():
     from lockstep_amd import moe_ref as MR
     L.call("lsk_moe_select", 2)            # the thread: the decode GEMV
     try:
-        for v in (0, 1, 3, 4, -1):
+        for v in (0, 1, 3, 4, 5, -1):
             with MR.kernel_choice(moe=v):
                 _run_case(300, 12, 4, 256, 192, seed=13)
         _run_case(40, 8, 3, 256, 192, seed=16)   # the thread's setting again

@@ -1,0 +1,88 @@
+"""The weights' row-pair copies are prepared weights: made once per weight, held by the weight
+tensor itself, made only where the GEMM reads them.  CPU-side: the C queries (no device work) and
+the caching logic with the pack counted (pack_row_pairs replaced by a counting stand-in)."""
+import pytest
+import torch
+
+from lockstep_amd import _lib as L
+from lockstep_amd import ops
+
+
+def test_gemm_row_pair_query():
+    lib = L.load()
+    # decode and mid row counts stream W8 or use the register-staged tile: no copy is read
+    for M in (1, 8, 32, 64, 128):
+        assert lib.lsk_gemm_reads_row_pairs(M, 28672, 4096) == 0, M
+    # prefill row counts on the ping-pong tiles read it
+    for M, N, K in ((2048, 28672, 4096), (2048, 4096, 14336), (8192, 37888, 3584), (8192, 3584, 18944)):
+        assert lib.lsk_gemm_reads_row_pairs(M, N, K) == 1, (M, N, K)
+    assert lib.lsk_gemm_reads_row_pairs(2048, 4096, 100) == 0        # K % 16 != 0
+    assert lib.lsk_gemm_reads_row_pairs(0, 4096, 4096) == 0
+
+
+def test_moe_row_pair_query():
+    lib = L.load()
+    E, k, H, I = 128, 8, 2048, 768
+    assert lib.lsk_moe_reads_row_pairs(1, k, E, H, I, 0, 0) == 0       # the grouped GEMV
+    assert lib.lsk_moe_reads_row_pairs(32, k, E, H, I, 0, 0) == 0
+    assert lib.lsk_moe_reads_row_pairs(4096, k, E, H, I, 0, 0) == 1    # the ping-pong tiles
+    # a per-call choice of the register-staged tile (select = variant + 2) reads none
+    assert lib.lsk_moe_reads_row_pairs(4096, k, E, H, I, 0, 2) == 0
+    # the thread's own setting is left as it was
+    assert lib.lsk_moe_reads_row_pairs(4096, k, E, H, I, 0, 0) == 1
+
+
+@pytest.fixture
+def counting_pack(monkeypatch):
+    made = []
+
+    def fake_pack(w):
+        made.append((w.data_ptr(), tuple(w.shape)))
+        return torch.empty((L.load().lsk_row_pairs_bytes(*w.shape),), dtype=torch.int8)
+    monkeypatch.setattr(ops, "pack_row_pairs", fake_pack)
+    return made
+
+
+def test_130_dense_weights_pack_once(counting_pack):
+    """A model's worth of distinct dense weights (130) cycled twice through the prefill path: each
+    copy is made on the first pass and reused on the second; decode row counts make none."""
+    ws = [torch.zeros((512, 256), dtype=torch.int8) for _ in range(130)]
+    for w in ws:
+        assert ops.row_pairs_of(w, 32) is None
+    assert counting_pack == []
+    first = [ops.row_pairs_of(w, 2048) for w in ws]
+    assert len(counting_pack) == 130 and all(p is not None for p in first)
+    second = [ops.row_pairs_of(w, 2048) for w in ws]
+    assert len(counting_pack) == 130
+    assert all(a is b for a, b in zip(first, second))
+    # views of the same storage (the reference's b8 = W8.t() turned back) share the copy
+    assert ops.row_pairs_of(ws[0].t().t(), 2048) is first[0]
+    # an in-place update re-makes that weight's copy only
+    ws[7].add_(1)
+    assert ops.row_pairs_of(ws[7], 2048) is not first[7]
+    assert len(counting_pack) == 131
+    assert ops.row_pairs_of(ws[8], 2048) is first[8] and len(counting_pack) == 131
+
+
+def test_copy_lives_with_the_weight(counting_pack):
+    import gc
+    import weakref
+    w = torch.zeros((64, 64), dtype=torch.int8)
+    p = ops.row_pairs_of(w, 4096)
+    ref = weakref.ref(p)
+    del p
+    assert ref() is not None                 # held by the weight
+    ops.release_row_pairs(w)
+    gc.collect()
+    assert ref() is None
+    p = ops.row_pairs_of(w, 4096)
+    ref = weakref.ref(p)
+    del p, w
+    gc.collect()
+    assert ref() is None                     # freed with the weight
+
+
+def test_copies_can_be_turned_off(counting_pack, monkeypatch):
+    monkeypatch.setattr(ops, "ROW_PAIR_COPIES", False)
+    assert ops.row_pairs_of(torch.zeros((64, 64), dtype=torch.int8), 4096) is None
+    assert counting_pack == []

@@ -4,7 +4,8 @@ On MI355X a 16-byte global / buffer store followed a few instructions later by V
 its data registers was measured to store the newer values; the compiler leaves only one wait
 state between them.  Every kernel therefore stores at most 8 bytes per instruction
 (`store16_split` in csrc/lsk_common.h).  This test disassembles the gfx950 code objects of the
-in-tree library and fails on any dwordx3 / dwordx4 global or buffer store."""
+in-tree library and fails on any 12- or 16-byte global, buffer, flat or scratch store (register
+spills included)."""
 import os
 import re
 import shutil
@@ -15,7 +16,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB = os.path.join(ROOT, "lockstep_amd", "liblockstep_amd.so")
 OBJDUMP = "/opt/rocm/llvm/bin/llvm-objdump"
-WIDE = re.compile(r"\b(global|buffer)_store_dwordx[34]\b")
+WIDE = re.compile(r"\b(global|buffer|flat|scratch)_store_(dwordx[34]|b96|b128)\b")
 
 
 @pytest.mark.skipif(not (os.path.exists(LIB) and os.path.exists(OBJDUMP)),
