@@ -319,7 +319,7 @@ def test_config1_o_proj_m16_bit_exact():
     assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, None, "bf16"))
 
 
-@pytest.mark.parametrize("seed", [1, 3, 4])
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
 @pytest.mark.parametrize("M", [1, 8, 32])
 @pytest.mark.parametrize("which", ["gate_up", "down"])
 def test_config2_decode_bit_exact(M, which, seed):
@@ -332,10 +332,10 @@ def test_config2_decode_bit_exact(M, which, seed):
     assert np.array_equal(bits(y), C.w8a8_matmul(x, W8, ws, None, "bf16"))
 
 
-@pytest.mark.parametrize("seed", [2, 4])
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
 @pytest.mark.parametrize("which", ["gate_up", "down"])
 def test_config2_prefill_rows_and_chunk_invariance(which, seed):
-    """M=2048: a seeded subset of rows against the oracle; for every row the quantised rows
+    """M=2048: a seeded subset of 256 rows against the oracle; for every row the quantised rows
     against the oracle's quantiser, the int32 accumulator's column and row sums against exact
     integer identities, the fused v2.1 epilogue against the separate epilogue over that
     accumulator, and the whole result equal to the same rows computed in 64-row chunks (row
@@ -350,7 +350,7 @@ def test_config2_prefill_rows_and_chunk_invariance(which, seed):
     x, W8, ws = WL.dense_inputs(M, N, K, seed=seed, outliers=True)
     xd, Wd, wsd = to_dev(x), to_dev(W8), to_dev(ws)
     y = FS.w8a8_matmul(xd, Wd, wsd, out_dtype=torch.bfloat16)
-    rows = np.sort(_rng(3 + seed).choice(M, 24, replace=False))
+    rows = np.sort(_rng(3 + seed).choice(M, 256, replace=False))
     ref = C.w8a8_matmul(x[rows], W8, ws, None, "bf16")
     assert np.array_equal(bits(y)[rows], ref)
     q, asc = ops.rowquant(xd)
