@@ -236,6 +236,13 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * The choice applies to the calling host thread's later launches only (thread-local). */
 int lsk_gemm_select(int tile_id);
 
+/* Tuning control with no counterpart in the reference: 1 (the default) runs lsk_w8a8_matmul /
+ * lsk_w8a8_matmul_pairs with one activation row and K <= 4096 as a single launch, the row quant
+ * fused into the whole-row decode GEMV (each block quantises the row itself into LDS); 0 runs the
+ * row quant and the GEMV as two launches.  Results are identical.  Thread-local, like
+ * lsk_gemm_select. */
+int lsk_gemm_fuse_rowquant(int on);
+
 /* Tuning control with no counterpart in the reference: the persistent form of the 256x256
  * ping-pong kernel, taken for whole tiles under the POW2 epilogue with binary32 output (the
  * ref_block_v1 GEMMs): 1 one block per compute unit (the default), 0 off (one tile per block),
@@ -535,6 +542,12 @@ int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const 
                         int64_t N, int64_t K, int safe, uint16_t* out, void* workspace, int64_t workspace_bytes,
                         void* stream);
 
+/* Tuning control with no counterpart in the reference: 1 (the default) runs a one-token int8 layer
+ * routed from its logits (lsk_moe_args.logits, the grouped GEMV path, k <= 8) with the router, the
+ * row quant of x and the gate/up GEMV in one launch, every wave routing the token and quantising x
+ * itself; 0 runs them as the prep launch and the GEMV.  Results are identical.  Thread-local. */
+int lsk_moe_fuse_route(int on);
+
 /* Tuning control with no counterpart in the reference: the int8 grouped expert GEMMs of
  * lsk_moe_forward on the 128x128 register-staged tile (0), on the eight-wave ping-pong
  * 128x256 tile (1), on the grouped GEMV (2: whole weight rows streamed once against up to 8
@@ -566,6 +579,13 @@ int lsk_moe_mx_select(int variant);
  * caller; 65536 int8 ops per MFMA.  Constant versus uniformly random operands shows the power cost
  * of toggling operands. */
 int lsk_mfma_probe(const void* ops, int64_t nops, int64_t blocks, int iters, int32_t* sink, void* stream);
+
+/* Diagnostic with no counterpart in the reference: one v_mfma_f32_16x16x32_bf16 per case with the
+ * caller's accumulator input, D = A B^T + C over K = 32.  Case c: a, b [16][32] bf16 (rows M / N,
+ * K contiguous, 16-byte aligned), cin, d [16][16] binary32 (row M, column N), ncases cases back to
+ * back.  It measures how the matrix core rounds the addition of C to an exact block sum. */
+int lsk_mfma_bf16_acc_probe(const uint16_t* a, const uint16_t* b, const float* cin, float* d, int ncases,
+                            void* stream);
 
 /* The library's bf16 conversion check, no counterpart in the reference: over the binary32
  * patterns start .. start + count - 1 (start + count <= 2^32), gfx950's packed v_cvt_pk_bf16_f32

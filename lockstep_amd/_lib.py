@@ -54,6 +54,8 @@ SIGNATURES = {
                                _I64, _P, _P, _P]),
     "lsk_tree_sum": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lsk_gemm_select": (_I, [_I]),
+    "lsk_gemm_fuse_rowquant": (_I, [_I]),
+    "lsk_moe_fuse_route": (_I, [_I]),
     "lsk_gemm_persist": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),
     "lsk_quant8_dyn_workspace": (_I64, []),
@@ -84,6 +86,7 @@ SIGNATURES = {
     "lsk_grouped_gemm_mx": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I, _P, _P, _I64,
                                  _P]),
     "lsk_moe_select": (_I, [_I]),
+    "lsk_mfma_bf16_acc_probe": (_I, [_P, _P, _P, _P, _I, _P]),
     "lsk_mfma_probe": (_I, [_P, _I64, _I64, _I, _P, _P]),
     "lsk_bf16_cvt_check": (_I, [ctypes.c_uint64, ctypes.c_uint64, _P, _P, _P]),
     "lsk_moe_mx_select": (_I, [_I]),

@@ -1043,6 +1043,138 @@ __global__ __launch_bounds__(256) void gemv_i8_row_kernel(const int8_t* __restri
   }
 }
 
+// The whole-row GEMV for one activation row with the contract's row quant fused in (the drop-in
+// w8a8_matmul at M = 1: one launch instead of the row quant and the GEMV).  Every block quantises
+// the row itself: thread t holds the 8-element chunks t, t + 256, ... of x in registers (x read
+// once per block, from L2 after the first block), the block takes their maximum, derives asc =
+// fl32(max(amax, 1e-8) / 127) and writes q = clamp(rint(x / asc)) to LDS with rowquant's arithmetic
+// (quant_one), then streams its weight rows as gemv_i8_row_kernel does, its first weight row
+// requested before x.  All blocks compute the same asc and q.  K % 16 == 0, K <= 2048 NV; x 16-byte
+// aligned.
+template <int NC, int NV, int DT>
+__global__ __launch_bounds__(256) void gemv_i8_rowq_kernel(const void* __restrict__ X, const int8_t* __restrict__ W,
+                                                           int ldw, int N, int K, int wk, int rpw, EpiParams ep) {
+  __shared__ int red[4][16];  // [wave][row of the wave], rpw <= 16
+  __shared__ float bred[4];
+  __shared__ __attribute__((aligned(16))) int8_t qs[NV * 2048];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int rg = wave / wk, ks = wave % wk;
+  const int rows_blk = rpw * (4 / wk);
+  const int n0 = blockIdx.x * rows_blk;
+  const int nrows = (N - n0) < rows_blk ? (N - n0) : rows_blk;
+  const int kb = ks * NC * 1024;
+  const int ke = (kb + NC * 1024) < K ? (kb + NC * 1024) : K;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)nrows * ldw);
+  uint32_t koff[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int kk = kb + j * 1024 + lane * 16;
+    koff[j] = kk < ke ? (uint32_t)kk : lsk::kOob;
+  }
+  const int r0 = rg * rpw;
+  auto load_row = [&](v4i* w, int i) {
+    const int rl = r0 + i;
+    const uint32_t rowoff = rl < nrows ? (uint32_t)(rl * ldw) : lsk::kOob;
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+      w[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rw, (rowoff == lsk::kOob || koff[j] == lsk::kOob) ? lsk::kOob : rowoff + koff[j],
+                                         0, 2 /* non-temporal */));
+  };
+  // x first, then the first two weight rows: vector loads complete in issue order, so the wait
+  // for x below leaves the weight rows in flight while x is quantised
+  const int K8 = K >> 3;
+  constexpr int kXW = DT == LSK_F32 ? 2 : 1;  // 16-byte loads per 8 elements
+  uint4 xr[NV][kXW];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = tid + j * 256;
+#pragma unroll
+    for (int h = 0; h < kXW; ++h)
+      xr[j][h] = c < K8 ? ((const uint4*)X)[(int64_t)c * kXW + h] : make_uint4(0, 0, 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  v4i w0[NC], w1[NC];
+  load_row(w0, 0);
+  if (rpw > 1) load_row(w1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the activation row: maximum, scale, quantised values into LDS
+  float v[NV][8];
+  float am = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    // (bf16 / f16: the first four words hold the eight elements)
+    const uint32_t wd[8] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w,
+                            xr[j][kXW - 1].x, xr[j][kXW - 1].y, xr[j][kXW - 1].z, xr[j][kXW - 1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (DT == LSK_F32) v[j][e] = __uint_as_float(wd[e]);
+      else if (DT == LSK_BF16) v[j][e] = bf16_to_f32((uint16_t)(wd[e >> 1] >> (16 * (e & 1))));
+      else v[j][e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wd[e >> 1] >> (16 * (e & 1))));
+      am = fmaxf(am, fabsf(v[j][e]));
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  if (lane == 0) bred[wave] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(bred[0], bred[1]), fmaxf(bred[2], bred[3]));
+  am = fmaxf(am, kAmaxFloor);
+  const float sc = f32_div(am, 127.0f), rs = f32_div(1.0f, sc);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = tid + j * 256;
+    if (c < K8) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lo |= ((uint32_t)(uint8_t)quant_one(v[j][e], sc, rs)) << (8 * e);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hi |= ((uint32_t)(uint8_t)quant_one(v[j][4 + e], sc, rs)) << (8 * e);
+      *(uint2*)(qs + 8 * c) = make_uint2(lo, hi);
+    }
+  }
+  __syncthreads();
+  v4i a[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) a[j] = koff[j] != lsk::kOob ? *(const v4i*)(qs + koff[j]) : v4i{0, 0, 0, 0};
+
+  auto row_sum = [&](const v4i* w, int i) {
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      acc = __builtin_amdgcn_sdot4(a[j][0], w[j][0], acc, false);
+      acc = __builtin_amdgcn_sdot4(a[j][1], w[j][1], acc, false);
+      acc = __builtin_amdgcn_sdot4(a[j][2], w[j][2], acc, false);
+      acc = __builtin_amdgcn_sdot4(a[j][3], w[j][3], acc, false);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    if (lane == 0) red[wave][i] = acc;
+  };
+  // two register sets in turn, each reloaded as soon as its row is summed
+  for (int i = 0; i < rpw; i += 2) {
+    row_sum(w0, i);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 2 < rpw) load_row(w0, i + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 1 >= rpw) break;
+    row_sum(w1, i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (i + 3 < rpw) load_row(w1, i + 3);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  __syncthreads();
+  // the K-slices of each row: one lane per row of the row group
+  if (ks != 0 || lane >= rpw) return;
+  const int rl = r0 + lane;
+  const int n = n0 + rl;
+  if (rl >= nrows) return;
+  const EpiCol ec = epi_col_load(ep, n);
+  int sum = 0;
+  for (int k2 = 0; k2 < wk; ++k2) sum += red[rg * wk + k2][lane];
+  epilogue_store_rc(ep, 0, n, sum, EpiRow{sc, 0}, ec);
+}
+
 // Correctness path for shapes the tiled kernels do not take (odd K, unaligned rows).
 __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(const int8_t* __restrict__ A, int64_t lda,
                                                               const int8_t* __restrict__ W, int64_t ldw, int64_t M,
@@ -1092,6 +1224,7 @@ int validate_epilogue(int order, int out_dtype, const float* asc, const float* w
 // Tile configurations of the dense kernel; id -1 lets the shape decide.
 thread_local int g_force_tile = -1;
 thread_local int g_row_rpw = 0;       // rows per wave of the whole-row GEMV (0: by shape)
+thread_local int g_rowq = 1;          // w8a8_matmul at M = 1: the row quant fused into the whole-row GEMV
 thread_local int g_gemv_variant = 0;  // M <= 4: 0 whole-row GEMV, 1 register double-buffered 8-row GEMV, 2 LDS-ring 8-row GEMV
 thread_local int g_gemv_mid = 0;      // 4 < M <= 32: 0 by shape, 1 direct 64-byte row pieces, 2 whole rows through LDS
 
@@ -1373,6 +1506,47 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
   return check_launch("gemv_i8_stream_kernel");
 }
 
+// Whether lsk_w8a8_matmul takes the fused row-quant GEMV for one activation row: the decode GEMV
+// would run (no forced tile other than the GEMV, the whole-row variant), K % 16 == 0 and
+// K <= 4096, x and w 16-byte aligned, the v2.1 or v2 order.  (Every block reads x, so the fusion
+// pays only while x is small: on MI355X, graph replays over weight copies, Llama-3.1-8B gate_up
+// M = 1 (K = 4096) 21.2 us fused against 22.1 us as two launches; the down projection (K = 14336,
+// 57 KB of x per block) 16.0 us at best against 15.3-16.1 us.)
+bool rowq_gemv_ok(const void* x, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int order) {
+  return g_rowq && M == 1 && N >= 1 && N <= 0x7fffffff && K >= 16 && K <= 4096 && K % 16 == 0 && ldw % 16 == 0 &&
+         aligned16(x) && aligned16(w) && (g_force_tile < 0 || g_force_tile == 5) && g_gemv_variant == 0 &&
+         (order == LSK_EPI_V21 || order == LSK_EPI_V2) && ldw * 64 < 0x7fffffff;
+}
+
+int launch_gemv_rowq(const void* x, int x_dtype, const int8_t* w, int ldw, int N, int K, const EpiParams& ep,
+                     hipStream_t s) {
+  const int nch = (K + 1023) / 1024;
+  int wk = 1;
+  while (wk < 4 && (nch + wk - 1) / wk > 4) wk *= 2;
+  const int nc = (nch + wk - 1) / wk;
+  // rows per wave: each block reads x once, so more than one row per wave amortises it (two
+  // measured best: 21.2 us at gate_up M = 1 against 26.9 / 23.0 / 23.5 us at 1 / 4 / 8); fewer
+  // when N leaves under about 2048 waves
+  int rpw = 2;
+  while (rpw > 1 && (int64_t)((N + rpw * (4 / wk) - 1) / (rpw * (4 / wk))) * 4 < 2048) rpw /= 2;
+  if (g_row_rpw > 0) rpw = g_row_rpw;
+  const int rows_blk = rpw * (4 / wk);
+  const int blocks = (N + rows_blk - 1) / rows_blk;
+#define LSK_RQ(NCV, NVV, DTV)                                                                              \
+  {                                                                                                        \
+    hipLaunchKernelGGL((gemv_i8_rowq_kernel<NCV, NVV, DTV>), dim3((unsigned)blocks), dim3(256), 0, s, x, w, ldw, N, K, \
+                       wk, rpw, ep);                                                                       \
+    return check_launch("gemv_i8_rowq_kernel");                                                            \
+  }
+#define LSK_RQ_DT(NCV, NVV) \
+  if (x_dtype == LSK_F32) LSK_RQ(NCV, NVV, LSK_F32) else if (x_dtype == LSK_BF16) LSK_RQ(NCV, NVV, LSK_BF16) else LSK_RQ(NCV, NVV, LSK_F16)
+  if (nc <= 1) LSK_RQ_DT(1, 2)
+  if (nc <= 2) LSK_RQ_DT(2, 2)
+  LSK_RQ_DT(4, 2)
+#undef LSK_RQ_DT
+#undef LSK_RQ
+}
+
 static bool tiles_fast(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K) {
   // the tile kernels address rows by 32-bit offsets inside a 256-row tile
   return (K % 16 == 0) && (lda % 16 == 0) && (ldw % 16 == 0) && aligned16(a) && aligned16(w) && M <= 0x7fffffff &&
@@ -1493,6 +1667,12 @@ extern "C" int lsk_w8a8_matmul_pairs(const void* x, int x_dtype, int64_t ldx, in
   LSK_REQUIRE(workspace && workspace_bytes >= need, "lsk_w8a8_matmul: workspace of %lld bytes needed",
               (long long)need);
   LSK_REQUIRE(((uintptr_t)workspace & 255) == 0, "lsk_w8a8_matmul: workspace must be 256-byte aligned");
+  // one activation row: the row quant fused into the whole-row GEMV (one launch)
+  if (lsk::rowq_gemv_ok(x, w, ldw, M, N, K, order) && (x_dtype == LSK_F32 || x_dtype == LSK_BF16 || x_dtype == LSK_F16)) {
+    LSK_REQUIRE(x && w && out && ldw >= K && ldo >= N, "lsk_w8a8_matmul: bad operand");
+    EpiParams ep{order, out_dtype, ws, nullptr, bias, nullptr, nullptr, 0, out, ldo};
+    return lsk::launch_gemv_rowq(x, x_dtype, w, (int)ldw, (int)N, (int)K, ep, (hipStream_t)stream);
+  }
   // the row-pair layout when every tile of the GEMM is a ping-pong tile; row-major otherwise
   const int64_t kp = (K + 63) / 64 * 64;
   const bool pair = lsk::rowquant_pair_ok(x, x_dtype, ldx, K) && lsk::gemm_takes_pp(w, ldw, M, N, K, kp);
@@ -1534,6 +1714,12 @@ extern "C" int lsk_epilogue_apply(const int32_t* acc, int64_t ldc, int64_t M, in
   hipLaunchKernelGGL(epilogue_apply_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, acc, ldc, M,
                      N, ep);
   return lsk::check_launch("epilogue_apply_kernel");
+}
+
+extern "C" int lsk_gemm_fuse_rowquant(int on) {
+  LSK_REQUIRE(on == 0 || on == 1, "lsk_gemm_fuse_rowquant: %d not 0 or 1", on);
+  lsk::g_rowq = on;
+  return LSK_OK;
 }
 
 extern "C" int lsk_gemm_persist(int blocks) {

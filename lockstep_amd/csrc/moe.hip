@@ -29,6 +29,7 @@ constexpr int kBM = lsk::kMoeBM;
 constexpr int kBM2 = 256;  // rows per tile of the 256 x 256 expert tiles (their own tile table)
 thread_local int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV,
                        // 3 the 128x256 tile on the four-wave main loop
+thread_local int g_rowq1 = 1;       // one-token layers from logits: router + row quant + gate/up GEMV in one launch
 thread_local int g_moe_w4 = 0;      // the ping-pong tile: 0 128x256 eight-wave ping-pong, 1 128x256 four waves,
                                     // 2 128x256 with 128-byte K stages, 3 256x256 (eight waves, four-stage ring)
 
@@ -43,10 +44,12 @@ LSK_DEV long long wave_max_ll(long long v) {
 
 // One wave per token; lane l owns experts l, l + 64, ... (EPL per lane, E <= 64 * EPL).  The
 // reference's ranking key s * E + (E - 1 - e) orders like the pair (s, E - 1 - e), so the key is
-// kept as s << 32 | (E - 1 - e) and decoded with shifts.
+// kept as s << 32 | (E - 1 - e) and decoded with shifts.  The selection: lane r < k gets the rank-r
+// expert e_r and its score s_r; S is the score sum the weights divide by (the selected scores, or
+// all of them without renormalisation), clamped to >= 1.
 template <int EPL>
-LSK_DEV void route_token(const void* __restrict__ g, int gdt, int64_t ldg, int t, int E, int k, int renorm,
-                         const int32_t* __restrict__ tab, int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
+LSK_DEV void route_select(const void* __restrict__ g, int gdt, int64_t ldg, int t, int E, int k, int renorm,
+                          const int32_t* __restrict__ tab, int& e_mine, int& s_mine, int& S) {
   const int lane = threadIdx.x & 63;
   float gv[EPL];
   float m = -__builtin_inff();
@@ -69,17 +72,18 @@ LSK_DEV void route_token(const void* __restrict__ g, int gdt, int64_t ldg, int t
     key[j] = -1;
     if (e < E) {
       const float v = rintf(f32_mul(m - gv[j], kRouterC));
-      int s = 0;
+      int sc = 0;
       if (v < 1073741824.0f) {  // d < 16 << 26 (also false for NaN / inf)
         const int d = v > 0.0f ? (int)v : 0;
-        s = tab[(d >> 13) & 8191] >> (d >> 26);
+        sc = tab[(d >> 13) & 8191] >> (d >> 26);
       }
-      s_all += s;
-      key[j] = ((long long)s << 32) | (long long)(unsigned)(E - 1 - e);
+      s_all += sc;
+      key[j] = ((long long)sc << 32) | (long long)(unsigned)(E - 1 - e);
     }
   }
   for (int o = 32; o > 0; o >>= 1) s_all += __shfl_xor(s_all, o, 64);
-  int s_sel_mine = 0;  // lane r keeps the score of rank r
+  s_mine = 0;
+  e_mine = 0;
   int s_sum = 0;
   for (int r = 0; r < k; ++r) {
     long long best = -1;
@@ -89,16 +93,27 @@ LSK_DEV void route_token(const void* __restrict__ g, int gdt, int64_t ldg, int t
     const int e = (E - 1) - (int)(unsigned)(best & 0xffffffffLL);
     const int sc = (int)(best >> 32);
     s_sum += sc;
-    if (lane == r) s_sel_mine = sc;
-    if (lane == 0) idx_out[(int64_t)t * k + r] = e;
+    if (lane == r) {
+      s_mine = sc;
+      e_mine = e;
+    }
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
       if (lane + 64 * j == e) key[j] = -1;
   }
+  S = renorm ? s_sum : s_all;
+  S = S < 1 ? 1 : S;
+}
+
+template <int EPL>
+LSK_DEV void route_token(const void* __restrict__ g, int gdt, int64_t ldg, int t, int E, int k, int renorm,
+                         const int32_t* __restrict__ tab, int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out) {
+  const int lane = threadIdx.x & 63;
+  int e_mine, s_mine, S;
+  route_select<EPL>(g, gdt, ldg, t, E, k, renorm, tab, e_mine, s_mine, S);
   if (lane < k) {
-    int S = renorm ? s_sum : s_all;
-    S = S < 1 ? 1 : S;
-    w_out[(int64_t)t * k + lane] = f32_to_bf16(f32_div((float)s_sel_mine, (float)S));
+    idx_out[(int64_t)t * k + lane] = e_mine;
+    w_out[(int64_t)t * k + lane] = f32_to_bf16(f32_div((float)s_mine, (float)S));
   }
 }
 
@@ -1058,6 +1073,178 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemmArgs a, uint16_t* 
   }
 }
 
+// The first launch of a one-token int8 layer routed from its logits: the router, the row quant of x
+// and the gate/up GEMV in one kernel.  Every wave routes the token itself (route_select: the same
+// arithmetic as router_topk_kernel) and quantises the whole row of x in registers (its lanes hold
+// the row's 16-element K chunks; the maximum is a wave reduction; rowquant's arithmetic), so no wave
+// waits on another; block (s, chunk) then takes the expert in slot s (the k experts ascending),
+// streams its RPW columns' gate and up weight rows and writes the bias-added gate and up values, as
+// moe_gemv_kernel's MODE 0 does for one row.  Block 0's first wave also writes the routing outputs
+// (idx_out / w_out in rank order) and the token's dispatch: offs, the tile table (slot s = the s-th
+// expert ascending, row s), row_tok / row_dst / row_w, tok_cnt and ascx, which the act + requant and
+// the down + combine launches read.  H = a.K, H % 16 == 0, H <= 1024 NC; k <= 8; E <= 64 EPL.
+template <int NC, int RPW, int EPL>
+__global__ __launch_bounds__(256) void moe_route_gemv1_kernel(MoeGemmArgs a, uint16_t* __restrict__ gu,
+                                                              const uint16_t* __restrict__ x, const void* __restrict__ g,
+                                                              int gdt, int E, int k, int renorm,
+                                                              const int32_t* __restrict__ rtab,
+                                                              int64_t* __restrict__ idx_out,
+                                                              uint16_t* __restrict__ w_out, int32_t* __restrict__ offs,
+                                                              int32_t* __restrict__ tiles, int32_t* __restrict__ row_tok,
+                                                              int32_t* __restrict__ row_dst, float* __restrict__ row_w,
+                                                              int32_t* __restrict__ tok_cnt, float* __restrict__ ascx) {
+  const int cols_blk = 4 * RPW;
+  const int nchunk = (a.N + cols_blk - 1) / cols_blk;
+  const int mt = blockIdx.x / nchunk, ch = blockIdx.x - mt * nchunk;
+  if (mt >= k) return;  // whole blocks; no barrier follows
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int H = a.K;
+  uint32_t koff[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int kk = j * 1024 + lane * 16;
+    koff[j] = kk < H ? (uint32_t)kk : lsk::kOob;
+  }
+  // the row of x (bf16): this lane's K chunks, requested before the routing
+  uint4 xr[NC][2];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    xr[j][0] = xr[j][1] = make_uint4(0, 0, 0, 0);
+    if (koff[j] != lsk::kOob) {
+      xr[j][0] = *(const uint4*)(x + koff[j]);
+      xr[j][1] = *(const uint4*)(x + koff[j] + 8);
+    }
+  }
+  // the routing: lane r < k holds the rank-r expert; pos = its slot among the k experts ascending
+  int e_r, s_r, S;
+  route_select<EPL>(g, gdt, E, 0, E, k, renorm, rtab, e_r, s_r, S);
+  int ek[8];  // the k experts in rank order, in every lane (gathered with the whole wave active)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ek[j] = __shfl(e_r, j < k ? j : 0, 64);
+  int pos = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pos += (j < k && ek[j] < e_r) ? 1 : 0;
+  const uint64_t sel = __builtin_amdgcn_ballot_w64(lane < k && pos == mt);
+  const int e = __shfl(e_r, (int)__builtin_ctzll(sel), 64);
+
+  // this wave's weight rows: gate c and up N + c of columns c0 .. c0 + RPW - 1
+  const int c0 = ch * cols_blk + wave * RPW;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)a.w_ptrs[e], a.w_bytes);
+  v4i w[RPW][2][NC];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int c = c0 + i;
+      const uint32_t ro = c < a.N ? (uint32_t)((r ? a.N + c : c) * a.ldw) : lsk::kOob;
+#pragma unroll
+      for (int j = 0; j < NC; ++j)
+        w[i][r][j] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, (ro == lsk::kOob || koff[j] == lsk::kOob) ? lsk::kOob
+                                                                                                   : ro + koff[j],
+                                                       0, 2 /* non-temporal */));
+    }
+  // the row quant of x (every wave holds the whole row)
+  float xv[NC][16];
+  float am = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const uint32_t wd[8] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w,
+                            xr[j][1].x, xr[j][1].y, xr[j][1].z, xr[j][1].w};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      xv[j][2 * q] = bf16_to_f32((uint16_t)(wd[q] & 0xffff));
+      xv[j][2 * q + 1] = bf16_to_f32((uint16_t)(wd[q] >> 16));
+      am = fmaxf(am, fmaxf(fabsf(xv[j][2 * q]), fabsf(xv[j][2 * q + 1])));
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  const float sc = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, sc);
+  v4i act[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    uint32_t pk[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < 16; ++q) pk[q >> 2] |= ((uint32_t)(uint8_t)quant_one(xv[j][q], sc, rs)) << (8 * (q & 3));
+    act[j] = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+  }
+
+  // block 0's first wave: the routing outputs and the one-token dispatch
+  if (blockIdx.x == 0 && wave == 0) {
+    if (lane < k) {
+      const uint16_t wb = f32_to_bf16(f32_div((float)s_r, (float)S));
+      idx_out[lane] = e_r;
+      w_out[lane] = wb;
+      tiles[1 + 2 * pos] = e_r;
+      tiles[2 + 2 * pos] = pos;
+      row_tok[pos] = 0;
+      row_dst[pos] = pos;
+      row_w[pos] = bf16_to_f32(wb);
+    }
+    for (int ee = lane; ee <= E; ee += 64) {
+      int before = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) before += (j < k && ek[j] < ee) ? 1 : 0;
+      offs[ee] = before;
+    }
+    if (lane == 0) {
+      tiles[0] = k;
+      tok_cnt[0] = k;
+      ascx[0] = sc;
+    }
+  }
+
+  // the gate / up dot products, reduced over the wave, and the epilogue of each column
+  constexpr int V = RPW * 2;
+  constexpr int kRep = 64 / V;
+  const int vi = lane / kRep;
+  const int vi_i = vi / 2, vi_r = vi % 2;
+  const int c = c0 + vi_i;
+  const bool owner = (lane % kRep) == 0 && vi_r == 0 && c < a.N;
+  const float* ws = (const float*)a.ws_ptrs[e];
+  const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  float ws0 = 0.0f, ws1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+  if (owner) {
+    ws0 = ws[c];
+    ws1 = ws[a.N + c];
+    if (bias) {
+      b0 = bias[c];
+      b1 = bias[a.N + c];
+    }
+  }
+  int v[V];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i)
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      int t = 0;
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        t = __builtin_amdgcn_sdot4(act[j][0], w[i][r][j][0], t, false);
+        t = __builtin_amdgcn_sdot4(act[j][1], w[i][r][j][1], t, false);
+        t = __builtin_amdgcn_sdot4(act[j][2], w[i][r][j][2], t, false);
+        t = __builtin_amdgcn_sdot4(act[j][3], w[i][r][j][3], t, false);
+      }
+      v[i * 2 + r] = t;
+    }
+  wave_xchg_sum<V, 32>(v, lane);
+  int tot = v[0];
+#pragma unroll
+  for (int o = kRep / 2; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+  const int upv = __shfl_xor(tot, kRep, 64);
+  if (owner) {
+    float yg = bfr(f32_mul(f32_mul((float)tot, ws0), sc));
+    float yu = bfr(f32_mul(f32_mul((float)upv, ws1), sc));
+    if (bias) {
+      yg = bfr(f32_add(yg, b0));
+      yu = bfr(f32_add(yu, b1));
+    }
+    uint16_t* row = gu + (int64_t)mt * 2 * a.N;
+    row[c] = f32_to_bf16(yg);
+    row[a.N + c] = f32_to_bf16(yu);
+  }
+}
+
 // The down projection and the combine of a one-token layer in one launch (the decode GEMV path at
 // T = 1).  The token's routed rows are its experts in ascending order, one row each (row s = slot
 // s, expert tiles[1 + 2 s]), so a wave owning RPW output columns computes every slot's value for
@@ -1707,6 +1894,12 @@ extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* 
   return lsk::launch_moe_mx_gemm(1, g, grouped_max_tiles(R, E), safe, s);
 }
 
+extern "C" int lsk_moe_fuse_route(int on) {
+  LSK_REQUIRE(on == 0 || on == 1, "lsk_moe_fuse_route: %d not 0 or 1", on);
+  g_rowq1 = on;
+  return LSK_OK;
+}
+
 extern "C" int lsk_moe_select(int variant) {
   LSK_REQUIRE(variant >= -1 && variant <= 5, "lsk_moe_select: variant %d not in [-1, 5]", variant);
   g_moe_force = variant >= 4 ? 1 : variant;
@@ -1845,6 +2038,10 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // save: Qwen3-30B-A3B on MI355X, T = 1 32.0 -> 31.4 us, T = 8 59.0 -> 63.4 us), else the
   // router kernel first
   const bool route_in_prep = a->logits && prep_decode && T <= 4 && E <= 256;
+  // one token routed from its logits on the int8 GEMV path: the router, the row quant of x and the
+  // gate/up GEMV in one launch (moe_route_gemv1_kernel; no prep launch)
+  const bool route_gemv1 = route_in_prep && T == 1 && use_gemv && !mx && k <= 8 && H % 16 == 0 && H <= 4096 &&
+                           I <= 2048 && ((uintptr_t)a->x & 15) == 0 && g_rowq1;
   if (a->logits && !route_in_prep) {
     const int rrc = lsk_router_topk(a->logits, a->logits_dtype, a->ld_logits, T, E, k, a->renormalize, a->router_tab,
                                     a->idx_out, a->w_out, stream);
@@ -1886,7 +2083,9 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   const int64_t nzero = mx == 2 ? R + 2 : R;
   int32_t* anyf = (int32_t*)(w.h_amax + R);
   const int64_t nchunks = (T + 255) / 256;
-  if (prep_decode) {
+  if (route_gemv1) {
+    // (the dispatch is written by the first launch below)
+  } else if (prep_decode) {
     const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
     hipLaunchKernelGGL(moe_decode_prep_kernel, dim3((unsigned)(T + 1)), dim3(256), dsm, s, ridx, rwt, (int)T, k,
                        (int)E, w.offs, w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.h_amax, nzero,
@@ -1949,6 +2148,21 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (route_gemv1) {
+    const int nchunk = (int)((I + 7) / 8);  // 4 waves x 2 columns per block
+    const dim3 grid((unsigned)(k * nchunk));
+#define LSK_RG1(NCV, EPLV)                                                                                     \
+  hipLaunchKernelGGL((moe_route_gemv1_kernel<NCV, 2, EPLV>), grid, dim3(256), 0, s, g1, w.gu, a->x, a->logits, \
+                     a->logits_dtype, (int)E, k, a->renormalize, a->router_tab, a->idx_out, a->w_out, w.offs,    \
+                     w.tiles, w.row_tok, w.row_dst, w.row_w, w.tok_cnt, w.ascx)
+    const int nc = (int)((H + 1023) / 1024);
+    if (E <= 128) {
+      if (nc <= 1) LSK_RG1(1, 2); else if (nc <= 2) LSK_RG1(2, 2); else LSK_RG1(4, 2);
+    } else {
+      if (nc <= 1) LSK_RG1(1, 4); else if (nc <= 2) LSK_RG1(2, 4); else LSK_RG1(4, 4);
+    }
+#undef LSK_RG1
+    if ((rc = lsk::check_launch("moe_route_gemv1_kernel"))) return rc;
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<0>(g1, w.max_tiles, T, w.gu, s, "moe_gemv_kernel<gate_up>"))) return rc;
   } else if (use_pp) {

@@ -4,6 +4,7 @@
 // lets the GEMM kernels reach at most; on constant operands it approaches the nominal peak.
 #include "lsk_common.h"
 #include "mfma_tile.h"
+#include "mx_tile.h"
 
 namespace {
 
@@ -62,7 +63,39 @@ __global__ __launch_bounds__(256) void bf16_cvt_check_kernel(uint64_t start, uin
   }
 }
 
+// One v_mfma_f32_16x16x32_bf16 per case with the caller's accumulator input: D = A B^T + C over
+// K = 32 (one MX block).  Case c: a [16][32] and b [16][32] bf16 (rows M / N, K contiguous), cin and
+// d [16][16] binary32 (row M, column N).  Lane l supplies row l % 16 of A and of B at K elements
+// 8 (l / 16) .. 8 (l / 16) + 7; register r of lane l holds D row 4 (l / 16) + r, column l % 16.
+// Four cases per 256-thread block; the grid covers ncases exactly.
+__global__ __launch_bounds__(256) void mfma_bf16_acc_kernel(const uint16_t* __restrict__ a,
+                                                            const uint16_t* __restrict__ b,
+                                                            const float* __restrict__ cin, float* __restrict__ d,
+                                                            int ncases) {
+  const int c = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (c >= ncases) return;
+  const int l = threadIdx.x & 63, row = l & 15, kg = l >> 4;
+  const v4i av = *(const v4i*)(a + (int64_t)c * 512 + row * 32 + 8 * kg);
+  const v4i bv = *(const v4i*)(b + (int64_t)c * 512 + row * 32 + 8 * kg);
+  v4f acc;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) acc[r] = cin[(int64_t)c * 256 + (4 * kg + r) * 16 + row];
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(lsk::v8bf, av), __builtin_bit_cast(lsk::v8bf, bv),
+                                                acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) d[(int64_t)c * 256 + (4 * kg + r) * 16 + row] = acc[r];
+}
+
 }  // namespace
+
+extern "C" int lsk_mfma_bf16_acc_probe(const uint16_t* a, const uint16_t* b, const float* cin, float* d, int ncases,
+                                       void* stream) {
+  LSK_REQUIRE(a && b && cin && d && ncases > 0 && ncases <= (1 << 24), "lsk_mfma_bf16_acc_probe: bad arguments");
+  LSK_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0, "lsk_mfma_bf16_acc_probe: a, b 16-byte aligned");
+  hipLaunchKernelGGL(mfma_bf16_acc_kernel, dim3((unsigned)((ncases + 3) / 4)), dim3(256), 0, (hipStream_t)stream, a, b,
+                     cin, d, ncases);
+  return lsk::check_launch("mfma_bf16_acc_kernel");
+}
 
 extern "C" int lsk_bf16_cvt_check(uint64_t start, uint64_t count, uint32_t* mismatches, uint32_t* first,
                                   void* stream) {

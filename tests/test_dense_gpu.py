@@ -517,3 +517,55 @@ def test_bf16_conversion_instruction_equals_rne_on_every_binary32():
         L.call("lsk_bf16_cvt_check", c << 30, 1 << 30, L.ptr(mism), L.ptr(first), s)
     torch.cuda.synchronize()
     assert int(mism.item()) == 0, "%d patterns differ, first 0x%08x" % (int(mism.item()), int(first.item()) & 0xffffffff)
+
+
+@pytest.mark.parametrize("xdt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("N,K", [(1, 16), (257, 1040), (3, 2048), (1000, 4096), (300, 5120), (4096, 14336),
+                                 (77, 16384)])
+def test_one_row_fused_rowquant_gemv(N, K, xdt):
+    """w8a8_matmul with one activation row runs the row quant inside the whole-row GEMV (one
+    launch, K <= 4096; two launches beyond): the oracle's bits for every order, bias and output
+    type, near-tie activations, and the same bits as the two-launch path
+    (lsk_gemm_fuse_rowquant(0))."""
+    import lockstep_amd._lib as L
+    from lockstep_amd import ops
+    say("fused one-row GEMV", N, K, xdt)
+    r = _rng(7 * N + K)
+    x = (r.standard_normal((1, K)) * 3).astype(F32)
+    x[0, : min(K, 6)] = [127.0, 2.5, -3.5, 0.5, 126.5, -40.0][: min(K, 6)]
+    if xdt == "bf16":
+        x = C.bf16_to_f32(C.bf16_bits(x))
+        xd = bf16_dev(x)
+    elif xdt == "f16":
+        x = x.astype(np.float16).astype(F32)
+        xd = to_dev(x.astype(np.float16))
+    else:
+        xd = to_dev(x)
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    bias = (r.standard_normal(N) * 0.1).astype(F32)
+    q, asc = C.rowquant(x)
+    acc = C.int_mm(q, W8.T)
+    Wd, wsd, bd = to_dev(W8), to_dev(ws), to_dev(bias)
+    for order, b in ((L.EPI_V21, None), (L.EPI_V21, bias), (L.EPI_V2, bias)):
+        for odt, name in ((L.LSK_BF16, "bf16"), (L.LSK_F32, "f32")):
+            y = ops.w8a8_matmul(xd, Wd, wsd, None if b is None else bd, order, odt)
+            f = C.epilogue_v21 if order == L.EPI_V21 else C.epilogue_v2
+            ref = f(acc, ws, asc, b, name)
+            want = ref if name == "bf16" else f32_bits(ref)
+            assert np.array_equal(bits(y), want), (order, b is not None, name)
+            L.call("lsk_gemm_fuse_rowquant", 0)
+            try:
+                y2 = ops.w8a8_matmul(xd, Wd, wsd, None if b is None else bd, order, odt)
+            finally:
+                L.call("lsk_gemm_fuse_rowquant", 1)
+            assert torch.equal(y.view(torch.int16) if name == "bf16" else y.view(torch.int32),
+                               y2.view(torch.int16) if name == "bf16" else y2.view(torch.int32))
+    # rows per wave 1, 2, 4, 8 (the whole-row GEMV's tuning control also sets the fused kernel's)
+    for tile in (8, 9, 10, 11):
+        L.call("lsk_gemm_select", tile)
+        try:
+            y = ops.w8a8_matmul(xd, Wd, wsd, bd, L.EPI_V21, L.LSK_BF16)
+        finally:
+            L.call("lsk_gemm_select", -1)
+        assert np.array_equal(bits(y), C.epilogue_v21(acc, ws, asc, bias, "bf16")), tile

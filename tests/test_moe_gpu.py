@@ -414,3 +414,40 @@ def test_moe_one_token_down_and_combine(k, I, extra):
     else:
         _run_case(1, E, k, H, I, seed=132 + k, bias=extra == "bias", act="swigluoai" if extra == "bias" else "silu",
                   shared=extra == "shared")
+
+
+@pytest.mark.parametrize("E,k,H,I,bias,act,renorm", [(16, 4, 256, 128, False, "silu", True),
+                                                     (128, 8, 2048, 768, False, "silu", True),
+                                                     (200, 6, 1040, 320, True, "swigluoai", False),
+                                                     (64, 1, 4096, 2048, True, "silu", True)])
+def test_moe_one_token_fused_route(E, k, H, I, bias, act, renorm):
+    """A one-token int8 layer routed from its logits runs the router, the row quant of x and the
+    gate/up GEMV in one launch: y, idx and w equal the oracle's and the three-launch path's
+    (lsk_moe_fuse_route(0)), logits as binary32 and bf16, with biases, SwiGLU-OAI, no
+    renormalisation, one expert and E above 128."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("one-token fused route", dict(E=E, k=k, H=H, I=I, bias=bias, act=act, renorm=renorm))
+    x, experts, logits = WL.moe_inputs(1, E, k, H, I, seed=E + k + H, bias=bias)
+    idx, w, _ = C.router_from_logits(logits, k, renorm)
+    oact = C.act_silu if act == "silu" else C.act_swigluoai
+    dact = MR.act_silu if act == "silu" else MR.act_swigluoai
+    if bias or act != "silu":
+        ref = C.moe_forward_b(x, oracle_experts(experts, True), idx, w, oact, rot_blk=0)
+    else:
+        ref = C.moe_forward(x, oracle_experts(experts), idx, w, act=oact)
+    dx, dexp = bf16_dev(x), device_experts(experts)
+    for g in (to_dev(logits), bf16_dev(logits)):
+        outs = []
+        for fuse in (1, 0):
+            L.call("lsk_moe_fuse_route", fuse)
+            try:
+                y, di, dw = MR.moe_forward(dx, None, dexp, k, renorm, _tab(), 0, dact, logits=g)
+            finally:
+                L.call("lsk_moe_fuse_route", 1)
+            assert np.array_equal(u16(y), ref), fuse
+            assert np.array_equal(di.cpu().numpy(), idx), fuse
+            assert np.array_equal(u16(dw), w), fuse
+            outs.append(u16(y))
+        assert np.array_equal(outs[0], outs[1])
