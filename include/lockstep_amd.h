@@ -243,6 +243,15 @@ int lsk_gemm_select(int tile_id);
  * lsk_gemm_select. */
 int lsk_gemm_fuse_rowquant(int on);
 
+/* Tuning control with no counterpart in the reference: 1 lets lsk_linear_dyn run its quant8_dyn in
+ * one pass when the activation fits on chip (a cooperative launch of four blocks per CU holding x
+ * in registers and LDS across one grid-wide barrier: M K <= 29,360,128 elements on a 256-CU part,
+ * ldx == K, K % 64 == 0, M even, the stream not being captured); 0 (the default: measured about 3x
+ * slower than the two passes on MI355X, the cooperative launch costing more than the second read
+ * of x saves) always uses the two passes (maxima, then quantise).  Results are identical.
+ * Thread-local. */
+int lsk_quant8_dyn_single_pass(int on);
+
 /* Tuning control with no counterpart in the reference: the persistent form of the 256x256
  * ping-pong kernel, taken for whole tiles under the POW2 epilogue with binary32 output (the
  * ref_block_v1 GEMMs): 1 one block per compute unit (the default), 0 off (one tile per block),

@@ -1,6 +1,11 @@
 // Activation quantisers: the contract's per-row int8 quant (true-division scale) and the
 // power-of-two quantisers of the golden training block.
+#include <hip/hip_cooperative_groups.h>
+
+#include <atomic>
+
 #include "lsk_common.h"
+#include "pp_tile.h"
 
 namespace lsk {
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
@@ -337,6 +342,29 @@ __global__ __launch_bounds__(256) void dyn_quant_pair_kernel(const float* __rest
                                                              int32_t* __restrict__ e_out,
                                                              int32_t* __restrict__ erow) {
   __shared__ float red[4];
+  const int64_t npair = (M + 1) >> 1;
+  const int per = (int)(ldq >> 2);  // 8-byte items per row pair
+  constexpr int U = 4;
+  // the loads of one step: every load issued before the first use, none under a branch (a lane
+  // without an element reads its pair's first row start and discards it)
+  auto load_step = [&](int64_t p, int r0, float4 (&v)[U][2], bool (&ok)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int o = (r0 + 256 * u) * 8;
+      const int64_t m = 2 * p + ((o >> 6) & 1);
+      const int64_t k = (int64_t)(o >> 7) * 64 + (o & 63);
+      ok[u] = r0 + 256 * u < per && m < M && k < K;
+      const float4* src = (const float4*)(x + (ok[u] ? m * ldx + k : 2 * p * ldx));
+      v[u][0] = ld_nt(src);
+      v[u][1] = ld_nt(src + 1);
+    }
+  };
+  // the block's first step requested before the partial maxima are reduced (it does not depend on
+  // the exponent), so the reduction's latency overlaps the first loads
+  float4 v0[U][2];
+  bool ok0[U];
+  const bool first = (int64_t)blockIdx.x < npair && (int)threadIdx.x < per;
+  if (first) load_step(blockIdx.x, threadIdx.x, v0, ok0);
   float am = 0.0f;
   for (int j = threadIdx.x; j < nparts; j += 256) am = fmaxf(am, partial[j]);
   am = block_max<256>(am, red);
@@ -345,25 +373,20 @@ __global__ __launch_bounds__(256) void dyn_quant_pair_kernel(const float* __rest
   if (blockIdx.x == 0 && threadIdx.x == 0) e_out[0] = e;
   if (erow)
     for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < M; r += (int64_t)gridDim.x * 256) erow[r] = e;
-  const int64_t npair = (M + 1) >> 1;
-  const int per = (int)(ldq >> 2);  // 8-byte items per row pair
-  constexpr int U = 4;
   for (int64_t p = blockIdx.x; p < npair; p += gridDim.x) {
     int8_t* qp = q + p * 2 * ldq;
     for (int r0 = threadIdx.x; r0 < per; r0 += 256 * U) {
       float4 v[U][2];
       bool ok[U];
-      // every load issued before the first use, none under a branch (a lane without an element
-      // reads its pair's first row start and discards it)
+      if (p == (int64_t)blockIdx.x && r0 == (int)threadIdx.x) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int o = (r0 + 256 * u) * 8;
-        const int64_t m = 2 * p + ((o >> 6) & 1);
-        const int64_t k = (int64_t)(o >> 7) * 64 + (o & 63);
-        ok[u] = r0 + 256 * u < per && m < M && k < K;
-        const float4* src = (const float4*)(x + (ok[u] ? m * ldx + k : 2 * p * ldx));
-        v[u][0] = ld_nt(src);
-        v[u][1] = ld_nt(src + 1);
+        for (int u = 0; u < U; ++u) {
+          v[u][0] = v0[u][0];
+          v[u][1] = v0[u][1];
+          ok[u] = ok0[u];
+        }
+      } else {
+        load_step(p, r0, v, ok);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -373,6 +396,91 @@ __global__ __launch_bounds__(256) void dyn_quant_pair_kernel(const float* __rest
         *(v2u32*)(qp + (int64_t)(r0 + 256 * u) * 8) = out;
       }
     }
+  }
+}
+
+// Single-pass quant8_dyn into the row-pair layout for a tensor that fits on chip (a cooperative
+// launch: every block resident, one grid-wide barrier).  Block b holds the contiguous run of
+// 256 * (kQ1Regs + kQ1Lds) float4s from b * 256 * (kQ1Regs + kQ1Lds): step j of thread t is float4
+// run + 256 j + t, kQ1Regs steps in registers and kQ1Lds in LDS (direct-to-LDS loads), so x is read
+// from memory once, each block from one contiguous run.  Each block writes its |x| maximum to
+// partial[block]; after the barrier every block reduces the G partials, derives the tensor exponent
+// (pow2_exponent) and quantises its float4s from registers and LDS into q (element (m, k) at
+// (m >> 1) 2 ldq + (k >> 6) 128 + (m & 1) 64 + (k & 63)).  Needs ldx == K, K % 64 == 0 (no padding
+// bytes), M even, M K < 2^31 and M K <= G * 256 * (kQ1Regs + kQ1Lds) * 4.  Same exponent and q as
+// the two-pass kernels: the maximum is exact in any order.
+constexpr int kQ1Regs = 19, kQ1Lds = 9;
+
+__global__ __launch_bounds__(256, 4) void dyn_quant1_pair_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                                float* __restrict__ partial, int8_t* __restrict__ q,
+                                                                int64_t ldq, int32_t* __restrict__ e_out,
+                                                                int32_t* __restrict__ erow) {
+  constexpr int NT = kQ1Regs + kQ1Lds;
+  __shared__ __attribute__((aligned(16))) char xs[kQ1Lds * 4096];  // [step][wave][lane] 16 bytes each
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n4 = (int)((M * K) >> 2);
+  const int i0 = (int)blockIdx.x * 256 * NT + tid;  // float4 of step 0
+  const float4* x4 = (const float4*)x;
+  const __amdgpu_buffer_rsrc_t rx = lsk::make_rsrc(x, (int64_t)n4 * 16);
+  float4 r[kQ1Regs];
+#pragma unroll
+  for (int j = 0; j < kQ1Regs; ++j) {
+    const int i = i0 + 256 * j;
+    r[j] = i < n4 ? ld_nt(x4 + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+#pragma unroll
+  for (int j = 0; j < kQ1Lds; ++j) {
+    const int i = i0 + 256 * (kQ1Regs + j);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lsk::lds_void_t)(xs + (j * 4 + wave) * 1024), 16,
+                                             i < n4 ? (uint32_t)i * 16u : lsk::kOob, 0, 0, 0);
+  }
+  float am = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kQ1Regs; ++j)
+    am = fmaxf(am, fmaxf(fmaxf(fabsf(r[j].x), fabsf(r[j].y)), fmaxf(fabsf(r[j].z), fabsf(r[j].w))));
+  lsk::wait_vm<0>();
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kQ1Lds; ++j) {
+    const float4 v = *(const float4*)(xs + (j * 4 + wave) * 1024 + lane * 16);
+    am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+  am = block_max<256>(am, red);
+  if (tid == 0) partial[blockIdx.x] = am;
+  cooperative_groups::this_grid().sync();
+  float m = 0.0f;
+  for (int j = tid; j < (int)gridDim.x; j += 256) m = fmaxf(m, partial[j]);
+  m = block_max<256>(m, red);
+  const int e = pow2_exponent(m);
+  const float sc = pow2f(e);
+  if (blockIdx.x == 0 && tid == 0) e_out[0] = e;
+  if (erow)
+    for (int64_t rr = (int64_t)blockIdx.x * 256 + tid; rr < M; rr += (int64_t)gridDim.x * 256) erow[rr] = e;
+  // element 4 i of x is (row mr, column kc); each step adds 1024 elements (dm rows + dk columns)
+  const int Ki = (int)K;
+  int mr = (4 * i0) / Ki, kc = (4 * i0) - mr * Ki;
+  const int dm = 1024 / Ki, dk = 1024 - dm * Ki;
+  auto put = [&](float4 v) {
+    *(uint32_t*)(q + (int64_t)(mr >> 1) * 2 * ldq + (kc >> 6) * 128 + (mr & 1) * 64 + (kc & 63)) = quant_pow2_x4(v, sc);
+  };
+  auto advance = [&]() {
+    mr += dm;
+    kc += dk;
+    if (kc >= Ki) {
+      kc -= Ki;
+      ++mr;
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kQ1Regs; ++j) {
+    if (i0 + 256 * j < n4) put(r[j]);
+    advance();
+  }
+#pragma unroll
+  for (int j = 0; j < kQ1Lds; ++j) {
+    if (i0 + 256 * (kQ1Regs + j) < n4) put(*(const float4*)(xs + (j * 4 + wave) * 1024 + lane * 16));
+    advance();
   }
 }
 
@@ -412,10 +520,52 @@ int launch_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t*
   return lsk::check_launch("dyn_quant_kernel");
 }
 
+// quant8_dyn in one pass where the tensor fits on chip: off by default.  Measured on MI355X
+// (ROCm 7.2, Qwen2.5-7B block at 8192 rows, alternating on one box): 171-178 us per 117 MB
+// activation against 60-65 us for the two passes (maxima 20 us, quantise 33 us); the cooperative
+// launch and its grid barrier cost more than the second read of x saves.
+thread_local int g_quant1 = 0;
+
+// Blocks of the single-pass kernel that the device keeps resident at once (four per CU when its
+// registers and LDS allow), cached per device; 0 when the device cannot launch it cooperatively.
+static int quant1_blocks() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int coop = 0, cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, dyn_quant1_pair_kernel, 256, 0) != hipSuccess)
+      n = -1;
+    else
+      n = per >= 4 ? 4 * cus : -1;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n > 0 ? (n > kDynBlocks ? kDynBlocks : n) : 0;
+}
+
 // quant8_dyn into the row-pair layout (ldq % 64 == 0, K % 8 == 0, x rows 16-byte aligned).
 int launch_quant8_dyn_pair(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq, int32_t* e_out,
                            int32_t* erow, float* partial, hipStream_t s) {
   const int64_t total = M * K;
+  // one pass when the tensor fits on chip and the stream is not being captured (a cooperative
+  // launch is not captured into graphs)
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  int G = 0;
+  if (g_quant1 && ldx == K && K % 64 == 0 && M % 2 == 0 && ldq == K && total < (int64_t)1 << 31 &&
+      ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 4) == 0 && hipStreamIsCapturing(s, &cap) == hipSuccess &&
+      cap == hipStreamCaptureStatusNone && (G = quant1_blocks()) > 0 &&
+      total <= (int64_t)G * 256 * (kQ1Regs + kQ1Lds) * 4) {
+    void* args[] = {(void*)&x, (void*)&M, (void*)&K, (void*)&partial, (void*)&q, (void*)&ldq, (void*)&e_out,
+                    (void*)&erow};
+    if (hipLaunchCooperativeKernel((const void*)dyn_quant1_pair_kernel, dim3((unsigned)G), dim3(256), args, 0, s) !=
+        hipSuccess)
+      return lsk::set_error("quant8_dyn: cooperative launch failed: %s", hipGetErrorString(hipGetLastError())),
+             LSK_ERR_HIP;
+    return LSK_OK;
+  }
   const int flat = (ldx == K && ((uintptr_t)x % 16) == 0) ? 1 : 0;
   int64_t blocks = flat ? (total + 256 * 16 - 1) / (256 * 16) : M;
   blocks = blocks < 1 ? 1 : (blocks > kDynBlocks ? kDynBlocks : blocks);
@@ -505,6 +655,12 @@ extern "C" int lsk_gemm_reads_row_pairs(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 != 0) return 0;
   const int64_t kp = (K + 63) / 64 * 64;
   return lsk::gemm_takes_pp((const int8_t*)(uintptr_t)256, kp, M, N, K, kp) ? 1 : 0;
+}
+
+extern "C" int lsk_quant8_dyn_single_pass(int on) {
+  LSK_REQUIRE(on == 0 || on == 1, "lsk_quant8_dyn_single_pass: %d not 0 or 1", on);
+  g_quant1 = on;
+  return LSK_OK;
 }
 
 extern "C" int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, const int8_t* w, int64_t ldw,

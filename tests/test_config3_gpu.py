@@ -267,3 +267,38 @@ def test_linear_dyn_partial_tiles_and_graph_capture():
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int32), eager.view(torch.int32))
         x.mul_(1.0)            # eager work between replays
+
+
+@pytest.mark.parametrize("T,N,K,scale", [(256, 512, 64, 1.0), (2048, 512, 3584, 1.0), (8192, 256, 3584, 1.0),
+                                         (302, 520, 3584, 3e4), (1000, 264, 192, 1e-30), (64, 320, 3584, 0.0)])
+def test_linear_dyn_single_pass_quant(T, N, K, scale):
+    """linear_dyn with the one-pass quant8_dyn (lsk_quant8_dyn_single_pass(1): a cooperative launch
+    holding x on chip; taken here for every shape, the largest at the on-chip capacity of a 256-CU
+    part) against the oracle on a
+    row sample and, bit for bit over every row, against the two-pass quantiser: tensors scaled so
+    the exponent clips at -32 and at 40 (subnormal x), an all-zero tensor (e = 0), and an element
+    whose scaled value is exactly 127."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import ref_block_v1 as RB
+    say("linear_dyn one-pass quant: T=%d N=%d K=%d scale=%g" % (T, N, K, scale))
+    g = np.random.default_rng(T + N + K)
+    x = (g.standard_normal((T, K)) * scale).astype(F32)
+    if scale == 1.0:
+        x[3, 5] = F32(127.0 / 32.0)          # exactly 127 after scaling by 2^5 (max |x| < 4)
+        x[np.abs(x) > 127.0 / 32.0] = F32(3.0)
+    W8 = g.integers(-127, 128, (N, K), dtype=np.int8)
+    xd, Wd = torch.from_numpy(x).to(dev()), torch.from_numpy(W8).to(dev())
+    L.call("lsk_quant8_dyn_single_pass", 1)
+    try:
+        y1, e1 = RB.linear_dyn(xd, Wd.t(), 5)
+    finally:
+        L.call("lsk_quant8_dyn_single_pass", 0)
+    y2, e2 = RB.linear_dyn(xd, Wd.t(), 5)
+    assert int(e1[0].item()) == int(e2[0].item())
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    rows = np.sort(np.random.default_rng(T).choice(T, min(T, 64), replace=False))
+    q_ref, e_ref = C.quant8_dyn(x)
+    assert int(e1[0].item()) == e_ref
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.dequant_pow2(C.gemm_int(q_ref[rows], W8.T.astype(np.int64)), e_ref + 5)
+    assert np.array_equal(bits(y1)[rows], f32_bits(ref))
