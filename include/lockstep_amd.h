@@ -482,7 +482,7 @@ typedef struct {
   uint16_t* w_out;               /* [T, k] bf16 */
   /* Kernel choice for this call only (no reference counterpart; results are the same bits either
    * way): 0 keeps the calling thread's lsk_moe_select / lsk_moe_mx_select settings; select = v + 2
-   * applies lsk_moe_select(v) (v in [-1, 5]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
+   * applies lsk_moe_select(v) (v in [-1, 6]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
    * (v in [0, 2]) to this call, leaving the thread's settings as they were. */
   int select;
   int mx_select;
@@ -568,9 +568,10 @@ int lsk_moe_fuse_route(int on);
  * block-scaled activations), the MX grouped tiles otherwise.  Results are identical for every
  * choice.  4: the ping-pong tile with 128-byte K stages (one block per CU).  5: the 256x256 ping-pong
  * tile (the dense kernel's tile: eight waves of 64x128, a four-stage ring, one block per CU, its own
- * 256-row tile table; slower than the two-blocks-per-CU 128x256 tile, so never chosen by size).  The
- * choice applies to the calling
- * host thread's later launches only (thread-local). */
+ * 256-row tile table) in a persistent kernel, one block per CU walking the tiles, the next tile's
+ * first stages loaded under the current tile's epilogue (K >= 384; 6 below otherwise).  6: the same
+ * tile, one block per tile.  The choice applies to the calling host thread's later launches only
+ * (thread-local). */
 int lsk_moe_select(int variant);
 
 /* Tuning control with no counterpart in the reference: the main loop of the grouped MXFP4

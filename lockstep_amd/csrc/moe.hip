@@ -909,6 +909,263 @@ __global__ __launch_bounds__(512, 1) void moe_pp256_kernel(MoeGemmArgs a) {
                          });
 }
 
+// Persistent form of the 256 x 256 expert tiles (lsk_moe_select(5)): one block per CU walks the
+// (256-row tile, N-tile) pairs v = blockIdx.x, blockIdx.x + gridDim.x, ... in moe_tile's logical order
+// (xcd_logical_id over the pair count, read from the tile table).  After a tile's main loop the block
+// parks the tile's epilogue operands in LDS past the ring, fills the whole ring with the next tile's
+// first stages, and only then applies the epilogue straight from the accumulators (no LDS staging:
+// the ring is being refilled), so the next tile's first loads run under the epilogue.  Register r of
+// lane l of a 32 x 32 block is row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32, so lanes l and
+// l ^ 1 hold neighbouring columns of the same rows: one exchange per register pair gives each lane
+// two neighbouring bf16 values of one row, stored with one 4-byte store.  MODE 0: the gate and up
+// values of an h-column sit in blocks 2t and 2t + 1 of the wave (the 32-interleave), so the
+// activation is thread-local; each row's |h| maximum is reduced over its 32 lanes by shuffles and
+// raised with one integer atomic per row and wave.  The arithmetic is moe_tile's.
+constexpr int kP256pSmem = PPM256::kMainBytes + (3 * 256 + 2 * 256) * 4;
+static_assert(kP256pSmem <= 160 * 1024, "one block per CU");
+
+// Issue this thread's direct-to-LDS loads of the first kRing stages of a 256 x 256 expert tile into
+// ring slots 0 .. kRing - 1 (pa / pb: the tile's load-slot row offsets; chunks past K read zeros).
+__device__ __forceinline__ void moe256_issue_ring(__amdgpu_buffer_rsrc_t ra, const uint32_t* pa,
+                                                  __amdgpu_buffer_rsrc_t rb, const uint32_t* pb, int K, char* smem,
+                                                  int pairs) {
+  using C = PPM256;
+  const int tid = threadIdx.x, wave = wave_id();
+  const int nk = (K + C::kBK - 1) / C::kBK;
+#pragma unroll
+  for (int st = 0; st < C::kRing; ++st) {
+    if (st >= nk) break;
+    char* base = smem + st * C::kStage;
+#pragma unroll
+    for (int j = 0; j < C::kLA; ++j) {
+      int row, kbyte;
+      lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kbyte);
+      const int kk = st * C::kBK + kbyte;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(base + (j * C::kThreads + wave * 64) * 16), 16,
+                                               kk < K ? pa[j] + lsk::pair_koff(kk, pairs & 1) : lsk::kOob, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < C::kLB; ++j) {
+      int row, kbyte;
+      lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kbyte);
+      const int kk = st * C::kBK + kbyte;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rb, (lsk::lds_void_t)(base + C::kStageA + (j * C::kThreads + wave * 64) * 16), 16,
+          kk < K ? pb[j] + lsk::pair_koff(kk, pairs & 2) : lsk::kOob, 0, 0, 0);
+    }
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void moe_pp256p_kernel(MoeGemmArgs a) {
+  using C = PPM256;
+  extern __shared__ __attribute__((aligned(16))) char smem_moe[];
+  const int ntiles = MODE == 0 ? (a.N + 127) / 128 : (a.N + 255) / 256;
+  const int total = a.tiles[0] * ntiles;
+  if ((int)blockIdx.x >= total) return;  // the whole block leaves: no barrier is left waiting
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm = wave / C::kWN, wn = wave % C::kWN;
+  float* sc_asc = (float*)(smem_moe + C::kMainBytes);
+  float* sc_w = sc_asc + 256;
+  int* sc_dst = (int*)(sc_w + 256);
+  float* sc_ws = (float*)(sc_dst + 256);
+  float* sc_b = sc_ws + 256;
+  const int apairs = (MODE == 1 ? (a.pairs & 1) : 0) | (a.pairs & 2);
+  __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+
+  struct Tile {
+    int p0, p1, nt;
+    const int8_t* wb;
+    typename C::RowsA pa;
+    typename C::RowsB pb;
+    float r_asc, r_w, c_ws, c_b;
+    int r_dst;
+  };
+  auto setup = [&](int v, Tile& t) {
+    const int L = lsk::xcd_logical_id(v, total);
+    const int mt = L / ntiles;
+    t.nt = L - mt * ntiles;
+    const int e = a.tiles[1 + 2 * mt];
+    t.p0 = a.tiles[2 + 2 * mt];
+    t.p1 = min(a.offs[e + 1], t.p0 + 256);
+    t.wb = (const int8_t*)a.w_ptrs[e];
+    const float* ws = (const float*)a.ws_ptrs[e];
+    const float* bias = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+    // weight row of local column c (gate/up interleave) and its h- or output column
+    auto wrow_of = [&](int c, int& hc) {
+      if (MODE == 0) {
+        const int blk = c >> 5;
+        hc = t.nt * 128 + (blk >> 1) * 32 + (c & 31);
+        return (blk & 1) ? a.N + hc : hc;
+      }
+      hc = t.nt * 256 + c;
+      return hc;
+    };
+    t.r_asc = t.r_w = t.c_ws = t.c_b = 0.0f;
+    t.r_dst = 0;
+    if (tid < 256) {
+      const int p = t.p0 + tid;
+      if (p < t.p1) {
+        if (MODE == 0) {
+          t.r_asc = a.a_scale[a.row_tok[p]];
+        } else {
+          t.r_asc = a.a_scale[p];
+          t.r_w = a.row_w ? a.row_w[p] : 1.0f;
+          t.r_dst = a.row_dst ? a.row_dst[p] : p;
+        }
+      }
+      int hc;
+      const int wr = wrow_of(tid, hc);
+      if (hc < a.N) {
+        t.c_ws = ws[wr];
+        if (bias) t.c_b = bias[wr];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < C::kLA; ++j) {
+      int row, kb;
+      lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
+      const int p = t.p0 + row;
+      const int src = p < t.p1 ? (MODE == 0 ? a.row_tok[p] : p) : -1;
+      const uint32_t ro = (MODE == 1 && (a.pairs & 1)) ? (uint32_t)((src >> 1) * 2 * a.lda + (src & 1) * 64)
+                                                        : (uint32_t)(src * a.lda);
+      t.pa[j] = src >= 0 ? ro : lsk::kOob;
+    }
+#pragma unroll
+    for (int j = 0; j < C::kLB; ++j) {
+      int row, kb, hc;
+      lsk::pp_slot<C::kThreads, C::kChunks>(tid, j, row, kb);
+      const int wr = wrow_of(row, hc);
+      const uint32_t ro = (a.pairs & 2) ? (uint32_t)((wr >> 1) * 2 * a.ldw + (wr & 1) * 64) : (uint32_t)(wr * a.ldw);
+      t.pb[j] = hc < a.N ? ro : lsk::kOob;
+    }
+  };
+
+  // ring slots 0 .. kRing - 1 take the first tile's first stages; later tiles' are issued under the
+  // previous tile's epilogue (no wave reads the ring any more by then)
+  Tile cur;
+  setup(blockIdx.x, cur);
+  moe256_issue_ring(ra, cur.pa, lsk::make_rsrc(cur.wb, a.w_bytes), cur.pb, a.K, smem_moe, apairs);
+  for (int v = blockIdx.x; v < total; v += gridDim.x) {
+    typename C::Acc acc;
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) acc[i][j] = lsk::zero16();
+    const int na = max(0, min(C::TM, (cur.p1 - cur.p0 - wm * C::WTM + 31) / 32));
+    lsk::pp_mainloop<256, 256, 4, 2, 4, 64, true, true, true>(acc, ra, cur.pa, lsk::make_rsrc(cur.wb, a.w_bytes),
+                                                              cur.pb, a.K, smem_moe, na, apairs);
+    // every wave is past its last ring read; the previous tile's epilogue (the last reader of the
+    // parked operands) ended before this tile's first barrier
+    if (tid < 256) {
+      sc_asc[tid] = cur.r_asc;
+      sc_w[tid] = cur.r_w;
+      sc_dst[tid] = cur.r_dst;
+      sc_ws[tid] = cur.c_ws;
+      sc_b[tid] = cur.c_b;
+    }
+    const int p0 = cur.p0, p1 = cur.p1, nt = cur.nt;
+    if (v + (int)gridDim.x < total) {
+      setup(v + gridDim.x, cur);
+      moe256_issue_ring(ra, cur.pa, lsk::make_rsrc(cur.wb, a.w_bytes), cur.pb, a.K, smem_moe, apairs);
+    }
+    __syncthreads();
+
+    // the lane's epilogue indices, derived afresh per tile (not kept live through the main loop)
+    int tid_e = tid;
+    asm volatile("" : "+v"(tid_e));
+    const int lane_e = tid_e & 63, half = lane_e >> 5, col = lane_e & 31, odd = lane_e & 1;
+    const bool bias = a.b_ptrs != nullptr;
+    // rows outermost (register pairs r, r + 1), columns innermost: a row's parked operands are read
+    // once and only two rows' worth are live next to the accumulators
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      if (i >= na) break;
+      const int rbase = wm * C::WTM + i * 32 + 4 * half;  // tile row of register 0
+      if (MODE == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const int ml0 = rbase + 8 * (r >> 2) + (r & 3);  // rows of registers r and r + 1
+          const int ml = ml0 + odd;                         // the row this lane stores
+          const float asc0 = sc_asc[ml0], asc1 = sc_asc[ml0 + 1];
+          const float w0 = sc_w[ml0], w1 = sc_w[ml0 + 1];
+          const bool live = p0 + ml < p1;
+          uint16_t* yrow = a.y + (int64_t)sc_dst[ml] * a.N;
+#pragma unroll
+          for (int j = 0; j < C::TN; ++j) {
+            const int cl = wn * C::WTN + j * 32 + col;
+            const int n2 = (nt * 256 + cl) & ~1;  // the even column of this lane's pair
+            const float ws = sc_ws[cl], b = sc_b[cl];
+            float y0 = bfr(f32_mul(f32_mul((float)acc[i][j][r], ws), asc0));
+            float y1 = bfr(f32_mul(f32_mul((float)acc[i][j][r + 1], ws), asc1));
+            if (bias) {
+              y0 = bfr(f32_add(y0, b));
+              y1 = bfr(f32_add(y1, b));
+            }
+            const float o0 = f32_mul(w0, y0), o1 = f32_mul(w1, y1);
+            // even lanes keep register r's row, odd lanes register r + 1's
+            const float got = __shfl_xor(odd ? o0 : o1, 1, 64);
+            const float lo = odd ? got : o0, hi = odd ? o1 : got;
+            if (live && n2 < a.N) {
+              uint16_t* dst = yrow + n2;
+              if (n2 + 1 < a.N) *(uint32_t*)dst = pack_bf16x2(lo, hi);
+              else dst[0] = f32_to_bf16(lo);
+            }
+          }
+        }
+      } else {
+        float am[16];
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const int ml0 = rbase + 8 * (r >> 2) + (r & 3);
+          const int ml = ml0 + odd;
+          const float asc0 = sc_asc[ml0], asc1 = sc_asc[ml0 + 1];
+          const bool live = p0 + ml < p1;
+          uint16_t* hrow = a.h + (int64_t)(p0 + ml) * a.N;
+          am[r] = am[r + 1] = 0.0f;
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int cg = wn * C::WTN + 2 * t * 32 + col;  // gate column in the tile; up at + 32
+            const int hc = nt * 128 + wn * 64 + t * 32 + col;
+            const int h2 = hc & ~1;
+            const float wsg = sc_ws[cg], wsu = sc_ws[cg + 32];
+            float hv[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float asc = h ? asc1 : asc0;
+              float yg = bfr(f32_mul(f32_mul((float)acc[i][2 * t][r + h], wsg), asc));
+              float yu = bfr(f32_mul(f32_mul((float)acc[i][2 * t + 1][r + h], wsu), asc));
+              if (bias) {
+                yg = bfr(f32_add(yg, sc_b[cg]));
+                yu = bfr(f32_add(yu, sc_b[cg + 32]));
+              }
+              hv[h] = a.act_tab ? lsk::act_from_entry(a.act, a.act_tab[__float_as_uint(yg) >> 16], yu)
+                                : lsk::act_eval(a.act, yg, yu, a.frac, nullptr);
+              if (hc < a.N) am[r + h] = fmaxf(am[r + h], fabsf(hv[h]));
+            }
+            const float got = __shfl_xor(odd ? hv[0] : hv[1], 1, 64);
+            const float lo = odd ? got : hv[0], hi = odd ? hv[1] : got;
+            if (live && h2 < a.N) {
+              uint16_t* dst = hrow + h2;
+              if (h2 + 1 < a.N) *(uint32_t*)dst = pack_bf16x2(lo, hi);
+              else dst[0] = f32_to_bf16(lo);
+            }
+          }
+        }
+        // each row's maximum over the 32 lanes holding it (this wave's 64 h-columns of the row; the
+        // maximum is order-free)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+#pragma unroll
+          for (int o = 1; o < 32; o <<= 1) am[r] = fmaxf(am[r], __shfl_xor(am[r], o, 64));
+          const int ml = rbase + 8 * (r >> 2) + (r & 3);
+          if (col == 0 && p0 + ml < p1) atomicMax(&a.h_amax[p0 + ml], __float_as_uint(am[r]));
+        }
+      }
+    }
+  }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(512, 1) void moe_pp128_kernel(MoeGemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem_moe[];
@@ -1562,7 +1819,7 @@ constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
 // layer at 256 / 2048 / 4096 tokens 222 / 358 / 520 us against 169 / 299 / 425 us, the grouped
 // gate/up and down stages at 16384 rows 179 / 137 us against 143 / 101 us, despite a third fewer
 // operand bytes per MFMA.
-static bool moe_uses_pp256(int64_t, int64_t) { return g_moe_w4 == 3; }
+static bool moe_uses_pp256(int64_t, int64_t) { return g_moe_w4 == 3 || g_moe_w4 == 4; }
 
 constexpr int64_t kMxGemvMaxT = 24;   // ... with MXFP4 experts
 constexpr int64_t kMx2GemvMaxT = 16;  // ... with MXFP4 experts and block-scaled activations
@@ -1652,13 +1909,41 @@ int launch_moe_pp(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const
   return lsk::check_launch(name);
 }
 
-// The 256 x 256 expert tiles: ga.tiles is the kBM2-row tile table, max_tiles its bound.
+// Compute units of the current device (the persistent grid), cached per device.
+static int moe_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The 256 x 256 expert tiles: ga.tiles is the kBM2-row tile table, max_tiles its bound.  g_moe_w4
+// == 3: the persistent kernel (one block per CU); 4: one tile per block.
 template <int MODE>
 int launch_moe_pp256(const MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s, const char* name) {
   const int ntiles = MODE == 0 ? (ga.N + 127) / 128 : (ga.N + 255) / 256;
   const int64_t blocks = max_tiles * ntiles;
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  if (g_moe_w4 == 3 && ga.K >= (PPM256::kRing + 2) * PPM256::kBK) {  // the persistent loop's first steps
+    static std::atomic<bool> attr_p{false};
+    if (!attr_p) {
+      if (hipFuncSetAttribute((const void*)moe_pp256p_kernel<MODE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kP256pSmem) != hipSuccess) {
+        lsk::set_error("%s: cannot reserve %d bytes of LDS", name, kP256pSmem);
+        return LSK_ERR_HIP;
+      }
+      attr_p = true;
+    }
+    const int64_t grid = blocks < moe_cu_count() ? blocks : moe_cu_count();
+    hipLaunchKernelGGL(moe_pp256p_kernel<MODE>, dim3((unsigned)grid), dim3(512), kP256pSmem, s, ga);
+    return lsk::check_launch(name);
+  }
   constexpr int kSmem = moe_smem_bytes<PPM256>();
   static std::atomic<bool> attr_set{false};
   if (!attr_set) {
@@ -1851,7 +2136,7 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
   g.y = out;  // row_w / row_dst null: weight 1, row p of the output
   const int64_t mt = grouped_max_tiles(R, E);
   if (pp) {
-    if (w_pair_ptrs && (g_moe_w4 == 0 || g_moe_w4 == 3)) {  // the weights' row-pair copies on the ping-pong tiles
+    if (w_pair_ptrs && (g_moe_w4 == 0 || g_moe_w4 == 3 || g_moe_w4 == 4)) {  // the row-pair copies, ping-pong tiles
       g.w_ptrs = w_pair_ptrs;
       g.ldw = (K + 63) / 64 * 64;
       g.w_bytes = ((N + 1) & ~(int64_t)1) * g.ldw;
@@ -1901,9 +2186,9 @@ extern "C" int lsk_moe_fuse_route(int on) {
 }
 
 extern "C" int lsk_moe_select(int variant) {
-  LSK_REQUIRE(variant >= -1 && variant <= 5, "lsk_moe_select: variant %d not in [-1, 5]", variant);
+  LSK_REQUIRE(variant >= -1 && variant <= 6, "lsk_moe_select: variant %d not in [-1, 6]", variant);
   g_moe_force = variant >= 4 ? 1 : variant;
-  g_moe_w4 = variant == 3 ? 1 : (variant == 4 ? 2 : (variant == 5 ? 3 : 0));
+  g_moe_w4 = variant == 3 ? 1 : (variant == 4 ? 2 : (variant == 5 ? 3 : (variant == 6 ? 4 : 0)));
   return LSK_OK;
 }
 
@@ -1921,11 +2206,11 @@ static bool moe_reads_pair_weights(int64_t T, int k, int64_t E, int64_t H, int64
   const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= 16 * E;
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
   const bool use_gemv = gemv_ok && H <= 4096 && I <= 4096;
-  return use_pp && !use_gemv && (g_moe_w4 == 0 || g_moe_w4 == 3);
+  return use_pp && !use_gemv && (g_moe_w4 == 0 || g_moe_w4 == 3 || g_moe_w4 == 4);
 }
 
 extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int select) {
-  if (T <= 0 || k < 1 || E < 1 || H <= 0 || I <= 0 || select < 0 || select > 7) return 0;
+  if (T <= 0 || k < 1 || E < 1 || H <= 0 || I <= 0 || select < 0 || select > 8) return 0;
   const int force = g_moe_force, w4 = g_moe_w4;
   if (select) lsk_moe_select(select - 2);
   const bool r = moe_reads_pair_weights(T, k, E, H, I, rot_blk);
@@ -1936,8 +2221,8 @@ extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, i
 
 extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(a, "lsk_moe_forward: null args");
-  LSK_REQUIRE(a->select >= 0 && a->select <= 7 && a->mx_select >= 0 && a->mx_select <= 3,
-              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 7] / [0, 3]", a->select, a->mx_select);
+  LSK_REQUIRE(a->select >= 0 && a->select <= 8 && a->mx_select >= 0 && a->mx_select <= 3,
+              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 8] / [0, 3]", a->select, a->mx_select);
   if (a->select == 0 && a->mx_select == 0) return moe_forward_call(a, stream);
   // this call's kernel choice, the thread's own restored afterwards
   const int force = g_moe_force, w4 = g_moe_w4, mxv = lsk::mx_variant();
@@ -2025,7 +2310,8 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
   // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
   // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
-  const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && I % 64 == 0 && (g_moe_w4 == 0 || g_moe_w4 == 3);
+  const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && I % 64 == 0 &&
+                         (g_moe_w4 == 0 || g_moe_w4 == 3 || g_moe_w4 == 4);
   // the 256 x 256 expert tiles (their own tile table) for the ping-pong GEMMs
   const bool pp256 = use_pp && !mx && !use_gemv && moe_uses_pp256(R, E);
   // the experts' row-pair weight copies on the same tiles, when the caller has them

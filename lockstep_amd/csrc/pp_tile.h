@@ -146,13 +146,21 @@ LSK_DEV void pp_issue_prologue(__amdgpu_buffer_rsrc_t ra, const typename PPCfg<B
 // SKIP (two 32-row strips per wave): only the wave's first na strips hold rows of the tile
 // (na in 0 .. 2, wave-uniform), so the fragment reads and MFMAs of the others are left out; their
 // accumulators stay zero.  The loads and barriers are the same for every wave.
-template <int BM, int BN, int WM, int WN, int RING, int BKB = 64, bool PRE = false, bool SKIP = false>
+// PREWAIT (with PRE): the first kRing stages were issued by pp_issue_prologue, and the loop starts
+// by waiting for every outstanding vector memory instruction of the thread (for callers whose
+// stores after the prologue are fewer or data-dependent).  The lane-dependent offsets are then
+// computed afresh on every call (a persistent caller's loop does not keep them live through its
+// epilogue).
+template <int BM, int BN, int WM, int WN, int RING, int BKB = 64, bool PRE = false, bool SKIP = false,
+          bool PREWAIT = false>
 LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __amdgpu_buffer_rsrc_t ra,
                          const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsA& pa, __amdgpu_buffer_rsrc_t rb,
                          const typename PPCfg<BM, BN, WM, WN, RING, BKB>::RowsB& pb, int K, char* smem, int na = 0,
                          int pairs = 0) {
   using C = PPCfg<BM, BN, WM, WN, RING, BKB>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  int tid = threadIdx.x;
+  if constexpr (PREWAIT) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = wave_id();
   const int group = wave >> 2;
   const int wm = wave / WN, wn = wave % WN;
   const int nk = (K + C::kBK - 1) / C::kBK;
@@ -255,6 +263,8 @@ LSK_DEV void pp_mainloop(typename PPCfg<BM, BN, WM, WN, RING, BKB>::Acc& acc, __
 #pragma unroll
     for (int s = 0; s < C::kAhead; ++s)
       if (s < nk) issue(s, Chk{});
+    wait_vm<0>();
+  } else if constexpr (PREWAIT) {
     wait_vm<0>();
   }
   phase_barrier();

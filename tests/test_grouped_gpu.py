@@ -91,13 +91,14 @@ def test_grouped_linear_mx(R, E, N, K, bias):
         assert np.array_equal(got[r0:r1], C.bf16_bits(ref)), "expert %d" % e
 
 
-@pytest.mark.parametrize("variant", [1, 5])
+@pytest.mark.parametrize("variant", [1, 5, 6])
 def test_grouped_linear_int8_tile_choice(variant):
-    """The grouped linear on the 128x256 (1) and the 256x256 (5) ping-pong tiles, each chosen, with
-    experts of several 256-row tiles and a bias: the oracle's bits."""
+    """The grouped linear on the 128x256 (1) and the 256x256 ping-pong tiles (5 persistent, 6 one
+    tile per block), each chosen, with experts of several 256-row tiles and a bias: the oracle's
+    bits."""
     from lockstep_amd import _lib as L
     from lockstep_amd import moe_ref as MR
-    R, E, N, K = 1500, 5, 384, 320
+    R, E, N, K = 1500, 5, 384, 448
     g = np.random.default_rng(91 + variant)
     cnt = _counts(g, E, R)
     offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)
@@ -135,7 +136,7 @@ def test_grouped_linear_clamps_bad_offsets():
                for _ in range(E)]
     dev_ex = [(to_dev(W).t(), to_dev(ws), to_dev(np.zeros((K, N // 2), np.int8)).t(), to_dev(np.ones(K, F32)),
                None, None) for (W, ws) in experts]
-    for variant in (-1, 0, 1, 5):
+    for variant in (-1, 0, 1, 5, 6):
         from lockstep_amd import _lib as L
         L.call("lsk_moe_select", variant)
         try:

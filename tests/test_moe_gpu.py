@@ -193,11 +193,11 @@ def test_moe_multi_chunk_dispatch(T, E, k):
     _run_case(T, E, k, 128, 64, seed=11 + T)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6])
 def test_moe_grouped_gemm_variants(variant):
     """Every grouped-GEMM kernel (register-staged 128x128 tile, ping-pong 128x256 tile, the
     decode GEMV, the 128x256 tile on four waves, the ping-pong tile with 128-byte K stages, the
-    256x256 tile) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
+    256x256 tile persistent and one tile per block) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
     their rows eight at a time), empty experts, a bias and SwiGLU-OAI; an odd number of routed rows
     (the down tiles' row-pair operand ends in a half pair)."""
     from lockstep_amd import _lib as L
@@ -207,18 +207,21 @@ def test_moe_grouped_gemm_variants(variant):
         _run_case(301, 8, 3, 256, 128, seed=17)
         _run_case(150, 6, 2, 320, 96, seed=14, bias=True, act="swigluoai")
         _run_case(5, 16, 4, 256, 128, seed=15)
-        if variant in (1, 5):
+        if variant in (1, 5, 6):
             # experts of several 256-row tiles and a partial last one, I not a multiple of 128
             _run_case(1100, 6, 3, 384, 320, seed=18)
+            # both projections with K >= 384 (the persistent 256x256 kernel takes both)
+            _run_case(1100, 6, 3, 448, 400, seed=19, bias=True, act="swigluoai")
     finally:
         L.call("lsk_moe_select", -1)
 
 
-def test_moe_256_tiles():
-    """The 256x256 expert tiles (chosen): Zipf-skewed experts of one to several 256-row tiles, with a
-    bias and SwiGLU-OAI, and with the shared expert on."""
+@pytest.mark.parametrize("variant", [5, 6])
+def test_moe_256_tiles(variant):
+    """The 256x256 expert tiles (chosen; persistent and one tile per block): Zipf-skewed experts of
+    one to several 256-row tiles, with a bias and SwiGLU-OAI, and with the shared expert on."""
     from lockstep_amd import _lib as L
-    L.call("lsk_moe_select", 5)
+    L.call("lsk_moe_select", variant)
     try:
         _run_case(700, 8, 4, 256, 256, seed=31)
         _run_case(513, 4, 2, 512, 192, seed=32, bias=True, act="swigluoai")
@@ -234,7 +237,7 @@ def test_moe_per_call_kernel_choice():
     from lockstep_amd import moe_ref as MR
     L.call("lsk_moe_select", 2)            # the thread: the decode GEMV
     try:
-        for v in (0, 1, 3, 4, 5, -1):
+        for v in (0, 1, 3, 4, 5, 6, -1):
             with MR.kernel_choice(moe=v):
                 _run_case(300, 12, 4, 256, 192, seed=13)
         _run_case(40, 8, 3, 256, 192, seed=16)   # the thread's setting again
@@ -296,14 +299,17 @@ def test_config4_full_bit_exact(T):
     _run_case(T, c["E"], c["k"], c["H"], c["I"], seed=40 + T)
 
 
-def test_config4_t4096_token_subset():
+@pytest.mark.parametrize("variant", [-1, 5])
+def test_config4_t4096_token_subset(variant):
     """T=4096 on the device; a seeded subset of tokens against the oracle run on just those
-    tokens (a token's output depends only on its own row and routing)."""
+    tokens (a token's output depends only on its own row and routing).  Under the default choice
+    and on the persistent 256x256 tiles (about a thousand tiles per projection: every block walks
+    several)."""
     from lockstep_amd import moe_ref as MR
     from lockstep_amd import workloads as WL
     c = WL.QWEN3_30B_A3B
     T = 4096
-    say("config4 T=4096")
+    say("config4 T=4096", dict(variant=variant))
     x, experts, logits = WL.moe_inputs(T, c["E"], c["k"], c["H"], c["I"], seed=44)
     dx = bf16_dev(x)
     dexp = device_experts(experts)
@@ -312,7 +318,8 @@ def test_config4_t4096_token_subset():
     assert np.array_equal(bits(idx_d), idx) and np.array_equal(u16(w_d), w)
     loads = np.bincount(idx.reshape(-1), minlength=c["E"])
     say("expert loads: max %d, min %d, zero-load experts %d" % (loads.max(), loads.min(), (loads == 0).sum()))
-    y, _, _ = MR.moe_forward(dx, None, dexp, c["k"], True, _tab(), 0, MR.act_silu, routing=(idx_d, w_d))
+    with MR.kernel_choice(moe=variant):
+        y, _, _ = MR.moe_forward(dx, None, dexp, c["k"], True, _tab(), 0, MR.act_silu, routing=(idx_d, w_d))
     rows = np.sort(np.random.default_rng(1).choice(T, 512, replace=False))
     ref = C.moe_forward(x[rows], oracle_experts(experts), idx[rows], w[rows])
     assert np.array_equal(u16(y)[rows], ref)
