@@ -252,6 +252,13 @@ int lsk_gemm_fuse_rowquant(int on);
  * Thread-local. */
 int lsk_quant8_dyn_single_pass(int on);
 
+/* Tuning control with no counterpart in the reference: the quantise pass of lsk_linear_dyn's
+ * quant8_dyn (0: row pairs per block; 1, the default: a contiguous tensor with K % 64 == 0 and M
+ * even walked in the order of q, a wave's stores covering two whole 128-byte lines of q, 0
+ * otherwise; 2: as 1 with ordinary rather than non-temporal loads in both passes).  The same
+ * exponent and q.  Thread-local. */
+int lsk_quant8_dyn_variant(int v);
+
 /* Tuning control with no counterpart in the reference: the persistent form of the 256x256
  * ping-pong kernel, taken for whole tiles under the POW2 epilogue with binary32 output (the
  * ref_block_v1 GEMMs): 1 one block per compute unit (the default), 0 off (one tile per block),

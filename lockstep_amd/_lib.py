@@ -56,6 +56,7 @@ SIGNATURES = {
     "lsk_gemm_select": (_I, [_I]),
     "lsk_gemm_fuse_rowquant": (_I, [_I]),
     "lsk_quant8_dyn_single_pass": (_I, [_I]),
+    "lsk_quant8_dyn_variant": (_I, [_I]),
     "lsk_moe_fuse_route": (_I, [_I]),
     "lsk_gemm_persist": (_I, [_I]),
     "lsk_quant8_pow2": (_I, [_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P, _P]),

@@ -248,8 +248,13 @@ LSK_DEV void block_run(int64_t n, int64_t& b0, int64_t& b1) {
   b1 = b0 + per < n ? b0 + per : n;
 }
 
+template <bool NT = true>
 __global__ __launch_bounds__(256) void dyn_amax_kernel(const float* __restrict__ x, int64_t M, int64_t K,
                                                        int64_t ldx, int flat, float* __restrict__ partial) {
+  auto ld = [](const float4* p) {
+    if constexpr (NT) return ld_nt(p);
+    return *p;
+  };
   __shared__ float red[4];
   float am = 0.0f;
   if (flat) {
@@ -261,13 +266,13 @@ __global__ __launch_bounds__(256) void dyn_amax_kernel(const float* __restrict__
     for (; i + 256 * (kDynUnroll - 1) < b1; i += 256 * kDynUnroll) {
       float4 v[kDynUnroll];
 #pragma unroll
-      for (int u = 0; u < kDynUnroll; ++u) v[u] = ld_nt(x4 + i + 256 * u);
+      for (int u = 0; u < kDynUnroll; ++u) v[u] = ld(x4 + i + 256 * u);
 #pragma unroll
       for (int u = 0; u < kDynUnroll; ++u)
         am = fmaxf(am, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
     }
     for (; i < b1; i += 256) {
-      const float4 v = ld_nt(x4 + i);
+      const float4 v = ld(x4 + i);
       am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     }
     if (blockIdx.x == gridDim.x - 1)
@@ -399,6 +404,84 @@ __global__ __launch_bounds__(256) void dyn_quant_pair_kernel(const float* __rest
   }
 }
 
+// Pass 2 of quant8_dyn into the row-pair layout for a contiguous tensor with no padding bytes
+// (ldx == ldq == K, K % 64 == 0, M even, M K < 2^31), walked in the order of q: unit f is q bytes
+// 4 f .. 4 f + 3, which (q byte o = p 2K + c 128 + r 64 + j: row pair p, K chunk c, row 2p + r,
+// column 64 c + j) come from one float4 of x.  Each block takes a contiguous run of units, lane-
+// contiguous, so a wave's store covers 256 contiguous bytes of q (two whole 128-byte lines, both
+// rows of a pair) and its load four 256-byte runs of x (a chunk of each row of the pair, twice).
+// Every load of a step is issued before any is used, none under a branch (a lane past the run
+// re-reads the run's first float4 and stores nothing).
+constexpr int kDynU2 = 8;
+
+template <bool NT>
+__global__ __launch_bounds__(256) void dyn_quant_pair_flat_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                                  const float* __restrict__ partial, int nparts,
+                                                                  int8_t* __restrict__ q, int32_t* __restrict__ e_out,
+                                                                  int32_t* __restrict__ erow) {
+  __shared__ float red[4];
+  const int n4 = (int)((M * K) >> 2);
+  const int per = (n4 + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int b0 = (int)blockIdx.x * per, b1 = min(b0 + per, n4);
+  const float4* x4 = (const float4*)x;
+  const int K2 = 2 * (int)K;
+  // q byte 4 f as (row pair pp, offset rem in the pair's 2K bytes); each step of 256 units adds 1024
+  const int f0 = b0 + (int)threadIdx.x;
+  int pp = (4 * f0) / K2, rem = 4 * f0 - pp * K2;
+  const int dp = 1024 / K2, drem = 1024 - dp * K2;
+  auto src = [&](int f, int p, int r) {
+    // element (2p + (r >> 6 & 1), 64 (r >> 7) + (r & 63)) of x, as a float4 index
+    const int e = (2 * p + ((r >> 6) & 1)) * (int)K + 64 * (r >> 7) + (r & 63);
+    return x4 + (f < b1 ? (e >> 2) : b0);
+  };
+  auto load = [&](const float4* p) {
+    if constexpr (NT) return ld_nt(p);
+    return *p;
+  };
+  int lp[kDynU2], lr[kDynU2];
+  auto addrs = [&]() {
+#pragma unroll
+    for (int u = 0; u < kDynU2; ++u) {
+      lp[u] = pp;
+      lr[u] = rem;
+      pp += dp;
+      rem += drem;
+      if (rem >= K2) {
+        rem -= K2;
+        ++pp;
+      }
+    }
+  };
+  // the first step requested before the partial maxima are reduced (it does not depend on them)
+  float4 v[kDynU2];
+  int f = f0;
+  if (b0 < b1) {
+    addrs();
+#pragma unroll
+    for (int u = 0; u < kDynU2; ++u) v[u] = load(src(f + 256 * u, lp[u], lr[u]));
+  }
+  float am = 0.0f;
+  for (int j = threadIdx.x; j < nparts; j += 256) am = fmaxf(am, partial[j]);
+  am = block_max<256>(am, red);
+  const int e = pow2_exponent(am);
+  const float sc = pow2f(e);
+  if (blockIdx.x == 0 && threadIdx.x == 0) e_out[0] = e;
+  if (erow)
+    for (int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x; r < M; r += (int64_t)gridDim.x * 256) erow[r] = e;
+  if (b0 >= b1) return;
+  uint32_t* q4 = (uint32_t*)q;
+  for (;;) {
+#pragma unroll
+    for (int u = 0; u < kDynU2; ++u)
+      if (f + 256 * u < b1) q4[f + 256 * u] = quant_pow2_x4(v[u], sc);
+    f += 256 * kDynU2;
+    if (f >= b1) break;
+    addrs();
+#pragma unroll
+    for (int u = 0; u < kDynU2; ++u) v[u] = load(src(f + 256 * u, lp[u], lr[u]));
+  }
+}
+
 // Single-pass quant8_dyn into the row-pair layout for a tensor that fits on chip (a cooperative
 // launch: every block resident, one grid-wide barrier).  Block b holds the contiguous run of
 // 256 * (kQ1Regs + kQ1Lds) float4s from b * 256 * (kQ1Regs + kQ1Lds): step j of thread t is float4
@@ -512,7 +595,7 @@ int launch_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t*
   const int flat = (ldx == K && ldq == K && ((uintptr_t)x % 16) == 0 && ((uintptr_t)q % 8) == 0) ? 1 : 0;
   int64_t blocks = flat ? (total + 256 * 16 - 1) / (256 * 16) : M;
   blocks = blocks < 1 ? 1 : (blocks > kDynBlocks ? kDynBlocks : blocks);
-  hipLaunchKernelGGL(dyn_amax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat, partial);
+  hipLaunchKernelGGL(dyn_amax_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat, partial);
   int rc = lsk::check_launch("dyn_amax_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL(dyn_quant_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat,
@@ -525,6 +608,13 @@ int launch_quant8_dyn(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t*
 // activation against 60-65 us for the two passes (maxima 20 us, quantise 33 us); the cooperative
 // launch and its grid barrier cost more than the second read of x saves.
 thread_local int g_quant1 = 0;
+
+// Pass 2 of the row-pair quant8_dyn: 0 row pairs per block; 1 (the default) the walk in the order
+// of q (non-temporal loads in both passes); 2 as 1 with ordinary loads in both passes.  Measured on
+// MI355X (Qwen2.5-7B block at 8192 rows, both passes): 117 MB of x 51.7 / 45.7 / 41.2 us and 620 MB
+// 248 / 228 / 274 us alone; in the block step the sites' quant 450 / 418 / 486 us in all (2 takes
+// the second pass from the Infinity Cache alone, but loses it to the GEMMs between the sites).
+thread_local int g_dynq = 1;
 
 // Blocks of the single-pass kernel that the device keeps resident at once (four per CU when its
 // registers and LDS allow), cached per device; 0 when the device cannot launch it cooperatively.
@@ -569,9 +659,24 @@ int launch_quant8_dyn_pair(const float* x, int64_t M, int64_t K, int64_t ldx, in
   const int flat = (ldx == K && ((uintptr_t)x % 16) == 0) ? 1 : 0;
   int64_t blocks = flat ? (total + 256 * 16 - 1) / (256 * 16) : M;
   blocks = blocks < 1 ? 1 : (blocks > kDynBlocks ? kDynBlocks : blocks);
-  hipLaunchKernelGGL(dyn_amax_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat, partial);
+  const bool nt = g_dynq != 2;
+  if (nt)
+    hipLaunchKernelGGL(dyn_amax_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat, partial);
+  else
+    hipLaunchKernelGGL(dyn_amax_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, ldx, flat, partial);
   int rc = lsk::check_launch("dyn_amax_kernel");
   if (rc) return rc;
+  if (g_dynq && flat && ldq == K && K % 64 == 0 && M % 2 == 0 && total < (int64_t)1 << 31 && ((uintptr_t)q % 4) == 0) {
+    int64_t fb = (total / 4 + 256 * kDynU2 * 2 - 1) / (256 * kDynU2 * 2);
+    fb = fb < 1 ? 1 : (fb > kDynBlocks ? kDynBlocks : fb);
+    if (nt)
+      hipLaunchKernelGGL(dyn_quant_pair_flat_kernel<true>, dim3((unsigned)fb), dim3(256), 0, s, x, M, K,
+                         (const float*)partial, (int)blocks, q, e_out, erow);
+    else
+      hipLaunchKernelGGL(dyn_quant_pair_flat_kernel<false>, dim3((unsigned)fb), dim3(256), 0, s, x, M, K,
+                         (const float*)partial, (int)blocks, q, e_out, erow);
+    return lsk::check_launch("dyn_quant_pair_flat_kernel");
+  }
   int64_t qblocks = (M + 1) / 2;
   qblocks = qblocks < 1 ? 1 : (qblocks > kDynBlocks ? kDynBlocks : qblocks);
   hipLaunchKernelGGL(dyn_quant_pair_kernel, dim3((unsigned)qblocks), dim3(256), 0, s, x, M, K, ldx,
@@ -655,6 +760,12 @@ extern "C" int lsk_gemm_reads_row_pairs(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 != 0) return 0;
   const int64_t kp = (K + 63) / 64 * 64;
   return lsk::gemm_takes_pp((const int8_t*)(uintptr_t)256, kp, M, N, K, kp) ? 1 : 0;
+}
+
+extern "C" int lsk_quant8_dyn_variant(int v) {
+  LSK_REQUIRE(v >= 0 && v <= 2, "lsk_quant8_dyn_variant: %d not in [0, 2]", v);
+  g_dynq = v;
+  return LSK_OK;
 }
 
 extern "C" int lsk_quant8_dyn_single_pass(int on) {

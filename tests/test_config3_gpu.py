@@ -302,3 +302,41 @@ def test_linear_dyn_single_pass_quant(T, N, K, scale):
     with np.errstate(over="ignore", invalid="ignore"):
         ref = C.dequant_pow2(C.gemm_int(q_ref[rows], W8.T.astype(np.int64)), e_ref + 5)
     assert np.array_equal(bits(y1)[rows], f32_bits(ref))
+
+
+@pytest.mark.parametrize("T,N,K,scale", [(256, 512, 64, 1.0), (2048, 512, 3584, 1.0), (302, 520, 3584, 3e4),
+                                         (6, 64, 64, 1e-30), (301, 520, 3600, 1.0), (1000, 264, 192, 0.0)])
+def test_linear_dyn_quant_pass_variants(T, N, K, scale):
+    """The quantise pass of linear_dyn's quant8_dyn in each form (lsk_quant8_dyn_variant 0: row
+    pairs per block; 1: the walk in the order of q, taken for K % 64 == 0 and even T; 2: as 1 with
+    ordinary loads) writes the same workspace bytes (partial maxima, exponents, q) and y: a tensor
+    smaller than one block's threads, exponents clipped at 40 (subnormal x) and an all-zero tensor,
+    and shapes that fall back to the row pairs (odd T, K % 64 != 0).  y against the oracle on a row
+    sample."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import ops
+    say("linear_dyn quant pass variants: T=%d N=%d K=%d scale=%g" % (T, N, K, scale))
+    g = np.random.default_rng(T + 3 * K)
+    x = (g.standard_normal((T, K)) * scale).astype(F32)
+    W8 = g.integers(-127, 128, (N, K), dtype=np.int8)
+    xd, Wd = torch.from_numpy(x).to(dev()), torch.from_numpy(W8).to(dev())
+    nbytes = L.load().lsk_linear_dyn_workspace(T, K)
+    got = []
+    for v in (0, 1, 2):
+        work = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=dev())
+        y = torch.empty((T, N), dtype=torch.float32, device=dev())
+        ex = torch.zeros((1,), dtype=torch.int32, device=dev())
+        L.call("lsk_quant8_dyn_variant", v)
+        try:
+            ops.linear_dyn(xd, Wd, 5, stages=3, work=work, y=y, ex=ex)
+        finally:
+            L.call("lsk_quant8_dyn_variant", 1)
+        got.append((work.cpu(), y.view(torch.int32).cpu(), int(ex[0].item())))
+    for w, y, e in got[1:]:
+        assert e == got[0][2] and torch.equal(w, got[0][0]) and torch.equal(y, got[0][1])
+    q_ref, e_ref = C.quant8_dyn(x)
+    assert got[0][2] == e_ref
+    rows = np.sort(np.random.default_rng(T).choice(T, min(T, 48), replace=False))
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.dequant_pow2(C.gemm_int(q_ref[rows], W8.T.astype(np.int64)), e_ref + 5)
+    assert np.array_equal(got[0][1].numpy()[rows].view(np.uint32), f32_bits(ref))
