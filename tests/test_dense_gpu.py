@@ -569,3 +569,24 @@ def test_one_row_fused_rowquant_gemv(N, K, xdt):
         finally:
             L.call("lsk_gemm_select", -1)
         assert np.array_equal(bits(y), C.epilogue_v21(acc, ws, asc, bias, "bf16")), tile
+
+
+def test_mfma_bf16_acc_probe_exact_cases():
+    """lsk_mfma_bf16_acc_probe (one v_mfma_f32_16x16x32_bf16 per case, D = A B^T + C) on cases whose
+    every partial sum is an integer below 2^24, so any order of additions and roundings gives the
+    exact value: the operand layout (a rows are M, b rows are N, K contiguous) and D's layout (row
+    M, column N) against a float64 matmul, with C = 0 and with integer C."""
+    from lockstep_amd import _lib as L
+    g = np.random.default_rng(5)
+    n = 64
+    a = g.integers(-64, 65, (n, 16, 32)).astype(np.float32)
+    b = g.integers(-64, 65, (n, 16, 32)).astype(np.float32)
+    c = np.where(np.arange(n)[:, None, None] % 2 == 0, 0.0,
+                 g.integers(-2 ** 20, 2 ** 20, (n, 16, 16))).astype(np.float32)
+    to_bf = lambda x: torch.from_numpy((x.view(np.uint32) >> 16).astype(np.uint16).view(np.int16)).to(dev())  # noqa: E731
+    ad, bd, cd = to_bf(a), to_bf(b), to_dev(c)
+    d = torch.full((n, 16, 16), float("nan"), device=dev())
+    L.call("lsk_mfma_bf16_acc_probe", L.ptr(ad), L.ptr(bd), L.ptr(cd), L.ptr(d), n, None)
+    torch.cuda.synchronize()
+    want = (np.einsum("nmk,njk->nmj", a.astype(np.float64), b.astype(np.float64)) + c).astype(np.float32)
+    assert np.array_equal(f32_bits(d.cpu().numpy()), f32_bits(want))
