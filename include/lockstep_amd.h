@@ -232,9 +232,18 @@ int lsk_tree_sum(const float* v, int64_t ldv, int64_t R, int64_t n, float* out, 
  * pieces straight into registers / for M <= 16 whole rows through LDS; 17: four-wave 256x128,
  * one wave per SIMD with 128x64 wave tiles (16, its 256x256 form, spilled registers and is
  * refused); 18: ping-pong 256x128 with 128-byte K stages
- * in a three-stage ring, the shape's default) or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
+ * in a three-stage ring, the shape's default; 19: for every M <= 32 whose activation rows fit in
+ * LDS (M * (ceil(K / 1024) * 1024 + 16) <= 160 KB) the skinny GEMV -- A staged in LDS once per
+ * block, weight rows streamed into the MFMA operand, the default for 4 < M <= 32 -- other M as 5)
+ * or -1 to choose by shape (the default).  Results are identical for every choice; only speed differs.
  * The choice applies to the calling host thread's later launches only (thread-local). */
 int lsk_gemm_select(int tile_id);
+
+/* Tuning control with no counterpart in the reference: the launch shape of the skinny decode GEMV
+ * (lsk_gemm_select 19): gpb groups of 16 weight rows per block, kw waves per group splitting K,
+ * depth weight steps in flight per wave (4 or 8); 0 leaves a parameter to the shape rule.
+ * gpb * kw <= 16.  Results are identical.  Thread-local. */
+int lsk_gemm_skinny_shape(int gpb, int kw, int depth);
 
 /* Tuning control with no counterpart in the reference: 1 (the default) runs lsk_w8a8_matmul /
  * lsk_w8a8_matmul_pairs with one activation row and K <= 4096 as a single launch, the row quant

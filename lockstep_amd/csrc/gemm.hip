@@ -10,6 +10,7 @@
 //
 // Integer accumulation is exact in any order (|acc| <= K * 127^2 < 2^31 for K <= 133144), so
 // tiling and K-splits never change a bit; the epilogue is applied once per output element.
+#include <algorithm>
 #include <atomic>
 
 #include "mfma_tile.h"
@@ -684,6 +685,148 @@ __global__ __launch_bounds__(1024) void gemv_i8_lds_kernel(const int8_t* __restr
     }
 }
 
+// Decode GEMV (4 < M <= 32) with the activation rows staged once per block in LDS and the weight
+// rows streamed straight into v_mfma_i32_16x16x64_i8 B registers.  A block of GPB x KW waves owns
+// GPB groups of 16 weight rows; the KW waves of a group split its K steps.  Prologue, all in
+// flight together: the epilogue operands of the lanes that will store, A by direct-to-LDS loads
+// (1 KB of one row per instruction; row r at r * ldsk, ldsk a multiple of 1024 plus 16 so that
+// consecutive rows start 16 bytes apart in the bank space; zeros past K), then each wave's first
+// D weight steps -- and a wait for everything but those D.  Then the weight stream is the only
+// traffic counted by a wave's vmcnt: lane l loads 16 bytes of weight row n0 + l % 16 at K-group
+// l / 16 of every 64-byte step, D steps in flight, and the matching A fragment comes from LDS.
+// With PAIRS the weights are a row-pair copy (rows 2i and 2i + 1 interleaved by 64-byte K chunks,
+// row stride ldw a multiple of 64): each load instruction then reads 8 whole 128-byte lines
+// instead of 16 half lines.  Weight bytes past K multiply zeros of A; rows past N and steps past
+// the slice load zeros through the buffer range.  The K-slices' exact int32 sums are added in LDS
+// (over the A area, after a barrier) and the group's first wave applies the epilogue.
+template <int MT, int D, bool PAIRS>
+__global__ __launch_bounds__(1024) void gemv_i8_skinny_kernel(const int8_t* __restrict__ A, int lda,
+                                                              const int8_t* __restrict__ W, int ldw, int M, int N,
+                                                              int K, int gpb, int kw, int sps, int ldsk, EpiParams ep) {
+  extern __shared__ __attribute__((aligned(16))) char smem_sk[];
+  const int lane = threadIdx.x & 63, wave = wave_id(), nw = blockDim.x >> 6;
+  const int steps = (K + 63) >> 6;
+  const int G = (N + 15) >> 4;
+  const int g = blockIdx.x * gpb + wave / kw;
+  const int ks = wave - (wave / kw) * kw;
+  const int s0 = ks * sps;
+  const int nst = g < G ? max(0, min(steps, s0 + sps) - s0) : 0;
+  const int col = lane & 15, kg = lane >> 4;
+  const int n = g * 16 + col;
+  // the raw epilogue operands of this lane's outputs (row: asc, or erow under POW2; column: ws and
+  // bias, or ecol), loaded ahead of everything else by branch-free buffer loads (zeros past M / N
+  // and for absent operands) and only combined at the stores, so no load waits here
+  const bool pow2 = ep.order == LSK_EPI_POW2, v2x = ep.order == LSK_EPI_V21 || ep.order == LSK_EPI_V2;
+  const bool mine = ks == 0 && g < G;
+  const __amdgpu_buffer_rsrc_t rrow =
+      lsk::make_rsrc(pow2 ? (const void*)ep.erow : (const void*)ep.asc, (pow2 ? ep.erow != nullptr : v2x) ? 4 * M : 0);
+  const __amdgpu_buffer_rsrc_t rcol0 =
+      lsk::make_rsrc(pow2 ? (const void*)ep.ecol : (const void*)ep.ws, (pow2 ? ep.ecol != nullptr : v2x) ? 4 * N : 0);
+  const __amdgpu_buffer_rsrc_t rcol1 = lsk::make_rsrc(ep.bias, v2x && ep.bias ? 4 * N : 0);
+  const uint32_t ocol = mine && n < N ? (uint32_t)(4 * n) : lsk::kOob;
+  const uint32_t col0 = __builtin_amdgcn_raw_buffer_load_b32(rcol0, ocol, 0, 0);
+  const uint32_t col1 = __builtin_amdgcn_raw_buffer_load_b32(rcol1, ocol, 0, 0);
+  uint32_t rowv[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + kg * 4 + r;
+      rowv[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rrow, mine && m < M ? (uint32_t)(4 * m) : lsk::kOob, 0, 0);
+    }
+  lsk::compiler_fence();
+  // A into LDS: chunk c = (row, 1 KB piece) per wave instruction
+  {
+    const int cpr = (K + 1023) >> 10;
+    const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(A, (int64_t)(M - 1) * lda + K);
+    for (int c = wave; c < M * cpr; c += nw) {
+      const int r = c / cpr, j = c - r * cpr;
+      const int kb = j * 1024 + lane * 16;
+      const uint32_t off = kb < K ? (uint32_t)(r * lda + kb) : lsk::kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(smem_sk + r * ldsk + j * 1024), 16, off, 0, 0,
+                                               0);
+    }
+  }
+  // the first D weight steps
+  const int n0 = g * 16;
+  const int nrows = g < G ? ((N - n0) < 16 ? (N - n0) : 16) : 0;
+  const int64_t wbytes = PAIRS ? (int64_t)((nrows + 1) >> 1) * 2 * ldw : (int64_t)nrows * ldw;
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)(g < G ? n0 : 0) * ldw, wbytes);
+  const uint32_t wbase = col < nrows ? (PAIRS ? (uint32_t)((col >> 1) * 2 * ldw + (col & 1) * 64 + kg * 16 + s0 * 128)
+                                              : (uint32_t)(col * ldw + s0 * 64 + kg * 16))
+                                     : lsk::kOob;
+  constexpr uint32_t kStep = PAIRS ? 128 : 64;
+  v4i w[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u)
+    w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, u < nst ? wbase + u * kStep : lsk::kOob,
+                                                                         0, 2 /* non-temporal */));
+  lsk::compiler_fence();
+  lsk::wait_vm<D>();  // everything older than the D weight steps: A and the epilogue operands
+  __syncthreads();
+  v4i acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = zero4();
+  if (nst > 0) {
+    // activation rows of this lane's A fragments (clamped to a staged row; zeroed past M)
+    const char* arow[MT];
+    bool alive[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int r = t * 16 + col;
+      alive[t] = r < M;
+      arow[t] = smem_sk + (r < M ? r : M - 1) * ldsk + s0 * 64 + kg * 16;
+    }
+    for (int s = 0; s < nst; s += D) {
+      // each step's A fragments are read one step ahead, so their LDS latency overlaps an MFMA
+      v4i a[2][MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) a[0][t] = *(const v4i*)(arow[t] + s * 64);
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
+        if (u + 1 < D) {
+          const int st = s + u + 1 < nst ? s + u + 1 : 0;
+#pragma unroll
+          for (int t = 0; t < MT; ++t) a[(u + 1) & 1][t] = *(const v4i*)(arow[t] + st * 64);
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[t] = lsk::mfma_i8(alive[t] ? a[u & 1][t] : zero4(), w[u], acc[t]);
+        const int nx = s + u + D;
+        w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                           rw, nx < nst ? wbase + nx * kStep : lsk::kOob, 0, 2 /* non-temporal */));
+      }
+    }
+  }
+  if (kw > 1) {
+    __syncthreads();  // every wave is past its last A read: the partial sums reuse the LDS
+    v4i* red = (v4i*)smem_sk;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) red[(wave * MT + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (ks != 0) return;
+    for (int j = 1; j < kw; ++j)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] += red[((wave + j) * MT + t) * 64 + lane];
+  }
+  if (g >= G) return;
+  EpiCol ec{};
+  if (pow2) ec.sh = (int)col0;
+  else {
+    ec.ws = __uint_as_float(col0);
+    ec.b = __uint_as_float(col1);
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + kg * 4 + r;
+      EpiRow er{};
+      if (pow2) er.sh = ep.shift + (int)rowv[t][r];
+      else er.row = __uint_as_float(rowv[t][r]);
+      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], er, ec);
+    }
+}
+
 // Batch-few decode GEMV (M <= MR <= 8) on the VALU (v_dot4c_i32_i8), bandwidth-bound on the
 // weight stream.  A block is four waves; each wave owns 8 weight rows and one of WK K-slices
 // (WK = 1, 2 or 4 waves per row group).  Lane l reads 16 bytes of row l / 8 at chunk l % 8 of
@@ -1226,7 +1369,9 @@ thread_local int g_force_tile = -1;
 thread_local int g_row_rpw = 0;       // rows per wave of the whole-row GEMV (0: by shape)
 thread_local int g_rowq = 1;          // w8a8_matmul at M = 1: the row quant fused into the whole-row GEMV
 thread_local int g_gemv_variant = 0;  // M <= 4: 0 whole-row GEMV, 1 register double-buffered 8-row GEMV, 2 LDS-ring 8-row GEMV
-thread_local int g_gemv_mid = 0;      // 4 < M <= 32: 0 by shape, 1 direct 64-byte row pieces, 2 whole rows through LDS
+thread_local int g_gemv_mid = 0;      // M <= 32: 0 by shape, 1 direct 64-byte row pieces, 2 whole rows through LDS, 3 A staged in LDS (skinny)
+// the skinny GEMV's launch shape: groups per block, waves per group, weight steps in flight (0: by shape)
+thread_local int g_skinny_gpb = 0, g_skinny_kw = 0, g_skinny_d = 0;
 
 // the persistent POW2 kernel: 1 on (one block per CU), 0 off, > 1 that many blocks (tests)
 thread_local int g_pp_persist = 1;
@@ -1380,10 +1525,84 @@ static EpiParams shift_columns(const EpiParams& ep, int64_t n1) {
   return e;
 }
 
+// Launch shape of gemv_i8_skinny_kernel: A (M rows of ceil(K / 1024) KB + 16 bytes) must fit in
+// LDS.  Groups of 16 weight rows are dealt to one block per CU (one round of blocks covers them),
+// then each group's K steps are split over waves up to 16 waves per block.  (Measured on MI355X,
+// Llama-3.1-8B gate_up, graph replays over weight copies, us for gpb x kw at M = 8 / 32: 7 x 2
+// 25.9 / 30.4, 4 x 2 (two blocks per CU) 27.5 / 35.4, 8 x 2 27.5 / 32.5, 8 x 1 29.6 / 31.8, 4 x 4
+// 28.2 / 36.8.)
+struct SkinnyShape {
+  int gpb, kw, sps, ldsk, blocks, D;
+  size_t smem;
+};
+
+static bool skinny_shape(int M, int N, int K, SkinnyShape& sh) {
+  if (M < 1 || M > 32 || N < 1 || K < 16) return false;
+  const int steps = (K + 63) / 64, MT = M <= 16 ? 1 : 2;
+  sh.ldsk = (K + 1023) / 1024 * 1024 + 16;
+  const int64_t lds_a = (int64_t)M * sh.ldsk;
+  if (lds_a > 160 * 1024) return false;
+  const int64_t G = (N + 15) / 16;
+  int64_t gpb = std::min<int64_t>(16, std::max<int64_t>(1, (G + 255) / 256));
+  if (g_skinny_gpb > 0) gpb = g_skinny_gpb;
+  const int64_t blocks = (G + gpb - 1) / gpb;
+  int64_t kw = std::max<int64_t>(1, 16 / gpb);
+  if (g_skinny_kw > 0 && g_skinny_kw * gpb <= 16) kw = g_skinny_kw;
+  const int64_t sps = (steps + kw - 1) / kw;
+  kw = (steps + sps - 1) / sps;
+  sh.gpb = (int)gpb;
+  sh.kw = (int)kw;
+  sh.sps = (int)sps;
+  sh.blocks = (int)blocks;
+  sh.D = g_skinny_d > 0 ? g_skinny_d : (sps <= 4 ? 4 : 8);
+  sh.smem = (size_t)std::max<int64_t>(lds_a, gpb * kw * MT * 1024);
+  return blocks <= 0x7fffffff && sh.smem <= 160 * 1024;
+}
+
+// Whether launch_gemv runs (M, N, K) on gemv_i8_skinny_kernel under the calling thread's
+// selection: by shape for 4 < M <= 32 and N >= 8192 wherever A fits in LDS, or for any M <= 32
+// when selected.  (Measured on MI355X, graph replays over weight copies, the GEMV alone: Llama-3.1-8B
+// gate_up M = 8 / 16 / 32 29.1 / 32.1 / 47.5 -> 25.9 / 28.3 / 30.4 us.  With N <= 4096 a block
+// holds one group of weight rows, A is staged once per 16 weight rows, and the GEMVs that stream
+// whole rows through LDS stay ahead: down M = 8 14.5 against 16.2 us, the Qwen2.5-7B o_proj at
+// M = 16 6.9 against 7.3 us.)
+bool gemv_takes_skinny(int64_t M, int64_t N, int64_t K) {
+  SkinnyShape sh;
+  if (M > 32 || !skinny_shape((int)M, (int)std::min<int64_t>(N, 0x7fffffff), (int)K, sh)) return false;
+  return g_gemv_mid == 3 || (g_gemv_mid == 0 && g_gemv_variant == 0 && M > 4 && N >= 8192);
+}
+
+static int launch_skinny(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K, const EpiParams& ep,
+                         hipStream_t s) {
+  SkinnyShape sh;
+  if (!skinny_shape(M, N, K, sh)) return set_error("gemv: M=%d K=%d does not fit the skinny GEMV", M, K), LSK_ERR_ARG;
+  const bool pairs = (ep.pairs & 2) != 0;
+#define LSK_SK(MTV, DV, PV)                                                                                    \
+  {                                                                                                            \
+    auto kern = gemv_i8_skinny_kernel<MTV, DV, PV>;                                                            \
+    if (sh.smem > 65536 &&                                                                                     \
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) \
+      return set_error("gemv: cannot reserve LDS"), LSK_ERR_HIP;                                               \
+    hipLaunchKernelGGL(kern, dim3((unsigned)sh.blocks), dim3(64 * sh.gpb * sh.kw), sh.smem, s, a, lda, w, ldw, M, N, \
+                       K, sh.gpb, sh.kw, sh.sps, sh.ldsk, ep);                                                 \
+    return check_launch("gemv_i8_skinny_kernel");                                                              \
+  }
+#define LSK_SK_D(MTV, PV) \
+  if (sh.D == 4) LSK_SK(MTV, 4, PV) else LSK_SK(MTV, 8, PV)
+  if (M <= 16) {
+    if (pairs) LSK_SK_D(1, true) else LSK_SK_D(1, false)
+  } else {
+    if (pairs) LSK_SK_D(2, true) else LSK_SK_D(2, false)
+  }
+#undef LSK_SK_D
+#undef LSK_SK
+}
+
 // Waves per block of the decode GEMV: enough blocks x waves (about 8192) to keep every CU's
 // memory pipeline full, K split into 64-byte-aligned slices.
 static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M, int N, int K, const EpiParams& ep,
                        hipStream_t s) {
+  if ((ep.pairs & 2) || gemv_takes_skinny(M, N, K)) return launch_skinny(a, lda, w, ldw, M, N, K, ep, s);
   const int64_t Kp = (K + 127) / 128 * 128;
   if (M <= 4 && g_gemv_variant == 0 && K <= 4 * 8 * 1024) {
     // whole-row streaming: K-slices of NC <= 8 chunks (WK <= 4 waves per row).  (With 8 or 16
@@ -1515,6 +1734,7 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
 bool rowq_gemv_ok(const void* x, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int order) {
   return g_rowq && M == 1 && N >= 1 && N <= 0x7fffffff && K >= 16 && K <= 4096 && K % 16 == 0 && ldw % 16 == 0 &&
          aligned16(x) && aligned16(w) && (g_force_tile < 0 || g_force_tile == 5) && g_gemv_variant == 0 &&
+         g_gemv_mid != 3 &&
          (order == LSK_EPI_V21 || order == LSK_EPI_V2) && ldw * 64 < 0x7fffffff;
 }
 
@@ -1553,6 +1773,13 @@ static bool tiles_fast(const int8_t* a, int64_t lda, const int8_t* w, int64_t ld
          N <= 0x7fffffff && K > 0 && lda * 256 < 0x7fffffff && ldw * 256 < 0x7fffffff;
 }
 
+// Whether launch_gemm runs (M, N, K) on the decode GEMV that reads the weight's row-pair copy
+// (gemv_i8_skinny_kernel), for a weight of row stride ldw at a 16-byte aligned address.
+bool gemm_takes_skinny(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int64_t lda) {
+  if (M <= 0 || M > 32 || N <= 0 || !tiles_fast(w, lda, w, ldw, M, N, K)) return false;
+  return (g_force_tile < 0 || g_force_tile == 5) && gemv_takes_skinny(M, N, K);
+}
+
 // Whether launch_gemm runs (M, N, K) on the ping-pong tile kernels only (the kernels that read an
 // A operand in the row-pair layout), for an A of row stride lda at a 16-byte aligned address.
 bool gemm_takes_pp(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int64_t lda) {
@@ -1566,9 +1793,11 @@ bool gemm_takes_pp(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiParams& ep, hipStream_t s) {
   if (M == 0 || N == 0) return LSK_OK;
-  LSK_REQUIRE(!ep.pairs || (aligned16(a) && gemm_takes_pp(w, ldw, M, N, K, lda) && (!(ep.pairs & 1) || lda % 64 == 0) &&
-                            (!(ep.pairs & 2) || ldw % 64 == 0)),
-              "gemm: operands in the row-pair layout need the ping-pong tiles (M=%lld N=%lld K=%lld lda=%lld ldw=%lld)",
+  LSK_REQUIRE(!ep.pairs || (ep.pairs == 2 && ldw % 64 == 0 && gemm_takes_skinny(w, ldw, M, N, K, lda)) ||
+                  (aligned16(a) && gemm_takes_pp(w, ldw, M, N, K, lda) && (!(ep.pairs & 1) || lda % 64 == 0) &&
+                   (!(ep.pairs & 2) || ldw % 64 == 0)),
+              "gemm: operands in the row-pair layout need the ping-pong tiles or the skinny decode GEMV (M=%lld "
+              "N=%lld K=%lld lda=%lld ldw=%lld)",
               (long long)M, (long long)N, (long long)K, (long long)lda, (long long)ldw);
   const bool fast = tiles_fast(a, lda, w, ldw, M, N, K);
   if (!fast) {
@@ -1679,6 +1908,14 @@ extern "C" int lsk_w8a8_matmul_pairs(const void* x, int x_dtype, int64_t ldx, in
   const int64_t ldq = pair ? kp : (K + 15) / 16 * 16;
   int8_t* q = (int8_t*)workspace;
   float* asc = (float*)((char*)workspace + w8a8_q_bytes(M, K));
+  if (!pair && w_pairs && lsk::gemm_takes_skinny(w_pairs, kp, M, N, K, ldq)) {
+    // decode rows: row-major q, the weight's row-pair copy streamed by the skinny GEMV
+    LSK_REQUIRE(w && out && ldw >= K && ldo >= N, "lsk_w8a8_matmul: bad operand");
+    if ((rc = lsk_rowquant(x, x_dtype, M, K, ldx, q, ldq, asc, stream))) return rc;
+    EpiParams ep{order, out_dtype, ws, asc, bias, nullptr, nullptr, 0, out, ldo};
+    ep.pairs = 2;
+    return lsk::launch_gemm(q, ldq, w_pairs, kp, M, N, K, ep, (hipStream_t)stream);
+  }
   if (!pair)
     return (rc = lsk_rowquant(x, x_dtype, M, K, ldx, q, ldq, asc, stream))
                ? rc
@@ -1722,6 +1959,16 @@ extern "C" int lsk_gemm_fuse_rowquant(int on) {
   return LSK_OK;
 }
 
+extern "C" int lsk_gemm_skinny_shape(int gpb, int kw, int depth) {
+  LSK_REQUIRE(gpb >= 0 && gpb <= 16 && kw >= 0 && kw <= 16 && (gpb == 0 || kw == 0 || gpb * kw <= 16) &&
+                  (depth == 0 || depth == 4 || depth == 8),
+              "lsk_gemm_skinny_shape: gpb=%d kw=%d depth=%d (gpb * kw <= 16, depth 0, 4 or 8)", gpb, kw, depth);
+  lsk::g_skinny_gpb = gpb;
+  lsk::g_skinny_kw = kw;
+  lsk::g_skinny_d = depth;
+  return LSK_OK;
+}
+
 extern "C" int lsk_gemm_persist(int blocks) {
   LSK_REQUIRE(blocks >= 0 && blocks <= 65536, "lsk_gemm_persist: %d blocks", blocks);
   lsk::g_pp_persist = blocks;
@@ -1729,10 +1976,10 @@ extern "C" int lsk_gemm_persist(int blocks) {
 }
 
 extern "C" int lsk_gemm_select(int tile_id) {
-  LSK_REQUIRE(tile_id >= -1 && tile_id <= 18 && tile_id != 16,
-              "lsk_gemm_select: tile id %d not in [-1, 18] (16, the four-wave 256x256 tile, was removed)", tile_id);
-  lsk::g_force_tile = ((tile_id >= 6 && tile_id <= 11) || tile_id == 14 || tile_id == 15) ? 5 : tile_id;
-  lsk::g_gemv_mid = tile_id == 14 ? 1 : (tile_id == 15 ? 2 : 0);
+  LSK_REQUIRE(tile_id >= -1 && tile_id <= 19 && tile_id != 16,
+              "lsk_gemm_select: tile id %d not in [-1, 19] (16, the four-wave 256x256 tile, was removed)", tile_id);
+  lsk::g_force_tile = ((tile_id >= 6 && tile_id <= 11) || tile_id == 14 || tile_id == 15 || tile_id == 19) ? 5 : tile_id;
+  lsk::g_gemv_mid = tile_id == 14 ? 1 : (tile_id == 15 ? 2 : (tile_id == 19 ? 3 : 0));
   lsk::g_gemv_variant = (tile_id == 6 || tile_id == 7) ? tile_id - 5 : 0;
   lsk::g_row_rpw = (tile_id >= 8 && tile_id <= 11) ? (1 << (tile_id - 8)) : 0;
   return LSK_OK;

@@ -11,6 +11,7 @@ namespace lsk {
 int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                 const EpiParams& ep, hipStream_t s);
 bool gemm_takes_pp(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int64_t lda);
+bool gemm_takes_skinny(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int64_t lda);
 }  // namespace lsk
 
 namespace {
@@ -759,7 +760,10 @@ extern "C" int lsk_gemm_reads_row_pairs(int64_t M, int64_t N, int64_t K) {
   // rows are kp bytes apart, with the calling thread's tile selection
   if (M <= 0 || N <= 0 || K <= 0 || K % 16 != 0) return 0;
   const int64_t kp = (K + 63) / 64 * 64;
-  return lsk::gemm_takes_pp((const int8_t*)(uintptr_t)256, kp, M, N, K, kp) ? 1 : 0;
+  return (lsk::gemm_takes_pp((const int8_t*)(uintptr_t)256, kp, M, N, K, kp) ||
+          lsk::gemm_takes_skinny((const int8_t*)(uintptr_t)256, kp, M, N, K, (K + 15) / 16 * 16))
+             ? 1
+             : 0;
 }
 
 extern "C" int lsk_quant8_dyn_variant(int v) {
@@ -810,6 +814,11 @@ extern "C" int lsk_linear_dyn(const float* x, int64_t M, int64_t K, int64_t ldx,
   // the weight's row-pair copy with the quantised rows' row-pair layout
   if (pair && w_pairs && lsk::gemm_takes_pp(w_pairs, kp, M, N, K, kp)) {
     ep.pairs = 3;
+    return lsk::launch_gemm(q, ldq, w_pairs, kp, M, N, K, ep, s);
+  }
+  // decode rows: the skinny GEMV streams the weight's row-pair copy
+  if (!pair && w_pairs && lsk::gemm_takes_skinny(w_pairs, kp, M, N, K, ldq)) {
+    ep.pairs = 2;
     return lsk::launch_gemm(q, ldq, w_pairs, kp, M, N, K, ep, s);
   }
   return lsk::launch_gemm(q, ldq, w, ldw, M, N, K, ep, s);

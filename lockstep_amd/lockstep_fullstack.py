@@ -56,8 +56,8 @@ def w8a8_matmul(x, W8, ws, bias=None, out_dtype=None, rowchunk: int = 0):
         return torch.zeros(*shp[:-1], N, dtype=odt, device=x.device)
     w = W8 if W8.stride(-1) == 1 else W8.contiguous()
     # prefill row counts run the GEMM on tiles that read the weight's row-pair copy (made once per
-    # weight and held by it while it is unchanged, only when the GEMM at this row count reads it);
-    # decode row counts stream W8 itself
+    # weight and held by it while it is unchanged, only when the GEMM at this row count reads it),
+    # and so do 5..32 rows of a wide weight (the skinny decode GEMV); other decode rows stream W8
     wp = ops.row_pairs_of(w, x2.shape[0]) if w.dtype == torch.int8 else None
     y = ops.w8a8_matmul(x2, w, ws, bias, L.EPI_V21, L.LSK_F32 if want64 else _OUT[odt], w_pairs=wp)
     if want64:

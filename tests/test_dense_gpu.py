@@ -244,6 +244,58 @@ def test_decode_w8a8_rows(M, N, K, xdt):
             assert np.array_equal(bits(y), want), (order, b is not None, name)
 
 
+@pytest.mark.parametrize("M", [1, 4, 5, 8, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [(1000, 4096), (77, 2880), (3584, 3584), (33, 48), (1001, 1040), (520, 14336),
+                                 (4100, 64), (16, 4096)])
+def test_skinny_gemv_parity(M, N, K):
+    """The skinny decode GEMV (activation rows staged in LDS, weight rows streamed into the MFMA B
+    operand) forced for every M it fits (tile 19), reading the weight row-major and as its row-pair
+    copy: V21 with bias and bf16 out, V2 with binary32 out, RAW int32 and POW2 with per-row
+    exponents, against the oracle; K tails (K % 64 != 0), partial 16-row groups, an all-zero
+    activation row."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import ops
+    say("skinny", M, N, K)
+    if M * ((K + 1023) // 1024 * 1024 + 16) > 160 * 1024:
+        pytest.skip("A does not fit in LDS: the skinny GEMV is not taken at this shape")
+    r = _rng(7 * M + 11 * N + K)
+    a8 = r.integers(-127, 128, (M, K), dtype=np.int8)
+    if M > 2:
+        a8[M - 2] = 0
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    asc = r.uniform(1e-3, 1e-2, M).astype(F32)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    bias = (r.standard_normal(N) * 0.1).astype(F32)
+    erow = r.integers(-20, 20, M).astype(np.int32)
+    acc = C.int_mm(a8, W8.T)
+    ad, Wd = to_dev(a8), to_dev(W8)
+    Wp = ops.pack_row_pairs(Wd)
+    # x whose row quant reproduces rows of a8 scaled: the row-pair copy is read through w8a8_matmul
+    x = (r.standard_normal((M, K)) * 2).astype(F32)
+    q, asc_q = C.rowquant(x)
+    accq = C.int_mm(q, W8.T)
+    L.call("lsk_gemm_select", 19)
+    try:
+        y = ops.gemm(ad, Wd, L.EPI_RAW, L.LSK_I32)
+        assert np.array_equal(bits(y), acc), "raw"
+        y = ops.gemm(ad, Wd, L.EPI_V21, L.LSK_BF16, asc=to_dev(asc), ws=to_dev(ws), bias=to_dev(bias))
+        assert np.array_equal(bits(y), C.epilogue_v21(acc, ws, asc, bias, "bf16")), "v21"
+        y = ops.gemm(ad, Wd, L.EPI_V2, L.LSK_F32, asc=to_dev(asc), ws=to_dev(ws))
+        assert np.array_equal(bits(y), f32_bits(C.epilogue_v2(acc, ws, asc, None, "f32"))), "v2"
+        y = ops.gemm(ad, Wd, L.EPI_POW2, L.LSK_F32, erow=to_dev(erow), shift=3)
+        with np.errstate(over="ignore"):
+            ref = C.dequant_pow2(acc, erow[:, None].astype(np.int64) + 3)
+        assert np.array_equal(bits(y), f32_bits(ref)), "pow2"
+        for wp in (None, Wp):
+            y = ops.w8a8_matmul(to_dev(x), Wd, to_dev(ws), to_dev(bias), L.EPI_V21, L.LSK_BF16, w_pairs=wp)
+            assert np.array_equal(bits(y), C.epilogue_v21(accq, ws, asc_q, bias, "bf16")), ("w8a8 v21", wp is None)
+            y = ops.w8a8_matmul(to_dev(x), Wd, to_dev(ws), None, L.EPI_V2, L.LSK_F32, w_pairs=wp)
+            assert np.array_equal(bits(y), f32_bits(C.epilogue_v2(accq, ws, asc_q, None, "f32"))), ("w8a8 v2",
+                                                                                                  wp is None)
+    finally:
+        L.call("lsk_gemm_select", -1)
+
+
 @pytest.mark.parametrize("tile", [1, 2, 3, 4, 12, 13, 17, 18])
 def test_pow2_whole_tile_epilogue_exponent_range(tile):
     """The POW2 epilogue of whole ping-pong / four-wave tiles (binary32 out, per-row exponents,
@@ -365,7 +417,7 @@ def test_config2_prefill_rows_and_chunk_invariance(which, seed):
     assert torch.equal(chunks.view(torch.int16), y.view(torch.int16))
 
 
-@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 17, 18])
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 12, 13, 14, 15, 17, 18, 19])
 @pytest.mark.parametrize("M,N,K", [(300, 1000, 2048), (129, 257, 640), (512, 520, 2880), (64, 64, 16),
                                    (1, 1000, 14336), (3, 77, 2880), (4, 300, 1040), (8, 1000, 4096),
                                    (17, 77, 2880), (32, 520, 14336), (5, 33, 48), (24, 32800, 320),

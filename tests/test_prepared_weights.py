@@ -10,9 +10,15 @@ from lockstep_amd import ops
 
 def test_gemm_row_pair_query():
     lib = L.load()
-    # decode and mid row counts stream W8 or use the register-staged tile: no copy is read
-    for M in (1, 8, 32, 64, 128):
+    # one activation row streams W8 whole rows; mid row counts use the register-staged tile: no copy
+    for M in (1, 4, 64, 128):
         assert lib.lsk_gemm_reads_row_pairs(M, 28672, 4096) == 0, M
+    # decode rows of wide weights whose activations fit in LDS: the skinny GEMV streams the copy
+    for M, N, K in ((8, 28672, 4096), (32, 28672, 4096), (16, 14336, 4096)):
+        assert lib.lsk_gemm_reads_row_pairs(M, N, K) == 1, (M, N, K)
+    # narrow weights stream whole rows through LDS; 32 rows of K = 14336 exceed the LDS
+    for M, N, K in ((16, 3584, 3584), (8, 4096, 14336), (32, 16384, 14336)):
+        assert lib.lsk_gemm_reads_row_pairs(M, N, K) == 0, (M, N, K)
     # prefill row counts on the ping-pong tiles read it
     for M, N, K in ((2048, 28672, 4096), (2048, 4096, 14336), (8192, 37888, 3584), (8192, 3584, 18944)):
         assert lib.lsk_gemm_reads_row_pairs(M, N, K) == 1, (M, N, K)
@@ -45,16 +51,18 @@ def counting_pack(monkeypatch):
 
 def test_130_dense_weights_pack_once(counting_pack):
     """A model's worth of distinct dense weights (130) cycled twice through the prefill path: each
-    copy is made on the first pass and reused on the second; decode row counts make none."""
-    ws = [torch.zeros((512, 256), dtype=torch.int8) for _ in range(130)]
+    copy is made on the first pass and reused on the second (decode rows that read it share the same
+    copy); one activation row makes none."""
+    ws = [torch.zeros((8192, 64), dtype=torch.int8) for _ in range(130)]
     for w in ws:
-        assert ops.row_pairs_of(w, 32) is None
+        assert ops.row_pairs_of(w, 1) is None
     assert counting_pack == []
     first = [ops.row_pairs_of(w, 2048) for w in ws]
     assert len(counting_pack) == 130 and all(p is not None for p in first)
     second = [ops.row_pairs_of(w, 2048) for w in ws]
     assert len(counting_pack) == 130
     assert all(a is b for a, b in zip(first, second))
+    assert all(ops.row_pairs_of(w, 32) is p for w, p in zip(ws, first)) and len(counting_pack) == 130
     # views of the same storage (the reference's b8 = W8.t() turned back) share the copy
     assert ops.row_pairs_of(ws[0].t().t(), 2048) is first[0]
     # an in-place update re-makes that weight's copy only
