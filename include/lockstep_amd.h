@@ -498,7 +498,7 @@ typedef struct {
   uint16_t* w_out;               /* [T, k] bf16 */
   /* Kernel choice for this call only (no reference counterpart; results are the same bits either
    * way): 0 keeps the calling thread's lsk_moe_select / lsk_moe_mx_select settings; select = v + 2
-   * applies lsk_moe_select(v) (v in [-1, 6]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
+   * applies lsk_moe_select(v) (v in [-1, 7]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
    * (v in [0, 2]) to this call, leaving the thread's settings as they were. */
   int select;
   int mx_select;
@@ -586,8 +586,10 @@ int lsk_moe_fuse_route(int on);
  * tile (the dense kernel's tile: eight waves of 64x128, a four-stage ring, one block per CU, its own
  * 256-row tile table) in a persistent kernel, one block per CU walking the tiles, the next tile's
  * first stages loaded under the current tile's epilogue (K >= 384; 6 below otherwise).  6: the same
- * tile, one block per tile.  The choice applies to the calling host thread's later launches only
- * (thread-local). */
+ * tile, one block per tile.  7: the skinny grouped GEMM (a block stages up to 32 of an expert's
+ * activation rows in LDS and streams its weight rows into the MFMA operand; int8 experts without
+ * rotation, T <= 64, H, I <= 4096; the default from 2 to 64 tokens).  The choice applies to the
+ * calling host thread's later launches only (thread-local). */
 int lsk_moe_select(int variant);
 
 /* Tuning control with no counterpart in the reference: the main loop of the grouped MXFP4

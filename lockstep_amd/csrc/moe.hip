@@ -28,7 +28,7 @@ constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
 constexpr int kBM = lsk::kMoeBM;
 constexpr int kBM2 = 256;  // rows per tile of the 256 x 256 expert tiles (their own tile table)
 thread_local int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV,
-                       // 3 the 128x256 tile on the four-wave main loop
+                       // 3 the 128x256 tile on the four-wave main loop, 7 the skinny grouped GEMM
 thread_local int g_rowq1 = 1;       // one-token layers from logits: router + row quant + gate/up GEMV in one launch
 thread_local int g_moe_w4 = 0;      // the ping-pong tile: 0 128x256 eight-wave ping-pong, 1 128x256 four waves,
                                     // 2 128x256 with 128-byte K stages, 3 256x256 (eight waves, four-stage ring)
@@ -1330,6 +1330,150 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemmArgs a, uint16_t* 
   }
 }
 
+// Few rows per expert (decode token counts), the weights streamed by the MFMA: a block takes
+// GPB groups of 16 weight rows of one expert tile (MODE 0: rows 0 .. 2N-1, gate rows then up
+// rows, so gu column = weight row; MODE 1: the N output columns); the KW waves of a group split
+// its K steps.  Per chunk of up to MT x 16 of the tile's rows: the rows' sources, row scales,
+// routing weights and slots go to LDS first; then the A rows (gathered by token for MODE 0) are
+// copied into LDS by direct loads (1 KB of a row per instruction, zeros past K, row stride ldsk =
+// a multiple of 1 KB plus 16 bytes) together with each wave's first D weight steps, and a wait
+// for everything but those.  Lane l then streams 16 bytes of weight row g * 16 + l % 16 at K-group
+// l / 16 of every 64-byte step (PAIRS: the expert's row-pair copy, whole 128-byte lines per
+// instruction) into the v_mfma_i32_16x16x64_i8 B operand, D steps in flight, the A fragments
+// read from LDS one step ahead.  The K-slices' exact int32 sums are added in LDS; the group's
+// first wave applies the epilogue of moe_gemv_kernel element by element: MODE 0 the bias-added
+// gate / up values into gu, MODE 1 the routing-weighted slot rows.  Rows past the chunk read a
+// clamped staged row and multiply zeros.
+template <int MODE, int MT, int D, bool PAIRS>
+__global__ __launch_bounds__(1024) void moe_skinny_kernel(MoeGemmArgs a, uint16_t* __restrict__ gu, int gpb, int kw,
+                                                          int sets, int ldsk) {
+  extern __shared__ __attribute__((aligned(16))) char smem_sk[];
+  constexpr int CR = MT * 16;  // rows per chunk
+  const int lane = threadIdx.x & 63, wave = wave_id(), nw = blockDim.x >> 6, tid = threadIdx.x;
+  const int mt = blockIdx.x / sets, gs = blockIdx.x - (blockIdx.x / sets) * sets;
+  if (mt >= a.tiles[0]) return;  // the whole block leaves
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + kBM);
+  const int K = a.K, steps = (K + 63) >> 6;
+  const int NWR = MODE == 0 ? 2 * a.N : a.N;  // weight rows
+  const int G = (NWR + 15) >> 4;
+  const int g = gs * gpb + wave / kw;
+  const int ks = wave - (wave / kw) * kw;
+  const int sps = (steps + kw - 1) / kw;
+  const int s0 = ks * sps;
+  const int nst = g < G ? max(0, min(steps, s0 + sps) - s0) : 0;
+  const int col = lane & 15, kg = lane >> 4;
+  const int n = g * 16 + col;
+  const bool mine = ks == 0 && g < G && n < NWR;
+  // this lane's column operands
+  const float* wsp = (const float*)a.ws_ptrs[e];
+  const float* bp = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  const __amdgpu_buffer_rsrc_t rcs = lsk::make_rsrc(wsp, 4 * (int64_t)NWR);
+  const __amdgpu_buffer_rsrc_t rcb = lsk::make_rsrc(bp, bp ? 4 * (int64_t)NWR : 0);
+  const float c_ws = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcs, mine ? (uint32_t)(4 * n) : lsk::kOob, 0, 0));
+  const float c_b = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcb, mine ? (uint32_t)(4 * n) : lsk::kOob, 0, 0));
+  // the chunk's row operands in LDS past the A rows (and past the reduction area)
+  const int arows = CR * ldsk;
+  int* r_src = (int*)(smem_sk + max(arows, nw * MT * 1024));
+  float* r_asc = (float*)(r_src + CR);
+  float* r_w = r_asc + CR;
+  int* r_dst = (int*)(r_w + CR);
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)a.w_ptrs[e], a.w_bytes);
+  const uint32_t wrow = n < NWR ? (uint32_t)(PAIRS ? (n >> 1) * 2 * a.ldw + (n & 1) * 64 : n * a.ldw) : lsk::kOob;
+  const uint32_t wbase = (g < G && n < NWR) ? wrow + (uint32_t)(PAIRS ? s0 * 128 + kg * 16 : s0 * 64 + kg * 16)
+                                            : lsk::kOob;
+  constexpr uint32_t kStep = PAIRS ? 128 : 64;
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+  const int cpr = (K + 1023) >> 10;
+  for (int q0 = p0; q0 < p1; q0 += CR) {
+    const int nr = min(CR, p1 - q0);
+    if (q0 > p0) __syncthreads();  // the previous chunk's LDS reads are done
+    if (tid < nr) {
+      const int p = q0 + tid;
+      const int src = MODE == 0 ? a.row_tok[p] : p;
+      r_src[tid] = src;
+      r_asc[tid] = a.a_scale[src];
+      if (MODE == 1) {
+        r_w[tid] = a.row_w ? a.row_w[p] : 1.0f;
+        r_dst[tid] = a.row_dst ? a.row_dst[p] : p;
+      }
+    }
+    __syncthreads();
+    // A rows into LDS, then this wave's first D weight steps
+    for (int c = wave; c < nr * cpr; c += nw) {
+      const int r = c / cpr, j = c - (c / cpr) * cpr;
+      const int kb = j * 1024 + lane * 16;
+      const uint32_t off = kb < K ? (uint32_t)(r_src[r] * a.lda + kb) : lsk::kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(smem_sk + r * ldsk + j * 1024), 16, off, 0, 0, 0);
+    }
+    v4i w[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+      w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, u < nst ? wbase + u * kStep : lsk::kOob,
+                                                                           0, 2 /* non-temporal */));
+    lsk::compiler_fence();
+    lsk::wait_vm<D>();
+    __syncthreads();
+    v4i acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = lsk::zero4();
+    if (nst > 0) {
+      const char* arow[MT];
+      bool alive[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int r = t * 16 + col;
+        alive[t] = r < nr;
+        arow[t] = smem_sk + (r < nr ? r : nr - 1) * ldsk + s0 * 64 + kg * 16;
+      }
+      for (int s = 0; s < nst; s += D) {
+        v4i af[2][MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) af[0][t] = *(const v4i*)(arow[t] + s * 64);
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+          if (u + 1 < D) {
+            const int st = s + u + 1 < nst ? s + u + 1 : 0;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) af[(u + 1) & 1][t] = *(const v4i*)(arow[t] + st * 64);
+          }
+#pragma unroll
+          for (int t = 0; t < MT; ++t) acc[t] = lsk::mfma_i8(alive[t] ? af[u & 1][t] : lsk::zero4(), w[u], acc[t]);
+          const int nx = s + u + D;
+          w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rw, nx < nst ? wbase + nx * kStep : lsk::kOob, 0, 2 /* non-temporal */));
+        }
+      }
+    }
+    if (kw > 1) {
+      __syncthreads();  // every wave is past its last A read: the partial sums reuse the LDS
+      v4i* red = (v4i*)smem_sk;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) red[(wave * MT + t) * 64 + lane] = acc[t];
+      __syncthreads();
+      if (ks == 0)
+        for (int j = 1; j < kw; ++j)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) acc[t] += red[((wave + j) * MT + t) * 64 + lane];
+    }
+    if (mine) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = t * 16 + kg * 4 + r;
+          if (m < nr) {
+            float yv = bfr(f32_mul(f32_mul((float)acc[t][r], c_ws), r_asc[m]));
+            if (bp) yv = bfr(f32_add(yv, c_b));
+            if (MODE == 0) gu[(int64_t)(q0 + m) * NWR + n] = f32_to_bf16(yv);
+            else a.y[(int64_t)r_dst[m] * a.N + n] = f32_to_bf16(f32_mul(r_w[m], yv));
+          }
+        }
+    }
+  }
+}
+
 // The first launch of a one-token int8 layer routed from its logits: the router, the row quant of x
 // and the gate/up GEMV in one kernel.  Every wave routes the token itself (route_select: the same
 // arithmetic as router_topk_kernel) and quantises the whole row of x in registers (its lanes hold
@@ -1821,6 +1965,14 @@ constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
 // operand bytes per MFMA.
 static bool moe_uses_pp256(int64_t, int64_t) { return g_moe_w4 == 3 || g_moe_w4 == 4; }
 
+// Whether the int8 grouped GEMMs of a layer run on moe_skinny_kernel: by size from 2 to kGemvMaxT
+// tokens (Qwen3-30B-A3B on MI355X ... ), or for up to kGemvMaxT tokens when chosen
+// (lsk_moe_select(7)); int8 experts without rotation and H, I <= 4096 (a chunk of 32 rows in LDS).
+static bool moe_takes_skinny(int64_t T, int rb, int mx, int64_t H, int64_t I) {
+  if (rb != 0 || mx || T > kGemvMaxT || H > 4096 || I > 4096) return false;
+  return g_moe_force == 7 || (g_moe_force < 0 && T >= 2);
+}
+
 constexpr int64_t kMxGemvMaxT = 24;   // ... with MXFP4 experts
 constexpr int64_t kMx2GemvMaxT = 16;  // ... with MXFP4 experts and block-scaled activations
 
@@ -1986,6 +2138,43 @@ int launch_moe_gemv(const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint16_
   if (T <= 2) return launch_moe_gemv_mr<MODE, 2>(ga, max_tiles, gu, s, name);
   if (T <= 4) return launch_moe_gemv_mr<MODE, 4>(ga, max_tiles, gu, s, name);
   return launch_moe_gemv_mr<MODE, 8>(ga, max_tiles, gu, s, name);
+}
+
+// moe_skinny_kernel's launch: chunks of 16 rows up to 16 tokens (no expert gets more rows than
+// there are tokens), else 32; eight groups of 16 weight rows per block, two waves per group when
+// K has at least 16 steps.  A (a chunk's rows) and the reduction share the LDS, the rows'
+// operands follow.
+template <int MODE>
+int launch_moe_skinny(const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint16_t* gu, hipStream_t s,
+                      const char* name) {
+  const int K = ga.K, steps = (K + 63) / 64;
+  const int MT = T <= 16 ? 1 : 2, CR = 16 * MT;
+  const int ldsk = (K + 1023) / 1024 * 1024 + 16;
+  const int NWR = MODE == 0 ? 2 * ga.N : ga.N;
+  const int G = (NWR + 15) / 16;
+  const int gpb = 8, kw = steps >= 16 ? 2 : 1, nw = gpb * kw;
+  const int sets = (G + gpb - 1) / gpb;
+  const size_t smem = (size_t)std::max(CR * ldsk, nw * MT * 1024) + (size_t)CR * 16;
+  LSK_REQUIRE(smem <= 160 * 1024, "%s: K=%d too long for the skinny grouped GEMM", name, K);
+  const int64_t blocks = max_tiles * sets;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  const bool pairs = (ga.pairs & 2) != 0;
+#define LSK_MSK(MTV, PV)                                                                                        \
+  {                                                                                                             \
+    auto kern = moe_skinny_kernel<MODE, MTV, 8, PV>;                                                            \
+    if (smem > 65536 &&                                                                                         \
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) \
+      return lsk::set_error("%s: cannot reserve LDS", name), LSK_ERR_HIP;                                      \
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * nw), smem, s, ga, gu, gpb, kw, sets, ldsk);      \
+    return lsk::check_launch(name);                                                                            \
+  }
+  if (MT == 1) {
+    if (pairs) LSK_MSK(1, true) else LSK_MSK(1, false)
+  } else {
+    if (pairs) LSK_MSK(2, true) else LSK_MSK(2, false)
+  }
+#undef LSK_MSK
 }
 
 template <int MODE>
@@ -2186,8 +2375,8 @@ extern "C" int lsk_moe_fuse_route(int on) {
 }
 
 extern "C" int lsk_moe_select(int variant) {
-  LSK_REQUIRE(variant >= -1 && variant <= 6, "lsk_moe_select: variant %d not in [-1, 6]", variant);
-  g_moe_force = variant >= 4 ? 1 : variant;
+  LSK_REQUIRE(variant >= -1 && variant <= 7, "lsk_moe_select: variant %d not in [-1, 7]", variant);
+  g_moe_force = (variant >= 4 && variant <= 6) ? 1 : variant;
   g_moe_w4 = variant == 3 ? 1 : (variant == 4 ? 2 : (variant == 5 ? 3 : (variant == 6 ? 4 : 0)));
   return LSK_OK;
 }
@@ -2205,12 +2394,13 @@ static bool moe_reads_pair_weights(int64_t T, int k, int64_t E, int64_t H, int64
   const int64_t R = T * k;
   const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= 16 * E;
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
-  const bool use_gemv = gemv_ok && H <= 4096 && I <= 4096;
-  return use_pp && !use_gemv && (g_moe_w4 == 0 || g_moe_w4 == 3 || g_moe_w4 == 4);
+  const bool skinny = moe_takes_skinny(T, rb, 0, H, I);
+  const bool use_gemv = gemv_ok && H <= 4096 && I <= 4096 && !skinny;
+  return skinny || (use_pp && !use_gemv && (g_moe_w4 == 0 || g_moe_w4 == 3 || g_moe_w4 == 4));
 }
 
 extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int select) {
-  if (T <= 0 || k < 1 || E < 1 || H <= 0 || I <= 0 || select < 0 || select > 8) return 0;
+  if (T <= 0 || k < 1 || E < 1 || H <= 0 || I <= 0 || select < 0 || select > 9) return 0;
   const int force = g_moe_force, w4 = g_moe_w4;
   if (select) lsk_moe_select(select - 2);
   const bool r = moe_reads_pair_weights(T, k, E, H, I, rot_blk);
@@ -2221,8 +2411,8 @@ extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, i
 
 extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(a, "lsk_moe_forward: null args");
-  LSK_REQUIRE(a->select >= 0 && a->select <= 8 && a->mx_select >= 0 && a->mx_select <= 3,
-              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 8] / [0, 3]", a->select, a->mx_select);
+  LSK_REQUIRE(a->select >= 0 && a->select <= 9 && a->mx_select >= 0 && a->mx_select <= 3,
+              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 9] / [0, 3]", a->select, a->mx_select);
   if (a->select == 0 && a->mx_select == 0) return moe_forward_call(a, stream);
   // this call's kernel choice, the thread's own restored afterwards
   const int force = g_moe_force, w4 = g_moe_w4, mxv = lsk::mx_variant();
@@ -2298,9 +2488,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // tokens, 16 rows per expert, 187 us against 225 us on the 128x128 register-staged tile, level at
   // 2048 tokens); the register-staged tile below that
   const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= 16 * E;
-  // the grouped GEMV for decode token counts (whole weight rows streamed once per tile)
+  // decode token counts: the skinny grouped GEMM (activation rows in LDS, weight rows streamed into
+  // the MFMA) from 2 tokens, the grouped GEMV (whole weight rows streamed once per tile, v_dot4)
+  // for one token or when chosen
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
-  const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096;
+  const bool use_skinny = moe_takes_skinny(T, rb, mx, H, I);
+  const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096 && !use_skinny;
   // (MX experts: the GEMV re-streams each expert's weights per 4-row pass, so past about 24 tokens
   // the tiled kernels win: GPT-OSS-20B on MI355X, T = 24 242 vs 276 us, T = 48 368 vs 278 us)
   const bool use_mx_gemv = gemv_ok && mx == 1 && (g_moe_force == 2 || T <= kMxGemvMaxT) && H <= 8192 && I <= 8192;
@@ -2310,10 +2503,10 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
   // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
   // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
-  const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && I % 64 == 0 &&
+  const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && !use_skinny && I % 64 == 0 &&
                          (g_moe_w4 == 0 || g_moe_w4 == 3 || g_moe_w4 == 4);
   // the 256 x 256 expert tiles (their own tile table) for the ping-pong GEMMs
-  const bool pp256 = use_pp && !mx && !use_gemv && moe_uses_pp256(R, E);
+  const bool pp256 = use_pp && !mx && !use_gemv && !use_skinny && moe_uses_pp256(R, E);
   // the experts' row-pair weight copies on the same tiles, when the caller has them
   const bool pair_w = !mx && moe_reads_pair_weights(T, k, E, H, I, rb) && a->w13_pair_ptrs && a->w2_pair_ptrs;
 
@@ -2449,6 +2642,14 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     }
 #undef LSK_RG1
     if ((rc = lsk::check_launch("moe_route_gemv1_kernel"))) return rc;
+  } else if (use_skinny) {
+    if (pair_w) {
+      g1.w_ptrs = a->w13_pair_ptrs;
+      g1.ldw = (H + 63) / 64 * 64;
+      g1.w_bytes = 2 * I * g1.ldw;
+      g1.pairs |= 2;
+    }
+    if ((rc = launch_moe_skinny<0>(g1, w.max_tiles, T, w.gu, s, "moe_skinny_kernel<gate_up>"))) return rc;
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<0>(g1, w.max_tiles, T, w.gu, s, "moe_gemv_kernel<gate_up>"))) return rc;
   } else if (use_pp) {
@@ -2467,7 +2668,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
     return rc;
   }
-  if (use_gemv || use_mx_gemv) {
+  if (use_gemv || use_skinny || use_mx_gemv) {
     const int per = (int)((I + 1023) / 1024);
     const dim3 grid((unsigned)R), blk(1024);
 #define LSK_ACTQ(P)                                                                                             \
@@ -2542,6 +2743,14 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     else LSK_DC(2);
 #undef LSK_DC
     return lsk::check_launch("moe_down_combine1_kernel");
+  } else if (use_skinny) {
+    if (pair_w) {
+      g2.w_ptrs = a->w2_pair_ptrs;
+      g2.ldw = (I + 63) / 64 * 64;
+      g2.w_bytes = H * g2.ldw;
+      g2.pairs |= 2;
+    }
+    if ((rc = launch_moe_skinny<1>(g2, w.max_tiles, T, nullptr, s, "moe_skinny_kernel<down>"))) return rc;
   } else if (use_gemv) {
     if ((rc = launch_moe_gemv<1>(g2, w.max_tiles, T, nullptr, s, "moe_gemv_kernel<down>"))) return rc;
   } else if (use_pp) {

@@ -328,9 +328,10 @@ def kernel_choice(moe=None, mx=None):
     (lsk_moe_args.select / mx_select; no reference counterpart, the same bits either way): moe as
     lsk_moe_select's variant (-1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV, 3 the
     four-wave tile, 4 128-byte K stages, 5 the persistent 256x256 tile, 6 the 256x256 tile one per
-    block), mx as lsk_moe_mx_select's (0, 1, 2); None keeps the calling thread's setting.  Scoped to this Python thread and the with-block."""
-    if moe is not None and not -1 <= moe <= 6:
-        raise ValueError("kernel_choice: moe=%r not in [-1, 6]" % (moe,))
+    block, 7 the skinny grouped GEMM), mx as lsk_moe_mx_select's (0, 1, 2); None keeps the calling
+    thread's setting.  Scoped to this Python thread and the with-block."""
+    if moe is not None and not -1 <= moe <= 7:
+        raise ValueError("kernel_choice: moe=%r not in [-1, 7]" % (moe,))
     if mx is not None and not 0 <= mx <= 2:
         raise ValueError("kernel_choice: mx=%r not in [0, 2]" % (mx,))
     prev = getattr(_CHOICE, "v", (0, 0))

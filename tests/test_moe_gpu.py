@@ -193,12 +193,13 @@ def test_moe_multi_chunk_dispatch(T, E, k):
     _run_case(T, E, k, 128, 64, seed=11 + T)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7])
 def test_moe_grouped_gemm_variants(variant):
     """Every grouped-GEMM kernel (register-staged 128x128 tile, ping-pong 128x256 tile, the
     decode GEMV, the 128x256 tile on four waves, the ping-pong tile with 128-byte K stages, the
-    256x256 tile persistent and one tile per block) gives the oracle's bits: skewed routing with multi-tile experts (the GEMV takes
-    their rows eight at a time), empty experts, a bias and SwiGLU-OAI; an odd number of routed rows
+    256x256 tile persistent and one tile per block, the skinny grouped GEMM) gives the oracle's
+    bits: skewed routing with multi-tile experts (the GEMV takes their rows eight at a time, the
+    skinny kernel 32 at a time), empty experts, a bias and SwiGLU-OAI; an odd number of routed rows
     (the down tiles' row-pair operand ends in a half pair)."""
     from lockstep_amd import _lib as L
     L.call("lsk_moe_select", variant)
@@ -214,6 +215,27 @@ def test_moe_grouped_gemm_variants(variant):
             _run_case(1100, 6, 3, 448, 400, seed=19, bias=True, act="swigluoai")
     finally:
         L.call("lsk_moe_select", -1)
+
+
+@pytest.mark.parametrize("pairs", [True, False])
+@pytest.mark.parametrize("T", [2, 3, 9, 16, 17, 40, 64])
+def test_moe_skinny_grouped(T, pairs):
+    """The skinny grouped GEMM (the default for int8 layers from 2 to 64 tokens), reading the experts'
+    row-pair copies and their row-major weights: Zipf-skewed routing over 16 experts (some empty),
+    H and I not multiples of 64 (partial last K steps of both projections), a bias with SwiGLU-OAI,
+    and every token routed to the same two experts (40 / 64 rows per expert: chunks of 32 rows, a
+    partial last chunk), all against the oracle."""
+    from lockstep_amd import moe_ref as MR
+    prev = MR.ROW_PAIRS
+    MR.ROW_PAIRS = pairs
+    try:
+        _run_case(T, 16, 4, 256, 128, seed=40 + T)
+        _run_case(T, 8, 3, 272, 208, seed=50 + T, bias=True, act="swigluoai")
+        idx = np.tile(np.array([[3, 1]]), (T, 1)).astype(np.int64)
+        w = C.bf16_bits(np.tile(np.array([[0.625, 0.375]], F32), (T, 1)))
+        _run_case(T, 4, 2, 320, 192, seed=60 + T, routing_override=(idx, w))
+    finally:
+        MR.ROW_PAIRS = prev
 
 
 @pytest.mark.parametrize("variant", [5, 6])
@@ -237,7 +259,7 @@ def test_moe_per_call_kernel_choice():
     from lockstep_amd import moe_ref as MR
     L.call("lsk_moe_select", 2)            # the thread: the decode GEMV
     try:
-        for v in (0, 1, 3, 4, 5, 6, -1):
+        for v in (0, 1, 3, 4, 5, 6, 7, -1):
             with MR.kernel_choice(moe=v):
                 _run_case(300, 12, 4, 256, 192, seed=13)
         _run_case(40, 8, 3, 256, 192, seed=16)   # the thread's setting again
