@@ -578,8 +578,9 @@ int lsk_moe_fuse_route(int on);
  * 128x256 tile (1), on the grouped GEMV (2: whole weight rows streamed once against up to 8
  * rows per expert at a time; taken only for int8 experts without rotation, T <= 64 and
  * H, I <= 4096, the tiles otherwise), on the 128x256 tile with the four-wave main loop (3: one wave
- * per SIMD per block, 64x128 wave tiles), or chosen by size (-1, the default: the GEMV where it
- * applies, the ping-pong tile once the routed rows reach 16 E).  MXFP4 experts (H, I <= 8192, no
+ * per SIMD per block, 64x128 wave tiles), or chosen by size (-1, the default: the GEMV for one
+ * token, the skinny grouped GEMM (7) from 2 tokens, the ping-pong tile once the routed rows reach
+ * 16 E; the register-staged tile where neither applies).  MXFP4 experts (H, I <= 8192, no
  * rotation) take the MX GEMV under 2 for T <= 64 and by default for T <= 24 (T <= 16 with
  * block-scaled activations), the MX grouped tiles otherwise.  Results are identical for every
  * choice.  4: the ping-pong tile with 128-byte K stages (one block per CU).  5: the 256x256 ping-pong
@@ -588,9 +589,15 @@ int lsk_moe_fuse_route(int on);
  * first stages loaded under the current tile's epilogue (K >= 384; 6 below otherwise).  6: the same
  * tile, one block per tile.  7: the skinny grouped GEMM (a block stages up to 32 of an expert's
  * activation rows in LDS and streams its weight rows into the MFMA operand; int8 experts without
- * rotation, T <= 64, H, I <= 4096; the default from 2 to 64 tokens).  The choice applies to the
+ * rotation, T <= 256, H, I <= 4096; the default from 2 tokens while the routed rows stay under
+ * 16 E).  The choice applies to the
  * calling host thread's later launches only (thread-local). */
 int lsk_moe_select(int variant);
+
+/* Tuning control with no counterpart in the reference: the skinny grouped GEMM's launch shape --
+ * gpb groups of 16 weight rows per block, kw waves per group splitting K (gpb * kw <= 16); 0 leaves
+ * a parameter to the size rule.  Results are identical.  Thread-local. */
+int lsk_moe_skinny_shape(int gpb, int kw);
 
 /* Tuning control with no counterpart in the reference: the main loop of the grouped MXFP4
  * expert GEMMs (0: direct-to-LDS operand staging with fp4 fragments converted per wave, a

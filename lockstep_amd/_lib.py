@@ -55,6 +55,7 @@ SIGNATURES = {
     "lsk_tree_sum": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lsk_gemm_select": (_I, [_I]),
     "lsk_gemm_skinny_shape": (_I, [_I, _I, _I]),
+    "lsk_moe_skinny_shape": (_I, [_I, _I]),
     "lsk_gemm_fuse_rowquant": (_I, [_I]),
     "lsk_quant8_dyn_single_pass": (_I, [_I]),
     "lsk_quant8_dyn_variant": (_I, [_I]),

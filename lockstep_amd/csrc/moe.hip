@@ -30,6 +30,7 @@ constexpr int kBM2 = 256;  // rows per tile of the 256 x 256 expert tiles (their
 thread_local int g_moe_force = -1;  // tuning control: -1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV,
                        // 3 the 128x256 tile on the four-wave main loop, 7 the skinny grouped GEMM
 thread_local int g_rowq1 = 1;       // one-token layers from logits: router + row quant + gate/up GEMV in one launch
+thread_local int g_msk_gpb = 0, g_msk_kw = 0;  // the skinny grouped GEMM's launch shape (0: by size)
 thread_local int g_moe_w4 = 0;      // the ping-pong tile: 0 128x256 eight-wave ping-pong, 1 128x256 four waves,
                                     // 2 128x256 with 128-byte K stages, 3 256x256 (eight waves, four-stage ring)
 
@@ -1333,17 +1334,18 @@ __global__ __launch_bounds__(256) void moe_gemv_kernel(MoeGemmArgs a, uint16_t* 
 // Few rows per expert (decode token counts), the weights streamed by the MFMA: a block takes
 // GPB groups of 16 weight rows of one expert tile (MODE 0: rows 0 .. 2N-1, gate rows then up
 // rows, so gu column = weight row; MODE 1: the N output columns); the KW waves of a group split
-// its K steps.  Per chunk of up to MT x 16 of the tile's rows: the rows' sources, row scales,
-// routing weights and slots go to LDS first; then the A rows (gathered by token for MODE 0) are
-// copied into LDS by direct loads (1 KB of a row per instruction, zeros past K, row stride ldsk =
-// a multiple of 1 KB plus 16 bytes) together with each wave's first D weight steps, and a wait
-// for everything but those.  Lane l then streams 16 bytes of weight row g * 16 + l % 16 at K-group
-// l / 16 of every 64-byte step (PAIRS: the expert's row-pair copy, whole 128-byte lines per
-// instruction) into the v_mfma_i32_16x16x64_i8 B operand, D steps in flight, the A fragments
-// read from LDS one step ahead.  The K-slices' exact int32 sums are added in LDS; the group's
-// first wave applies the epilogue of moe_gemv_kernel element by element: MODE 0 the bias-added
-// gate / up values into gu, MODE 1 the routing-weighted slot rows.  Rows past the chunk read a
-// clamped staged row and multiply zeros.
+// its K steps.  Per chunk of up to MT x 16 of the tile's rows: each wave first issues its first D
+// weight steps (they depend on nothing), the chunk's row sources go to LDS (MODE 0: the token
+// rows; the wait counts only those, the weights stay in flight), then the A rows are copied into
+// LDS by direct loads (1 KB of a row per instruction, zeros past K, row stride ldsk = a multiple
+// of 1 KB plus 16 bytes) with the rows' scales, routing weights and slots behind them.  Lane l
+// streams 16 bytes of weight row g * 16 + l % 16 at K-group l / 16 of every 64-byte step (PAIRS:
+// the expert's row-pair copy, whole 128-byte lines per instruction) into the
+// v_mfma_i32_16x16x64_i8 B operand, D steps in flight, the A fragments read from LDS one step
+// ahead.  The K-slices' exact int32 sums are added in LDS; the group's first wave applies the
+// epilogue of moe_gemv_kernel element by element: MODE 0 the bias-added gate / up values into
+// gu, MODE 1 the routing-weighted slot rows.  Rows past the chunk read a clamped staged row and
+// multiply zeros.
 template <int MODE, int MT, int D, bool PAIRS>
 __global__ __launch_bounds__(1024) void moe_skinny_kernel(MoeGemmArgs a, uint16_t* __restrict__ gu, int gpb, int kw,
                                                           int sets, int ldsk) {
@@ -1373,7 +1375,7 @@ __global__ __launch_bounds__(1024) void moe_skinny_kernel(MoeGemmArgs a, uint16_
   const __amdgpu_buffer_rsrc_t rcb = lsk::make_rsrc(bp, bp ? 4 * (int64_t)NWR : 0);
   const float c_ws = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcs, mine ? (uint32_t)(4 * n) : lsk::kOob, 0, 0));
   const float c_b = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcb, mine ? (uint32_t)(4 * n) : lsk::kOob, 0, 0));
-  // the chunk's row operands in LDS past the A rows (and past the reduction area)
+  // the chunk's row sources and operands in LDS past the A rows (and past the reduction area)
   const int arows = CR * ldsk;
   int* r_src = (int*)(smem_sk + max(arows, nw * MT * 1024));
   float* r_asc = (float*)(r_src + CR);
@@ -1386,34 +1388,47 @@ __global__ __launch_bounds__(1024) void moe_skinny_kernel(MoeGemmArgs a, uint16_
   constexpr uint32_t kStep = PAIRS ? 128 : 64;
   const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
   const int cpr = (K + 1023) >> 10;
+  lsk::compiler_fence();
   for (int q0 = p0; q0 < p1; q0 += CR) {
     const int nr = min(CR, p1 - q0);
     if (q0 > p0) __syncthreads();  // the previous chunk's LDS reads are done
-    if (tid < nr) {
-      const int p = q0 + tid;
-      const int src = MODE == 0 ? a.row_tok[p] : p;
-      r_src[tid] = src;
-      r_asc[tid] = a.a_scale[src];
-      if (MODE == 1) {
-        r_w[tid] = a.row_w ? a.row_w[p] : 1.0f;
-        r_dst[tid] = a.row_dst ? a.row_dst[p] : p;
-      }
-    }
-    __syncthreads();
-    // A rows into LDS, then this wave's first D weight steps
-    for (int c = wave; c < nr * cpr; c += nw) {
-      const int r = c / cpr, j = c - (c / cpr) * cpr;
-      const int kb = j * 1024 + lane * 16;
-      const uint32_t off = kb < K ? (uint32_t)(r_src[r] * a.lda + kb) : lsk::kOob;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(smem_sk + r * ldsk + j * 1024), 16, off, 0, 0, 0);
-    }
     v4i w[D];
 #pragma unroll
     for (int u = 0; u < D; ++u)
       w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rw, u < nst ? wbase + u * kStep : lsk::kOob,
                                                                            0, 2 /* non-temporal */));
+    if (MODE == 0) {
+      // the token rows of the chunk: loaded behind the weight steps, waited for alone
+      const int src = tid < nr ? a.row_tok[q0 + tid] : 0;
+      lsk::compiler_fence();
+      if (tid < nr) r_src[tid] = src;
+      __syncthreads();
+    }
+    // A rows into LDS, then the rows' operands (needed only by the epilogue)
+    for (int c = wave; c < nr * cpr; c += nw) {
+      const int r = c / cpr, j = c - (c / cpr) * cpr;
+      const int kb = j * 1024 + lane * 16;
+      const int src = MODE == 0 ? r_src[r] : q0 + r;
+      const uint32_t off = kb < K ? (uint32_t)(src * a.lda + kb) : lsk::kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(smem_sk + r * ldsk + j * 1024), 16, off, 0, 0, 0);
+    }
+    float o_asc = 0.0f, o_w = 1.0f;
+    int o_dst = 0;
+    if (tid < nr) {
+      const int p = q0 + tid;
+      o_asc = a.a_scale[MODE == 0 ? r_src[tid] : p];
+      if (MODE == 1) {
+        o_w = a.row_w ? a.row_w[p] : 1.0f;
+        o_dst = a.row_dst ? a.row_dst[p] : p;
+      }
+    }
     lsk::compiler_fence();
-    lsk::wait_vm<D>();
+    lsk::wait_vm<0>();  // A, the rows' operands and the first weight steps
+    if (tid < nr) {
+      r_asc[tid] = o_asc;
+      r_w[tid] = o_w;
+      r_dst[tid] = o_dst;
+    }
     __syncthreads();
     v4i acc[MT];
 #pragma unroll
@@ -1439,7 +1454,8 @@ __global__ __launch_bounds__(1024) void moe_skinny_kernel(MoeGemmArgs a, uint16_
             for (int t = 0; t < MT; ++t) af[(u + 1) & 1][t] = *(const v4i*)(arow[t] + st * 64);
           }
 #pragma unroll
-          for (int t = 0; t < MT; ++t) acc[t] = lsk::mfma_i8(alive[t] ? af[u & 1][t] : lsk::zero4(), w[u], acc[t]);
+          for (int t = 0; t < MT; ++t)
+            acc[t] = lsk::mfma_i8(alive[t] ? af[u & 1][t] : lsk::zero4(), w[u], acc[t]);
           const int nx = s + u + D;
           w[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
                                              rw, nx < nst ? wbase + nx * kStep : lsk::kOob, 0, 2 /* non-temporal */));
@@ -1956,6 +1972,7 @@ struct MoeWs {
 inline int64_t up256(int64_t v) { return (v + 255) / 256 * 256; }
 
 constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
+constexpr int64_t kSkinnyMaxT = 256;  // ... the skinny grouped GEMM
 
 // Whether the ping-pong grouped GEMM runs on the 256 x 256 tiles: only when chosen
 // (lsk_moe_select(5)).  One block per CU there leaves the load latency and the epilogue of a tile
@@ -1965,12 +1982,15 @@ constexpr int64_t kGemvMaxT = 64;  // token counts the grouped GEMV may take
 // operand bytes per MFMA.
 static bool moe_uses_pp256(int64_t, int64_t) { return g_moe_w4 == 3 || g_moe_w4 == 4; }
 
-// Whether the int8 grouped GEMMs of a layer run on moe_skinny_kernel: by size from 2 to kGemvMaxT
-// tokens (Qwen3-30B-A3B on MI355X ... ), or for up to kGemvMaxT tokens when chosen
-// (lsk_moe_select(7)); int8 experts without rotation and H, I <= 4096 (a chunk of 32 rows in LDS).
-static bool moe_takes_skinny(int64_t T, int rb, int mx, int64_t H, int64_t I) {
-  if (rb != 0 || mx || T > kGemvMaxT || H > 4096 || I > 4096) return false;
-  return g_moe_force == 7 || (g_moe_force < 0 && T >= 2);
+// Whether the int8 grouped GEMMs of a layer run on moe_skinny_kernel: by size from 2 tokens up to
+// where the ping-pong tiles take over (16 routed rows per expert) -- Qwen3-30B-A3B on MI355X, graph
+// replays, us at T = 8 / 32 / 64 / 96 / 128 / 192: 51.3 / 65.0 / 85.4 / 113 / 143 / 149 against
+// 56.2 / 94.0 / 129.6 on the grouped GEMV and 196 / 183 / 205 on the register-staged tile; at 256
+// tokens the ping-pong tile 155 against 182 -- or whenever chosen (lsk_moe_select(7)); int8
+// experts without rotation, T <= kSkinnyMaxT, H, I <= 4096 (a chunk of 32 rows in LDS).
+static bool moe_takes_skinny(int64_t T, int k, int64_t E, int rb, int mx, int64_t H, int64_t I) {
+  if (rb != 0 || mx || T > kSkinnyMaxT || H > 4096 || I > 4096) return false;
+  return g_moe_force == 7 || (g_moe_force < 0 && T >= 2 && T * k < 16 * E);
 }
 
 constexpr int64_t kMxGemvMaxT = 24;   // ... with MXFP4 experts
@@ -2005,7 +2025,7 @@ MoeWs moe_layout(char* base, int64_t T, int k, int64_t E, int64_t H, int64_t I, 
   w.asch = (float*)take(R * 4);
   w.slots = (uint16_t*)take(R * H * 2);
   w.xrot = rot_blk > 0 ? (float*)take(T * H * 4) : nullptr;
-  w.gu = T <= kGemvMaxT ? (uint16_t*)take(R * 2 * I * 2) : nullptr;
+  w.gu = T <= std::max(kGemvMaxT, kSkinnyMaxT) ? (uint16_t*)take(R * 2 * I * 2) : nullptr;
   if (wfmt == 2) {
     w.kax = (int32_t*)take(T * (H / 32) * 4);
     w.flagx = (int32_t*)take(T * 4);
@@ -2141,9 +2161,13 @@ int launch_moe_gemv(const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint16_
 }
 
 // moe_skinny_kernel's launch: chunks of 16 rows up to 16 tokens (no expert gets more rows than
-// there are tokens), else 32; eight groups of 16 weight rows per block, two waves per group when
-// K has at least 16 steps.  A (a chunk's rows) and the reduction share the LDS, the rows'
-// operands follow.
+// there are tokens), else 32; up to 64 tokens eight groups of 16 weight rows per block, one wave
+// per group over the whole K, above that four groups of two waves.  (Qwen3-30B-A3B int8 layer on
+// MI355X, graph replays, us at T = 8 / 32 / 64 for gpb x kw reading the row-pair copies: 8 x 1
+// 51.3 / 65.0 / 85.4, 16 x 1 50.2 / 69.2 / 94.5, 4 x 2 50.6 / 67.2 / 87.3, 8 x 2 56.9 / 71.1 /
+// 96.3, 4 x 4 64.2 / 90.0 / 112.6; at T = 96 / 128 / 192: 8 x 1 124.5 / 148.5 / 157.0, 4 x 2
+// 113.3 / 142.8 / 149.5; row-major weights 8-15% slower.)  A (a chunk's rows) and the reduction
+// share the LDS, the rows' operands follow.
 template <int MODE>
 int launch_moe_skinny(const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint16_t* gu, hipStream_t s,
                       const char* name) {
@@ -2152,7 +2176,11 @@ int launch_moe_skinny(const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uint1
   const int ldsk = (K + 1023) / 1024 * 1024 + 16;
   const int NWR = MODE == 0 ? 2 * ga.N : ga.N;
   const int G = (NWR + 15) / 16;
-  const int gpb = 8, kw = steps >= 16 ? 2 : 1, nw = gpb * kw;
+  int kw = T > 64 ? 2 : 1, gpb = T > 64 ? 4 : 8;
+  if (g_msk_kw > 0) kw = g_msk_kw;
+  if (g_msk_gpb > 0) gpb = g_msk_gpb;
+  LSK_REQUIRE(gpb * kw <= 16, "%s: %d x %d waves", name, gpb, kw);
+  const int nw = gpb * kw;
   const int sets = (G + gpb - 1) / gpb;
   const size_t smem = (size_t)std::max(CR * ldsk, nw * MT * 1024) + (size_t)CR * 16;
   LSK_REQUIRE(smem <= 160 * 1024, "%s: K=%d too long for the skinny grouped GEMM", name, K);
@@ -2374,6 +2402,14 @@ extern "C" int lsk_moe_fuse_route(int on) {
   return LSK_OK;
 }
 
+extern "C" int lsk_moe_skinny_shape(int gpb, int kw) {
+  LSK_REQUIRE(gpb >= 0 && kw >= 0 && gpb <= 16 && kw <= 16 && (gpb == 0 || kw == 0 || gpb * kw <= 16),
+              "lsk_moe_skinny_shape: gpb=%d kw=%d (gpb * kw <= 16)", gpb, kw);
+  g_msk_gpb = gpb;
+  g_msk_kw = kw;
+  return LSK_OK;
+}
+
 extern "C" int lsk_moe_select(int variant) {
   LSK_REQUIRE(variant >= -1 && variant <= 7, "lsk_moe_select: variant %d not in [-1, 7]", variant);
   g_moe_force = (variant >= 4 && variant <= 6) ? 1 : variant;
@@ -2394,7 +2430,7 @@ static bool moe_reads_pair_weights(int64_t T, int k, int64_t E, int64_t H, int64
   const int64_t R = T * k;
   const bool use_pp = g_moe_force >= 0 ? (g_moe_force == 1 || g_moe_force == 3) : R >= 16 * E;
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
-  const bool skinny = moe_takes_skinny(T, rb, 0, H, I);
+  const bool skinny = moe_takes_skinny(T, k, E, rb, 0, H, I);
   const bool use_gemv = gemv_ok && H <= 4096 && I <= 4096 && !skinny;
   return skinny || (use_pp && !use_gemv && (g_moe_w4 == 0 || g_moe_w4 == 3 || g_moe_w4 == 4));
 }
@@ -2492,7 +2528,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // the MFMA) from 2 tokens, the grouped GEMV (whole weight rows streamed once per tile, v_dot4)
   // for one token or when chosen
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
-  const bool use_skinny = moe_takes_skinny(T, rb, mx, H, I);
+  const bool use_skinny = moe_takes_skinny(T, k, E, rb, mx, H, I);
   const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096 && !use_skinny;
   // (MX experts: the GEMV re-streams each expert's weights per 4-row pass, so past about 24 tokens
   // the tiled kernels win: GPT-OSS-20B on MI355X, T = 24 242 vs 276 us, T = 48 368 vs 278 us)

@@ -218,22 +218,24 @@ def test_moe_grouped_gemm_variants(variant):
 
 
 @pytest.mark.parametrize("pairs", [True, False])
-@pytest.mark.parametrize("T", [2, 3, 9, 16, 17, 40, 64])
+@pytest.mark.parametrize("T", [2, 3, 9, 16, 17, 40, 64, 96, 200])
 def test_moe_skinny_grouped(T, pairs):
-    """The skinny grouped GEMM (the default for int8 layers from 2 to 64 tokens), reading the experts'
-    row-pair copies and their row-major weights: Zipf-skewed routing over 16 experts (some empty),
-    H and I not multiples of 64 (partial last K steps of both projections), a bias with SwiGLU-OAI,
-    and every token routed to the same two experts (40 / 64 rows per expert: chunks of 32 rows, a
-    partial last chunk), all against the oracle."""
+    """The skinny grouped GEMM (the default for int8 layers from 2 tokens while the routed rows stay
+    under 16 E; chosen here at every size), reading the experts' row-pair copies and their row-major
+    weights: Zipf-skewed routing over 16 experts (some empty), H and I not multiples of 64 (partial
+    last K steps of both projections), a bias with SwiGLU-OAI, and every token routed to the same
+    two experts (up to 200 rows per expert: chunks of 32 rows, a partial last chunk), all against
+    the oracle."""
     from lockstep_amd import moe_ref as MR
     prev = MR.ROW_PAIRS
     MR.ROW_PAIRS = pairs
     try:
-        _run_case(T, 16, 4, 256, 128, seed=40 + T)
-        _run_case(T, 8, 3, 272, 208, seed=50 + T, bias=True, act="swigluoai")
-        idx = np.tile(np.array([[3, 1]]), (T, 1)).astype(np.int64)
-        w = C.bf16_bits(np.tile(np.array([[0.625, 0.375]], F32), (T, 1)))
-        _run_case(T, 4, 2, 320, 192, seed=60 + T, routing_override=(idx, w))
+        with MR.kernel_choice(moe=7):
+            _run_case(T, 16, 4, 256, 128, seed=40 + T)
+            _run_case(T, 8, 3, 272, 208, seed=50 + T, bias=True, act="swigluoai")
+            idx = np.tile(np.array([[3, 1]]), (T, 1)).astype(np.int64)
+            w = C.bf16_bits(np.tile(np.array([[0.625, 0.375]], F32), (T, 1)))
+            _run_case(T, 4, 2, 320, 192, seed=60 + T, routing_override=(idx, w))
     finally:
         MR.ROW_PAIRS = prev
 

@@ -30,10 +30,13 @@ def test_moe_row_pair_query():
     lib = L.load()
     E, k, H, I = 128, 8, 2048, 768
     assert lib.lsk_moe_reads_row_pairs(1, k, E, H, I, 0, 0) == 0       # the grouped GEMV
-    assert lib.lsk_moe_reads_row_pairs(32, k, E, H, I, 0, 0) == 0
+    for T in (2, 32, 192):                                                 # the skinny grouped GEMM
+        assert lib.lsk_moe_reads_row_pairs(T, k, E, H, I, 0, 0) == 1, T
     assert lib.lsk_moe_reads_row_pairs(4096, k, E, H, I, 0, 0) == 1    # the ping-pong tiles
-    # a per-call choice of the register-staged tile (select = variant + 2) reads none
+    assert lib.lsk_moe_reads_row_pairs(32, k, E, H, I, 8, 0) == 0      # rotated layers: the tiles
+    # a per-call choice of the register-staged tile or the GEMV (select = variant + 2) reads none
     assert lib.lsk_moe_reads_row_pairs(4096, k, E, H, I, 0, 2) == 0
+    assert lib.lsk_moe_reads_row_pairs(32, k, E, H, I, 0, 4) == 0
     # the thread's own setting is left as it was
     assert lib.lsk_moe_reads_row_pairs(4096, k, E, H, I, 0, 0) == 1
 
