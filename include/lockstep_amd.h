@@ -246,7 +246,7 @@ int lsk_gemm_select(int tile_id);
 int lsk_gemm_skinny_shape(int gpb, int kw, int depth);
 
 /* Tuning control with no counterpart in the reference: 1 (the default) runs lsk_w8a8_matmul /
- * lsk_w8a8_matmul_pairs with one activation row and K <= 4096 as a single launch, the row quant
+ * lsk_w8a8_matmul_pairs with one activation row and K <= 16384 as a single launch, the row quant
  * fused into the whole-row decode GEMV (each block quantises the row itself into LDS); 0 runs the
  * row quant and the GEMV as two launches.  Results are identical.  Thread-local, like
  * lsk_gemm_select. */

@@ -483,6 +483,17 @@ __global__ __launch_bounds__(1024) void gemv_i8_stream_kernel(const int8_t* __re
   for (int t = 0; t < MT; ++t) arow[t] = (t * 16 + col < M) ? (uint32_t)((t * 16 + col) * lda) : lsk::kOob;
   const int kb = wave * kslice;
   const int ke = (kb + kslice) < K ? (kb + kslice) : K;
+  // wave 0's epilogue operands, requested first (used at the end)
+  const EpiRaw er_ = epi_raw(ep, M, N);
+  const uint32_t c0w = epi_raw_col0(er_, n0 + col, wave == 0 && col < nrows);
+  const uint32_t c1w = epi_raw_col1(er_, n0 + col, wave == 0 && col < nrows);
+  // (the row operands too with one activation tile; with two, their registers would spill)
+  uint32_t rw_[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      rw_[t][r] = MT == 1 ? epi_raw_row(er_, t * 16 + kg * 4 + r, wave == 0 && t * 16 + kg * 4 + r < M) : 0u;
 
   // one batch = U 64-byte steps: weights (non-temporal) and activations, loaded one batch
   // ahead of the MFMAs that consume them (register double buffer)
@@ -528,15 +539,13 @@ __global__ __launch_bounds__(1024) void gemv_i8_stream_kernel(const int8_t* __re
   __syncthreads();
   if (wave != 0) return;
   const int n = n0 + col;
-  const EpiCol ec = n < N ? epi_col_load(ep, n) : EpiCol{};
-  EpiRow er[MT][4];
+  const EpiCol ec = epi_col_of(ep, c0w, c1w);
+  if (MT > 1) {
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+    for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = t * 16 + kg * 4 + r;
-      er[t][r] = m < M ? epi_row_load(ep, m) : EpiRow{};
-    }
+      for (int r = 0; r < 4; ++r) rw_[t][r] = epi_raw_row(er_, t * 16 + kg * 4 + r, t * 16 + kg * 4 + r < M);
+  }
   for (int w2 = 1; w2 < KW; ++w2)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] += red_gemv[((w2 - 1) * MT + t) * 64 + lane];
@@ -545,7 +554,7 @@ __global__ __launch_bounds__(1024) void gemv_i8_stream_kernel(const int8_t* __re
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = t * 16 + kg * 4 + r;
-      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], er[t][r], ec);
+      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], epi_row_of(ep, rw_[t][r]), ec);
     }
 }
 
@@ -577,6 +586,16 @@ __global__ __launch_bounds__(1024) void gemv_i8_lds_kernel(const int8_t* __restr
   const int ke = (kb + kslice) < K ? (kb + kslice) : K;
   const int nst = ke > kb ? (ke - kb + SB - 1) / SB : 0;
   char* ring = smem_lds + wave * R * kStage;
+  // wave 0's epilogue operands, requested first (used at the end)
+  const int rr0 = lane & 15, kg0 = lane >> 4;
+  const EpiRaw er_ = epi_raw(ep, M, N);
+  const uint32_t c0w = epi_raw_col0(er_, n0 + rr0, wave == 0 && rr0 < nrows);
+  const uint32_t c1w = epi_raw_col1(er_, n0 + rr0, wave == 0 && rr0 < nrows);
+  uint32_t rw_[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rw_[t][r] = epi_raw_row(er_, t * 16 + kg0 * 4 + r, wave == 0 && t * 16 + kg0 * 4 + r < M);
   const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(W + (int64_t)n0 * ldw, (int64_t)nrows * ldw);
   const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(A, (int64_t)M * lda);
 
@@ -664,15 +683,7 @@ __global__ __launch_bounds__(1024) void gemv_i8_lds_kernel(const int8_t* __restr
   __syncthreads();
   if (wave != 0) return;
   const int n = n0 + rr;
-  const EpiCol ec = n < N ? epi_col_load(ep, n) : EpiCol{};
-  EpiRow er[MT][4];
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = t * 16 + 4 * (lane >> 4) + r;
-      er[t][r] = m < M ? epi_row_load(ep, m) : EpiRow{};
-    }
+  const EpiCol ec = epi_col_of(ep, c0w, c1w);
   for (int w2 = 1; w2 < NW; ++w2)
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[t] += red[((w2 - 1) * MT + t) * 64 + lane];
@@ -681,7 +692,7 @@ __global__ __launch_bounds__(1024) void gemv_i8_lds_kernel(const int8_t* __restr
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = t * 16 + 4 * (lane >> 4) + r;
-      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], er[t][r], ec);
+      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], epi_row_of(ep, rw_[t][r]), ec);
     }
 }
 
@@ -716,24 +727,14 @@ __global__ __launch_bounds__(1024) void gemv_i8_skinny_kernel(const int8_t* __re
   // the raw epilogue operands of this lane's outputs (row: asc, or erow under POW2; column: ws and
   // bias, or ecol), loaded ahead of everything else by branch-free buffer loads (zeros past M / N
   // and for absent operands) and only combined at the stores, so no load waits here
-  const bool pow2 = ep.order == LSK_EPI_POW2, v2x = ep.order == LSK_EPI_V21 || ep.order == LSK_EPI_V2;
   const bool mine = ks == 0 && g < G;
-  const __amdgpu_buffer_rsrc_t rrow =
-      lsk::make_rsrc(pow2 ? (const void*)ep.erow : (const void*)ep.asc, (pow2 ? ep.erow != nullptr : v2x) ? 4 * M : 0);
-  const __amdgpu_buffer_rsrc_t rcol0 =
-      lsk::make_rsrc(pow2 ? (const void*)ep.ecol : (const void*)ep.ws, (pow2 ? ep.ecol != nullptr : v2x) ? 4 * N : 0);
-  const __amdgpu_buffer_rsrc_t rcol1 = lsk::make_rsrc(ep.bias, v2x && ep.bias ? 4 * N : 0);
-  const uint32_t ocol = mine && n < N ? (uint32_t)(4 * n) : lsk::kOob;
-  const uint32_t col0 = __builtin_amdgcn_raw_buffer_load_b32(rcol0, ocol, 0, 0);
-  const uint32_t col1 = __builtin_amdgcn_raw_buffer_load_b32(rcol1, ocol, 0, 0);
+  const EpiRaw er_ = epi_raw(ep, M, N);
+  const uint32_t col0 = epi_raw_col0(er_, n, mine && n < N), col1 = epi_raw_col1(er_, n, mine && n < N);
   uint32_t rowv[MT][4];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = t * 16 + kg * 4 + r;
-      rowv[t][r] = __builtin_amdgcn_raw_buffer_load_b32(rrow, mine && m < M ? (uint32_t)(4 * m) : lsk::kOob, 0, 0);
-    }
+    for (int r = 0; r < 4; ++r) rowv[t][r] = epi_raw_row(er_, t * 16 + kg * 4 + r, mine && t * 16 + kg * 4 + r < M);
   lsk::compiler_fence();
   // A into LDS: chunk c = (row, 1 KB piece) per wave instruction
   {
@@ -809,21 +810,13 @@ __global__ __launch_bounds__(1024) void gemv_i8_skinny_kernel(const int8_t* __re
       for (int t = 0; t < MT; ++t) acc[t] += red[((wave + j) * MT + t) * 64 + lane];
   }
   if (g >= G) return;
-  EpiCol ec{};
-  if (pow2) ec.sh = (int)col0;
-  else {
-    ec.ws = __uint_as_float(col0);
-    ec.b = __uint_as_float(col1);
-  }
+  const EpiCol ec = epi_col_of(ep, col0, col1);
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = t * 16 + kg * 4 + r;
-      EpiRow er{};
-      if (pow2) er.sh = ep.shift + (int)rowv[t][r];
-      else er.row = __uint_as_float(rowv[t][r]);
-      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], er, ec);
+      if (m < M && n < N) epilogue_store_rc(ep, m, n, acc[t][r], epi_row_of(ep, rowv[t][r]), ec);
     }
 }
 
@@ -1123,6 +1116,13 @@ __global__ __launch_bounds__(256) void gemv_i8_row_kernel(const int8_t* __restri
       a[m][j] = lsk::buf_load16(ra, (m < M && koff[j] != lsk::kOob) ? (uint32_t)(m * lda) + koff[j] : lsk::kOob);
 
   const int r0 = rg * rpw;  // first row of this wave within the block
+  // the epilogue operands of the lane that stores row r0 + lane (requested now, used at the end)
+  const bool owner = ks == 0 && lane < rpw && r0 + lane < nrows;
+  const EpiRaw er_ = epi_raw(ep, M, N);
+  const uint32_t c0w = epi_raw_col0(er_, n0 + r0 + lane, owner), c1w = epi_raw_col1(er_, n0 + r0 + lane, owner);
+  uint32_t rw_[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) rw_[m] = epi_raw_row(er_, m, owner && m < M);
   auto load_row = [&](v4i* w, int i) {
     const int rl = r0 + i;
     const uint32_t rowoff = rl < nrows ? (uint32_t)(rl * ldw) : lsk::kOob;
@@ -1168,20 +1168,16 @@ __global__ __launch_bounds__(256) void gemv_i8_row_kernel(const int8_t* __restri
   }
   __syncthreads();
   // the K-slices of each row: one lane per (row of the row group)
-  if (ks != 0 || lane >= rpw) return;
+  if (!owner) return;
   const int rl = r0 + lane;
   const int n = n0 + rl;
-  if (rl >= nrows) return;
-  const EpiCol ec = epi_col_load(ep, n);
-  EpiRow er[MR];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) er[m] = m < M ? epi_row_load(ep, m) : EpiRow{};
+  const EpiCol ec = epi_col_of(ep, c0w, c1w);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m < M) {
       int sum = 0;
       for (int k2 = 0; k2 < wk; ++k2) sum += red[rg * wk + k2][lane][m];
-      epilogue_store_rc(ep, m, n, sum, er[m], ec);
+      epilogue_store_rc(ep, m, n, sum, epi_row_of(ep, rw_[m]), ec);
     }
   }
 }
@@ -1192,17 +1188,18 @@ __global__ __launch_bounds__(256) void gemv_i8_row_kernel(const int8_t* __restri
 // once per block, from L2 after the first block), the block takes their maximum, derives asc =
 // fl32(max(amax, 1e-8) / 127) and writes q = clamp(rint(x / asc)) to LDS with rowquant's arithmetic
 // (quant_one), then streams its weight rows as gemv_i8_row_kernel does, its first weight row
-// requested before x.  All blocks compute the same asc and q.  K % 16 == 0, K <= 2048 NV; x 16-byte
+// requested before x.  All blocks compute the same asc and q.  K % 16 == 0, K <= 512 NV WV; x 16-byte
 // aligned.
-template <int NC, int NV, int DT>
-__global__ __launch_bounds__(256) void gemv_i8_rowq_kernel(const void* __restrict__ X, const int8_t* __restrict__ W,
-                                                           int ldw, int N, int K, int wk, int rpw, EpiParams ep) {
-  __shared__ int red[4][16];  // [wave][row of the wave], rpw <= 16
-  __shared__ float bred[4];
-  __shared__ __attribute__((aligned(16))) int8_t qs[NV * 2048];
+template <int NC, int NV, int DT, int WV = 4>
+__global__ __launch_bounds__(WV * 64) void gemv_i8_rowq_kernel(const void* __restrict__ X, const int8_t* __restrict__ W,
+                                                               int ldw, int N, int K, int wk, int rpw, EpiParams ep) {
+  constexpr int kThr = WV * 64;
+  __shared__ int red[WV][16];  // [wave][row of the wave], rpw <= 16
+  __shared__ float bred[WV];
+  __shared__ __attribute__((aligned(16))) int8_t qs[NV * kThr * 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int rg = wave / wk, ks = wave % wk;
-  const int rows_blk = rpw * (4 / wk);
+  const int rows_blk = rpw * (WV / wk);
   const int n0 = blockIdx.x * rows_blk;
   const int nrows = (N - n0) < rows_blk ? (N - n0) : rows_blk;
   const int kb = ks * NC * 1024;
@@ -1231,7 +1228,7 @@ __global__ __launch_bounds__(256) void gemv_i8_rowq_kernel(const void* __restric
   uint4 xr[NV][kXW];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int c = tid + j * 256;
+    const int c = tid + j * kThr;
 #pragma unroll
     for (int h = 0; h < kXW; ++h)
       xr[j][h] = c < K8 ? ((const uint4*)X)[(int64_t)c * kXW + h] : make_uint4(0, 0, 0, 0);
@@ -1240,6 +1237,11 @@ __global__ __launch_bounds__(256) void gemv_i8_rowq_kernel(const void* __restric
   v4i w0[NC], w1[NC];
   load_row(w0, 0);
   if (rpw > 1) load_row(w1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  // the column operands of the lane that stores row r0 + lane (used at the end)
+  const bool owner = ks == 0 && lane < rpw && r0 + lane < nrows;
+  const EpiRaw er_ = epi_raw(ep, 1, N);
+  const uint32_t c0w = epi_raw_col0(er_, n0 + r0 + lane, owner), c1w = epi_raw_col1(er_, n0 + r0 + lane, owner);
   __builtin_amdgcn_sched_barrier(0);
 
   // the activation row: maximum, scale, quantised values into LDS
@@ -1261,12 +1263,14 @@ __global__ __launch_bounds__(256) void gemv_i8_rowq_kernel(const void* __restric
   for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
   if (lane == 0) bred[wave] = am;
   __syncthreads();
-  am = fmaxf(fmaxf(bred[0], bred[1]), fmaxf(bred[2], bred[3]));
+  am = bred[0];
+#pragma unroll
+  for (int w2 = 1; w2 < WV; ++w2) am = fmaxf(am, bred[w2]);
   am = fmaxf(am, kAmaxFloor);
   const float sc = f32_div(am, 127.0f), rs = f32_div(1.0f, sc);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int c = tid + j * 256;
+    const int c = tid + j * kThr;
     if (c < K8) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -1308,11 +1312,10 @@ __global__ __launch_bounds__(256) void gemv_i8_rowq_kernel(const void* __restric
   }
   __syncthreads();
   // the K-slices of each row: one lane per row of the row group
-  if (ks != 0 || lane >= rpw) return;
+  if (!owner) return;
   const int rl = r0 + lane;
   const int n = n0 + rl;
-  if (rl >= nrows) return;
-  const EpiCol ec = epi_col_load(ep, n);
+  const EpiCol ec = epi_col_of(ep, c0w, c1w);
   int sum = 0;
   for (int k2 = 0; k2 < wk; ++k2) sum += red[rg * wk + k2][lane];
   epilogue_store_rc(ep, 0, n, sum, EpiRow{sc, 0}, ec);
@@ -1727,12 +1730,13 @@ static int launch_gemv(const int8_t* a, int lda, const int8_t* w, int ldw, int M
 
 // Whether lsk_w8a8_matmul takes the fused row-quant GEMV for one activation row: the decode GEMV
 // would run (no forced tile other than the GEMV, the whole-row variant), K % 16 == 0 and
-// K <= 4096, x and w 16-byte aligned, the v2.1 or v2 order.  (Every block reads x, so the fusion
-// pays only while x is small: on MI355X, graph replays over weight copies, Llama-3.1-8B gate_up
-// M = 1 (K = 4096) 21.2 us fused against 22.1 us as two launches; the down projection (K = 14336,
-// 57 KB of x per block) 16.0 us at best against 15.3-16.1 us.)
+// K <= 16384, x and w 16-byte aligned, the v2.1 or v2 order.  (Every block reads x, so long rows
+// take 16-wave blocks that serve 16 weight rows per read of x: on MI355X, graph replays over weight
+// copies, Llama-3.1-8B gate_up M = 1 (K = 4096) 21.2 us fused against 22.1 us as two launches; the
+// down projection (K = 14336, 57 KB of x per block) 13.5 us against 16.0 us; with four-wave blocks
+// it measured 16.0 us.)
 bool rowq_gemv_ok(const void* x, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int order) {
-  return g_rowq && M == 1 && N >= 1 && N <= 0x7fffffff && K >= 16 && K <= 4096 && K % 16 == 0 && ldw % 16 == 0 &&
+  return g_rowq && M == 1 && N >= 1 && N < (1 << 29) && K >= 16 && K <= 16384 && K % 16 == 0 && ldw % 16 == 0 &&
          aligned16(x) && aligned16(w) && (g_force_tile < 0 || g_force_tile == 5) && g_gemv_variant == 0 &&
          g_gemv_mid != 3 &&
          (order == LSK_EPI_V21 || order == LSK_EPI_V2) && ldw * 64 < 0x7fffffff;
@@ -1740,6 +1744,26 @@ bool rowq_gemv_ok(const void* x, const int8_t* w, int64_t ldw, int64_t M, int64_
 
 int launch_gemv_rowq(const void* x, int x_dtype, const int8_t* w, int ldw, int N, int K, const EpiParams& ep,
                      hipStream_t s) {
+  if (K > 4096) {
+    // long rows: 16-wave blocks (four K-slices of up to 4 KB per row, RPW rows per wave) so that
+    // each block's read of x serves 4 RPW weight rows and about 256 blocks cover N.  (Llama-3.1-8B
+    // down, M = 1, graph replays: 16.0 us as two launches -> 13.5 us; RPW 1 / 2 / 4 / 8: 22.0 / 17.2
+    // / 13.5 / 16.1 us.  Up to K = 4096 the four-wave blocks measured level with this form.)
+    const int wk = 4;
+    int rpw = (N * wk / 16 + 255) / 256;
+    rpw = rpw < 1 ? 1 : (rpw > 16 ? 16 : rpw);
+    if (g_row_rpw > 0) rpw = g_row_rpw;
+    const int rows_blk = rpw * (16 / wk);
+    const int blocks = (N + rows_blk - 1) / rows_blk;
+#define LSK_RQL(DTV)                                                                                       \
+  {                                                                                                        \
+    hipLaunchKernelGGL((gemv_i8_rowq_kernel<4, 2, DTV, 16>), dim3((unsigned)blocks), dim3(1024), 0, s, x, w, ldw, N, \
+                       K, wk, rpw, ep);                                                                    \
+    return check_launch("gemv_i8_rowq_kernel");                                                            \
+  }
+    if (x_dtype == LSK_F32) LSK_RQL(LSK_F32) else if (x_dtype == LSK_BF16) LSK_RQL(LSK_BF16) else LSK_RQL(LSK_F16)
+#undef LSK_RQL
+  }
   const int nch = (K + 1023) / 1024;
   int wk = 1;
   while (wk < 4 && (nch + wk - 1) / wk > 4) wk *= 2;
@@ -1776,7 +1800,7 @@ static bool tiles_fast(const int8_t* a, int64_t lda, const int8_t* w, int64_t ld
 // Whether launch_gemm runs (M, N, K) on the decode GEMV that reads the weight's row-pair copy
 // (gemv_i8_skinny_kernel), for a weight of row stride ldw at a 16-byte aligned address.
 bool gemm_takes_skinny(const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K, int64_t lda) {
-  if (M <= 0 || M > 32 || N <= 0 || !tiles_fast(w, lda, w, ldw, M, N, K)) return false;
+  if (M <= 0 || M > 32 || N <= 0 || !epi_raw_fits(M, N) || !tiles_fast(w, lda, w, ldw, M, N, K)) return false;
   return (g_force_tile < 0 || g_force_tile == 5) && gemv_takes_skinny(M, N, K);
 }
 
@@ -1808,7 +1832,14 @@ int launch_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int6
     return check_launch("gemm_i8_generic_kernel");
   }
   const int iM = (int)M, iN = (int)N, iK = (int)K;
-  if (M <= 32 && (g_force_tile < 0 || g_force_tile == 5)) return launch_gemv(a, (int)lda, w, (int)ldw, iM, iN, iK, ep, s);
+  if (M <= 32 && (g_force_tile < 0 || g_force_tile == 5)) {
+    if (!epi_raw_fits(M, N)) {  // (the GEMVs address their epilogue operands by 32-bit offsets)
+      hipLaunchKernelGGL(gemm_i8_generic_kernel, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, s, a, lda, w,
+                         ldw, M, N, K, ep);
+      return check_launch("gemm_i8_generic_kernel");
+    }
+    return launch_gemv(a, (int)lda, w, (int)ldw, iM, iN, iK, ep, s);
+  }
   const int vec_ok = out_vec_ok(ep.out, ep.out_dtype, ep.ldo) ? 1 : 0;
   const int ilda = (int)lda, ildw = (int)ldw;
   int64_t n1 = 0;

@@ -388,6 +388,59 @@ LSK_DEV void epilogue_store_rc(const EpiParams& p, int64_t m, int64_t n, int32_t
   epilogue_store_ops(p, m, n, acc, EpiOps{r.row, c.ws, c.b, r.sh + c.sh});
 }
 
+// The same row and column operands as raw 32-bit words from branch-free buffer loads, for kernels
+// that request them at their start and combine them only at their stores: a load whose value is
+// used at once (the POW2 shift added, a branch on the order around it) makes the compiler wait for
+// it there, so the operands of a short kernel would cost a round trip each.  Offsets of absent
+// operands (the other orders' arrays, a null bias or exponent vector, rows / columns out of range)
+// read zero.  Row m < 2^29 and column n < 2^29 (4-byte offsets inside one buffer range).
+struct EpiRaw {
+  __amdgpu_buffer_rsrc_t row, col0, col1;
+};
+
+LSK_DEV EpiRaw epi_raw(const EpiParams& p, int64_t M, int64_t N) {
+  const bool pow2 = p.order == LSK_EPI_POW2, v2x = p.order == LSK_EPI_V21 || p.order == LSK_EPI_V2;
+  const int64_t rb = (pow2 ? p.erow != nullptr : v2x) ? 4 * M : 0;
+  const int64_t cb = (pow2 ? p.ecol != nullptr : v2x) ? 4 * N : 0;
+  const int64_t bb = v2x && p.bias ? 4 * N : 0;
+  EpiRaw r;
+  r.row = __builtin_amdgcn_make_buffer_rsrc(pow2 ? (void*)p.erow : (void*)p.asc, (short)0,
+                                            (int)(rb > 0x7fffffff ? 0x7fffffff : rb), 0x00020000);
+  r.col0 = __builtin_amdgcn_make_buffer_rsrc(pow2 ? (void*)p.ecol : (void*)p.ws, (short)0,
+                                             (int)(cb > 0x7fffffff ? 0x7fffffff : cb), 0x00020000);
+  r.col1 = __builtin_amdgcn_make_buffer_rsrc((void*)p.bias, (short)0, (int)(bb > 0x7fffffff ? 0x7fffffff : bb),
+                                             0x00020000);
+  return r;
+}
+
+LSK_DEV uint32_t epi_raw_row(const EpiRaw& r, int64_t m, bool ok) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r.row, ok ? (int)(4 * m) : (int)0x80000000u, 0, 0);
+}
+LSK_DEV uint32_t epi_raw_col0(const EpiRaw& r, int64_t n, bool ok) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r.col0, ok ? (int)(4 * n) : (int)0x80000000u, 0, 0);
+}
+LSK_DEV uint32_t epi_raw_col1(const EpiRaw& r, int64_t n, bool ok) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r.col1, ok ? (int)(4 * n) : (int)0x80000000u, 0, 0);
+}
+// The EpiRow / EpiCol those words stand for (epi_row_load / epi_col_load's values).
+LSK_DEV EpiRow epi_row_of(const EpiParams& p, uint32_t raw) {
+  EpiRow r{0.0f, 0};
+  if (p.order == LSK_EPI_POW2) r.sh = p.shift + (int)raw;
+  else r.row = __uint_as_float(raw);
+  return r;
+}
+LSK_DEV EpiCol epi_col_of(const EpiParams& p, uint32_t raw0, uint32_t raw1) {
+  EpiCol c{0.0f, 0.0f, 0};
+  if (p.order == LSK_EPI_POW2) c.sh = (int)raw0;
+  else {
+    c.ws = __uint_as_float(raw0);
+    c.b = __uint_as_float(raw1);
+  }
+  return c;
+}
+// Whether epi_raw's offsets cover M rows and N columns.
+inline bool epi_raw_fits(int64_t M, int64_t N) { return M < (1 << 29) && N < (1 << 29); }
+
 // Round four epilogue values to the output type and store them at element offset o with one
 // vector store (the row segment is aligned and in range).  RAW stores the accumulators.
 LSK_DEV void store4_out(void* out, int order, int out_dtype, int64_t o, const float* y, v4i acc) {

@@ -576,7 +576,8 @@ def test_bf16_conversion_instruction_equals_rne_on_every_binary32():
                                  (77, 16384)])
 def test_one_row_fused_rowquant_gemv(N, K, xdt):
     """w8a8_matmul with one activation row runs the row quant inside the whole-row GEMV (one
-    launch, K <= 4096; two launches beyond): the oracle's bits for every order, bias and output
+    launch: four-wave blocks up to K = 4096, sixteen-wave blocks up to 16384; two launches beyond):
+    the oracle's bits for every order, bias and output
     type, near-tie activations, and the same bits as the two-launch path
     (lsk_gemm_fuse_rowquant(0))."""
     import lockstep_amd._lib as L
