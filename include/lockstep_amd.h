@@ -599,6 +599,13 @@ int lsk_moe_select(int variant);
  * a parameter to the size rule.  Results are identical.  Thread-local. */
 int lsk_moe_skinny_shape(int gpb, int kw);
 
+/* Tuning control with no counterpart in the reference: the int8 ping-pong expert tiles (and the
+ * grouped linear's) that hold at most `rows` routed rows (0..32; 32 the default, 0 none) run on the
+ * skinny path -- the tile's rows staged in LDS once, its weight rows streamed into the MFMA
+ * operand -- instead of the main loop; the epilogue is the tile's.  Results are identical.
+ * Thread-local. */
+int lsk_moe_pp_skinny_rows(int rows);
+
 /* Tuning control with no counterpart in the reference: the main loop of the grouped MXFP4
  * expert GEMMs (0: direct-to-LDS operand staging with fp4 fragments converted per wave, a
  * two-stage ring, three blocks per CU, the default; 1: register-staged operands converted to bf16

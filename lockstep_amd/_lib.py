@@ -56,6 +56,7 @@ SIGNATURES = {
     "lsk_gemm_select": (_I, [_I]),
     "lsk_gemm_skinny_shape": (_I, [_I, _I, _I]),
     "lsk_moe_skinny_shape": (_I, [_I, _I]),
+    "lsk_moe_pp_skinny_rows": (_I, [_I]),
     "lsk_gemm_fuse_rowquant": (_I, [_I]),
     "lsk_quant8_dyn_single_pass": (_I, [_I]),
     "lsk_quant8_dyn_variant": (_I, [_I]),

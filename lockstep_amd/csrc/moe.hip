@@ -31,6 +31,10 @@ thread_local int g_moe_force = -1;  // tuning control: -1 by size, 0 register-st
                        // 3 the 128x256 tile on the four-wave main loop, 7 the skinny grouped GEMM
 thread_local int g_rowq1 = 1;       // one-token layers from logits: router + row quant + gate/up GEMV in one launch
 thread_local int g_msk_gpb = 0, g_msk_kw = 0;  // the skinny grouped GEMM's launch shape (0: by size)
+// ping-pong expert tiles of at most this many rows take the skinny path (Qwen3-30B-A3B layer on
+// MI355X, graph replays, T = 256 / 2048 / 4096: 167 / 294 / 418 us without, 153 / 284 / 412 at 16
+// rows, 155 / 280 / 420 at 32)
+thread_local int g_pp_skinny = 32;
 thread_local int g_moe_w4 = 0;      // the ping-pong tile: 0 128x256 eight-wave ping-pong, 1 128x256 four waves,
                                     // 2 128x256 with 128-byte K stages, 3 256x256 (eight waves, four-stage ring)
 
@@ -646,6 +650,107 @@ constexpr int moe_smem_bytes() {
 static_assert(moe_smem_bytes<PPM128>() <= 160 * 1024 && moe_smem_bytes<PPM256>() <= 160 * 1024, "one block per CU");
 static_assert(2 * moe_smem_bytes<W4M>() <= 160 * 1024 && 2 * moe_smem_bytes<PPM>() <= 160 * 1024, "two blocks per CU");
 
+// A ping-pong tile of at most 32 rows on the skinny path: the main loop's LDS stages would move a
+// 128-row activation panel for a few rows while the weight panel, the whole cost of such a tile,
+// streams through a three-stage ring.  Instead the block copies the tile's rows into LDS once
+// (direct loads, 1 KB of a row per instruction, row stride ldsk = a multiple of 1 KB plus 16 bytes;
+// the down projection's rows from their row-pair layout when a.pairs & 1), and each wave streams the
+// weight rows of two groups of 16 of the tile's columns (local columns 32 w .. 32 w + 31, weight rows
+// wrow_of(c), the row-pair copy when a.pairs & 2) into the v_mfma_i32_16x16x64_i8 B operand, D steps
+// per group in flight, the A fragments from LDS.  The exact sums go to the strip regions in the layout
+// pp_stage_strip leaves them (row m, column c at region(c / WTN)[m * kLdc + c % WTN]), so the tile's
+// epilogue runs unchanged on the waves of the first row of waves.
+template <class C, int MODE, class WROW>
+__device__ __forceinline__ void moe_tile_skinny(const MoeGemmArgs& a, char* smem, int p0, int p1, const int8_t* wb,
+                                                WROW wrow_of) {
+  constexpr int D = 4;
+  static_assert(C::kThreads == 512 && C::kBN == 256, "eight waves of two 16-column groups");
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int nr = p1 - p0;
+  const int K = a.K, steps = (K + 63) >> 6;
+  const int ldsk = (K + 1023) / 1024 * 1024 + 16;
+  const int col = lane & 15, kg = lane >> 4;
+  const bool pa = (a.pairs & 1) != 0, pw = (a.pairs & 2) != 0;
+  // the tile's rows into LDS: their sources read once per wave (lane r holds row r's), then taken
+  // by readlane, so no load sits between the direct loads
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+  const int cpr = (K + 1023) >> 10;
+  int srcv = p0 + lane;
+  if (MODE == 0) {
+    const __amdgpu_buffer_rsrc_t rt = lsk::make_rsrc(a.row_tok + p0, 4 * (int64_t)nr);
+    srcv = (int)__builtin_amdgcn_raw_buffer_load_b32(rt, lane < nr ? (uint32_t)(4 * lane) : lsk::kOob, 0, 0);
+  }
+  for (int c = wave; c < nr * cpr; c += 8) {
+    const int r = c / cpr, j = c - (c / cpr) * cpr;
+    const int src = __builtin_amdgcn_readlane(srcv, r);
+    const int kk = j * 1024 + lane * 16;
+    const uint32_t rowoff = (MODE == 1 && pa) ? (uint32_t)((src >> 1) * 2 * a.lda + (src & 1) * 64) : (uint32_t)(src * a.lda);
+    const uint32_t koff = (MODE == 1 && pa) ? (uint32_t)((kk >> 6) * 128 + (kk & 63)) : (uint32_t)kk;
+    const uint32_t off = kk < K ? rowoff + koff : lsk::kOob;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(smem + r * ldsk + j * 1024), 16, off, 0, 0, 0);
+  }
+  // this wave's two groups of weight rows, their first D steps
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc(wb, a.w_bytes);
+  const uint32_t kstep = pw ? 128 : 64;
+  uint32_t wbase[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    int hc;
+    const int wr = wrow_of(32 * wave + 16 * h + col, hc);
+    wbase[h] = hc < a.N ? (uint32_t)(pw ? (wr >> 1) * 2 * a.ldw + (wr & 1) * 64 : wr * a.ldw) + kg * 16 : lsk::kOob;
+  }
+  v4i w[2][D];
+#pragma unroll
+  for (int u = 0; u < D; ++u)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      w[h][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rw, (u < steps && wbase[h] != lsk::kOob) ? wbase[h] + u * kstep : lsk::kOob,
+                                            0, 2 /* non-temporal */));
+  lsk::compiler_fence();
+  lsk::wait_vm<2 * D>();  // the rows (and the tile's operands requested before them)
+  __syncthreads();
+  v4i acc[2][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) acc[h][0] = acc[h][1] = lsk::zero4();
+  const char* arow[2];
+  bool alive[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int r = t * 16 + col;
+    alive[t] = r < nr;
+    arow[t] = smem + (r < nr ? r : nr - 1) * ldsk + kg * 16;
+  }
+  for (int s = 0; s < steps; s += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int st = s + u < steps ? s + u : 0;
+      v4i af[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) af[t] = alive[t] ? *(const v4i*)(arow[t] + st * 64) : lsk::zero4();
+      const int nx = s + u + D;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        acc[h][0] = lsk::mfma_i8(af[0], w[h][u], acc[h][0]);
+        acc[h][1] = lsk::mfma_i8(af[1], w[h][u], acc[h][1]);
+        w[h][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rw, (nx < steps && wbase[h] != lsk::kOob) ? wbase[h] + nx * kstep : lsk::kOob,
+                                              0, 2 /* non-temporal */));
+      }
+    }
+  }
+  __syncthreads();  // every wave is past its last read of the rows: the strip regions reuse the LDS
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = 32 * wave + 16 * h + col;
+    int32_t* region = (int32_t*)(smem + (c / C::WTN) * C::kStripBytes) + (c % C::WTN);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) region[(t * 16 + kg * 4 + r) * C::kLdc] = acc[h][t][r];
+  }
+}
+
 template <class C, int MODE, class MAIN>
 __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, MAIN main) {
   static_assert((C::kBM == 128 || C::kBM == 256) && C::kBN == 256 && C::TM == 2,
@@ -727,7 +832,14 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
 
   // the wave's 32-row strips that hold rows of the tile (the others are neither multiplied nor stored)
   const int na = max(0, min(C::TM, (p1 - p0 - wm * C::WTM + 31) / 32));
-  main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe, na, (MODE == 1 ? (a.pairs & 1) : 0) | (a.pairs & 2));
+  // a tile of few rows: the skinny path, its sums left in the strip regions
+  bool skinny = false;
+  if constexpr (C::kThreads == 512 && C::kBN == 256) {
+    skinny = p1 - p0 <= a.skinny_rows && p1 - p0 <= 32 && 32 * ((a.K + 1023) / 1024 * 1024 + 16) <= C::kScaleOff;
+    if (skinny) moe_tile_skinny<C, MODE>(a, smem_moe, p0, p1, wb, wrow_of);
+  }
+  if (!skinny)
+    main(acc, ra_res, pa, rb_res, pb, a.K, smem_moe, na, (MODE == 1 ? (a.pairs & 1) : 0) | (a.pairs & 2));
 
   // park the operands in LDS (past every wave's last ring read)
   float* sc_asc = (float*)(smem_moe + C::kScaleOff);
@@ -881,7 +993,7 @@ __device__ __forceinline__ void moe_tile(const MoeGemmArgs& a, char* smem_moe, M
     }
   };
   if (na > 0) {
-    lsk::pp_stage_strip<C::TN, C::kLdc>(acc[0], region);
+    if (!skinny) lsk::pp_stage_strip<C::TN, C::kLdc>(acc[0], region);
     strip(0);
   }
   if (na > 1) {
@@ -2337,6 +2449,7 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
                   R * lda < 0x7fffffff,
               "lsk_grouped_gemm_w8a8: row strides must cover K and be multiples of 16 (31-bit buffer offsets)");
   MoeGemmArgs g{};
+  g.skinny_rows = g_pp_skinny;
   g.A = a;
   g.lda = lda;
   g.a_bytes = R * lda;
@@ -2378,6 +2491,7 @@ extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* 
               "lsk_grouped_gemm_mx: K %% 32 == 0; row strides must cover K (bf16 rows, multiples of 8), K/2 (code "
               "bytes, multiples of 16) and K/32 (31-bit buffer offsets)");
   MoeGemmArgs g{};
+  g.skinny_rows = g_pp_skinny;
   g.A = a;
   g.lda = lda;
   g.a_bytes = R * lda * 2;
@@ -2399,6 +2513,12 @@ extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* 
 extern "C" int lsk_moe_fuse_route(int on) {
   LSK_REQUIRE(on == 0 || on == 1, "lsk_moe_fuse_route: %d not 0 or 1", on);
   g_rowq1 = on;
+  return LSK_OK;
+}
+
+extern "C" int lsk_moe_pp_skinny_rows(int rows) {
+  LSK_REQUIRE(rows >= 0 && rows <= 32, "lsk_moe_pp_skinny_rows: %d not in [0, 32]", rows);
+  g_pp_skinny = rows;
   return LSK_OK;
 }
 
@@ -2627,6 +2747,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
                                        use_mx2_gemv ? 1 : lo13, use_mx2_gemv ? 0 : hi13, s)))
     return rc;
   MoeGemmArgs g1{};
+  g1.skinny_rows = g_pp_skinny;
   g1.A = w.qx;
   g1.lda = H;
   g1.a_bytes = T * H * (mx ? 2 : 1);
@@ -2735,6 +2856,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::check_launch("moe_requant_kernel"))) return rc;
   }
   MoeGemmArgs g2{};
+  g2.skinny_rows = g_pp_skinny;
   g2.A = w.qh;
   g2.lda = I;
   g2.a_bytes = pair_down ? ((R + 1) & ~(int64_t)1) * I : R * I * (mx ? 2 : 1);

@@ -43,6 +43,8 @@ struct MoeGemmArgs {
   // (k & 63), lda % 64 == 0; bit 1: the weights (w_ptrs) in that layout, ldw % 64 == 0
   // (ping-pong tiles only)
   int pairs;
+  // ping-pong tiles of at most this many rows take the skinny path (0: none)
+  int skinny_rows;
 };
 
 // The calling thread's grouped MX main-loop choice (lsk_moe_mx_select).
