@@ -2440,8 +2440,10 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
                                            int64_t N, int64_t K, uint16_t* out, void* workspace,
                                            int64_t workspace_bytes, void* stream) {
   hipStream_t s = (hipStream_t)stream;
-  // the ping-pong tiles once experts average 16 rows (the 256 x 256 ones when chosen)
-  const bool pp = R >= 16 * E, pp256 = pp && moe_uses_pp256(R, E);
+  // the ping-pong tiles once experts average 16 rows (the 256 x 256 ones when chosen); the
+  // register-staged tile (lsk_moe_select(0)) or the skinny grouped GEMM (7) when chosen
+  const bool pp = g_moe_force != 0 && g_moe_force != 7 && (g_moe_force == 1 || g_moe_force == 3 || R >= 16 * E);
+  const bool pp256 = pp && moe_uses_pp256(R, E);
   int rc = grouped_setup("lsk_grouped_gemm_w8a8", a, asc, offs, E, R, w_ptrs, ws_ptrs, N, K, out, workspace,
                          workspace_bytes, s, pp256 ? kBM2 : kBM);
   if (rc || R == 0) return rc;
@@ -2474,6 +2476,19 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
     }
     if (pp256) return launch_moe_pp256<1>(g, R / kBM2 + (E < R ? E : R), s, "moe_pp256_kernel<grouped>");
     return launch_moe_pp<1>(g, mt, s, "moe_pp_kernel<grouped>");
+  }
+  // few rows per expert: the skinny grouped GEMM (chunks of 32 of an expert's rows in LDS) while
+  // they fit, the register-staged tile otherwise or when chosen
+  if (K <= 4096 && g_moe_force != 0) {
+    if (w_pair_ptrs) {
+      g.w_ptrs = w_pair_ptrs;
+      g.ldw = (K + 63) / 64 * 64;
+      g.w_bytes = ((N + 1) & ~(int64_t)1) * g.ldw;
+      g.pairs = 2;
+    }
+    // (the launch shape by rows per expert: twice the average, the skew a Zipf routing leaves)
+    const int64_t rpe = std::min<int64_t>(kSkinnyMaxT, std::max<int64_t>(1, 2 * ((R + E - 1) / E)));
+    return launch_moe_skinny<1>(g, mt, rpe, nullptr, s, "moe_skinny_kernel<grouped>");
   }
   return launch_moe_gemm<1>(g, mt, (int)((N + 127) / 128), s, "moe_gemm_kernel<grouped>");
 }

@@ -33,7 +33,8 @@ def _counts(g, E, R):
 
 
 @pytest.mark.parametrize("R,E,N,K,bias", [(300, 8, 192, 256, False), (40, 6, 96, 320, True),
-                                          (2200, 12, 256, 512, False), (1600, 8, 320, 128, True)])
+                                          (2200, 12, 256, 512, False), (1600, 8, 320, 128, True),
+                                          (256, 32, 400, 2880, True), (100, 16, 48, 208, False)])
 def test_grouped_linear_int8(R, E, N, K, bias):
     from lockstep_amd import moe_ref as MR
     say("grouped int8", dict(R=R, E=E, N=N, K=K, bias=bias))
@@ -91,11 +92,12 @@ def test_grouped_linear_mx(R, E, N, K, bias):
         assert np.array_equal(got[r0:r1], C.bf16_bits(ref)), "expert %d" % e
 
 
-@pytest.mark.parametrize("variant", [1, 5, 6])
+@pytest.mark.parametrize("variant", [0, 1, 5, 6, 7])
 def test_grouped_linear_int8_tile_choice(variant):
-    """The grouped linear on the 128x256 (1) and the 256x256 ping-pong tiles (5 persistent, 6 one
-    tile per block), each chosen, with experts of several 256-row tiles and a bias: the oracle's
-    bits."""
+    """The grouped linear on the register-staged tile (0), the 128x256 (1) and the 256x256 ping-pong
+    tiles (5 persistent, 6 one tile per block) and the skinny grouped GEMM (7: experts of about 300
+    rows in ten 32-row chunks), each chosen, with experts of several 256-row tiles and a bias: the
+    oracle's bits."""
     from lockstep_amd import _lib as L
     from lockstep_amd import moe_ref as MR
     R, E, N, K = 1500, 5, 384, 448
