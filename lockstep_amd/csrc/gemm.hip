@@ -1144,8 +1144,7 @@ __global__ __launch_bounds__(256) void gemv_i8_row_kernel(const int8_t* __restri
         acc[m] = __builtin_amdgcn_sdot4(a[m][j][2], w[j][2], acc[m], false);
         acc[m] = __builtin_amdgcn_sdot4(a[m][j][3], w[j][3], acc[m], false);
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, 64);
+      acc[m] = wave_sum_i32(acc[m]);
     }
     if (lane == 0) {
 #pragma unroll
@@ -1260,7 +1259,7 @@ __global__ __launch_bounds__(WV * 64) void gemv_i8_rowq_kernel(const void* __res
       am = fmaxf(am, fabsf(v[j][e]));
     }
   }
-  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  am = wave_fmax(am);
   if (lane == 0) bred[wave] = am;
   __syncthreads();
   am = bred[0];
@@ -1294,8 +1293,7 @@ __global__ __launch_bounds__(WV * 64) void gemv_i8_rowq_kernel(const void* __res
       acc = __builtin_amdgcn_sdot4(a[j][2], w[j][2], acc, false);
       acc = __builtin_amdgcn_sdot4(a[j][3], w[j][3], acc, false);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    acc = wave_sum_i32(acc);
     if (lane == 0) red[wave][i] = acc;
   };
   // two register sets in turn, each reloaded as soon as its row is summed

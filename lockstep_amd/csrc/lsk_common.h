@@ -33,6 +33,35 @@ LSK_DEV int64_t wave_uniform64(int64_t v) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// Wave-wide reductions by DPP row moves: two quad swaps and the half-row and row mirrors leave
+// each row's total in all 16 of its lanes, the row broadcasts 15 and 31 carry rows 0-2 into row 3,
+// and lane 63's total is returned as a wave-uniform value.  Lanes of the rows a broadcast does not
+// write keep their value (the identity is passed as the DPP "old" operand).  Six VALU steps and a
+// readlane, against six LDS-crossbar round trips for a __shfl_xor butterfly.  Every lane of the
+// wave must be active.
+template <class Op>
+LSK_DEV uint32_t wave_reduce_dpp(uint32_t v, uint32_t ident, Op op) {
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, 0xb1, 0xf, 0xf, false));   // quad [1,0,3,2]
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, 0x4e, 0xf, 0xf, false));   // quad [2,3,0,1]
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, 0x141, 0xf, 0xf, false));  // half-row mirror
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, 0x140, 0xf, 0xf, false));  // row mirror
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, 0x142, 0xa, 0xf, false));  // row bcast 15
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)ident, (int)v, 0x143, 0xc, 0xf, false));  // row bcast 31
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+LSK_DEV uint32_t wave_max_u32(uint32_t v) {
+  return wave_reduce_dpp(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+LSK_DEV int wave_sum_i32(int v) {
+  return (int)wave_reduce_dpp((uint32_t)v, 0u, [](uint32_t a, uint32_t b) { return (uint32_t)((int)a + (int)b); });
+}
+// fmaxf over the wave (a NaN lane is passed over as fmaxf passes it; -inf is the identity).
+LSK_DEV float wave_fmax(float v) {
+  return __uint_as_float(wave_reduce_dpp(__float_as_uint(v), 0xff800000u, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
+
 // binary32 -> bf16, round to nearest even; every NaN becomes 0x7FC0 (the conversion torch's
 // c10::BFloat16 performs, which is what the reference's `.to(torch.bfloat16)` runs).
 // binary32 -> bf16 by the round-to-nearest-even bit method torch uses, every NaN to 0x7FC0: the

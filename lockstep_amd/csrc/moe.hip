@@ -39,19 +39,13 @@ thread_local int g_moe_w4 = 0;      // the ping-pong tile: 0 128x256 eight-wave 
                                     // 2 128x256 with 128-byte K stages, 3 256x256 (eight waves, four-stage ring)
 
 // ---------------------------------------------------------------- router
-LSK_DEV long long wave_max_ll(long long v) {
-  for (int o = 32; o > 0; o >>= 1) {
-    const long long w = __shfl_xor(v, o, 64);
-    v = w > v ? w : v;
-  }
-  return v;
-}
-
 // One wave per token; lane l owns experts l, l + 64, ... (EPL per lane, E <= 64 * EPL).  The
-// reference's ranking key s * E + (E - 1 - e) orders like the pair (s, E - 1 - e), so the key is
-// kept as s << 32 | (E - 1 - e) and decoded with shifts.  The selection: lane r < k gets the rank-r
-// expert e_r and its score s_r; S is the score sum the weights divide by (the selected scores, or
-// all of them without renormalisation), clamped to >= 1.
+// reference's ranking key s * E + (E - 1 - e) orders like the pair (s, E - 1 - e); with scores
+// below 2^16 (entries of the FRAC table are at most 2^15, and a score is an entry shifted right) and
+// E <= 2^16 the pair packs into one 32-bit key s << 16 | (0xffff - e), so each of the k rounds is
+// one DPP maximum over the wave and the winner is decoded from the wave-uniform key.  The
+// selection: lane r < k gets the rank-r expert e_r and its score s_r; S is the score sum the
+// weights divide by (the selected scores, or all of them without renormalisation), clamped to >= 1.
 template <int EPL>
 LSK_DEV void route_select(const void* __restrict__ g, int gdt, int64_t ldg, int t, int E, int k, int renorm,
                           const int32_t* __restrict__ tab, int& e_mine, int& s_mine, int& S) {
@@ -68,13 +62,13 @@ LSK_DEV void route_select(const void* __restrict__ g, int gdt, int64_t ldg, int 
       m = fmaxf(m, gv[j]);
     }
   }
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  long long key[EPL];
+  m = wave_fmax(m);
+  uint32_t key[EPL];
   int s_all = 0;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
-    key[j] = -1;
+    key[j] = 0;
     if (e < E) {
       const float v = rintf(f32_mul(m - gv[j], kRouterC));
       int sc = 0;
@@ -83,20 +77,20 @@ LSK_DEV void route_select(const void* __restrict__ g, int gdt, int64_t ldg, int 
         sc = tab[(d >> 13) & 8191] >> (d >> 26);
       }
       s_all += sc;
-      key[j] = ((long long)sc << 32) | (long long)(unsigned)(E - 1 - e);
+      key[j] = ((uint32_t)sc << 16) | (uint32_t)(0xffff - e);
     }
   }
-  for (int o = 32; o > 0; o >>= 1) s_all += __shfl_xor(s_all, o, 64);
+  s_all = wave_sum_i32(s_all);
   s_mine = 0;
   e_mine = 0;
   int s_sum = 0;
   for (int r = 0; r < k; ++r) {
-    long long best = -1;
+    uint32_t best = 0;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
-    best = wave_max_ll(best);
-    const int e = (E - 1) - (int)(unsigned)(best & 0xffffffffLL);
-    const int sc = (int)(best >> 32);
+    best = wave_max_u32(best);
+    const int e = 0xffff - (int)(best & 0xffffu);
+    const int sc = (int)(best >> 16);
     s_sum += sc;
     if (lane == r) {
       s_mine = sc;
@@ -104,7 +98,7 @@ LSK_DEV void route_select(const void* __restrict__ g, int gdt, int64_t ldg, int 
     }
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
-      if (lane + 64 * j == e) key[j] = -1;
+      if (lane + 64 * j == e) key[j] = 0;
   }
   S = renorm ? s_sum : s_all;
   S = S < 1 ? 1 : S;
@@ -364,7 +358,7 @@ __global__ __launch_bounds__(256) void moe_decode_prep_kernel(const int64_t* __r
       for (int e = 0; e < 4; ++e)
         am = fmaxf(am, fmaxf(fabsf(bf16_to_f32((uint16_t)(wd[e] & 0xffff))), fabsf(bf16_to_f32((uint16_t)(wd[e] >> 16)))));
     }
-    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    am = wave_fmax(am);
     if ((tid & 63) == 0) red[tid >> 6] = am;
     __syncthreads();
     am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -398,7 +392,7 @@ __global__ __launch_bounds__(256) void moe_decode_prep_kernel(const int64_t* __r
   }
   float am = 0.0f;
   for (int i = tid; i < H; i += 256) am = fmaxf(am, fabsf(bf16_to_f32(row[i])));
-  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  am = wave_fmax(am);
   if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
   am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -1687,7 +1681,7 @@ __global__ __launch_bounds__(256) void moe_route_gemv1_kernel(MoeGemmArgs a, uin
       am = fmaxf(am, fmaxf(fabsf(xv[j][2 * q]), fabsf(xv[j][2 * q + 1])));
     }
   }
-  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  am = wave_fmax(am);
   const float sc = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, sc);
   v4i act[NC];
 #pragma unroll
@@ -1897,8 +1891,7 @@ __global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* _
       am = fmaxf(am, fabsf(hv[t]));
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  am = wave_fmax(am);
   if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
   am = red[0];
@@ -1997,7 +1990,7 @@ __global__ __launch_bounds__(256) void moe_rot_requant_kernel(const uint16_t* __
     rv[i] = v;
     am = fmaxf(am, fabsf(v));
   }
-  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  am = wave_fmax(am);
   if ((tid & 63) == 0) red[tid >> 6] = am;
   __syncthreads();
   am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

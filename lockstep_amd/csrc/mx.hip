@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void rowquant_bf16_kernel(const uint16_t* __re
   const uint16_t* row = x + t * H;
   float am = 0.0f;
   for (int64_t i = threadIdx.x; i < H; i += 256) am = fmaxf(am, fabsf(bf16_to_f32(row[i])));
-  for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+  am = wave_fmax(am);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
   __syncthreads();
   am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

@@ -150,7 +150,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_float_kernel(NormArgs p, int vec
   }
   if (!p.q) return;
   // the contract row quant of the bf16 outputs (max is exact and order-free)
-  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  amax = wave_fmax(amax);
   if (W > 1) {
     if ((threadIdx.x & 63) == 0) redq[threadIdx.x >> 6] = amax;
     __syncthreads();
