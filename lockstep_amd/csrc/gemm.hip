@@ -1189,7 +1189,7 @@ __global__ __launch_bounds__(256) void gemv_i8_row_kernel(const int8_t* __restri
 // (quant_one), then streams its weight rows as gemv_i8_row_kernel does, its first weight row
 // requested before x.  All blocks compute the same asc and q.  K % 16 == 0, K <= 512 NV WV; x 16-byte
 // aligned.
-template <int NC, int NV, int DT, int WV = 4>
+template <int NC, int NV, int DT, int WV = 4, int PF = 2>
 __global__ __launch_bounds__(WV * 64) void gemv_i8_rowq_kernel(const void* __restrict__ X, const int8_t* __restrict__ W,
                                                                int ldw, int N, int K, int wk, int rpw, EpiParams ep) {
   constexpr int kThr = WV * 64;
@@ -1233,9 +1233,11 @@ __global__ __launch_bounds__(WV * 64) void gemv_i8_rowq_kernel(const void* __res
       xr[j][h] = c < K8 ? ((const uint4*)X)[(int64_t)c * kXW + h] : make_uint4(0, 0, 0, 0);
   }
   __builtin_amdgcn_sched_barrier(0);
-  v4i w0[NC], w1[NC];
-  load_row(w0, 0);
-  if (rpw > 1) load_row(w1, 1);
+  // the wave's first PF weight rows, all in flight while x is quantised
+  v4i w[PF][NC];
+#pragma unroll
+  for (int p = 0; p < PF; ++p)
+    if (p < rpw) load_row(w[p], p);
   __builtin_amdgcn_sched_barrier(0);
   // the column operands of the lane that stores row r0 + lane (used at the end)
   const bool owner = ks == 0 && lane < rpw && r0 + lane < nrows;
@@ -1271,12 +1273,7 @@ __global__ __launch_bounds__(WV * 64) void gemv_i8_rowq_kernel(const void* __res
   for (int j = 0; j < NV; ++j) {
     const int c = tid + j * kThr;
     if (c < K8) {
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) lo |= ((uint32_t)(uint8_t)quant_one(v[j][e], sc, rs)) << (8 * e);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hi |= ((uint32_t)(uint8_t)quant_one(v[j][4 + e], sc, rs)) << (8 * e);
-      *(uint2*)(qs + 8 * c) = make_uint2(lo, hi);
+      *(uint2*)(qs + 8 * c) = quant8_pack(v[j], sc, rs);
     }
   }
   __syncthreads();
@@ -1296,17 +1293,16 @@ __global__ __launch_bounds__(WV * 64) void gemv_i8_rowq_kernel(const void* __res
     acc = wave_sum_i32(acc);
     if (lane == 0) red[wave][i] = acc;
   };
-  // two register sets in turn, each reloaded as soon as its row is summed
-  for (int i = 0; i < rpw; i += 2) {
-    row_sum(w0, i);
-    __builtin_amdgcn_sched_barrier(0);
-    if (i + 2 < rpw) load_row(w0, i + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    if (i + 1 >= rpw) break;
-    row_sum(w1, i + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    if (i + 3 < rpw) load_row(w1, i + 3);
-    __builtin_amdgcn_sched_barrier(0);
+  // PF register sets in turn, each reloaded as soon as its row is summed
+  for (int i = 0; i < rpw; i += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      if (i + p >= rpw) break;
+      row_sum(w[p], i + p);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + p + PF < rpw) load_row(w[p], i + p + PF);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   __syncthreads();
   // the K-slices of each row: one lane per row of the row group
@@ -1746,7 +1742,8 @@ int launch_gemv_rowq(const void* x, int x_dtype, const int8_t* w, int ldw, int N
     // long rows: 16-wave blocks (four K-slices of up to 4 KB per row, RPW rows per wave) so that
     // each block's read of x serves 4 RPW weight rows and about 256 blocks cover N.  (Llama-3.1-8B
     // down, M = 1, graph replays: 16.0 us as two launches -> 13.5 us; RPW 1 / 2 / 4 / 8: 22.0 / 17.2
-    // / 13.5 / 16.1 us.  Up to K = 4096 the four-wave blocks measured level with this form.)
+    // / 13.5 / 16.1 us.  Up to K = 4096 the four-wave blocks measured level with this form.  All four
+    // rows of a wave in flight before the quant, PF = 4: 14.5 against 13.4 us.)
     const int wk = 4;
     int rpw = (N * wk / 16 + 255) / 256;
     rpw = rpw < 1 ? 1 : (rpw > 16 ? 16 : rpw);
@@ -1755,7 +1752,7 @@ int launch_gemv_rowq(const void* x, int x_dtype, const int8_t* w, int ldw, int N
     const int blocks = (N + rows_blk - 1) / rows_blk;
 #define LSK_RQL(DTV)                                                                                       \
   {                                                                                                        \
-    hipLaunchKernelGGL((gemv_i8_rowq_kernel<4, 2, DTV, 16>), dim3((unsigned)blocks), dim3(1024), 0, s, x, w, ldw, N, \
+    hipLaunchKernelGGL((gemv_i8_rowq_kernel<4, 2, DTV, 16, 2>), dim3((unsigned)blocks), dim3(1024), 0, s, x, w, ldw, N, \
                        K, wk, rpw, ep);                                                                    \
     return check_launch("gemv_i8_rowq_kernel");                                                            \
   }

@@ -160,6 +160,36 @@ LSK_DEV int8_t quant_one(float v, float s, float r) {
   return (int8_t)(int)t;
 }
 
+// quant_one of eight elements, packed as int8 bytes (element e in byte e % 4 of word e / 4), in
+// fewer VALU instructions: the near-half-integer test of an element is |(|y - rint(y)|) - 0.5| <
+// 2^-13, the same set as rint_div8's |y - floor(y) - 0.5| < 2^-13 (with f = y - floor(y),
+// |y - rint(y)| = min(f, 1 - f), and both differences are exact for |y| < 2^23, where the test is
+// decided), with one ballot for the eight; the clamped value (a NaN becomes -127 through fmaxf, as
+// in quant_one) plus 128 is an integer in [1, 255] that v_cvt_pk_u8_f32 writes into its byte
+// exactly, and the xor with 0x80 turns that byte into the value's two's-complement byte.
+LSK_DEV uint2 quant8_pack(const float (&v)[8], float s, float r) {
+  float t[8];
+  bool near = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float y = f32_mul(v[e], r);
+    t[e] = rintf(y);
+    near |= fabsf(fabsf(y - t[e]) - 0.5f) < 0x1p-13f;
+  }
+  if (__builtin_amdgcn_ballot_w64(near) != 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = f32_mul(v[e], r);
+      if (fabsf(fabsf(y - t[e]) - 0.5f) < 0x1p-13f) t[e] = rintf(f32_div(v[e], s));
+    }
+  }
+  uint32_t w[2] = {0, 0};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    w[e >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(f32_add(fminf(fmaxf(t[e], -127.0f), 127.0f), 128.0f), e & 3, w[e >> 2]);
+  return make_uint2(w[0] ^ 0x80808080u, w[1] ^ 0x80808080u);
+}
+
 // Load 8 consecutive elements of dtype DT (16-byte aligned) as binary32.
 template <int DT>
 LSK_DEV void load8_as_f32(const void* x, int64_t i8, float* v) {

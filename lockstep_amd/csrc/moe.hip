@@ -1686,10 +1686,14 @@ __global__ __launch_bounds__(256) void moe_route_gemv1_kernel(MoeGemmArgs a, uin
   v4i act[NC];
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    uint32_t pk[4] = {0, 0, 0, 0};
+    float lo8[8], hi8[8];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) pk[q >> 2] |= ((uint32_t)(uint8_t)quant_one(xv[j][q], sc, rs)) << (8 * (q & 3));
-    act[j] = v4i{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+    for (int q = 0; q < 8; ++q) {
+      lo8[q] = xv[j][q];
+      hi8[q] = xv[j][8 + q];
+    }
+    const uint2 p0 = quant8_pack(lo8, sc, rs), p1 = quant8_pack(hi8, sc, rs);
+    act[j] = v4i{(int)p0.x, (int)p0.y, (int)p1.x, (int)p1.y};
   }
 
   // block 0's first wave: the routing outputs and the one-token dispatch

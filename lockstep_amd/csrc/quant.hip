@@ -97,12 +97,7 @@ __global__ __launch_bounds__(THREADS) void rowquant_kernel(const void* __restric
           }
         }
       }
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= ((uint32_t)(uint8_t)quant_one(v[j], s, rs)) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= ((uint32_t)(uint8_t)quant_one(v[4 + j], s, rs)) << (8 * j);
-      ((uint2*)qrow)[c] = make_uint2(lo, hi);
+      ((uint2*)qrow)[c] = quant8_pack(v, s, rs);
     }
   } else {
     for (int64_t k = tid; k < K; k += THREADS) qrow[k] = quant_one(load_as_f32(x, dtype, base + k), s, rs);
@@ -144,13 +139,8 @@ __global__ __launch_bounds__(THREADS) void rowquant_reg_kernel(const void* __res
   for (int j = 0; j < NV; ++j) {
     const int64_t c = tid + (int64_t)j * THREADS;
     if (c < K8) {
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) lo |= ((uint32_t)(uint8_t)quant_one(v[j][e], s, rs)) << (8 * e);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hi |= ((uint32_t)(uint8_t)quant_one(v[j][4 + e], s, rs)) << (8 * e);
       // 8 elements from K byte 8c: ((8c) >> 6) * 128 + (8c & 63) in the row-pair layout
-      *(uint2*)(qrow + (PAIR ? (c >> 3) * 128 + (c & 7) * 8 : c * 8)) = make_uint2(lo, hi);
+      *(uint2*)(qrow + (PAIR ? (c >> 3) * 128 + (c & 7) * 8 : c * 8)) = quant8_pack(v[j], s, rs);
     }
   }
 }

@@ -554,6 +554,15 @@ def test_rowquant_near_half_integer_quotients(dtype, K):
     rq, rasc = C.rowquant(x)
     assert np.array_equal(bits(asc), f32_bits(rasc))
     assert np.array_equal(bits(q), rq)
+    # the same rows one at a time through the one-row GEMV with the row quant fused in
+    from lockstep_amd import lockstep_fullstack as FS
+    r = _rng(K)
+    N = 40
+    W8 = r.integers(-127, 128, (N, K), dtype=np.int8)
+    ws = r.uniform(1e-3, 1e-2, N).astype(F32)
+    for i in range(x.shape[0]):
+        y = FS.w8a8_matmul(xd[i:i + 1], to_dev(W8), to_dev(ws), out_dtype=torch.bfloat16)
+        assert np.array_equal(bits(y), C.w8a8_matmul(x[i:i + 1], W8, ws, None, "bf16")), i
 
 
 def test_bf16_conversion_instruction_equals_rne_on_every_binary32():
