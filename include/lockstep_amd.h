@@ -570,7 +570,9 @@ int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const 
 /* Tuning control with no counterpart in the reference: 1 (the default) runs a one-token int8 layer
  * routed from its logits (lsk_moe_args.logits, the grouped GEMV path, k <= 8) with the router, the
  * row quant of x and the gate/up GEMV in one launch, every wave routing the token and quantising x
- * itself; 0 runs them as the prep launch and the GEMV.  Results are identical.  Thread-local. */
+ * itself; 0 runs them as the prep launch and the GEMV.  Also (1) int8 layers of more than 256
+ * tokens routed from logits (E <= 256, H <= 4096, no rotation) route and quantise x in one launch,
+ * a wave per token; 0 runs the router and lsk_rowquant.  Results are identical.  Thread-local. */
 int lsk_moe_fuse_route(int on);
 
 /* Tuning control with no counterpart in the reference: the int8 grouped expert GEMMs of

@@ -125,6 +125,52 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const void* __restrict
   route_token<EPL>(g, gdt, ldg, t, E, k, renorm, tab, idx_out, w_out);
 }
 
+// Layers of more than 256 tokens routed from logits: the router and the row quant of x in one launch
+// (router_topk_kernel's and lsk_rowquant's values).  One wave per token: its row of x (bf16, H % 8
+// == 0, H <= 512 NXC, 16-byte aligned) is requested first, the wave routes the token
+// (route_token), takes the row's maximum over the wave and writes asc[t] = fl32(max(amax, 1e-8) /
+// 127) and the row's int8 values (quant8_pack, row-major, row stride H).
+template <int EPL, int NXC>
+__global__ __launch_bounds__(256) void moe_route_rowq_kernel(const void* __restrict__ g, int gdt, int64_t ldg, int T,
+                                                             int E, int k, int renorm, const int32_t* __restrict__ tab,
+                                                             int64_t* __restrict__ idx_out, uint16_t* __restrict__ w_out,
+                                                             const uint16_t* __restrict__ x, int H,
+                                                             int8_t* __restrict__ q, float* __restrict__ asc) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves; no barrier follows
+  const int lane = threadIdx.x & 63;
+  const int H8 = H >> 3;
+  const uint4* xr = (const uint4*)(x + (int64_t)t * H);
+  uint4 u[NXC];
+#pragma unroll
+  for (int j = 0; j < NXC; ++j) {
+    const int c = lane + 64 * j;
+    u[j] = c < H8 ? xr[c] : make_uint4(0, 0, 0, 0);
+  }
+  route_token<EPL>(g, gdt, ldg, t, E, k, renorm, tab, idx_out, w_out);
+  float v[NXC][8];
+  float am = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NXC; ++j) {
+    const uint32_t wd[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[j][2 * e] = bf16_to_f32((uint16_t)(wd[e] & 0xffff));
+      v[j][2 * e + 1] = bf16_to_f32((uint16_t)(wd[e] >> 16));
+      am = fmaxf(am, fmaxf(fabsf(v[j][2 * e]), fabsf(v[j][2 * e + 1])));
+    }
+  }
+  am = wave_fmax(am);
+  const float sc = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, sc);
+  if (lane == 0) asc[t] = sc;
+  uint2* qr = (uint2*)(q + (int64_t)t * H);
+#pragma unroll
+  for (int j = 0; j < NXC; ++j) {
+    const int c = lane + 64 * j;
+    if (c < H8) qr[c] = quant8_pack(v[j], sc, rs);
+  }
+}
+
 // ---------------------------------------------------------------- dispatch
 // Rows are placed expert-major, token-ascending inside each expert: a counting sort over
 // chunks of 256 tokens whose in-chunk ranks come from per-expert token bitmasks (no atomics
@@ -2689,13 +2735,30 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // gate/up GEMV in one launch (moe_route_gemv1_kernel; no prep launch)
   const bool route_gemv1 = route_in_prep && T == 1 && use_gemv && !mx && k <= 8 && H % 16 == 0 && H <= 4096 &&
                            I <= 2048 && ((uintptr_t)a->x & 15) == 0 && g_rowq1;
-  if (a->logits && !route_in_prep) {
+  // above 256 tokens (int8 experts, no rotation): the router and the row quant of x in one launch
+  const bool route_rowq = a->logits && !route_in_prep && !prep_decode && rb == 0 && !mx && H % 8 == 0 &&
+                          H <= 4096 && E <= 256 && ((uintptr_t)a->x & 15) == 0 && g_rowq1;
+  int rc;
+  if (route_rowq) {
+    const dim3 grid((unsigned)((T + 3) / 4)), blk(256);
+#define LSK_RRQ(EPLV, NXCV)                                                                                  \
+  hipLaunchKernelGGL((moe_route_rowq_kernel<EPLV, NXCV>), grid, blk, 0, s, a->logits, a->logits_dtype,       \
+                     a->ld_logits, (int)T, (int)E, k, a->renormalize, a->router_tab, a->idx_out, a->w_out, a->x, \
+                     (int)H, w.qx, w.ascx)
+#define LSK_RRQ_E(NXCV) \
+  if (E <= 64) LSK_RRQ(1, NXCV); else if (E <= 128) LSK_RRQ(2, NXCV); else LSK_RRQ(4, NXCV);
+    if (H <= 512) LSK_RRQ_E(1) else if (H <= 1024) LSK_RRQ_E(2) else if (H <= 2048) LSK_RRQ_E(4) else LSK_RRQ_E(8)
+#undef LSK_RRQ_E
+#undef LSK_RRQ
+    if ((rc = lsk::check_launch("moe_route_rowq_kernel"))) return rc;
+  } else if (a->logits && !route_in_prep) {
     const int rrc = lsk_router_topk(a->logits, a->logits_dtype, a->ld_logits, T, E, k, a->renormalize, a->router_tab,
                                     a->idx_out, a->w_out, stream);
     if (rrc) return rrc;
   }
-  int rc;
-  if (prep_decode) {
+  if (route_rowq) {
+    rc = LSK_OK;  // x quantised above
+  } else if (prep_decode) {
     rc = LSK_OK;  // the prep kernel below quantises x
   } else if (rb > 0) {
     // xrot = fwht_blocks(fl32(x)): widen, then butterfly in place

@@ -406,6 +406,31 @@ def test_moe_forward_from_logits(T):
         assert np.array_equal(u16(dw), w)
 
 
+@pytest.mark.parametrize("T,E,k,H,I", [(300, 128, 8, 2048, 128), (260, 200, 6, 4096, 64), (400, 64, 2, 1040, 64)])
+def test_moe_route_and_row_quant_in_one_launch(T, E, k, H, I):
+    """Past 256 tokens the router and the row quant of x run in one launch (a wave per token;
+    E up to 256, H up to 4096, H % 8 == 0): y, idx and w equal the oracle's and the two-launch
+    path's (lsk_moe_fuse_route(0)), for one to eight chunks of 512 values per lane and 64 to 256
+    experts."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("route + row quant", dict(T=T, E=E, k=k, H=H, I=I))
+    x, experts, logits = WL.moe_inputs(T, E, k, H, I, seed=T + E)
+    idx, w = routing_from_logits(logits, k)
+    ref = C.moe_forward(x, oracle_experts(experts), idx, w, act=C.act_silu)
+    dx, dexp, g = bf16_dev(x), device_experts(experts), bf16_dev(logits)
+    for fuse in (1, 0):
+        L.call("lsk_moe_fuse_route", fuse)
+        try:
+            y, di, dw = MR.moe_forward(dx, None, dexp, k, True, _tab(), 0, MR.act_silu, logits=g)
+        finally:
+            L.call("lsk_moe_fuse_route", 1)
+        assert np.array_equal(u16(y), ref), fuse
+        assert np.array_equal(di.cpu().numpy(), idx), fuse
+        assert np.array_equal(u16(dw), w), fuse
+
+
 @pytest.mark.parametrize("T", [1, 6, 40])
 @pytest.mark.parametrize("wfmt", [1, 2])
 def test_moe_mx_forward_from_logits(T, wfmt):
