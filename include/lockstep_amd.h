@@ -383,6 +383,16 @@ int lsk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows,
  * *bad (device int32, caller-zeroed) receives 1 if some m2 is not 2 * an E2M1 value. */
 int lsk_mx_pack_m2(const int8_t* m2, int64_t n, uint8_t* packed, int32_t* bad, void* stream);
 
+/* A prepared copy of MXFP4 expert codes with no counterpart in the reference (the same weights; the
+ * skinny grouped MX GEMM of lsk_moe_forward reads it instead of the [rows, K/2] codes, one whole
+ * kilobyte per wave load): for each group g of 16 rows, each step s of four 32-blocks and each row
+ * c of the group, 64 bytes = the four blocks' 16 code bytes, block by block (rows past `rows` and
+ * blocks past K/32 are zero).  codes: [rows, K/2] uint8 (row stride ldw bytes, 4-byte aligned,
+ * ldw % 4 == 0); out: lsk_mx_skinny_bytes(rows, K) bytes, 16-byte aligned.  K % 32 == 0.  Made
+ * once per weight, like the row-pair copies of the int8 experts. */
+int64_t lsk_mx_skinny_bytes(int64_t rows, int64_t K);
+int lsk_mx_skinny_pack(const uint8_t* codes, int64_t ldw, int64_t rows, int64_t K, uint8_t* out, void* stream);
+
 /* ---------------------------------------------------------------- mixture of experts (v3) */
 
 /* Activation of the gate/up pair in the expert block. */
@@ -499,12 +509,13 @@ typedef struct {
   /* Kernel choice for this call only (no reference counterpart; results are the same bits either
    * way): 0 keeps the calling thread's lsk_moe_select / lsk_moe_mx_select settings; select = v + 2
    * applies lsk_moe_select(v) (v in [-1, 7]) and mx_select = v + 1 applies lsk_moe_mx_select(v)
-   * (v in [0, 2]) to this call, leaving the thread's settings as they were. */
+   * (v in [0, 3]) to this call, leaving the thread's settings as they were. */
   int select;
   int mx_select;
   /* NULL, or per expert the same int8 weights in the row-pair layout (lsk_pack_row_pairs of the
    * [2I, H] and [H, I] matrices; row stride (K + 63) / 64 * 64), which the ping-pong expert tiles
-   * read instead (int8 experts; the same results). */
+   * read instead (int8 experts; the same results).  MXFP4 experts (wfmt 1): NULL, or per expert
+   * the codes' skinny-layout copies (lsk_mx_skinny_pack), read by the skinny grouped MX GEMM. */
   const int64_t* w13_pair_ptrs;
   const int64_t* w2_pair_ptrs;
 } lsk_moe_args;
@@ -528,6 +539,15 @@ int lsk_moe_forward(const lsk_moe_args* args, void* stream);
  * copies (w13_pair_ptrs / w2_pair_ptrs); 0 otherwise.  No device work, callable without a GPU: a
  * caller makes the copies only when a call will read them. */
 int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int select);
+
+/* No counterpart in the reference: 1 when lsk_moe_forward on MXFP4 experts with per-row activation
+ * scales (wfmt 1), T tokens, top-k over E experts, hidden H, intermediate I and E8M0 row strides
+ * lds13 / lds2, under the per-call choices select / mx_select (lsk_moe_args) and the calling
+ * thread's settings, reads the experts' skinny-layout code copies (lsk_mx_skinny_pack of the
+ * [2I, H/2] and [H, I/2] codes, passed as w13_pair_ptrs / w2_pair_ptrs); 0 otherwise.  No device
+ * work, callable without a GPU. */
+int lsk_moe_mx_reads_skinny(int64_t T, int k, int64_t E, int64_t H, int64_t I, int64_t lds13, int64_t lds2,
+                            int select, int mx_select);
 
 /* One grouped expert linear over rows already sorted by expert: expert e owns rows
  * offs[e] .. offs[e + 1] - 1 (offs [E + 1] int32 on the device, nondecreasing) of a, and
@@ -611,8 +631,12 @@ int lsk_moe_pp_skinny_rows(int rows);
 /* Tuning control with no counterpart in the reference: the main loop of the grouped MXFP4
  * expert GEMMs (0: direct-to-LDS operand staging with fp4 fragments converted per wave, a
  * two-stage ring, three blocks per CU, the default; 1: register-staged operands converted to bf16
- * before LDS; 2: as 0 with a three-stage ring and two blocks per CU).  Results are identical; only
- * speed differs.  The choice applies to the calling host thread's later launches only (thread-local). */
+ * before LDS; 2: as 0 with a three-stage ring and two blocks per CU; 3: as 0, with the skinny
+ * grouped MX GEMM -- an expert's rows 16 at a time in LDS, the codes streamed into the bf16 MFMA --
+ * wherever the layer can take it, which 0 does by size: MXFP4 layers with per-row activation
+ * scales past the decode GEMV's token counts while T k < 16 E, up to 256 tokens).  Results are
+ * identical; only speed differs.  The choice applies to the calling host thread's later launches
+ * only (thread-local). */
 int lsk_moe_mx_select(int variant);
 
 /* ---------------------------------------------------------------- diagnostics */

@@ -82,8 +82,11 @@ SIGNATURES = {
     "lsk_act_table": (_I, [_P, _I, _P, _P]),
     "lsk_gemm_mx2": (_I, [_P, _I64, _P, _I64, _P, _I, _I64, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _P]),
     "lsk_mx_pack_m2": (_I, [_P, _I64, _P, _P, _P]),
+    "lsk_mx_skinny_bytes": (_I64, [_I64, _I64]),
+    "lsk_mx_skinny_pack": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lsk_moe_workspace": (_I64, [_I64, _I, _I64, _I64, _I64, _I, _I]),
     "lsk_moe_forward": (_I, [_P, _P]),
+    "lsk_moe_mx_reads_skinny": (_I, [_I64, _I, _I64, _I64, _I64, _I64, _I64, _I, _I]),
     "lsk_grouped_gemm_workspace": (_I64, [_I64, _I64]),
     "lsk_grouped_gemm_w8a8": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P, _I64, _P]),
     "lsk_grouped_gemm_w8a8_pairs": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _P, _P, _I64,

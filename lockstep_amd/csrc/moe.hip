@@ -2623,10 +2623,34 @@ extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, i
   return r ? 1 : 0;
 }
 
+// Whether an MXFP4 layer (per-row activation scales) past the MX GEMV's token counts takes the skinny
+// grouped MX GEMM: by size (T k < 16 E, up to 256 tokens) under lsk_moe_mx_select(0), wherever it
+// fits under (3); its LDS (the chunk's bf16 rows and the E8M0 rows) within 160 KB; no rotation.
+static bool mx_takes_skinny(int64_t T, int k, int64_t E, int64_t H, int64_t I, int64_t lds13, int64_t lds2, int rb) {
+  const bool mx_gemv = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : T <= kMxGemvMaxT);
+  return !mx_gemv && rb == 0 && T >= 1 && T <= kSkinnyMaxT && H % 32 == 0 && I % 32 == 0 &&
+         (lsk::mx_variant() == 3 || (lsk::mx_variant() == 0 && g_moe_force < 0 && T * k < 16 * E)) &&
+         lsk::moe_mx_skinny_lds(H, lds13) <= 160 * 1024 && lsk::moe_mx_skinny_lds(I, lds2) <= 160 * 1024;
+}
+
+extern "C" int lsk_moe_mx_reads_skinny(int64_t T, int k, int64_t E, int64_t H, int64_t I, int64_t lds13, int64_t lds2,
+                                       int select, int mx_select) {
+  if (T <= 0 || k < 1 || E < 1 || H <= 0 || I <= 0 || select < 0 || select > 9 || mx_select < 0 || mx_select > 4)
+    return 0;
+  const int force = g_moe_force, w4 = g_moe_w4, mxv = lsk::mx_variant();
+  if (select) lsk_moe_select(select - 2);
+  if (mx_select) lsk_moe_mx_select(mx_select - 1);
+  const bool r = mx_takes_skinny(T, k, E, H, I, lds13, lds2, 0);
+  g_moe_force = force;
+  g_moe_w4 = w4;
+  lsk_moe_mx_select(mxv);
+  return r ? 1 : 0;
+}
+
 extern "C" int lsk_moe_forward(const lsk_moe_args* a, void* stream) {
   LSK_REQUIRE(a, "lsk_moe_forward: null args");
-  LSK_REQUIRE(a->select >= 0 && a->select <= 9 && a->mx_select >= 0 && a->mx_select <= 3,
-              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 9] / [0, 3]", a->select, a->mx_select);
+  LSK_REQUIRE(a->select >= 0 && a->select <= 9 && a->mx_select >= 0 && a->mx_select <= 4,
+              "lsk_moe_forward: select=%d / mx_select=%d outside [0, 9] / [0, 4]", a->select, a->mx_select);
   if (a->select == 0 && a->mx_select == 0) return moe_forward_call(a, stream);
   // this call's kernel choice, the thread's own restored afterwards
   const int force = g_moe_force, w4 = g_moe_w4, mxv = lsk::mx_variant();
@@ -2715,6 +2739,11 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // quantised in the general form) with the block exponents (T = 1 50 vs 116 us, T = 16 221 vs
   // 278 us, T = 24 281 vs 277 us)
   const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
+  // MXFP4 experts (per-row scales) holding few rows each past the GEMV's token counts: the skinny
+  // grouped MX GEMM on the experts' skinny-layout copies (w13_pair_ptrs / w2_pair_ptrs for MXFP4
+  // experts), when the caller has them
+  const bool use_mx_skinny = mx == 1 && !use_mx_gemv && a->w13_pair_ptrs && a->w2_pair_ptrs &&
+                             mx_takes_skinny(T, k, E, H, I, a->lds13, a->lds2, rb);
   // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
   // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
   const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && !use_skinny && I % 64 == 0 &&
@@ -2857,6 +2886,10 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
     g1.mx2 = 2;
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (use_mx_skinny) {
+    g1.w_ptrs = a->w13_pair_ptrs;
+    g1.w_bytes = lsk::mx_skinny_bytes(2 * I, H);
+    if ((rc = lsk::launch_moe_mx_skinny(0, g1, w.max_tiles, a->mx_safe, w.gu, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (route_gemv1) {
@@ -2900,7 +2933,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   } else if ((rc = launch_moe_gemm<0>(g1, w.max_tiles, (int)((I + 63) / 64), s, "moe_gemm_kernel<gate_up>"))) {
     return rc;
   }
-  if (use_gemv || use_skinny || use_mx_gemv) {
+  if (use_gemv || use_skinny || use_mx_gemv || use_mx_skinny) {
     const int per = (int)((I + 1023) / 1024);
     const dim3 grid((unsigned)R), blk(1024);
 #define LSK_ACTQ(P)                                                                                             \
@@ -2964,6 +2997,10 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
     g2.mx2 = 2;
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
+  } else if (use_mx_skinny) {
+    g2.w_ptrs = a->w2_pair_ptrs;
+    g2.w_bytes = lsk::mx_skinny_bytes(H, I);
+    if ((rc = lsk::launch_moe_mx_skinny(1, g2, w.max_tiles, a->mx_safe, nullptr, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (use_gemv && T == 1 && k <= 8 && I <= 2048) {

@@ -58,6 +58,12 @@ int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int s
 int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,
                        hipStream_t s);
 
+// Skinny grouped MX GEMM (experts with few rows; per-row activation scales): the chunk's rows in
+// LDS, the codes streamed into the bf16 MFMA (mode 0: gate / up values into gu; mode 1: slot rows).
+int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, uint16_t* gu, hipStream_t s);
+int moe_mx_skinny_lds(int64_t K, int64_t lds);
+int64_t mx_skinny_bytes(int64_t rows, int64_t K);
+
 // Row quant emitting the int8 values as bf16 (the MX GEMM's operand form).
 int launch_rowquant_bf16(const uint16_t* x, int64_t T, int64_t H, uint16_t* q, float* asc, hipStream_t s);
 

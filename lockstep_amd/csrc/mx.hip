@@ -532,7 +532,8 @@ unsigned grid_for(int64_t n) {
 }
 
 thread_local int g_mx_variant = 0;  // grouped MX main loop: 0 direct-to-LDS, two-stage ring, three blocks per CU (mx_pp.h);
-                       // 1 register-staged (mx_tile.h); 2 direct-to-LDS, three-stage ring, two blocks per CU
+                       // 1 register-staged (mx_tile.h); 2 direct-to-LDS, three-stage ring, two blocks per CU;
+                       // 3 as 0, with the skinny grouped GEMM wherever the layer can take it
 
 template <int MODE, bool SAFE>
 int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s) {
@@ -562,7 +563,7 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
     return lsk::check_launch(MODE == 0 ? "moe_mx_gemm_kernel<gate_up>" : "moe_mx_gemm_kernel<down>");
   }
   static_assert(lsk::MxPPCfg<2>::kRingBytes >= Cfg::kEpiBytes, "the epilogue strips fit in the ring");
-  if (g_mx_variant == 0) {
+  if (g_mx_variant == 0 || g_mx_variant == 3) {
     static std::atomic<bool> attr_pp2{false};
     auto kern = moe_mx_pp_kernel<MODE, SAFE, 2>;
     if (!attr_pp2) {
@@ -844,6 +845,186 @@ int launch_mx_gemv(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uin
   return launch_mx_gemv_mr<MODE, 4, SAFE, MX2>(ga, max_tiles, gu, s, name);
 }
 
+// ---------------------------------------------------------------- skinny grouped MX GEMM
+// MXFP4 experts holding few routed rows each (layers of tens of tokens): the layout of moe.hip's
+// skinny int8 kernel on the bf16 MFMA.  A block takes one expert tile's rows 16 at a time, copied
+// into LDS as their bf16 values, and 16 groups of 16 weight rows, one per wave, each over the whole
+// K (the ordered block updates cannot be split over K).  For block b, lane (col, g) of a wave holds
+// the 4 code bytes of k = 32 b + 8 g .. + 7 of weight row 16 w + col, converted to the doubled
+// mantissas as moe_mx_pp's main loop does, and the same k of activation row col; the MFMA's sum
+// s_b of (row 4 g + i, col) is applied in block order as acc = fl32(acc + s_b 2^(e - 128)) (one
+// FMA; with SAFE the product and the sum apart), e the weight row's E8M0 byte of block b, staged
+// in LDS per wave with one contiguous copy of the group's rows.  The codes come from the experts'
+// skinny-layout copies (lsk_mx_skinny_pack: per group of 16 rows and step of 4 blocks, lane
+// (col, g)'s 4 code bytes of the 4 blocks side by side, so a wave reads each step as one
+// contiguous 1 KB; the codes' own layout, 16 bytes per row and block, measured 2.6x slower for the
+// whole layer) and stream D steps ahead of their MFMAs in registers, so each expert's codes are read
+// once per 16-row chunk.  The epilogue is
+// moe_mx_gemv_kernel's: the bias-added gate / up values into gu (mode 0), the routing-weighted slot
+// rows (mode 1).  LDS: the chunk's rows [16][ldsk], the waves' E8M0 bytes [16][scb], the rows'
+// operands.
+template <int MODE, bool SAFE, int D>
+__global__ __launch_bounds__(1024) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu, int sets,
+                                                             int ldsk, int scb) {
+  extern __shared__ __attribute__((aligned(16))) char smem_mxs[];
+  constexpr int CR = 16;
+  const int lane = threadIdx.x & 63, wave = wave_id(), tid = threadIdx.x;
+  const int mt = blockIdx.x / sets, gs = blockIdx.x - (blockIdx.x / sets) * sets;
+  if (mt >= a.tiles[0]) return;  // the whole block leaves
+  const int e = a.tiles[1 + 2 * mt];
+  const int p0 = a.tiles[2 + 2 * mt];
+  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  const int K = a.K, nb = K >> 5;
+  const int NWR = MODE == 0 ? 2 * a.N : a.N;  // weight rows
+  const int G = (NWR + 15) >> 4;
+  const int g = gs * 16 + wave;  // this wave's group of 16 weight rows (wave-uniform)
+  const int col = lane & 15, kg = lane >> 4;
+  const int n = g * 16 + col;
+  const bool live = g < G && n < NWR;
+  const float* bp = a.b_ptrs ? (const float*)a.b_ptrs[e] : nullptr;
+  const __amdgpu_buffer_rsrc_t rcb = lsk::make_rsrc(bp, bp ? 4 * (int64_t)NWR : 0);
+  const float c_b =
+      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcb, (live && bp) ? (uint32_t)(4 * n) : lsk::kOob, 0, 0));
+  const __amdgpu_buffer_rsrc_t rw = lsk::make_rsrc((const void*)wave_uniform64(a.w_ptrs[e]), a.w_bytes);
+  const __amdgpu_buffer_rsrc_t rsc =
+      lsk::make_rsrc((const void*)wave_uniform64(a.ws_ptrs[e]), (int64_t)NWR * a.lds);
+  const __amdgpu_buffer_rsrc_t ra = lsk::make_rsrc(a.A, a.a_bytes);
+  const int nst = (nb + 3) >> 2;  // steps of 4 blocks
+  // this lane's 16 code bytes of step s (blocks 4 s .. 4 s + 3, 4 bytes each) at wbase + 1024 s
+  const uint32_t wbase = g < G ? (uint32_t)(((g * nst) * 16 + col) * 64 + kg * 16) : lsk::kOob;
+  char* sc_w = smem_mxs + CR * ldsk + wave * scb;
+  int* r_src = (int*)(smem_mxs + CR * ldsk + 16 * scb);
+  float* r_asc = (float*)(r_src + CR);
+  float* r_w = r_asc + CR;
+  int* r_dst = (int*)(r_w + CR);
+  // the group's E8M0 rows 16 g .. 16 g + 15: one contiguous run of 16 lds bytes (zeros past NWR)
+  {
+    const int sbytes = 16 * (int)a.lds;
+    const uint32_t sbase = (uint32_t)(g * 16) * (uint32_t)a.lds;
+    for (int j = 0; j * 1024 < sbytes; ++j) {
+      const int o = j * 1024 + lane * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lsk::lds_void_t)(sc_w + j * 1024), 16,
+                                               (g < G && o < sbytes) ? sbase + (uint32_t)o : lsk::kOob, 0, 0, 0);
+    }
+  }
+  const int cpr = (2 * K + 1023) >> 10;  // 1 KB chunks of an activation row
+  const char* arow = smem_mxs + col * ldsk + 16 * kg;              // A fragment of block b at + 64 b
+  const uint8_t* srow = (const uint8_t*)sc_w + col * (int)a.lds;  // E8M0 byte of block b at [b]
+  lsk::compiler_fence();
+  for (int q0 = p0; q0 < p1; q0 += CR) {
+    const int nr = min(CR, p1 - q0);
+    if (q0 > p0) __syncthreads();  // the previous chunk's LDS reads are done
+    v4i cw[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+      cw[u] = lsk::buf_load16(rw, (u < nst && wbase != lsk::kOob) ? wbase + 1024u * u : lsk::kOob);
+    if (MODE == 0) {
+      // the token rows of the chunk: loaded behind the first code steps, waited for alone
+      const int src = tid < nr ? a.row_tok[q0 + tid] : 0;
+      lsk::compiler_fence();
+      if (tid < nr) r_src[tid] = src;
+      __syncthreads();
+    }
+    // the chunk's rows into LDS (bf16 values, zeros past K), then the rows' operands
+    for (int c = wave; c < nr * cpr; c += 16) {
+      const int r = c / cpr, j = c - (c / cpr) * cpr;
+      const int kb = j * 1024 + lane * 16;
+      const int src = MODE == 0 ? r_src[r] : q0 + r;
+      const uint32_t off = kb < 2 * K ? (uint32_t)(src * 2 * a.lda + kb) : lsk::kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lsk::lds_void_t)(smem_mxs + r * ldsk + j * 1024), 16, off, 0, 0,
+                                               0);
+    }
+    float o_asc = 1.0f, o_w = 1.0f;
+    int o_dst = 0;
+    if (tid < nr) {
+      const int p = q0 + tid;
+      if (a.a_scale) o_asc = a.a_scale[MODE == 0 ? r_src[tid] : p];
+      if (MODE == 1) {
+        o_w = a.row_w ? a.row_w[p] : 1.0f;
+        o_dst = a.row_dst ? a.row_dst[p] : p;
+      }
+    }
+    lsk::compiler_fence();
+    lsk::wait_vm<0>();  // rows, E8M0 bytes, the rows' operands and the first code steps
+    if (tid < nr) {
+      r_asc[tid] = o_asc;
+      r_w[tid] = o_w;
+      r_dst[tid] = o_dst;
+    }
+    __syncthreads();
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto blk = [&](int b, uint32_t q) {
+      const v4i af = *(const v4i*)(arow + 64 * b);
+      const v4i bf = v4i{(int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 0)),
+                         (int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 1)),
+                         (int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 2)),
+                         (int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 3))};
+      const v4f d = lsk::mfma_bf16(af, bf);
+      const float sc = pow2f((int)srow[b] - 128);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = SAFE ? f32_add(acc[i], f32_mul(d[i], sc)) : __builtin_fmaf(d[i], sc, acc[i]);
+    };
+    auto step = [&](int st, const v4i& q4) {
+      if (4 * st + 4 <= nb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) blk(4 * st + j, (uint32_t)q4[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (4 * st + j < nb) blk(4 * st + j, (uint32_t)q4[j]);
+      }
+    };
+    if (g < G) {
+      const int nfull = nst / D * D;
+      for (int s0 = 0; s0 < nfull; s0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+          step(s0 + u, cw[u]);
+          const int nx = s0 + u + D;
+          cw[u] = lsk::buf_load16(rw, (nx < nst && wbase != lsk::kOob) ? wbase + 1024u * nx : lsk::kOob);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < D; ++u)
+        if (nfull + u < nst) step(nfull + u, cw[u]);
+    }
+    lsk::wait_vm<0>();  // no code load outlives the chunk (the next one reuses the registers)
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * kg + i;
+        if (m < nr) {
+          float yv = bfr(f32_mul(acc[i], r_asc[m]));
+          if (bp) yv = bfr(f32_add(yv, c_b));
+          if (MODE == 0) gu[(int64_t)(q0 + m) * NWR + n] = f32_to_bf16(yv);
+          else a.y[(int64_t)r_dst[m] * a.N + n] = f32_to_bf16(f32_mul(r_w[m], yv));
+        }
+      }
+    }
+  }
+}
+
+template <int MODE, bool SAFE>
+int launch_mx_skinny(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
+  const int NWR = MODE == 0 ? 2 * ga.N : ga.N;
+  const int sets = ((NWR + 15) / 16 + 15) / 16;
+  const int ldsk = (2 * ga.K + 1023) / 1024 * 1024 + 16;
+  const int scb = (16 * (int)ga.lds + 1023) / 1024 * 1024;
+  const int smem = 16 * ldsk + 16 * scb + 4 * 16 * 4;
+  LSK_REQUIRE(smem <= 160 * 1024, "%s: %d bytes of LDS", name, smem);
+  const int64_t blocks = max_tiles * sets;
+  if (blocks == 0) return LSK_OK;
+  LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
+  auto kern = moe_mx_skinny_kernel<MODE, SAFE, SAFE ? 4 : 8>;  // steps of 4 blocks in flight
+  static std::atomic<bool> attr{false};
+  if (!attr) {
+    if (int rc = reserve_lds(kern, 160 * 1024, name)) return rc;
+    attr = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(1024), smem, s, ga, gu, sets, ldsk, scb);
+  return lsk::check_launch(name);
+}
+
 }  // namespace
 
 namespace lsk {
@@ -851,6 +1032,23 @@ namespace lsk {
 int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, hipStream_t s) {
   if (mode == 0) return safe ? launch_grouped<0, true>(ga, max_tiles, s) : launch_grouped<0, false>(ga, max_tiles, s);
   return safe ? launch_grouped<1, true>(ga, max_tiles, s) : launch_grouped<1, false>(ga, max_tiles, s);
+}
+
+// Bytes of a skinny-layout copy of rows x K packed E2M1 codes (see lsk_mx_skinny_pack).
+int64_t mx_skinny_bytes(int64_t rows, int64_t K) { return (rows + 15) / 16 * ((K / 32 + 3) / 4) * 1024; }
+
+// LDS bytes the skinny grouped MX GEMM needs for K and an E8M0 row stride lds (<= 160 KB to run).
+int moe_mx_skinny_lds(int64_t K, int64_t lds) {
+  return (int)((2 * K + 1023) / 1024 * 1024 + 16) * 16 + (int)((16 * lds + 1023) / 1024 * 1024) * 16 + 256;
+}
+
+int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, uint16_t* gu, hipStream_t s) {
+  LSK_REQUIRE(!ga.a_ka && ga.K % 32 == 0 && (mode == 1 || gu), "moe_mx_skinny: arguments");
+  if (mode == 0)
+    return safe ? launch_mx_skinny<0, true>(ga, max_tiles, gu, s, "moe_mx_skinny_kernel<gate_up>")
+                : launch_mx_skinny<0, false>(ga, max_tiles, gu, s, "moe_mx_skinny_kernel<gate_up>");
+  return safe ? launch_mx_skinny<1, true>(ga, max_tiles, nullptr, s, "moe_mx_skinny_kernel<down>")
+              : launch_mx_skinny<1, false>(ga, max_tiles, nullptr, s, "moe_mx_skinny_kernel<down>");
 }
 
 int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,
@@ -1011,8 +1209,45 @@ namespace lsk {
 int mx_variant() { return g_mx_variant; }
 }  // namespace lsk
 
+// ---------------------------------------------------------------- skinny-layout copies of MXFP4 codes
+// codes: rows x K/2 packed E2M1 bytes, row stride ldw (ldw % 4 == 0); out [ceil(rows / 16)]
+// [ceil(K / 128)][16][4][16] bytes: group of 16 rows, step of 4 blocks of 32, row of the group,
+// lane group g, then the 4 code bytes of k = 32 b + 8 g .. + 7 for the step's blocks b; zeros
+// past `rows` and past K / 32 blocks.  One thread per output dword (4-byte loads and stores).
+__global__ __launch_bounds__(256) void mx_skinny_pack_kernel(const uint8_t* __restrict__ codes, int64_t ldw,
+                                                             int64_t rows, int64_t nb, uint32_t* __restrict__ out,
+                                                             int64_t nwords) {
+  const int64_t nst = (nb + 3) / 4;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nwords; i += (int64_t)gridDim.x * 256) {
+    const int64_t j = i & 3, kg = (i >> 2) & 3, c = (i >> 4) & 15, rest = i >> 8;
+    const int64_t st = rest % nst, gi = rest / nst;
+    const int64_t r = gi * 16 + c, b = 4 * st + j;
+    uint32_t v = 0;
+    if (r < rows && b < nb) v = *(const uint32_t*)(codes + r * ldw + 16 * b + 4 * kg);
+    out[i] = v;
+  }
+}
+
+extern "C" int64_t lsk_mx_skinny_bytes(int64_t rows, int64_t K) {
+  return (rows > 0 && K > 0 && K % 32 == 0) ? lsk::mx_skinny_bytes(rows, K) : 0;
+}
+
+extern "C" int lsk_mx_skinny_pack(const uint8_t* codes, int64_t ldw, int64_t rows, int64_t K, uint8_t* out,
+                                  void* stream) {
+  LSK_REQUIRE(rows >= 0 && K > 0 && K % 32 == 0, "lsk_mx_skinny_pack: rows=%lld, K=%lld (K %% 32 == 0)",
+              (long long)rows, (long long)K);
+  if (rows == 0) return LSK_OK;
+  LSK_REQUIRE(codes && out, "lsk_mx_skinny_pack: null pointer");
+  LSK_REQUIRE(ldw >= K / 2 && ldw % 4 == 0 && ((uintptr_t)codes & 3) == 0 && ((uintptr_t)out & 15) == 0,
+              "lsk_mx_skinny_pack: ldw=%lld below K/2 or not a multiple of 4, or misaligned pointers", (long long)ldw);
+  const int64_t nwords = lsk::mx_skinny_bytes(rows, K) / 4;
+  hipLaunchKernelGGL(mx_skinny_pack_kernel, dim3(grid_for(nwords)), dim3(256), 0, (hipStream_t)stream, codes, ldw,
+                     rows, K / 32, (uint32_t*)out, nwords);
+  return lsk::check_launch("mx_skinny_pack_kernel");
+}
+
 extern "C" int lsk_moe_mx_select(int variant) {
-  LSK_REQUIRE(variant >= 0 && variant <= 2, "lsk_moe_mx_select: variant %d not in [0, 2]", variant);
+  LSK_REQUIRE(variant >= 0 && variant <= 3, "lsk_moe_mx_select: variant %d not in [0, 3]", variant);
   g_mx_variant = variant;
   return LSK_OK;
 }

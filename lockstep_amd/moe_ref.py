@@ -328,12 +328,12 @@ def kernel_choice(moe=None, mx=None):
     (lsk_moe_args.select / mx_select; no reference counterpart, the same bits either way): moe as
     lsk_moe_select's variant (-1 by size, 0 register-staged tile, 1 ping-pong tile, 2 GEMV, 3 the
     four-wave tile, 4 128-byte K stages, 5 the persistent 256x256 tile, 6 the 256x256 tile one per
-    block, 7 the skinny grouped GEMM), mx as lsk_moe_mx_select's (0, 1, 2); None keeps the calling
+    block, 7 the skinny grouped GEMM), mx as lsk_moe_mx_select's (0, 1, 2, 3); None keeps the calling
     thread's setting.  Scoped to this Python thread and the with-block."""
     if moe is not None and not -1 <= moe <= 7:
         raise ValueError("kernel_choice: moe=%r not in [-1, 7]" % (moe,))
-    if mx is not None and not 0 <= mx <= 2:
-        raise ValueError("kernel_choice: mx=%r not in [0, 2]" % (mx,))
+    if mx is not None and not 0 <= mx <= 3:
+        raise ValueError("kernel_choice: mx=%r not in [0, 3]" % (mx,))
     prev = getattr(_CHOICE, "v", (0, 0))
     _CHOICE.v = (0 if moe is None else moe + 2, 0 if mx is None else mx + 1)
     try:
@@ -499,6 +499,36 @@ class ExpertTablesMX:
         self.b2 = table(b2) if any(b2) else None
         self._keep = keep
         self._derived = _derived(pairs)
+        # the codes' skinny-layout copies (lsk_mx_skinny_pack), which the skinny grouped MX GEMM
+        # reads a kilobyte per wave load: made by skinny_ptrs() on the first call that reads them,
+        # remade when a code tensor changes in place
+        self._codes = [keep[i] for i in range(0, len(keep), 6)] + [keep[i] for i in range(1, len(keep), 6)]
+        self._skinny = None
+
+    def skinny_ptrs(self, T, k, select, mx_select):
+        """(w13_pair_ptrs, w2_pair_ptrs) for an MXFP4 layer call (per-row scales) of T tokens, top-k:
+        the tables of the skinny-layout code copies when that call reads them
+        (lsk_moe_mx_reads_skinny), else (None, None); (None, None) while a graph is being captured
+        (the graph then runs the kernels that read the codes themselves)."""
+        lib = L.load()
+        if not lib.lsk_moe_mx_reads_skinny(int(T), int(k), self.E, self.H, self.I, self.lds13, self.lds2,
+                                           int(select), int(mx_select)):
+            return None, None
+        vers = [c._version for c in self._codes]
+        if self._skinny is None or self._skinny[0] != vers:
+            if torch.cuda.is_current_stream_capturing():
+                return None, None
+            self._skinny = None
+            E = self.E
+            copies = []
+            for c, (rows, K) in zip(self._codes, [(2 * self.I, self.H)] * E + [(self.H, self.I)] * E):
+                out = torch.empty((lib.lsk_mx_skinny_bytes(rows, K),), dtype=torch.uint8, device=self.device)
+                L.call("lsk_mx_skinny_pack", L.ptr(c), int(c.stride(0)), rows, K, L.ptr(out), L.stream_of(out))
+                copies.append(out)
+            t13 = torch.tensor([t.data_ptr() for t in copies[:E]], dtype=torch.int64).to(self.device)
+            t2 = torch.tensor([t.data_ptr() for t in copies[E:]], dtype=torch.int64).to(self.device)
+            self._skinny = (vers, copies, t13, t2)
+        return self._skinny[2], self._skinny[3]
 
 
 def expert_tables_mx(experts) -> ExpertTablesMX:
@@ -580,6 +610,8 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1, route=N
     nbytes = L.load().lsk_moe_workspace(T, k, t.E, H, t.I, 0, wfmt)
     work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     kb = t.kw_bounds
+    choice = _choice_fields()
+    s13, s2 = t.skinny_ptrs(T, k, choice["select"], choice["mx_select"]) if wfmt == 1 else (None, None)
     a = L.MoeArgs(T=T, H=H, I=t.I, E=t.E, k=k, act=act, wfmt=wfmt, mx_safe=t.mx_safe, lds13=t.lds13, lds2=t.lds2,
                   kw13_min=kb[0], kw13_max=kb[1], kw2_min=kb[2], kw2_max=kb[3],
                   x=x.data_ptr(), idx=idx.data_ptr(), w=w.data_ptr(), w13_ptrs=t.w13.data_ptr(), ldw13=t.ldw13,
@@ -587,7 +619,8 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1, route=N
                   w2_ptrs=t.w2.data_ptr(), ldw2=t.ldw2, ws2_ptrs=t.ws2.data_ptr(),
                   b2_ptrs=t.b2.data_ptr() if t.b2 is not None else None, frac=ops.frac_i32(x.device).data_ptr(),
                   act_tab=_act_tab(x.device, act), rot_blk=0, rot_scale=0.0, shared=None, y=y.data_ptr(), workspace=work.data_ptr(),
-                  workspace_bytes=nbytes, **fields, **_choice_fields())
+                  workspace_bytes=nbytes, w13_pair_ptrs=s13.data_ptr() if s13 is not None else None,
+                  w2_pair_ptrs=s2.data_ptr() if s2 is not None else None, **fields, **choice)
     L.call("lsk_moe_forward", ctypes.addressof(a), L.stream_of(x))
     del keep
     return y if route is None else (y, idx, w)

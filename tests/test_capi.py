@@ -111,7 +111,7 @@ def test_moe_forward_rejects_bad_kernel_choice():
     import ctypes
     from lockstep_amd import _lib as L
     lib = L.load()
-    for sel, mxsel in ((10, 0), (0, 4), (-1, 0)):
+    for sel, mxsel in ((10, 0), (0, 5), (-1, 0)):
         a = L.MoeArgs(T=1, H=16, I=16, E=1, k=1, select=sel, mx_select=mxsel)
         assert lib.lsk_moe_forward(ctypes.addressof(a), None) != 0
         assert b"select" in lib.lsk_last_error()

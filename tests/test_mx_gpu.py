@@ -190,6 +190,83 @@ def test_config5_t4096_token_subset():
     assert np.array_equal(got[rows], ref)
 
 
+def _skinny_layout(codes, K):
+    """The skinny-layout copy of codes [rows, K/2] as lsk_mx_skinny_pack documents it, in numpy:
+    per group of 16 rows, step of 4 blocks and row of the group, the 4 blocks' 16 code bytes in
+    4-byte pieces ordered (k-quarter, block)."""
+    rows = codes.shape[0]
+    nb = K // 32
+    G, nst = (rows + 15) // 16, (nb + 3) // 4
+    c = np.zeros((G * 16, nst * 4, 16), np.uint8)
+    c[:rows, :nb] = codes[:, :K // 2].reshape(rows, nb, 16)
+    # [G, 16 rows, nst, 4 blocks, 4 quarters, 4 bytes] -> [G, nst, 16 rows, 4 quarters, 4 blocks, 4 bytes]
+    c = c.reshape(G, 16, nst, 4, 4, 4).transpose(0, 2, 1, 4, 3, 5)
+    return c.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,K,ldw", [(16, 128, 64), (37, 2880, 1440), (5, 96, 64), (64, 4096, 2048)])
+def test_mx_skinny_pack(rows, K, ldw):
+    """lsk_mx_skinny_pack against the layout restated in numpy: partial groups of 16 rows, partial
+    steps of 4 blocks, a row stride above K/2; lsk_mx_skinny_bytes its size."""
+    from lockstep_amd import _lib as L
+    say("mx skinny pack", rows, K, ldw)
+    rng = np.random.default_rng(rows * 7 + K)
+    codes = rng.integers(0, 256, size=(rows, ldw), dtype=np.uint8)
+    nbytes = L.load().lsk_mx_skinny_bytes(rows, K)
+    exp = _skinny_layout(codes, K)
+    assert nbytes == exp.size
+    dc = torch.from_numpy(codes).cuda()
+    out = torch.full((nbytes,), 0xA5, dtype=torch.uint8, device="cuda")
+    L.call("lsk_mx_skinny_pack", dc.data_ptr(), ldw, rows, K, out.data_ptr(),
+           torch.cuda.current_stream().cuda_stream)
+    assert np.array_equal(out.cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("T,E,k,H,I,big_exp", [(32, 32, 4, 2880, 2880, False), (100, 16, 2, 1088, 576, False),
+                                               (25, 8, 3, 2048, 3040, False), (40, 8, 2, 1088, 576, True)])
+def test_moe_mx_skinny(T, E, k, H, I, big_exp):
+    """The skinny grouped MX GEMM on the experts' skinny-layout code copies, taken by size past the
+    GEMV's token counts while experts hold few rows (GPT-OSS-20B at 32 tokens; 16-row chunks, up to
+    several per expert; whole and partial steps of 4 blocks; a bias; K up to 3040; exponent bytes
+    >= 240, the multiply-then-add update), against the oracle and the tiled path
+    (lsk_moe_select(0))."""
+    from lockstep_amd import _lib as L
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("mx skinny", dict(T=T, E=E, k=k, H=H, I=I, big_exp=big_exp))
+    x, experts, logits = WL.moe_mx_inputs(T, E, k, H, I, seed=80 + T, bias=True)
+    if big_exp:
+        p13, s13, p2, s2, b13, b2 = experts[1]
+        s2 = s2.copy()
+        s2[::5, 2] = 241
+        s2[::9, 7] = 250
+        experts[1] = (p13, s13, p2, s2, b13, b2)
+    idx, w = routing_from_logits(logits, k)
+    oexp, dexp = [], []
+    for (p13, s13, p2, s2, b13, b2) in experts:
+        m13, _ = C.mx_to_m2(p13, s13)
+        m2_, _ = C.mx_to_m2(p2, s2)
+        oexp.append(((m13, s13), (m2_, s2), b13, b2))
+        dexp.append(((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2)))
+    dexp = MR.ExpertTablesMX(dexp, packed=True)
+    assert L.load().lsk_moe_mx_reads_skinny(T, k, E, H, I, dexp.lds13, dexp.lds2, 0, 0) == 1
+    assert L.load().lsk_moe_mx_reads_skinny(T, k, E, H, I, dexp.lds13, dexp.lds2, 2, 0) == 0
+    assert dexp.mx_safe == (1 if big_exp else 0)
+    ridx, rw = routing_device(idx, w)
+    y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai, routing=(ridx, rw))
+    assert dexp._skinny is not None              # the call made and read the copies
+    L.call("lsk_moe_select", 0)
+    try:
+        yt, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai,
+                                     routing=(ridx, rw))
+    finally:
+        L.call("lsk_moe_select", -1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx(x, oexp, idx, w, C.act_swigluoai)
+    assert np.array_equal(u16(y), ref)
+    assert np.array_equal(u16(yt), ref)
+
+
 @pytest.mark.parametrize("variant", [0, 2])
 @pytest.mark.parametrize("big_exp", [False, True])
 def test_moe_mx_tiles_and_gemv(variant, big_exp):
@@ -232,12 +309,12 @@ def test_moe_mx_tiles_and_gemv(variant, big_exp):
     assert np.array_equal(u16(y), ref)
 
 
-@pytest.mark.parametrize("mxv", [0, 1, 2])
+@pytest.mark.parametrize("mxv", [0, 1, 2, 3])
 @pytest.mark.parametrize("big_exp", [False, True])
 def test_moe_mx_grouped_main_loops(mxv, big_exp):
     """Every main loop of the grouped MX GEMM (0 / 2: direct-to-LDS with a two / three-stage ring,
-    1: register-staged) on the tiled
-    path against the oracle: several 128-row tiles per expert, a half 64-wide K stage in both
+    1: register-staged; 3 past the skinny GEMM's 256 tokens: loop 0) on the tiled path against the
+    oracle: several 128-row tiles per expert, a half 64-wide K stage in both
     projections (H = 352, I = 224), partial column tiles, biases, and optionally exponent bytes
     >= 240 (the multiply-then-add update)."""
     from lockstep_amd import _lib as L
