@@ -586,6 +586,18 @@ int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const 
                         const int64_t* w_ptrs, int64_t ldw, const int64_t* kx_ptrs, int64_t lds, const int64_t* b_ptrs,
                         int64_t N, int64_t K, int safe, uint16_t* out, void* workspace, int64_t workspace_bytes,
                         void* stream);
+/* The same with w_skinny_ptrs: NULL, or per expert the codes' skinny-layout copy
+ * (lsk_mx_skinny_pack of the [N, K/2] codes), read by the skinny grouped MX GEMM where
+ * lsk_grouped_mx_reads_skinny says so (experts averaging at most 32 rows) instead of w_ptrs (no
+ * reference counterpart as an argument: prepared weight copies; the same results). */
+int lsk_grouped_gemm_mx_skinny(const uint16_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E,
+                               int64_t R, const int64_t* w_ptrs, int64_t ldw, const int64_t* w_skinny_ptrs,
+                               const int64_t* kx_ptrs, int64_t lds, const int64_t* b_ptrs, int64_t N, int64_t K,
+                               int safe, uint16_t* out, void* workspace, int64_t workspace_bytes, void* stream);
+/* No counterpart in the reference: 1 when lsk_grouped_gemm_mx_skinny over R rows, E experts, depth K
+ * and E8M0 row stride lds reads the skinny-layout copies under the calling thread's
+ * lsk_moe_mx_select setting; 0 otherwise.  No device work. */
+int lsk_grouped_mx_reads_skinny(int64_t R, int64_t E, int64_t K, int64_t lds);
 
 /* Tuning control with no counterpart in the reference: 1 (the default) runs a one-token int8 layer
  * routed from its logits (lsk_moe_args.logits, the grouped GEMV path, k <= 8) with the router, the
@@ -634,7 +646,8 @@ int lsk_moe_pp_skinny_rows(int rows);
  * before LDS; 2: as 0 with a three-stage ring and two blocks per CU; 3: as 0, with the skinny
  * grouped MX GEMM -- an expert's rows 16 at a time in LDS, the codes streamed into the bf16 MFMA --
  * wherever the layer can take it, which 0 does by size: MXFP4 layers with per-row activation
- * scales past the decode GEMV's token counts while T k < 16 E, up to 256 tokens).  Results are
+ * scales from 2 to 256 tokens, whose callers pass the codes' skinny-layout copies; 0 keeps the
+ * decode GEMV for one token).  Results are
  * identical; only speed differs.  The choice applies to the calling host thread's later launches
  * only (thread-local). */
 int lsk_moe_mx_select(int variant);

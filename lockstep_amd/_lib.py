@@ -93,6 +93,9 @@ SIGNATURES = {
                                          _P]),
     "lsk_grouped_gemm_mx": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I, _P, _P, _I64,
                                  _P]),
+    "lsk_grouped_gemm_mx_skinny": (_I, [_P, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I,
+                                        _P, _P, _I64, _P]),
+    "lsk_grouped_mx_reads_skinny": (_I, [_I64, _I64, _I64, _I64]),
     "lsk_moe_select": (_I, [_I]),
     "lsk_mfma_bf16_acc_probe": (_I, [_P, _P, _P, _P, _I, _P]),
     "lsk_mfma_probe": (_I, [_P, _I64, _I64, _I, _P, _P]),

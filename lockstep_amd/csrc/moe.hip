@@ -2536,11 +2536,21 @@ extern "C" int lsk_grouped_gemm_w8a8_pairs(const int8_t* a, int64_t lda, const f
   return launch_moe_gemm<1>(g, mt, (int)((N + 127) / 128), s, "moe_gemm_kernel<grouped>");
 }
 
-extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E,
-                                   int64_t R, const int64_t* w_ptrs, int64_t ldw, const int64_t* kx_ptrs, int64_t lds,
-                                   const int64_t* b_ptrs, int64_t N, int64_t K, int safe, uint16_t* out,
-                                   void* workspace, int64_t workspace_bytes, void* stream) {
-  hipStream_t s = (hipStream_t)stream;
+// Whether the grouped MX linear takes the skinny grouped MX GEMM when the caller passes the weights'
+// skinny-layout copies: experts averaging at most 32 rows (R <= 32 E) under lsk_moe_mx_select(0),
+// any row count under (3); its LDS within 160 KB.  (The layer's measurements: GPT-OSS-20B shapes on
+// MI355X, 32 rows per expert 118.7 against 137.6 us on the tiles, 64 level, 181.9 / 183.5.)
+static bool grouped_mx_takes_skinny(int64_t R, int64_t E, int64_t K, int64_t lds) {
+  if (R < 1 || E < 1 || K <= 0 || K % 32 != 0 || lds < K / 32 || lsk::moe_mx_skinny_lds(K, lds) > 160 * 1024)
+    return false;
+  const int v = lsk::mx_variant();
+  return v == 3 || (v == 0 && R <= 32 * E);
+}
+
+static int grouped_mx(const uint16_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E, int64_t R,
+                      const int64_t* w_ptrs, int64_t ldw, const int64_t* w_skinny_ptrs, const int64_t* kx_ptrs,
+                      int64_t lds, const int64_t* b_ptrs, int64_t N, int64_t K, int safe, uint16_t* out,
+                      void* workspace, int64_t workspace_bytes, hipStream_t s) {
   int rc = grouped_setup("lsk_grouped_gemm_mx", a, asc, offs, E, R, w_ptrs, kx_ptrs, N, K, out, workspace,
                          workspace_bytes, s);
   if (rc || R == 0) return rc;
@@ -2565,7 +2575,35 @@ extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* 
   g.K = (int)K;
   g.N = (int)N;
   g.y = out;
+  if (w_skinny_ptrs && grouped_mx_takes_skinny(R, E, K, lds)) {
+    LSK_REQUIRE(lsk::mx_skinny_bytes(N, K) < 0x7fffffff, "lsk_grouped_gemm_mx_skinny: a copy beyond 2 GB");
+    g.w_ptrs = w_skinny_ptrs;
+    g.w_bytes = lsk::mx_skinny_bytes(N, K);
+    // no routing weights or slot rows: row p of out, bfr(fl32(acc * asc[p])) (+ b) as the tiles write it
+    return lsk::launch_moe_mx_skinny(1, g, grouped_max_tiles(R, E), safe, nullptr, s);
+  }
   return lsk::launch_moe_mx_gemm(1, g, grouped_max_tiles(R, E), safe, s);
+}
+
+extern "C" int lsk_grouped_gemm_mx(const uint16_t* a, int64_t lda, const float* asc, const int32_t* offs, int64_t E,
+                                   int64_t R, const int64_t* w_ptrs, int64_t ldw, const int64_t* kx_ptrs, int64_t lds,
+                                   const int64_t* b_ptrs, int64_t N, int64_t K, int safe, uint16_t* out,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  return grouped_mx(a, lda, asc, offs, E, R, w_ptrs, ldw, nullptr, kx_ptrs, lds, b_ptrs, N, K, safe, out, workspace,
+                    workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int lsk_grouped_gemm_mx_skinny(const uint16_t* a, int64_t lda, const float* asc, const int32_t* offs,
+                                          int64_t E, int64_t R, const int64_t* w_ptrs, int64_t ldw,
+                                          const int64_t* w_skinny_ptrs, const int64_t* kx_ptrs, int64_t lds,
+                                          const int64_t* b_ptrs, int64_t N, int64_t K, int safe, uint16_t* out,
+                                          void* workspace, int64_t workspace_bytes, void* stream) {
+  return grouped_mx(a, lda, asc, offs, E, R, w_ptrs, ldw, w_skinny_ptrs, kx_ptrs, lds, b_ptrs, N, K, safe, out,
+                    workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int lsk_grouped_mx_reads_skinny(int64_t R, int64_t E, int64_t K, int64_t lds) {
+  return grouped_mx_takes_skinny(R, E, K, lds) ? 1 : 0;
 }
 
 extern "C" int lsk_moe_fuse_route(int on) {
@@ -2623,14 +2661,22 @@ extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, i
   return r ? 1 : 0;
 }
 
-// Whether an MXFP4 layer (per-row activation scales) past the MX GEMV's token counts takes the skinny
-// grouped MX GEMM: by size (T k < 16 E, up to 256 tokens) under lsk_moe_mx_select(0), wherever it
-// fits under (3); its LDS (the chunk's bf16 rows and the E8M0 rows) within 160 KB; no rotation.
+// Whether an MXFP4 layer (per-row activation scales) takes the skinny grouped MX GEMM when the caller
+// has the skinny-layout code copies: by size from 2 tokens under lsk_moe_mx_select(0) (the MX GEMV
+// keeps one token), from 1 under (3); up to 256 tokens; its LDS (the chunk's bf16 rows and the E8M0
+// rows) within 160 KB; no rotation.  A forced GEMV (lsk_moe_select(2)) or forced tiles take none
+// unless (3) asks for it.  GPT-OSS-20B on MI355X (E 32, top 4, H = I = 2880): T = 2 56 us against
+// 64 (GEMV), T = 16 124 / 193, T = 32 129 / 262 (tiles), T = 128 177 / 330, T = 256 267 / 390; at
+// 64 rows per expert (E 8, top 2, T = 256) level with the tiles, 182 / 184.
 static bool mx_takes_skinny(int64_t T, int k, int64_t E, int64_t H, int64_t I, int64_t lds13, int64_t lds2, int rb) {
-  const bool mx_gemv = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : T <= kMxGemvMaxT);
-  return !mx_gemv && rb == 0 && T >= 1 && T <= kSkinnyMaxT && H % 32 == 0 && I % 32 == 0 &&
-         (lsk::mx_variant() == 3 || (lsk::mx_variant() == 0 && g_moe_force < 0 && T * k < 16 * E)) &&
-         lsk::moe_mx_skinny_lds(H, lds13) <= 160 * 1024 && lsk::moe_mx_skinny_lds(I, lds2) <= 160 * 1024;
+  (void)k;
+  (void)E;
+  if (rb != 0 || T < 1 || T > kSkinnyMaxT || H % 32 != 0 || I % 32 != 0) return false;
+  if (lsk::moe_mx_skinny_lds(H, lds13) > 160 * 1024 || lsk::moe_mx_skinny_lds(I, lds2) > 160 * 1024) return false;
+  const int v = lsk::mx_variant();
+  if (g_moe_force == 2) return false;
+  if (v == 3) return true;
+  return v == 0 && g_moe_force < 0 && T >= 2;
 }
 
 extern "C" int lsk_moe_mx_reads_skinny(int64_t T, int k, int64_t E, int64_t H, int64_t I, int64_t lds13, int64_t lds2,
@@ -2732,18 +2778,18 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   const bool gemv_ok = rb == 0 && T <= kGemvMaxT && (g_moe_force >= 0 ? g_moe_force == 2 : true);
   const bool use_skinny = moe_takes_skinny(T, k, E, rb, mx, H, I);
   const bool use_gemv = gemv_ok && !mx && H <= 4096 && I <= 4096 && !use_skinny;
-  // (MX experts: the GEMV re-streams each expert's weights per 4-row pass, so past about 24 tokens
-  // the tiled kernels win: GPT-OSS-20B on MI355X, T = 24 242 vs 276 us, T = 48 368 vs 278 us)
-  const bool use_mx_gemv = gemv_ok && mx == 1 && (g_moe_force == 2 || T <= kMxGemvMaxT) && H <= 8192 && I <= 8192;
+  // MXFP4 experts (per-row scales) past one token: the skinny grouped MX GEMM on the experts'
+  // skinny-layout copies (w13_pair_ptrs / w2_pair_ptrs for MXFP4 experts), when the caller has them;
+  // else the MX GEMV, which re-streams each expert's weights per 4-row pass, so past about 24 tokens
+  // the tiled kernels win (GPT-OSS-20B on MI355X, T = 24 242 vs 276 us, T = 48 368 vs 278 us)
+  const bool use_mx_skinny =
+      mx == 1 && a->w13_pair_ptrs && a->w2_pair_ptrs && mx_takes_skinny(T, k, E, H, I, a->lds13, a->lds2, rb);
+  const bool use_mx_gemv = gemv_ok && mx == 1 && !use_mx_skinny && (g_moe_force == 2 || T <= kMxGemvMaxT) &&
+                           H <= 8192 && I <= 8192;
   // block-scaled activations at decode sizes: the same GEMV over integer-valued rows (every row
   // quantised in the general form) with the block exponents (T = 1 50 vs 116 us, T = 16 221 vs
   // 278 us, T = 24 281 vs 277 us)
   const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
-  // MXFP4 experts (per-row scales) holding few rows each past the GEMV's token counts: the skinny
-  // grouped MX GEMM on the experts' skinny-layout copies (w13_pair_ptrs / w2_pair_ptrs for MXFP4
-  // experts), when the caller has them
-  const bool use_mx_skinny = mx == 1 && !use_mx_gemv && a->w13_pair_ptrs && a->w2_pair_ptrs &&
-                             mx_takes_skinny(T, k, E, H, I, a->lds13, a->lds2, rb);
   // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
   // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
   const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && !use_skinny && I % 64 == 0 &&

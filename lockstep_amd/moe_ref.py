@@ -500,35 +500,46 @@ class ExpertTablesMX:
         self._keep = keep
         self._derived = _derived(pairs)
         # the codes' skinny-layout copies (lsk_mx_skinny_pack), which the skinny grouped MX GEMM
-        # reads a kilobyte per wave load: made by skinny_ptrs() on the first call that reads them,
+        # reads a kilobyte per wave load: made by make_skinny() on the first call that reads them,
         # remade when a code tensor changes in place
         self._codes = [keep[i] for i in range(0, len(keep), 6)] + [keep[i] for i in range(1, len(keep), 6)]
-        self._skinny = None
+        self._skinny = [None, None]
 
     def skinny_ptrs(self, T, k, select, mx_select):
         """(w13_pair_ptrs, w2_pair_ptrs) for an MXFP4 layer call (per-row scales) of T tokens, top-k:
         the tables of the skinny-layout code copies when that call reads them
         (lsk_moe_mx_reads_skinny), else (None, None); (None, None) while a graph is being captured
         (the graph then runs the kernels that read the codes themselves)."""
-        lib = L.load()
-        if not lib.lsk_moe_mx_reads_skinny(int(T), int(k), self.E, self.H, self.I, self.lds13, self.lds2,
-                                           int(select), int(mx_select)):
+        if not L.load().lsk_moe_mx_reads_skinny(int(T), int(k), self.E, self.H, self.I, self.lds13, self.lds2,
+                                                int(select), int(mx_select)):
             return None, None
-        vers = [c._version for c in self._codes]
-        if self._skinny is None or self._skinny[0] != vers:
-            if torch.cuda.is_current_stream_capturing():
-                return None, None
-            self._skinny = None
-            E = self.E
-            copies = []
-            for c, (rows, K) in zip(self._codes, [(2 * self.I, self.H)] * E + [(self.H, self.I)] * E):
-                out = torch.empty((lib.lsk_mx_skinny_bytes(rows, K),), dtype=torch.uint8, device=self.device)
-                L.call("lsk_mx_skinny_pack", L.ptr(c), int(c.stride(0)), rows, K, L.ptr(out), L.stream_of(out))
-                copies.append(out)
-            t13 = torch.tensor([t.data_ptr() for t in copies[:E]], dtype=torch.int64).to(self.device)
-            t2 = torch.tensor([t.data_ptr() for t in copies[E:]], dtype=torch.int64).to(self.device)
-            self._skinny = (vers, copies, t13, t2)
-        return self._skinny[2], self._skinny[3]
+        t13, t2 = self.make_skinny(0), self.make_skinny(1)
+        return (t13, t2) if t13 is not None and t2 is not None else (None, None)
+
+    def make_skinny(self, j):
+        """The device table of projection j's (0: w13 [2I, H/2], 1: w2 [H, I/2]) skinny-layout code
+        copies, made on first use and remade after an in-place update of those codes; None where its
+        K is not a multiple of 32 or while a graph is being captured before they exist."""
+        rows, K = (2 * self.I, self.H) if j == 0 else (self.H, self.I)
+        if K % 32:
+            return None
+        codes = self._codes[j * self.E:(j + 1) * self.E]
+        vers = [c._version for c in codes]
+        hit = self._skinny[j]
+        if hit is not None and hit[0] == vers:
+            return hit[2]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        self._skinny[j] = None                  # stale: freed before the new copies are made
+        lib = L.load()
+        copies = []
+        for c in codes:
+            out = torch.empty((lib.lsk_mx_skinny_bytes(rows, K),), dtype=torch.uint8, device=self.device)
+            L.call("lsk_mx_skinny_pack", L.ptr(c), int(c.stride(0)), rows, K, L.ptr(out), L.stream_of(out))
+            copies.append(out)
+        table = torch.tensor([t.data_ptr() for t in copies], dtype=torch.int64).to(self.device)
+        self._skinny[j] = (vers, copies, table)
+        return table
 
 
 def expert_tables_mx(experts) -> ExpertTablesMX:
@@ -583,9 +594,13 @@ def grouped_linear_mx(tables, which: str, a8, asc, offs):
     w, kx, b = (tables.w13, tables.ws13, tables.b13) if which == "w13" else (tables.w2, tables.ws2, tables.b2)
     ldw, lds = (tables.ldw13, tables.lds13) if which == "w13" else (tables.ldw2, tables.lds2)
     asc = asc.to(F32).contiguous()
-    L.call("lsk_grouped_gemm_mx", L.ptr(ab), ab.stride(0) if R > 1 else ab.shape[1], L.ptr(asc), L.ptr(offs),
-           tables.E, R, L.ptr(w), ldw, L.ptr(kx), lds, L.ptr(b), N, ab.shape[1], tables.mx_safe, L.ptr(out),
-           L.ptr(work), nbytes, L.stream_of(ab))
+    # experts averaging few rows: the skinny grouped MX GEMM on the codes' skinny-layout copies
+    wsk = None
+    if L.load().lsk_grouped_mx_reads_skinny(R, tables.E, ab.shape[1], lds):
+        wsk = tables.make_skinny(0 if which == "w13" else 1)
+    L.call("lsk_grouped_gemm_mx_skinny", L.ptr(ab), ab.stride(0) if R > 1 else ab.shape[1], L.ptr(asc),
+           L.ptr(offs), tables.E, R, L.ptr(w), ldw, L.ptr(wsk), L.ptr(kx), lds, L.ptr(b), N, ab.shape[1],
+           tables.mx_safe, L.ptr(out), L.ptr(work), nbytes, L.stream_of(ab))
     return out
 
 

@@ -63,10 +63,16 @@ def test_grouped_linear_int8(R, E, N, K, bias):
         assert np.array_equal(got[r0:r1], C.bf16_bits(ref)), "expert %d" % e
 
 
-@pytest.mark.parametrize("R,E,N,K,bias", [(200, 6, 128, 256, False), (1500, 8, 256, 320, True)])
-def test_grouped_linear_mx(R, E, N, K, bias):
+@pytest.mark.parametrize("R,E,N,K,bias,mxv", [(200, 6, 128, 256, False, 0), (1500, 8, 256, 320, True, 0),
+                                              (256, 32, 384, 2880, True, 0), (100, 8, 400, 320, False, 0),
+                                              (1500, 8, 256, 320, True, 3)])
+def test_grouped_linear_mx(R, E, N, K, bias, mxv):
+    """The grouped MX linear on the tiles and, for experts averaging at most 32 rows (256 rows over
+    32 experts, 100 over 8) or under lsk_moe_mx_select(3) (full 128-row tiles, eight 16-row chunks
+    each), on the skinny grouped MX GEMM reading the codes' skinny-layout copies."""
+    from lockstep_amd import _lib as L
     from lockstep_amd import moe_ref as MR
-    say("grouped mx", dict(R=R, E=E, N=N, K=K, bias=bias))
+    say("grouped mx", dict(R=R, E=E, N=N, K=K, bias=bias, mxv=mxv))
     g = np.random.default_rng(7 * R + N)
     cnt = _counts(g, E, R)
     offs = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)
@@ -81,7 +87,14 @@ def test_grouped_linear_mx(R, E, N, K, bias):
         dummy = (to_dev(np.zeros((K, N // 4), np.uint8)), to_dev(np.full((K, N // 64), 127, np.uint8)))
         dev_ex.append(((to_dev(codes), to_dev(kx)), dummy, None if b is None else to_dev(b), None))
     tables = MR.ExpertTablesMX(dev_ex, packed=True)
-    out = MR.grouped_linear_mx(tables, "w13", to_dev(a8), to_dev(asc), to_dev(offs))
+    L.call("lsk_moe_mx_select", mxv)
+    try:
+        skinny = L.load().lsk_grouped_mx_reads_skinny(R, E, K, tables.lds13) == 1
+        out = MR.grouped_linear_mx(tables, "w13", to_dev(a8), to_dev(asc), to_dev(offs))
+    finally:
+        L.call("lsk_moe_mx_select", 0)
+    assert skinny == (R <= 32 * E or mxv == 3)
+    assert (tables._skinny[0] is not None) == skinny
     got = bits(out)
     for e, (codes, kx, b) in enumerate(experts):
         r0, r1 = offs[e], offs[e + 1]

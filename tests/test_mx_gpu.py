@@ -143,7 +143,8 @@ def test_moe_mx_small():
 
 @pytest.mark.parametrize("T", [5, 300])
 def test_moe_mx_step_by_step_activation(T):
-    """Without the activation table (decode GEMV at T = 5, tiles at T = 300) the same bits."""
+    """Without the activation table (the skinny grouped GEMM at T = 5, tiles at T = 300) the same
+    bits."""
     from lockstep_amd import moe_ref as MR
     MR.USE_ACT_TABLE = False
     try:
@@ -225,9 +226,8 @@ def test_mx_skinny_pack(rows, K, ldw):
 @pytest.mark.parametrize("T,E,k,H,I,big_exp", [(32, 32, 4, 2880, 2880, False), (100, 16, 2, 1088, 576, False),
                                                (25, 8, 3, 2048, 3040, False), (40, 8, 2, 1088, 576, True)])
 def test_moe_mx_skinny(T, E, k, H, I, big_exp):
-    """The skinny grouped MX GEMM on the experts' skinny-layout code copies, taken by size past the
-    GEMV's token counts while experts hold few rows (GPT-OSS-20B at 32 tokens; 16-row chunks, up to
-    several per expert; whole and partial steps of 4 blocks; a bias; K up to 3040; exponent bytes
+    """The skinny grouped MX GEMM on the experts' skinny-layout code copies, taken by size from 2
+    tokens (GPT-OSS-20B at 32 tokens; 16-row chunks, up to several per expert; whole and partial steps of 4 blocks; a bias; K up to 3040; exponent bytes
     >= 240, the multiply-then-add update), against the oracle and the tiled path
     (lsk_moe_select(0))."""
     from lockstep_amd import _lib as L
@@ -254,7 +254,7 @@ def test_moe_mx_skinny(T, E, k, H, I, big_exp):
     assert dexp.mx_safe == (1 if big_exp else 0)
     ridx, rw = routing_device(idx, w)
     y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai, routing=(ridx, rw))
-    assert dexp._skinny is not None              # the call made and read the copies
+    assert all(t is not None for t in dexp._skinny)  # the call made and read the copies
     L.call("lsk_moe_select", 0)
     try:
         yt, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai,

@@ -43,25 +43,31 @@ def test_moe_row_pair_query():
 
 def test_moe_mx_skinny_query():
     """MXFP4 layers (GPT-OSS-20B: E 32, top 4, H = I = 2880, 90 E8M0 bytes a row) read the codes'
-    skinny-layout copies past the GEMV's 24 tokens while T k < 16 E, up to 256 tokens; under
-    lsk_moe_mx_select(3) up to 256 tokens whatever the rows per expert."""
+    skinny-layout copies from 2 to 256 tokens (one token: the MX GEMV); under lsk_moe_mx_select(3)
+    from one token; forced kernel families read none."""
     lib = L.load()
     E, k, H, I, lds = 32, 4, 2880, 2880, 90
-    for T in (1, 24):                                                      # the MX GEMV
-        assert lib.lsk_moe_mx_reads_skinny(T, k, E, H, I, lds, lds, 0, 0) == 0, T
-    for T in (25, 32, 127):
+    assert lib.lsk_moe_mx_reads_skinny(1, k, E, H, I, lds, lds, 0, 0) == 0            # the MX GEMV
+    for T in (2, 24, 25, 128, 256):
         assert lib.lsk_moe_mx_reads_skinny(T, k, E, H, I, lds, lds, 0, 0) == 1, T
-    for T in (128, 4096):                                                  # 16 rows per expert: the tiles
+    for T in (257, 4096):                                                             # the tiles
         assert lib.lsk_moe_mx_reads_skinny(T, k, E, H, I, lds, lds, 0, 0) == 0, T
-    assert lib.lsk_moe_mx_reads_skinny(200, k, E, H, I, lds, lds, 0, 4) == 1       # mx_select 3
-    assert lib.lsk_moe_mx_reads_skinny(300, k, E, H, I, lds, lds, 0, 4) == 0
+    assert lib.lsk_moe_mx_reads_skinny(1, k, E, H, I, lds, lds, 0, 4) == 1            # mx_select 3
+    assert lib.lsk_moe_mx_reads_skinny(200, k, E, H, I, lds, lds, 2, 4) == 1          # ... over the tiles
     # a forced kernel family (select = variant + 2) reads none; the thread's settings stay as they were
     assert lib.lsk_moe_mx_reads_skinny(32, k, E, H, I, lds, lds, 2, 0) == 0
-    assert lib.lsk_moe_mx_reads_skinny(32, k, E, H, I, lds, lds, 0, 2) == 0        # mx_select 1
+    assert lib.lsk_moe_mx_reads_skinny(32, k, E, H, I, lds, lds, 4, 4) == 0           # the GEMV forced
+    assert lib.lsk_moe_mx_reads_skinny(32, k, E, H, I, lds, lds, 0, 2) == 0           # mx_select 1
     assert lib.lsk_moe_mx_reads_skinny(32, k, E, H, I, lds, lds, 0, 0) == 1
     # the chunk's rows and the E8M0 rows must fit the LDS: K = 16384 does not
     assert lib.lsk_moe_mx_reads_skinny(32, k, E, 16384, I, 512, lds, 0, 0) == 0
-    assert lib.lsk_moe_mx_reads_skinny(32, k, E, 2880, 2880, lds, lds, 0, 10) == 0  # out of range
+    assert lib.lsk_moe_mx_reads_skinny(32, k, E, H, I, lds, lds, 0, 10) == 0          # out of range
+    # the grouped linear alone: experts averaging at most 32 rows
+    assert lib.lsk_grouped_mx_reads_skinny(256, E, H, lds) == 1
+    assert lib.lsk_grouped_mx_reads_skinny(32 * E, E, H, lds) == 1
+    assert lib.lsk_grouped_mx_reads_skinny(32 * E + 1, E, H, lds) == 0
+    assert lib.lsk_grouped_mx_reads_skinny(256, E, 16384, 512) == 0
+    assert lib.lsk_grouped_mx_reads_skinny(256, E, 100, 4) == 0                        # K % 32 != 0
 
 
 @pytest.fixture
