@@ -2580,7 +2580,7 @@ static int grouped_mx(const uint16_t* a, int64_t lda, const float* asc, const in
     g.w_ptrs = w_skinny_ptrs;
     g.w_bytes = lsk::mx_skinny_bytes(N, K);
     // no routing weights or slot rows: row p of out, bfr(fl32(acc * asc[p])) (+ b) as the tiles write it
-    return lsk::launch_moe_mx_skinny(1, g, grouped_max_tiles(R, E), safe, nullptr, s);
+    return lsk::launch_moe_mx_skinny(1, g, grouped_max_tiles(R, E), R, safe, nullptr, s);
   }
   return lsk::launch_moe_mx_gemm(1, g, grouped_max_tiles(R, E), safe, s);
 }
@@ -2935,7 +2935,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   } else if (use_mx_skinny) {
     g1.w_ptrs = a->w13_pair_ptrs;
     g1.w_bytes = lsk::mx_skinny_bytes(2 * I, H);
-    if ((rc = lsk::launch_moe_mx_skinny(0, g1, w.max_tiles, a->mx_safe, w.gu, s))) return rc;
+    if ((rc = lsk::launch_moe_mx_skinny(0, g1, w.max_tiles, T, a->mx_safe, w.gu, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (route_gemv1) {
@@ -3046,7 +3046,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   } else if (use_mx_skinny) {
     g2.w_ptrs = a->w2_pair_ptrs;
     g2.w_bytes = lsk::mx_skinny_bytes(H, I);
-    if ((rc = lsk::launch_moe_mx_skinny(1, g2, w.max_tiles, a->mx_safe, nullptr, s))) return rc;
+    if ((rc = lsk::launch_moe_mx_skinny(1, g2, w.max_tiles, T, a->mx_safe, nullptr, s))) return rc;
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (use_gemv && T == 1 && k <= 8 && I <= 2048) {

@@ -60,7 +60,9 @@ int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64
 
 // Skinny grouped MX GEMM (experts with few rows; per-row activation scales): the chunk's rows in
 // LDS, the codes streamed into the bf16 MFMA (mode 0: gate / up values into gu; mode 1: slot rows).
-int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, uint16_t* gu, hipStream_t s);
+// rows: at least the most rows any expert holds (the layer's T; the grouped linear's R).
+int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t rows, int safe, uint16_t* gu,
+                         hipStream_t s);
 int moe_mx_skinny_lds(int64_t K, int64_t lds);
 int64_t mx_skinny_bytes(int64_t rows, int64_t K);
 

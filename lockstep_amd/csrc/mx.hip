@@ -859,15 +859,16 @@ int launch_mx_gemv(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uin
 // (col, g)'s 4 code bytes of the 4 blocks side by side, so a wave reads each step as one
 // contiguous 1 KB; the codes' own layout, 16 bytes per row and block, measured 2.6x slower for the
 // whole layer) and stream D steps ahead of their MFMAs in registers, so each expert's codes are read
-// once per 16-row chunk.  The epilogue is
+// once per chunk.  The epilogue is
 // moe_mx_gemv_kernel's: the bias-added gate / up values into gu (mode 0), the routing-weighted slot
-// rows (mode 1).  LDS: the chunk's rows [16][ldsk], the waves' E8M0 bytes [16][scb], the rows'
-// operands.
-template <int MODE, bool SAFE, int D>
-__global__ __launch_bounds__(1024) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu, int sets,
-                                                             int ldsk, int scb) {
+// rows (mode 1).  WPB waves per block (one group each); chunks of cr <= 16 rows, the most any
+// expert holds when that is fewer (one token: one row, so the LDS holds one row and more blocks fit
+// a CU; MFMA rows past the chunk read its last row and their outputs are dropped).  LDS: the
+// chunk's rows [cr][ldsk], the waves' E8M0 bytes [WPB][scb], the rows' operands.
+template <int MODE, bool SAFE, int D, int WPB>
+__global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu,
+                                                                 int sets, int ldsk, int scb, int cr) {
   extern __shared__ __attribute__((aligned(16))) char smem_mxs[];
-  constexpr int CR = 16;
   const int lane = threadIdx.x & 63, wave = wave_id(), tid = threadIdx.x;
   const int mt = blockIdx.x / sets, gs = blockIdx.x - (blockIdx.x / sets) * sets;
   if (mt >= a.tiles[0]) return;  // the whole block leaves
@@ -877,7 +878,7 @@ __global__ __launch_bounds__(1024) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a,
   const int K = a.K, nb = K >> 5;
   const int NWR = MODE == 0 ? 2 * a.N : a.N;  // weight rows
   const int G = (NWR + 15) >> 4;
-  const int g = gs * 16 + wave;  // this wave's group of 16 weight rows (wave-uniform)
+  const int g = gs * WPB + wave;  // this wave's group of 16 weight rows (wave-uniform)
   const int col = lane & 15, kg = lane >> 4;
   const int n = g * 16 + col;
   const bool live = g < G && n < NWR;
@@ -892,11 +893,11 @@ __global__ __launch_bounds__(1024) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a,
   const int nst = (nb + 3) >> 2;  // steps of 4 blocks
   // this lane's 16 code bytes of step s (blocks 4 s .. 4 s + 3, 4 bytes each) at wbase + 1024 s
   const uint32_t wbase = g < G ? (uint32_t)(((g * nst) * 16 + col) * 64 + kg * 16) : lsk::kOob;
-  char* sc_w = smem_mxs + CR * ldsk + wave * scb;
-  int* r_src = (int*)(smem_mxs + CR * ldsk + 16 * scb);
-  float* r_asc = (float*)(r_src + CR);
-  float* r_w = r_asc + CR;
-  int* r_dst = (int*)(r_w + CR);
+  char* sc_w = smem_mxs + cr * ldsk + wave * scb;
+  int* r_src = (int*)(smem_mxs + cr * ldsk + WPB * scb);
+  float* r_asc = (float*)(r_src + 16);
+  float* r_w = r_asc + 16;
+  int* r_dst = (int*)(r_w + 16);
   // the group's E8M0 rows 16 g .. 16 g + 15: one contiguous run of 16 lds bytes (zeros past NWR)
   {
     const int sbytes = 16 * (int)a.lds;
@@ -908,11 +909,11 @@ __global__ __launch_bounds__(1024) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a,
     }
   }
   const int cpr = (2 * K + 1023) >> 10;  // 1 KB chunks of an activation row
-  const char* arow = smem_mxs + col * ldsk + 16 * kg;              // A fragment of block b at + 64 b
+  const char* arow = smem_mxs + min(col, cr - 1) * ldsk + 16 * kg;  // A fragment of block b at + 64 b
   const uint8_t* srow = (const uint8_t*)sc_w + col * (int)a.lds;  // E8M0 byte of block b at [b]
   lsk::compiler_fence();
-  for (int q0 = p0; q0 < p1; q0 += CR) {
-    const int nr = min(CR, p1 - q0);
+  for (int q0 = p0; q0 < p1; q0 += cr) {
+    const int nr = min(cr, p1 - q0);
     if (q0 > p0) __syncthreads();  // the previous chunk's LDS reads are done
     v4i cw[D];
 #pragma unroll
@@ -926,7 +927,7 @@ __global__ __launch_bounds__(1024) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a,
       __syncthreads();
     }
     // the chunk's rows into LDS (bf16 values, zeros past K), then the rows' operands
-    for (int c = wave; c < nr * cpr; c += 16) {
+    for (int c = wave; c < nr * cpr; c += WPB) {
       const int r = c / cpr, j = c - (c / cpr) * cpr;
       const int kb = j * 1024 + lane * 16;
       const int src = MODE == 0 ? r_src[r] : q0 + r;
@@ -1005,23 +1006,41 @@ __global__ __launch_bounds__(1024) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a,
 }
 
 template <int MODE, bool SAFE>
-int launch_mx_skinny(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
+int launch_mx_skinny(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t rows, uint16_t* gu, hipStream_t s,
+                     const char* name) {
   const int NWR = MODE == 0 ? 2 * ga.N : ga.N;
-  const int sets = ((NWR + 15) / 16 + 15) / 16;
+  const int G = (NWR + 15) / 16;
+  // chunks of up to 16 rows, fewer when no expert holds more; with few rows four waves per block
+  // (more blocks over the CUs, the LDS a few rows deep)
+  const int cr = (int)(rows < 1 ? 1 : (rows > 16 ? 16 : rows));
+  const bool small = cr <= 8;
+  const int wpb = small ? 4 : 16;
+  const int sets = (G + wpb - 1) / wpb;
   const int ldsk = (2 * ga.K + 1023) / 1024 * 1024 + 16;
   const int scb = (16 * (int)ga.lds + 1023) / 1024 * 1024;
-  const int smem = 16 * ldsk + 16 * scb + 4 * 16 * 4;
+  const int smem = cr * ldsk + wpb * scb + 4 * 16 * 4;
   LSK_REQUIRE(smem <= 160 * 1024, "%s: %d bytes of LDS", name, smem);
   const int64_t blocks = max_tiles * sets;
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
-  auto kern = moe_mx_skinny_kernel<MODE, SAFE, SAFE ? 4 : 8>;  // steps of 4 blocks in flight
-  static std::atomic<bool> attr{false};
-  if (!attr) {
-    if (int rc = reserve_lds(kern, 160 * 1024, name)) return rc;
-    attr = true;
+  constexpr int D = SAFE ? 4 : 8;  // steps of 4 blocks in flight
+  if (small) {
+    auto kern = moe_mx_skinny_kernel<MODE, SAFE, D, 4>;
+    static std::atomic<bool> attr{false};
+    if (!attr) {
+      if (int rc = reserve_lds(kern, 160 * 1024, name)) return rc;
+      attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), smem, s, ga, gu, sets, ldsk, scb, cr);
+  } else {
+    auto kern = moe_mx_skinny_kernel<MODE, SAFE, D, 16>;
+    static std::atomic<bool> attr{false};
+    if (!attr) {
+      if (int rc = reserve_lds(kern, 160 * 1024, name)) return rc;
+      attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(1024), smem, s, ga, gu, sets, ldsk, scb, cr);
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(1024), smem, s, ga, gu, sets, ldsk, scb);
   return lsk::check_launch(name);
 }
 
@@ -1042,13 +1061,14 @@ int moe_mx_skinny_lds(int64_t K, int64_t lds) {
   return (int)((2 * K + 1023) / 1024 * 1024 + 16) * 16 + (int)((16 * lds + 1023) / 1024 * 1024) * 16 + 256;
 }
 
-int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, uint16_t* gu, hipStream_t s) {
+int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t rows, int safe, uint16_t* gu,
+                         hipStream_t s) {
   LSK_REQUIRE(!ga.a_ka && ga.K % 32 == 0 && (mode == 1 || gu), "moe_mx_skinny: arguments");
   if (mode == 0)
-    return safe ? launch_mx_skinny<0, true>(ga, max_tiles, gu, s, "moe_mx_skinny_kernel<gate_up>")
-                : launch_mx_skinny<0, false>(ga, max_tiles, gu, s, "moe_mx_skinny_kernel<gate_up>");
-  return safe ? launch_mx_skinny<1, true>(ga, max_tiles, nullptr, s, "moe_mx_skinny_kernel<down>")
-              : launch_mx_skinny<1, false>(ga, max_tiles, nullptr, s, "moe_mx_skinny_kernel<down>");
+    return safe ? launch_mx_skinny<0, true>(ga, max_tiles, rows, gu, s, "moe_mx_skinny_kernel<gate_up>")
+                : launch_mx_skinny<0, false>(ga, max_tiles, rows, gu, s, "moe_mx_skinny_kernel<gate_up>");
+  return safe ? launch_mx_skinny<1, true>(ga, max_tiles, rows, nullptr, s, "moe_mx_skinny_kernel<down>")
+              : launch_mx_skinny<1, false>(ga, max_tiles, rows, nullptr, s, "moe_mx_skinny_kernel<down>");
 }
 
 int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,

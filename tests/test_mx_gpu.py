@@ -224,7 +224,9 @@ def test_mx_skinny_pack(rows, K, ldw):
 
 
 @pytest.mark.parametrize("T,E,k,H,I,big_exp", [(32, 32, 4, 2880, 2880, False), (100, 16, 2, 1088, 576, False),
-                                               (25, 8, 3, 2048, 3040, False), (40, 8, 2, 1088, 576, True)])
+                                               (25, 8, 3, 2048, 3040, False), (40, 8, 2, 1088, 576, True),
+                                               (1, 32, 4, 2880, 2880, False), (2, 8, 2, 1088, 576, True),
+                                               (6, 16, 3, 2048, 3040, False), (12, 4, 2, 1088, 576, False)])
 def test_moe_mx_skinny(T, E, k, H, I, big_exp):
     """The skinny grouped MX GEMM on the experts' skinny-layout code copies, taken by size from 2
     tokens (GPT-OSS-20B at 32 tokens; 16-row chunks, up to several per expert; whole and partial steps of 4 blocks; a bias; K up to 3040; exponent bytes
@@ -249,11 +251,14 @@ def test_moe_mx_skinny(T, E, k, H, I, big_exp):
         oexp.append(((m13, s13), (m2_, s2), b13, b2))
         dexp.append(((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2)))
     dexp = MR.ExpertTablesMX(dexp, packed=True)
-    assert L.load().lsk_moe_mx_reads_skinny(T, k, E, H, I, dexp.lds13, dexp.lds2, 0, 0) == 1
+    mxv = 3 if T == 1 else 0            # one token takes the MX GEMV unless the skinny form is chosen
+    assert L.load().lsk_moe_mx_reads_skinny(T, k, E, H, I, dexp.lds13, dexp.lds2, 0, mxv + 1) == 1
     assert L.load().lsk_moe_mx_reads_skinny(T, k, E, H, I, dexp.lds13, dexp.lds2, 2, 0) == 0
     assert dexp.mx_safe == (1 if big_exp else 0)
     ridx, rw = routing_device(idx, w)
-    y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai, routing=(ridx, rw))
+    with MR.kernel_choice(mx=mxv):
+        y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai,
+                                    routing=(ridx, rw))
     assert all(t is not None for t in dexp._skinny)  # the call made and read the copies
     L.call("lsk_moe_select", 0)
     try:
