@@ -954,40 +954,57 @@ __global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArg
     }
     __syncthreads();
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto blk = [&](int b, uint32_t q) {
+    // block b's exact sums: the MFMA of the rows' fragments with the weight row's doubled mantissas
+    auto bsum = [&](int b, uint32_t q) -> v4f {
       const v4i af = *(const v4i*)(arow + 64 * b);
       const v4i bf = v4i{(int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 0)),
                          (int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 1)),
                          (int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 2)),
                          (int)__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, 2.0f, 3))};
-      const v4f d = lsk::mfma_bf16(af, bf);
-      const float sc = pow2f((int)srow[b] - 128);
+      return lsk::mfma_bf16(af, bf);
+    };
+    // the ordered update with the weight row's 2^(e - 128): v_ldexp_f32 of 1 is exact for every E8M0
+    // byte (2^-128 and 2^-127 as binary32 subnormals, denormals kept)
+    auto upd = [&](const v4f& d, int b) {
+      const float sc = __builtin_amdgcn_ldexpf(1.0f, (int)srow[b] - 128);
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] = SAFE ? f32_add(acc[i], f32_mul(d[i], sc)) : __builtin_fmaf(d[i], sc, acc[i]);
     };
-    auto step = [&](int st, const v4i& q4) {
-      if (4 * st + 4 <= nb) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) blk(4 * st + j, (uint32_t)q4[j]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (4 * st + j < nb) blk(4 * st + j, (uint32_t)q4[j]);
-      }
+    // a whole step: its four MFMAs issued before the first of its updates, which stay in block order
+    auto step4 = [&](int st, const v4i& q4) {
+      const int b0 = 4 * st;
+      const v4f d0 = bsum(b0, (uint32_t)q4[0]);
+      const v4f d1 = bsum(b0 + 1, (uint32_t)q4[1]);
+      const v4f d2 = bsum(b0 + 2, (uint32_t)q4[2]);
+      const v4f d3 = bsum(b0 + 3, (uint32_t)q4[3]);
+      upd(d0, b0);
+      upd(d1, b0 + 1);
+      upd(d2, b0 + 2);
+      upd(d3, b0 + 3);
     };
     if (g < G) {
-      const int nfull = nst / D * D;
+      const int nfs = nb >> 2;          // whole steps (the last step may hold fewer blocks)
+      const int nfull = nfs / D * D;    // rounds of D whole steps
       for (int s0 = 0; s0 < nfull; s0 += D) {
 #pragma unroll
         for (int u = 0; u < D; ++u) {
-          step(s0 + u, cw[u]);
+          step4(s0 + u, cw[u]);
           const int nx = s0 + u + D;
           cw[u] = lsk::buf_load16(rw, (nx < nst && wbase != lsk::kOob) ? wbase + 1024u * nx : lsk::kOob);
         }
       }
+      // the rest: up to D - 1 whole steps and the partial one, already loaded
 #pragma unroll
-      for (int u = 0; u < D; ++u)
-        if (nfull + u < nst) step(nfull + u, cw[u]);
+      for (int u = 0; u < D; ++u) {
+        const int st = nfull + u;
+        if (st < nfs) {
+          step4(st, cw[u]);
+        } else if (st < nst) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (4 * st + j < nb) upd(bsum(4 * st + j, (uint32_t)cw[u][j]), 4 * st + j);
+        }
+      }
     }
     lsk::wait_vm<0>();  // no code load outlives the chunk (the next one reuses the registers)
     if (live) {

@@ -223,11 +223,15 @@ def test_mx_skinny_pack(rows, K, ldw):
     assert np.array_equal(out.cpu().numpy(), exp)
 
 
-@pytest.mark.parametrize("T,E,k,H,I,big_exp", [(32, 32, 4, 2880, 2880, False), (100, 16, 2, 1088, 576, False),
-                                               (25, 8, 3, 2048, 3040, False), (40, 8, 2, 1088, 576, True),
-                                               (1, 32, 4, 2880, 2880, False), (2, 8, 2, 1088, 576, True),
-                                               (6, 16, 3, 2048, 3040, False), (12, 4, 2, 1088, 576, False)])
-def test_moe_mx_skinny(T, E, k, H, I, big_exp):
+@pytest.mark.parametrize("T,E,k,H,I,big_exp,small_exp", [(32, 32, 4, 2880, 2880, False, False),
+                                                         (100, 16, 2, 1088, 576, False, True),
+                                                         (25, 8, 3, 2048, 3040, False, False),
+                                                         (40, 8, 2, 1088, 576, True, True),
+                                                         (1, 32, 4, 2880, 2880, False, False),
+                                                         (2, 8, 2, 1088, 576, True, False),
+                                                         (6, 16, 3, 2048, 3040, False, True),
+                                                         (12, 4, 2, 1088, 576, False, False)])
+def test_moe_mx_skinny(T, E, k, H, I, big_exp, small_exp):
     """The skinny grouped MX GEMM on the experts' skinny-layout code copies, taken by size from 2
     tokens (GPT-OSS-20B at 32 tokens; 16-row chunks, up to several per expert; whole and partial steps of 4 blocks; a bias; K up to 3040; exponent bytes
     >= 240, the multiply-then-add update), against the oracle and the tiled path
@@ -235,7 +239,7 @@ def test_moe_mx_skinny(T, E, k, H, I, big_exp):
     from lockstep_amd import _lib as L
     from lockstep_amd import moe_ref as MR
     from lockstep_amd import workloads as WL
-    say("mx skinny", dict(T=T, E=E, k=k, H=H, I=I, big_exp=big_exp))
+    say("mx skinny", dict(T=T, E=E, k=k, H=H, I=I, big_exp=big_exp, small_exp=small_exp))
     x, experts, logits = WL.moe_mx_inputs(T, E, k, H, I, seed=80 + T, bias=True)
     if big_exp:
         p13, s13, p2, s2, b13, b2 = experts[1]
@@ -243,6 +247,16 @@ def test_moe_mx_skinny(T, E, k, H, I, big_exp):
         s2[::5, 2] = 241
         s2[::9, 7] = 250
         experts[1] = (p13, s13, p2, s2, b13, b2)
+    if small_exp:
+        # block scales 2^-128 and 2^-127 (binary32 subnormals) in every expert's gate/up and down
+        for e in range(E):
+            p13, s13, p2, s2, b13, b2 = experts[e]
+            s13, s2 = s13.copy(), s2.copy()
+            s13[::3, 1] = 0
+            s13[1::4, 4] = 1
+            s2[::5, 0] = 1
+            s2[2::7, 3] = 0
+            experts[e] = (p13, s13, p2, s2, b13, b2)
     idx, w = routing_from_logits(logits, k)
     oexp, dexp = [], []
     for (p13, s13, p2, s2, b13, b2) in experts:
