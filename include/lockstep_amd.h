@@ -646,8 +646,8 @@ int lsk_moe_pp_skinny_rows(int rows);
  * before LDS; 2: as 0 with a three-stage ring and two blocks per CU; 3: as 0, with the skinny
  * grouped MX GEMM -- an expert's rows 16 at a time in LDS, the codes streamed into the bf16 MFMA --
  * wherever the layer can take it, which 0 does by size: MXFP4 layers with per-row activation
- * scales from 2 to 256 tokens, whose callers pass the codes' skinny-layout copies; 0 keeps the
- * decode GEMV for one token).  Results are
+ * scales from 2 to 256 tokens, whose callers pass the codes' skinny-layout copies, and one token
+ * when k * 2I / 64 >= 320; 0 keeps the decode GEMV for other single tokens).  Results are
  * identical; only speed differs.  The choice applies to the calling host thread's later launches
  * only (thread-local). */
 int lsk_moe_mx_select(int variant);

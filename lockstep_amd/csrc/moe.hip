@@ -2662,21 +2662,22 @@ extern "C" int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, i
 }
 
 // Whether an MXFP4 layer (per-row activation scales) takes the skinny grouped MX GEMM when the caller
-// has the skinny-layout code copies: by size from 2 tokens under lsk_moe_mx_select(0) (the MX GEMV
-// keeps one token), from 1 under (3); up to 256 tokens; its LDS (the chunk's bf16 rows and the E8M0
-// rows) within 160 KB; no rotation.  A forced GEMV (lsk_moe_select(2)) or forced tiles take none
-// unless (3) asks for it.  GPT-OSS-20B on MI355X (E 32, top 4, H = I = 2880): T = 2 56 us against
-// 64 (GEMV), T = 16 124 / 193, T = 32 129 / 262 (tiles), T = 128 177 / 330, T = 256 267 / 390; at
-// 64 rows per expert (E 8, top 2, T = 256) level with the tiles, 182 / 184.
+// has the skinny-layout code copies: by size from 2 tokens under lsk_moe_mx_select(0), and for one
+// token when its gate/up launch has at least 320 four-wave blocks (k * 2I / 64; fewer leave CUs
+// idle and the MX GEMV keeps the token); from 1 under (3); up to 256 tokens; its LDS (the chunk's
+// bf16 rows and the E8M0 rows) within 160 KB; no rotation.  A forced GEMV (lsk_moe_select(2)) or
+// forced tiles take none unless (3) asks for it.  GPT-OSS-20B on MI355X (E 32, top 4, H = I =
+// 2880), us: T = 1 41.0 against 43.7 (GEMV), T = 2 47.7 / 64, T = 16 124 / 193, T = 32 129 / 262
+// (tiles), T = 128 177 / 330, T = 256 267 / 390; at 64 rows per expert (E 8, top 2, T = 256) level
+// with the tiles, 182 / 184; one token of E 8, top 2 35.4 against 34.4 on the GEMV.
 static bool mx_takes_skinny(int64_t T, int k, int64_t E, int64_t H, int64_t I, int64_t lds13, int64_t lds2, int rb) {
-  (void)k;
   (void)E;
   if (rb != 0 || T < 1 || T > kSkinnyMaxT || H % 32 != 0 || I % 32 != 0) return false;
   if (lsk::moe_mx_skinny_lds(H, lds13) > 160 * 1024 || lsk::moe_mx_skinny_lds(I, lds2) > 160 * 1024) return false;
   const int v = lsk::mx_variant();
   if (g_moe_force == 2) return false;
   if (v == 3) return true;
-  return v == 0 && g_moe_force < 0 && T >= 2;
+  return v == 0 && g_moe_force < 0 && (T >= 2 || (int64_t)k * ((2 * I + 63) / 64) >= 320);
 }
 
 extern "C" int lsk_moe_mx_reads_skinny(int64_t T, int k, int64_t E, int64_t H, int64_t I, int64_t lds13, int64_t lds2,

@@ -43,12 +43,14 @@ def test_moe_row_pair_query():
 
 def test_moe_mx_skinny_query():
     """MXFP4 layers (GPT-OSS-20B: E 32, top 4, H = I = 2880, 90 E8M0 bytes a row) read the codes'
-    skinny-layout copies from 2 to 256 tokens (one token: the MX GEMV); under lsk_moe_mx_select(3)
-    from one token; forced kernel families read none."""
+    skinny-layout copies from 1 to 256 tokens (one token only when k * 2I / 64 >= 320: with top 2
+    the MX GEMV keeps it); under lsk_moe_mx_select(3) from one token; forced kernel families read
+    none."""
     lib = L.load()
     E, k, H, I, lds = 32, 4, 2880, 2880, 90
-    assert lib.lsk_moe_mx_reads_skinny(1, k, E, H, I, lds, lds, 0, 0) == 0            # the MX GEMV
-    for T in (2, 24, 25, 128, 256):
+    assert lib.lsk_moe_mx_reads_skinny(1, 2, E, H, I, lds, lds, 0, 0) == 0            # the MX GEMV
+    assert lib.lsk_moe_mx_reads_skinny(1, 2, E, H, I, lds, lds, 0, 4) == 1            # mx_select 3
+    for T in (1, 2, 24, 25, 128, 256):
         assert lib.lsk_moe_mx_reads_skinny(T, k, E, H, I, lds, lds, 0, 0) == 1, T
     for T in (257, 4096):                                                             # the tiles
         assert lib.lsk_moe_mx_reads_skinny(T, k, E, H, I, lds, lds, 0, 0) == 0, T
