@@ -514,8 +514,9 @@ typedef struct {
   int mx_select;
   /* NULL, or per expert the same int8 weights in the row-pair layout (lsk_pack_row_pairs of the
    * [2I, H] and [H, I] matrices; row stride (K + 63) / 64 * 64), which the ping-pong expert tiles
-   * read instead (int8 experts; the same results).  MXFP4 experts (wfmt 1): NULL, or per expert
-   * the codes' skinny-layout copies (lsk_mx_skinny_pack), read by the skinny grouped MX GEMM. */
+   * read instead (int8 experts; the same results).  MXFP4 experts (wfmt 1 and 2): NULL, or per
+   * expert the codes' skinny-layout copies (lsk_mx_skinny_pack), read by the skinny grouped MX
+   * GEMM. */
   const int64_t* w13_pair_ptrs;
   const int64_t* w2_pair_ptrs;
 } lsk_moe_args;
@@ -540,8 +541,8 @@ int lsk_moe_forward(const lsk_moe_args* args, void* stream);
  * caller makes the copies only when a call will read them. */
 int lsk_moe_reads_row_pairs(int64_t T, int k, int64_t E, int64_t H, int64_t I, int rot_blk, int select);
 
-/* No counterpart in the reference: 1 when lsk_moe_forward on MXFP4 experts with per-row activation
- * scales (wfmt 1), T tokens, top-k over E experts, hidden H, intermediate I and E8M0 row strides
+/* No counterpart in the reference: 1 when lsk_moe_forward on MXFP4 experts (wfmt 1, or 2 with
+ * block-scaled activations), T tokens, top-k over E experts, hidden H, intermediate I and E8M0 row strides
  * lds13 / lds2, under the per-call choices select / mx_select (lsk_moe_args) and the calling
  * thread's settings, reads the experts' skinny-layout code copies (lsk_mx_skinny_pack of the
  * [2I, H/2] and [H, I/2] codes, passed as w13_pair_ptrs / w2_pair_ptrs); 0 otherwise.  No device

@@ -1961,6 +1961,24 @@ __global__ __launch_bounds__(1024) void moe_act_requant_kernel(const uint16_t* _
   }
 }
 
+// Block-scaled activations after the skinny gate/up GEMM: h = act(gate, up) [R, I] bf16 from its
+// bias-added values gu [R, 2I] (the values the tiled kernels store into h), unless a row of x was
+// flagged (*any != 0: the general tile kernel then wrote h itself).  Grid-stride over R x I.
+__global__ __launch_bounds__(256) void moe_act_h_kernel(const uint16_t* __restrict__ gu,
+                                                        const int32_t* __restrict__ nrows, int I, int act,
+                                                        const int32_t* __restrict__ frac,
+                                                        const float* __restrict__ tab,
+                                                        const int32_t* __restrict__ any, uint16_t* __restrict__ h) {
+  if (*any != 0) return;
+  const int64_t n = (int64_t)(*nrows) * I;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t p = i / I;
+    const int64_t c = i - p * I;
+    const uint16_t* g = gu + p * 2 * I;
+    h[i] = f32_to_bf16(lsk::act_eval(act, bf16_to_f32(g[c]), bf16_to_f32(g[I + c]), frac, tab));
+  }
+}
+
 // ---------------------------------------------------------------- requant and combine
 // rowquant of the activation output h (bf16 values), with the row maxima from the GEMM; q row-major
 // [R, I], or with pair in the row-pair layout the down tiles read (I % 64 == 0).  One wave per
@@ -2790,7 +2808,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // block-scaled activations at decode sizes: the same GEMV over integer-valued rows (every row
   // quantised in the general form) with the block exponents (T = 1 50 vs 116 us, T = 16 221 vs
   // 278 us, T = 24 281 vs 277 us)
-  const bool use_mx2_gemv = gemv_ok && mx == 2 && (g_moe_force == 2 || T <= kMx2GemvMaxT) && H <= 8192 && I <= 8192;
+  // and the skinny grouped MX GEMM where the MX layer would take it (the rows' dequantised bf16
+  // values, no row scale; a flagged row sends the projection to the general tile kernel instead)
+  const bool use_mx2_skinny =
+      mx == 2 && a->w13_pair_ptrs && a->w2_pair_ptrs && mx_takes_skinny(T, k, E, H, I, a->lds13, a->lds2, rb);
+  const bool use_mx2_gemv = gemv_ok && mx == 2 && !use_mx2_skinny && (g_moe_force == 2 || T <= kMx2GemvMaxT) &&
+                            H <= 8192 && I <= 8192;
   // the down projection's quantised rows in the row-pair layout when the ping-pong tiles read them
   // (int8 experts, no rotation): its load instructions then read whole 128-byte lines
   const bool pair_down = use_pp && !mx && rb == 0 && !use_gemv && !use_skinny && I % 64 == 0 &&
@@ -2928,6 +2951,16 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   }
   if (use_mx_gemv || use_mx2_gemv) {
     if ((rc = lsk::launch_moe_mx_gemv(0, g1, w.max_tiles, T, a->mx_safe, use_mx2_gemv ? nullptr : w.gu, s))) return rc;
+  } else if (use_mx2_skinny) {
+    // the skinny GEMM when no row of x is flagged (gate / up values into gu), else the general tile
+    // kernel over every tile (h itself)
+    MoeGemmArgs gs = g1;
+    gs.w_ptrs = a->w13_pair_ptrs;
+    gs.w_bytes = lsk::mx_skinny_bytes(2 * I, H);
+    gs.mx2 = 1;
+    if ((rc = lsk::launch_moe_mx_skinny(0, gs, w.max_tiles, T, a->mx_safe, w.gu, s))) return rc;
+    g1.mx2 = 3;
+    if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (mx == 2) {
     g1.mx2 = 1;
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
@@ -2998,6 +3031,12 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
                        rb, a->rot_scale, w.qh, w.asch);
     if ((rc = lsk::check_launch("moe_rot_requant_kernel"))) return rc;
   } else if (mx == 2) {
+    if (use_mx2_skinny) {
+      const int64_t blocks = std::min<int64_t>(4096, std::max<int64_t>(1, (R * I + 255) / 256));
+      hipLaunchKernelGGL(moe_act_h_kernel, dim3((unsigned)blocks), dim3(256), 0, s, w.gu, w.offs + E, (int)I, a->act,
+                         a->frac, a->act_tab, anyf, w.h);
+      if ((rc = lsk::check_launch("moe_act_h_kernel"))) return rc;
+    }
     if ((rc = lsk::launch_blockquant_mx2(w.h, I, R, w.offs + E, (int)I, (uint16_t*)w.qh, w.kah, w.flagh, anyf + 1,
                                          use_mx2_gemv ? 1 : lo2, use_mx2_gemv ? 0 : hi2, s)))
       return rc;
@@ -3039,6 +3078,14 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   }
   if (use_mx_gemv || use_mx2_gemv) {
     if ((rc = lsk::launch_moe_mx_gemv(1, g2, w.max_tiles, T, a->mx_safe, nullptr, s))) return rc;
+  } else if (use_mx2_skinny) {
+    MoeGemmArgs gs = g2;
+    gs.w_ptrs = a->w2_pair_ptrs;
+    gs.w_bytes = lsk::mx_skinny_bytes(H, I);
+    gs.mx2 = 1;
+    if ((rc = lsk::launch_moe_mx_skinny(1, gs, w.max_tiles, T, a->mx_safe, nullptr, s))) return rc;
+    g2.mx2 = 3;
+    if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (mx == 2) {
     g2.mx2 = 1;
     if ((rc = lsk::launch_moe_mx_gemm(1, g2, w.max_tiles, a->mx_safe, s))) return rc;

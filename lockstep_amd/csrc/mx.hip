@@ -370,10 +370,12 @@ LSK_DEV void moe_mx_epilogue(const lsk::MoeGemmArgs& a, const Cfg::Acc& acc, int
 }
 
 // Block-scaled activations: a tile goes to the fused-update kernel (mx2 == 1) when none of its
-// rows is flagged, to the general one (mx2 == 2) otherwise.  Every thread of the block calls it;
+// rows is flagged, to the general one (mx2 == 2) otherwise; with mx2 == 3 (after the skinny GEMM,
+// which runs only when no row is flagged) every tile goes to the general kernel when some row is.  Every thread of the block calls it;
 // when no row at all is flagged (the usual case) it decides without a barrier.
 template <int MODE>
 LSK_DEV bool mx2_takes_tile(const lsk::MoeGemmArgs& a, int p0, int p1) {
+  if (a.mx2 == 3) return *a.any_flag != 0;  // every tile, when some row is flagged
   if (*a.any_flag == 0) return a.mx2 == 1;
   int f = 0;
   const int t = threadIdx.x;
@@ -541,7 +543,7 @@ int launch_grouped(const lsk::MoeGemmArgs& ga, int64_t max_tiles, hipStream_t s)
   const int64_t blocks = max_tiles * ntiles;
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "moe_mx_gemm_kernel: grid too large");
-  if (ga.mx2 == 2) {
+  if (ga.mx2 >= 2) {
     static std::atomic<bool> attr_rs{false};
     auto kern = moe_mx_gemm_kernel<MODE, true, true>;
     if (!attr_rs) {
@@ -872,6 +874,7 @@ __global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArg
   const int lane = threadIdx.x & 63, wave = wave_id(), tid = threadIdx.x;
   const int mt = blockIdx.x / sets, gs = blockIdx.x - (blockIdx.x / sets) * sets;
   if (mt >= a.tiles[0]) return;  // the whole block leaves
+  if (a.mx2 == 1 && *a.any_flag != 0) return;  // block-scaled rows with a flagged row: not here
   const int e = a.tiles[1 + 2 * mt];
   const int p0 = a.tiles[2 + 2 * mt];
   const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
@@ -1080,7 +1083,7 @@ int moe_mx_skinny_lds(int64_t K, int64_t lds) {
 
 int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t rows, int safe, uint16_t* gu,
                          hipStream_t s) {
-  LSK_REQUIRE(!ga.a_ka && ga.K % 32 == 0 && (mode == 1 || gu), "moe_mx_skinny: arguments");
+  LSK_REQUIRE((!ga.a_ka || ga.mx2 == 1) && ga.K % 32 == 0 && (mode == 1 || gu), "moe_mx_skinny: arguments");
   if (mode == 0)
     return safe ? launch_mx_skinny<0, true>(ga, max_tiles, rows, gu, s, "moe_mx_skinny_kernel<gate_up>")
                 : launch_mx_skinny<0, false>(ga, max_tiles, rows, gu, s, "moe_mx_skinny_kernel<gate_up>");

@@ -626,7 +626,7 @@ def _moe_layer_mx(x, idx, w, t: ExpertTablesMX, act: int, wfmt: int = 1, route=N
     work = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     kb = t.kw_bounds
     choice = _choice_fields()
-    s13, s2 = t.skinny_ptrs(T, k, choice["select"], choice["mx_select"]) if wfmt == 1 else (None, None)
+    s13, s2 = t.skinny_ptrs(T, k, choice["select"], choice["mx_select"])
     a = L.MoeArgs(T=T, H=H, I=t.I, E=t.E, k=k, act=act, wfmt=wfmt, mx_safe=t.mx_safe, lds13=t.lds13, lds2=t.lds2,
                   kw13_min=kb[0], kw13_max=kb[1], kw2_min=kb[2], kw2_max=kb[3],
                   x=x.data_ptr(), idx=idx.data_ptr(), w=w.data_ptr(), w13_ptrs=t.w13.data_ptr(), ldw13=t.ldw13,

@@ -251,7 +251,8 @@ def test_moe_mx2_gemv_extreme_exponents(act):
 @pytest.mark.parametrize("T", [2, 8, 16])
 @pytest.mark.parametrize("H,I", [(352, 224), (4160, 128)])
 def test_moe_mx2_gemv_token_counts(T, H, I):
-    """The decode GEMV at the token counts the default routes to it (T <= 16): T = 2 takes two rows
+    """The decode GEMV (forced; by default these token counts take the skinny grouped MX GEMM where
+    its LDS allows, the GEMV otherwise) at T <= 16: T = 2 takes two rows
     per pass, T = 8 and 16 four (the per-row block exponents sa[m * kB + b] of every row of a pass).
     H = 352 (11 blocks) keeps the gate/up in the one-chunk form; H = 4160 (130 blocks, above 128)
     takes the four-chunk form with one row per pass, and I = 128 (4 blocks) the down projection's
@@ -259,7 +260,29 @@ def test_moe_mx2_gemv_token_counts(T, H, I):
     both ends of the binary32 range.  (Every MX row count is a multiple of 32, so a GEMV column
     chunk of 8 or 16 columns is always whole.)"""
     x, oexp, idx, w, oact, got, dexp = _mx2_layer(T, 4, 2, H, I, seed=100 + T + H, tiny_rows=0.3, low_exp=True,
-                                                  big_exp=True, moe_force=-1)
+                                                  big_exp=True, moe_force=2)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx2(x, oexp, idx, w, oact)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("T,E,k,H,I,tiny,low,big", [(32, 32, 4, 2880, 2880, 0.0, False, False),
+                                                    (1, 32, 4, 2880, 2880, 0.0, False, False),
+                                                    (40, 8, 2, 1088, 576, 0.0, False, True),
+                                                    (8, 4, 2, 352, 224, 0.3, True, True),
+                                                    (60, 6, 2, 352, 224, 0.05, True, False)])
+def test_moe_mx2_skinny(T, E, k, H, I, tiny, low, big):
+    """Block-scaled layers on the skinny grouped MX GEMM (the default from 2 tokens, and one token
+    of GPT-OSS-20B): the dequantised rows through the fused update with no row scale, gate / up
+    values through moe_act_h_kernel into h; with a flagged row (tiny rows against low E8M0 bytes)
+    the general tile kernel takes every tile of that projection instead; exponent bytes >= 240
+    (the multiply-then-add update)."""
+    from lockstep_amd import _lib as L
+    x, oexp, idx, w, oact, got, dexp = _mx2_layer(T, E, k, H, I, seed=120 + T, tiny_rows=tiny, low_exp=low,
+                                                  big_exp=big, bias=True)
+    assert L.load().lsk_moe_mx_reads_skinny(T, k, E, H, I, dexp.lds13, dexp.lds2, 0, 0) == 1
+    assert all(t is not None for t in dexp._skinny)
+    assert bool(_flagged_tokens(x, dexp).any()) == (tiny > 0)
     with np.errstate(over="ignore", invalid="ignore"):
         ref = C.moe_forward_mx2(x, oexp, idx, w, oact)
     assert np.array_equal(got, ref)
