@@ -3076,7 +3076,11 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
     g2.a_ka = w.kah;
     g2.ldka = I / 32;
   }
-  if (use_mx_gemv || use_mx2_gemv) {
+  if (mx == 1 && T == 1 && k <= 4 && (use_mx_gemv || use_mx_skinny) && lsk::mx_variant() == 0 && H <= 8192 &&
+      I <= 8192) {
+    // one token: the down GEMV of its (at most four) experts and the combine in one launch
+    return lsk::launch_moe_mx_down_combine1(g2, a->mx_safe, a->shared, a->y, s);
+  } else if (use_mx_gemv || use_mx2_gemv) {
     if ((rc = lsk::launch_moe_mx_gemv(1, g2, w.max_tiles, T, a->mx_safe, nullptr, s))) return rc;
   } else if (use_mx2_skinny) {
     MoeGemmArgs gs = g2;

@@ -58,6 +58,10 @@ int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int s
 int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,
                        hipStream_t s);
 
+// One token of MXFP4 experts (per-row scales, at most four): the down GEMV of every slot and the
+// ordered combine (+ bfr(shared)) in one launch, writing the token's row of y.
+int launch_moe_mx_down_combine1(const MoeGemmArgs& ga, int safe, const float* shared, uint16_t* y, hipStream_t s);
+
 // Skinny grouped MX GEMM (experts with few rows; per-row activation scales): the chunk's rows in
 // LDS, the codes streamed into the bf16 MFMA (mode 0: gate / up values into gu; mode 1: slot rows).
 // rows: at least the most rows any expert holds (the layer's T; the grouped linear's R).

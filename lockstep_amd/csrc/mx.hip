@@ -616,10 +616,15 @@ int launch_dense(const int8_t* a, int64_t lda, const int32_t* ka, int64_t ldka, 
 // MX2 (block-scaled activations, integer-valued rows with block exponents ka): the update is
 // acc = fl32(acc + fl32(s_b * fl32(2^ka_b * 2^(k_b - 128)))) with no row scale, and MODE 0 writes
 // the activation h = act(gate, up) straight into h (the owner lane holds both values).
+// MODE 2 (one token, at most four experts): the down projection and the combine in one launch --
+// wave s of a block computes slot s's MODE 1 values bfr(w * y) for the block's RPW columns into
+// LDS, and wave 0 adds the slots in order from +0 (the token's rows are its experts in ascending
+// order, the combine's order), then bfr(shared) when given, and writes the token's row of y (gu).
 typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
 
 template <int MODE, int MR, int NCH, int RPW, bool SAFE, bool MX2>
-__global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu) {
+__global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu,
+                                                          const float* __restrict__ shared) {
   constexpr int kRows = MODE == 0 ? 2 : 1;
   constexpr int V = MR * RPW * kRows;  // chains per row chunk, q = (m * RPW + i) * kRows + r
   static_assert(V <= 64, "one lane per chain");
@@ -627,16 +632,18 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
   constexpr int kSbStride = kB + 4;     // floats per chain row in LDS (16-byte aligned, skewed banks)
   constexpr int kWaveBytes = V * kSbStride * 4 + RPW * kRows * kB * 4 + (MX2 ? MR * kB * 4 : 0);
   extern __shared__ __attribute__((aligned(16))) char gemv_smem[];
-  const int cols_blk = 4 * RPW;
+  const int cols_blk = MODE == 2 ? RPW : 4 * RPW;
   const int nchunk = (a.N + cols_blk - 1) / cols_blk;
-  const int mt = blockIdx.x / nchunk, ch = blockIdx.x - mt * nchunk;
-  if (mt >= a.tiles[0]) return;
-  const int e = a.tiles[1 + 2 * mt];
-  const int p0 = a.tiles[2 + 2 * mt];
-  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
   const int lane = threadIdx.x & 63, wave = wave_id();
+  const int mt = MODE == 2 ? wave : (int)(blockIdx.x / nchunk);
+  const int ch = MODE == 2 ? (int)blockIdx.x : (int)(blockIdx.x - mt * nchunk);
+  const bool tile_ok = mt < a.tiles[0];
+  if (MODE != 2 && !tile_ok) return;  // (MODE 2: every wave reaches the combine's barrier)
+  const int e = tile_ok ? a.tiles[1 + 2 * mt] : 0;
+  const int p0 = tile_ok ? a.tiles[2 + 2 * mt] : 0;
+  const int p1 = tile_ok ? min(a.offs[e + 1], p0 + lsk::kMoeBM) : 0;
   const int nb = a.K / 32;
-  const int c0 = ch * cols_blk + wave * RPW;
+  const int c0 = MODE == 2 ? ch * RPW : ch * cols_blk + wave * RPW;
   const int nw = MODE == 0 ? 2 * a.N : a.N;  // weight rows of the expert
   float* sb = (float*)(gemv_smem + wave * kWaveBytes);
   float* scl = sb + V * kSbStride;  // 2^(k - 128) per (weight row, block)
@@ -657,7 +664,7 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
 #pragma unroll
       for (int j = 0; j < NCH; ++j) {
         const int b = lane + 64 * j;
-        const bool in = c < a.N && b < nb;
+        const bool in = tile_ok && c < a.N && b < nb;
         codes[i][r][j] = lsk::buf_load16(rw, in ? (uint32_t)(wr * a.ldw + b * 16) : lsk::kOob);
         kxs[i][r][j] = __builtin_amdgcn_raw_buffer_load_b8(rsc, in ? (int)(wr * a.lds + b) : (int)lsk::kOob, 0, 0);
       }
@@ -700,7 +707,7 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
     int dst = 0;
     if (rowok) {
       asc = a.a_scale ? a.a_scale[MODE == 0 ? a.row_tok[p] : p] : 1.0f;
-      if (MODE == 1) {
+      if (MODE >= 1) {
         wt = a.row_w ? a.row_w[p] : 1.0f;
         dst = a.row_dst ? a.row_dst[p] : p;
       }
@@ -803,29 +810,44 @@ __global__ __launch_bounds__(256) void moe_mx_gemv_kernel(lsk::MoeGemmArgs a, ui
       } else {
         float yv = bfr(f32_mul(acc, asc));
         if (bias) yv = bfr(f32_add(yv, b0));
-        a.y[(int64_t)dst * a.N + c] = f32_to_bf16(f32_mul(wt, yv));
+        if (MODE == 1) a.y[(int64_t)dst * a.N + c] = f32_to_bf16(f32_mul(wt, yv));
+        else ((float*)(gemv_smem + 4 * kWaveBytes))[mt * RPW + q_i] = bfr(f32_mul(wt, yv));
       }
+    }
+  }
+  if constexpr (MODE == 2) {
+    __syncthreads();
+    const float* comb = (const float*)(gemv_smem + 4 * kWaveBytes);  // [slot][RPW]
+    const int cc = c0 + lane;
+    if (wave == 0 && lane < RPW && cc < a.N) {
+      const int n = a.tiles[0];
+      float acc = 0.0f;
+      for (int s2 = 0; s2 < n; ++s2) acc = f32_add(acc, comb[s2 * RPW + lane]);
+      if (shared) acc = f32_add(acc, bfr(shared[cc]));
+      gu[cc] = f32_to_bf16(acc);
     }
   }
 }
 
 template <int MODE, int MR, int NCH, bool SAFE, bool MX2>
-int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name) {
+int launch_mx_gemv_k(const lsk::MoeGemmArgs& ga, int64_t max_tiles, uint16_t* gu, hipStream_t s, const char* name,
+                     const float* shared = nullptr) {
   constexpr int RPW = MODE == 0 ? 2 : 4;
   constexpr int kRows = MODE == 0 ? 2 : 1;
   constexpr int V = MR * RPW * kRows;
-  constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH * 4 + (MX2 ? MR * 64 * NCH * 4 : 0));
+  constexpr int smem = 4 * (V * (64 * NCH + 4) * 4 + RPW * kRows * 64 * NCH * 4 + (MX2 ? MR * 64 * NCH * 4 : 0)) +
+                       (MODE == 2 ? 4 * RPW * 4 : 0);
   static std::atomic<bool> attr{false};
   auto kern = moe_mx_gemv_kernel<MODE, MR, NCH, RPW, SAFE, MX2>;
   if (!attr) {
     if (int rc = reserve_lds(kern, smem, name)) return rc;
     attr = true;
   }
-  const int nchunk = (ga.N + 4 * RPW - 1) / (4 * RPW);
-  const int64_t blocks = max_tiles * nchunk;
+  const int nchunk = MODE == 2 ? (ga.N + RPW - 1) / RPW : (ga.N + 4 * RPW - 1) / (4 * RPW);
+  const int64_t blocks = MODE == 2 ? nchunk : max_tiles * nchunk;
   if (blocks == 0) return LSK_OK;
   LSK_REQUIRE(blocks <= 0x7fffffff, "%s: grid too large", name);
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), smem, s, ga, gu);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), smem, s, ga, gu, shared);
   return lsk::check_launch(name);
 }
 
@@ -1089,6 +1111,19 @@ int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int
                 : launch_mx_skinny<0, false>(ga, max_tiles, rows, gu, s, "moe_mx_skinny_kernel<gate_up>");
   return safe ? launch_mx_skinny<1, true>(ga, max_tiles, rows, nullptr, s, "moe_mx_skinny_kernel<down>")
               : launch_mx_skinny<1, false>(ga, max_tiles, rows, nullptr, s, "moe_mx_skinny_kernel<down>");
+}
+
+int launch_moe_mx_down_combine1(const MoeGemmArgs& ga, int safe, const float* shared, uint16_t* y, hipStream_t s) {
+  LSK_REQUIRE(!ga.a_ka && ga.K % 32 == 0 && y, "moe_mx_down_combine1: arguments");
+  const int nch = (ga.K / 32 + 63) / 64;
+  const char* name = "moe_mx_gemv_kernel<down + combine>";
+#define LSK_DC1(NCHV) \
+  return safe ? launch_mx_gemv_k<2, 1, NCHV, true, false>(ga, 1, y, s, name, shared) \
+              : launch_mx_gemv_k<2, 1, NCHV, false, false>(ga, 1, y, s, name, shared)
+  if (nch <= 1) LSK_DC1(1);
+  if (nch <= 2) LSK_DC1(2);
+  LSK_DC1(4);
+#undef LSK_DC1
 }
 
 int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,

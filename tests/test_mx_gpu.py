@@ -286,6 +286,46 @@ def test_moe_mx_skinny(T, E, k, H, I, big_exp, small_exp):
     assert np.array_equal(u16(yt), ref)
 
 
+@pytest.mark.parametrize("E,k,H,I,big_exp,bad_slot", [(32, 4, 2880, 2880, False, False), (8, 3, 1088, 576, True, True),
+                                                     (6, 2, 320, 192, False, True), (16, 4, 2048, 4160, True, False)])
+def test_moe_mx_one_token_down_combine(E, k, H, I, big_exp, bad_slot):
+    """One token of MXFP4 experts (k <= 4): the down GEMV of every slot and the ordered combine in
+    one launch (a wave per slot, the slots added in ascending expert order), against the oracle and
+    the slot-row path (lsk_moe_mx_select(3)): biases, the multiply-then-add update (exponent bytes
+    >= 240), one-, two- and four-chunk K (I = 192, 576 / 2880, 4160), and a slot whose expert index
+    is outside [0, E) (skipped, as the reference's loop over range(E) skips it)."""
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("mx one token down + combine", dict(E=E, k=k, H=H, I=I, big_exp=big_exp, bad_slot=bad_slot))
+    x, experts, logits = WL.moe_mx_inputs(1, E, k, H, I, seed=140 + E + k, bias=True)
+    if big_exp:
+        for e in range(E):
+            p13, s13, p2, s2, b13, b2 = experts[e]
+            s2 = s2.copy()
+            s2[::5, 1] = 242
+            experts[e] = (p13, s13, p2, s2, b13, b2)
+    idx, w = routing_from_logits(logits, k)
+    if bad_slot:
+        idx = idx.copy()
+        idx[0, 1] = E
+    oexp, dexp = [], []
+    for (p13, s13, p2, s2, b13, b2) in experts:
+        m13, _ = C.mx_to_m2(p13, s13)
+        m2_, _ = C.mx_to_m2(p2, s2)
+        oexp.append(((m13, s13), (m2_, s2), b13, b2))
+        dexp.append(((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2)))
+    dexp = MR.ExpertTablesMX(dexp, packed=True)
+    ridx, rw = routing_device(idx, w)
+    y, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai, routing=(ridx, rw))
+    with MR.kernel_choice(mx=3):
+        y3, _, _ = MR.moe_forward_mx(bf16_dev(x), None, dexp, k, True, _tab(), 0, MR.act_swigluoai,
+                                     routing=(ridx, rw))
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx(x, oexp, idx, w, C.act_swigluoai)
+    assert np.array_equal(u16(y), ref)
+    assert np.array_equal(u16(y3), ref)
+
+
 @pytest.mark.parametrize("variant", [0, 2])
 @pytest.mark.parametrize("big_exp", [False, True])
 def test_moe_mx_tiles_and_gemv(variant, big_exp):
