@@ -18,12 +18,12 @@
 #include "contract_act.h"
 #include "mfma_tile.h"
 #include "moe_internal.h"
+#include "moe_route.h"
 #include "pp_tile.h"
 #include "w4_tile.h"
 
 namespace {
 
-constexpr float kRouterC = 0x1.715476p+26f;    // fl32(2^26 / ln 2) (moe_ref.py:61)
 constexpr float kAmaxFloor = 0x1.5798eep-27f;  // fl32(1e-8)
 constexpr int kBM = lsk::kMoeBM;
 constexpr int kBM2 = 256;  // rows per tile of the 256 x 256 expert tiles (their own tile table)
@@ -39,70 +39,8 @@ thread_local int g_moe_w4 = 0;      // the ping-pong tile: 0 128x256 eight-wave 
                                     // 2 128x256 with 128-byte K stages, 3 256x256 (eight waves, four-stage ring)
 
 // ---------------------------------------------------------------- router
-// One wave per token; lane l owns experts l, l + 64, ... (EPL per lane, E <= 64 * EPL).  The
-// reference's ranking key s * E + (E - 1 - e) orders like the pair (s, E - 1 - e); with scores
-// below 2^16 (entries of the FRAC table are at most 2^15, and a score is an entry shifted right) and
-// E <= 2^16 the pair packs into one 32-bit key s << 16 | (0xffff - e), so each of the k rounds is
-// one DPP maximum over the wave and the winner is decoded from the wave-uniform key.  The
-// selection: lane r < k gets the rank-r expert e_r and its score s_r; S is the score sum the
-// weights divide by (the selected scores, or all of them without renormalisation), clamped to >= 1.
-template <int EPL>
-LSK_DEV void route_select(const void* __restrict__ g, int gdt, int64_t ldg, int t, int E, int k, int renorm,
-                          const int32_t* __restrict__ tab, int& e_mine, int& s_mine, int& S) {
-  const int lane = threadIdx.x & 63;
-  float gv[EPL];
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    gv[j] = 0.0f;
-    if (e < E) {
-      gv[j] = gdt == LSK_BF16 ? bf16_to_f32(((const uint16_t*)g)[(int64_t)t * ldg + e])
-                              : ((const float*)g)[(int64_t)t * ldg + e];
-      m = fmaxf(m, gv[j]);
-    }
-  }
-  m = wave_fmax(m);
-  uint32_t key[EPL];
-  int s_all = 0;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    key[j] = 0;
-    if (e < E) {
-      const float v = rintf(f32_mul(m - gv[j], kRouterC));
-      int sc = 0;
-      if (v < 1073741824.0f) {  // d < 16 << 26 (also false for NaN / inf)
-        const int d = v > 0.0f ? (int)v : 0;
-        sc = tab[(d >> 13) & 8191] >> (d >> 26);
-      }
-      s_all += sc;
-      key[j] = ((uint32_t)sc << 16) | (uint32_t)(0xffff - e);
-    }
-  }
-  s_all = wave_sum_i32(s_all);
-  s_mine = 0;
-  e_mine = 0;
-  int s_sum = 0;
-  for (int r = 0; r < k; ++r) {
-    uint32_t best = 0;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
-    best = wave_max_u32(best);
-    const int e = 0xffff - (int)(best & 0xffffu);
-    const int sc = (int)(best >> 16);
-    s_sum += sc;
-    if (lane == r) {
-      s_mine = sc;
-      e_mine = e;
-    }
-#pragma unroll
-    for (int j = 0; j < EPL; ++j)
-      if (lane + 64 * j == e) key[j] = 0;
-  }
-  S = renorm ? s_sum : s_all;
-  S = S < 1 ? 1 : S;
-}
+// (route_select: moe_route.h)
+using lsk::route_select;
 
 template <int EPL>
 LSK_DEV void route_token(const void* __restrict__ g, int gdt, int64_t ldg, int t, int E, int k, int renorm,
@@ -2834,6 +2772,10 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   // gate/up GEMV in one launch (moe_route_gemv1_kernel; no prep launch)
   const bool route_gemv1 = route_in_prep && T == 1 && use_gemv && !mx && k <= 8 && H % 16 == 0 && H <= 4096 &&
                            I <= 2048 && ((uintptr_t)a->x & 15) == 0 && g_rowq1;
+  // one MXFP4 token routed from its logits on the skinny path: the router and the row quant of x
+  // inside the gate/up launch (no prep launch)
+  const bool route_skinny1 = route_in_prep && T == 1 && use_mx_skinny && k <= 8 && H <= 8192 &&
+                             ((uintptr_t)a->x & 15) == 0 && g_rowq1;
   // above 256 tokens (int8 experts, no rotation): the router and the row quant of x in one launch
   const bool route_rowq = a->logits && !route_in_prep && !prep_decode && rb == 0 && !mx && H % 8 == 0 &&
                           H <= 4096 && E <= 256 && ((uintptr_t)a->x & 15) == 0 && g_rowq1;
@@ -2892,7 +2834,7 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   const int64_t nzero = mx == 2 ? R + 2 : R;
   int32_t* anyf = (int32_t*)(w.h_amax + R);
   const int64_t nchunks = (T + 255) / 256;
-  if (route_gemv1) {
+  if (route_gemv1 || route_skinny1) {
     // (the dispatch is written by the first launch below)
   } else if (prep_decode) {
     const size_t dsm = (size_t)(10 * E + 1) * 4 + (size_t)256 * k * 6;
@@ -2969,7 +2911,29 @@ static int moe_forward_call(const lsk_moe_args* a, void* stream) {
   } else if (use_mx_skinny) {
     g1.w_ptrs = a->w13_pair_ptrs;
     g1.w_bytes = lsk::mx_skinny_bytes(2 * I, H);
-    if ((rc = lsk::launch_moe_mx_skinny(0, g1, w.max_tiles, T, a->mx_safe, w.gu, s))) return rc;
+    if (route_skinny1) {
+      lsk::MxRouteArgs ra{};
+      ra.g = a->logits;
+      ra.gdt = a->logits_dtype;
+      ra.ldg = a->ld_logits;
+      ra.E = (int)E;
+      ra.k = k;
+      ra.renorm = a->renormalize;
+      ra.rtab = a->router_tab;
+      ra.x = a->x;
+      ra.idx_out = a->idx_out;
+      ra.w_out = a->w_out;
+      ra.offs = w.offs;
+      ra.tiles = w.tiles;
+      ra.row_tok = w.row_tok;
+      ra.row_dst = w.row_dst;
+      ra.tok_cnt = w.tok_cnt;
+      ra.row_w = w.row_w;
+      ra.ascx = w.ascx;
+      if ((rc = lsk::launch_moe_mx_route_skinny1(g1, ra, a->mx_safe, w.gu, s))) return rc;
+    } else if ((rc = lsk::launch_moe_mx_skinny(0, g1, w.max_tiles, T, a->mx_safe, w.gu, s))) {
+      return rc;
+    }
   } else if (mx) {
     if ((rc = lsk::launch_moe_mx_gemm(0, g1, w.max_tiles, a->mx_safe, s))) return rc;
   } else if (route_gemv1) {

@@ -58,6 +58,22 @@ int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int s
 int launch_moe_mx_gemv(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t T, int safe, uint16_t* gu,
                        hipStream_t s);
 
+// One token routed from its logits inside the skinny MX gate/up launch: the router's inputs, the
+// token's row of x, and the routing outputs and one-token dispatch its block 0 writes.
+struct MxRouteArgs {
+  const void* g;  // logits [E] (f32 or bf16)
+  int gdt;
+  int64_t ldg;
+  int E, k, renorm;
+  const int32_t* rtab;
+  const uint16_t* x;  // [K] bf16, 16-byte aligned
+  int64_t* idx_out;
+  uint16_t* w_out;
+  int32_t *offs, *tiles, *row_tok, *row_dst, *tok_cnt;
+  float *row_w, *ascx;
+};
+int launch_moe_mx_route_skinny1(const MoeGemmArgs& ga, const MxRouteArgs& ra, int safe, uint16_t* gu, hipStream_t s);
+
 // One token of MXFP4 experts (per-row scales, at most four): the down GEMV of every slot and the
 // ordered combine (+ bfr(shared)) in one launch, writing the token's row of y.
 int launch_moe_mx_down_combine1(const MoeGemmArgs& ga, int safe, const float* shared, uint16_t* y, hipStream_t s);

@@ -4,6 +4,7 @@
 
 #include "contract_act.h"
 #include "moe_internal.h"
+#include "moe_route.h"
 #include "mx_pp.h"
 #include "mx_tile.h"
 
@@ -889,17 +890,46 @@ int launch_mx_gemv(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t T, uin
 // expert holds when that is fewer (one token: one row, so the LDS holds one row and more blocks fit
 // a CU; MFMA rows past the chunk read its last row and their outputs are dropped).  LDS: the
 // chunk's rows [cr][ldsk], the waves' E8M0 bytes [WPB][scb], the rows' operands.
-template <int MODE, bool SAFE, int D, int WPB>
+// ROUTE = EPL > 0 (MODE 0, one token, one-row chunks): the token is routed from its logits in the
+// launch itself -- every wave runs the router's selection (route_select), the block takes the
+// mt-th of the k experts ascending, quantises the token's row of x into its LDS row (rowquant's
+// arithmetic, the values as bf16), and block 0's first wave writes the routing outputs and the
+// one-token dispatch the later launches read (as moe_route_gemv1_kernel does for int8 experts).
+template <int MODE, bool SAFE, int D, int WPB, int ROUTE = 0>
 __global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArgs a, uint16_t* __restrict__ gu,
-                                                                 int sets, int ldsk, int scb, int cr) {
+                                                                 int sets, int ldsk, int scb, int cr,
+                                                                 lsk::MxRouteArgs rt) {
   extern __shared__ __attribute__((aligned(16))) char smem_mxs[];
   const int lane = threadIdx.x & 63, wave = wave_id(), tid = threadIdx.x;
   const int mt = blockIdx.x / sets, gs = blockIdx.x - (blockIdx.x / sets) * sets;
-  if (mt >= a.tiles[0]) return;  // the whole block leaves
-  if (a.mx2 == 1 && *a.any_flag != 0) return;  // block-scaled rows with a flagged row: not here
-  const int e = a.tiles[1 + 2 * mt];
-  const int p0 = a.tiles[2 + 2 * mt];
-  const int p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  int e, p0, p1;
+  int e_r = 0, s_r = 0, S = 1, pos = 0;
+  int ek[8];
+  uint4 xr[4];  // ROUTE: this thread's 8-element chunks of the token's row of x
+  if constexpr (ROUTE > 0) {
+    if (mt >= rt.k) return;  // the whole block leaves
+    // x first (its wait then leaves the code loads issued below in flight), then the routing
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = tid + WPB * 64 * j;
+      xr[j] = c < (a.K >> 3) ? *(const uint4*)(rt.x + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+    lsk::route_select<ROUTE>(rt.g, rt.gdt, rt.ldg, 0, rt.E, rt.k, rt.renorm, rt.rtab, e_r, s_r, S);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ek[j] = __shfl(e_r, j < rt.k ? j : 0, 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pos += (j < rt.k && ek[j] < e_r) ? 1 : 0;
+    const uint64_t sel = __builtin_amdgcn_ballot_w64(lane < rt.k && pos == mt);
+    e = __shfl(e_r, (int)__builtin_ctzll(sel), 64);
+    p0 = mt;
+    p1 = mt + 1;
+  } else {
+    if (mt >= a.tiles[0]) return;  // the whole block leaves
+    if (a.mx2 == 1 && *a.any_flag != 0) return;  // block-scaled rows with a flagged row: not here
+    e = a.tiles[1 + 2 * mt];
+    p0 = a.tiles[2 + 2 * mt];
+    p1 = min(a.offs[e + 1], p0 + lsk::kMoeBM);
+  }
   const int K = a.K, nb = K >> 5;
   const int NWR = MODE == 0 ? 2 * a.N : a.N;  // weight rows
   const int G = (NWR + 15) >> 4;
@@ -923,6 +953,7 @@ __global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArg
   float* r_asc = (float*)(r_src + 16);
   float* r_w = r_asc + 16;
   int* r_dst = (int*)(r_w + 16);
+  float* r_red = (float*)(r_dst + 16);  // ROUTE: the waves' maxima of |x|
   // the group's E8M0 rows 16 g .. 16 g + 15: one contiguous run of 16 lds bytes (zeros past NWR)
   {
     const int sbytes = 16 * (int)a.lds;
@@ -944,7 +975,69 @@ __global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArg
 #pragma unroll
     for (int u = 0; u < D; ++u)
       cw[u] = lsk::buf_load16(rw, (u < nst && wbase != lsk::kOob) ? wbase + 1024u * u : lsk::kOob);
-    if (MODE == 0) {
+    float rsc_x = 0.0f;  // ROUTE: the token's row scale
+    if constexpr (ROUTE > 0) {
+      // the token's row of x quantised into LDS row 0: q = clamp(rint(x / asc)) as bf16 values
+      constexpr int NTH = WPB * 64;
+      const int K8 = K >> 3;
+      float am = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wd[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          am = fmaxf(am, fmaxf(fabsf(bf16_to_f32((uint16_t)(wd[q] & 0xffff))),
+                               fabsf(bf16_to_f32((uint16_t)(wd[q] >> 16)))));
+      }
+      am = wave_fmax(am);
+      if (lane == 0) r_red[wave] = am;
+      __syncthreads();
+      am = r_red[0];
+#pragma unroll
+      for (int w2 = 1; w2 < WPB; ++w2) am = fmaxf(am, r_red[w2]);
+      const float sc = f32_div(fmaxf(am, kAmaxFloor), 127.0f), rs = f32_div(1.0f, sc);
+      rsc_x = sc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = tid + NTH * j;
+        if (c < K8) {
+          const uint32_t wd[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+          uint32_t ob[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float q0v = fminf(fmaxf(rint_div8(bf16_to_f32((uint16_t)(wd[q] & 0xffff)), sc, rs), -127.0f), 127.0f);
+            const float q1v = fminf(fmaxf(rint_div8(bf16_to_f32((uint16_t)(wd[q] >> 16)), sc, rs), -127.0f), 127.0f);
+            ob[q] = (__float_as_uint(q0v) >> 16) | (__float_as_uint(q1v) & 0xffff0000u);  // exact bf16
+          }
+          *(uint2*)(smem_mxs + 16 * c) = make_uint2(ob[0], ob[1]);
+          *(uint2*)(smem_mxs + 16 * c + 8) = make_uint2(ob[2], ob[3]);
+        }
+      }
+      // block 0's first wave: the routing outputs and the one-token dispatch
+      if (blockIdx.x == 0 && wave == 0) {
+        if (lane < rt.k) {
+          const uint16_t wb = f32_to_bf16(f32_div((float)s_r, (float)S));
+          rt.idx_out[lane] = e_r;
+          rt.w_out[lane] = wb;
+          rt.tiles[1 + 2 * pos] = e_r;
+          rt.tiles[2 + 2 * pos] = pos;
+          rt.row_tok[pos] = 0;
+          rt.row_dst[pos] = pos;
+          rt.row_w[pos] = bf16_to_f32(wb);
+        }
+        for (int ee = lane; ee <= rt.E; ee += 64) {
+          int before = 0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) before += (j < rt.k && ek[j] < ee) ? 1 : 0;
+          rt.offs[ee] = before;
+        }
+        if (lane == 0) {
+          rt.tiles[0] = rt.k;
+          rt.tok_cnt[0] = rt.k;
+          rt.ascx[0] = sc;
+        }
+      }
+    } else if (MODE == 0) {
       // the token rows of the chunk: loaded behind the first code steps, waited for alone
       const int src = tid < nr ? a.row_tok[q0 + tid] : 0;
       lsk::compiler_fence();
@@ -952,7 +1045,7 @@ __global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArg
       __syncthreads();
     }
     // the chunk's rows into LDS (bf16 values, zeros past K), then the rows' operands
-    for (int c = wave; c < nr * cpr; c += WPB) {
+    for (int c = wave; c < (ROUTE > 0 ? 0 : nr * cpr); c += WPB) {
       const int r = c / cpr, j = c - (c / cpr) * cpr;
       const int kb = j * 1024 + lane * 16;
       const int src = MODE == 0 ? r_src[r] : q0 + r;
@@ -964,7 +1057,8 @@ __global__ __launch_bounds__(WPB * 64) void moe_mx_skinny_kernel(lsk::MoeGemmArg
     int o_dst = 0;
     if (tid < nr) {
       const int p = q0 + tid;
-      if (a.a_scale) o_asc = a.a_scale[MODE == 0 ? r_src[tid] : p];
+      if (ROUTE > 0) o_asc = rsc_x;
+      else if (a.a_scale) o_asc = a.a_scale[MODE == 0 ? r_src[tid] : p];
       if (MODE == 1) {
         o_w = a.row_w ? a.row_w[p] : 1.0f;
         o_dst = a.row_dst ? a.row_dst[p] : p;
@@ -1060,7 +1154,7 @@ int launch_mx_skinny(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t rows
   const int sets = (G + wpb - 1) / wpb;
   const int ldsk = (2 * ga.K + 1023) / 1024 * 1024 + 16;
   const int scb = (16 * (int)ga.lds + 1023) / 1024 * 1024;
-  const int smem = cr * ldsk + wpb * scb + 4 * 16 * 4;
+  const int smem = cr * ldsk + wpb * scb + 5 * 16 * 4;
   LSK_REQUIRE(smem <= 160 * 1024, "%s: %d bytes of LDS", name, smem);
   const int64_t blocks = max_tiles * sets;
   if (blocks == 0) return LSK_OK;
@@ -1073,7 +1167,7 @@ int launch_mx_skinny(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t rows
       if (int rc = reserve_lds(kern, 160 * 1024, name)) return rc;
       attr = true;
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), smem, s, ga, gu, sets, ldsk, scb, cr);
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), smem, s, ga, gu, sets, ldsk, scb, cr, lsk::MxRouteArgs{});
   } else {
     auto kern = moe_mx_skinny_kernel<MODE, SAFE, D, 16>;
     static std::atomic<bool> attr{false};
@@ -1081,14 +1175,53 @@ int launch_mx_skinny(const lsk::MoeGemmArgs& ga, int64_t max_tiles, int64_t rows
       if (int rc = reserve_lds(kern, 160 * 1024, name)) return rc;
       attr = true;
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(1024), smem, s, ga, gu, sets, ldsk, scb, cr);
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(1024), smem, s, ga, gu, sets, ldsk, scb, cr, lsk::MxRouteArgs{});
   }
+  return lsk::check_launch(name);
+}
+
+// One token routed inside the gate/up launch (ROUTE = EPL): four-wave blocks, one-row chunks, k
+// experts x the column groups' sets.
+template <bool SAFE, int EPL>
+int launch_mx_route_skinny1(const lsk::MoeGemmArgs& ga, const lsk::MxRouteArgs& ra, uint16_t* gu, hipStream_t s,
+                            const char* name) {
+  const int G = (2 * ga.N + 15) / 16;
+  const int sets = (G + 3) / 4;
+  const int ldsk = (2 * ga.K + 1023) / 1024 * 1024 + 16;
+  const int scb = (16 * (int)ga.lds + 1023) / 1024 * 1024;
+  const int smem = ldsk + 4 * scb + 5 * 16 * 4;
+  LSK_REQUIRE(smem <= 160 * 1024, "%s: %d bytes of LDS", name, smem);
+  const int64_t blocks = (int64_t)ra.k * sets;
+  if (blocks == 0) return LSK_OK;
+  auto kern = moe_mx_skinny_kernel<0, SAFE, SAFE ? 4 : 8, 4, EPL>;
+  static std::atomic<bool> attr{false};
+  if (!attr) {
+    if (int rc = reserve_lds(kern, 160 * 1024, name)) return rc;
+    attr = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), smem, s, ga, gu, sets, ldsk, scb, 1, ra);
   return lsk::check_launch(name);
 }
 
 }  // namespace
 
 namespace lsk {
+
+int launch_moe_mx_route_skinny1(const MoeGemmArgs& ga, const MxRouteArgs& ra, int safe, uint16_t* gu, hipStream_t s) {
+  LSK_REQUIRE(ga.K % 32 == 0 && ga.K <= 8192 && gu && ra.x && ((uintptr_t)ra.x & 15) == 0 && ra.k >= 1 &&
+                  ra.k <= 8 && ra.E >= ra.k && ra.E <= 256,
+              "moe_mx_route_skinny1: arguments");
+  const char* name = "moe_mx_skinny_kernel<gate_up, routed>";
+  const int epl = ra.E <= 64 ? 1 : (ra.E <= 128 ? 2 : 4);
+  if (safe) {
+    if (epl == 1) return launch_mx_route_skinny1<true, 1>(ga, ra, gu, s, name);
+    if (epl == 2) return launch_mx_route_skinny1<true, 2>(ga, ra, gu, s, name);
+    return launch_mx_route_skinny1<true, 4>(ga, ra, gu, s, name);
+  }
+  if (epl == 1) return launch_mx_route_skinny1<false, 1>(ga, ra, gu, s, name);
+  if (epl == 2) return launch_mx_route_skinny1<false, 2>(ga, ra, gu, s, name);
+  return launch_mx_route_skinny1<false, 4>(ga, ra, gu, s, name);
+}
 
 int launch_moe_mx_gemm(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int safe, hipStream_t s) {
   if (mode == 0) return safe ? launch_grouped<0, true>(ga, max_tiles, s) : launch_grouped<0, false>(ga, max_tiles, s);
@@ -1100,7 +1233,7 @@ int64_t mx_skinny_bytes(int64_t rows, int64_t K) { return (rows + 15) / 16 * ((K
 
 // LDS bytes the skinny grouped MX GEMM needs for K and an E8M0 row stride lds (<= 160 KB to run).
 int moe_mx_skinny_lds(int64_t K, int64_t lds) {
-  return (int)((2 * K + 1023) / 1024 * 1024 + 16) * 16 + (int)((16 * lds + 1023) / 1024 * 1024) * 16 + 256;
+  return (int)((2 * K + 1023) / 1024 * 1024 + 16) * 16 + (int)((16 * lds + 1023) / 1024 * 1024) * 16 + 320;
 }
 
 int launch_moe_mx_skinny(int mode, const MoeGemmArgs& ga, int64_t max_tiles, int64_t rows, int safe, uint16_t* gu,

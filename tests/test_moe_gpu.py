@@ -451,6 +451,44 @@ def test_moe_mx_forward_from_logits(T, wfmt):
     assert torch.equal(di, ri) and torch.equal(dw.view(torch.int16), rw.view(torch.int16))
 
 
+@pytest.mark.parametrize("E,k,H,I,gdt,renorm,big_exp", [(32, 4, 2880, 2880, "bf16", True, False),
+                                                       (128, 4, 2880, 2880, "f32", False, True),
+                                                       (160, 8, 576, 1344, "bf16", True, False)])
+def test_moe_mx_one_token_routed_in_gate_up_launch(E, k, H, I, gdt, renorm, big_exp):
+    """One MXFP4 token routed from its logits inside the skinny gate/up launch (every wave runs the
+    router's selection, each block quantises x itself, block 0 writes the dispatch): the same bits
+    as router_from_logits followed by the layer, and the oracle's y; one, two and four experts per
+    router lane (E = 32, 128, 160), f32 and bf16 logits, with and without renormalisation, and the
+    multiply-then-add update."""
+    from lockstep_amd import moe_ref as MR
+    from lockstep_amd import workloads as WL
+    say("moe mx token routed in the gate/up launch", dict(E=E, k=k, H=H, I=I, gdt=gdt, renorm=renorm))
+    x, experts, logits = WL.moe_mx_inputs(1, E, k, H, I, seed=150 + E, bias=True)
+    if big_exp:
+        p13, s13, p2, s2, b13, b2 = experts[3]
+        s2 = s2.copy()
+        s2[::6, 2] = 245
+        experts[3] = (p13, s13, p2, s2, b13, b2)
+    dexp = MR.ExpertTablesMX([((to_dev(p13), to_dev(s13)), (to_dev(p2), to_dev(s2)), to_dev(b13), to_dev(b2))
+                              for (p13, s13, p2, s2, b13, b2) in experts], packed=True)
+    dx = bf16_dev(x)
+    g = bf16_dev(logits) if gdt == "bf16" else torch.from_numpy(logits.astype(F32)).to(dev())
+    ri, rw, _ = MR.router_from_logits(g, k, renorm, _tab())
+    y0, _, _ = MR.moe_forward_mx(dx, None, dexp, k, renorm, _tab(), 0, MR.act_swigluoai, routing=(ri, rw))
+    y1, di, dw = MR.moe_forward_mx(dx, None, dexp, k, renorm, _tab(), 0, MR.act_swigluoai, logits=g)
+    assert torch.equal(di, ri) and torch.equal(dw.view(torch.int16), rw.view(torch.int16))
+    assert torch.equal(y1.view(torch.int16), y0.view(torch.int16))
+    oexp = []
+    for (p13, s13, p2, s2, b13, b2) in experts:
+        m13, _ = C.mx_to_m2(p13, s13)
+        m2_, _ = C.mx_to_m2(p2, s2)
+        oexp.append(((m13, s13), (m2_, s2), b13, b2))
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = C.moe_forward_mx(x, oexp, di.cpu().numpy(), dw.view(torch.int16).cpu().numpy().view(np.uint16),
+                               C.act_swigluoai)
+    assert np.array_equal(y1.view(torch.int16).cpu().numpy().view(np.uint16), ref)
+
+
 @pytest.mark.parametrize("k,I,extra", [(8, 768, None), (4, 1024, "shared"), (6, 2048, "bias"), (3, 512, "skip"),
                                        (8, 1536, "skip_all"), (1, 256, None)])
 def test_moe_one_token_down_and_combine(k, I, extra):
