@@ -603,7 +603,9 @@ int lsk_grouped_mx_reads_skinny(int64_t R, int64_t E, int64_t K, int64_t lds);
 /* Tuning control with no counterpart in the reference: 1 (the default) runs a one-token int8 layer
  * routed from its logits (lsk_moe_args.logits, the grouped GEMV path, k <= 8) with the router, the
  * row quant of x and the gate/up GEMV in one launch, every wave routing the token and quantising x
- * itself; 0 runs them as the prep launch and the GEMV.  Also (1) int8 layers of more than 256
+ * itself, and likewise a one-token MXFP4 layer on the skinny grouped MX GEMM (k <= 8, H <= 8192)
+ * with the router and the row quant inside its gate/up launch; 0 runs them as the prep launch and
+ * the GEMV or GEMM.  Also (1) int8 layers of more than 256
  * tokens routed from logits (E <= 256, H <= 4096, no rotation) route and quantise x in one launch,
  * a wave per token; 0 runs the router and lsk_rowquant.  Results are identical.  Thread-local. */
 int lsk_moe_fuse_route(int on);
