@@ -72,6 +72,22 @@ def test_moe_mx_skinny_query():
     assert lib.lsk_grouped_mx_reads_skinny(256, E, 100, 4) == 0                        # K % 32 != 0
 
 
+def test_mx_skinny_copy_size_and_argument_checks():
+    """lsk_mx_skinny_bytes: 1 KB per group of 16 rows and step of 4 blocks (partial ones whole); the
+    pack refuses K % 32 != 0, a row stride below K / 2 or not a multiple of 4, and null pointers,
+    before any device work."""
+    lib = L.load()
+    assert lib.lsk_mx_skinny_bytes(16, 128) == 1024
+    assert lib.lsk_mx_skinny_bytes(17, 128) == 2048
+    assert lib.lsk_mx_skinny_bytes(16, 160) == 2048            # 5 blocks: two steps
+    assert lib.lsk_mx_skinny_bytes(5760, 2880) == 360 * 23 * 1024
+    for args in ((64, 16, 40), (16, 16, 64), (34, 16, 64)):     # (ldw, rows, K)
+        ldw, rows, K = args
+        assert lib.lsk_mx_skinny_pack(16, ldw, rows, K, 4096, None) != 0, args
+    assert lib.lsk_mx_skinny_pack(None, 64, 16, 64, 4096, None) != 0
+    assert "lsk_mx_skinny_pack" in L.last_error()
+
+
 @pytest.fixture
 def counting_pack(monkeypatch):
     made = []
